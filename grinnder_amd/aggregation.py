@@ -1,0 +1,254 @@
+"""Autograd wrappers of the HIP aggregation kernels (GCN SpMM, GAT attention).
+
+These replace the third-party calls the reference reaches through PyG:
+torch_sparse ``spmm_sum`` and its ``csr2csc`` backward for GCNConv
+(grinnder/nn/gcn.py:53-56,65), and GATConv's logits / segment softmax /
+message aggregation (grinnder/nn/gat.py:54-61,73).
+"""
+
+from __future__ import annotations
+
+import contextlib
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+from torch import Tensor
+
+from grinnder_amd import _lib
+from grinnder_amd.data.adjacency import Adjacency, DevicePlan
+
+
+@dataclass
+class KernelRecord:
+    """One timed aggregation pass: algorithmic bytes and edges, HIP events."""
+
+    name: str
+    nbytes: int
+    edges: int
+    dim: int
+    start: "torch.cuda.Event"
+    end: "torch.cuda.Event"
+
+    def ms(self) -> float:
+        return self.start.elapsed_time(self.end)
+
+
+class KernelTimer:
+    """Records HIP events around every aggregation pass while active.
+
+    Events are recorded on the stream the kernels are launched on (the
+    current stream), so elapsed times are the passes' device durations.
+    Algorithmic bytes per pass (fp32 features, int32 index + fp32 value
+    per edge):
+      GCN pass over R rows of width D: nnz*(4D + 8) + R*(4D + 4)
+      GAT forward:  nnz*(4HC + 8H + 4) + B*(4HC + 4H + 4)
+      GAT backward: nnz*(8HC + 16H + 8) + E*(4HC + 4H) + B*(4HC + 4H)
+    """
+
+    active: Optional["KernelTimer"] = None
+
+    def __init__(self):
+        self.records: List[KernelRecord] = []
+
+    def __enter__(self):
+        KernelTimer.active = self
+        return self
+
+    def __exit__(self, *exc):
+        KernelTimer.active = None
+        return False
+
+    @staticmethod
+    @contextlib.contextmanager
+    def region(name: str, nbytes: int, edges: int, dim: int):
+        timer = KernelTimer.active
+        if timer is None:
+            yield
+            return
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        yield
+        end.record()
+        timer.records.append(KernelRecord(name, nbytes, edges, dim, start, end))
+
+
+def _check_device_tensor(name: str, t: Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (HIP); got {t.device}")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32; got {t.dtype}")
+
+
+def _workspace(n_slots: int, width: int, device) -> Optional[Tensor]:
+    if n_slots == 0:
+        return None
+    return torch.empty(n_slots * width, dtype=torch.float32, device=device)
+
+
+def spmm(plan, idx: Tensor, val: Tensor, x: Tensor, rows: int,
+         bias: Optional[Tensor] = None, out: Optional[Tensor] = None,
+         name: str = "gcn_spmm") -> Tensor:
+    """out[r] = sum_e val[e] * x[idx[e]] (+ bias) for the rows of `plan`."""
+    dim = x.size(1)
+    if out is None:
+        out = torch.empty((rows, dim), dtype=torch.float32, device=x.device)
+    ws = _workspace(plan.n_slots, dim, x.device)
+    nnz = idx.numel()
+    with KernelTimer.region(name, nnz * (4 * dim + 8) + rows * (4 * dim + 4), nnz, dim):
+        _lib.call("gr_gcn_aggregate", plan.units.data_ptr(), plan.n_units,
+                  plan.fixups.data_ptr() if plan.n_fix else None, plan.n_fix,
+                  idx.data_ptr(), val.data_ptr(), x.data_ptr(), x.stride(0), out.data_ptr(),
+                  out.stride(0), _lib.ptr(bias), rows, dim, _lib.ptr(ws), plan.n_slots,
+                  _lib.stream_handle())
+    return out
+
+
+class _GCNAggregate(torch.autograd.Function):
+    """Y = A Z + b forward; dZ = A^T G (CSC plan) and db = sum G backward."""
+
+    @staticmethod
+    def forward(ctx, z: Tensor, bias: Optional[Tensor], plan: DevicePlan) -> Tensor:
+        z = z.contiguous()
+        y = spmm(plan.fwd, plan.idx, plan.val, z, plan.num_dst,
+                 bias.contiguous() if bias is not None else None, name="gcn_fwd")
+        ctx.plan = plan
+        ctx.has_bias = bias is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy: Tensor):
+        plan: DevicePlan = ctx.plan
+        gy = gy.contiguous()
+        dz = None
+        if ctx.needs_input_grad[0]:
+            dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gy, plan.num_src, name="gcn_bwd")
+        db = gy.sum(0) if (ctx.has_bias and ctx.needs_input_grad[1]) else None
+        return dz, db, None
+
+
+def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None) -> Tensor:
+    """GCN neighbour aggregation A·Z (+ bias) of one partition, on the GPU."""
+    _check_device_tensor("z", z)
+    plan = adj.device_plan(z.device)
+    if z.size(0) != plan.num_src:
+        raise ValueError(f"z has {z.size(0)} rows, adjacency has {plan.num_src} columns")
+    return _GCNAggregate.apply(z, bias, plan)
+
+
+class _GATAttention(torch.autograd.Function):
+    """Attention logits + edge softmax + weighted aggregation of GATConv."""
+
+    @staticmethod
+    def forward(ctx, hs: Tensor, att_src: Tensor, att_dst: Tensor, bias: Optional[Tensor],
+                plan: DevicePlan, heads: int, channels: int, concat: bool) -> Tensor:
+        hs = hs.contiguous()
+        dev = hs.device
+        H, C = heads, channels
+        HC = H * C
+        E, B = plan.num_src, plan.num_dst
+        a_src = att_src.reshape(-1).contiguous()
+        a_dst = att_dst.reshape(-1).contiguous()
+        stream = _lib.stream_handle()
+        nnz = plan.nnz
+        region = KernelTimer.region(
+            "gat_fwd", nnz * (4 * HC + 8 * H + 4) + B * (4 * HC + 4 * H + 4), nnz, HC)
+        region.__enter__()
+        s = torch.empty((E, H), dtype=torch.float32, device=dev)
+        d = torch.empty((B, H), dtype=torch.float32, device=dev)
+        _lib.call("gr_gat_scores", hs.data_ptr(), hs.stride(0), E, B, H, C, a_src.data_ptr(),
+                  a_dst.data_ptr(), s.data_ptr(), d.data_ptr(), stream)
+        m = torch.empty((B, H), dtype=torch.float32, device=dev)
+        den = torch.empty((B, H), dtype=torch.float32, device=dev)
+        f = plan.fwd
+        ws = _workspace(f.n_slots, 2 * H, dev)
+        _lib.call("gr_gat_softmax_stats", f.units.data_ptr(), f.n_units,
+                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
+                  s.data_ptr(), d.data_ptr(), H, m.data_ptr(), den.data_ptr(), _lib.ptr(ws),
+                  f.n_slots, stream)
+        o = torch.empty((B, HC), dtype=torch.float32, device=dev)
+        fused_bias = concat or H == 1
+        y = torch.empty((B, HC), dtype=torch.float32, device=dev) if fused_bias else None
+        b = bias.contiguous() if (bias is not None and fused_bias) else None
+        ws = _workspace(f.n_slots, HC, dev)
+        _lib.call("gr_gat_aggregate", f.units.data_ptr(), f.n_units,
+                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
+                  hs.data_ptr(), hs.stride(0), s.data_ptr(), d.data_ptr(), m.data_ptr(),
+                  den.data_ptr(), H, C, _lib.ptr(b), o.data_ptr(), _lib.ptr(y),
+                  HC, _lib.ptr(ws), f.n_slots, stream)
+        region.__exit__(None, None, None)
+        if not fused_bias:
+            y = o.view(B, H, C).mean(dim=1)
+            if bias is not None:
+                y = y + bias
+        ctx.save_for_backward(hs, a_src, a_dst, s, d, m, den, o)
+        ctx.plan = plan
+        ctx.shape = (H, C, concat)
+        ctx.has_bias = bias is not None
+        ctx.att_shape = att_src.shape
+        return y
+
+    @staticmethod
+    def backward(ctx, gy: Tensor):
+        hs, a_src, a_dst, s, d, m, den, o = ctx.saved_tensors
+        plan: DevicePlan = ctx.plan
+        H, C, concat = ctx.shape
+        HC = H * C
+        E, B = plan.num_src, plan.num_dst
+        dev = hs.device
+        gy = gy.contiguous()
+        if concat or H == 1:
+            go = gy
+        else:
+            go = (gy / H).unsqueeze(1).expand(B, H, C).reshape(B, HC).contiguous()
+        db = gy.sum(0) if ctx.has_bias else None
+        cdot = (go.view(B, H, C) * o.view(B, H, C)).sum(-1).contiguous()
+        stream = _lib.stream_handle()
+        nnz = plan.nnz
+        region = KernelTimer.region(
+            "gat_bwd", nnz * (8 * HC + 16 * H + 8) + E * (4 * HC + 4 * H) + B * (4 * HC + 4 * H),
+            nnz, HC)
+        region.__enter__()
+        dhs = torch.empty((E, HC), dtype=torch.float32, device=dev)
+        ds = torch.empty((E, H), dtype=torch.float32, device=dev)
+        gt = torch.empty((max(plan.nnz, 1), H), dtype=torch.float32, device=dev)
+        bw = plan.bwd
+        ws = _workspace(bw.n_slots, HC + H, dev)
+        _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
+                  bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                  plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(), hs.stride(0),
+                  go.data_ptr(), s.data_ptr(), d.data_ptr(), m.data_ptr(), den.data_ptr(),
+                  cdot.data_ptr(), a_src.data_ptr(), H, C, dhs.data_ptr(), ds.data_ptr(),
+                  gt.data_ptr(), _lib.ptr(ws), bw.n_slots, stream)
+        dd = torch.empty((B, H), dtype=torch.float32, device=dev)
+        f = plan.fwd
+        ws = _workspace(f.n_slots, H, dev)
+        _lib.call("gr_gat_backward_dst", f.units.data_ptr(), f.n_units,
+                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, gt.data_ptr(),
+                  a_dst.data_ptr(), H, C, dd.data_ptr(), dhs.data_ptr(), _lib.ptr(ws),
+                  f.n_slots, stream)
+        region.__exit__(None, None, None)
+        # Attention-vector gradients: per head, ds[:,h]^T Hs[:, h] and dd[:,h]^T Hs[:B, h].
+        hs3 = hs.view(E, H, C)
+        datt_src = torch.stack([ds[:, h] @ hs3[:, h, :] for h in range(H)])
+        datt_dst = torch.stack([dd[:, h] @ hs3[:B, h, :] for h in range(H)])
+        return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
+                None, None, None, None)
+
+
+def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
+                  bias: Optional[Tensor], heads: int, channels: int,
+                  concat: bool = True) -> Tensor:
+    """GATConv attention over a bipartite partition adjacency, on the GPU.
+
+    hs = lin(x) for all E source rows; destination features are hs[:B].
+    Returns [B, H*C] (concat) or [B, C] (mean over heads), bias added.
+    """
+    _check_device_tensor("hs", hs)
+    plan = adj.device_plan(hs.device)
+    if hs.size(0) != plan.num_src:
+        raise ValueError(f"hs has {hs.size(0)} rows, adjacency has {plan.num_src} columns")
+    if hs.size(1) != heads * channels:
+        raise ValueError(f"hs has {hs.size(1)} features, expected {heads * channels}")
+    return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat)

@@ -1,0 +1,194 @@
+"""HostBuffer: one layer of per-partition host tensors (grinnder/buffer/host.py:55-478).
+
+Transfers go through the native op table (grinnder_amd._C).  With
+``pin_memory=True`` (what the Trainer uses) partitions live in pinned host
+memory, so the halo gather and the gradient scatter-add run as device kernels
+reading / updating the host rows in place over PCIe.  Synchronisation waits
+on the transfer stream only, never on the whole device.
+"""
+
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+from torch import Tensor
+
+from grinnder_amd import _C
+
+
+def _empty_host_tensor(rows: int, cols: int, *, pin_memory: bool, allocate: bool) -> Tensor:
+    shape = (rows, cols) if allocate else (0, cols)
+    return torch.empty(shape, dtype=torch.float32, pin_memory=pin_memory)
+
+
+def _none_to_empty(pid: int, boundaries: List[Optional[Tensor]], num_parts: int) -> List[Tensor]:
+    out = []
+    for i in range(num_parts):
+        b = boundaries[i] if i < len(boundaries) else None
+        out.append(torch.empty(0, dtype=torch.long) if (i == pid or b is None) else b)
+    return out
+
+
+class HostBuffer:
+    """Partition-wise fp32 tensors on the host.
+
+    Gather layout on the device: [intra(pid) | boundary_from_p0 | ... ]; the
+    scatter uses the same layout and accumulates (+=) into host partitions.
+    Storage is allocated lazily per partition and can be released.
+    """
+
+    def __init__(self, num_parts: int, part_sizes: List[int], embedding_dim: int,
+                 backend=None, file_prefix: str = "host", lazy: bool = True,
+                 pin_memory: bool = False):
+        if backend is not None:
+            raise NotImplementedError("the NVMe storage tier is outside this package's scope")
+        self.num_parts = num_parts
+        self.part_sizes = list(part_sizes)
+        self.embedding_dim = embedding_dim
+        self._file_prefix = file_prefix
+        self._element_size = 4
+        self._lazy = lazy
+        self._pin_memory = pin_memory
+        self._zero_initialized = [False] * num_parts
+        self._tensors: List[Tensor] = []
+        for i in range(num_parts):
+            t = _empty_host_tensor(part_sizes[i], embedding_dim, pin_memory=pin_memory,
+                                   allocate=not lazy)
+            if not lazy:
+                t.zero_()
+                self._zero_initialized[i] = True
+            self._tensors.append(t)
+
+    def __getitem__(self, pid: int) -> Tensor:
+        self.allocate(pid)
+        return self._tensors[pid]
+
+    def __len__(self) -> int:
+        return self.num_parts
+
+    def partition_nbytes(self, pid: int) -> int:
+        return self.part_sizes[pid] * self.embedding_dim * self._element_size
+
+    @property
+    def total_nbytes(self) -> int:
+        return sum(self.partition_nbytes(p) for p in range(self.num_parts))
+
+    def allocate(self, pid: int) -> Tensor:
+        t = self._tensors[pid]
+        expected = self.partition_nbytes(pid)
+        if t.untyped_storage().size() < expected:
+            if self._pin_memory:
+                t = torch.empty((self.part_sizes[pid], self.embedding_dim), dtype=torch.float32,
+                                pin_memory=True)
+                self._tensors[pid] = t
+            else:
+                t.untyped_storage().resize_(expected)
+        shape = (self.part_sizes[pid], self.embedding_dim)
+        if tuple(t.shape) != shape:
+            t.set_(t.untyped_storage(), 0, shape, (self.embedding_dim, 1))
+        return t
+
+    def release(self, pid: int) -> None:
+        self._tensors[pid] = _empty_host_tensor(self.part_sizes[pid], self.embedding_dim,
+                                                pin_memory=self._pin_memory, allocate=False)
+        self._zero_initialized[pid] = False
+
+    def release_all(self) -> None:
+        for pid in range(self.num_parts):
+            self.release(pid)
+
+    def is_allocated(self, pid: int) -> bool:
+        return self._tensors[pid].untyped_storage().size() >= self.partition_nbytes(pid)
+
+    def allocated_pids(self) -> List[int]:
+        return [p for p in range(self.num_parts) if self.is_allocated(p)]
+
+    def zero_partition(self, pid: int) -> None:
+        self.allocate(pid).zero_()
+        self._zero_initialized[pid] = True
+
+    @property
+    def resident_bytes(self) -> int:
+        return sum(self.partition_nbytes(p) for p in range(self.num_parts)
+                   if self.is_allocated(p))
+
+    # ---------------------------------------------------------- GPU -> host
+
+    def async_fill(self, pid: int, gpu_data: Tensor, stream: torch.cuda.Stream) -> None:
+        """D2H copy of a partition's [B, D] device tensor into host partition pid."""
+        assert gpu_data.is_cuda
+        self.allocate(pid)
+        stream.wait_stream(torch.cuda.current_stream(gpu_data.device))
+        with torch.cuda.stream(stream):
+            _C.d2h_copy_async(gpu_data.contiguous(), self._tensors[pid])
+        self._zero_initialized[pid] = True
+
+    def d2h_synchronize(self, stream: torch.cuda.Stream) -> None:
+        """Waits for the oldest queued D2H entry, then for `stream` itself."""
+        _C.d2h_synchronize()
+        stream.synchronize()
+
+    # ---------------------------------------------------------- host -> GPU
+
+    def async_upload(self, pid: int, gpu_target: Tensor, stream: torch.cuda.Stream) -> None:
+        assert gpu_target.is_cuda
+        if not self.is_allocated(pid):
+            raise RuntimeError(f"HostBuffer partition {pid} is not resident for upload")
+        stream.wait_stream(torch.cuda.current_stream(gpu_target.device))
+        with torch.cuda.stream(stream):
+            _C.h2d_copy_async(self._tensors[pid], gpu_target)
+
+    def h2d_synchronize(self, stream: torch.cuda.Stream) -> None:
+        _C.h2d_synchronize()
+        stream.synchronize()
+
+    # ---------------------------------------------------------------- gather
+
+    def async_gather(self, pid: int, gpu_target: Tensor, boundaries: List[Optional[Tensor]],
+                     stream: torch.cuda.Stream) -> None:
+        """gpu_target = [self[pid] | self[p][boundaries[p]] for p ascending]."""
+        assert gpu_target.is_cuda
+        required = {pid}
+        for p, b in enumerate(boundaries):
+            if p != pid and b is not None and b.numel() > 0:
+                required.add(p)
+        missing = [p for p in sorted(required) if not self.is_allocated(p)]
+        if missing:
+            raise RuntimeError(f"HostBuffer partitions {missing} are not resident for gather")
+        bnd = _none_to_empty(pid, boundaries, self.num_parts)
+        stream.wait_stream(torch.cuda.current_stream(gpu_target.device))
+        with torch.cuda.stream(stream):
+            _C.gather_partitions(pid, self._tensors, gpu_target, bnd)
+
+    # --------------------------------------------------------------- scatter
+
+    def async_scatter(self, pid: int, gpu_source: Tensor, boundaries: List[Optional[Tensor]],
+                      stream: torch.cuda.Stream) -> None:
+        """Accumulates gpu_source (gather layout) into the host partitions."""
+        assert gpu_source.is_cuda
+        for p, b in enumerate(boundaries):
+            if p == pid or (b is not None and b.numel() > 0):
+                self.allocate(p)
+                if not self._zero_initialized[p]:
+                    self._tensors[p].zero_()
+                    self._zero_initialized[p] = True
+        bnd = _none_to_empty(pid, boundaries, self.num_parts)
+        with torch.cuda.stream(stream):
+            _C.scatter_partitions(pid, gpu_source, self._tensors, bnd)
+
+    # ------------------------------------------------------------- utilities
+
+    def initialize_zeros(self, lazy: bool = False) -> None:
+        if lazy:
+            self.release_all()
+            return
+        for pid in range(self.num_parts):
+            self.allocate(pid).zero_()
+            self._zero_initialized[pid] = True
+
+    def reset(self) -> None:
+        self.initialize_zeros()
+
+    def storage_exists(self, pid: int) -> bool:
+        return False

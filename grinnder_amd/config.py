@@ -1,0 +1,60 @@
+"""GriNNderConfig: the reference's configuration dataclass (grinnder/config.py:17-67).
+
+Same field names, defaults and environment override, so user code written for
+the reference constructs it unchanged.  Fields that select subsystems outside
+this package's scope (the NVMe storage tier and its partition-LRU cache) are
+accepted and validated by the Trainer.
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, field
+from typing import Any, Dict, Literal
+
+
+def _default_threads() -> int:
+    env_value = os.environ.get("GRINNDER_PARTITION_THREADS")
+    if env_value:
+        return max(1, int(env_value))
+    return os.cpu_count() or 1
+
+
+@dataclass
+class GriNNderConfig:
+    """Training configuration.
+
+    mode: 'hongtu' keeps a CPU snapshot of each gathered input for the
+        backward recompute; 'grinnder' re-gathers it from the host buffers
+        (scattered checkpointing, no snapshot redundancy).
+    num_parts / partitioner / partitioner_kwargs: graph partitioning.
+    cache_mode: 'auto' | 'lru_layer' | 'partition_lru' (host cache policy of
+        the storage tier; this package keeps every layer host-resident, which
+        is what 'auto' resolves to when the working set fits).
+    device: GPU device string; pool_size: transfer double-buffering depth.
+    """
+
+    mode: Literal["hongtu", "grinnder"] = "grinnder"
+
+    num_parts: int = 8
+    partitioner: Literal["grinnder", "spinner"] = "grinnder"
+    partitioner_kwargs: Dict[str, Any] = field(
+        default_factory=lambda: {
+            "capacity": 1.1,
+            "beta": 1.0,
+            "max_iter": 50,
+            "num_threads": _default_threads(),
+        }
+    )
+
+    storage_dir: str = "/pci5_nvme/grinnder"
+
+    cache_mode: Literal["auto", "lru_layer", "partition_lru"] = "auto"
+    host_memory_budget_gb: float = 0
+    runtime_safety_margin_gb: float = 0.0
+
+    device: str = "cuda:0"
+    pool_size: int = 2
+    preprocess_workers: int = field(default_factory=_default_threads)
+
+    num_gpus: int = 1

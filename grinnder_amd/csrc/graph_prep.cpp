@@ -1,0 +1,353 @@
+// Host-side partition bookkeeping and aggregation-plan preparation.
+//
+// Everything here is integer work that must be bit-exact with the reference
+// (build_subgraph, boundary ordering) or deterministic by construction
+// (CSR->CSC transpose, work plans).  It runs once per partition adjacency,
+// never inside the training loop.
+#include <algorithm>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "gr_internal.h"
+
+namespace {
+
+// Dense old-id -> new-id map used by the subgraph extraction.  The reference
+// uses std::unordered_map (csrc/cpu/subgraph.cpp:27); a dense array gives the
+// same mapping (same insertion order, last assignment wins for repeated
+// seeds) with O(1) loads and no hashing.
+struct DenseMap {
+  std::vector<int64_t> slot;
+  explicit DenseMap(int64_t n) : slot(static_cast<size_t>(n), -1) {}
+};
+
+}  // namespace
+
+extern "C" int gr_build_subgraph(const int64_t* rowptr, const int64_t* col,
+                                 const void* value, int64_t value_elem_size,
+                                 int64_t num_rows, const int64_t* idx,
+                                 int64_t n_idx, int32_t bipartite,
+                                 int64_t* out_rowptr, int64_t* out_col,
+                                 void* out_value, int64_t* out_n_id,
+                                 int64_t* out_nnz, int64_t* out_num_nodes) {
+  gr::clear_error();
+  GR_REQUIRE(rowptr != nullptr && num_rows >= 0 && n_idx >= 0,
+             "build_subgraph: invalid rowptr/num_rows/n_idx");
+  GR_REQUIRE(n_idx == 0 || idx != nullptr, "build_subgraph: idx is NULL");
+  GR_REQUIRE(out_nnz != nullptr && out_num_nodes != nullptr,
+             "build_subgraph: out_nnz/out_num_nodes are NULL");
+  if (value != nullptr) {
+    GR_REQUIRE(value_elem_size == 1 || value_elem_size == 2 ||
+                   value_elem_size == 4 || value_elem_size == 8,
+               "build_subgraph: value element size %lld unsupported",
+               (long long)value_elem_size);
+  }
+
+  // Pass 0: validate seeds, count edges, find the id range to map.
+  int64_t nnz = 0;
+  int64_t max_id = num_rows - 1;
+  for (int64_t i = 0; i < n_idx; ++i) {
+    const int64_t v = idx[i];
+    GR_REQUIRE(v >= 0 && v < num_rows, "build_subgraph: seed %lld out of range [0, %lld)",
+               (long long)v, (long long)num_rows);
+    const int64_t b = rowptr[v], e = rowptr[v + 1];
+    GR_REQUIRE(b >= 0 && e >= b, "build_subgraph: rowptr not monotone at row %lld",
+               (long long)v);
+    nnz += e - b;
+    if (col != nullptr) {
+      for (int64_t j = b; j < e; ++j) {
+        GR_REQUIRE(col[j] >= 0, "build_subgraph: negative column %lld", (long long)col[j]);
+        max_id = std::max(max_id, col[j]);
+      }
+    }
+  }
+  GR_REQUIRE(nnz == 0 || col != nullptr, "build_subgraph: col is NULL");
+
+  DenseMap map(max_id + 1);
+  for (int64_t i = 0; i < n_idx; ++i) map.slot[idx[i]] = i;
+
+  const bool fill = out_col != nullptr;
+  if (fill) {
+    GR_REQUIRE(out_rowptr != nullptr && out_n_id != nullptr,
+               "build_subgraph: output arrays are NULL");
+    GR_REQUIRE(value == nullptr || out_value != nullptr,
+               "build_subgraph: out_value is NULL while value is given");
+  }
+
+  // Pass 1: row-major scan; unseen neighbours get the next id in first-seen
+  // order (csrc/cpu/subgraph.cpp:56-75 and :79-98).
+  int64_t n_new = 0;
+  int64_t offset = 0;
+  if (fill) out_rowptr[0] = 0;
+  const size_t esz = static_cast<size_t>(value_elem_size);
+  for (int64_t i = 0; i < n_idx; ++i) {
+    const int64_t v = idx[i];
+    for (int64_t j = rowptr[v]; j < rowptr[v + 1]; ++j) {
+      const int64_t w = col[j];
+      int64_t id = map.slot[w];
+      if (id < 0) {
+        id = n_idx + n_new;
+        map.slot[w] = id;
+        if (fill) out_n_id[id] = w;
+        ++n_new;
+      }
+      if (fill) {
+        out_col[offset] = id;
+        if (value != nullptr) {
+          std::memcpy(static_cast<char*>(out_value) + offset * esz,
+                      static_cast<const char*>(value) + j * esz, esz);
+        }
+      }
+      ++offset;
+    }
+    if (fill) out_rowptr[i + 1] = offset;
+  }
+
+  *out_nnz = nnz;
+  *out_num_nodes = n_idx + n_new;
+  if (!fill) return GR_OK;
+
+  for (int64_t i = 0; i < n_idx; ++i) out_n_id[i] = idx[i];
+  // Non-bipartite: boundary nodes get empty rows (subgraph.cpp:102-107).
+  if (!bipartite) {
+    for (int64_t k = 0; k < n_new; ++k) out_rowptr[n_idx + 1 + k] = nnz;
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_partition_boundaries(int32_t pid, int32_t num_parts,
+                                       const int64_t* ptr, int64_t batch_size,
+                                       const int64_t* halo_ids, int64_t n_halo,
+                                       int64_t* col, int64_t nnz,
+                                       int64_t* boundary_flat,
+                                       int64_t* boundary_lens) {
+  gr::clear_error();
+  GR_REQUIRE(num_parts >= 1 && pid >= 0 && pid < num_parts && ptr != nullptr,
+             "partition_boundaries: bad pid %d / num_parts %d", pid, num_parts);
+  GR_REQUIRE(boundary_lens != nullptr, "partition_boundaries: boundary_lens is NULL");
+  GR_REQUIRE(n_halo == 0 || (halo_ids != nullptr && boundary_flat != nullptr),
+             "partition_boundaries: halo arrays are NULL");
+  for (int32_t p = 0; p < num_parts; ++p) {
+    GR_REQUIRE(ptr[p + 1] >= ptr[p], "partition_boundaries: ptr not monotone");
+  }
+
+  // Owner of each halo node (partitions are contiguous id ranges).
+  std::vector<int32_t> owner(static_cast<size_t>(n_halo));
+  std::vector<int64_t> count(static_cast<size_t>(num_parts), 0);
+  for (int64_t k = 0; k < n_halo; ++k) {
+    const int64_t g = halo_ids[k];
+    GR_REQUIRE(g >= ptr[0] && g < ptr[num_parts],
+               "partition_boundaries: halo node %lld outside all partitions", (long long)g);
+    const int64_t* it = std::upper_bound(ptr, ptr + num_parts + 1, g);
+    const int32_t p = static_cast<int32_t>((it - ptr) - 1);
+    GR_REQUIRE(p != pid, "partition_boundaries: halo node %lld lies in partition %d itself",
+               (long long)g, pid);
+    owner[k] = p;
+    ++count[p];
+  }
+
+  // Stable grouping by owner ascending (partition.py:201-212): discovery
+  // order is kept inside each group.
+  std::vector<int64_t> start(static_cast<size_t>(num_parts), 0);
+  int64_t run = 0;
+  for (int32_t p = 0; p < num_parts; ++p) {
+    start[p] = run;
+    run += count[p];
+    boundary_lens[p] = count[p];
+  }
+  std::vector<int64_t> new_pos(static_cast<size_t>(n_halo));
+  for (int64_t k = 0; k < n_halo; ++k) {
+    const int32_t p = owner[k];
+    const int64_t pos = start[p]++;
+    new_pos[k] = pos;
+    boundary_flat[pos] = halo_ids[k] - ptr[p];
+  }
+
+  // Column remap: discovery order -> partition order (partition.py:213-225).
+  if (n_halo > 0 && col != nullptr) {
+    for (int64_t e = 0; e < nnz; ++e) {
+      const int64_t c = col[e];
+      if (c >= batch_size) {
+        GR_REQUIRE(c - batch_size < n_halo, "partition_boundaries: column %lld out of range",
+                   (long long)c);
+        col[e] = batch_size + new_pos[c - batch_size];
+      }
+    }
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_csr_transpose(const int64_t* rowptr, const int64_t* col,
+                                const float* val, int64_t rows, int64_t cols,
+                                int64_t* colptr, int32_t* row_idx, float* val_t,
+                                int32_t* perm) {
+  gr::clear_error();
+  GR_REQUIRE(rowptr != nullptr && colptr != nullptr && rows >= 0 && cols >= 0,
+             "csr_transpose: invalid arguments");
+  const int64_t nnz = rowptr[rows];
+  GR_REQUIRE(nnz == 0 || (col != nullptr && row_idx != nullptr),
+             "csr_transpose: col/row_idx are NULL");
+  GR_REQUIRE(rows <= INT32_MAX && nnz <= INT32_MAX,
+             "csr_transpose: rows/nnz exceed int32 (%lld/%lld)", (long long)rows,
+             (long long)nnz);
+
+  std::vector<int64_t> next(static_cast<size_t>(cols) + 1, 0);
+  for (int64_t e = 0; e < nnz; ++e) {
+    const int64_t c = col[e];
+    GR_REQUIRE(c >= 0 && c < cols, "csr_transpose: column %lld out of range [0, %lld)",
+               (long long)c, (long long)cols);
+    ++next[c + 1];
+  }
+  for (int64_t c = 0; c < cols; ++c) next[c + 1] += next[c];
+  std::memcpy(colptr, next.data(), sizeof(int64_t) * (static_cast<size_t>(cols) + 1));
+
+  // Stable placement: CSR order is row-major, so each column receives its
+  // entries in (row, position) order.
+  const bool with_val = val != nullptr && val_t != nullptr;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) {
+      const int64_t dst = next[col[e]]++;
+      row_idx[dst] = static_cast<int32_t>(r);
+      if (with_val) val_t[dst] = val[e];
+      if (perm != nullptr) perm[dst] = static_cast<int32_t>(e);
+    }
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len,
+                            int32_t* units, int64_t* n_units, int32_t* fixups,
+                            int64_t* n_fix, int64_t* n_slots) {
+  gr::clear_error();
+  GR_REQUIRE(rowptr != nullptr && rows >= 0 && seg_len > 0,
+             "spmm_plan: invalid arguments");
+  GR_REQUIRE(n_units != nullptr && n_fix != nullptr && n_slots != nullptr,
+             "spmm_plan: count outputs are NULL");
+  GR_REQUIRE(rows <= INT32_MAX && rowptr[rows] <= INT32_MAX,
+             "spmm_plan: rows/nnz exceed int32");
+
+  int64_t nu = 0, nf = 0, ns = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t len = rowptr[r + 1] - rowptr[r];
+    GR_REQUIRE(len >= 0, "spmm_plan: rowptr not monotone at row %lld", (long long)r);
+    if (len > seg_len) {
+      const int64_t k = (len + seg_len - 1) / seg_len;
+      nu += k;
+      ns += k;
+      ++nf;
+    } else {
+      ++nu;
+    }
+  }
+  *n_units = nu;
+  *n_fix = nf;
+  *n_slots = ns;
+  if (units == nullptr) return GR_OK;
+  GR_REQUIRE(nf == 0 || fixups != nullptr, "spmm_plan: fixups is NULL");
+
+  int64_t u = 0, f = 0, slot = 0;
+  // Split rows first.
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t b = rowptr[r], e = rowptr[r + 1];
+    if (e - b <= seg_len) continue;
+    fixups[3 * f + 0] = static_cast<int32_t>(r);
+    fixups[3 * f + 1] = static_cast<int32_t>(slot);
+    int32_t k = 0;
+    for (int64_t s = b; s < e; s += seg_len, ++k) {
+      units[4 * u + 0] = static_cast<int32_t>(r);
+      units[4 * u + 1] = static_cast<int32_t>(s);
+      units[4 * u + 2] = static_cast<int32_t>(std::min<int64_t>(s + seg_len, e));
+      units[4 * u + 3] = static_cast<int32_t>(slot++);
+      ++u;
+    }
+    fixups[3 * f + 2] = k;
+    ++f;
+  }
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t b = rowptr[r], e = rowptr[r + 1];
+    if (e - b > seg_len) continue;
+    units[4 * u + 0] = static_cast<int32_t>(r);
+    units[4 * u + 1] = static_cast<int32_t>(b);
+    units[4 * u + 2] = static_cast<int32_t>(e);
+    units[4 * u + 3] = -1;
+    ++u;
+  }
+  return GR_OK;
+}
+
+namespace {
+
+// SplitMix64 finaliser (Steele, Lea, Flood 2014): a bijective 64-bit mixer.
+inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+}  // namespace
+
+extern "C" int gr_rmat_sample(uint64_t seed, int32_t scale, double a, double b,
+                              double c, int64_t first, int64_t n, int64_t* src,
+                              int64_t* dst, int32_t nthreads) {
+  gr::clear_error();
+  GR_REQUIRE(scale >= 1 && scale <= 40, "rmat_sample: scale %d out of range", scale);
+  GR_REQUIRE(a >= 0 && b >= 0 && c >= 0 && a + b + c <= 1.0,
+             "rmat_sample: invalid probabilities");
+  GR_REQUIRE(n >= 0 && first >= 0, "rmat_sample: invalid range");
+  GR_REQUIRE(n == 0 || (src != nullptr && dst != nullptr), "rmat_sample: NULL outputs");
+  // Quadrant thresholds on a 32-bit uniform integer.
+  const double two32 = 4294967296.0;
+  const uint64_t ta = static_cast<uint64_t>(a * two32);
+  const uint64_t tab = static_cast<uint64_t>((a + b) * two32);
+  const uint64_t tabc = static_cast<uint64_t>((a + b + c) * two32);
+  const uint64_t key = mix64(seed ^ 0x5851F42D4C957F2Dull);
+
+  auto work = [&](int64_t lo, int64_t hi) {
+    for (int64_t i = lo; i < hi; ++i) {
+      const uint64_t ctr = static_cast<uint64_t>(first + i);
+      uint64_t s = 0, d = 0;
+      uint64_t bits = 0;
+      for (int32_t lvl = 0; lvl < scale; ++lvl) {
+        uint32_t u;
+        if ((lvl & 1) == 0) {
+          bits = mix64(key + 0x9E3779B97F4A7C15ull * (ctr * 32u + static_cast<uint64_t>(lvl >> 1) + 1u));
+          u = static_cast<uint32_t>(bits);
+        } else {
+          u = static_cast<uint32_t>(bits >> 32);
+        }
+        uint64_t sb, db;
+        if (u < ta) {
+          sb = 0; db = 0;
+        } else if (u < tab) {
+          sb = 0; db = 1;
+        } else if (u < tabc) {
+          sb = 1; db = 0;
+        } else {
+          sb = 1; db = 1;
+        }
+        s = (s << 1) | sb;
+        d = (d << 1) | db;
+      }
+      src[i] = static_cast<int64_t>(s);
+      dst[i] = static_cast<int64_t>(d);
+    }
+  };
+
+  int32_t nt = nthreads > 0 ? nthreads : static_cast<int32_t>(std::thread::hardware_concurrency());
+  if (nt < 1) nt = 1;
+  if (n < (int64_t)1 << 16) nt = 1;
+  if (nt == 1) {
+    work(0, n);
+    return GR_OK;
+  }
+  std::vector<std::thread> pool;
+  const int64_t chunk = (n + nt - 1) / nt;
+  for (int32_t t = 0; t < nt; ++t) {
+    const int64_t lo = t * chunk, hi = std::min<int64_t>(n, lo + chunk);
+    if (lo >= hi) break;
+    pool.emplace_back(work, lo, hi);
+  }
+  for (auto& th : pool) th.join();
+  return GR_OK;
+}

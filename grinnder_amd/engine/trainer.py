@@ -1,0 +1,400 @@
+"""Trainer: layer-wise, partition-wise full-graph training (grinnder/engine/trainer.py).
+
+The algorithm is the reference's (Algorithm 1 of the GriNNder paper as
+implemented in trainer.py:334-1138):
+
+forward, per layer l, per partition p (double-buffered):
+    gather x = [h_l[p] | halo rows from other partitions] host -> device,
+    out = checkpoint(GradOffload(x) -> model.forward_layer(l, x, adj_p)),
+    D2H out into the host buffer h_{l+1}[p], free device memory;
+loss: upload each partition's logits, cross-entropy (sum) on its train rows;
+backward, last layer first, per partition:
+    re-gather x (grinnder mode) or restore its snapshot (hongtu mode),
+    backpropagate (the checkpoint recomputes the layer), GradOffload
+    scatter-adds dL/dx into the host gradient buffer of layer l (halo rows go
+    to their owning partitions), and the next layer down uploads that buffer
+    as the gradient of its outputs;
+finally grads /= number of training nodes, optimizer step.
+
+With one partition the reference's fast path is used (trainer.py:418-471):
+plain full-graph forward/backward.  Here its inputs (features, labels, masks,
+adjacency plans) stay resident in HBM across epochs.
+
+Differences by design: host buffers are pinned so halo traffic moves by
+device kernels; waits are per stream, not device-wide; the NVMe storage tier
+and its partition-LRU cache are out of scope (every layer stays in host RAM,
+which is what the reference's 'auto' cache resolves to when it fits).
+"""
+
+from __future__ import annotations
+
+from typing import Dict, List, Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+from torch.utils.checkpoint import checkpoint
+
+from grinnder_amd.autograd.checkpoint import HongtuCheckpoint, ScatteredCheckpoint
+from grinnder_amd.autograd.grad_offload import GradOffload
+from grinnder_amd.buffer.device import DeviceBuffer
+from grinnder_amd.buffer.host import HostBuffer
+from grinnder_amd.config import GriNNderConfig
+from grinnder_amd.data.graph import PartitionedGraph
+from grinnder_amd.engine.streams import StreamManager
+from grinnder_amd.nn.base import GriNNderModel
+from grinnder_amd.utils import compute_micro_f1
+
+
+class Trainer:
+    def __init__(self, model: GriNNderModel, graph: PartitionedGraph, config: GriNNderConfig,
+                 partition_range: Optional[tuple] = None):
+        if config.mode not in ("hongtu", "grinnder"):
+            raise ValueError(f"unknown mode {config.mode!r}")
+        if config.cache_mode not in ("auto", "lru_layer", "partition_lru"):
+            raise ValueError(f"Unsupported cache mode {config.cache_mode!r}")
+        if config.cache_mode == "partition_lru":
+            raise NotImplementedError(
+                "cache_mode='partition_lru' needs the NVMe storage tier, which is outside "
+                "this package's scope")
+        if config.pool_size < 1:
+            raise ValueError("pool_size must be >= 1")
+        self.model = model
+        self.graph = graph
+        self.config = config
+        self.device = torch.device(config.device)
+        self.cache = None
+        if partition_range is not None:
+            self._pid_start, self._pid_end = partition_range
+        else:
+            self._pid_start, self._pid_end = 0, graph.num_parts
+        self._my_pids = list(range(self._pid_start, self._pid_end))
+
+        dims = model.layer_dims()
+        if len(dims) != model.num_layers + 1:
+            raise ValueError("layer_dims() must have num_layers + 1 entries")
+        L, P = model.num_layers, graph.num_parts
+        self.streams = StreamManager(pool_size=config.pool_size, device=config.device)
+        self._fast = graph.num_parts == 1 and partition_range is None
+
+        self.host_features: List[HostBuffer] = []
+        self.host_gradients: List[Optional[HostBuffer]] = [None]
+        self.device_features: List[DeviceBuffer] = []
+        self.device_gradients: List[Optional[DeviceBuffer]] = [None]
+        self.activations: List[List[Optional[Tensor]]] = [[None] * P for _ in range(L)]
+        self._pid_to_loss_idx: Dict[int, int] = {}
+        self._resident: Dict[str, Tensor] = {}
+        if not self._fast:
+            for l in range(L + 1):
+                self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
+                                                     file_prefix=f"feat_l{l}", pin_memory=True))
+            for l in range(1, L):
+                self.host_gradients.append(HostBuffer(P, graph.partition_sizes, dims[l],
+                                                      file_prefix=f"grad_l{l}",
+                                                      pin_memory=True))
+            for l in range(L):
+                self.device_features.append(DeviceBuffer(P, graph.expanded_sizes, dims[l],
+                                                         device=config.device))
+            for l in range(1, L):
+                self.device_gradients.append(DeviceBuffer(P, graph.partition_sizes, dims[l],
+                                                          device=config.device))
+            for pid in range(P):
+                self.host_features[0][pid].copy_(graph.partition_features(pid))
+
+    # ------------------------------------------------------------ public API
+
+    def reset_epoch(self) -> None:
+        for l in range(1, len(self.host_features)):
+            self.host_features[l].reset()
+        for buf in self.host_gradients:
+            if buf is not None:
+                buf.reset()
+        for buf in self.device_features:
+            buf.reset()
+        for buf in self.device_gradients:
+            if buf is not None:
+                buf.reset()
+        for acts in self.activations:
+            for i in range(len(acts)):
+                acts[i] = None
+
+    def train_epoch(self, optimizer: torch.optim.Optimizer,
+                    criterion: torch.nn.Module) -> Dict[str, float]:
+        self.model.train()
+        if self._fast:
+            return self._train_fast(optimizer)
+        self.reset_epoch()
+        optimizer.zero_grad()
+        for l in range(self.model.num_layers):
+            self._forward_layer(l)
+        losses, metrics = self._compute_losses()
+        self._backward_last_layer(losses)
+        for l in reversed(range(self.model.num_layers - 1)):
+            self._backward_layer(l)
+        n_train = metrics.get("_n_train", 1)
+        if n_train > 0:
+            for p in self.model.parameters():
+                if p.grad is not None:
+                    p.grad.div_(n_train)
+        optimizer.step()
+        return metrics
+
+    @torch.no_grad()
+    def evaluate(self, criterion: torch.nn.Module) -> Dict[str, float]:
+        self.model.eval()
+        if self._fast:
+            out = self._fast_logits()
+            _, metrics = self._fast_metrics(out)
+            return metrics
+        self.reset_epoch()
+        for l in range(self.model.num_layers):
+            self._forward_layer(l)
+        _, metrics = self._compute_losses()
+        return metrics
+
+    # ------------------------------------------------ single-partition path
+
+    def _res(self, name: str, make) -> Tensor:
+        t = self._resident.get(name)
+        if t is None:
+            t = make()
+            self._resident[name] = t
+        return t
+
+    def _fast_logits(self) -> Tensor:
+        g = self.graph
+        x = self._res("x", lambda: g.partition_features(0).to(self.device))
+        adj = g.adjacency(0)
+        out = x
+        for l in range(self.model.num_layers):
+            out = self.model.forward_layer(l, out, adj)
+        return out
+
+    def _fast_metrics(self, out: Tensor):
+        g = self.graph
+        y = self._res("y", lambda: g.partition_labels(0).to(self.device))
+        train = self._res("train", lambda: g.partition_train_mask(0).to(self.device))
+        val = self._res("val", lambda: g.partition_val_mask(0).to(self.device))
+        test = self._res("test", lambda: g.partition_test_mask(0).to(self.device))
+        n_train = self._res("n_train", lambda: torch.tensor(int(train.sum())))
+        n_train = int(n_train)
+        if n_train > 0:
+            loss = F.cross_entropy(out[train], y[train], reduction="mean")
+            loss_value = float(loss.item())
+        else:
+            loss = out.sum() * 0.0
+            loss_value = 0.0
+        metrics = {
+            "loss": loss_value,
+            "val_acc": compute_micro_f1(out, y, val),
+            "test_acc": compute_micro_f1(out, y, test),
+            "_n_train": n_train,
+        }
+        return loss, metrics
+
+    def _train_fast(self, optimizer) -> Dict[str, float]:
+        optimizer.zero_grad()
+        out = self._fast_logits()
+        loss, metrics = self._fast_metrics(out)
+        loss.backward()
+        optimizer.step()
+        return metrics
+
+    # ------------------------------------------------- partitioned helpers
+
+    def _gather(self, layer: int, pid: int, stream: torch.cuda.Stream) -> None:
+        with torch.cuda.stream(self.streams.compute):
+            self.device_features[layer].async_gather(
+                pid, self.host_features[layer], self.graph.boundaries[pid], stream)
+
+    def _upload_grad(self, layer: int, pid: int, stream: torch.cuda.Stream) -> None:
+        buf = self.device_gradients[layer]
+        if buf is None or self.host_gradients[layer] is None:
+            return
+        with torch.cuda.stream(self.streams.compute):
+            buf.allocate(pid)
+            self.host_gradients[layer].async_upload(pid, buf[pid], stream)
+
+    def _upoffload_wrapper(self, layer_id: int, pid: int, x: Tensor) -> Tensor:
+        x = GradOffload.apply(
+            x, layer_id, pid,
+            self.host_gradients[layer_id] if layer_id > 0 else None,
+            self.graph.boundaries[pid],
+            self.streams.d2h[pid % self.config.pool_size],
+            self.streams.compute,
+        )
+        return self.model.forward_layer(layer_id, x, self.graph.adjacency(pid))
+
+    def _checkpointed(self, layer: int, pid: int, slot: int) -> Tensor:
+        x = self.device_features[layer][pid]
+        x.requires_grad_(True)
+        if self.config.mode == "hongtu":
+            hooks = HongtuCheckpoint(pid, self.device_features[layer])
+        else:
+            hooks = ScatteredCheckpoint(pid, self.device_features[layer],
+                                        self.streams.act_h2d[slot])
+        with hooks:
+            return checkpoint(self._upoffload_wrapper, layer, pid, x, use_reentrant=True)
+
+    @staticmethod
+    def _free(t: Optional[Tensor]) -> None:
+        if t is not None:
+            t.untyped_storage().resize_(0)
+
+    # ------------------------------------------------------------- forward
+
+    def _forward_layer(self, layer: int) -> None:
+        pids, pool, s = self._my_pids, self.config.pool_size, self.streams
+        if not pids:
+            return
+        self._gather(layer, pids[0], s.h2d[0])
+        for i, pid in enumerate(pids):
+            k = i % pool
+            self.device_features[layer].h2d_synchronize(s.h2d[k])
+            s.compute.wait_stream(s.h2d[k])
+            with torch.cuda.stream(s.compute):
+                if i + 1 < len(pids) and pool > 1:
+                    self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
+                out = self._checkpointed(layer, pid, k)
+                self.activations[layer][pid] = out
+                self.host_features[layer + 1].async_fill(pid, out, s.d2h[k])
+                self.device_features[layer].release(pid)
+                if i > 0 and pool > 1:
+                    prev, pk = pids[i - 1], (i - 1) % pool
+                    self.host_features[layer + 1].d2h_synchronize(s.d2h[pk])
+                    self._free(self.activations[layer][prev])
+            if pool == 1:
+                self.host_features[layer + 1].d2h_synchronize(s.d2h[0])
+                self._free(self.activations[layer][pid])
+                if i + 1 < len(pids):
+                    self._gather(layer, pids[i + 1], s.h2d[0])
+        if pool > 1:
+            last = (len(pids) - 1) % pool
+            self.host_features[layer + 1].d2h_synchronize(s.d2h[last])
+            self._free(self.activations[layer][pids[-1]])
+
+    # ---------------------------------------------------------------- loss
+
+    def _compute_losses(self):
+        pids, pool, s = self._my_pids, self.config.pool_size, self.streams
+        last = self.model.num_layers - 1
+        losses: List[Tensor] = []
+        self._pid_to_loss_idx = {}
+        total_loss, n_train = 0.0, 0
+        val_correct = val_n = test_correct = test_n = 0.0
+        if not pids:
+            return losses, {"loss": 0.0, "val_acc": 0.0, "test_acc": 0.0, "_n_train": 0}
+
+        def upload(pid: int, stream) -> None:
+            act = self.activations[last][pid]
+            with torch.cuda.stream(s.compute):
+                act.untyped_storage().resize_(act.numel() * act.element_size())
+            self.host_features[-1].async_upload(pid, act, stream)
+
+        with torch.cuda.stream(s.compute):
+            upload(pids[0], s.h2d[0])
+            for i, pid in enumerate(pids):
+                k = i % pool
+                self.host_features[-1].h2d_synchronize(s.h2d[k])
+                s.compute.wait_stream(s.h2d[k])
+                if i + 1 < len(pids):
+                    upload(pids[i + 1], s.h2d[(i + 1) % pool])
+                out = self.activations[last][pid]
+                y = self.graph.partition_labels(pid).to(self.device, non_blocking=False)
+                train = self.graph.partition_train_mask(pid).to(self.device)
+                val = self.graph.partition_val_mask(pid)
+                test = self.graph.partition_test_mask(pid)
+                n_part = int(self.graph.partition_train_mask(pid).sum())
+                if n_part > 0:
+                    loss = F.cross_entropy(out[train], y[train], reduction="sum")
+                    total_loss += loss.item()
+                    n_train += n_part
+                else:
+                    loss = out.sum() * 0.0
+                self._pid_to_loss_idx[pid] = len(losses)
+                losses.append(loss)
+                with torch.no_grad():
+                    nv, nt = int(val.sum()), int(test.sum())
+                    if nv > 0:
+                        val_correct += compute_micro_f1(out, y, val) * nv
+                        val_n += nv
+                    if nt > 0:
+                        test_correct += compute_micro_f1(out, y, test) * nt
+                        test_n += nt
+                self._free(out)
+        metrics = {
+            "loss": total_loss / max(n_train, 1),
+            "val_acc": val_correct / max(val_n, 1),
+            "test_acc": test_correct / max(test_n, 1),
+            "_n_train": n_train,
+        }
+        return losses, metrics
+
+    # ------------------------------------------------------------ backward
+
+    def _regathers(self, layer: int) -> bool:
+        return self.config.mode == "grinnder"
+
+    def _backward_last_layer(self, losses: List[Tensor]) -> None:
+        layer = self.model.num_layers - 1
+        self._backward_pass(layer, lambda pid: losses[self._pid_to_loss_idx[pid]].backward())
+        for i in range(len(losses)):
+            losses[i] = None
+
+    def _backward_layer(self, layer: int) -> None:
+        def run(pid: int) -> None:
+            act = self.activations[layer][pid]
+            if act is None or act.grad_fn is None:
+                return
+            gbuf = self.device_gradients[layer + 1]
+            if gbuf is not None and gbuf.is_allocated(pid):
+                act.backward(gbuf[pid])
+            else:
+                act.backward()
+        self._backward_pass(layer, run, upload_grad=True)
+
+    def _backward_pass(self, layer: int, run, upload_grad: bool = False) -> None:
+        """Per partition: re-gather x_layer, upload dL/d(out) if needed, backprop."""
+        pids, pool, s = self._my_pids, self.config.pool_size, self.streams
+        if not pids:
+            return
+        if self.host_gradients[layer] is not None:
+            self.host_gradients[layer].initialize_zeros()
+        regather = self._regathers(layer)
+        if regather:
+            self._gather(layer, pids[0], s.act_h2d[0])
+        if upload_grad:
+            self._upload_grad(layer + 1, pids[0], s.h2d[0])
+        for i, pid in enumerate(pids):
+            k = i % pool
+            if regather:
+                self.device_features[layer].h2d_synchronize(s.act_h2d[k])
+            if upload_grad and self.host_gradients[layer + 1] is not None:
+                self.host_gradients[layer + 1].h2d_synchronize(s.h2d[k])
+            s.compute.wait_stream(s.act_h2d[k])
+            s.compute.wait_stream(s.h2d[k])
+            with torch.cuda.stream(s.compute):
+                if i + 1 < len(pids) and pool > 1:
+                    if regather:
+                        self._gather(layer, pids[i + 1], s.act_h2d[(i + 1) % pool])
+                    if upload_grad:
+                        self._upload_grad(layer + 1, pids[i + 1], s.h2d[(i + 1) % pool])
+                run(pid)
+                s.compute.synchronize()
+                act = self.activations[layer][pid]
+                if act is not None:
+                    self._free(act)
+                    act.grad = None
+                    self.activations[layer][pid] = None
+                gbuf = self.device_gradients[layer + 1] if layer + 1 < len(
+                    self.device_gradients) else None
+                if gbuf is not None:
+                    gbuf.release(pid)
+                if self.host_gradients[layer] is not None:
+                    self.host_gradients[layer].d2h_synchronize(s.d2h[pid % pool])
+                self.device_features[layer].release(pid)
+            if pool == 1 and i + 1 < len(pids):
+                if regather:
+                    self._gather(layer, pids[i + 1], s.act_h2d[0])
+                if upload_grad:
+                    self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])

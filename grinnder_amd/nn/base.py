@@ -1,0 +1,35 @@
+"""GriNNderModel: per-layer model interface (grinnder/nn/base.py:11-74)."""
+
+from __future__ import annotations
+
+from abc import abstractmethod
+from typing import List
+
+import torch
+from torch import Tensor
+
+
+class GriNNderModel(torch.nn.Module):
+    """Base class of models trained layer-wise and partition-wise by the Trainer.
+
+    Subclasses implement ``forward_layer(layer, x, adj)`` — x holds the E
+    gathered source rows of one partition ([intra | halo]); the result holds
+    its B destination rows — and ``layer_dims()`` ([in, hidden..., out],
+    length num_layers + 1).
+    """
+
+    def __init__(self, num_layers: int):
+        super().__init__()
+        self._num_layers = num_layers
+
+    @property
+    def num_layers(self) -> int:
+        return self._num_layers
+
+    @abstractmethod
+    def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
+        ...
+
+    @abstractmethod
+    def layer_dims(self) -> List[int]:
+        ...

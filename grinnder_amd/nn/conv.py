@@ -1,0 +1,122 @@
+"""GCNConv / GATConv layers backed by the HIP aggregation kernels.
+
+Parameter names and shapes follow PyG (the reference instantiates
+``GCNConv(in, out, normalize=False)`` and ``GATConv(in, out, heads,
+concat, add_self_loops=False)``, grinnder/nn/gcn.py:53-56 and
+grinnder/nn/gat.py:54-61), so state_dicts are interchangeable:
+``lin.weight``, ``bias``, ``att_src``, ``att_dst``.  PyG < 2.5 named the GAT
+projection ``lin_src``/``lin_dst``; both spellings load.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Tuple, Union
+
+import torch
+from torch import Tensor
+from torch.nn import Linear, Module, Parameter
+
+from grinnder_amd.aggregation import gat_attention, gcn_aggregate
+from grinnder_amd.data.adjacency import Adjacency
+
+
+def glorot_(t: Tensor) -> Tensor:
+    """PyG's glorot: U(-a, a), a = sqrt(6 / (size(-2) + size(-1)))."""
+    a = math.sqrt(6.0 / (t.size(-2) + t.size(-1)))
+    with torch.no_grad():
+        return t.uniform_(-a, a)
+
+
+class GCNConv(Module):
+    """out = A · (x Wᵀ) + b with the adjacency's precomputed GCN weights.
+
+    Only ``normalize=False`` is supported: the normalisation is computed once
+    on the full graph and stored as adjacency values, as in the reference.
+    """
+
+    def __init__(self, in_channels: int, out_channels: int, normalize: bool = False,
+                 bias: bool = True):
+        super().__init__()
+        if normalize:
+            raise ValueError("GCNConv expects precomputed full-graph normalisation "
+                             "(normalize=False)")
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.lin = Linear(in_channels, out_channels, bias=False)
+        self.bias = Parameter(torch.empty(out_channels)) if bias else None
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        glorot_(self.lin.weight)
+        if self.bias is not None:
+            torch.nn.init.zeros_(self.bias)
+
+    def forward(self, x: Tensor, adj: Adjacency) -> Tensor:
+        return gcn_aggregate(self.lin(x), adj, self.bias)
+
+    def __repr__(self) -> str:
+        return f"{self.__class__.__name__}({self.in_channels}, {self.out_channels})"
+
+
+class GATConv(Module):
+    """Graph attention over a bipartite partition adjacency (PyG GATConv semantics).
+
+    Called as ``conv((x, x[:B]), adj)``; the destination features must be the
+    first B rows of the source features (one shared projection), which is how
+    the reference's GAT.forward_layer calls it.
+    """
+
+    def __init__(self, in_channels: int, out_channels: int, heads: int = 1,
+                 concat: bool = True, negative_slope: float = 0.2, dropout: float = 0.0,
+                 add_self_loops: bool = True, bias: bool = True):
+        super().__init__()
+        if add_self_loops:
+            raise ValueError("bipartite partition adjacencies already contain self-loops; "
+                             "use add_self_loops=False")
+        if negative_slope != 0.2:
+            raise ValueError("the attention kernels implement negative_slope=0.2")
+        if dropout != 0.0:
+            raise ValueError("attention dropout is not supported (the reference uses 0)")
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.heads = heads
+        self.concat = concat
+        self.lin = Linear(in_channels, heads * out_channels, bias=False)
+        self.att_src = Parameter(torch.empty(1, heads, out_channels))
+        self.att_dst = Parameter(torch.empty(1, heads, out_channels))
+        self.bias = Parameter(torch.empty(heads * out_channels if concat else out_channels)) \
+            if bias else None
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        glorot_(self.lin.weight)
+        glorot_(self.att_src)
+        glorot_(self.att_dst)
+        if self.bias is not None:
+            torch.nn.init.zeros_(self.bias)
+
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        old = prefix + "lin_src.weight"
+        if old in state_dict and prefix + "lin.weight" not in state_dict:
+            state_dict[prefix + "lin.weight"] = state_dict.pop(old)
+            state_dict.pop(prefix + "lin_dst.weight", None)
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+
+    def forward(self, x: Union[Tensor, Tuple[Tensor, Tensor]], adj: Adjacency) -> Tensor:
+        num_dst = adj.sparse_sizes()[0]
+        if isinstance(x, tuple):
+            x_src, x_dst = x
+            same = (x_dst.size(0) == num_dst and x_dst.data_ptr() == x_src.data_ptr()
+                    and x_dst.stride() == x_src.stride())
+            if not same:
+                raise ValueError("GATConv expects (x, x[:num_dst]) with a shared projection")
+        else:
+            x_src = x
+        hs = self.lin(x_src)
+        return gat_attention(hs, adj, self.att_src, self.att_dst, self.bias, self.heads,
+                             self.out_channels, self.concat)
+
+    def __repr__(self) -> str:
+        return (f"{self.__class__.__name__}({self.in_channels}, {self.out_channels}, "
+                f"heads={self.heads})")

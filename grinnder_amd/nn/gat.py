@@ -1,0 +1,57 @@
+"""GAT model (grinnder/nn/gat.py:17-87) on the HIP GATConv."""
+
+from __future__ import annotations
+
+from typing import List
+
+import torch.nn.functional as F
+from torch import Tensor
+from torch.nn import LayerNorm, ModuleList
+
+from grinnder_amd.nn.base import GriNNderModel
+from grinnder_amd.nn.conv import GATConv
+
+
+class GAT(GriNNderModel):
+    """Graph Attention Network on bipartite partition inputs (x, x[:num_dst]).
+
+    Layer l: dropout(x) -> GATConv -> (LayerNorm) -> ELU, except the last
+    layer (one head, mean over heads, no activation).
+    """
+
+    def __init__(self, in_channels: int, hidden_channels: int, out_channels: int,
+                 num_layers: int, heads: int = 8, dropout: float = 0.6, norm: bool = False):
+        super().__init__(num_layers)
+        self.dropout = dropout
+        self.heads = heads
+        self.convs = ModuleList()
+        self.convs.append(GATConv(in_channels, hidden_channels, heads=heads,
+                                  add_self_loops=False))
+        for _ in range(num_layers - 2):
+            self.convs.append(GATConv(hidden_channels * heads, hidden_channels, heads=heads,
+                                      add_self_loops=False))
+        self.convs.append(GATConv(hidden_channels * heads, out_channels, heads=1, concat=False,
+                                  add_self_loops=False))
+        self.norms = None
+        if norm:
+            self.norms = ModuleList(LayerNorm(hidden_channels * heads)
+                                    for _ in range(num_layers - 1))
+
+    def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
+        x = F.dropout(x, p=self.dropout, training=self.training)
+        num_dst = adj.sparse_sizes()[0]
+        x = self.convs[layer]((x, x[:num_dst]), adj)
+        if layer < self.num_layers - 1:
+            if self.norms is not None:
+                x = self.norms[layer](x)
+            x = F.elu(x)
+        return x
+
+    def layer_dims(self) -> List[int]:
+        dims = [self.convs[0].in_channels]
+        for i, conv in enumerate(self.convs):
+            if i < len(self.convs) - 1:
+                dims.append(conv.out_channels * conv.heads)
+            else:
+                dims.append(conv.out_channels)
+        return dims

@@ -1,0 +1,273 @@
+/*
+ * grinnder_amd.h — C ABI of the MI355X (gfx950) partitioned-GNN-layer library
+ * (libgrinnder_amd.so).
+ *
+ * Conventions shared by every entry point:
+ *   - Returns int status: 0 on success, a negative GR_E* code on failure.
+ *     The message of the most recent failure on the calling thread is
+ *     available from gr_last_error().  Nothing is launched or copied when a
+ *     precondition check fails (checks run before the first enqueue).
+ *   - Plain pointers and int64 extents only.  "stream" is a hipStream_t
+ *     passed as void* (NULL means the legacy default stream).
+ *   - The library never frees caller memory.  Device work is enqueued on the
+ *     given stream and is asynchronous unless stated otherwise.
+ *   - Index arrays crossing the boundary in the reference's layout are int64
+ *     (rowptr, col, boundaries); device-resident index arrays produced by the
+ *     preparation calls below are int32.
+ *
+ * Reference interfaces replaced (paths relative to the GriNNder repository):
+ *   csrc/grinnder_ops.cpp:7-34          pybind op table of grinnder._C
+ *   csrc/cuda/async_transfer.cu:17-186  h2d/d2h copies, gather/scatter
+ *   csrc/cpu/subgraph.cpp:8-114         build_subgraph
+ *   grinnder/data/partition.py:178-228  _build_partition_subgraph (boundaries)
+ *   torch_sparse spmm_sum / csr2csc, called through PyG GCNConv
+ *       (grinnder/nn/gcn.py:53-56,65; grinnder/engine/trainer.py:288-302)
+ *   PyG GATConv attention + softmax + aggregation
+ *       (grinnder/nn/gat.py:54-61,69-78)
+ */
+#ifndef GRINNDER_AMD_H
+#define GRINNDER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status                                                                    */
+/* ------------------------------------------------------------------------ */
+
+#define GR_OK 0
+#define GR_EINVAL (-1)   /* bad argument / size mismatch / index out of range */
+#define GR_EHIP (-2)     /* HIP runtime call failed */
+#define GR_ENOMEM (-3)   /* host allocation failed */
+#define GR_EUNSUP (-4)   /* shape or dtype not supported */
+
+/* Message of the last failure on this thread ("" if none). */
+const char* gr_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int gr_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Host <-> device transfers (grinnder._C transfer ops)                      */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces h2d_copy_async, csrc/cuda/async_transfer.cu:40-58.
+ * Copies nbytes from host memory to device memory on `stream`.  Pinned host
+ * memory gives a truly asynchronous DMA; pageable memory is accepted and is
+ * staged by the runtime.  The copy is recorded in the H2D completion queue
+ * consumed by gr_h2d_synchronize(). */
+int gr_h2d_copy_async(const void* src_host, void* dst_dev, int64_t nbytes,
+                      void* stream);
+
+/* Replaces d2h_copy_async, csrc/cuda/async_transfer.cu:20-38. */
+int gr_d2h_copy_async(const void* src_dev, void* dst_host, int64_t nbytes,
+                      void* stream);
+
+/* Replaces h2d_synchronize / d2h_synchronize,
+ * csrc/cuda/async_transfer.cu:17-18 and csrc/thread_pool.h:65-70: waits
+ * for the OLDEST queued operation of that direction (FIFO, one entry per
+ * call) and returns its error, if any.  Returns 0 when the queue is empty. */
+int gr_h2d_synchronize(void);
+int gr_d2h_synchronize(void);
+
+/* Replaces gather_partitions, csrc/cuda/async_transfer.cu:60-120.
+ * dst (device, dst_rows x row_bytes) receives
+ *   [ srcs[pid] (all src_rows[pid] rows)
+ *   | srcs[p][boundaries[p][k]] for p = 0..num_parts-1, p != pid,
+ *     boundary_lens[p] > 0, k in order ].
+ * srcs are host partition buffers (pinned: rows are read by a device kernel
+ * over PCIe; pageable: rows are gathered by host threads into a pinned
+ * staging slot and copied by DMA).  boundaries are host int64 arrays
+ * (entries for p == pid, NULL pointers and zero lengths are skipped).
+ * Errors (GR_EINVAL) if the rows do not add up to dst_rows or if a boundary
+ * index is out of range — checked before anything is enqueued. */
+int gr_gather_partitions(int32_t pid, int32_t num_parts,
+                         const void* const* srcs, const int64_t* src_rows,
+                         void* dst, int64_t dst_rows, int64_t row_bytes,
+                         const int64_t* const* boundaries,
+                         const int64_t* boundary_lens, void* stream);
+
+/* Replaces scatter_partitions, csrc/cuda/async_transfer.cu:122-186.
+ * fp32 accumulate of src (device, src_rows x dim) into host partitions:
+ *   dsts[pid][r]           += src[r]            r < dst_rows[pid]
+ *   dsts[p][boundaries[p][k]] += src[off + k]   p ascending, p != pid
+ * Pinned destinations are updated by one device kernel (read-add-write over
+ * PCIe, asynchronous on `stream`); pageable destinations are updated on the
+ * host after a D2H copy (synchronous).  Repeated indices inside one boundary
+ * are accumulated sequentially in index order, like index_put_(accumulate).
+ * Errors (GR_EINVAL) on row-count mismatch or out-of-range index. */
+int gr_scatter_partitions(int32_t pid, int32_t num_parts, const float* src,
+                          int64_t src_rows, int64_t dim, float* const* dsts,
+                          const int64_t* dst_rows,
+                          const int64_t* const* boundaries,
+                          const int64_t* boundary_lens, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Partition bookkeeping (host, bit-exact)                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces build_subgraph, csrc/cpu/subgraph.cpp:8-114 (int64 only, as the
+ * reference reads data_ptr<int64_t>).  Two calls:
+ *   1) out_col == NULL: writes *out_nnz and *out_num_nodes (seeds + newly
+ *      discovered neighbours) and returns.
+ *   2) with out_rowptr [n_idx+1 or out_num_nodes+1 if !bipartite],
+ *      out_col [nnz], out_value [nnz] (NULL if value == NULL) and
+ *      out_n_id [num_nodes]: fills them.
+ * Seeds get ids [0, n_idx); unseen neighbours get n_idx, n_idx+1, ... in
+ * first-seen order of a row-major scan.  value is copied as raw
+ * value_elem_size-byte elements. */
+int gr_build_subgraph(const int64_t* rowptr, const int64_t* col,
+                      const void* value, int64_t value_elem_size,
+                      int64_t num_rows, const int64_t* idx, int64_t n_idx,
+                      int32_t bipartite, int64_t* out_rowptr, int64_t* out_col,
+                      void* out_value, int64_t* out_n_id, int64_t* out_nnz,
+                      int64_t* out_num_nodes);
+
+/* Replaces the boundary split and column remap of _build_partition_subgraph,
+ * grinnder/data/partition.py:195-225.  Given n_id[batch_size:] (global ids of
+ * the halo in discovery order) and the partition pointer ptr[num_parts+1]:
+ *   boundary_lens[p] = number of halo nodes owned by p (0 for p == pid),
+ *   boundary_flat = concatenation over p ascending of (n_id - ptr[p]) in
+ *                   discovery order (length n_halo),
+ *   col (in place, length nnz): halo columns c >= batch_size are remapped to
+ *       batch_size + (position of c's node in boundary_flat).
+ * Errors if a halo node lies in partition pid or outside [0, ptr[P]). */
+int gr_partition_boundaries(int32_t pid, int32_t num_parts, const int64_t* ptr,
+                            int64_t batch_size, const int64_t* halo_ids,
+                            int64_t n_halo, int64_t* col, int64_t nnz,
+                            int64_t* boundary_flat, int64_t* boundary_lens);
+
+/* ------------------------------------------------------------------------ */
+/* Aggregation-side preparation (host, done once per partition adjacency)    */
+/* ------------------------------------------------------------------------ */
+
+/* Deterministic CSR -> CSC transpose of a rows x cols matrix (no reference
+ * counterpart in the repository: replaces torch_sparse csr2csc, which the
+ * reference's SparseTensor recomputes on every backward,
+ * grinnder/engine/trainer.py:288-302).  Within each column the entries are
+ * ordered by (row, CSR position) — a stable transpose.
+ *   colptr [cols+1] int64, row_idx [nnz] int32, val_t [nnz] f32 (skipped if
+ *   val or val_t is NULL), perm [nnz] int32 = CSR position of each CSC entry
+ *   (skipped if NULL). */
+int gr_csr_transpose(const int64_t* rowptr, const int64_t* col,
+                     const float* val, int64_t rows, int64_t cols,
+                     int64_t* colptr, int32_t* row_idx, float* val_t,
+                     int32_t* perm);
+
+/* Work plan for the row-parallel aggregation kernels.  A row whose length
+ * exceeds seg_len is split into ceil(len / seg_len) units whose partial sums
+ * go to a workspace and are reduced in unit order by a second kernel, so the
+ * result is deterministic.  Units of split rows come first (they start
+ * early), then single-unit rows in row order.
+ *   units [n_units*4] int32 = (row, edge_begin, edge_end, slot or -1)
+ *   fixups [n_fix*3] int32   = (row, first_slot, n_slots)
+ * Two calls: with units == NULL only the counts are written. */
+int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len,
+                 int32_t* units, int64_t* n_units, int32_t* fixups,
+                 int64_t* n_fix, int64_t* n_slots);
+
+/* ------------------------------------------------------------------------ */
+/* GCN aggregation (device)                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Y[r, :D] = sum_e val[e] * X[idx[e], :D] (+ bias[:D] if bias != NULL) for
+ * every row r of the plan, fp32, deterministic (no atomics).  Replaces the
+ * torch_sparse spmm_sum forward of PyG GCNConv (grinnder/nn/gcn.py:53-56,65;
+ * adjacency from grinnder/engine/trainer.py:288-302) when called with the
+ * CSR plan, and its backward dZ = A^T G when called with the CSC plan of
+ * gr_csr_transpose.  Rows with no edges get bias (or 0).
+ *   X: ldx-strided device rows (ldx >= D), Y: ldy-strided (ldy >= D).
+ *   workspace: n_slots * D floats (may be NULL when n_slots == 0). */
+int gr_gcn_aggregate(const int32_t* units, int64_t n_units,
+                     const int32_t* fixups, int64_t n_fix,
+                     const int32_t* idx, const float* val, const float* x,
+                     int64_t ldx, float* y, int64_t ldy, const float* bias,
+                     int64_t rows, int64_t dim, float* workspace,
+                     int64_t n_slots, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* GAT attention (device)                                                    */
+/*                                                                           */
+/* Replace PyG GATConv's attention path as the reference calls it            */
+/* (grinnder/nn/gat.py:54-61 heads/concat/add_self_loops=False; :69-78       */
+/* bipartite input (x, x[:B])): logits s_j + d_i, LeakyReLU(0.2), edge       */
+/* softmax with max subtraction and +1e-16 in the denominator, and the       */
+/* alpha-weighted sum of source rows.  Because the reference applies one     */
+/* shared lin to x and to x[:B], destination features are the first B rows  */
+/* of Hs.  Layout: Hs [E, H*C] (row stride ldh), s [E,H], d/m/den [B,H].     */
+/* ------------------------------------------------------------------------ */
+
+/* s[j,h] = <Hs[j,h,:], att_src[h,:]> for j < n_src and
+ * d[i,h] = <Hs[i,h,:], att_dst[h,:]> for i < n_dst. */
+int gr_gat_scores(const float* hs, int64_t ldh, int64_t n_src, int64_t n_dst,
+                  int64_t heads, int64_t channels, const float* att_src,
+                  const float* att_dst, float* s, float* d, void* stream);
+
+/* Row max m[i,h] of LeakyReLU(s_j + d_i) over the CSR row and
+ * den[i,h] = sum exp(v - m) + 1e-16 (rows without edges: m = 0, den = 1).
+ * Uses the CSR plan of gr_spmm_plan; workspace: n_slots * 2H floats. */
+int gr_gat_softmax_stats(const int32_t* units, int64_t n_units,
+                         const int32_t* fixups, int64_t n_fix,
+                         const int32_t* idx, const float* s, const float* d,
+                         int64_t heads, float* m, float* den, float* workspace,
+                         int64_t n_slots, void* stream);
+
+/* O[i,:] = sum_e alpha_e Hs[idx[e],:] with
+ * alpha_e = exp(LeakyReLU(s + d) - m) / den, written to o [B, H*C]; when y is
+ * not NULL also Y = O + bias (bias may be NULL) with row stride ldy.
+ * workspace: n_slots * H*C floats. */
+int gr_gat_aggregate(const int32_t* units, int64_t n_units,
+                     const int32_t* fixups, int64_t n_fix, const int32_t* idx,
+                     const float* hs, int64_t ldh, const float* s,
+                     const float* d, const float* m, const float* den,
+                     int64_t heads, int64_t channels, const float* bias,
+                     float* o, float* y, int64_t ldy, float* workspace,
+                     int64_t n_slots, void* stream);
+
+/* Backward over source rows j (CSC plan, row_idx/perm from
+ * gr_csr_transpose).  go = dL/dO [B, H*C]; cdot[i,h] = <go_i,h, O_i,h>.
+ * Writes dhs [E, H*C] = sum_i alpha_ij go_i + ds_j * att_src,
+ * ds [E,H] = sum_i g_t,ij and gt [nnz,H] (CSR order) = g_t per edge, where
+ * g_t = alpha (<go_i, Hs_j> - cdot_i) * (t > 0 ? 1 : 0.2).
+ * workspace: n_slots * (H*C + H) floats. */
+int gr_gat_backward_src(const int32_t* units, int64_t n_units,
+                        const int32_t* fixups, int64_t n_fix,
+                        const int32_t* row_idx, const int32_t* perm,
+                        const float* hs, int64_t ldh, const float* go,
+                        const float* s, const float* d, const float* m,
+                        const float* den, const float* cdot,
+                        const float* att_src, int64_t heads, int64_t channels,
+                        float* dhs, float* ds, float* gt, float* workspace,
+                        int64_t n_slots, void* stream);
+
+/* Backward over destination rows i (CSR plan): dd[i,h] = sum_e gt[e,h] and
+ * dhs[i,:] += dd[i,h(f)] * att_dst[f].  Must run after
+ * gr_gat_backward_src on the same stream.  workspace: n_slots * H floats. */
+int gr_gat_backward_dst(const int32_t* units, int64_t n_units,
+                        const int32_t* fixups, int64_t n_fix, const float* gt,
+                        const float* att_dst, int64_t heads, int64_t channels,
+                        float* dd, float* dhs, float* workspace,
+                        int64_t n_slots, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic inputs (no reference counterpart)                               */
+/* ------------------------------------------------------------------------ */
+
+/* Seeded R-MAT edge sampler: sample i (i in [first, first+n)) picks, for each
+ * of `scale` levels, a quadrant with probabilities (a, b, c, 1-a-b-c) using a
+ * counter-based 64-bit hash of (seed, i, level), so the sample stream is
+ * independent of thread count.  Writes src[n], dst[n] (int64).  Host,
+ * multi-threaded (nthreads <= 0: hardware concurrency). */
+int gr_rmat_sample(uint64_t seed, int32_t scale, double a, double b, double c,
+                   int64_t first, int64_t n, int64_t* src, int64_t* dst,
+                   int32_t nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRINNDER_AMD_H */

@@ -1,0 +1,348 @@
+"""Pins the CPU oracle against the reference's known answers, the compiled
+reference code (oracle/_ref) and independent closed forms (CPU only)."""
+
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.graphs import random_bipartite
+
+
+# ---------------------------------------------------------------- gcn norm --
+
+def test_gcn_norm_triangle_known_answer():
+    """tests/test_data.py:11-20 of the reference (weights in (0, 1]): on the
+    triangle + self-loops every degree is 3, so every weight is the fp32
+    square of fp32(3^-1/2), within one ulp of 1/3."""
+    ei = torch.tensor([[0, 1, 1, 2, 0, 2], [1, 0, 2, 1, 2, 0]])
+    w = oracle.compute_gcn_norm(ei, 3, True)
+    assert w.shape == (9,)
+    assert (w > 0).all() and (w <= 1).all()
+    r = np.float32(1.0) / np.sqrt(np.float32(3.0))
+    assert torch.equal(w, torch.full((9,), float(np.float32(r * r))))
+    assert abs(float(w[0]) - 1.0 / 3.0) <= float(np.spacing(np.float32(1.0 / 3.0)))
+
+
+def test_gcn_norm_matches_brute_force_degrees():
+    g = torch.Generator().manual_seed(0)
+    n = 40
+    ei = torch.randint(0, n, (2, 300), generator=g)
+    ei[:, :5] = torch.tensor([[3] * 5, [7] * 5])  # repeated edges are kept
+    w = oracle.compute_gcn_norm(ei, n, True)
+    full = torch.cat([ei, torch.arange(n).repeat(2, 1)], dim=1)
+    deg = [0] * n
+    for c in full[1].tolist():
+        deg[c] += 1
+    for e, (r, c) in enumerate(full.t().tolist()):
+        expect = np.float32(1.0 / np.sqrt(np.float32(deg[r]))) * np.float32(1.0 / np.sqrt(np.float32(deg[c])))
+        assert w[e].item() == pytest.approx(float(expect), rel=2e-7)
+
+
+def test_pow_minus_half_is_reciprocal_sqrt():
+    """deg.pow(-0.5) on integer degrees equals the correctly rounded
+    1/sqrt (so a C restatement 1.0f/sqrtf(d) is bit-exact)."""
+    d = torch.arange(1, 200001, dtype=torch.float32)
+    a = d.pow(-0.5)
+    b = torch.from_numpy((np.float32(1.0) / np.sqrt(d.numpy())).astype(np.float32))
+    assert torch.equal(a, b)
+
+
+def test_gcn_norm_isolated_node_weight_zero_not_inf():
+    ei = torch.tensor([[0], [1]])
+    w = oracle.compute_gcn_norm(ei, 3, add_loops=False)
+    assert torch.isfinite(w).all()
+
+
+# --------------------------------------------------------------------- CSR --
+
+def test_csr_rows_and_permutation():
+    g = torch.Generator().manual_seed(1)
+    n = 50
+    ei = torch.randint(0, n, (2, 700), generator=g)
+    rowptr, col, perm = oracle.edge_index_to_csr(ei, n)
+    counts = torch.bincount(ei[0], minlength=n)
+    assert torch.equal(rowptr[1:] - rowptr[:-1], counts)
+    assert torch.equal(col, ei[1][perm])
+    for r in range(n):
+        got = sorted(col[rowptr[r]:rowptr[r + 1]].tolist())
+        expect = sorted(ei[1][ei[0] == r].tolist())
+        assert got == expect
+
+
+# --------------------------------------------------------- build_subgraph --
+
+def test_build_subgraph_reference_known_answer():
+    """tests/test_cpp_extensions.py:64-84."""
+    rowptr = torch.tensor([0, 2, 3, 4, 4])
+    col = torch.tensor([1, 2, 2, 3])
+    r, c, v, n_id = oracle.build_subgraph(rowptr, col, None, torch.tensor([0, 1]), True)
+    assert r.tolist() == [0, 2, 3]
+    assert c.tolist() == [1, 2, 2]
+    assert n_id.tolist() == [0, 1, 2]
+    assert v is None
+
+
+def test_build_subgraph_values_and_non_bipartite():
+    """tests/test_cpp_extensions.py:86-106."""
+    rowptr = torch.tensor([0, 2, 3, 4, 4])
+    col = torch.tensor([1, 2, 2, 3])
+    value = torch.tensor([0.5, 0.3, 0.7, 0.1])
+    r, c, v, n_id = oracle.build_subgraph(rowptr, col, value, torch.tensor([0]), True)
+    assert v.tolist() == pytest.approx([0.5, 0.3])
+    assert c.tolist() == [1, 2] and n_id.tolist() == [0, 1, 2]
+    rowptr = torch.tensor([0, 2, 3, 3])
+    col = torch.tensor([1, 2, 2])
+    r, c, v, n_id = oracle.build_subgraph(rowptr, col, None, torch.tensor([0]), False)
+    assert r.numel() == n_id.numel() + 1
+    assert r.tolist() == [0, 2, 2, 2]
+
+
+def _random_csr(n, m, seed):
+    g = torch.Generator().manual_seed(seed)
+    ei = torch.randint(0, n, (2, m), generator=g)
+    rowptr, col, _ = oracle.edge_index_to_csr(ei, n)
+    val = torch.rand(col.numel(), generator=g)
+    return rowptr, col, val
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_build_subgraph_matches_compiled_reference(seed):
+    ref = oracle.ref_build_subgraph()
+    if ref is None:
+        pytest.skip("reference build (oracle/_ref) not present")
+    rowptr, col, val = _random_csr(120, 900, seed)
+    g = torch.Generator().manual_seed(seed + 10)
+    idx = torch.randperm(120, generator=g)[:37]
+    for bip in (True, False):
+        a = oracle.build_subgraph(rowptr, col, val, idx, bip)
+        b = ref(rowptr, col, val, idx, bip)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        assert torch.equal(a[2], b[2]) and torch.equal(a[3], b[3])
+
+
+def test_build_subgraph_brute_force_relabel():
+    """Every output edge maps back to an input edge of the same seed row."""
+    rowptr, col, val = _random_csr(60, 400, 5)
+    idx = torch.tensor([5, 17, 3, 44])
+    r, c, v, n_id = oracle.build_subgraph(rowptr, col, val, idx, True)
+    for i, s in enumerate(idx.tolist()):
+        got = [(int(n_id[x]), float(y)) for x, y in zip(c[r[i]:r[i + 1]], v[r[i]:r[i + 1]])]
+        exp = [(int(x), float(y)) for x, y in zip(col[rowptr[s]:rowptr[s + 1]],
+                                                   val[rowptr[s]:rowptr[s + 1]])]
+        assert got == exp
+    assert len(set(n_id.tolist())) == n_id.numel()
+
+
+# ---------------------------------------------- partition subgraph / pipeline --
+
+def _banded(n, reach):
+    edges = set()
+    for i in range(n):
+        for j in range(max(0, i - reach), min(n, i + reach + 1)):
+            if i != j:
+                edges.add((i, j))
+    return torch.tensor([[e[0] for e in edges], [e[1] for e in edges]], dtype=torch.long)
+
+
+def test_partition_subgraph_serial_equals_parallel():
+    """tests/test_partition.py:207-249: banded 20-node graph, ptr [0,5,10,15,20]."""
+    ei = _banded(20, 3)
+    w = oracle.compute_gcn_norm(ei, 20, True)
+    ei = oracle.add_self_loops(ei, 20)
+    rowptr, col, sp = oracle.edge_index_to_csr(ei, 20)
+    w = w[sp]
+    ptr = torch.tensor([0, 5, 10, 15, 20])
+    serial = [oracle.build_partition_subgraph(p, ptr, rowptr, col, w, 4) for p in range(4)]
+    with ThreadPoolExecutor(4) as ex:
+        par = list(ex.map(lambda p: oracle.build_partition_subgraph(p, ptr, rowptr, col, w, 4),
+                          range(4)))
+    for s, q in zip(serial, par):
+        assert s[0] == q[0] and s[3:] == q[3:]
+        for a, b in zip(s[1], q[1]):
+            assert torch.equal(a, b)
+        for a, b in zip(s[2], q[2]):
+            assert (a is None and b is None) or torch.equal(a, b)
+    for pid, (rp, c, v), bnd, expanded, batch in serial:
+        assert rp.numel() == batch + 1
+        assert bnd[pid] is None
+        assert int(c.max()) < expanded
+
+
+def test_partition_subgraph_gather_invariant():
+    """Gathering rows in the [intra | halo by owner] layout and aggregating with
+    the remapped columns equals aggregating the global rows directly."""
+    ei = _banded(30, 4)
+    n = 30
+    w = oracle.compute_gcn_norm(ei, n, True)
+    ei = oracle.add_self_loops(ei, n)
+    rowptr, col, sp = oracle.edge_index_to_csr(ei, n)
+    w = w[sp]
+    ptr = torch.tensor([0, 8, 17, 30])
+    x = torch.randn(n, 5, generator=torch.Generator().manual_seed(3))
+    full = oracle.spmm(rowptr, col, w, x)
+    for pid in range(3):
+        _, (rp, c, v), bnd, expanded, batch = oracle.build_partition_subgraph(
+            pid, ptr, rowptr, col, w, 3)
+        srcs = [x[ptr[p]:ptr[p + 1]] for p in range(3)]
+        gathered = torch.from_numpy(oracle.gather_partitions(pid, srcs, bnd))
+        assert gathered.shape[0] == expanded
+        part = oracle.spmm(rp, c, v, gathered)
+        assert np.allclose(part, full[int(ptr[pid]):int(ptr[pid + 1])], rtol=0, atol=1e-12)
+
+
+# ----------------------------------------------------------- arithmetic --
+
+def _dense(rowptr, col, val, rows, cols):
+    a = torch.zeros(rows, cols, dtype=torch.float64)
+    for i in range(rows):
+        for e in range(int(rowptr[i]), int(rowptr[i + 1])):
+            a[i, col[e]] += float(val[e])
+    return a
+
+
+def test_spmm_matches_dense_brute_force():
+    rowptr, col, val = random_bipartite(40, 55, 6, seed=2, long_rows=1, long_len=90)
+    x = torch.randn(55, 9, dtype=torch.float32, generator=torch.Generator().manual_seed(0))
+    b = torch.randn(9)
+    a = _dense(rowptr, col, val, 40, 55)
+    ref = a @ x.double() + b.double()
+    got = oracle.spmm(rowptr, col, val, x, b)
+    assert np.allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+    g = torch.randn(40, 9)
+    got_t = oracle.spmm_t(rowptr, col, val, g, 55)
+    assert np.allclose(got_t, (a.t() @ g.double()).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_special_cases():
+    # identity adjacency (self-loops only): Y = X + b
+    n = 7
+    rowptr = torch.arange(n + 1)
+    col = torch.arange(n)
+    val = torch.ones(n)
+    x = torch.randn(n, 4)
+    assert np.array_equal(oracle.spmm(rowptr, col, val, x), x.double().numpy())
+    # all-ones features: each output row equals its row's weight sum
+    rowptr, col, val = random_bipartite(20, 30, 5, seed=9)
+    ones = torch.ones(30, 3)
+    rs = torch.zeros(20, dtype=torch.float64)
+    for i in range(20):
+        rs[i] = val[rowptr[i]:rowptr[i + 1]].double().sum()
+    got = oracle.spmm(rowptr, col, val, ones)
+    assert np.allclose(got, rs[:, None].expand(20, 3).numpy(), atol=1e-12)
+
+
+def _dense_gat(a_mask, hs, att_src, att_dst, bias, H, C, concat):
+    """Dense float64 GAT: masked logits, softmax with max subtraction and +1e-16."""
+    B = a_mask.shape[0]
+    h3 = hs.view(-1, H, C)
+    s = (h3 * att_src.view(1, H, C)).sum(-1)  # [E,H]
+    d = (h3[:B] * att_dst.view(1, H, C)).sum(-1)  # [B,H]
+    t = s.t().unsqueeze(1) + d.t().unsqueeze(2)  # [H,B,E]
+    v = torch.nn.functional.leaky_relu(t, 0.2)
+    cnt = a_mask.unsqueeze(0).to(torch.float64)  # multiplicity of each (i, j)
+    neg = torch.finfo(torch.float64).min
+    m = torch.where(cnt > 0, v, torch.full_like(v, neg)).amax(-1, keepdim=True).detach()
+    m = torch.where(m == neg, torch.zeros_like(m), m)  # rows without edges
+    p = torch.exp(torch.where(cnt > 0, v - m, torch.zeros_like(v))) * cnt
+    den = p.sum(-1, keepdim=True) + 1e-16
+    alpha = p / den  # [H,B,E] (summed over duplicate edges)
+    o = torch.einsum("hbe,ehc->bhc", alpha, h3)
+    out = o.reshape(B, H * C) if concat else o.mean(1)
+    return out + bias
+
+
+@pytest.mark.parametrize("H,C,concat", [(1, 5, True), (3, 4, True), (2, 3, False)])
+def test_gat_oracle_matches_dense_autograd(H, C, concat):
+    B, E = 9, 13
+    rowptr, col, _ = random_bipartite(B, E, 3, seed=H + C, empty_frac=0.1)
+    # dense multiplicity matrix (duplicates allowed)
+    mask = torch.zeros(B, E)
+    for i in range(B):
+        for e in range(int(rowptr[i]), int(rowptr[i + 1])):
+            mask[i, col[e]] += 1
+    g = torch.Generator().manual_seed(4)
+    hs = torch.randn(E, H * C, generator=g)
+    a_s = torch.randn(1, H, C, generator=g)
+    a_d = torch.randn(1, H, C, generator=g)
+    out_w = H * C if concat else C
+    b = torch.randn(out_w, generator=g)
+    gy = torch.randn(B, out_w, generator=g)
+
+    ref_out, alpha, tpre = oracle.gat_forward(rowptr, col, hs, H, C, a_s, a_d, b, concat)
+    dhs, das, dad, db = oracle.gat_backward(rowptr, col, hs, H, C, a_s, a_d, concat, alpha,
+                                            tpre, gy)
+
+    hs64 = hs.double().requires_grad_(True)
+    as64 = a_s.double().requires_grad_(True)
+    ad64 = a_d.double().requires_grad_(True)
+    b64 = b.double().requires_grad_(True)
+    out = _dense_gat(mask, hs64, as64, ad64, b64, H, C, concat)
+    out.backward(gy.double())
+    assert np.allclose(ref_out, out.detach().numpy(), rtol=1e-10, atol=1e-10)
+    assert np.allclose(dhs, hs64.grad.numpy(), rtol=1e-9, atol=1e-10)
+    assert np.allclose(das, as64.grad.reshape(-1).numpy(), rtol=1e-9, atol=1e-10)
+    assert np.allclose(dad, ad64.grad.reshape(-1).numpy(), rtol=1e-9, atol=1e-10)
+    assert np.allclose(db, b64.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_dense_gat_gradcheck():
+    """The dense restatement itself is differentiated correctly (finite differences)."""
+    B, E, H, C = 4, 6, 2, 3
+    rowptr, col, _ = random_bipartite(B, E, 2, seed=1, empty_frac=0.0)
+    mask = torch.zeros(B, E)
+    for i in range(B):
+        for e in range(int(rowptr[i]), int(rowptr[i + 1])):
+            mask[i, col[e]] += 1
+    g = torch.Generator().manual_seed(0)
+    hs = torch.randn(E, H * C, generator=g, dtype=torch.float64, requires_grad=True)
+    a_s = torch.randn(1, H, C, generator=g, dtype=torch.float64, requires_grad=True)
+    a_d = torch.randn(1, H, C, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(H * C, generator=g, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(
+        lambda h, s, d, bb: _dense_gat(mask, h, s, d, bb, H, C, True), (hs, a_s, a_d, b))
+
+
+# ------------------------------------------------------- gather / scatter --
+
+def _arange_fixture():
+    """tests/test_cpp_extensions.py:144-171 / tests/test_buffers.py:49-76."""
+    p0 = torch.arange(8, dtype=torch.float).reshape(4, 2)
+    p1 = torch.arange(8, 14, dtype=torch.float).reshape(3, 2)
+    p2 = torch.arange(14, 24, dtype=torch.float).reshape(5, 2)
+    return [p0, p1, p2], [None, torch.tensor([0, 2]), torch.tensor([3])]
+
+
+def test_gather_reference_fixture():
+    srcs, bnd = _arange_fixture()
+    out = oracle.gather_partitions(0, srcs, bnd)
+    assert out.shape == (7, 2)
+    assert np.array_equal(out[:4], srcs[0].numpy())
+    assert np.array_equal(out[4:6], srcs[1][[0, 2]].numpy())
+    assert np.array_equal(out[6:7], srcs[2][[3]].numpy())
+    assert out.tolist() == [[0, 1], [2, 3], [4, 5], [6, 7], [8, 9], [12, 13], [20, 21]]
+
+
+def test_scatter_reference_fixtures():
+    # tests/test_cpp_extensions.py:173-202: ones into zeros
+    dsts = [torch.zeros(4, 2), torch.zeros(3, 2), torch.zeros(5, 2)]
+    bnd = [None, torch.tensor([0, 2]), torch.tensor([3])]
+    out = oracle.scatter_partitions(0, torch.ones(7, 2), dsts, bnd)
+    assert np.array_equal(out[0], np.ones((4, 2), np.float32))
+    assert out[1].tolist() == [[1, 1], [0, 0], [1, 1]]
+    assert out[2][3].tolist() == [1, 1] and out[2].sum() == 2
+    # tests/test_host_buffer_ops.py:40-60: 1.0 + 2.0 = 3.0 on the self block
+    dsts = [torch.ones(4, 2), torch.zeros(3, 2), torch.zeros(5, 2)]
+    out = oracle.scatter_partitions(0, torch.full((7, 2), 2.0), dsts, bnd)
+    assert np.array_equal(out[0], np.full((4, 2), 3.0, np.float32))
+
+
+def test_scatter_repeated_indices_accumulate_in_order():
+    """index_put_(accumulate=True) semantics: repeated indices all add."""
+    dsts = [torch.zeros(2, 1), torch.zeros(3, 1)]
+    bnd = [None, torch.tensor([1, 1, 2])]
+    src = torch.tensor([[1.0], [2.0], [3.0], [4.0], [5.0]])
+    out = oracle.scatter_partitions(0, src, dsts, bnd)
+    assert out[1].reshape(-1).tolist() == [0.0, 7.0, 5.0]
