@@ -41,6 +41,9 @@ def parse_args():
     ap.add_argument("--config", choices=["c1", "c2"], default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the run, copy a 1 GiB device buffer 3 times (a kernel of "
+                         "known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -217,6 +220,13 @@ def main():
         "passes": passes,
     }
     print(json.dumps(out), flush=True)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration: 3 device copies of 1 GiB (read 1 GiB + write 1 GiB each)")
 
 
 if __name__ == "__main__":

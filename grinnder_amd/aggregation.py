@@ -214,7 +214,8 @@ class _GATAttention(torch.autograd.Function):
         ds = torch.empty((E, H), dtype=torch.float32, device=dev)
         gt = torch.empty((max(plan.nnz, 1), H), dtype=torch.float32, device=dev)
         bw = plan.bwd
-        ws = _workspace(bw.n_slots, HC + H, dev)
+        ws_stride = ((HC + 3) // 4) * 4 + ((H + 3) // 4) * 4
+        ws = _workspace(bw.n_slots, ws_stride, dev)
         _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
                   bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
                   plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(), hs.stride(0),

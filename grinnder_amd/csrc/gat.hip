@@ -394,12 +394,14 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
       if (head_lead[ch]) ds[j * H + hd[ch]] = dsl[ch];
     }
   } else {
-    float* p = ws + (int64_t)w.w * (HC + H);
+    // Slot layout [acc (H*C) | ds (H)], each part padded to 4 floats.
+    const int hc4 = ((HC + 3) / 4) * 4;
+    float* p = ws + (int64_t)w.w * (hc4 + ((H + 3) / 4) * 4);
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
       if (!fvalid[ch]) continue;
       st<VEC>(p + foff[ch], acc[ch]);
-      if (head_lead[ch]) p[HC + hd[ch]] = dsl[ch];
+      if (head_lead[ch]) p[hc4 + hd[ch]] = dsl[ch];
     }
   }
 }
@@ -415,13 +417,15 @@ __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restri
   if (wid >= n_fix) return;
   const int row = fix[3 * wid + 0], first = fix[3 * wid + 1], n = fix[3 * wid + 2];
   const int HC = H * C;
+  const int hc4 = ((HC + 3) / 4) * 4;
+  const int stride = hc4 + ((H + 3) / 4) * 4;
   for (int f = lane; f < HC; f += 64) {
     const int h = f / C;
     float acc = 0.f, dsum = 0.f;
     for (int k = 0; k < n; ++k) {
-      const float* p = ws + (int64_t)(first + k) * (HC + H);
+      const float* p = ws + (int64_t)(first + k) * stride;
       acc += p[f];
-      dsum += p[HC + h];
+      dsum += p[hc4 + h];
     }
     dhs[(int64_t)row * HC + f] = fmaf(dsum, att_src[f], acc);
     if (f == h * C) ds[(int64_t)row * H + h] = dsum;
@@ -511,13 +515,15 @@ int check_heads(int64_t H, int64_t C) {
   return GR_OK;
 }
 
-// Vector width and chunk count for a row of HC features: float4 when every
-// float4 lies inside one head and rows are 16-byte aligned.
+// Vector width and chunk count for a row of HC <= 1024 features: float4 when
+// every float4 lies inside one head and rows are 16-byte aligned; nch is the
+// number of 64-lane chunks rounded up to a power of two (1..16).
 void pick_shape(int64_t HC, int64_t C, bool aligned, int* vec, int* nch) {
   *vec = (C % 4 == 0 && HC % 4 == 0 && aligned) ? 4 : 1;
   const int64_t chunks = (HC + *vec - 1) / *vec;
-  *nch = chunks <= 64 ? 1 : (chunks <= 128 ? 2 : 4);
-  if (*vec == 1 && chunks > 256) *nch = 16;  // rejected by the callers
+  int n = 1;
+  while (n * 64 < chunks) n <<= 1;
+  *nch = n;
 }
 
 }  // namespace
@@ -568,7 +574,7 @@ static hipError_t launch_gat_agg(hipStream_t st, const int4* units, int64_t n_un
                                  const int32_t* idx, const float* hs, int64_t ldh, const float* s,
                                  const float* d, const float* m, const float* den, int H, int C,
                                  const float* bias, float* o, float* y, int64_t ldy, float* ws) {
-  constexpr int U = NCH == 1 ? 8 : (NCH == 2 ? 4 : 2);
+  constexpr int U = NCH == 1 ? 8 : (NCH == 2 ? 4 : (NCH == 4 ? 2 : 1));
   hipLaunchKernelGGL((gat_aggregate_kernel<VEC, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, ws);
   return hipGetLastError();
@@ -604,10 +610,11 @@ extern "C" int gr_gat_aggregate(const int32_t* units, int64_t n_units, const int
     else if (nch == 2) err = launch_gat_agg<4, 2>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
     else err = launch_gat_agg<4, 4>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
   } else {
-    GR_REQUIRE(nch <= 4, "gat_aggregate: H*C too wide for scalar rows");
     if (nch == 1) err = launch_gat_agg<1, 1>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
     else if (nch == 2) err = launch_gat_agg<1, 2>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else err = launch_gat_agg<1, 4>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
+    else if (nch == 4) err = launch_gat_agg<1, 4>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
+    else if (nch == 8) err = launch_gat_agg<1, 8>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
+    else err = launch_gat_agg<1, 16>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
   }
   GR_HIP_CHECK(err);
   if (n_fix > 0) {
@@ -625,7 +632,7 @@ static hipError_t launch_gat_bwd(hipStream_t st, const int4* units, int64_t n_un
                                  const float* m, const float* den, const float* cdot,
                                  const float* att_src, int H, int C, float* dhs, float* ds,
                                  float* gt, float* ws) {
-  constexpr int U = NCH == 1 ? 4 : 2;
+  constexpr int U = NCH == 1 ? 4 : (NCH <= 4 ? 2 : 1);
   hipLaunchKernelGGL((gat_bwd_src_kernel<VEC, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src,
                      H, C, dhs, ds, gt, ws);
@@ -650,8 +657,7 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
                  cdot && att_src && dhs && ds && gt,
              "gat_backward_src: NULL or misaligned pointer");
   const bool al = aligned16(hs) && aligned16(go) && aligned16(dhs) && aligned16(att_src) &&
-                  ldh % 4 == 0 && (workspace == nullptr || aligned16(workspace)) &&
-                  (HC + heads) % 4 == 0;
+                  ldh % 4 == 0 && (workspace == nullptr || aligned16(workspace));
   int vec, nch;
   pick_shape(HC, channels, al, &vec, &nch);
   hipStream_t st = gr::as_stream(stream);
@@ -663,10 +669,11 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
     else if (nch == 2) err = launch_gat_bwd<4, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
     else err = launch_gat_bwd<4, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
   } else {
-    GR_REQUIRE(nch <= 4, "gat_backward_src: H*C too wide for scalar rows");
     if (nch == 1) err = launch_gat_bwd<1, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
     else if (nch == 2) err = launch_gat_bwd<1, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else err = launch_gat_bwd<1, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else if (nch == 4) err = launch_gat_bwd<1, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else if (nch == 8) err = launch_gat_bwd<1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else err = launch_gat_bwd<1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
   }
   GR_HIP_CHECK(err);
   if (n_fix > 0) {

@@ -233,7 +233,7 @@ int gr_gat_aggregate(const int32_t* units, int64_t n_units,
  * Writes dhs [E, H*C] = sum_i alpha_ij go_i + ds_j * att_src,
  * ds [E,H] = sum_i g_t,ij and gt [nnz,H] (CSR order) = g_t per edge, where
  * g_t = alpha (<go_i, Hs_j> - cdot_i) * (t > 0 ? 1 : 0.2).
- * workspace: n_slots * (H*C + H) floats. */
+ * workspace: n_slots * (round_up(H*C, 4) + round_up(H, 4)) floats. */
 int gr_gat_backward_src(const int32_t* units, int64_t n_units,
                         const int32_t* fixups, int64_t n_fix,
                         const int32_t* row_idx, const int32_t* perm,
