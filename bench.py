@@ -41,6 +41,8 @@ def parse_args():
     ap.add_argument("--config", choices=["c1", "c2"], default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--summarize-profile", metavar="DIR", default=None,
+                    help="print a text summary of the rocprofv3 CSV output under DIR and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the run, copy a 1 GiB device buffer 3 times (a kernel of "
                          "known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE)")
@@ -112,8 +114,49 @@ def cpu_baseline(graph, dim: int, seconds: float):
     return edges_done / elapsed / 1e9, sample
 
 
+def summarize_profile(root: str) -> None:
+    """Text summary of rocprofv3 CSV output (kernel stats and/or PMC counters)."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    for path in sorted(glob.glob(os.path.join(root, "**", "*kernel_stats.csv"), recursive=True)):
+        with open(path) as f:
+            rows = list(csv.DictReader(f))
+        rows.sort(key=lambda r: -float(r.get("TotalDurationNs", 0) or 0))
+        total = sum(float(r.get("TotalDurationNs", 0) or 0) for r in rows)
+        print(f"# kernel stats ({os.path.basename(path)}), total {total / 1e6:.3f} ms")
+        print(f"{'calls':>6} {'avg_us':>10} {'total_ms':>10} {'pct':>6}  kernel")
+        for r in rows[:30]:
+            tot = float(r["TotalDurationNs"])
+            print(f"{int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>10.1f} "
+                  f"{tot / 1e6:>10.3f} {100 * tot / total:>6.2f}  {r['Name'][:150]}")
+    for path in sorted(glob.glob(os.path.join(root, "**", "*counter_collection.csv"),
+                                 recursive=True)):
+        acc = defaultdict(lambda: [0, 0.0, 0.0])
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                key = (r["Kernel_Name"], r["Counter_Name"])
+                e = acc[key]
+                e[0] += 1
+                e[1] += float(r["Counter_Value"])
+                e[2] += float(r.get("End_Timestamp", 0)) - float(r.get("Start_Timestamp", 0))
+        print(f"# counters ({os.path.basename(path)}): per-dispatch means")
+        print(f"{'dispatches':>10} {'mean_value':>16} {'avg_us':>10}  counter  kernel")
+        for (k, c), (n, v, t) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
+            if n == 0:
+                continue
+            if not any(s in k for s in ("aggregate", "gat_", "copy", "gemm", "Cijk", "gather",
+                                        "scatter")):
+                continue
+            print(f"{n:>10} {v / n:>16.1f} {t / n / 1e3:>10.1f}  {c}  {k[:140]}")
+
+
 def main():
     args = parse_args()
+    if args.summarize_profile:
+        summarize_profile(args.summarize_profile)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the "
               "multi-GPU path is design-only in this build", file=sys.stderr)

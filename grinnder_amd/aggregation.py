@@ -81,6 +81,16 @@ def _check_device_tensor(name: str, t: Tensor) -> None:
         raise RuntimeError(f"{name} must be float32; got {t.dtype}")
 
 
+def column_sum(g: Tensor) -> Tensor:
+    """sum over rows of a [rows, D] fp32 matrix as one GEMV (ones^T g).
+
+    torch's generic reduction handles a tall matrix with a narrow odd width
+    (e.g. D = 47) poorly; a matrix-vector product reads g once at full rate.
+    """
+    ones = torch.ones(g.size(0), dtype=g.dtype, device=g.device)
+    return torch.mv(g.t(), ones)
+
+
 def _workspace(n_slots: int, width: int, device) -> Optional[Tensor]:
     if n_slots == 0:
         return None
@@ -124,7 +134,7 @@ class _GCNAggregate(torch.autograd.Function):
         dz = None
         if ctx.needs_input_grad[0]:
             dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gy, plan.num_src, name="gcn_bwd")
-        db = gy.sum(0) if (ctx.has_bias and ctx.needs_input_grad[1]) else None
+        db = column_sum(gy) if (ctx.has_bias and ctx.needs_input_grad[1]) else None
         return dz, db, None
 
 
@@ -202,7 +212,7 @@ class _GATAttention(torch.autograd.Function):
             go = gy
         else:
             go = (gy / H).unsqueeze(1).expand(B, H, C).reshape(B, HC).contiguous()
-        db = gy.sum(0) if ctx.has_bias else None
+        db = column_sum(gy) if ctx.has_bias else None
         cdot = (go.view(B, H, C) * o.view(B, H, C)).sum(-1).contiguous()
         stream = _lib.stream_handle()
         nnz = plan.nnz

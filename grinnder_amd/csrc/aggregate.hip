@@ -160,25 +160,35 @@ __global__ __launch_bounds__(256) void aggregate_units(
   }
 }
 
-// Ordered reduction of the partial sums of split rows (one wavefront per row).
+// Ordered reduction of the partial sums of split rows: one workgroup per
+// (split row, 256-feature chunk), one thread per feature; the slot loop is
+// unrolled so its loads are independent.
 __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict__ fix,
-                                                       int64_t n_fix,
                                                        const float* __restrict__ ws, int dim,
                                                        float* __restrict__ y, int64_t ldy,
                                                        const float* __restrict__ bias) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wid =
-      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  if (wid >= n_fix) return;
-  const int row = fix[3 * wid + 0];
-  const int first = fix[3 * wid + 1];
-  const int n = fix[3 * wid + 2];
-  for (int f = lane; f < dim; f += 64) {
-    float s = 0.f;
-    for (int k = 0; k < n; ++k) s += ws[(int64_t)(first + k) * dim + f];
-    if (bias != nullptr) s += bias[f];
-    y[(int64_t)row * ldy + f] = s;
+  const int64_t r = blockIdx.x;
+  const int f = blockIdx.y * 256 + threadIdx.x;
+  if (f >= dim) return;
+  const int row = fix[3 * r + 0];
+  const int first = fix[3 * r + 1];
+  const int n = fix[3 * r + 2];
+  const float* p = ws + (int64_t)first * dim + f;
+  float s = 0.f;
+  int k = 0;
+  for (; k + 4 <= n; k += 4) {
+    const float a = p[(int64_t)(k + 0) * dim];
+    const float b = p[(int64_t)(k + 1) * dim];
+    const float c = p[(int64_t)(k + 2) * dim];
+    const float d = p[(int64_t)(k + 3) * dim];
+    s += a;
+    s += b;
+    s += c;
+    s += d;
   }
+  for (; k < n; ++k) s += p[(int64_t)k * dim];
+  if (bias != nullptr) s += bias[f];
+  y[(int64_t)row * ldy + f] = s;
 }
 
 template <int VEC, int G, int NCH>
@@ -258,9 +268,10 @@ extern "C" int gr_gcn_aggregate(const int32_t* units, int64_t n_units, const int
     err = dispatch_g<1>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, s);
   GR_HIP_CHECK(err);
   if (n_fix > 0) {
-    const int64_t blocks = (n_fix + 3) / 4;
-    hipLaunchKernelGGL(aggregate_fixup, dim3((unsigned)blocks), dim3(256), 0, s, fixups, n_fix,
-                       workspace, d, y, ldy, bias);
+    GR_REQUIRE(n_fix <= INT32_MAX, "gcn_aggregate: too many split rows");
+    const int threads = d >= 256 ? 256 : ((d + 63) / 64) * 64;
+    hipLaunchKernelGGL(aggregate_fixup, dim3((unsigned)n_fix, (unsigned)((d + 255) / 256)),
+                       dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;

@@ -31,7 +31,6 @@ from __future__ import annotations
 from typing import Dict, List, Optional
 
 import torch
-import torch.nn.functional as F
 from torch import Tensor
 from torch.utils.checkpoint import checkpoint
 
@@ -44,6 +43,13 @@ from grinnder_amd.data.graph import PartitionedGraph
 from grinnder_amd.engine.streams import StreamManager
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.utils import compute_micro_f1
+
+
+def cross_entropy(logits: Tensor, target: Tensor, reduction: str) -> Tensor:
+    """Cross-entropy as log_softmax + gather + mean/sum (the same arithmetic as
+    F.cross_entropy; its fused NLL reduction kernel is slow for millions of rows)."""
+    nll = -logits.log_softmax(dim=-1).gather(1, target.unsqueeze(1)).squeeze(1)
+    return nll.mean() if reduction == "mean" else nll.sum()
 
 
 class Trainer:
@@ -179,7 +185,7 @@ class Trainer:
         n_train = self._res("n_train", lambda: torch.tensor(int(train.sum())))
         n_train = int(n_train)
         if n_train > 0:
-            loss = F.cross_entropy(out[train], y[train], reduction="mean")
+            loss = cross_entropy(out[train], y[train], "mean")
             loss_value = float(loss.item())
         else:
             loss = out.sum() * 0.0
@@ -306,7 +312,7 @@ class Trainer:
                 test = self.graph.partition_test_mask(pid)
                 n_part = int(self.graph.partition_train_mask(pid).sum())
                 if n_part > 0:
-                    loss = F.cross_entropy(out[train], y[train], reduction="sum")
+                    loss = cross_entropy(out[train], y[train], "sum")
                     total_loss += loss.item()
                     n_train += n_part
                 else:

@@ -1,0 +1,217 @@
+"""GPU: models, autograd hooks and the Trainer (reference tests test_models.py,
+test_autograd.py, test_trainer.py, test_gradient_identity.py), with the
+reference's tolerances tightened to the north-star 1e-5 where it applies."""
+
+import copy
+
+import pytest
+import torch
+from torch.autograd.graph import saved_tensors_hooks
+
+from grinnder_amd.autograd.checkpoint import HongtuCheckpoint, ScatteredCheckpoint
+from grinnder_amd.autograd.grad_offload import GradOffload
+from grinnder_amd.buffer.device import DeviceBuffer
+from grinnder_amd.buffer.host import HostBuffer
+from grinnder_amd.config import GriNNderConfig
+from grinnder_amd.data.adjacency import Adjacency
+from grinnder_amd.data.datasets import append_self_loops, compute_gcn_norm
+from grinnder_amd.data.partition import build_partitioned_graph
+from grinnder_amd.data.synthetic import banded_graph
+from grinnder_amd.engine.streams import StreamManager
+from grinnder_amd.engine.trainer import Trainer
+from grinnder_amd.nn import GAT, GCN
+from tests.graphs import max_abs_norm_err
+
+pytestmark = pytest.mark.gpu
+
+
+# -------------------------------------------------------------- models --
+
+@pytest.fixture
+def small_adj():
+    """tests/test_models.py:13-20: 4 dst nodes, 7 source nodes."""
+    row = torch.tensor([0, 0, 1, 1, 2, 3, 3])
+    col = torch.tensor([0, 4, 1, 5, 2, 3, 6])
+    rowptr = torch.zeros(5, dtype=torch.long)
+    rowptr[1:] = torch.bincount(row, minlength=4).cumsum(0)
+    return Adjacency(rowptr, col, None, (4, 7))
+
+
+def test_model_shapes(gpu, small_adj):
+    m = GCN(16, 32, 7, num_layers=3).to(gpu)
+    assert m.forward_layer(0, torch.randn(7, 16, device=gpu), small_adj).shape == (4, 32)
+    assert m.layer_dims() == [16, 32, 32, 7]
+    g = GAT(16, 4, 7, num_layers=2, heads=8).to(gpu)
+    assert g.forward_layer(0, torch.randn(7, 16, device=gpu), small_adj).shape == (4, 32)
+    assert g.forward_layer(1, torch.randn(7, 32, device=gpu), small_adj).shape == (4, 7)
+
+
+def test_stream_manager(gpu):
+    sm = StreamManager(pool_size=2, device="cuda:0")
+    assert len(sm.h2d) == 2 and len(sm.d2h) == 2 and len(sm.act_h2d) == 2
+    assert sm.compute is not None
+
+
+def test_device_buffer(gpu):
+    buf = DeviceBuffer(3, [10, 15, 12], 8)
+    assert not buf.is_allocated(0)
+    buf.allocate(0)
+    assert buf.is_allocated(0) and buf[0].shape == (10, 8)
+    buf.allocate(1)
+    buf.reset()
+    assert buf.allocated_pids() == []
+
+
+# ------------------------------------------------------------ autograd --
+
+def test_grad_offload(gpu):
+    """tests/test_autograd.py:14-74."""
+    x = torch.randn(10, 4, device=gpu, requires_grad=True)
+    hg = HostBuffer(2, [10, 8], 4)
+    out = GradOffload.apply(x, 1, 0, hg, [None, torch.tensor([0, 1, 2])], torch.cuda.Stream(),
+                            torch.cuda.current_stream())
+    assert torch.equal(out, x)
+
+    hg = HostBuffer(2, [5, 8], 4, pin_memory=True)
+    hg.initialize_zeros()
+    d2h = torch.cuda.Stream()
+    x = torch.randn(8, 4, device=gpu, requires_grad=True)
+    out = GradOffload.apply(x, 1, 0, hg, [None, torch.tensor([0, 2, 4])], d2h,
+                            torch.cuda.current_stream())
+    (out * 2).sum().backward()
+    hg.d2h_synchronize(d2h)
+    assert torch.equal(hg[0], torch.full((5, 4), 2.0))
+    assert hg[1][[0, 2, 4]].eq(2.0).all() and hg[1][[1, 3, 5, 6, 7]].eq(0).all()
+    assert x.grad is None
+
+    hg = HostBuffer(2, [5, 5], 4)
+    hg.initialize_zeros()
+    x = torch.randn(5, 4, device=gpu, requires_grad=True)
+    out = GradOffload.apply(x, 0, 0, hg, [None, torch.empty(0, dtype=torch.long)],
+                            torch.cuda.Stream(), torch.cuda.current_stream())
+    out.sum().backward()
+    torch.cuda.synchronize()
+    assert hg[0].abs().sum() == 0 and x.grad is None
+
+
+def test_checkpoint_hooks(gpu):
+    """tests/test_autograd.py:77-106."""
+    from torch.utils.checkpoint import checkpoint
+
+    buf = DeviceBuffer(1, [5], 4)
+    buf.allocate(0)
+    assert isinstance(ScatteredCheckpoint(0, buf, torch.cuda.Stream()), saved_tensors_hooks)
+    x = torch.randn(5, 4, device=gpu, requires_grad=True)
+    with HongtuCheckpoint(0, buf):
+        y = checkpoint(lambda t: t * 3, x, use_reentrant=True)
+    y.sum().backward()
+    assert torch.equal(x.grad, torch.full((5, 4), 3.0, device=gpu))
+
+
+# ------------------------------------------------------------- trainer --
+
+def _graph_data(n=20, reach=2, feat=8, classes=3, seed=42, train_all=True):
+    """tests/test_gradient_identity.py:27-45 (banded graph, seed 42)."""
+    torch.manual_seed(seed)
+    ei = banded_graph(n, reach)
+    x = torch.randn(n, feat)
+    y = torch.randint(0, classes, (n,))
+    train = torch.ones(n, dtype=torch.bool) if train_all else torch.arange(n) < int(0.7 * n)
+    val = torch.zeros(n, dtype=torch.bool) if train_all else (torch.arange(n) >= int(0.7 * n))
+    test = torch.zeros(n, dtype=torch.bool)
+    return ei, x, y, train, val, test
+
+
+def _step(data, state, make_model, num_parts, mode, pool_size=2):
+    ei, x, y, tr, va, te = data
+    config = GriNNderConfig(num_parts=num_parts, mode=mode, pool_size=pool_size)
+    graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+    model = make_model().cuda()
+    model.load_state_dict(state)
+    trainer = Trainer(model, graph, config)
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    metrics = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()
+             if p.grad is not None}
+    return metrics["loss"], grads, trainer, graph
+
+
+def _vanilla(data, state, make_model):
+    """Dense float64 full-batch GCN (the reference's 'vanilla PyG' step)."""
+    ei, x, y, tr, _, _ = data
+    n = x.size(0)
+    w = compute_gcn_norm(ei, n, True).double()
+    full = append_self_loops(ei, n)
+    a = torch.zeros(n, n, dtype=torch.float64)
+    a.index_put_((full[0], full[1]), w, accumulate=True)
+    model = make_model().double()
+    model.load_state_dict({k: v.double() for k, v in state.items()})
+    h = x.double()
+    for i, conv in enumerate(model.convs):
+        h = a @ (h @ conv.lin.weight.t()) + conv.bias
+        if i < len(model.convs) - 1:
+            if model.norms is not None:
+                h = model.norms[i](h)
+            h = torch.relu(h)
+    loss = torch.nn.functional.cross_entropy(h[tr], y[tr])
+    loss.backward()
+    return float(loss), {k: p.grad for k, p in model.named_parameters()}
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_gcn_matches_dense_vanilla(gpu, norm):
+    data = _graph_data()
+    torch.manual_seed(7)
+    make = lambda: GCN(8, 16, 3, num_layers=2, dropout=0.0, norm=norm)  # noqa: E731
+    state = make().state_dict()
+    ref_loss, ref_grads = _vanilla(data, state, make)
+    for parts, mode in [(1, "grinnder"), (4, "grinnder"), (4, "hongtu")]:
+        loss, grads, *_ = _step(data, state, make, parts, mode)
+        assert abs(loss - ref_loss) < 1e-5, (parts, mode, loss, ref_loss)
+        for k in ref_grads:
+            assert max_abs_norm_err(grads[k], ref_grads[k]) <= 1e-5, (parts, mode, k)
+
+
+@pytest.mark.parametrize("model_kind", ["gcn", "gat"])
+@pytest.mark.parametrize("pool_size", [1, 2])
+def test_partition_invariance(gpu, model_kind, pool_size):
+    """tests/test_gradient_identity.py:290-410 at 1e-5 instead of 1e-4."""
+    data = _graph_data(n=50, reach=3, feat=16, classes=4, train_all=False)
+    torch.manual_seed(7)
+    if model_kind == "gcn":
+        make = lambda: GCN(16, 32, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
+    else:
+        make = lambda: GAT(16, 8, 4, num_layers=3, heads=2, dropout=0.0, norm=True)  # noqa
+    state = make().state_dict()
+    loss1, g1, *_ = _step(data, state, make, 1, "grinnder")
+    for parts in (2, 4, 5):
+        for mode in ("grinnder", "hongtu"):
+            loss, g, *_ = _step(data, state, make, parts, mode, pool_size)
+            assert abs(loss - loss1) < 1e-5, (parts, mode)
+            for k in g1:
+                assert max_abs_norm_err(g[k], g1[k]) <= 1e-5, (parts, mode, k)
+
+
+def test_buffers_released_and_loss_decreases(gpu):
+    """tests/test_gradient_identity.py:412-456 and tests/test_trainer.py (5 epochs)."""
+    data = _graph_data(n=50, reach=3, feat=16, classes=4, train_all=False)
+    torch.manual_seed(0)
+    for make in (lambda: GCN(16, 32, 4, num_layers=2),
+                 lambda: GAT(16, 8, 4, num_layers=2, heads=2)):
+        ei, x, y, tr, va, te = data
+        config = GriNNderConfig(num_parts=4)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.Adam(model.parameters(), lr=0.01)
+        losses = [trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())["loss"]
+                  for _ in range(5)]
+        assert losses[-1] < losses[0]
+        for buf in trainer.device_features:
+            assert buf.allocated_pids() == []
+            assert all(buf[p].grad is None for p in range(4))
+        for buf in trainer.device_gradients:
+            if buf is not None:
+                assert buf.allocated_pids() == []
+        ev = trainer.evaluate(torch.nn.CrossEntropyLoss())
+        assert 0.0 <= ev["val_acc"] <= 1.0
