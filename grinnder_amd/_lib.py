@@ -36,13 +36,15 @@ _SIGNATURES = {
     "gr_spmm_plan": [_P, _i64, _i32, _P, _P, _P, _P, _P],
     "gr_gcn_aggregate": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64, _i64, _P,
                          _i64, _P],
+    "gr_column_sum": [_P, _i64, _i64, _i64, _P, _P, _i64, _P],
     "gr_gat_scores": [_P, _i64, _i64, _i64, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_gat_softmax_stats": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _i64, _P],
     "gr_gat_aggregate": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P,
                          _P, _i64, _P, _i64, _P],
     "gr_gat_backward_src": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P, _P,
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
-    "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _i64, _i64, _P, _P, _P, _i64, _P],
+    "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
+                            _P],
     "gr_rmat_sample": [_u64, _i32, _dbl, _dbl, _dbl, _i64, _i64, _P, _P, _i32],
 }
 

@@ -82,13 +82,15 @@ def _check_device_tensor(name: str, t: Tensor) -> None:
 
 
 def column_sum(g: Tensor) -> Tensor:
-    """sum over rows of a [rows, D] fp32 matrix as one GEMV (ones^T g).
-
-    torch's generic reduction handles a tall matrix with a narrow odd width
-    (e.g. D = 47) poorly; a matrix-vector product reads g once at full rate.
-    """
-    ones = torch.ones(g.size(0), dtype=g.dtype, device=g.device)
-    return torch.mv(g.t(), ones)
+    """Sum over the rows of a [rows, D] fp32 device matrix (deterministic HIP kernel)."""
+    g = g.contiguous()
+    rows, dim = g.shape
+    out = torch.empty(dim, dtype=torch.float32, device=g.device)
+    nblk = max(1, min(1024, (rows + 2047) // 2048))
+    ws = torch.empty(nblk * dim, dtype=torch.float32, device=g.device)
+    _lib.call("gr_column_sum", g.data_ptr(), rows, dim, g.stride(0), out.data_ptr(),
+              ws.data_ptr(), ws.numel(), _lib.stream_handle())
+    return out
 
 
 def _workspace(n_slots: int, width: int, device) -> Optional[Tensor]:
@@ -237,8 +239,8 @@ class _GATAttention(torch.autograd.Function):
         ws = _workspace(f.n_slots, H, dev)
         _lib.call("gr_gat_backward_dst", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix, gt.data_ptr(),
-                  a_dst.data_ptr(), H, C, dd.data_ptr(), dhs.data_ptr(), _lib.ptr(ws),
-                  f.n_slots, stream)
+                  a_dst.data_ptr(), cdot.data_ptr(), den.data_ptr(), H, C, dd.data_ptr(),
+                  dhs.data_ptr(), _lib.ptr(ws), f.n_slots, stream)
         region.__exit__(None, None, None)
         # Attention-vector gradients: per head, ds[:,h]^T Hs[:, h] and dd[:,h]^T Hs[:B, h].
         hs3 = hs.view(E, H, C)

@@ -191,6 +191,37 @@ __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict
   y[(int64_t)row * ldy + f] = s;
 }
 
+// Column sums of a [rows, dim] matrix, two passes, fixed order: workgroup b
+// sums rows [b*chunk, (b+1)*chunk) into part[b, :]; then part is reduced over
+// b in ascending order.  Each thread owns columns f = tid, tid + 256, ...
+__global__ __launch_bounds__(256) void colsum_partial(const float* __restrict__ x, int64_t rows,
+                                                      int dim, int64_t ldx, int64_t chunk,
+                                                      float* __restrict__ part) {
+  const int64_t r0 = (int64_t)blockIdx.x * chunk;
+  const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
+  for (int f = threadIdx.x; f < dim; f += 256) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+      a0 += x[(r + 0) * ldx + f];
+      a1 += x[(r + 1) * ldx + f];
+      a2 += x[(r + 2) * ldx + f];
+      a3 += x[(r + 3) * ldx + f];
+    }
+    for (; r < r1; ++r) a0 += x[r * ldx + f];
+    part[(int64_t)blockIdx.x * dim + f] = (a0 + a1) + (a2 + a3);
+  }
+}
+
+__global__ __launch_bounds__(256) void colsum_final(const float* __restrict__ part, int nblk,
+                                                    int dim, float* __restrict__ out) {
+  const int f = blockIdx.x * 256 + threadIdx.x;
+  if (f >= dim) return;
+  float s = 0.f;
+  for (int b = 0; b < nblk; ++b) s += part[(int64_t)b * dim + f];
+  out[f] = s;
+}
+
 template <int VEC, int G, int NCH>
 hipError_t launch_units(const int4* units, int64_t n_units, const int32_t* idx,
                         const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
@@ -274,5 +305,27 @@ extern "C" int gr_gcn_aggregate(const int32_t* units, int64_t n_units, const int
                        dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias);
     GR_HIP_CHECK(hipGetLastError());
   }
+  return GR_OK;
+}
+
+extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx, float* out,
+                             float* workspace, int64_t workspace_floats, void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(rows >= 0 && dim >= 1 && ldx >= dim, "column_sum: bad shape");
+  GR_REQUIRE(out != nullptr && (rows == 0 || x != nullptr), "column_sum: NULL pointer");
+  hipStream_t s = gr::as_stream(stream);
+  const int64_t nblk_max = workspace_floats / dim;
+  GR_REQUIRE(workspace != nullptr && nblk_max >= 1,
+             "column_sum: workspace must hold at least dim floats");
+  int64_t nblk = rows == 0 ? 1 : (rows + 2047) / 2048;  // ~2048 rows per workgroup
+  if (nblk > 1024) nblk = 1024;
+  if (nblk > nblk_max) nblk = nblk_max;
+  const int64_t chunk = rows == 0 ? 0 : (rows + nblk - 1) / nblk;
+  hipLaunchKernelGGL(gr_agg::colsum_partial, dim3((unsigned)nblk), dim3(256), 0, s, x, rows, (int)dim,
+                     ldx, chunk, workspace);
+  GR_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, s,
+                     workspace, (int)nblk, (int)dim, out);
+  GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }

@@ -276,9 +276,15 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 //   alpha = exp(LeakyReLU(s_j + d_i) - m_i) / den_i
 //   g_alpha = <GO_i, Hs_j>  (per head);  g_e = alpha (g_alpha - c_i)
 //   g_t = g_e * (t > 0 ? 1 : 0.2)
-//   dHs_j += alpha GO_i;  ds_j += g_t;  gt[csr position of e] = g_t
+//   dHs_j += alpha GO_i;  ds_j += g_t;  gdd[csr position of e] = g_e * (t > 0 ? 0 : -0.8)
 // and finally dHs_j += ds_j * att_src.  c_i = <GO_i, O_i> per head equals
 // sum_k alpha_ik g_alpha_ik.
+//
+// gdd feeds dd_i = sum_j g_t,ij.  Softmax is invariant to a shift of row i's
+// logits, so sum_j g_e,ij = c_i (1 - sum_j alpha_ij) = c_i * 1e-16 / den_i
+// exactly; summing g_t directly would cancel to fp32 noise.  The destination
+// pass therefore forms dd_i = sum_j g_e,ij (slope_ij - 1) + c_i * 1e-16 / den_i,
+// the same value without the cancellation.
 template <int VEC, int NCH, int U>
 __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
@@ -371,12 +377,13 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
         const int64_t ih = i * H + hd[ch];
         const float tt = sj[ch] + d[ih];
         const float a = expf(leaky(tt) - m[ih]) / den[ih];
-        const float gtv = a * (ga[ch] - cdot[ih]) * (tt > 0.f ? 1.f : 0.2f);
+        const float ge = a * (ga[ch] - cdot[ih]);
+        const bool pos = tt > 0.f;
         if (ok[k]) {
-          dsl[ch] += gtv;
+          dsl[ch] += pos ? ge : 0.2f * ge;
 #pragma unroll
           for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a, g[k][ch][q], acc[ch][q]);
-          if (head_lead[ch]) gt[(int64_t)perm[e + k] * H + hd[ch]] = gtv;
+          if (head_lead[ch]) gt[(int64_t)perm[e + k] * H + hd[ch]] = pos ? 0.f : -0.8f * ge;
         }
       }
     }
@@ -432,13 +439,16 @@ __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restri
   }
 }
 
-// Row-parallel (CSR) pass over destination rows i: dd[i,h] = sum_e gt[e,h]
-// and dHs[i,:] += dd[i,h(f)] * att_dst[f].
+// Row-parallel (CSR) pass over destination rows i:
+// dd[i,h] = sum_e gdd[e,h] + c[i,h] * 1e-16 / den[i,h] and
+// dHs[i,:] += dd[i,h(f)] * att_dst[f].
 __global__ __launch_bounds__(256) void gat_bwd_dst_kernel(const int4* __restrict__ units,
                                                           int64_t n_units,
                                                           const float* __restrict__ gt, int H,
                                                           int C,
                                                           const float* __restrict__ att_dst,
+                                                          const float* __restrict__ cdot,
+                                                          const float* __restrict__ den,
                                                           float* __restrict__ dd,
                                                           float* __restrict__ dhs,
                                                           float* __restrict__ ws) {
@@ -452,6 +462,10 @@ __global__ __launch_bounds__(256) void gat_bwd_dst_kernel(const int4* __restrict
     float p = 0.f;
     for (int e = w.y + lane; e < w.z; e += 64) p += gt[(int64_t)e * H + h];
     part[h] = wave_sum(p);
+    if (w.w < 0) {
+      const int64_t ih = (int64_t)w.x * H + h;
+      part[h] += cdot[ih] * (1e-16f / den[ih]);
+    }
   }
   if (w.w < 0) {
     if (lane < H) {
@@ -481,6 +495,8 @@ __global__ __launch_bounds__(256) void gat_bwd_dst_fixup(const int32_t* __restri
                                                          const float* __restrict__ ws, int H,
                                                          int C,
                                                          const float* __restrict__ att_dst,
+                                                         const float* __restrict__ cdot,
+                                                         const float* __restrict__ den,
                                                          float* __restrict__ dd,
                                                          float* __restrict__ dhs) {
   const int lane = threadIdx.x & 63;
@@ -492,6 +508,8 @@ __global__ __launch_bounds__(256) void gat_bwd_dst_fixup(const int32_t* __restri
     const int h = f / C;
     float v = 0.f;
     for (int k = 0; k < n; ++k) v += ws[(int64_t)(first + k) * H + h];
+    const int64_t ih = (int64_t)row * H + h;
+    v += cdot[ih] * (1e-16f / den[ih]);
     float* p = dhs + (int64_t)row * HC + f;
     *p = fmaf(v, att_dst[f], *p);
     if (f == h * C) dd[(int64_t)row * H + h] = v;
@@ -686,23 +704,24 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
 
 extern "C" int gr_gat_backward_dst(const int32_t* units, int64_t n_units, const int32_t* fixups,
                                    int64_t n_fix, const float* gt, const float* att_dst,
-                                   int64_t heads, int64_t channels, float* dd, float* dhs,
-                                   float* workspace, int64_t n_slots, void* stream) {
+                                   const float* cdot, const float* den, int64_t heads,
+                                   int64_t channels, float* dd, float* dhs, float* workspace,
+                                   int64_t n_slots, void* stream) {
   gr::clear_error();
   int rc = check_heads(heads, channels);
   if (rc) return rc;
   GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_backward_dst: NULL fixups/workspace");
   if (n_units == 0) return GR_OK;
-  GR_REQUIRE(units && aligned16(units) && gt && att_dst && dd && dhs,
+  GR_REQUIRE(units && aligned16(units) && gt && att_dst && cdot && den && dd && dhs,
              "gat_backward_dst: NULL or misaligned pointer");
   hipStream_t st = gr::as_stream(stream);
   hipLaunchKernelGGL(gat_bwd_dst_kernel, dim3(blocks_for(n_units)), dim3(256), 0, st,
                      reinterpret_cast<const int4*>(units), n_units, gt, (int)heads, (int)channels,
-                     att_dst, dd, dhs, workspace);
+                     att_dst, cdot, den, dd, dhs, workspace);
   GR_HIP_CHECK(hipGetLastError());
   if (n_fix > 0) {
     hipLaunchKernelGGL(gat_bwd_dst_fixup, dim3(blocks_for(n_fix)), dim3(256), 0, st, fixups,
-                       n_fix, workspace, (int)heads, (int)channels, att_dst, dd, dhs);
+                       n_fix, workspace, (int)heads, (int)channels, att_dst, cdot, den, dd, dhs);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;

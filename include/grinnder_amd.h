@@ -189,6 +189,14 @@ int gr_gcn_aggregate(const int32_t* units, int64_t n_units,
                      int64_t rows, int64_t dim, float* workspace,
                      int64_t n_slots, void* stream);
 
+/* Bias gradient of the GCN layer, db = sum_i G[i, :D] (fp32, deterministic:
+ * fixed row chunks, partials reduced in chunk order).  Replaces the bias
+ * gradient of PyG GCNConv's "+ bias" (grinnder/nn/gcn.py:53-56).
+ * workspace: at least D floats (up to 1024 * D are used for parallelism). */
+int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
+                  float* out, float* workspace, int64_t workspace_floats,
+                  void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GAT attention (device)                                                    */
 /*                                                                           */
@@ -230,9 +238,11 @@ int gr_gat_aggregate(const int32_t* units, int64_t n_units,
 
 /* Backward over source rows j (CSC plan, row_idx/perm from
  * gr_csr_transpose).  go = dL/dO [B, H*C]; cdot[i,h] = <go_i,h, O_i,h>.
- * Writes dhs [E, H*C] = sum_i alpha_ij go_i + ds_j * att_src,
- * ds [E,H] = sum_i g_t,ij and gt [nnz,H] (CSR order) = g_t per edge, where
- * g_t = alpha (<go_i, Hs_j> - cdot_i) * (t > 0 ? 1 : 0.2).
+ * With g_e = alpha (<go_i, Hs_j> - cdot_i) and g_t = g_e * (t > 0 ? 1 : 0.2),
+ * writes dhs [E, H*C] = sum_i alpha_ij go_i + ds_j * att_src,
+ * ds [E,H] = sum_i g_t,ij and gt [nnz,H] (CSR order) = g_e * (t > 0 ? 0 : -0.8),
+ * the per-edge part of dd_i = sum_j g_t,ij left after the exact softmax
+ * shift-invariance identity sum_j g_e,ij = cdot_i * 1e-16 / den_i.
  * workspace: n_slots * (round_up(H*C, 4) + round_up(H, 4)) floats. */
 int gr_gat_backward_src(const int32_t* units, int64_t n_units,
                         const int32_t* fixups, int64_t n_fix,
@@ -244,12 +254,14 @@ int gr_gat_backward_src(const int32_t* units, int64_t n_units,
                         float* dhs, float* ds, float* gt, float* workspace,
                         int64_t n_slots, void* stream);
 
-/* Backward over destination rows i (CSR plan): dd[i,h] = sum_e gt[e,h] and
+/* Backward over destination rows i (CSR plan):
+ * dd[i,h] = sum_e gt[e,h] + cdot[i,h] * 1e-16 / den[i,h] (= sum_j g_t,ij) and
  * dhs[i,:] += dd[i,h(f)] * att_dst[f].  Must run after
  * gr_gat_backward_src on the same stream.  workspace: n_slots * H floats. */
 int gr_gat_backward_dst(const int32_t* units, int64_t n_units,
                         const int32_t* fixups, int64_t n_fix, const float* gt,
-                        const float* att_dst, int64_t heads, int64_t channels,
+                        const float* att_dst, const float* cdot,
+                        const float* den, int64_t heads, int64_t channels,
                         float* dd, float* dhs, float* workspace,
                         int64_t n_slots, void* stream);
 

@@ -44,4 +44,24 @@ def max_abs_norm_err(got, ref) -> float:
     return diff / scale if scale > 0 else diff
 
 
+def grad_errs(grads, ref_grads, floor_frac: float = 1e-2):
+    """Per-parameter max-abs error normalised by max(|ref param|max,
+    floor_frac * largest |ref| gradient of the model).
+
+    The floor matters for parameters whose true gradient is (nearly) zero by
+    an invariance — e.g. GAT's destination attention vector, which only acts
+    through the LeakyReLU kink because softmax is shift-invariant — where
+    per-tensor normalisation would divide fp32 rounding noise by ~0.  With the
+    1e-5 bound, such a parameter may be off by at most 1e-7 of the model's
+    largest gradient (about two fp32 ulps of it)."""
+    scale = max(float(torch.as_tensor(r).abs().max()) for r in ref_grads.values())
+    out = {}
+    for k, r in ref_grads.items():
+        r = torch.as_tensor(r, dtype=torch.float64).cpu()
+        g = torch.as_tensor(grads[k], dtype=torch.float64).cpu()
+        denom = max(float(r.abs().max()), floor_frac * scale)
+        out[k] = float((g - r).abs().max()) / denom
+    return out
+
+
 TOL = 1e-5

@@ -82,3 +82,15 @@ def test_gcn_rejects_cpu_tensors():
     adj = Adjacency(rowptr, col, val, (10, 10))
     with pytest.raises(RuntimeError):
         gcn_aggregate(torch.randn(10, 4), adj)
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 1), (1000, 47), (300000, 256), (5000, 1000)])
+def test_column_sum_matches_float64(gpu, rows, dim):
+    from grinnder_amd.aggregation import column_sum
+
+    x = torch.randn(rows, dim, generator=torch.Generator().manual_seed(rows))
+    got = column_sum(x.to(gpu))
+    again = column_sum(x.to(gpu))
+    torch.cuda.synchronize()
+    assert max_abs_norm_err(got, x.double().sum(0)) <= TOL
+    assert torch.equal(got, again)
