@@ -27,6 +27,7 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
+CONFIGS_NAMES = ("c1", "c2", "c3", "c4", "c5")
 
 
 def log(msg: str) -> None:
@@ -38,7 +39,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", choices=["c1", "c2"], default="c2")
+    ap.add_argument("--config", choices=sorted(CONFIGS_NAMES), default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
@@ -51,11 +52,23 @@ def parse_args():
 
 CONFIGS = {
     "c2": dict(workload="products-scale GCN (BASELINE configs[1])", num_nodes=2_449_029,
-               undirected_edges=61_859_140, scale=22, feat_dim=100, hidden=256,
-               num_classes=47, num_layers=3, num_parts=1),
-    "c1": dict(workload="CPU-runnable plumbing GCN (BASELINE configs[0]) at num_parts=1",
-               num_nodes=10_000, undirected_edges=50_000, scale=None, feat_dim=128, hidden=64,
-               num_classes=10, num_layers=2, num_parts=1),
+               edges=61_859_140, undirected=True, scale=22, feat_dim=100, hidden=256,
+               num_classes=47, num_layers=3, num_parts=1, model="gcn"),
+    "c3": dict(workload="products-scale GCN, 16 partitions, pinned host halos "
+                        "(BASELINE configs[2])", num_nodes=2_449_029, edges=61_859_140,
+               undirected=True, scale=22, feat_dim=100, hidden=256, num_classes=47,
+               num_layers=3, num_parts=16, model="gcn"),
+    "c4": dict(workload="10M-node R-MAT GCN, dim 1024, 16 partitions (BASELINE configs[3])",
+               num_nodes=10_000_000, edges=120_000_000, undirected=False, scale=24,
+               feat_dim=1024, hidden=256, num_classes=19, num_layers=3, num_parts=16,
+               model="gcn", lazy_features=True),
+    "c5": dict(workload="10M-node R-MAT GAT h256 heads 1, 64 partitions (BASELINE configs[4])",
+               num_nodes=10_000_000, edges=120_000_000, undirected=False, scale=24,
+               feat_dim=1024, hidden=256, num_classes=19, num_layers=2, num_parts=64,
+               model="gat", lazy_features=True),
+    "c1": dict(workload="CPU-runnable plumbing GCN (BASELINE configs[0])", num_nodes=10_000,
+               edges=50_000, undirected=True, scale=None, feat_dim=128, hidden=64,
+               num_classes=10, num_layers=2, num_parts=2, model="gcn"),
 }
 
 
@@ -68,19 +81,26 @@ def build_graph(cfg, device):
 
     t0 = time.perf_counter()
     if cfg["scale"] is None:
-        ei = synthetic.uniform_graph(cfg["num_nodes"], cfg["undirected_edges"], seed=42)
+        ei = synthetic.uniform_graph(cfg["num_nodes"], cfg["edges"], seed=42)
     else:
-        ei = synthetic.rmat_graph(cfg["num_nodes"], cfg["undirected_edges"], scale=cfg["scale"],
-                                  seed=42, device=device)
+        ei = synthetic.rmat_graph(cfg["num_nodes"], cfg["edges"], scale=cfg["scale"], seed=42,
+                                  undirected=cfg["undirected"], device=device)
     log(f"graph: {ei.size(1)} directed edges in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
-    nd = synthetic.node_data(cfg["num_nodes"], cfg["feat_dim"], cfg["num_classes"], seed=42)
+    n = cfg["num_nodes"]
+    if cfg.get("lazy_features"):
+        nd = synthetic.node_data(n, 1, cfg["num_classes"], seed=42)
+        x = synthetic.SyntheticFeatures(n, cfg["feat_dim"], seed=42)
+    else:
+        nd = synthetic.node_data(n, cfg["feat_dim"], cfg["num_classes"], seed=42)
+        x = nd.x
     config = GriNNderConfig(num_parts=cfg["num_parts"], device=device)
-    graph = build_partitioned_graph(ei, nd.x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
+    graph = build_partitioned_graph(ei, x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
                                     config)
     del ei
-    log(f"partitioned graph (P={cfg['num_parts']}, nnz={graph.adj_csr[0][1].numel()}) "
-        f"in {time.perf_counter() - t0:.1f}s")
+    nnz = sum(int(a[1].numel()) for a in graph.adj_csr)
+    log(f"partitioned graph (P={cfg['num_parts']}, nnz={nnz}, halo amplification "
+        f"{graph.halo_amplification():.3f}) in {time.perf_counter() - t0:.1f}s")
     return graph, config
 
 
@@ -166,7 +186,7 @@ def main():
     from grinnder_amd import _lib
     from grinnder_amd.aggregation import KernelTimer
     from grinnder_amd.engine.trainer import Trainer
-    from grinnder_amd.nn.gcn import GCN
+    from grinnder_amd.nn import GAT, GCN
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -176,17 +196,24 @@ def main():
     device = "cuda:0"
     cfg = CONFIGS[args.config]
     graph, config = build_graph(cfg, device)
-    nnz = int(graph.adj_csr[0][1].numel())
+    nnz = sum(int(a[1].numel()) for a in graph.adj_csr)
 
     torch.manual_seed(42)
-    model = GCN(cfg["feat_dim"], cfg["hidden"], cfg["num_classes"], cfg["num_layers"],
-                dropout=0.0, norm=True).to(device)
+    if cfg["model"] == "gcn":
+        model = GCN(cfg["feat_dim"], cfg["hidden"], cfg["num_classes"], cfg["num_layers"],
+                    dropout=0.0, norm=True).to(device)
+    else:
+        model = GAT(cfg["feat_dim"], cfg["hidden"], cfg["num_classes"], cfg["num_layers"],
+                    heads=1, dropout=0.0, norm=True).to(device)
+    t0 = time.perf_counter()
     trainer = Trainer(model, graph, config)
+    log(f"trainer (host buffers, prefill) in {time.perf_counter() - t0:.1f}s")
     opt = torch.optim.Adam(model.parameters(), lr=0.01, weight_decay=5e-4)
     crit = torch.nn.CrossEntropyLoss()
 
     t0 = time.perf_counter()
-    graph.adjacency(0).device_plan(device)
+    for pid in range(graph.num_parts):
+        graph.adjacency(pid).device_plan(device)
     torch.cuda.synchronize()
     log(f"device plans (CSR + CSC) in {time.perf_counter() - t0:.1f}s")
     for w in range(args.warmup):
@@ -206,11 +233,12 @@ def main():
     log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f})")
 
     recs = timer.records
-    agg_ms = sum(r.ms() for r in recs)
-    agg_bytes = sum(r.nbytes for r in recs)
+    agg_ms = sum(r.ms() for r in recs if r.name.startswith(("gcn_", "gat_")))
+    agg_bytes = sum(r.nbytes for r in recs if r.name.startswith(("gcn_", "gat_")))
     useful_edges = 2 * cfg["num_layers"] * nnz * args.steps
     epoch_s = wall / args.steps
-    dom = [r for r in recs if r.dim == cfg["hidden"]]
+    recs_agg = [r for r in recs if r.name.startswith(("gcn_", "gat_"))]
+    dom = [r for r in recs_agg if r.dim == cfg["hidden"]]
     dom_ms = sum(r.ms() for r in dom)
     dom_bytes = sum(r.nbytes for r in dom)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
@@ -246,11 +274,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded R-MAT graph, N(0,1) features, uniform labels)",
+        "data": "synthetic (seeded graph, N(0,1) features, uniform labels)",
         "config": {"workload": cfg["workload"], "num_nodes": cfg["num_nodes"],
                    "nnz": nnz, "feat_dim": cfg["feat_dim"], "hidden": cfg["hidden"],
                    "num_classes": cfg["num_classes"], "num_layers": cfg["num_layers"],
-                   "num_parts": cfg["num_parts"]},
+                   "num_parts": cfg["num_parts"], "model": cfg["model"],
+                   "halo_amplification": round(graph.halo_amplification(), 4)},
         "epoch_s": round(epoch_s, 5),
         "agg_kernel_gteps": round(useful_edges / (agg_ms / 1e3) / 1e9, 4),
         "agg_hbm_frac": round(agg_bytes / (agg_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -258,7 +287,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": None,
-                     "kernel": f"aggregate_units (GCN SpMM, D={cfg['hidden']}, fwd CSR + bwd CSC)"},
+                     "kernel": (f"aggregate_units (GCN SpMM, D={cfg['hidden']}, fwd CSR + bwd CSC)"
+                                if cfg["model"] == "gcn" else
+                                f"GAT attention fwd+bwd kernels, H*C={cfg['hidden']}")},
         "cpu_baseline": cpu,
         "passes": passes,
     }

@@ -26,6 +26,7 @@ import torch
 from torch import Tensor
 
 from grinnder_amd import _lib
+from grinnder_amd.aggregation import KernelTimer
 from grinnder_amd.data.partition import build_subgraph  # noqa: F401  (re-export)
 
 __all__ = [
@@ -118,8 +119,9 @@ def gather_partitions(pid: int, srcs: List[Tensor], dst: Tensor,
     keep, bptr, blen = _boundary_arrays(pid, boundaries, P)
     src_ptrs = _lib.ptr_array([s.data_ptr() if s.numel() else None for s in srcs])
     src_rows = _lib.i64_array([s.size(0) if s.dim() else 0 for s in srcs])
-    _lib.call("gr_gather_partitions", pid, P, src_ptrs, src_rows, dst.data_ptr(),
-              dst.size(0), max(row_bytes, 1), bptr, blen, stream.cuda_stream)
+    with KernelTimer.region("halo_gather", dst.size(0) * row_bytes, 0, row_bytes // 4):
+        _lib.call("gr_gather_partitions", pid, P, src_ptrs, src_rows, dst.data_ptr(),
+                  dst.size(0), max(row_bytes, 1), bptr, blen, stream.cuda_stream)
     del keep
 
 
@@ -139,6 +141,7 @@ def scatter_partitions(pid: int, src: Tensor, dsts: List[Tensor],
     keep, bptr, blen = _boundary_arrays(pid, boundaries, P)
     dst_ptrs = _lib.ptr_array([d.data_ptr() if d.numel() else None for d in dsts])
     dst_rows = _lib.i64_array([d.size(0) for d in dsts])
-    _lib.call("gr_scatter_partitions", pid, P, src.data_ptr(), src.size(0), max(dim, 1),
-              dst_ptrs, dst_rows, bptr, blen, stream.cuda_stream)
+    with KernelTimer.region("halo_scatter", src.numel() * 4, 0, dim):
+        _lib.call("gr_scatter_partitions", pid, P, src.data_ptr(), src.size(0), max(dim, 1),
+                  dst_ptrs, dst_rows, bptr, blen, stream.cuda_stream)
     del keep

@@ -32,6 +32,7 @@ _SIGNATURES = {
     "gr_scatter_partitions": [_i32, _i32, _P, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_build_subgraph": [_P, _P, _P, _i64, _i64, _P, _i64, _i32, _P, _P, _P, _P, _P, _P],
     "gr_partition_boundaries": [_i32, _i32, _P, _i64, _P, _i64, _P, _i64, _P, _P],
+    "gr_partition_graph": [_P, _P, _i64, _i64, _i32, _dbl, _i32, _P, _P],
     "gr_csr_transpose": [_P, _P, _P, _i64, _i64, _P, _P, _P, _P],
     "gr_spmm_plan": [_P, _i64, _i32, _P, _P, _P, _P, _P],
     "gr_gcn_aggregate": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64, _i64, _P,
@@ -46,6 +47,7 @@ _SIGNATURES = {
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],
     "gr_rmat_sample": [_u64, _i32, _dbl, _dbl, _dbl, _i64, _i64, _P, _P, _i32],
+    "gr_gaussian_rows": [_u64, _P, _i64, _i64, _P, _i32],
 }
 
 EXPORTED = tuple(_SIGNATURES) + ("gr_last_error", "gr_abi_version")

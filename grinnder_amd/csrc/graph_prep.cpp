@@ -5,6 +5,7 @@
 // (CSR->CSC transpose, work plans).  It runs once per partition adjacency,
 // never inside the training loop.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <thread>
 #include <vector>
@@ -337,6 +338,168 @@ extern "C" int gr_rmat_sample(uint64_t seed, int32_t scale, double a, double b,
   int32_t nt = nthreads > 0 ? nthreads : static_cast<int32_t>(std::thread::hardware_concurrency());
   if (nt < 1) nt = 1;
   if (n < (int64_t)1 << 16) nt = 1;
+  if (nt == 1) {
+    work(0, n);
+    return GR_OK;
+  }
+  std::vector<std::thread> pool;
+  const int64_t chunk = (n + nt - 1) / nt;
+  for (int32_t t = 0; t < nt; ++t) {
+    const int64_t lo = t * chunk, hi = std::min<int64_t>(n, lo + chunk);
+    if (lo >= hi) break;
+    pool.emplace_back(work, lo, hi);
+  }
+  for (auto& th : pool) th.join();
+  return GR_OK;
+}
+
+// ------------------------------------------------------------ partitioner --
+//
+// The reference delegates partitioning to grdpart (not available).  This is
+// the library's own deterministic partitioner:
+//   1. undirected adjacency of the COO graph (both directions, counting sort),
+//   2. breadth-first order (components visited in id order, neighbours in
+//      adjacency order) — or the natural id order,
+//   3. linear deterministic greedy streaming assignment in that order:
+//      p* = argmax_p |N(v) ∩ P_p| * (1 - |P_p| / cap), cap = ceil(capacity*n/P),
+//      ties -> lighter partition, then lower id; full partitions are skipped,
+//   4. perm = nodes grouped by partition, each group in visit order (so a
+//      partition's rows are also BFS-local), ptr = group offsets.
+extern "C" int gr_partition_graph(const int64_t* src, const int64_t* dst, int64_t m, int64_t n,
+                                  int32_t num_parts, double capacity, int32_t bfs_order,
+                                  int64_t* perm, int64_t* ptr) {
+  gr::clear_error();
+  GR_REQUIRE(n >= 1 && n <= INT32_MAX && m >= 0, "partition_graph: bad sizes");
+  GR_REQUIRE(num_parts >= 1 && num_parts <= 4096 && num_parts <= n,
+             "partition_graph: num_parts %d invalid for %lld nodes", num_parts, (long long)n);
+  GR_REQUIRE(capacity >= 1.0, "partition_graph: capacity must be >= 1");
+  GR_REQUIRE(m == 0 || (src != nullptr && dst != nullptr), "partition_graph: NULL edges");
+  GR_REQUIRE(perm != nullptr && ptr != nullptr, "partition_graph: NULL outputs");
+
+  // 1. symmetric adjacency (self-loops dropped), int32 ids.
+  std::vector<int64_t> off(static_cast<size_t>(n) + 1, 0);
+  for (int64_t e = 0; e < m; ++e) {
+    const int64_t a = src[e], b = dst[e];
+    GR_REQUIRE(a >= 0 && a < n && b >= 0 && b < n, "partition_graph: edge (%lld, %lld) out of range",
+               (long long)a, (long long)b);
+    if (a == b) continue;
+    ++off[a + 1];
+    ++off[b + 1];
+  }
+  for (int64_t v = 0; v < n; ++v) off[v + 1] += off[v];
+  std::vector<int32_t> adj(static_cast<size_t>(off[n]));
+  {
+    std::vector<int64_t> fill(off.begin(), off.end() - 1);
+    for (int64_t e = 0; e < m; ++e) {
+      const int64_t a = src[e], b = dst[e];
+      if (a == b) continue;
+      adj[fill[a]++] = static_cast<int32_t>(b);
+      adj[fill[b]++] = static_cast<int32_t>(a);
+    }
+  }
+
+  // 2. visit order.
+  std::vector<int32_t> order(static_cast<size_t>(n));
+  if (bfs_order) {
+    std::vector<uint8_t> seen(static_cast<size_t>(n), 0);
+    int64_t head = 0, tail = 0;
+    for (int64_t s = 0; s < n; ++s) {
+      if (seen[s]) continue;
+      seen[s] = 1;
+      order[tail++] = static_cast<int32_t>(s);
+      while (head < tail) {
+        const int32_t v = order[head++];
+        for (int64_t k = off[v]; k < off[v + 1]; ++k) {
+          const int32_t u = adj[k];
+          if (!seen[u]) {
+            seen[u] = 1;
+            order[tail++] = u;
+          }
+        }
+      }
+    }
+  } else {
+    for (int64_t v = 0; v < n; ++v) order[v] = static_cast<int32_t>(v);
+  }
+
+  // 3. greedy assignment.
+  const int32_t P = num_parts;
+  std::vector<int32_t> part(static_cast<size_t>(n), -1);
+  std::vector<int64_t> load(P, 0);
+  const int64_t cap = static_cast<int64_t>(std::ceil(capacity * static_cast<double>(n) / P));
+  std::vector<int64_t> cnt(P, 0);
+  std::vector<int32_t> touched;
+  touched.reserve(P);
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t v = order[i];
+    touched.clear();
+    for (int64_t k = off[v]; k < off[v + 1]; ++k) {
+      const int32_t q = part[adj[k]];
+      if (q < 0) continue;
+      if (cnt[q]++ == 0) touched.push_back(q);
+    }
+    int32_t best = -1;
+    double best_score = -1.0;
+    for (int32_t q : touched) {
+      if (load[q] >= cap) continue;
+      const double score = static_cast<double>(cnt[q]) *
+                           (1.0 - static_cast<double>(load[q]) / static_cast<double>(cap));
+      if (score > best_score || (score == best_score &&
+                                 (load[q] < load[best] || (load[q] == load[best] && q < best)))) {
+        best = q;
+        best_score = score;
+      }
+    }
+    for (int32_t q : touched) cnt[q] = 0;
+    if (best < 0 || best_score <= 0.0) {
+      best = 0;
+      for (int32_t q = 1; q < P; ++q)
+        if (load[q] < load[best]) best = q;
+    }
+    part[v] = best;
+    ++load[best];
+  }
+
+  // 4. group by partition, keeping visit order inside each group.
+  ptr[0] = 0;
+  for (int32_t q = 0; q < P; ++q) ptr[q + 1] = ptr[q] + load[q];
+  std::vector<int64_t> pos(ptr, ptr + P);
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t v = order[i];
+    perm[pos[part[v]]++] = v;
+  }
+  return GR_OK;
+}
+
+// Counter-based N(0,1) rows: out[i, j] depends only on (seed, ids[i], j), so a
+// partition's feature rows can be produced on demand, in any order, by any
+// number of threads.  Uniforms from the SplitMix64 mixer, normals by the
+// Box-Muller transform on (j & ~1, j | 1) pairs.
+extern "C" int gr_gaussian_rows(uint64_t seed, const int64_t* ids, int64_t n, int64_t dim,
+                                float* out, int32_t nthreads) {
+  gr::clear_error();
+  GR_REQUIRE(n >= 0 && dim >= 1, "gaussian_rows: bad shape");
+  GR_REQUIRE(n == 0 || (ids != nullptr && out != nullptr), "gaussian_rows: NULL pointer");
+  const uint64_t key = mix64(seed ^ 0xD1B54A32D192ED03ull);
+  auto work = [&](int64_t lo, int64_t hi) {
+    for (int64_t i = lo; i < hi; ++i) {
+      const uint64_t row = static_cast<uint64_t>(ids[i]);
+      float* o = out + i * dim;
+      for (int64_t j = 0; j < dim; j += 2) {
+        const uint64_t h = mix64(key + 0x9E3779B97F4A7C15ull * (row * 0x100000001B3ull + static_cast<uint64_t>(j >> 1) + 1));
+        // 24-bit uniforms in (0, 1] and [0, 1).
+        const double u1 = (static_cast<double>(h >> 40) + 1.0) / 16777216.0;
+        const double u2 = static_cast<double>((h >> 16) & 0xFFFFFF) / 16777216.0;
+        const double r = std::sqrt(-2.0 * std::log(u1));
+        const double t = 6.283185307179586 * u2;
+        o[j] = static_cast<float>(r * std::cos(t));
+        if (j + 1 < dim) o[j + 1] = static_cast<float>(r * std::sin(t));
+      }
+    }
+  };
+  int32_t nt = nthreads > 0 ? nthreads : static_cast<int32_t>(std::thread::hardware_concurrency());
+  if (nt < 1) nt = 1;
+  if (n * dim < (int64_t)1 << 18) nt = 1;
   if (nt == 1) {
     work(0, n);
     return GR_OK;

@@ -117,14 +117,16 @@ def _build_partition_subgraph(pid: int, ptr: Tensor, rowptr: Tensor, col: Tensor
 
 
 def partition_nodes(edge_index: Tensor, num_nodes: int, num_parts: int,
-                    partitioner: str = "grinnder", **kwargs) -> Tuple[Tensor, Tensor]:
+                    partitioner: str = "grinnder", capacity: float = 1.1,
+                    order: str = "bfs", **_unused) -> Tuple[Tensor, Tensor]:
     """Returns (perm, ptr): new position -> old node id, and partition pointers.
 
     grdpart is not available, so both partitioner names map to this package's
-    deterministic partitioner: nodes keep their id order and are cut into
-    num_parts contiguous, balanced ranges (ids are assumed to carry locality,
-    as for banded graphs; partition quality only changes halo size, never
-    results, since full-graph training is partition-invariant).
+    deterministic partitioner (gr_partition_graph): breadth-first visit order
+    (``order="bfs"``; ``"natural"`` keeps id order) and linear deterministic
+    greedy assignment under ``capacity`` (the reference's partitioner_kwargs
+    key).  Partition quality changes only halo sizes, never results: training
+    is partition-invariant.
     """
     if partitioner not in ("grinnder", "spinner"):
         raise ValueError(
@@ -133,11 +135,15 @@ def partition_nodes(edge_index: Tensor, num_nodes: int, num_parts: int,
         )
     if num_parts < 1 or num_parts > max(1, num_nodes):
         raise ValueError(f"num_parts={num_parts} invalid for {num_nodes} nodes")
-    perm = torch.arange(num_nodes, dtype=torch.long)
-    base, rem = divmod(num_nodes, num_parts)
-    sizes = [base + (1 if p < rem else 0) for p in range(num_parts)]
-    ptr = torch.zeros(num_parts + 1, dtype=torch.long)
-    ptr[1:] = torch.tensor(sizes, dtype=torch.long).cumsum(0)
+    if order not in ("bfs", "natural"):
+        raise ValueError(f"unknown visit order {order!r}")
+    ei = edge_index.to(torch.int64)
+    src = ei[0].contiguous()
+    dst = ei[1].contiguous()
+    perm = torch.empty(num_nodes, dtype=torch.int64)
+    ptr = torch.empty(num_parts + 1, dtype=torch.int64)
+    _lib.call("gr_partition_graph", src.data_ptr(), dst.data_ptr(), src.numel(), num_nodes,
+              num_parts, float(capacity), int(order == "bfs"), perm.data_ptr(), ptr.data_ptr())
     return perm, ptr
 
 

@@ -135,3 +135,54 @@ def node_data(num_nodes: int, feat_dim: int, num_classes: int, seed: int = 42,
     val[order[n_tr:n_tr + n_va]] = True
     test[order[n_tr + n_va:]] = True
     return NodeData(x, y, train, val, test)
+
+
+class SyntheticFeatures:
+    """A [num_nodes, dim] N(0,1) fp32 feature matrix that is never materialised.
+
+    Row v is generated from (seed, v) by gr_gaussian_rows, so partitions are
+    produced on demand (the role of the reference's memory-mapped
+    NumpyFeatureStore, grinnder/data/datasets.py:59-100): ``partition(start,
+    end)`` returns the rows at new positions [start, end) after
+    ``with_permutation(perm)``.
+    """
+
+    def __init__(self, num_nodes: int, dim: int, seed: int = 42,
+                 perm: Optional[Tensor] = None):
+        self.num_nodes = num_nodes
+        self.dim = dim
+        self.seed = seed
+        self.perm = perm
+
+    @property
+    def shape(self):
+        return (self.num_nodes, self.dim)
+
+    def size(self, i: Optional[int] = None):
+        return self.shape if i is None else self.shape[i]
+
+    def with_permutation(self, perm: Tensor) -> "SyntheticFeatures":
+        base = perm if self.perm is None else self.perm[perm]
+        return SyntheticFeatures(self.num_nodes, self.dim, self.seed, base)
+
+    def rows(self, ids: Tensor, out: Optional[Tensor] = None) -> Tensor:
+        ids = ids.to(torch.int64).contiguous()
+        if out is None:
+            out = torch.empty((ids.numel(), self.dim), dtype=torch.float32)
+        _lib.call("gr_gaussian_rows", self.seed, ids.data_ptr(), ids.numel(), self.dim,
+                  out.data_ptr(), 0)
+        return out
+
+    def partition(self, start: int, end: int) -> Tensor:
+        ids = torch.arange(start, end) if self.perm is None else self.perm[start:end]
+        return self.rows(ids)
+
+    def __getitem__(self, idx):
+        if isinstance(idx, slice):
+            start, stop, step = idx.indices(self.num_nodes)
+            if step == 1:
+                return self.partition(start, stop)
+        ids = torch.arange(self.num_nodes)[idx]
+        if self.perm is not None:
+            ids = self.perm[ids]
+        return self.rows(ids.reshape(-1))

@@ -105,16 +105,16 @@ class Trainer:
                 self.device_gradients.append(DeviceBuffer(P, graph.partition_sizes, dims[l],
                                                           device=config.device))
             for pid in range(P):
-                self.host_features[0][pid].copy_(graph.partition_features(pid))
+                feats = graph.partition_features(pid)
+                self.host_features[0][pid].copy_(feats)
+                del feats
 
     # ------------------------------------------------------------ public API
 
     def reset_epoch(self) -> None:
-        for l in range(1, len(self.host_features)):
-            self.host_features[l].reset()
-        for buf in self.host_gradients:
-            if buf is not None:
-                buf.reset()
+        # Host activation buffers of layers >= 1 are fully overwritten by the
+        # forward D2H fills and gradient buffers are zeroed before each
+        # backward phase, so neither needs clearing here.
         for buf in self.device_features:
             buf.reset()
         for buf in self.device_gradients:

@@ -141,6 +141,18 @@ int gr_partition_boundaries(int32_t pid, int32_t num_parts, const int64_t* ptr,
                             int64_t n_halo, int64_t* col, int64_t nnz,
                             int64_t* boundary_flat, int64_t* boundary_lens);
 
+/* Graph partitioner (replaces the grdpart GrinnderPartitioner / Spinner call
+ * of build_partitioned_graph, grinnder/data/partition.py:285-300; grdpart is
+ * not available, so this is the library's own algorithm): breadth-first
+ * visit order (bfs_order != 0; else id order) of the undirected graph, then
+ * linear deterministic greedy assignment with partition capacity
+ * ceil(capacity * n / num_parts).  Outputs perm [n] (new position -> node
+ * id; nodes grouped by partition, visit order inside a partition) and
+ * ptr [num_parts + 1] (partition p = perm[ptr[p]:ptr[p+1]]). */
+int gr_partition_graph(const int64_t* src, const int64_t* dst, int64_t m,
+                       int64_t n, int32_t num_parts, double capacity,
+                       int32_t bfs_order, int64_t* perm, int64_t* ptr);
+
 /* ------------------------------------------------------------------------ */
 /* Aggregation-side preparation (host, done once per partition adjacency)    */
 /* ------------------------------------------------------------------------ */
@@ -277,6 +289,12 @@ int gr_gat_backward_dst(const int32_t* units, int64_t n_units,
 int gr_rmat_sample(uint64_t seed, int32_t scale, double a, double b, double c,
                    int64_t first, int64_t n, int64_t* src, int64_t* dst,
                    int32_t nthreads);
+
+/* Counter-based N(0,1) feature rows: out[i, :dim] depends only on
+ * (seed, ids[i]), so any subset of a large feature matrix is produced on
+ * demand (Box-Muller on SplitMix64 uniforms).  Host, multi-threaded. */
+int gr_gaussian_rows(uint64_t seed, const int64_t* ids, int64_t n, int64_t dim,
+                     float* out, int32_t nthreads);
 
 #ifdef __cplusplus
 }
