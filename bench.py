@@ -195,6 +195,12 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     device = "cuda:0"
     cfg = CONFIGS[args.config]
+    try:
+        meminfo = {l.split(":")[0]: l.split()[1] for l in open("/proc/meminfo")}
+        log(f"host memory: MemTotal {int(meminfo['MemTotal']) / 2**20:.1f} GiB, "
+            f"MemAvailable {int(meminfo['MemAvailable']) / 2**20:.1f} GiB, cpus {os.cpu_count()}")
+    except OSError:
+        pass
     graph, config = build_graph(cfg, device)
     nnz = sum(int(a[1].numel()) for a in graph.adj_csr)
 

@@ -28,6 +28,8 @@ _SIGNATURES = {
     "gr_d2h_copy_async": [_P, _P, _i64, _P],
     "gr_h2d_synchronize": [],
     "gr_d2h_synchronize": [],
+    "gr_host_alloc": [_i64, _P],
+    "gr_host_free": [_P],
     "gr_gather_partitions": [_i32, _i32, _P, _P, _P, _i64, _i64, _P, _P, _P],
     "gr_scatter_partitions": [_i32, _i32, _P, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_build_subgraph": [_P, _P, _P, _i64, _i64, _P, _i64, _i32, _P, _P, _P, _P, _P, _P],

@@ -9,17 +9,55 @@ on the transfer stream only, never on the whole device.
 
 from __future__ import annotations
 
+import ctypes
 from typing import List, Optional
 
 import torch
 from torch import Tensor
 
-from grinnder_amd import _C
+from grinnder_amd import _C, _lib
+
+
+class _PinnedBlock:
+    """Owns one exact-size pinned host allocation (gr_host_alloc)."""
+
+    def __init__(self, nbytes: int):
+        ptr = ctypes.c_void_p()
+        _lib.call("gr_host_alloc", nbytes, ctypes.byref(ptr))
+        self.ptr = ptr.value
+        self.nbytes = nbytes
+        self.array = (ctypes.c_char * nbytes).from_address(self.ptr)
+        self.array._owner = self  # the tensor keeps the array, the array keeps us
+
+    def __del__(self):
+        ptr = getattr(self, "ptr", None)
+        if ptr:
+            self.ptr = None
+            try:
+                _lib.load().gr_host_free(ptr)
+            except Exception:  # interpreter shutdown: the process frees it anyway
+                pass
+
+
+def pinned_empty(rows: int, cols: int) -> Tensor:
+    """Exact-size pinned fp32 host tensor; pageable if pinning is refused
+    (the reference's HostBuffer also falls back, grinnder/buffer/host.py:36-45)."""
+    nbytes = rows * cols * 4
+    if nbytes == 0:
+        return torch.empty((rows, cols), dtype=torch.float32)
+    try:
+        block = _PinnedBlock(nbytes)
+    except _lib.GrError:
+        return torch.empty((rows, cols), dtype=torch.float32)
+    return torch.frombuffer(block.array, dtype=torch.float32).view(rows, cols)
 
 
 def _empty_host_tensor(rows: int, cols: int, *, pin_memory: bool, allocate: bool) -> Tensor:
-    shape = (rows, cols) if allocate else (0, cols)
-    return torch.empty(shape, dtype=torch.float32, pin_memory=pin_memory)
+    if not allocate:
+        return torch.empty((0, cols), dtype=torch.float32)
+    if pin_memory:
+        return pinned_empty(rows, cols)
+    return torch.empty((rows, cols), dtype=torch.float32)
 
 
 def _none_to_empty(pid: int, boundaries: List[Optional[Tensor]], num_parts: int) -> List[Tensor]:
@@ -79,8 +117,7 @@ class HostBuffer:
         expected = self.partition_nbytes(pid)
         if t.untyped_storage().size() < expected:
             if self._pin_memory:
-                t = torch.empty((self.part_sizes[pid], self.embedding_dim), dtype=torch.float32,
-                                pin_memory=True)
+                t = pinned_empty(self.part_sizes[pid], self.embedding_dim)
                 self._tensors[pid] = t
             else:
                 t.untyped_storage().resize_(expected)

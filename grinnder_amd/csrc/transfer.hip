@@ -492,3 +492,27 @@ extern "C" int gr_scatter_partitions(int32_t pid, int32_t num_parts, const float
   if (rc != GR_OK) return rc;
   return fifo_push(d2h_fifo(), s);
 }
+
+// Exact-size pinned host allocations for partition buffers (torch's pinned
+// allocator rounds every block up to a power of two, which nearly doubles
+// the footprint of large partitions).
+extern "C" int gr_host_alloc(int64_t nbytes, void** out) {
+  gr::clear_error();
+  GR_REQUIRE(out != nullptr && nbytes >= 0, "host_alloc: bad arguments");
+  *out = nullptr;
+  if (nbytes == 0) return GR_OK;
+  hipError_t e = hipHostMalloc(out, (size_t)nbytes, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    *out = nullptr;
+    return gr::fail(GR_ENOMEM, "hipHostMalloc(%lld) failed: %s", (long long)nbytes,
+                    hipGetErrorString(e));
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_host_free(void* p) {
+  gr::clear_error();
+  if (p != nullptr) GR_HIP_CHECK(hipHostFree(p));
+  return GR_OK;
+}

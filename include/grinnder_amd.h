@@ -106,6 +106,14 @@ int gr_scatter_partitions(int32_t pid, int32_t num_parts, const float* src,
                           const int64_t* const* boundaries,
                           const int64_t* boundary_lens, void* stream);
 
+/* Exact-size pinned (page-locked, device-mapped) host allocation for the
+ * host partition buffers (the reference allocates them with torch, optionally
+ * pinned, grinnder/buffer/host.py:27-45).  GR_ENOMEM if the driver refuses;
+ * callers then fall back to pageable memory as the reference does.
+ * gr_host_free releases a pointer returned by gr_host_alloc (NULL is a no-op). */
+int gr_host_alloc(int64_t nbytes, void** out);
+int gr_host_free(void* p);
+
 /* ------------------------------------------------------------------------ */
 /* Partition bookkeeping (host, bit-exact)                                   */
 /* ------------------------------------------------------------------------ */
