@@ -213,7 +213,10 @@ def main():
                     heads=1, dropout=0.0, norm=True).to(device)
     t0 = time.perf_counter()
     trainer = Trainer(model, graph, config)
-    log(f"trainer (host buffers, prefill) in {time.perf_counter() - t0:.1f}s")
+    from grinnder_amd.buffer.host import PINNED_STATS
+    log(f"trainer (host buffers, prefill) in {time.perf_counter() - t0:.1f}s; pinned "
+        f"{PINNED_STATS['bytes'] / 2**30:.1f} GiB in {PINNED_STATS['blocks']} blocks, "
+        f"{PINNED_STATS['fallbacks']} pageable fallbacks")
     opt = torch.optim.Adam(model.parameters(), lr=0.01, weight_decay=5e-4)
     crit = torch.nn.CrossEntropyLoss()
 
@@ -237,6 +240,11 @@ def main():
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f})")
+    if cfg["num_parts"] > 1:
+        from grinnder_amd.buffer.host import PINNED_STATS
+        log(f"pinned host memory {PINNED_STATS['bytes'] / 2**30:.1f} GiB, "
+            f"{PINNED_STATS['fallbacks']} pageable fallbacks "
+            f"({PINNED_STATS['fallback_bytes'] / 2**30:.1f} GiB)")
 
     recs = timer.records
     agg_ms = sum(r.ms() for r in recs if r.name.startswith(("gcn_", "gat_")))

@@ -18,6 +18,9 @@ from torch import Tensor
 from grinnder_amd import _C, _lib
 
 
+PINNED_STATS = {"bytes": 0, "blocks": 0, "fallbacks": 0, "fallback_bytes": 0}
+
+
 class _PinnedBlock:
     """Owns one exact-size pinned host allocation (gr_host_alloc)."""
 
@@ -25,6 +28,8 @@ class _PinnedBlock:
         ptr = ctypes.c_void_p()
         _lib.call("gr_host_alloc", nbytes, ctypes.byref(ptr))
         self.ptr = ptr.value
+        PINNED_STATS["bytes"] += nbytes
+        PINNED_STATS["blocks"] += 1
         self.nbytes = nbytes
         self.array = (ctypes.c_char * nbytes).from_address(self.ptr)
         self.array._owner = self  # the tensor keeps the array, the array keeps us
@@ -34,6 +39,8 @@ class _PinnedBlock:
         if ptr:
             self.ptr = None
             try:
+                PINNED_STATS["bytes"] -= self.nbytes
+                PINNED_STATS["blocks"] -= 1
                 _lib.load().gr_host_free(ptr)
             except Exception:  # interpreter shutdown: the process frees it anyway
                 pass
@@ -48,6 +55,8 @@ def pinned_empty(rows: int, cols: int) -> Tensor:
     try:
         block = _PinnedBlock(nbytes)
     except _lib.GrError:
+        PINNED_STATS["fallbacks"] += 1
+        PINNED_STATS["fallback_bytes"] += nbytes
         return torch.empty((rows, cols), dtype=torch.float32)
     return torch.frombuffer(block.array, dtype=torch.float32).view(rows, cols)
 

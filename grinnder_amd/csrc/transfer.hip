@@ -37,6 +37,9 @@ EventFifo& d2h_fifo() {
 
 constexpr size_t kMaxQueued = 4096;
 
+// Pinned staging slots hold at most this many bytes (pageable paths chunk).
+constexpr int64_t kChunkBytes = int64_t(64) << 20;
+
 int fifo_push(EventFifo& f, hipStream_t s) {
   hipEvent_t ev = nullptr;
   GR_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
@@ -347,28 +350,33 @@ extern "C" int gr_gather_partitions(int32_t pid, int32_t num_parts, const void* 
       }
       GR_HIP_CHECK(hipGetLastError());
     } else {
-      int rc = staging_acquire((size_t)(halo * row_bytes), &stage, &slot);
-      if (rc != GR_OK) return rc;
-      // Offsets of each partition's block in the staging slot.
-      std::vector<int64_t> first(num_parts, 0);
+      // Pageable sources: host threads gather rows into pinned staging chunks
+      // of at most kChunkBytes, each copied by DMA as soon as it is full.
+      const int64_t rows_per_chunk = std::max<int64_t>(1, kChunkBytes / row_bytes);
+      std::vector<const char*> row_src((size_t)halo);
       int64_t o = 0;
-      for (int32_t p = 0; p < num_parts; ++p) {
-        first[p] = o;
-        if (p != pid && boundary_lens[p] > 0) o += boundary_lens[p];
-      }
-      char* st = static_cast<char*>(stage);
       for (int32_t p = 0; p < num_parts; ++p) {
         if (p == pid || boundary_lens[p] <= 0) continue;
         const int64_t* b = boundaries[p];
         const char* base = static_cast<const char*>(srcs[p]);
-        char* out = st + first[p] * row_bytes;
-        parallel_for(boundary_lens[p], 4096, [&](int64_t lo, int64_t hi) {
-          for (int64_t k = lo; k < hi; ++k)
-            std::memcpy(out + k * row_bytes, base + b[k] * row_bytes, (size_t)row_bytes);
-        });
+        for (int64_t k = 0; k < boundary_lens[p]; ++k) row_src[o++] = base + b[k] * row_bytes;
       }
-      GR_HIP_CHECK(hipMemcpyAsync(d + intra * row_bytes, stage, (size_t)(halo * row_bytes),
-                                  hipMemcpyHostToDevice, s));
+      for (int64_t r0 = 0; r0 < halo; r0 += rows_per_chunk) {
+        const int64_t n = std::min(rows_per_chunk, halo - r0);
+        int rc = staging_acquire((size_t)(n * row_bytes), &stage, &slot);
+        if (rc != GR_OK) return rc;
+        char* st = static_cast<char*>(stage);
+        parallel_for(n, 4096, [&](int64_t lo, int64_t hi) {
+          for (int64_t k = lo; k < hi; ++k)
+            std::memcpy(st + k * row_bytes, row_src[r0 + k], (size_t)row_bytes);
+        });
+        hipError_t e = hipMemcpyAsync(d + (intra + r0) * row_bytes, stage, (size_t)(n * row_bytes),
+                                      hipMemcpyHostToDevice, s);
+        rc = staging_release(slot, s);
+        GR_HIP_CHECK(e);
+        if (rc != GR_OK) return rc;
+      }
+      return fifo_push(h2d_fifo(), s);
     }
     int rc = staging_release(slot, s);
     if (rc != GR_OK) return rc;
@@ -459,43 +467,56 @@ extern "C" int gr_scatter_partitions(int32_t pid, int32_t num_parts, const float
     return fifo_push(d2h_fifo(), s);
   }
 
-  // Host path: D2H into a pinned slot, then ordered host accumulation
-  // (self block first, then partitions ascending, indices in order).
-  void* stage = nullptr;
-  int slot = -1;
-  int rc = staging_acquire((size_t)(src_rows * dim) * sizeof(float), &stage, &slot);
-  if (rc != GR_OK) return rc;
-  GR_HIP_CHECK(hipMemcpyAsync(stage, src, (size_t)(src_rows * dim) * sizeof(float),
-                              hipMemcpyDeviceToHost, s));
-  GR_HIP_CHECK(hipStreamSynchronize(s));
-  const float* g = static_cast<const float*>(stage);
+  // Host path: D2H in pinned staging chunks of at most kChunkBytes, each
+  // accumulated on the host in row order (self block first, then partitions
+  // ascending, indices in order) before the next chunk is fetched.
+  std::vector<float*> row_dst((size_t)src_rows);
+  for (int64_t r = 0; r < dst_rows[pid]; ++r) row_dst[r] = dsts[pid] + r * dim;
   {
-    float* out = dsts[pid];
-    const int64_t n = dst_rows[pid] * dim;
-    parallel_for(n, 1 << 18, [&](int64_t lo, int64_t hi) {
-      for (int64_t i = lo; i < hi; ++i) out[i] = out[i] + g[i];
-    });
-  }
-  int64_t off = dst_rows[pid];
-  for (int32_t p = 0; p < num_parts; ++p) {
-    if (p == pid || boundary_lens[p] <= 0) continue;
-    const int64_t* b = boundaries[p];
-    float* out = dsts[p];
-    for (int64_t k = 0; k < boundary_lens[p]; ++k) {
-      float* row = out + b[k] * dim;
-      const float* in = g + (off + k) * dim;
-      for (int64_t j = 0; j < dim; ++j) row[j] = row[j] + in[j];
+    int64_t o = dst_rows[pid];
+    for (int32_t p = 0; p < num_parts; ++p) {
+      if (p == pid || boundary_lens[p] <= 0) continue;
+      const int64_t* b = boundaries[p];
+      for (int64_t k = 0; k < boundary_lens[p]; ++k) row_dst[o++] = dsts[p] + b[k] * dim;
     }
-    off += boundary_lens[p];
   }
-  rc = staging_release(slot, s);
-  if (rc != GR_OK) return rc;
+  const int64_t row_bytes = dim * (int64_t)sizeof(float);
+  const int64_t rows_per_chunk = std::max<int64_t>(1, kChunkBytes / row_bytes);
+  for (int64_t r0 = 0; r0 < src_rows; r0 += rows_per_chunk) {
+    const int64_t n = std::min(rows_per_chunk, src_rows - r0);
+    void* stage = nullptr;
+    int slot = -1;
+    int rc = staging_acquire((size_t)(n * row_bytes), &stage, &slot);
+    if (rc != GR_OK) return rc;
+    hipError_t e = hipMemcpyAsync(stage, src + r0 * dim, (size_t)(n * row_bytes),
+                                  hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      staging_release(slot, s);
+      return gr::fail(GR_EHIP, "scatter_partitions D2H failed: %s", hipGetErrorString(e));
+    }
+    const float* g = static_cast<const float*>(stage);
+    if (repeated) {
+      for (int64_t k = 0; k < n; ++k) {
+        float* row = row_dst[r0 + k];
+        const float* in = g + k * dim;
+        for (int64_t j = 0; j < dim; ++j) row[j] = row[j] + in[j];
+      }
+    } else {
+      parallel_for(n, 1024, [&](int64_t lo, int64_t hi) {
+        for (int64_t k = lo; k < hi; ++k) {
+          float* row = row_dst[r0 + k];
+          const float* in = g + k * dim;
+          for (int64_t j = 0; j < dim; ++j) row[j] = row[j] + in[j];
+        }
+      });
+    }
+    rc = staging_release(slot, s);
+    if (rc != GR_OK) return rc;
+  }
   return fifo_push(d2h_fifo(), s);
 }
 
-// Exact-size pinned host allocations for partition buffers (torch's pinned
-// allocator rounds every block up to a power of two, which nearly doubles
-// the footprint of large partitions).
 extern "C" int gr_host_alloc(int64_t nbytes, void** out) {
   gr::clear_error();
   GR_REQUIRE(out != nullptr && nbytes >= 0, "host_alloc: bad arguments");

@@ -173,3 +173,27 @@ def test_host_buffer_fill_upload_gather_scatter(gpu):
         buf.d2h_synchronize(stream)
         assert torch.equal(buf[0], torch.full((4, 2), 3.0))
         assert buf[1].tolist() == [[2, 2], [0, 0], [2, 2]]
+
+
+def test_pageable_paths_span_several_staging_chunks(gpu):
+    """Pageable gather / scatter larger than one 64 MiB staging chunk."""
+    g = torch.Generator().manual_seed(0)
+    dim = 64
+    sizes = [150_000, 200_000, 180_000]
+    srcs = [torch.randn(n, dim, generator=g) for n in sizes]
+    bnd = [None, torch.randperm(sizes[1], generator=g)[:170_000],
+           torch.randperm(sizes[2], generator=g)[:160_000]]
+    ref = oracle.gather_partitions(0, srcs, bnd)
+    dst = torch.empty(ref.shape, device=gpu)
+    b64 = [torch.empty(0, dtype=torch.long) if b is None else b for b in bnd]
+    _on_side_stream(lambda: _C.gather_partitions(0, srcs, dst, b64))
+    _C.h2d_synchronize()
+    assert np.array_equal(dst.cpu().numpy(), ref)
+    grad = torch.randn(ref.shape, generator=g)
+    dsts = [torch.randn(n, dim, generator=g) for n in sizes]
+    expect = oracle.scatter_partitions(0, grad, dsts, bnd)
+    gd = grad.to(gpu)
+    _on_side_stream(lambda: _C.scatter_partitions(0, gd, dsts, b64))
+    _C.d2h_synchronize()
+    for d, e in zip(dsts, expect):
+        assert np.array_equal(d.numpy(), e)
