@@ -20,6 +20,7 @@ _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _u64 = ctypes.c_uint64
 _dbl = ctypes.c_double
+_f32 = ctypes.c_float
 _P = ctypes.c_void_p  # every pointer crosses as void*
 
 # name -> argument types (all return int status)
@@ -40,6 +41,9 @@ _SIGNATURES = {
     "gr_gcn_aggregate": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64, _i64, _P,
                          _i64, _P],
     "gr_column_sum": [_P, _i64, _i64, _i64, _P, _P, _i64, _P],
+    "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,
+                                 _i64, _P, _P, _P, _P, _P, _i64, _P],
+    "gr_ln_relu_backward": [_P, _P, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_scores": [_P, _i64, _i64, _i64, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_gat_softmax_stats": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _i64, _P],
     "gr_gat_aggregate": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P,

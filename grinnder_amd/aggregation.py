@@ -149,6 +149,70 @@ def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None) -> T
     return _GCNAggregate.apply(z, bias, plan)
 
 
+class _GCNAggregateLNReLU(torch.autograd.Function):
+    """out = ReLU(LayerNorm(A Z + b)) with the LayerNorm/ReLU fused into the
+    aggregation epilogue; backward: fused LN/ReLU gradient, then dZ = A^T gh."""
+
+    @staticmethod
+    def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
+                plan: DevicePlan, eps: float) -> Tensor:
+        z = z.contiguous()
+        dev = z.device
+        B, D = plan.num_dst, z.size(1)
+        f = plan.fwd
+        h = torch.empty((B, D), dtype=torch.float32, device=dev)
+        out = torch.empty((B, D), dtype=torch.float32, device=dev)
+        mean = torch.empty(B, dtype=torch.float32, device=dev)
+        rstd = torch.empty(B, dtype=torch.float32, device=dev)
+        ws = _workspace(f.n_slots, D, dev)
+        b = bias.contiguous() if bias is not None else None
+        g, bt = gamma.contiguous(), beta.contiguous()
+        nnz = plan.nnz
+        with KernelTimer.region("gcn_fwd", nnz * (4 * D + 8) + B * (4 * D + 4), nnz, D):
+            _lib.call("gr_gcn_aggregate_ln_relu", f.units.data_ptr(), f.n_units,
+                      f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
+                      plan.val.data_ptr(), z.data_ptr(), z.stride(0), _lib.ptr(b), g.data_ptr(),
+                      bt.data_ptr(), float(eps), B, D, h.data_ptr(), out.data_ptr(),
+                      mean.data_ptr(), rstd.data_ptr(), _lib.ptr(ws), f.n_slots,
+                      _lib.stream_handle())
+        ctx.save_for_backward(h, mean, rstd, g, bt)
+        ctx.plan = plan
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, gout: Tensor):
+        h, mean, rstd, g, bt = ctx.saved_tensors
+        plan: DevicePlan = ctx.plan
+        gout = gout.contiguous()
+        B, D = h.shape
+        dev = h.device
+        gh = torch.empty_like(h)
+        dgamma = torch.empty(D, dtype=torch.float32, device=dev)
+        dbeta = torch.empty(D, dtype=torch.float32, device=dev)
+        nwaves = min(4096, max(4, (B + 15) // 16))
+        nwaves = (nwaves + 3) // 4 * 4
+        ws = torch.empty((2 * nwaves + 1) * D, dtype=torch.float32, device=dev)
+        _lib.call("gr_ln_relu_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
+                  rstd.data_ptr(), g.data_ptr(), bt.data_ptr(), B, D, gh.data_ptr(),
+                  dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws.numel(),
+                  _lib.stream_handle())
+        dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd") \
+            if ctx.needs_input_grad[0] else None
+        db = column_sum(gh) if ctx.has_bias else None
+        return dz, db, dgamma, dbeta, None, None
+
+
+def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gamma: Tensor,
+                          beta: Tensor, eps: float = 1e-5) -> Tensor:
+    """ReLU(LayerNorm(A·Z + bias)) of one partition in one fused pass (GPU)."""
+    _check_device_tensor("z", z)
+    plan = adj.device_plan(z.device)
+    if z.size(0) != plan.num_src:
+        raise ValueError(f"z has {z.size(0)} rows, adjacency has {plan.num_src} columns")
+    return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps)
+
+
 class _GATAttention(torch.autograd.Function):
     """Attention logits + edge softmax + weighted aggregation of GATConv."""
 

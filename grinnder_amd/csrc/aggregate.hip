@@ -191,6 +191,269 @@ __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict
   y[(int64_t)row * ldy + f] = s;
 }
 
+// ---------------------------------------------------------------------------
+// Fused epilogue: h = A*X + bias, then LayerNorm(h; gamma, beta, eps) and
+// ReLU, for rows held by one wavefront (G = 64 lanes, NCH chunks of VEC).
+// Writes h (kept for the backward), out = ReLU(LN(h)) and the row statistics
+// mean / rstd.  LayerNorm uses the biased variance of the row, as torch does.
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// y = (h - mean) * rstd * gamma + beta; the backward recomputes it with the
+// same expression so the ReLU mask is bit-identical.
+__device__ __forceinline__ float ln_affine(float h, float mean, float rstd, float g, float b) {
+  return fmaf((h - mean) * rstd, g, b);
+}
+
+template <int VEC, int NCH>
+__device__ __forceinline__ void ln_relu_store_row(float (&acc)[NCH][VEC], const bool (&fvalid)[NCH],
+                                                  const int (&foff)[NCH], int dim,
+                                                  const float* __restrict__ gamma,
+                                                  const float* __restrict__ beta, float eps,
+                                                  float* __restrict__ hrow, float* __restrict__ orow,
+                                                  float* __restrict__ mean_out,
+                                                  float* __restrict__ rstd_out, int lane) {
+  float s = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) s += fvalid[ch] ? acc[ch][j] : 0.f;
+  const float mean = wave_sum64(s) / (float)dim;
+  float q = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float dlt = acc[ch][j] - mean;
+      q += fvalid[ch] ? dlt * dlt : 0.f;
+    }
+  const float var = wave_sum64(q) / (float)dim;
+  const float rstd = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    if (!fvalid[ch]) continue;
+    float g[VEC], b[VEC], o[VEC];
+    load_vec<VEC>(gamma + foff[ch], g);
+    load_vec<VEC>(beta + foff[ch], b);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) o[j] = fmaxf(ln_affine(acc[ch][j], mean, rstd, g[j], b[j]), 0.f);
+    store_vec<VEC>(hrow + foff[ch], acc[ch]);
+    store_vec<VEC>(orow + foff[ch], o);
+  }
+  if (lane == 0) {
+    *mean_out = mean;
+    *rstd_out = rstd;
+  }
+}
+
+template <int VEC, int NCH, int U>
+__global__ __launch_bounds__(256) void aggregate_ln_relu_units(
+    const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
+    const float* __restrict__ val, const float* __restrict__ x, int64_t ldx,
+    const float* __restrict__ bias, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, int dim, float* __restrict__ h,
+    float* __restrict__ out, float* __restrict__ mean, float* __restrict__ rstd,
+    float* __restrict__ ws) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (wid >= n_units) return;
+  const int4 w = units[wid];
+  float acc[NCH][VEC];
+  bool fvalid[NCH];
+  int foff[NCH], fld[NCH];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    foff[ch] = (ch * 64 + lane) * VEC;
+    fvalid[ch] = foff[ch] < dim;
+    fld[ch] = fvalid[ch] ? foff[ch] : dim - VEC;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc[ch][j] = 0.f;
+  }
+  int e = w.y;
+  const int end = w.z;
+  for (; e + U <= end; e += U) {
+    int c[U];
+    float v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      c[k] = idx[e + k];
+      v[k] = val[e + k];
+    }
+    float r[U][NCH][VEC];
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld[ch], r[k][ch]);
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[ch][j] = fmaf(v[k], r[k][ch][j], acc[ch][j]);
+  }
+  // Tail: masked iterations of TU edges; out-of-range slots re-read the
+  // first tail edge's row with weight 0.
+  constexpr int TU = (U < 4) ? U : 4;
+  if (e < end) {
+    const int safe_c = idx[e];
+    for (; e < end; e += TU) {
+      int c[TU];
+      float v[TU];
+#pragma unroll
+      for (int k = 0; k < TU; ++k) {
+        const bool ok = e + k < end;
+        c[k] = ok ? idx[e + k] : safe_c;
+        v[k] = ok ? val[e + k] : 0.f;
+      }
+      float r[TU][NCH][VEC];
+#pragma unroll
+      for (int k = 0; k < TU; ++k)
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+          load_vec<VEC>(x + (int64_t)c[k] * ldx + fld[ch], r[k][ch]);
+#pragma unroll
+      for (int k = 0; k < TU; ++k)
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) acc[ch][j] = fmaf(v[k], r[k][ch][j], acc[ch][j]);
+    }
+  }
+  if (w.w >= 0) {
+    float* p = ws + (int64_t)w.w * dim;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+      if (fvalid[ch]) store_vec<VEC>(p + foff[ch], acc[ch]);
+    return;
+  }
+  if (bias != nullptr) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      float b[VEC];
+      load_vec<VEC>(bias + fld[ch], b);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[ch][j] += b[j];
+    }
+  }
+  const int64_t row = w.x;
+  ln_relu_store_row<VEC, NCH>(acc, fvalid, foff, dim, gamma, beta, eps, h + row * dim,
+                              out + row * dim, mean + row, rstd + row, lane);
+}
+
+// Split rows of the fused epilogue: ordered sum of the partials + bias into
+// h (one wavefront per row), then the LayerNorm/ReLU over that row.
+__global__ __launch_bounds__(256) void aggregate_ln_relu_fixup(
+    const int32_t* __restrict__ fix, int64_t n_fix, const float* __restrict__ ws, int dim,
+    const float* __restrict__ bias, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float* __restrict__ h, float* __restrict__ out,
+    float* __restrict__ mean, float* __restrict__ rstd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (wid >= n_fix) return;
+  const int row = fix[3 * wid + 0], first = fix[3 * wid + 1], n = fix[3 * wid + 2];
+  float* hrow = h + (int64_t)row * dim;
+  float s = 0.f;
+  for (int f = lane; f < dim; f += 64) {
+    float a = 0.f;
+    for (int k = 0; k < n; ++k) a += ws[(int64_t)(first + k) * dim + f];
+    if (bias != nullptr) a += bias[f];
+    hrow[f] = a;
+    s += a;
+  }
+  const float mu = wave_sum64(s) / (float)dim;
+  float q = 0.f;
+  for (int f = lane; f < dim; f += 64) {
+    const float dlt = hrow[f] - mu;
+    q += dlt * dlt;
+  }
+  const float rs = 1.0f / sqrtf(wave_sum64(q) / (float)dim + eps);
+  float* orow = out + (int64_t)row * dim;
+  for (int f = lane; f < dim; f += 64)
+    orow[f] = fmaxf(ln_affine(hrow[f], mu, rs, gamma[f], beta[f]), 0.f);
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+}
+
+// Backward of ReLU(LayerNorm(h)): for each row, with xh = (h - mean) * rstd,
+// y = xh * gamma + beta and gy = g * (y > 0):
+//   gh = rstd * (gy*gamma - mean(gy*gamma) - xh * mean(gy*gamma*xh)),
+// and per-wavefront partial sums of dgamma = sum gy*xh, dbeta = sum gy
+// (reduced afterwards in wavefront order).  Grid-stride over rows.
+template <int VEC, int NCH>
+__global__ __launch_bounds__(256) void ln_relu_backward(
+    const float* __restrict__ g, const float* __restrict__ h, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma,
+    const float* __restrict__ beta, int dim, int64_t rows, float* __restrict__ gh,
+    float* __restrict__ part_gamma, float* __restrict__ part_beta) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  bool fvalid[NCH];
+  int foff[NCH], fld[NCH];
+  float gam[NCH][VEC], bet[NCH][VEC], dg[NCH][VEC], db[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    foff[ch] = (ch * 64 + lane) * VEC;
+    fvalid[ch] = foff[ch] < dim;
+    fld[ch] = fvalid[ch] ? foff[ch] : dim - VEC;
+    load_vec<VEC>(gamma + fld[ch], gam[ch]);
+    load_vec<VEC>(beta + fld[ch], bet[ch]);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      dg[ch][j] = 0.f;
+      db[ch][j] = 0.f;
+    }
+  }
+  const float inv_d = 1.0f / (float)dim;
+  for (int64_t r = wid; r < rows; r += nwaves) {
+    const float mu = mean[r], rs = rstd[r];
+    float gv[NCH][VEC], xh[NCH][VEC], gx[NCH][VEC];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      float hv[VEC];
+      load_vec<VEC>(g + r * dim + fld[ch], gv[ch]);
+      load_vec<VEC>(h + r * dim + fld[ch], hv);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float y = ln_affine(hv[j], mu, rs, gam[ch][j], bet[ch][j]);
+        const float gy = (fvalid[ch] && y > 0.f) ? gv[ch][j] : 0.f;
+        xh[ch][j] = (hv[j] - mu) * rs;
+        gx[ch][j] = gy * gam[ch][j];
+        dg[ch][j] = fmaf(gy, xh[ch][j], dg[ch][j]);
+        db[ch][j] += gy;
+        s1 += gx[ch][j];
+        s2 = fmaf(gx[ch][j], xh[ch][j], s2);
+      }
+    }
+    s1 = wave_sum64(s1) * inv_d;
+    s2 = wave_sum64(s2) * inv_d;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      if (!fvalid[ch]) continue;
+      float o[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) o[j] = rs * (gx[ch][j] - s1 - xh[ch][j] * s2);
+      store_vec<VEC>(gh + r * dim + foff[ch], o);
+    }
+  }
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    if (!fvalid[ch]) continue;
+    store_vec<VEC>(part_gamma + wid * dim + foff[ch], dg[ch]);
+    store_vec<VEC>(part_beta + wid * dim + foff[ch], db[ch]);
+  }
+}
+
 // Column sums of a [rows, dim] matrix, two passes, fixed order: workgroup b
 // sums rows [b*chunk, (b+1)*chunk) into part[b, :]; then part is reduced over
 // b in ascending order.  Each thread owns columns f = tid, tid + 256, ...
@@ -326,6 +589,134 @@ extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t 
   GR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, s,
                      workspace, (int)nblk, (int)dim, out);
+  GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}
+
+namespace {
+
+template <int VEC, int NCH>
+hipError_t launch_ln_relu(const int4* units, int64_t n_units, const int32_t* idx,
+                          const float* val, const float* x, int64_t ldx, const float* bias,
+                          const float* gamma, const float* beta, float eps, int dim, float* h,
+                          float* out, float* mean, float* rstd, float* ws, hipStream_t s) {
+  constexpr int U = NCH == 1 ? 8 : (NCH == 2 ? 4 : 2);
+  hipLaunchKernelGGL((gr_agg::aggregate_ln_relu_units<VEC, NCH, U>),
+                     dim3((unsigned)((n_units + 3) / 4)), dim3(256), 0, s, units, n_units, idx,
+                     val, x, ldx, bias, gamma, beta, eps, dim, h, out, mean, rstd, ws);
+  return hipGetLastError();
+}
+
+bool fused_shape(int64_t dim, int* vec, int* nch) {
+  *vec = dim % 4 == 0 ? 4 : 1;
+  const int64_t chunks = dim / *vec + (dim % *vec ? 1 : 0);
+  if (chunks <= 64) *nch = 1;
+  else if (chunks <= 128) *nch = 2;
+  else if (chunks <= 256) *nch = 4;
+  else return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
+                                        const int32_t* fixups, int64_t n_fix, const int32_t* idx,
+                                        const float* val, const float* x, int64_t ldx,
+                                        const float* bias, const float* gamma, const float* beta,
+                                        float eps, int64_t rows, int64_t dim, float* h,
+                                        float* out, float* mean, float* rstd, float* workspace,
+                                        int64_t n_slots, void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(n_units >= 0 && n_fix >= 0 && rows >= 0, "gcn_aggregate_ln_relu: negative extent");
+  int vec, nch;
+  GR_REQUIRE(dim >= 1 && fused_shape(dim, &vec, &nch),
+             "gcn_aggregate_ln_relu: dim %lld unsupported (max 1024)", (long long)dim);
+  GR_REQUIRE(ldx >= dim, "gcn_aggregate_ln_relu: ldx < dim");
+  GR_REQUIRE(gamma && beta && h && out && mean && rstd, "gcn_aggregate_ln_relu: NULL output");
+  GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gcn_aggregate_ln_relu: NULL fixups/workspace");
+  if (n_units == 0) return GR_OK;
+  GR_REQUIRE(units && gr_agg::aligned(units, 16) && idx && val && x,
+             "gcn_aggregate_ln_relu: NULL or misaligned input");
+  if (vec == 4) {
+    const bool al = gr_agg::aligned(x, 16) && ldx % 4 == 0 && gr_agg::aligned(h, 16) &&
+                    gr_agg::aligned(out, 16) && gr_agg::aligned(gamma, 16) &&
+                    gr_agg::aligned(beta, 16) && (bias == nullptr || gr_agg::aligned(bias, 16)) &&
+                    (workspace == nullptr || gr_agg::aligned(workspace, 16));
+    if (!al) {
+      GR_REQUIRE(dim <= 256, "gcn_aggregate_ln_relu: misaligned rows wider than 256");
+      vec = 1;
+      nch = dim <= 64 ? 1 : (dim <= 128 ? 2 : 4);
+    }
+  }
+  hipStream_t s = gr::as_stream(stream);
+  const int4* u4 = reinterpret_cast<const int4*>(units);
+  const int d = (int)dim;
+  hipError_t err;
+  if (vec == 4) {
+    if (nch == 1) err = launch_ln_relu<4, 1>(u4, n_units, idx, val, x, ldx, bias, gamma, beta, eps, d, h, out, mean, rstd, workspace, s);
+    else if (nch == 2) err = launch_ln_relu<4, 2>(u4, n_units, idx, val, x, ldx, bias, gamma, beta, eps, d, h, out, mean, rstd, workspace, s);
+    else err = launch_ln_relu<4, 4>(u4, n_units, idx, val, x, ldx, bias, gamma, beta, eps, d, h, out, mean, rstd, workspace, s);
+  } else {
+    if (nch == 1) err = launch_ln_relu<1, 1>(u4, n_units, idx, val, x, ldx, bias, gamma, beta, eps, d, h, out, mean, rstd, workspace, s);
+    else if (nch == 2) err = launch_ln_relu<1, 2>(u4, n_units, idx, val, x, ldx, bias, gamma, beta, eps, d, h, out, mean, rstd, workspace, s);
+    else err = launch_ln_relu<1, 4>(u4, n_units, idx, val, x, ldx, bias, gamma, beta, eps, d, h, out, mean, rstd, workspace, s);
+  }
+  GR_HIP_CHECK(err);
+  if (n_fix > 0) {
+    hipLaunchKernelGGL(gr_agg::aggregate_ln_relu_fixup, dim3((unsigned)((n_fix + 3) / 4)),
+                       dim3(256), 0, s, fixups, n_fix, workspace, d, bias, gamma, beta, eps, h,
+                       out, mean, rstd);
+    GR_HIP_CHECK(hipGetLastError());
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
+                                   const float* rstd, const float* gamma, const float* beta,
+                                   int64_t rows, int64_t dim, float* gh, float* dgamma,
+                                   float* dbeta, float* workspace, int64_t workspace_floats,
+                                   void* stream) {
+  gr::clear_error();
+  int vec, nch;
+  GR_REQUIRE(rows >= 0 && dim >= 1 && fused_shape(dim, &vec, &nch),
+             "ln_relu_backward: dim %lld unsupported", (long long)dim);
+  GR_REQUIRE(g && h && mean && rstd && gamma && beta && gh && dgamma && dbeta && workspace,
+             "ln_relu_backward: NULL pointer");
+  const bool al = gr_agg::aligned(g, 16) && gr_agg::aligned(h, 16) && gr_agg::aligned(gh, 16) &&
+                  gr_agg::aligned(gamma, 16) && gr_agg::aligned(beta, 16) &&
+                  gr_agg::aligned(workspace, 16);
+  if (vec == 4 && !al) {
+    GR_REQUIRE(dim <= 256, "ln_relu_backward: misaligned rows wider than 256");
+    vec = 1;
+    nch = dim <= 64 ? 1 : (dim <= 128 ? 2 : 4);
+  }
+  // Wavefront count: enough to fill the chip, bounded by the workspace
+  // (2 * nwaves * dim floats of partials + dim for the reduction pass).
+  int64_t nwaves = std::min<int64_t>(4096, std::max<int64_t>(4, (rows + 15) / 16));
+  nwaves = (nwaves + 3) / 4 * 4;
+  const int64_t cap = (workspace_floats / dim - 1) / 2 / 4 * 4;
+  GR_REQUIRE(cap >= 4, "ln_relu_backward: workspace too small");
+  if (nwaves > cap) nwaves = cap;
+  float* pg = workspace;
+  float* pb = workspace + nwaves * dim;
+  hipStream_t s = gr::as_stream(stream);
+  const int d = (int)dim;
+  const unsigned blocks = (unsigned)(nwaves / 4);
+#define GR_LNB(V, N)                                                                        \
+  hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N>), dim3(blocks), dim3(256), 0, s, g, h, \
+                     mean, rstd, gamma, beta, d, rows, gh, pg, pb)
+  if (vec == 4) {
+    if (nch == 1) GR_LNB(4, 1); else if (nch == 2) GR_LNB(4, 2); else GR_LNB(4, 4);
+  } else {
+    if (nch == 1) GR_LNB(1, 1); else if (nch == 2) GR_LNB(1, 2); else GR_LNB(1, 4);
+  }
+#undef GR_LNB
+  GR_HIP_CHECK(hipGetLastError());
+  // dgamma / dbeta = column sums of the partials, in wavefront order.
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 255) / 256)), dim3(256), 0, s, pg,
+                     (int)nwaves, d, dgamma);
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 255) / 256)), dim3(256), 0, s, pb,
+                     (int)nwaves, d, dbeta);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }

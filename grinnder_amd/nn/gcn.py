@@ -8,6 +8,7 @@ import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
 
+from grinnder_amd.aggregation import gcn_aggregate_ln_relu
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.nn.conv import GCNConv
 
@@ -34,7 +35,25 @@ class GCN(GriNNderModel):
         if norm:
             self.norms = ModuleList(LayerNorm(hidden_channels) for _ in range(num_layers - 1))
 
+    def _fusable(self, layer: int, x: Tensor, adj) -> bool:
+        """conv -> LayerNorm -> ReLU runs as one fused kernel when nothing else
+        sits between them: no residual add, no active dropout, affine LayerNorm
+        over the full feature width."""
+        if self.norms is None or layer >= self.num_layers - 1 or not x.is_cuda:
+            return False
+        norm = self.norms[layer]
+        conv = self.convs[layer]
+        out_shape = (adj.sparse_sizes()[0], conv.out_channels)
+        return (norm.elementwise_affine and norm.bias is not None
+                and tuple(norm.normalized_shape) == (conv.out_channels,)
+                and not (self.residual and tuple(x.shape) == out_shape)
+                and (self.dropout == 0.0 or not self.training))
+
     def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
+        if self._fusable(layer, x, adj):
+            conv, norm = self.convs[layer], self.norms[layer]
+            return gcn_aggregate_ln_relu(conv.lin(x), adj, conv.bias, norm.weight, norm.bias,
+                                         norm.eps)
         h = self.convs[layer](x, adj)
         if layer < self.num_layers - 1:
             if self.norms is not None:

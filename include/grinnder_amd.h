@@ -209,6 +209,33 @@ int gr_gcn_aggregate(const int32_t* units, int64_t n_units,
                      int64_t rows, int64_t dim, float* workspace,
                      int64_t n_slots, void* stream);
 
+/* Fused GCN layer epilogue (bias + LayerNorm + ReLU of grinnder/nn/gcn.py:
+ * 64-72, LayerNorm of torch with biased variance and eps):
+ *   h[r]   = sum_e val[e] * X[idx[e]] + bias       (written, kept for backward)
+ *   out[r] = max((h[r] - mean_r) * rstd_r * gamma + beta, 0)
+ *   mean[r], rstd[r] = 1 / sqrt(var_r + eps)
+ * Same plan / workspace conventions as gr_gcn_aggregate; h and out are
+ * dense [rows, dim] (dim <= 1024).  No reference counterpart as one call: it
+ * fuses PyG GCNConv's aggregation with the LayerNorm and ReLU that follow it. */
+int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
+                             const int32_t* fixups, int64_t n_fix,
+                             const int32_t* idx, const float* val,
+                             const float* x, int64_t ldx, const float* bias,
+                             const float* gamma, const float* beta, float eps,
+                             int64_t rows, int64_t dim, float* h, float* out,
+                             float* mean, float* rstd, float* workspace,
+                             int64_t n_slots, void* stream);
+
+/* Backward of out = ReLU(LayerNorm(h)) given g = dL/dout: writes
+ * gh = dL/dh [rows, dim], dgamma [dim] and dbeta [dim] (deterministic:
+ * per-wavefront partials reduced in order).  workspace: at least
+ * (2 * 4 + 1) * dim floats; up to (2 * 4096 + 1) * dim are used. */
+int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
+                        const float* rstd, const float* gamma, const float* beta,
+                        int64_t rows, int64_t dim, float* gh, float* dgamma,
+                        float* dbeta, float* workspace, int64_t workspace_floats,
+                        void* stream);
+
 /* Bias gradient of the GCN layer, db = sum_i G[i, :D] (fp32, deterministic:
  * fixed row chunks, partials reduced in chunk order).  Replaces the bias
  * gradient of PyG GCNConv's "+ bias" (grinnder/nn/gcn.py:53-56).
