@@ -153,23 +153,28 @@ def summarize_profile(root: str) -> None:
                   f"{tot / 1e6:>10.3f} {100 * tot / total:>6.2f}  {r['Name'][:150]}")
     for path in sorted(glob.glob(os.path.join(root, "**", "*counter_collection.csv"),
                                  recursive=True)):
-        acc = defaultdict(lambda: [0, 0.0, 0.0])
+        acc = defaultdict(lambda: [0, 0.0, 0.0, float("inf"), 0.0])
         with open(path) as f:
             for r in csv.DictReader(f):
                 key = (r["Kernel_Name"], r["Counter_Name"])
                 e = acc[key]
+                v = float(r["Counter_Value"])
                 e[0] += 1
-                e[1] += float(r["Counter_Value"])
+                e[1] += v
                 e[2] += float(r.get("End_Timestamp", 0)) - float(r.get("Start_Timestamp", 0))
-        print(f"# counters ({os.path.basename(path)}): per-dispatch means")
-        print(f"{'dispatches':>10} {'mean_value':>16} {'avg_us':>10}  counter  kernel")
-        for (k, c), (n, v, t) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
+                e[3] = min(e[3], v)
+                e[4] = max(e[4], v)
+        print(f"# counters ({os.path.basename(path)}): per-dispatch mean / min / max")
+        print(f"{'dispatches':>10} {'mean_value':>16} {'min':>14} {'max':>14} {'avg_us':>10}"
+              f"  counter  kernel")
+        for (k, c), (n, v, t, lo, hi) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
             if n == 0:
                 continue
             if not any(s in k for s in ("aggregate", "gat_", "copy", "gemm", "Cijk", "gather",
                                         "scatter", "neg_kernel", "ln_relu")):
                 continue
-            print(f"{n:>10} {v / n:>16.1f} {t / n / 1e3:>10.1f}  {c}  {k[:140]}")
+            print(f"{n:>10} {v / n:>16.1f} {lo:>14.1f} {hi:>14.1f} {t / n / 1e3:>10.1f}  {c}"
+                  f"  {k[:140]}")
 
 
 def main():

@@ -190,7 +190,7 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
         gh = torch.empty_like(h)
         dgamma = torch.empty(D, dtype=torch.float32, device=dev)
         dbeta = torch.empty(D, dtype=torch.float32, device=dev)
-        nwaves = min(4096, max(4, (B + 15) // 16))
+        nwaves = min(8192, max(4, (B + 15) // 16))
         nwaves = (nwaves + 3) // 4 * 4
         ws = torch.empty((2 * nwaves + 1) * D, dtype=torch.float32, device=dev)
         _lib.call("gr_ln_relu_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),

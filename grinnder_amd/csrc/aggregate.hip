@@ -345,38 +345,57 @@ __global__ __launch_bounds__(256) void aggregate_ln_relu_units(
                               out + row * dim, mean + row, rstd + row, lane);
 }
 
-// Split rows of the fused epilogue: ordered sum of the partials + bias into
-// h (one wavefront per row), then the LayerNorm/ReLU over that row.
+// Split rows of the fused epilogue: one workgroup per split row.  Each thread
+// owns features f = tid, tid + 256, ... (dim <= 1024): ordered sum of the
+// partials + bias into h, then the row's LayerNorm statistics by a fixed-order
+// workgroup reduction, then out = ReLU(LN(h)).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum64(v);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 __global__ __launch_bounds__(256) void aggregate_ln_relu_fixup(
-    const int32_t* __restrict__ fix, int64_t n_fix, const float* __restrict__ ws, int dim,
+    const int32_t* __restrict__ fix, const float* __restrict__ ws, int dim,
     const float* __restrict__ bias, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ h, float* __restrict__ out,
     float* __restrict__ mean, float* __restrict__ rstd) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wid =
-      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  if (wid >= n_fix) return;
-  const int row = fix[3 * wid + 0], first = fix[3 * wid + 1], n = fix[3 * wid + 2];
-  float* hrow = h + (int64_t)row * dim;
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int row = fix[3 * r + 0], first = fix[3 * r + 1], n = fix[3 * r + 2];
+  float hv[4];
   float s = 0.f;
-  for (int f = lane; f < dim; f += 64) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int f = threadIdx.x + q * 256;
     float a = 0.f;
-    for (int k = 0; k < n; ++k) a += ws[(int64_t)(first + k) * dim + f];
-    if (bias != nullptr) a += bias[f];
-    hrow[f] = a;
+    if (f < dim) {
+      const float* p = ws + (int64_t)first * dim + f;
+      for (int k = 0; k < n; ++k) a += p[(int64_t)k * dim];
+      if (bias != nullptr) a += bias[f];
+      h[(int64_t)row * dim + f] = a;
+    }
+    hv[q] = a;
     s += a;
   }
-  const float mu = wave_sum64(s) / (float)dim;
-  float q = 0.f;
-  for (int f = lane; f < dim; f += 64) {
-    const float dlt = hrow[f] - mu;
-    q += dlt * dlt;
+  const float mu = block_sum256(s, red) / (float)dim;
+  float qv = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int f = threadIdx.x + q * 256;
+    const float dlt = hv[q] - mu;
+    qv += f < dim ? dlt * dlt : 0.f;
   }
-  const float rs = 1.0f / sqrtf(wave_sum64(q) / (float)dim + eps);
-  float* orow = out + (int64_t)row * dim;
-  for (int f = lane; f < dim; f += 64)
-    orow[f] = fmaxf(ln_affine(hrow[f], mu, rs, gamma[f], beta[f]), 0.f);
-  if (lane == 0) {
+  const float rs = 1.0f / sqrtf(block_sum256(qv, red) / (float)dim + eps);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int f = threadIdx.x + q * 256;
+    if (f < dim) out[(int64_t)row * dim + f] = fmaxf(ln_affine(hv[q], mu, rs, gamma[f], beta[f]), 0.f);
+  }
+  if (threadIdx.x == 0) {
     mean[row] = mu;
     rstd[row] = rs;
   }
@@ -476,13 +495,38 @@ __global__ __launch_bounds__(256) void colsum_partial(const float* __restrict__ 
   }
 }
 
+// Column sums of part[nblk, dim] over nblk, deterministic: a workgroup owns
+// 16 columns; its 16 row groups each sum rows g, g+16, ... of their column in
+// order, then the 16 group sums are added in group order.
 __global__ __launch_bounds__(256) void colsum_final(const float* __restrict__ part, int nblk,
                                                     int dim, float* __restrict__ out) {
-  const int f = blockIdx.x * 256 + threadIdx.x;
-  if (f >= dim) return;
+  __shared__ float red[16][17];
+  const int cl = threadIdx.x & 15;
+  const int grp = threadIdx.x >> 4;
+  const int f = blockIdx.x * 16 + cl;
   float s = 0.f;
-  for (int b = 0; b < nblk; ++b) s += part[(int64_t)b * dim + f];
-  out[f] = s;
+  if (f < dim) {
+    int b = grp;
+    for (; b + 48 < nblk; b += 64) {
+      const float a0 = part[(int64_t)b * dim + f];
+      const float a1 = part[(int64_t)(b + 16) * dim + f];
+      const float a2 = part[(int64_t)(b + 32) * dim + f];
+      const float a3 = part[(int64_t)(b + 48) * dim + f];
+      s += a0;
+      s += a1;
+      s += a2;
+      s += a3;
+    }
+    for (; b < nblk; b += 16) s += part[(int64_t)b * dim + f];
+  }
+  red[grp][cl] = s;
+  __syncthreads();
+  if (grp == 0 && f < dim) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) t += red[g][cl];
+    out[f] = t;
+  }
 }
 
 template <int VEC, int G, int NCH>
@@ -587,7 +631,7 @@ extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t 
   hipLaunchKernelGGL(gr_agg::colsum_partial, dim3((unsigned)nblk), dim3(256), 0, s, x, rows, (int)dim,
                      ldx, chunk, workspace);
   GR_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, s,
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((dim + 15) / 16)), dim3(256), 0, s,
                      workspace, (int)nblk, (int)dim, out);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
@@ -663,9 +707,9 @@ extern "C" int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
   }
   GR_HIP_CHECK(err);
   if (n_fix > 0) {
-    hipLaunchKernelGGL(gr_agg::aggregate_ln_relu_fixup, dim3((unsigned)((n_fix + 3) / 4)),
-                       dim3(256), 0, s, fixups, n_fix, workspace, d, bias, gamma, beta, eps, h,
-                       out, mean, rstd);
+    GR_REQUIRE(n_fix <= INT32_MAX, "gcn_aggregate_ln_relu: too many split rows");
+    hipLaunchKernelGGL(gr_agg::aggregate_ln_relu_fixup, dim3((unsigned)n_fix), dim3(256), 0, s,
+                       fixups, workspace, d, bias, gamma, beta, eps, h, out, mean, rstd);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;
@@ -692,7 +736,7 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
   }
   // Wavefront count: enough to fill the chip, bounded by the workspace
   // (2 * nwaves * dim floats of partials + dim for the reduction pass).
-  int64_t nwaves = std::min<int64_t>(4096, std::max<int64_t>(4, (rows + 15) / 16));
+  int64_t nwaves = std::min<int64_t>(8192, std::max<int64_t>(4, (rows + 15) / 16));
   nwaves = (nwaves + 3) / 4 * 4;
   const int64_t cap = (workspace_floats / dim - 1) / 2 / 4 * 4;
   GR_REQUIRE(cap >= 4, "ln_relu_backward: workspace too small");
@@ -713,9 +757,9 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
 #undef GR_LNB
   GR_HIP_CHECK(hipGetLastError());
   // dgamma / dbeta = column sums of the partials, in wavefront order.
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 255) / 256)), dim3(256), 0, s, pg,
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s, pg,
                      (int)nwaves, d, dgamma);
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 255) / 256)), dim3(256), 0, s, pb,
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s, pb,
                      (int)nwaves, d, dbeta);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;

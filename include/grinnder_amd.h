@@ -229,7 +229,7 @@ int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
 /* Backward of out = ReLU(LayerNorm(h)) given g = dL/dout: writes
  * gh = dL/dh [rows, dim], dgamma [dim] and dbeta [dim] (deterministic:
  * per-wavefront partials reduced in order).  workspace: at least
- * (2 * 4 + 1) * dim floats; up to (2 * 4096 + 1) * dim are used. */
+ * (2 * 4 + 1) * dim floats; up to (2 * 8192 + 1) * dim are used. */
 int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
                         const float* rstd, const float* gamma, const float* beta,
                         int64_t rows, int64_t dim, float* gh, float* dgamma,
