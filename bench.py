@@ -9,8 +9,12 @@ Adam(lr=0.01, wd=5e-4).  A step is one Trainer.train_epoch (forward +
 backward of all layers + optimizer step) with every input resident in HBM.
 
 Printed JSON line (rank 0): metric/value/unit = aggregation fwd+bwd GTEPS of
-the whole epoch (6 passes x nnz edges per epoch / epoch wall time), with the
-kernel-level aggregation GTEPS, HBM fraction and epoch time alongside, the
+the whole epoch: the reference model's 2 x num_layers aggregation passes of
+nnz edges each per epoch, divided by the epoch wall time.  (A layer that
+widens aggregates first here, so its backward needs no aggregation; the
+edges actually traversed per epoch are reported as `edges_per_epoch`.)  The
+kernel-level aggregation GTEPS (edges traversed / time inside the aggregation
+passes), HBM fraction and epoch time go alongside, with the
 roofline of the dominant kernel (the D=256 GCN aggregation passes, timed with
 HIP events on their stream) and a CPU baseline (the oracle's sequential
 aggregation on a bounded row sample).
@@ -300,7 +304,8 @@ def main():
                    "num_parts": cfg["num_parts"], "model": cfg["model"],
                    "halo_amplification": round(graph.halo_amplification(), 4)},
         "epoch_s": round(epoch_s, 5),
-        "agg_kernel_gteps": round(useful_edges / (agg_ms / 1e3) / 1e9, 4),
+        "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,
+        "agg_kernel_gteps": round(sum(r.edges for r in recs_agg) / (agg_ms / 1e3) / 1e9, 4),
         "agg_hbm_frac": round(agg_bytes / (agg_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "agg_ms_per_epoch": round(agg_ms / args.steps, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,

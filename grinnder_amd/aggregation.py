@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import contextlib
 from dataclasses import dataclass
-from typing import List, Optional
+from typing import List, Optional, Tuple
 
 import torch
 from torch import Tensor
@@ -149,6 +149,25 @@ def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None) -> T
     return _GCNAggregate.apply(z, bias, plan)
 
 
+def ln_relu_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: Tensor,
+                     beta: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """(dL/dh, dgamma, dbeta) of out = ReLU(LayerNorm(h)) given dL/dout (GPU)."""
+    gout = gout.contiguous()
+    B, D = h.shape
+    dev = h.device
+    gh = torch.empty_like(h)
+    dgamma = torch.empty(D, dtype=torch.float32, device=dev)
+    dbeta = torch.empty(D, dtype=torch.float32, device=dev)
+    nwaves = min(8192, max(4, (B + 15) // 16))
+    nwaves = (nwaves + 3) // 4 * 4
+    ws = torch.empty((2 * nwaves + 1) * D, dtype=torch.float32, device=dev)
+    _lib.call("gr_ln_relu_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
+              rstd.data_ptr(), gamma.data_ptr(), beta.data_ptr(), B, D, gh.data_ptr(),
+              dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws.numel(),
+              _lib.stream_handle())
+    return gh, dgamma, dbeta
+
+
 class _GCNAggregateLNReLU(torch.autograd.Function):
     """out = ReLU(LayerNorm(A Z + b)) with the LayerNorm/ReLU fused into the
     aggregation epilogue; backward: fused LN/ReLU gradient, then dZ = A^T gh."""
@@ -184,19 +203,7 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
     def backward(ctx, gout: Tensor):
         h, mean, rstd, g, bt = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
-        gout = gout.contiguous()
-        B, D = h.shape
-        dev = h.device
-        gh = torch.empty_like(h)
-        dgamma = torch.empty(D, dtype=torch.float32, device=dev)
-        dbeta = torch.empty(D, dtype=torch.float32, device=dev)
-        nwaves = min(8192, max(4, (B + 15) // 16))
-        nwaves = (nwaves + 3) // 4 * 4
-        ws = torch.empty((2 * nwaves + 1) * D, dtype=torch.float32, device=dev)
-        _lib.call("gr_ln_relu_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
-                  rstd.data_ptr(), g.data_ptr(), bt.data_ptr(), B, D, gh.data_ptr(),
-                  dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws.numel(),
-                  _lib.stream_handle())
+        gh, dgamma, dbeta = ln_relu_backward(gout, h, mean, rstd, g, bt)
         dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd") \
             if ctx.needs_input_grad[0] else None
         db = column_sum(gh) if ctx.has_bias else None

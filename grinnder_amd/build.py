@@ -27,6 +27,7 @@ SOURCES = [
     "transfer.hip",
     "aggregate.hip",
     "gat.hip",
+    "gemm.hip",
 ]
 
 # Packed-FP32 instructions are disabled for every device compile.

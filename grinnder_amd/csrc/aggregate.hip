@@ -473,6 +473,49 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
   }
 }
 
+// Dense epilogue of a layer whose product was formed outside the aggregation:
+// h = z + bias, out = ReLU(LayerNorm(h)), with the same row statistics and
+// affine expression as the fused aggregation epilogue.  One wavefront per row,
+// grid-stride.  h may be z itself (ldz == dim): each lane reads its elements
+// of the row before the row statistics are reduced, and writes them after.
+template <int VEC, int NCH>
+__global__ __launch_bounds__(256) void bias_ln_relu_rows(
+    const float* z, int64_t ldz, const float* __restrict__ bias,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps, int dim,
+    int64_t rows, float* h, float* __restrict__ out, float* __restrict__ mean,
+    float* __restrict__ rstd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  bool fvalid[NCH];
+  int foff[NCH], fld[NCH];
+  float bv[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    foff[ch] = (ch * 64 + lane) * VEC;
+    fvalid[ch] = foff[ch] < dim;
+    fld[ch] = fvalid[ch] ? foff[ch] : dim - VEC;
+    if (bias != nullptr) {
+      load_vec<VEC>(bias + fld[ch], bv[ch]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) bv[ch][j] = 0.f;
+    }
+  }
+  for (int64_t r = wid; r < rows; r += nwaves) {
+    float acc[NCH][VEC];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      load_vec<VEC>(z + r * ldz + fld[ch], acc[ch]);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[ch][j] += bv[ch][j];
+    }
+    ln_relu_store_row<VEC, NCH>(acc, fvalid, foff, dim, gamma, beta, eps, h + r * dim,
+                                out + r * dim, mean + r, rstd + r, lane);
+  }
+}
+
 // Column sums of a [rows, dim] matrix, two passes, fixed order: workgroup b
 // sums rows [b*chunk, (b+1)*chunk) into part[b, :]; then part is reduced over
 // b in ascending order.  Each thread owns columns f = tid, tid + 256, ...
@@ -724,7 +767,8 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
   int vec, nch;
   GR_REQUIRE(rows >= 0 && dim >= 1 && fused_shape(dim, &vec, &nch),
              "ln_relu_backward: dim %lld unsupported", (long long)dim);
-  GR_REQUIRE(g && h && mean && rstd && gamma && beta && gh && dgamma && dbeta && workspace,
+  GR_REQUIRE(gamma && beta && dgamma && dbeta && workspace &&
+                 (rows == 0 || (g && h && mean && rstd && gh)),
              "ln_relu_backward: NULL pointer");
   const bool al = gr_agg::aligned(g, 16) && gr_agg::aligned(h, 16) && gr_agg::aligned(gh, 16) &&
                   gr_agg::aligned(gamma, 16) && gr_agg::aligned(beta, 16) &&
@@ -761,6 +805,44 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
                      (int)nwaves, d, dgamma);
   hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s, pb,
                      (int)nwaves, d, dbeta);
+  GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}
+
+extern "C" int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
+                               const float* gamma, const float* beta, float eps, int64_t rows,
+                               int64_t dim, float* h, float* out, float* mean, float* rstd,
+                               void* stream) {
+  gr::clear_error();
+  int vec, nch;
+  GR_REQUIRE(rows >= 0 && dim >= 1 && fused_shape(dim, &vec, &nch),
+             "bias_ln_relu: dim %lld unsupported (max 1024)", (long long)dim);
+  GR_REQUIRE(ldz >= dim, "bias_ln_relu: ldz < dim");
+  GR_REQUIRE(h != z || ldz == dim, "bias_ln_relu: in-place h needs ldz == dim");
+  if (rows == 0) return GR_OK;
+  GR_REQUIRE(z && gamma && beta && h && out && mean && rstd, "bias_ln_relu: NULL pointer");
+  if (vec == 4) {
+    const bool al = gr_agg::aligned(z, 16) && ldz % 4 == 0 && gr_agg::aligned(h, 16) &&
+                    gr_agg::aligned(out, 16) && gr_agg::aligned(gamma, 16) &&
+                    gr_agg::aligned(beta, 16) && (bias == nullptr || gr_agg::aligned(bias, 16));
+    if (!al) {
+      GR_REQUIRE(dim <= 256, "bias_ln_relu: misaligned rows wider than 256");
+      vec = 1;
+      nch = dim <= 64 ? 1 : (dim <= 128 ? 2 : 4);
+    }
+  }
+  hipStream_t s = gr::as_stream(stream);
+  const int d = (int)dim;
+  const unsigned blocks = (unsigned)std::min<int64_t>(8192, (rows + 3) / 4);
+#define GR_BLR(V, N)                                                                    \
+  hipLaunchKernelGGL((gr_agg::bias_ln_relu_rows<V, N>), dim3(blocks), dim3(256), 0, s, z, \
+                     ldz, bias, gamma, beta, eps, d, rows, h, out, mean, rstd)
+  if (vec == 4) {
+    if (nch == 1) GR_BLR(4, 1); else if (nch == 2) GR_BLR(4, 2); else GR_BLR(4, 4);
+  } else {
+    if (nch == 1) GR_BLR(1, 1); else if (nch == 2) GR_BLR(1, 2); else GR_BLR(1, 4);
+  }
+#undef GR_BLR
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }

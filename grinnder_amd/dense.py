@@ -1,0 +1,141 @@
+"""Dense per-layer transform of the conv layers, on the HIP kernels.
+
+PyG's GCNConv / GATConv (grinnder/nn/gcn.py:53-56, grinnder/nn/gat.py:54-61)
+apply a bias-free ``Linear`` to the node features.  Its forward and input
+gradient are plain tall-skinny matrix products (``torch.mm`` on hipBLASLt);
+its weight gradient dW = dZ^T X reduces over all K node rows of the
+partition with M, N <= a few hundred, a shape the library GEMMs split poorly.
+``linear`` keeps the forward on torch and computes dW with ``gr_gemm_tn``
+(split-K fp32 MFMA, partials summed in a fixed order).
+
+``bias_ln_relu`` is the dense counterpart of the fused aggregation epilogue,
+used when a layer aggregates first and multiplies afterwards.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from grinnder_amd import _lib
+
+
+def _check(name: str, t: Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (HIP); got {t.device}")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32; got {t.dtype}")
+
+
+def gemm_tn_splits(m: int, n: int, k: int) -> Tuple[int, int]:
+    """Default K split count and workspace floats of ``gemm_tn`` for a shape."""
+    splits = ctypes.c_int64(0)
+    ws = ctypes.c_int64(0)
+    _lib.call("gr_gemm_tn_workspace", m, n, k, ctypes.addressof(splits), ctypes.addressof(ws))
+    return splits.value, ws.value
+
+
+def gemm_tn(a: Tensor, b: Tensor, out: Optional[Tensor] = None, beta: float = 0.0,
+            splits: Optional[int] = None) -> Tensor:
+    """C = a^T b (+ beta * out) for a [K, M], b [K, N] row-major fp32 device matrices."""
+    _check("a", a)
+    _check("b", b)
+    if a.dim() != 2 or b.dim() != 2 or a.size(0) != b.size(0):
+        raise ValueError(f"gemm_tn: a {tuple(a.shape)} and b {tuple(b.shape)} need equal rows")
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    if b.stride(1) != 1:
+        b = b.contiguous()
+    k, m = a.shape
+    n = b.size(1)
+    if out is None:
+        if beta != 0.0:
+            raise ValueError("gemm_tn: beta != 0 needs `out`")
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    elif out.shape != (m, n) or not out.is_contiguous():
+        raise ValueError(f"gemm_tn: out must be a contiguous [{m}, {n}] matrix")
+    default_splits, _ = gemm_tn_splits(m, n, k)
+    s = default_splits if splits is None else int(splits)
+    ws = torch.empty(max(1, s * m * n), dtype=torch.float32, device=a.device)
+    _lib.call("gr_gemm_tn", a.data_ptr(), max(a.stride(0), m), b.data_ptr(),
+              max(b.stride(0), n), m, n, k, float(beta), out.data_ptr(), ws.data_ptr(),
+              ws.numel(), s, _lib.stream_handle())
+    return out
+
+
+class _Linear(torch.autograd.Function):
+    """y = x W^T (+ b); dx = dy W (torch), dW = dy^T x (gr_gemm_tn), db = sum dy."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+        x2 = x.reshape(-1, x.size(-1))
+        if bias is not None:
+            y = torch.addmm(bias, x2, weight.t())
+        else:
+            y = torch.mm(x2, weight.t())
+        ctx.save_for_backward(x2, weight)
+        ctx.in_shape = x.shape
+        ctx.has_bias = bias is not None
+        return y.reshape(*x.shape[:-1], weight.size(0))
+
+    @staticmethod
+    def backward(ctx, gy: Tensor):
+        x2, weight = ctx.saved_tensors
+        gy2 = gy.reshape(-1, weight.size(0)).contiguous()
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(gy2, weight).reshape(ctx.in_shape)
+        if ctx.needs_input_grad[1]:
+            dw = gemm_tn(gy2, x2)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            from grinnder_amd.aggregation import column_sum
+            db = column_sum(gy2)
+        return dx, dw, db
+
+
+def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+    """``F.linear`` whose weight gradient runs on the split-K MFMA kernel (GPU)."""
+    if not x.is_cuda:
+        raise RuntimeError(f"linear: x must be a GPU tensor (HIP); got {x.device}")
+    return _Linear.apply(x, weight, bias)
+
+
+class _BiasLNReLU(torch.autograd.Function):
+    """out = ReLU(LayerNorm(z + b)); backward with gr_ln_relu_backward."""
+
+    @staticmethod
+    def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
+                eps: float) -> Tensor:
+        z = z.contiguous()
+        rows, dim = z.shape
+        dev = z.device
+        h = torch.empty_like(z)
+        out = torch.empty_like(z)
+        mean = torch.empty(rows, dtype=torch.float32, device=dev)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        b = bias.contiguous() if bias is not None else None
+        g, bt = gamma.contiguous(), beta.contiguous()
+        _lib.call("gr_bias_ln_relu", z.data_ptr(), z.stride(0), _lib.ptr(b), g.data_ptr(),
+                  bt.data_ptr(), float(eps), rows, dim, h.data_ptr(), out.data_ptr(),
+                  mean.data_ptr(), rstd.data_ptr(), _lib.stream_handle())
+        ctx.save_for_backward(h, mean, rstd, g, bt)
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, gout: Tensor):
+        from grinnder_amd.aggregation import column_sum, ln_relu_backward
+        h, mean, rstd, g, bt = ctx.saved_tensors
+        gh, dgamma, dbeta = ln_relu_backward(gout, h, mean, rstd, g, bt)
+        db = column_sum(gh) if ctx.has_bias else None
+        return gh, db, dgamma, dbeta, None
+
+
+def bias_ln_relu(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
+                 eps: float = 1e-5) -> Tensor:
+    """ReLU(LayerNorm(z + bias)) over the rows of z (GPU, one pass)."""
+    _check("z", z)
+    return _BiasLNReLU.apply(z, bias, gamma, beta, eps)

@@ -19,6 +19,7 @@ from torch.nn import Linear, Module, Parameter
 
 from grinnder_amd.aggregation import gat_attention, gcn_aggregate
 from grinnder_amd.data.adjacency import Adjacency
+from grinnder_amd.dense import linear
 
 
 def glorot_(t: Tensor) -> Tensor:
@@ -33,6 +34,12 @@ class GCNConv(Module):
 
     Only ``normalize=False`` is supported: the normalisation is computed once
     on the full graph and stored as adjacency values, as in the reference.
+
+    PyG multiplies first and aggregates the out_channels-wide product.  When
+    the layer widens (in_channels < out_channels) this layer aggregates first,
+    (A x) Wᵀ + b: the same function with the fp32 sums reassociated, but the
+    neighbour gather moves in_channels-wide rows, and when x needs no gradient
+    the backward has no aggregation at all.
     """
 
     def __init__(self, in_channels: int, out_channels: int, normalize: bool = False,
@@ -52,8 +59,13 @@ class GCNConv(Module):
         if self.bias is not None:
             torch.nn.init.zeros_(self.bias)
 
+    def aggregate_first(self) -> bool:
+        return self.in_channels < self.out_channels
+
     def forward(self, x: Tensor, adj: Adjacency) -> Tensor:
-        return gcn_aggregate(self.lin(x), adj, self.bias)
+        if self.aggregate_first():
+            return linear(gcn_aggregate(x, adj), self.lin.weight, self.bias)
+        return gcn_aggregate(linear(x, self.lin.weight), adj, self.bias)
 
     def __repr__(self) -> str:
         return f"{self.__class__.__name__}({self.in_channels}, {self.out_channels})"
@@ -113,7 +125,7 @@ class GATConv(Module):
                 raise ValueError("GATConv expects (x, x[:num_dst]) with a shared projection")
         else:
             x_src = x
-        hs = self.lin(x_src)
+        hs = linear(x_src, self.lin.weight)
         return gat_attention(hs, adj, self.att_src, self.att_dst, self.bias, self.heads,
                              self.out_channels, self.concat)
 

@@ -8,7 +8,8 @@ import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
 
-from grinnder_amd.aggregation import gcn_aggregate_ln_relu
+from grinnder_amd.aggregation import gcn_aggregate, gcn_aggregate_ln_relu
+from grinnder_amd.dense import bias_ln_relu, linear
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.nn.conv import GCNConv
 
@@ -52,8 +53,11 @@ class GCN(GriNNderModel):
     def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
         if self._fusable(layer, x, adj):
             conv, norm = self.convs[layer], self.norms[layer]
-            return gcn_aggregate_ln_relu(conv.lin(x), adj, conv.bias, norm.weight, norm.bias,
-                                         norm.eps)
+            if conv.aggregate_first():
+                z = linear(gcn_aggregate(x, adj), conv.lin.weight)
+                return bias_ln_relu(z, conv.bias, norm.weight, norm.bias, norm.eps)
+            return gcn_aggregate_ln_relu(linear(x, conv.lin.weight), adj, conv.bias,
+                                         norm.weight, norm.bias, norm.eps)
         h = self.convs[layer](x, adj)
         if layer < self.num_layers - 1:
             if self.norms is not None:

@@ -244,6 +244,37 @@ int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
                   float* out, float* workspace, int64_t workspace_floats,
                   void* stream);
 
+/* Dense form of the fused epilogue, for a layer whose product Z was formed
+ * outside the aggregation (aggregate-first GCN: Z = (A X) W^T):
+ *   h = Z + bias, out = ReLU(LayerNorm(h)), mean, rstd
+ * with the same expressions as gr_gcn_aggregate_ln_relu, so gr_ln_relu_backward
+ * is its backward.  Z is ldz-strided; h, out dense [rows, dim]; h may be Z
+ * itself when ldz == dim.  Replaces the LayerNorm + ReLU that follow the conv
+ * in grinnder/nn/gcn.py:64-72. */
+int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
+                    const float* gamma, const float* beta, float eps,
+                    int64_t rows, int64_t dim, float* h, float* out,
+                    float* mean, float* rstd, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dense weight gradient                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* C[M, N] = A^T B (+ beta * C) with A [K, M] (lda-strided rows) and B [K, N]
+ * (ldb-strided rows), fp32 on the matrix cores, split over K into `splits`
+ * chunks whose partial tiles are summed in chunk order (deterministic).  This
+ * is the weight gradient dW = dZ^T X of the conv's dense transform (the
+ * Linear inside PyG GCNConv / GATConv of grinnder/nn/gcn.py:53-56 and
+ * grinnder/nn/gat.py:54-61), whose K is the partition's row count.
+ * gr_gemm_tn_workspace returns the default split count and the workspace size
+ * in floats (splits * M * N) for a shape. */
+int gr_gemm_tn_workspace(int64_t m, int64_t n, int64_t k, int64_t* splits,
+                         int64_t* workspace_floats);
+int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t ldb,
+               int64_t m, int64_t n, int64_t k, float beta, float* c,
+               float* workspace, int64_t workspace_floats, int64_t splits,
+               void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GAT attention (device)                                                    */
 /*                                                                           */

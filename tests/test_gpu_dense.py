@@ -1,0 +1,143 @@
+"""GPU: the dense per-layer transform — split-K weight-gradient GEMM
+(gr_gemm_tn), the Linear autograd function built on it, and the dense
+bias + LayerNorm + ReLU epilogue (gr_bias_ln_relu) — against float64 torch.
+fp32 tolerance: max-abs-normalised error <= 1e-5 (TOL)."""
+
+import pytest
+import torch
+
+from grinnder_amd import _lib
+from grinnder_amd.dense import bias_ln_relu, gemm_tn, gemm_tn_splits, linear
+from tests.graphs import TOL, max_abs_norm_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _randn(*shape, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dev)
+
+
+@pytest.mark.parametrize("k,m,n", [(0, 5, 7), (1, 1, 1), (37, 3, 5), (1000, 47, 256),
+                                   (5000, 256, 100), (3001, 130, 129), (200_000, 256, 256),
+                                   (70_000, 47, 256)])
+def test_gemm_tn_matches_fp64(gpu, k, m, n):
+    a = _randn(k, m, seed=k + m, dev=gpu)
+    b = _randn(k, n, seed=k + n + 1, dev=gpu)
+    c = gemm_tn(a, b)
+    ref = a.double().t() @ b.double()
+    if k == 0:
+        assert torch.equal(c.cpu(), torch.zeros(m, n))
+    else:
+        assert max_abs_norm_err(c, ref) <= TOL
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8, 64, 1000])
+def test_gemm_tn_split_counts(gpu, splits):
+    """Any split count gives the same product (chunks of 16-row steps)."""
+    a = _randn(20_000, 64, seed=1, dev=gpu)
+    b = _randn(20_000, 200, seed=2, dev=gpu)
+    c = gemm_tn(a, b, splits=splits)
+    assert max_abs_norm_err(c, a.double().t() @ b.double()) <= TOL
+
+
+def test_gemm_tn_strided_beta_and_determinism(gpu):
+    big_a = _randn(9000, 300, seed=3, dev=gpu)
+    big_b = _randn(9000, 260, seed=4, dev=gpu)
+    a, b = big_a[:, 17:273], big_b[:, :256]  # lda = 300, ldb = 260, offset rows
+    c0 = _randn(256, 256, seed=5, dev=gpu)
+    c = c0.clone()
+    gemm_tn(a, b, out=c, beta=0.5)
+    ref = 0.5 * c0.double() + a.double().t() @ b.double()
+    assert max_abs_norm_err(c, ref) <= TOL
+    again = gemm_tn(a, b)
+    assert torch.equal(again, gemm_tn(a, b))  # fixed reduction order
+
+
+def test_gemm_tn_workspace_checked(gpu):
+    a = torch.zeros(100, 8, device=gpu)
+    b = torch.zeros(100, 8, device=gpu)
+    c = torch.empty(8, 8, device=gpu)
+    ws = torch.empty(8 * 8 * 2, device=gpu)
+    with pytest.raises(_lib.GrError, match="workspace"):
+        _lib.call("gr_gemm_tn", a.data_ptr(), 8, b.data_ptr(), 8, 8, 8, 100, 0.0,
+                  c.data_ptr(), ws.data_ptr(), ws.numel(), 7, _lib.stream_handle())
+
+
+@pytest.mark.parametrize("rows,fin,fout,bias", [(5000, 100, 256, True), (777, 256, 47, False),
+                                                (0, 16, 32, True)])
+def test_linear_autograd_matches_fp64(gpu, rows, fin, fout, bias):
+    x = _randn(rows, fin, seed=rows, dev=gpu).requires_grad_(True)
+    w = _randn(fout, fin, seed=fin, dev=gpu).mul_(0.1).requires_grad_(True)
+    b = _randn(fout, seed=fout, dev=gpu).requires_grad_(True) if bias else None
+    go = _randn(rows, fout, seed=7, dev=gpu)
+    y = linear(x, w, b)
+    y.backward(go)
+    xd = x.detach().double().requires_grad_(True)
+    wd = w.detach().double().requires_grad_(True)
+    bd = b.detach().double().requires_grad_(True) if bias else None
+    yd = torch.nn.functional.linear(xd, wd, bd)
+    yd.backward(go.double())
+    if rows == 0:
+        assert y.shape == (0, fout) and torch.equal(w.grad.cpu(), torch.zeros(fout, fin))
+        return
+    assert max_abs_norm_err(y, yd) <= TOL
+    assert max_abs_norm_err(x.grad, xd.grad) <= TOL
+    assert max_abs_norm_err(w.grad, wd.grad) <= TOL
+    if bias:
+        assert max_abs_norm_err(b.grad, bd.grad) <= TOL
+
+
+@pytest.mark.parametrize("rows,dim,bias", [(4000, 256, True), (1500, 47, True), (300, 100, False),
+                                           (0, 64, True)])
+def test_bias_ln_relu_matches_fp64(gpu, rows, dim, bias):
+    z = _randn(rows, dim, seed=dim, dev=gpu).requires_grad_(True)
+    b = _randn(dim, seed=1, dev=gpu).requires_grad_(True) if bias else None
+    gamma = (1 + 0.1 * _randn(dim, seed=2, dev=gpu)).requires_grad_(True)
+    beta = (0.1 * _randn(dim, seed=3, dev=gpu)).requires_grad_(True)
+    go = _randn(rows, dim, seed=4, dev=gpu)
+    out = bias_ln_relu(z, b, gamma, beta, 1e-5)
+    out.backward(go)
+    zd = z.detach().double().requires_grad_(True)
+    bd = b.detach().double().requires_grad_(True) if bias else None
+    gd = gamma.detach().double().requires_grad_(True)
+    btd = beta.detach().double().requires_grad_(True)
+    h = zd + bd if bias else zd
+    ref = torch.relu(torch.nn.functional.layer_norm(h, (dim,), gd, btd, 1e-5))
+    ref.backward(go.double())
+    if rows == 0:
+        assert out.shape == (0, dim)
+        return
+    assert max_abs_norm_err(out, ref) <= TOL
+    assert max_abs_norm_err(z.grad, zd.grad) <= TOL
+    assert max_abs_norm_err(gamma.grad, gd.grad) <= TOL
+    assert max_abs_norm_err(beta.grad, btd.grad) <= TOL
+    if bias:
+        assert max_abs_norm_err(b.grad, bd.grad) <= TOL
+
+
+def test_bias_ln_relu_in_place_h(gpu):
+    """h may overwrite z (ldz == dim): same out and h as the out-of-place call."""
+    rows, dim = 999, 128
+    z = _randn(rows, dim, seed=9, dev=gpu)
+    bias = _randn(dim, seed=10, dev=gpu)
+    gamma = torch.ones(dim, device=gpu)
+    beta = torch.zeros(dim, device=gpu)
+    outs = []
+    for in_place in (False, True):
+        zz = z.clone()
+        h = zz if in_place else torch.empty_like(z)
+        out = torch.empty_like(z)
+        mean = torch.empty(rows, device=gpu)
+        rstd = torch.empty(rows, device=gpu)
+        _lib.call("gr_bias_ln_relu", zz.data_ptr(), dim, bias.data_ptr(), gamma.data_ptr(),
+                  beta.data_ptr(), 1e-5, rows, dim, h.data_ptr(), out.data_ptr(),
+                  mean.data_ptr(), rstd.data_ptr(), _lib.stream_handle())
+        outs.append((h.clone(), out.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][0], z + bias)
+
+
+def test_default_splits_shape(gpu):
+    s, ws = gemm_tn_splits(256, 256, 2_449_029)
+    assert s % 8 == 0 and ws == s * 256 * 256

@@ -159,10 +159,13 @@ def _vanilla(data, state, make_model):
 
 
 @pytest.mark.parametrize("norm", [False, True])
-def test_gcn_matches_dense_vanilla(gpu, norm):
-    data = _graph_data()
+@pytest.mark.parametrize("feat,hidden", [(8, 16), (24, 16)])
+def test_gcn_matches_dense_vanilla(gpu, norm, feat, hidden):
+    """feat < hidden: the first layer aggregates first, (A X) W^T; feat >
+    hidden: it multiplies first, A (X W^T), as PyG does."""
+    data = _graph_data(feat=feat)
     torch.manual_seed(7)
-    make = lambda: GCN(8, 16, 3, num_layers=2, dropout=0.0, norm=norm)  # noqa: E731
+    make = lambda: GCN(feat, hidden, 3, num_layers=2, dropout=0.0, norm=norm)  # noqa: E731
     state = make().state_dict()
     ref_loss, ref_grads = _vanilla(data, state, make)
     for parts, mode in [(1, "grinnder"), (4, "grinnder"), (4, "hongtu")]:

@@ -291,3 +291,23 @@ def test_partitioner_keeps_banded_graph_local():
                                 *(torch.ones(400, dtype=torch.bool),) * 3,
                                 GriNNderConfig(num_parts=4))
     assert g.halo_amplification() < 1.2  # a random cut would be ~ 2.7
+
+
+def test_gemm_tn_split_heuristic_and_argument_checks():
+    """Host-side planning of the split-K weight-gradient GEMM; the argument
+    checks reject a short workspace before anything reaches the device."""
+    from grinnder_amd.dense import gemm_tn_splits
+
+    for m, n, k in [(256, 256, 2_449_029), (47, 256, 10), (1, 1, 0), (256, 100, 100_000)]:
+        s, ws = gemm_tn_splits(m, n, k)
+        assert 1 <= s <= 4096 and ws == s * m * n
+    s, _ = gemm_tn_splits(256, 256, 2_449_029)
+    assert s % 8 == 0 and s * 4 >= 1024
+    fake = 256  # non-NULL pointers: the call must fail before any device access
+    with pytest.raises(_lib.GrError, match="workspace"):
+        _lib.call("gr_gemm_tn", fake, 8, fake, 8, 8, 8, 100, 0.0, fake, fake, 128, 7, None)
+    with pytest.raises(_lib.GrError, match="leading dimension"):
+        _lib.call("gr_gemm_tn", fake, 4, fake, 8, 8, 8, 100, 0.0, fake, fake, 10**6, 1, None)
+    with pytest.raises(_lib.GrError, match="in-place"):
+        _lib.call("gr_bias_ln_relu", fake, 12, None, fake, fake, 1e-5, 4, 8, fake, fake, fake,
+                  fake, None)
