@@ -28,6 +28,7 @@ SOURCES = [
     "aggregate.hip",
     "gat.hip",
     "gemm.hip",
+    "loss.hip",
 ]
 
 # Packed-FP32 instructions are disabled for every device compile.

@@ -42,14 +42,7 @@ from grinnder_amd.config import GriNNderConfig
 from grinnder_amd.data.graph import PartitionedGraph
 from grinnder_amd.engine.streams import StreamManager
 from grinnder_amd.nn.base import GriNNderModel
-from grinnder_amd.utils import compute_micro_f1
-
-
-def cross_entropy(logits: Tensor, target: Tensor, reduction: str) -> Tensor:
-    """Cross-entropy as log_softmax + gather + mean/sum (the same arithmetic as
-    F.cross_entropy; its fused NLL reduction kernel is slow for millions of rows)."""
-    nll = -logits.log_softmax(dim=-1).gather(1, target.unsqueeze(1)).squeeze(1)
-    return nll.mean() if reduction == "mean" else nll.sum()
+from grinnder_amd.loss import check_stats, mask_codes, masked_cross_entropy
 
 
 class Trainer:
@@ -90,6 +83,7 @@ class Trainer:
         self.activations: List[List[Optional[Tensor]]] = [[None] * P for _ in range(L)]
         self._pid_to_loss_idx: Dict[int, int] = {}
         self._resident: Dict[str, Tensor] = {}
+        self._label_cache: Dict[int, tuple] = {}
         if not self._fast:
             for l in range(L + 1):
                 self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
@@ -180,20 +174,16 @@ class Trainer:
         g = self.graph
         y = self._res("y", lambda: g.partition_labels(0).to(self.device))
         train = self._res("train", lambda: g.partition_train_mask(0).to(self.device))
-        val = self._res("val", lambda: g.partition_val_mask(0).to(self.device))
-        test = self._res("test", lambda: g.partition_test_mask(0).to(self.device))
-        n_train = self._res("n_train", lambda: torch.tensor(int(train.sum())))
-        n_train = int(n_train)
-        if n_train > 0:
-            loss = cross_entropy(out[train], y[train], "mean")
-            loss_value = float(loss.item())
-        else:
-            loss = out.sum() * 0.0
-            loss_value = 0.0
+        codes = self._res("codes", lambda: mask_codes(
+            train, g.partition_val_mask(0), g.partition_test_mask(0)))
+        loss, stats = masked_cross_entropy(out, y, codes, "mean")
+        st = stats.tolist()
+        check_stats(st)
+        n_train = st[0]
         metrics = {
-            "loss": loss_value,
-            "val_acc": compute_micro_f1(out, y, val),
-            "test_acc": compute_micro_f1(out, y, test),
+            "loss": float(loss) if n_train > 0 else 0.0,
+            "val_acc": st[1] / st[2] if st[2] else 0.0,
+            "test_acc": st[3] / st[4] if st[4] else 0.0,
             "_n_train": n_train,
         }
         return loss, metrics
@@ -286,10 +276,11 @@ class Trainer:
         last = self.model.num_layers - 1
         losses: List[Tensor] = []
         self._pid_to_loss_idx = {}
-        total_loss, n_train = 0.0, 0
-        val_correct = val_n = test_correct = test_n = 0.0
         if not pids:
             return losses, {"loss": 0.0, "val_acc": 0.0, "test_acc": 0.0, "_n_train": 0}
+
+        loss_sums: List[Tensor] = []
+        stat_rows: List[Tensor] = []
 
         def upload(pid: int, stream) -> None:
             act = self.activations[last][pid]
@@ -306,35 +297,38 @@ class Trainer:
                 if i + 1 < len(pids):
                     upload(pids[i + 1], s.h2d[(i + 1) % pool])
                 out = self.activations[last][pid]
-                y = self.graph.partition_labels(pid).to(self.device, non_blocking=False)
-                train = self.graph.partition_train_mask(pid).to(self.device)
-                val = self.graph.partition_val_mask(pid)
-                test = self.graph.partition_test_mask(pid)
-                n_part = int(self.graph.partition_train_mask(pid).sum())
-                if n_part > 0:
-                    loss = cross_entropy(out[train], y[train], "sum")
-                    total_loss += loss.item()
-                    n_train += n_part
-                else:
-                    loss = out.sum() * 0.0
+                y, codes = self._labels_and_codes(pid)
+                # Sum over the partition's train rows (zero, with a zero
+                # gradient, when it has none); the accuracy counts ride along.
+                loss, stats = masked_cross_entropy(out, y, codes, "sum")
                 self._pid_to_loss_idx[pid] = len(losses)
                 losses.append(loss)
-                with torch.no_grad():
-                    nv, nt = int(val.sum()), int(test.sum())
-                    if nv > 0:
-                        val_correct += compute_micro_f1(out, y, val) * nv
-                        val_n += nv
-                    if nt > 0:
-                        test_correct += compute_micro_f1(out, y, test) * nt
-                        test_n += nt
+                loss_sums.append(loss.detach())
+                stat_rows.append(stats)
                 self._free(out)
+            st = torch.stack(stat_rows).sum(0).tolist()
+            total_loss = float(torch.stack(loss_sums).double().sum())
+        check_stats(st)
+        n_train = st[0]
         metrics = {
             "loss": total_loss / max(n_train, 1),
-            "val_acc": val_correct / max(val_n, 1),
-            "test_acc": test_correct / max(test_n, 1),
+            "val_acc": st[1] / max(st[2], 1),
+            "test_acc": st[3] / max(st[4], 1),
             "_n_train": n_train,
         }
         return losses, metrics
+
+    def _labels_and_codes(self, pid: int):
+        """Device labels and uint8 train/val/test codes of a partition (cached)."""
+        hit = self._label_cache.get(pid)
+        if hit is None:
+            g = self.graph
+            y = g.partition_labels(pid).to(self.device)
+            codes = mask_codes(g.partition_train_mask(pid), g.partition_val_mask(pid),
+                               g.partition_test_mask(pid)).to(self.device)
+            hit = (y, codes)
+            self._label_cache[pid] = hit
+        return hit
 
     # ------------------------------------------------------------ backward
 

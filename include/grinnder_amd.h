@@ -257,6 +257,31 @@ int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
                     float* mean, float* rstd, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Loss and accuracy                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Masked softmax cross-entropy and argmax accuracy of a partition's logits
+ * [rows, classes] (ld-strided), one pass.  mask[r]: bit 0 train, bit 1 val,
+ * bit 2 test; labels int64.  Replaces the per-partition
+ * F.cross_entropy(out[train], y[train], reduction="sum") of
+ * grinnder/engine/trainer.py:709-721 (mean = 0) and the fast path's
+ * reduction="mean" (trainer.py:430-453, mean = 1), and the argmax accuracy of
+ * compute_micro_f1 (grinnder/utils.py:24-44) for val and test rows.
+ * Outputs (device): *loss (fp32; 0 when there are no train rows), stats[6] =
+ * {train rows, val correct, val rows, test correct, test rows, rows with a
+ * label outside [0, classes)} (the caller raises on the last), lse[r] =
+ * log-sum-exp of row r (may be NULL), and, when grad != NULL, the gradient of
+ * the train-row nll sum, grad[r, c] = softmax(x_r)_c - [c == y_r] on train
+ * rows and 0 elsewhere (ldg-strided); the caller scales it by dL/dloss (and
+ * 1 / train rows for the mean).  Sums are reduced in a fixed order in double.
+ * workspace: 1024 * 7 doubles suffice for any shape. */
+int gr_xent_forward(const float* logits, int64_t ld, int64_t rows,
+                    int64_t classes, const int64_t* labels, const uint8_t* mask,
+                    int32_t mean, float* lse, float* grad, int64_t ldg,
+                    float* loss, int64_t* stats, double* workspace,
+                    int64_t workspace_doubles, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Dense weight gradient                                                     */
 /* ------------------------------------------------------------------------ */
 

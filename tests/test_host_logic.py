@@ -311,3 +311,18 @@ def test_gemm_tn_split_heuristic_and_argument_checks():
     with pytest.raises(_lib.GrError, match="in-place"):
         _lib.call("gr_bias_ln_relu", fake, 12, None, fake, fake, 1e-5, 4, 8, fake, fake, fake,
                   fake, None)
+
+
+def test_loss_mask_codes_and_argument_checks():
+    from grinnder_amd.loss import mask_codes
+
+    b = lambda v: torch.tensor(v, dtype=torch.bool)  # noqa: E731
+    codes = mask_codes(b([1, 0, 1, 0]), b([0, 1, 1, 0]), b([0, 0, 1, 1]))
+    assert codes.dtype == torch.uint8 and codes.tolist() == [1, 2, 7, 4]
+    fake = 256  # rejected before any device access
+    with pytest.raises(_lib.GrError, match="ldg"):
+        _lib.call("gr_xent_forward", fake, 10, 5, 10, fake, fake, 0, None, fake, 4, fake, fake,
+                  fake, 7168, None)
+    with pytest.raises(_lib.GrError, match="workspace"):
+        _lib.call("gr_xent_forward", fake, 10, 5, 10, fake, fake, 0, None, None, 0, fake, fake,
+                  fake, 3, None)
