@@ -29,8 +29,16 @@ import json
 import os
 import sys
 import time
+from typing import Optional
 
 HBM_PEAK_GBPS = 8000.0
+CALIBRATION_KIB = 1 << 20      # bytes read (and written) by one calibration launch, in KiB
+CALIBRATION_KERNEL = "bitwise_not"
+# PMC summary whose FETCH_SIZE / WRITE_SIZE rows give roofline.traffic for C2.
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "c2_gcn_aggregate_traffic.txt")
+# The D=256 aggregation kernels of C2 (fused forward, CSC backward).
+C2_DOMINANT = ("aggregate_ln_relu_units<4, 1, 8>", "aggregate_units<4, 64, 1, 8>")
 CONFIGS_NAMES = ("c1", "c2", "c3", "c4", "c5")
 
 
@@ -175,10 +183,50 @@ def summarize_profile(root: str) -> None:
             if n == 0:
                 continue
             if not any(s in k for s in ("aggregate", "gat_", "copy", "gemm", "Cijk", "gather",
-                                        "scatter", "neg_kernel", "ln_relu")):
+                                        "scatter", CALIBRATION_KERNEL, "ln_relu", "xent")):
                 continue
             print(f"{n:>10} {v / n:>16.1f} {lo:>14.1f} {hi:>14.1f} {t / n / 1e3:>10.1f}  {c}"
                   f"  {k[:140]}")
+        for (k, c), (n, v, t, lo, hi) in acc.items():
+            if CALIBRATION_KERNEL in k and n:
+                print(f"# calibration {c}: {CALIBRATION_KERNEL} moves {CALIBRATION_KIB} KiB, "
+                      f"counter mean {v / n:.1f} KiB -> scale x{CALIBRATION_KIB / (v / n):.4f}")
+
+
+def traffic_from_profile(path: str, kernels) -> Optional[float]:
+    """HBM bytes per launch of `kernels` (averaged) from a committed PMC summary.
+
+    Each counter (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) is scaled by what
+    the same counter read for the calibration kernel, which moves a known
+    CALIBRATION_KIB.  None when the summary or a row is missing."""
+    if not os.path.exists(path):
+        return None
+    means = {}
+    with open(path) as f:
+        for line in f:
+            parts = line.split(None, 6)
+            if len(parts) < 7 or line.startswith("#"):
+                continue
+            try:
+                mean = float(parts[1])
+            except ValueError:
+                continue
+            counter, name = parts[5], parts[6]
+            if CALIBRATION_KERNEL in name:
+                means[("cal", counter)] = mean
+            for k in kernels:
+                if k in name:
+                    means[(k, counter)] = mean
+    total = 0.0
+    for k in kernels:
+        b = 0.0
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            cal, val = means.get(("cal", counter)), means.get((k, counter))
+            if not cal or val is None:
+                return None
+            b += val * (CALIBRATION_KIB / cal) * 1024.0
+        total += b
+    return total / len(kernels)
 
 
 def main():
@@ -276,6 +324,14 @@ def main():
                   "GBps": round(v[2] / (v[1] / 1e3) / 1e9, 1)} for k, v in per_pass.items()}
     log(f"passes: {json.dumps(passes)}")
 
+    traffic = None
+    if args.config == "c2":
+        t = traffic_from_profile(TRAFFIC_PROFILE, C2_DOMINANT)
+        traffic = None if t is None else round(t)
+        if traffic is not None:
+            log(f"roofline.traffic {traffic / 1e9:.1f} GB per D={cfg['hidden']} launch (PMC, "
+                f"calibrated) vs {dom_bytes / len(dom) / 1e9:.1f} GB algorithmic")
+
     cpu = None
     if not args.no_cpu_baseline:
         try:
@@ -310,7 +366,7 @@ def main():
         "agg_ms_per_epoch": round(agg_ms / args.steps, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None,
+                     "traffic": traffic,
                      "kernel": (f"aggregate_units (GCN SpMM, D={cfg['hidden']}, fwd CSR + bwd CSC)"
                                 if cfg["model"] == "gcn" else
                                 f"GAT attention fwd+bwd kernels, H*C={cfg['hidden']}")},
@@ -319,14 +375,15 @@ def main():
     }
     print(json.dumps(out), flush=True)
     if args.calibrate_copy:
-        # torch.neg is a plain elementwise kernel (its own name in the trace):
-        # it reads exactly 1 GiB and writes exactly 1 GiB per launch.
-        src = torch.ones(1 << 28, dtype=torch.float32, device=device)
+        # torch.bitwise_not on int32 is a plain elementwise kernel that no
+        # other part of the run launches: it reads exactly 1 GiB and writes
+        # exactly 1 GiB per launch (CALIBRATION_KIB of each).
+        src = torch.ones(1 << 28, dtype=torch.int32, device=device)
         dst = torch.empty_like(src)
         for _ in range(3):
-            torch.neg(src, out=dst)
+            torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
-        log("calibration: 3 x torch.neg over 1 GiB (reads 1048576 KiB, writes 1048576 KiB)")
+        log(f"calibration: 3 x bitwise_not over 1 GiB (reads and writes {CALIBRATION_KIB} KiB)")
 
 
 if __name__ == "__main__":

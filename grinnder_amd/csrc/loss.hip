@@ -7,8 +7,8 @@
 //   m = max_c x_c,  lse = m + log(sum_c exp(x_c - m)),  nll = lse - x_y,
 //   pred = the first c with x_c == m,
 // the arithmetic of torch's log_softmax + NLL and argmax.  Sums and counts
-// are reduced in a fixed order (per-workgroup partials in double, then one
-// ordered pass), so results do not depend on scheduling.  Labels of train /
+// are reduced in a fixed order (per-workgroup partials in double, then a
+// fixed tree), so results do not depend on scheduling.  Labels of train /
 // val / test rows outside [0, C) are counted and reported, not read.
 // Gradient rows: g[r, c] = exp(x_c - lse) - [c == y] on train rows, 0 on the
 // others, i.e. d(sum of train nll)/dx, the backward of log_softmax + NLL.
@@ -19,7 +19,6 @@
 namespace gr_loss {
 
 constexpr int kStats = 7;  // nll_sum, train_n, val_ok, val_n, test_ok, test_n, bad_labels
-constexpr int kMaxBlocks = 1024;
 
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
@@ -42,79 +41,175 @@ __device__ __forceinline__ int group_min_int(int v) {
   return v;
 }
 
-// G lanes per row (64 / G rows per wavefront); each lane owns columns
-// lane_in_row + k * G.  Grid-stride over row groups; per-thread partial
-// statistics, then an ordered reduction inside the workgroup.
-template <int G>
-__global__ __launch_bounds__(256) void xent_forward(const float* __restrict__ x, int64_t ld,
-                                                   int64_t rows, int C,
-                                                   const int64_t* __restrict__ labels,
-                                                   const uint8_t* __restrict__ mask,
-                                                   float* __restrict__ lse_out,
-                                                   float* __restrict__ grad, int64_t ldg,
-                                                   double* __restrict__ part) {
-  constexpr int RPW = 64 / G;  // rows per wavefront
-  const int lane = threadIdx.x & 63;
-  const int sub = lane / G;
-  const int li = lane % G;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * 4;
+// Accumulates one row's contribution to the seven statistics.
+__device__ __forceinline__ void add_row_stats(double (&acc)[kStats], uint8_t mk, bool ok_label,
+                                              float lse, float xy, bool hit) {
+  if (mk != 0 && !ok_label) {
+    acc[6] += 1.0;
+    return;
+  }
+  if (mk & 1) {
+    acc[0] += (double)(lse - xy);
+    acc[1] += 1.0;
+  }
+  if (mk & 2) {
+    acc[2] += hit ? 1.0 : 0.0;
+    acc[3] += 1.0;
+  }
+  if (mk & 4) {
+    acc[4] += hit ? 1.0 : 0.0;
+    acc[5] += 1.0;
+  }
+}
+
+// Ordered sum of the workgroup's 256 per-thread statistics into part[blockIdx]:
+// a butterfly inside each wavefront, then the 4 wavefront sums in order.
+__device__ __forceinline__ void block_stats(double (&acc)[kStats], double* __restrict__ part) {
+  __shared__ double red[4][kStats];
+#pragma unroll
+  for (int k = 0; k < kStats; ++k) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc[k] += __shfl_xor(acc[k], off, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k < kStats; ++k) red[wave][k] = acc[k];
+  }
+  __syncthreads();
+  if (threadIdx.x < kStats) {
+    const int k = threadIdx.x;
+    part[(int64_t)blockIdx.x * kStats + k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
+  }
+}
+
+// C <= 63: one thread per row.  The workgroup's 256 rows are loaded with
+// coalesced accesses into LDS (row stride CP = C rounded up to odd, so the
+// per-thread row walks hit distinct banks), each thread reduces its row from
+// LDS, writes its gradient row back into LDS, and the workgroup stores the
+// gradient rows with coalesced accesses.
+constexpr int kRowsPerBlock = 256;
+constexpr int kSmallC = 63;  // 256 rows x 63 floats = 63 KiB of LDS, within 64 KiB
+
+__global__ __launch_bounds__(256) void xent_rows_small(const float* __restrict__ x, int64_t ld,
+                                                       int64_t rows, int C,
+                                                       const int64_t* __restrict__ labels,
+                                                       const uint8_t* __restrict__ mask,
+                                                       float* __restrict__ lse_out,
+                                                       float* __restrict__ grad, int64_t ldg,
+                                                       double* __restrict__ part) {
+  extern __shared__ float tile[];  // kRowsPerBlock * (C | 1) floats
+  const int CP = C | 1;
+  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock;
+  const int nr = (int)min<int64_t>(kRowsPerBlock, rows - row0);
+  const int n = nr * C;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int r = i / C;
+    const int c = i - r * C;
+    tile[r * CP + c] = x[(row0 + r) * ld + c];
+  }
+  __syncthreads();
   double acc[kStats];
 #pragma unroll
   for (int k = 0; k < kStats; ++k) acc[k] = 0.0;
-  for (int64_t r0 = wave * RPW; r0 < rows; r0 += nwaves * RPW) {
-    const int64_t r = r0 + sub;
-    const bool live = r < rows;
-    const float* row = x + (live ? r : 0) * ld;
+  const int t = threadIdx.x;
+  if (t < nr) {
+    float* row = tile + t * CP;
+    float m = row[0];
+    int first = 0;
+    for (int c = 1; c < C; ++c) {
+      const float v = row[c];
+      if (v > m) {
+        m = v;
+        first = c;
+      }
+    }
+    float s = 0.f;
+    for (int c = 0; c < C; ++c) s += expf(row[c] - m);
+    const float lse = m + logf(s);
+    const int64_t r = row0 + t;
+    const uint8_t mk = mask[r];
+    const int64_t y = labels[r];
+    const bool ok_label = y >= 0 && y < C;
+    const float xy = ok_label ? row[y] : 0.f;
+    if (lse_out != nullptr) lse_out[r] = lse;
+    add_row_stats(acc, mk, ok_label, lse, xy, first == (int)y);
+    if (grad != nullptr) {
+      const bool train = (mk & 1) && ok_label;
+      for (int c = 0; c < C; ++c)
+        row[c] = train ? expf(row[c] - lse) - (c == (int)y ? 1.f : 0.f) : 0.f;
+    }
+  }
+  if (grad != nullptr) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const int r = i / C;
+      const int c = i - r * C;
+      grad[(row0 + r) * ldg + c] = tile[r * CP + c];
+    }
+  }
+  block_stats(acc, part);
+}
+
+// C > 63: one wavefront per row (lanes over columns), 64 rows per wavefront
+// of a 256-row workgroup.
+__global__ __launch_bounds__(256) void xent_rows_wide(const float* __restrict__ x, int64_t ld,
+                                                      int64_t rows, int C,
+                                                      const int64_t* __restrict__ labels,
+                                                      const uint8_t* __restrict__ mask,
+                                                      float* __restrict__ lse_out,
+                                                      float* __restrict__ grad, int64_t ldg,
+                                                      double* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6) * 64;
+  double acc[kStats];
+#pragma unroll
+  for (int k = 0; k < kStats; ++k) acc[k] = 0.0;
+  for (int64_t r = row0; r < row0 + 64 && r < rows; ++r) {
+    const float* row = x + r * ld;
     float m = -INFINITY;
-    for (int c = li; c < C; c += G) m = fmaxf(m, live ? row[c] : -INFINITY);
-    m = group_max<G>(m);
+    for (int c = lane; c < C; c += 64) m = fmaxf(m, row[c]);
+    m = group_max<64>(m);
     float s = 0.f;
     int first = C;
-    for (int c = li; c < C; c += G) {
-      const float v = live ? row[c] : 0.f;
+    for (int c = lane; c < C; c += 64) {
+      const float v = row[c];
       s += expf(v - m);
       if (v == m && c < first) first = c;
     }
-    s = group_sum<G>(s);
-    first = group_min_int<G>(first);
+    s = group_sum<64>(s);
+    first = group_min_int<64>(first);
     const float lse = m + logf(s);
-    const uint8_t mk = live ? mask[r] : 0;
-    const int64_t y = live ? labels[r] : 0;
+    const uint8_t mk = mask[r];
+    const int64_t y = labels[r];
     const bool ok_label = y >= 0 && y < C;
-    // x_y: the one lane owning column y contributes it.
-    float xy = 0.f;
-    if (ok_label && (int)(y % G) == li) xy = row[y];
-    xy = group_sum<G>(xy);
-    if (grad != nullptr && live) {
+    if (grad != nullptr) {
       const bool train = (mk & 1) && ok_label;
       float* g = grad + r * ldg;
-      for (int c = li; c < C; c += G)
+      for (int c = lane; c < C; c += 64)
         g[c] = train ? expf(row[c] - lse) - (c == (int)y ? 1.f : 0.f) : 0.f;
     }
-    if (li == 0 && live) {
+    if (lane == 0) {
       if (lse_out != nullptr) lse_out[r] = lse;
-      if (mk != 0 && !ok_label) {
-        acc[6] += 1.0;
-      } else {
-        if (mk & 1) {
-          acc[0] += (double)(lse - xy);
-          acc[1] += 1.0;
-        }
-        const double hit = (first == (int)y) ? 1.0 : 0.0;
-        if (mk & 2) {
-          acc[2] += hit;
-          acc[3] += 1.0;
-        }
-        if (mk & 4) {
-          acc[4] += hit;
-          acc[5] += 1.0;
-        }
-      }
+      add_row_stats(acc, mk, ok_label, lse, ok_label ? row[y] : 0.f, first == (int)y);
     }
   }
-  // Ordered reduction of the 256 threads' partials (only li == 0 lanes hold
-  // non-zero values; the tree order is fixed).
+  block_stats(acc, part);
+}
+
+// Sums the per-workgroup partials: thread t adds workgroups t, t+256, ... in
+// order, then a fixed tree over the 256 threads; writes the loss (sum, or
+// mean over train rows when `mean`) and the integer statistics.
+__global__ __launch_bounds__(256) void xent_finish(const double* __restrict__ part, int64_t nblk,
+                                                   int mean, float* __restrict__ loss,
+                                                   int64_t* __restrict__ stats) {
+  double acc[kStats];
+#pragma unroll
+  for (int k = 0; k < kStats; ++k) acc[k] = 0.0;
+  for (int64_t b = threadIdx.x; b < nblk; b += 256) {
+#pragma unroll
+    for (int k = 0; k < kStats; ++k) acc[k] += part[b * kStats + k];
+  }
   __shared__ double red[kStats][256];
 #pragma unroll
   for (int k = 0; k < kStats; ++k) red[k][threadIdx.x] = acc[k];
@@ -126,37 +221,12 @@ __global__ __launch_bounds__(256) void xent_forward(const float* __restrict__ x,
     }
     __syncthreads();
   }
-  if (threadIdx.x < kStats) part[(int64_t)blockIdx.x * kStats + threadIdx.x] = red[threadIdx.x][0];
-}
-
-// Sums the per-workgroup partials in workgroup order; writes the loss (sum,
-// or mean over train rows when `mean`) and the integer statistics.
-__global__ __launch_bounds__(64) void xent_finish(const double* __restrict__ part, int nblk,
-                                                  int mean, float* __restrict__ loss,
-                                                  int64_t* __restrict__ stats) {
-  double t = 0.0;
-  if (threadIdx.x < kStats)
-    for (int b = 0; b < nblk; ++b) t += part[(int64_t)b * kStats + threadIdx.x];
-  // Lane k holds statistic k; the mean needs the train count (lane 1).
-  const double n_train = __shfl(t, 1, 64);
   if (threadIdx.x == 0) {
-    *loss = (float)((mean && n_train > 0.0) ? t / n_train : t);
+    const double n_train = red[1][0];
+    *loss = (float)((mean && n_train > 0.0) ? red[0][0] / n_train : red[0][0]);
   } else if (threadIdx.x < kStats) {
-    stats[threadIdx.x - 1] = (int64_t)t;
+    stats[threadIdx.x - 1] = (int64_t)red[threadIdx.x][0];
   }
-}
-
-inline int lanes_for(int64_t C) {
-  if (C <= 8) return 8;
-  if (C <= 16) return 16;
-  if (C <= 32) return 32;
-  return 64;
-}
-
-inline int64_t blocks_for(int64_t rows, int G) {
-  const int64_t rows_per_block = 4 * (64 / G);
-  return std::max<int64_t>(1, std::min<int64_t>(kMaxBlocks, (rows + rows_per_block - 1) /
-                                                                 rows_per_block));
 }
 
 }  // namespace gr_loss
@@ -174,19 +244,22 @@ extern "C" int gr_xent_forward(const float* logits, int64_t ld, int64_t rows, in
   GR_REQUIRE(loss && stats && workspace, "xent_forward: NULL output");
   GR_REQUIRE(rows == 0 || (logits && labels && mask), "xent_forward: NULL input");
   GR_REQUIRE(grad == nullptr || ldg >= classes, "xent_forward: ldg < classes");
-  const int G = lanes_for(classes);
-  const int64_t nblk = blocks_for(rows, G);
+  const int64_t nblk = std::max<int64_t>(1, (rows + kRowsPerBlock - 1) / kRowsPerBlock);
+  GR_REQUIRE(nblk <= INT32_MAX, "xent_forward: too many rows");
   GR_REQUIRE(workspace_doubles >= nblk * kStats, "xent_forward: workspace of %lld doubles, "
              "%lld needed", (long long)workspace_doubles, (long long)(nblk * kStats));
   hipStream_t s = gr::as_stream(stream);
   const int c = (int)classes;
-#define GR_XF(GG)                                                                            \
-  hipLaunchKernelGGL((xent_forward<GG>), dim3((unsigned)nblk), dim3(256), 0, s, logits, ld, \
-                     rows, c, labels, mask, lse, grad, ldg, workspace)
-  if (G == 8) GR_XF(8); else if (G == 16) GR_XF(16); else if (G == 32) GR_XF(32); else GR_XF(64);
-#undef GR_XF
+  // With rows == 0 the single workgroup writes zero partials.
+  if (classes <= kSmallC)
+    hipLaunchKernelGGL(xent_rows_small, dim3((unsigned)nblk), dim3(256),
+                       (size_t)kRowsPerBlock * (c | 1) * sizeof(float), s, logits, ld, rows, c,
+                       labels, mask, lse, grad, ldg, workspace);
+  else
+    hipLaunchKernelGGL(xent_rows_wide, dim3((unsigned)nblk), dim3(256), 0, s, logits, ld, rows, c,
+                       labels, mask, lse, grad, ldg, workspace);
   GR_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(xent_finish, dim3(1), dim3(64), 0, s, workspace, (int)nblk, (int)mean, loss,
+  hipLaunchKernelGGL(xent_finish, dim3(1), dim3(256), 0, s, workspace, nblk, (int)mean, loss,
                      stats);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;

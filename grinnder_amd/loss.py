@@ -20,7 +20,8 @@ from torch import Tensor
 from grinnder_amd import _lib
 
 TRAIN, VAL, TEST = 1, 2, 4
-_WORKSPACE_DOUBLES = 1024 * 7
+_STATS = 7            # per-workgroup partial statistics of gr_xent_forward
+_ROWS_PER_BLOCK = 256
 
 
 def mask_codes(train: Optional[Tensor], val: Optional[Tensor] = None,
@@ -43,7 +44,8 @@ class _MaskedCrossEntropy(torch.autograd.Function):
         dev = logits.device
         loss = torch.empty((), dtype=torch.float32, device=dev)
         stats = torch.empty(6, dtype=torch.int64, device=dev)
-        ws = torch.empty(_WORKSPACE_DOUBLES, dtype=torch.float64, device=dev)
+        nblk = max(1, (rows + _ROWS_PER_BLOCK - 1) // _ROWS_PER_BLOCK)
+        ws = torch.empty(nblk * _STATS, dtype=torch.float64, device=dev)
         need_grad = ctx.needs_input_grad[0]
         grad = torch.empty((rows, classes), dtype=torch.float32, device=dev) if need_grad \
             else None

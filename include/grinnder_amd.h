@@ -274,7 +274,7 @@ int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
  * the train-row nll sum, grad[r, c] = softmax(x_r)_c - [c == y_r] on train
  * rows and 0 elsewhere (ldg-strided); the caller scales it by dL/dloss (and
  * 1 / train rows for the mean).  Sums are reduced in a fixed order in double.
- * workspace: 1024 * 7 doubles suffice for any shape. */
+ * workspace: 7 * max(1, ceil(rows / 256)) doubles. */
 int gr_xent_forward(const float* logits, int64_t ld, int64_t rows,
                     int64_t classes, const int64_t* labels, const uint8_t* mask,
                     int32_t mean, float* lse, float* grad, int64_t ldg,
