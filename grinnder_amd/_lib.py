@@ -43,7 +43,7 @@ _SIGNATURES = {
     "gr_column_sum": [_P, _i64, _i64, _i64, _P, _P, _i64, _P],
     "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,
                                  _i64, _P, _P, _P, _P, _P, _i64, _P],
-    "gr_ln_relu_backward": [_P, _P, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _P, _i64, _P],
+    "gr_ln_relu_backward": [_P, _P, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _P, _P, _i64, _P],
     "gr_bias_ln_relu": [_P, _i64, _P, _P, _P, _f32, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_gemm_tn_workspace": [_i64, _i64, _i64, _P, _P],
     "gr_xent_forward": [_P, _i64, _i64, _i64, _P, _P, _i32, _P, _P, _i64, _P, _P, _P, _i64, _P],

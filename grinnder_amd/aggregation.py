@@ -149,23 +149,81 @@ def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None) -> T
     return _GCNAggregate.apply(z, bias, plan)
 
 
+class _GCNLinearAggregatePadded(torch.autograd.Function):
+    """Y = A (X Wᵀ) + b for an output width D that is not a multiple of 4.
+
+    The product is formed with W padded by zero rows to Dp = round_up(D, 4)
+    columns, so both aggregation passes move 16-byte row vectors instead of
+    scalars; the pad columns stay exactly zero and are sliced off.  Backward:
+    dZ = Aᵀ [gY | 0], dW = dZᵀ X (first D rows), dX = dZ Wp, db = sum gY.
+    """
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor],
+                plan: DevicePlan) -> Tensor:
+        from torch.nn.functional import pad
+        d = weight.size(0)
+        dp = (d + 3) // 4 * 4
+        x = x.contiguous()
+        wp = pad(weight, (0, 0, 0, dp - d))
+        z = torch.mm(x, wp.t())
+        bp = pad(bias, (0, dp - d)).contiguous() if bias is not None else None
+        y = spmm(plan.fwd, plan.idx, plan.val, z, plan.num_dst, bp, name="gcn_fwd")
+        ctx.save_for_backward(x, wp)
+        ctx.plan = plan
+        ctx.d = d
+        ctx.has_bias = bias is not None
+        return y[:, :d]
+
+    @staticmethod
+    def backward(ctx, gy: Tensor):
+        from torch.nn.functional import pad
+
+        from grinnder_amd.dense import gemm_tn
+        x, wp = ctx.saved_tensors
+        plan: DevicePlan = ctx.plan
+        d, dp = ctx.d, wp.size(0)
+        gyp = pad(gy, (0, dp - d)).contiguous()
+        dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gyp, plan.num_src, name="gcn_bwd")
+        dx = torch.mm(dz, wp) if ctx.needs_input_grad[0] else None
+        dw = gemm_tn(dz, x)[:d] if ctx.needs_input_grad[1] else None
+        db = column_sum(gyp)[:d] if (ctx.has_bias and ctx.needs_input_grad[2]) else None
+        return dx, dw, db, None
+
+
+def gcn_linear_aggregate(x: Tensor, weight: Tensor, adj: Adjacency,
+                         bias: Optional[Tensor] = None) -> Tensor:
+    """A·(x Wᵀ) + bias of one partition (GPU), for any output width."""
+    _check_device_tensor("x", x)
+    plan = adj.device_plan(x.device)
+    if x.size(0) != plan.num_src:
+        raise ValueError(f"x has {x.size(0)} rows, adjacency has {plan.num_src} columns")
+    if weight.size(0) % 4 == 0:
+        from grinnder_amd.dense import linear
+        return _GCNAggregate.apply(linear(x, weight), bias, plan)
+    return _GCNLinearAggregatePadded.apply(x, weight, bias, plan)
+
+
 def ln_relu_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: Tensor,
-                     beta: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
-    """(dL/dh, dgamma, dbeta) of out = ReLU(LayerNorm(h)) given dL/dout (GPU)."""
+                     beta: Tensor, with_bias: bool = False):
+    """(dL/dh, dgamma, dbeta, dbias or None) of out = ReLU(LayerNorm(h)) given
+    dL/dout (GPU); dbias = the column sums of dL/dh, formed in the same pass."""
     gout = gout.contiguous()
     B, D = h.shape
     dev = h.device
     gh = torch.empty_like(h)
     dgamma = torch.empty(D, dtype=torch.float32, device=dev)
     dbeta = torch.empty(D, dtype=torch.float32, device=dev)
+    dbias = torch.empty(D, dtype=torch.float32, device=dev) if with_bias else None
     nwaves = min(8192, max(4, (B + 15) // 16))
     nwaves = (nwaves + 3) // 4 * 4
-    ws = torch.empty((2 * nwaves + 1) * D, dtype=torch.float32, device=dev)
+    ws = torch.empty(((3 if with_bias else 2) * nwaves + 1) * D, dtype=torch.float32,
+                     device=dev)
     _lib.call("gr_ln_relu_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
               rstd.data_ptr(), gamma.data_ptr(), beta.data_ptr(), B, D, gh.data_ptr(),
-              dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws.numel(),
+              dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias), ws.data_ptr(), ws.numel(),
               _lib.stream_handle())
-    return gh, dgamma, dbeta
+    return gh, dgamma, dbeta, dbias
 
 
 class _GCNAggregateLNReLU(torch.autograd.Function):
@@ -203,10 +261,9 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
     def backward(ctx, gout: Tensor):
         h, mean, rstd, g, bt = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
-        gh, dgamma, dbeta = ln_relu_backward(gout, h, mean, rstd, g, bt)
+        gh, dgamma, dbeta, db = ln_relu_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
         dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd") \
             if ctx.needs_input_grad[0] else None
-        db = column_sum(gh) if ctx.has_bias else None
         return dz, db, dgamma, dbeta, None, None
 
 

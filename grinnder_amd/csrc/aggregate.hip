@@ -405,20 +405,24 @@ __global__ __launch_bounds__(256) void aggregate_ln_relu_fixup(
 // y = xh * gamma + beta and gy = g * (y > 0):
 //   gh = rstd * (gy*gamma - mean(gy*gamma) - xh * mean(gy*gamma*xh)),
 // and per-wavefront partial sums of dgamma = sum gy*xh, dbeta = sum gy
-// (reduced afterwards in wavefront order).  Grid-stride over rows.
+// (reduced afterwards in wavefront order).  With part_bias != NULL the
+// per-wavefront column sums of gh itself are kept too: the gradient of the
+// bias added before the LayerNorm, without a second read of gh.
+// Grid-stride over rows.
 template <int VEC, int NCH>
 __global__ __launch_bounds__(256) void ln_relu_backward(
     const float* __restrict__ g, const float* __restrict__ h, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, int dim, int64_t rows, float* __restrict__ gh,
-    float* __restrict__ part_gamma, float* __restrict__ part_beta) {
+    float* __restrict__ part_gamma, float* __restrict__ part_beta,
+    float* __restrict__ part_bias) {
   const int lane = threadIdx.x & 63;
   const int64_t wid =
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t nwaves = (int64_t)gridDim.x * 4;
   bool fvalid[NCH];
   int foff[NCH], fld[NCH];
-  float gam[NCH][VEC], bet[NCH][VEC], dg[NCH][VEC], db[NCH][VEC];
+  float gam[NCH][VEC], bet[NCH][VEC], dg[NCH][VEC], db[NCH][VEC], dh[NCH][VEC];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     foff[ch] = (ch * 64 + lane) * VEC;
@@ -430,6 +434,7 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     for (int j = 0; j < VEC; ++j) {
       dg[ch][j] = 0.f;
       db[ch][j] = 0.f;
+      dh[ch][j] = 0.f;
     }
   }
   const float inv_d = 1.0f / (float)dim;
@@ -461,7 +466,10 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
       if (!fvalid[ch]) continue;
       float o[VEC];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) o[j] = rs * (gx[ch][j] - s1 - xh[ch][j] * s2);
+      for (int j = 0; j < VEC; ++j) {
+        o[j] = rs * (gx[ch][j] - s1 - xh[ch][j] * s2);
+        dh[ch][j] += o[j];
+      }
       store_vec<VEC>(gh + r * dim + foff[ch], o);
     }
   }
@@ -470,6 +478,7 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     if (!fvalid[ch]) continue;
     store_vec<VEC>(part_gamma + wid * dim + foff[ch], dg[ch]);
     store_vec<VEC>(part_beta + wid * dim + foff[ch], db[ch]);
+    if (part_bias != nullptr) store_vec<VEC>(part_bias + wid * dim + foff[ch], dh[ch]);
   }
 }
 
@@ -761,7 +770,8 @@ extern "C" int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
 extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
                                    const float* rstd, const float* gamma, const float* beta,
                                    int64_t rows, int64_t dim, float* gh, float* dgamma,
-                                   float* dbeta, float* workspace, int64_t workspace_floats,
+                                   float* dbeta, float* dbias, float* workspace,
+                                   int64_t workspace_floats,
                                    void* stream) {
   gr::clear_error();
   int vec, nch;
@@ -782,17 +792,19 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
   // (2 * nwaves * dim floats of partials + dim for the reduction pass).
   int64_t nwaves = std::min<int64_t>(8192, std::max<int64_t>(4, (rows + 15) / 16));
   nwaves = (nwaves + 3) / 4 * 4;
-  const int64_t cap = (workspace_floats / dim - 1) / 2 / 4 * 4;
+  const int nparts = dbias != nullptr ? 3 : 2;
+  const int64_t cap = (workspace_floats / dim - 1) / nparts / 4 * 4;
   GR_REQUIRE(cap >= 4, "ln_relu_backward: workspace too small");
   if (nwaves > cap) nwaves = cap;
   float* pg = workspace;
   float* pb = workspace + nwaves * dim;
+  float* ph = dbias != nullptr ? workspace + 2 * nwaves * dim : nullptr;
   hipStream_t s = gr::as_stream(stream);
   const int d = (int)dim;
   const unsigned blocks = (unsigned)(nwaves / 4);
 #define GR_LNB(V, N)                                                                        \
   hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N>), dim3(blocks), dim3(256), 0, s, g, h, \
-                     mean, rstd, gamma, beta, d, rows, gh, pg, pb)
+                     mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph)
   if (vec == 4) {
     if (nch == 1) GR_LNB(4, 1); else if (nch == 2) GR_LNB(4, 2); else GR_LNB(4, 4);
   } else {
@@ -805,6 +817,9 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
                      (int)nwaves, d, dgamma);
   hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s, pb,
                      (int)nwaves, d, dbeta);
+  if (dbias != nullptr)
+    hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s,
+                       ph, (int)nwaves, d, dbias);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }

@@ -127,10 +127,9 @@ class _BiasLNReLU(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gout: Tensor):
-        from grinnder_amd.aggregation import column_sum, ln_relu_backward
+        from grinnder_amd.aggregation import ln_relu_backward
         h, mean, rstd, g, bt = ctx.saved_tensors
-        gh, dgamma, dbeta = ln_relu_backward(gout, h, mean, rstd, g, bt)
-        db = column_sum(gh) if ctx.has_bias else None
+        gh, dgamma, dbeta, db = ln_relu_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
         return gh, db, dgamma, dbeta, None
 
 

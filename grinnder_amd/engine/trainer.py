@@ -219,7 +219,9 @@ class Trainer:
             self.streams.d2h[pid % self.config.pool_size],
             self.streams.compute,
         )
-        return self.model.forward_layer(layer_id, x, self.graph.adjacency(pid))
+        # Activations are stored, freed and re-uploaded as dense [B, D] blocks;
+        # a layer may return a strided view (a padded product), made dense here.
+        return self.model.forward_layer(layer_id, x, self.graph.adjacency(pid)).contiguous()
 
     def _checkpointed(self, layer: int, pid: int, slot: int) -> Tensor:
         x = self.device_features[layer][pid]

@@ -17,7 +17,7 @@ import torch
 from torch import Tensor
 from torch.nn import Linear, Module, Parameter
 
-from grinnder_amd.aggregation import gat_attention, gcn_aggregate
+from grinnder_amd.aggregation import gat_attention, gcn_aggregate, gcn_linear_aggregate
 from grinnder_amd.data.adjacency import Adjacency
 from grinnder_amd.dense import linear
 
@@ -65,7 +65,7 @@ class GCNConv(Module):
     def forward(self, x: Tensor, adj: Adjacency) -> Tensor:
         if self.aggregate_first():
             return linear(gcn_aggregate(x, adj), self.lin.weight, self.bias)
-        return gcn_aggregate(linear(x, self.lin.weight), adj, self.bias)
+        return gcn_linear_aggregate(x, self.lin.weight, adj, self.bias)
 
     def __repr__(self) -> str:
         return f"{self.__class__.__name__}({self.in_channels}, {self.out_channels})"

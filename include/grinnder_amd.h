@@ -227,14 +227,16 @@ int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
                              int64_t n_slots, void* stream);
 
 /* Backward of out = ReLU(LayerNorm(h)) given g = dL/dout: writes
- * gh = dL/dh [rows, dim], dgamma [dim] and dbeta [dim] (deterministic:
- * per-wavefront partials reduced in order).  workspace: at least
- * (2 * 4 + 1) * dim floats; up to (2 * 8192 + 1) * dim are used. */
+ * gh = dL/dh [rows, dim], dgamma [dim], dbeta [dim] and, when dbias != NULL,
+ * dbias = sum_rows gh (the gradient of a bias added before the LayerNorm)
+ * (deterministic: per-wavefront partials reduced in order).  workspace: at
+ * least (k * 4 + 1) * dim floats with k = 3 when dbias != NULL, else 2; up to
+ * (k * 8192 + 1) * dim are used. */
 int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
                         const float* rstd, const float* gamma, const float* beta,
                         int64_t rows, int64_t dim, float* gh, float* dgamma,
-                        float* dbeta, float* workspace, int64_t workspace_floats,
-                        void* stream);
+                        float* dbeta, float* dbias, float* workspace,
+                        int64_t workspace_floats, void* stream);
 
 /* Bias gradient of the GCN layer, db = sum_i G[i, :D] (fp32, deterministic:
  * fixed row chunks, partials reduced in chunk order).  Replaces the bias

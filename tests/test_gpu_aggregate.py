@@ -128,3 +128,29 @@ def test_fused_ln_relu_matches_float64(gpu, B, E, deg, longs, dim):
     assert max_abs_norm_err(out.detach(), ref.detach()) <= TOL
     for got, exp in zip(leaves, ref_leaves):
         assert max_abs_norm_err(got.grad, exp.grad) <= TOL
+
+
+@pytest.mark.parametrize("B,E,fin,fout", [(500, 900, 256, 47), (400, 600, 64, 19),
+                                          (300, 300, 16, 3), (350, 500, 32, 64)])
+def test_gcn_linear_aggregate_matches_oracle(gpu, B, E, fin, fout):
+    """A·(X Wᵀ) + b with the product padded to a multiple of 4 columns when
+    fout is not one: outputs and the gradients of X, W and b vs the oracle."""
+    from grinnder_amd.aggregation import gcn_linear_aggregate
+    rowptr, col, val = random_bipartite(B, E, 12, seed=B + fout, long_rows=2)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=512)
+    g = torch.Generator().manual_seed(fout)
+    x = torch.randn(E, fin, generator=g)
+    w = torch.randn(fout, fin, generator=g) * 0.1
+    bias = torch.randn(fout, generator=g)
+    gy = torch.randn(B, fout, generator=g)
+    xd, wd, bd = (t.to(gpu).requires_grad_(True) for t in (x, w, bias))
+    y = gcn_linear_aggregate(xd, wd, adj, bd)
+    assert y.shape == (B, fout)
+    y.backward(gy.to(gpu))
+    z = x.double() @ w.double().t()
+    ref_y = oracle.spmm(rowptr, col, val, z, bias.double())
+    ref_dz = torch.as_tensor(oracle.spmm_t(rowptr, col, val, gy, E), dtype=torch.float64)
+    assert max_abs_norm_err(y.detach(), ref_y) <= TOL
+    assert max_abs_norm_err(xd.grad, ref_dz @ w.double()) <= TOL
+    assert max_abs_norm_err(wd.grad, ref_dz.t() @ x.double()) <= TOL
+    assert max_abs_norm_err(bd.grad, gy.double().sum(0)) <= TOL
