@@ -40,7 +40,7 @@ _SIGNATURES = {
     "gr_spmm_plan": [_P, _i64, _i32, _P, _P, _P, _P, _P],
     "gr_gcn_aggregate": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64, _i64, _P,
                          _i64, _P],
-    "gr_column_sum": [_P, _i64, _i64, _i64, _P, _P, _i64, _P],
+    "gr_column_sum": [_P, _i64, _i64, _i64, _P, _i64, _i64, _P, _P, _i64, _P],
     "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,
                                  _i64, _P, _P, _P, _P, _P, _i64, _P],
     "gr_ln_relu_backward": [_P, _P, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _P, _P, _i64, _P],
@@ -49,10 +49,10 @@ _SIGNATURES = {
     "gr_xent_forward": [_P, _i64, _i64, _i64, _P, _P, _i32, _P, _P, _i64, _P, _P, _P, _i64, _P],
     "gr_gemm_tn": [_P, _i64, _P, _i64, _i64, _i64, _i64, _f32, _P, _P, _i64, _i64, _P],
     "gr_gat_scores": [_P, _i64, _i64, _i64, _i64, _i64, _P, _P, _P, _P, _P],
-    "gr_gat_softmax_stats": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _i64, _P],
-    "gr_gat_aggregate": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P,
-                         _P, _i64, _P, _i64, _P],
-    "gr_gat_backward_src": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P, _P,
+    "gr_gat_softmax_stats": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _i64, _P],
+    "gr_gat_aggregate": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _i64, _i64, _i64, _P, _P, _P,
+                         _i64, _P, _i64, _P],
+    "gr_gat_backward_src": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],

@@ -81,15 +81,24 @@ def _check_device_tensor(name: str, t: Tensor) -> None:
         raise RuntimeError(f"{name} must be float32; got {t.dtype}")
 
 
-def column_sum(g: Tensor) -> Tensor:
-    """Sum over the rows of a [rows, D] fp32 device matrix (deterministic HIP kernel)."""
-    g = g.contiguous()
+def column_sum(g: Tensor, weights: Optional[Tensor] = None, group: int = 1) -> Tensor:
+    """Sum over the rows of a [rows, D] fp32 device matrix (deterministic HIP
+    kernel); with `weights` [rows, ceil(D / group)], row i of column f is
+    scaled by weights[i, f // group] first."""
+    if g.stride(-1) != 1:
+        g = g.contiguous()
     rows, dim = g.shape
     out = torch.empty(dim, dtype=torch.float32, device=g.device)
-    nblk = max(1, min(1024, (rows + 2047) // 2048))
+    nblk = max(1, min(4096, (rows + 255) // 256))
     ws = torch.empty(nblk * dim, dtype=torch.float32, device=g.device)
-    _lib.call("gr_column_sum", g.data_ptr(), rows, dim, g.stride(0), out.data_ptr(),
-              ws.data_ptr(), ws.numel(), _lib.stream_handle())
+    w = None
+    if weights is not None:
+        w = weights.contiguous()
+        if w.dim() != 2 or w.size(0) != rows or w.size(1) * group < dim:
+            raise ValueError("column_sum: weights must be [rows, ceil(D / group)]")
+    _lib.call("gr_column_sum", g.data_ptr(), rows, dim, max(g.stride(0), dim), _lib.ptr(w),
+              w.size(1) if w is not None else 0, group, out.data_ptr(), ws.data_ptr(),
+              ws.numel(), _lib.stream_handle())
     return out
 
 
@@ -301,12 +310,13 @@ class _GATAttention(torch.autograd.Function):
                   a_dst.data_ptr(), s.data_ptr(), d.data_ptr(), stream)
         m = torch.empty((B, H), dtype=torch.float32, device=dev)
         den = torch.empty((B, H), dtype=torch.float32, device=dev)
+        alpha = torch.empty((max(nnz, 1), H), dtype=torch.float32, device=dev)
         f = plan.fwd
         ws = _workspace(f.n_slots, 2 * H, dev)
         _lib.call("gr_gat_softmax_stats", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
-                  s.data_ptr(), d.data_ptr(), H, m.data_ptr(), den.data_ptr(), _lib.ptr(ws),
-                  f.n_slots, stream)
+                  s.data_ptr(), d.data_ptr(), H, m.data_ptr(), den.data_ptr(), alpha.data_ptr(),
+                  _lib.ptr(ws), f.n_slots, stream)
         o = torch.empty((B, HC), dtype=torch.float32, device=dev)
         fused_bias = concat or H == 1
         y = torch.empty((B, HC), dtype=torch.float32, device=dev) if fused_bias else None
@@ -314,15 +324,14 @@ class _GATAttention(torch.autograd.Function):
         ws = _workspace(f.n_slots, HC, dev)
         _lib.call("gr_gat_aggregate", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
-                  hs.data_ptr(), hs.stride(0), s.data_ptr(), d.data_ptr(), m.data_ptr(),
-                  den.data_ptr(), H, C, _lib.ptr(b), o.data_ptr(), _lib.ptr(y),
-                  HC, _lib.ptr(ws), f.n_slots, stream)
+                  hs.data_ptr(), hs.stride(0), alpha.data_ptr(), B, H, C, _lib.ptr(b),
+                  o.data_ptr(), _lib.ptr(y), HC, _lib.ptr(ws), f.n_slots, stream)
         region.__exit__(None, None, None)
         if not fused_bias:
             y = o.view(B, H, C).mean(dim=1)
             if bias is not None:
                 y = y + bias
-        ctx.save_for_backward(hs, a_src, a_dst, s, d, m, den, o)
+        ctx.save_for_backward(hs, a_src, a_dst, s, d, alpha, den, o)
         ctx.plan = plan
         ctx.shape = (H, C, concat)
         ctx.has_bias = bias is not None
@@ -331,7 +340,7 @@ class _GATAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gy: Tensor):
-        hs, a_src, a_dst, s, d, m, den, o = ctx.saved_tensors
+        hs, a_src, a_dst, s, d, alpha, den, o = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
         H, C, concat = ctx.shape
         HC = H * C
@@ -359,7 +368,7 @@ class _GATAttention(torch.autograd.Function):
         _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
                   bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
                   plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(), hs.stride(0),
-                  go.data_ptr(), s.data_ptr(), d.data_ptr(), m.data_ptr(), den.data_ptr(),
+                  go.data_ptr(), s.data_ptr(), d.data_ptr(), alpha.data_ptr(),
                   cdot.data_ptr(), a_src.data_ptr(), H, C, dhs.data_ptr(), ds.data_ptr(),
                   gt.data_ptr(), _lib.ptr(ws), bw.n_slots, stream)
         dd = torch.empty((B, H), dtype=torch.float32, device=dev)
@@ -371,9 +380,8 @@ class _GATAttention(torch.autograd.Function):
                   dhs.data_ptr(), _lib.ptr(ws), f.n_slots, stream)
         region.__exit__(None, None, None)
         # Attention-vector gradients: per head, ds[:,h]^T Hs[:, h] and dd[:,h]^T Hs[:B, h].
-        hs3 = hs.view(E, H, C)
-        datt_src = torch.stack([ds[:, h] @ hs3[:, h, :] for h in range(H)])
-        datt_dst = torch.stack([dd[:, h] @ hs3[:B, h, :] for h in range(H)])
+        datt_src = column_sum(hs, ds, C)
+        datt_dst = column_sum(hs[:B], dd, C)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
                 None, None, None, None)
 

@@ -528,21 +528,32 @@ __global__ __launch_bounds__(256) void bias_ln_relu_rows(
 // Column sums of a [rows, dim] matrix, two passes, fixed order: workgroup b
 // sums rows [b*chunk, (b+1)*chunk) into part[b, :]; then part is reduced over
 // b in ascending order.  Each thread owns columns f = tid, tid + 256, ...
+// Weighted form: x[r, f] is scaled by w[r * ldw + f / group] (per-row weights
+// shared by groups of `group` columns, e.g. one weight per attention head).
+template <bool WEIGHTED>
 __global__ __launch_bounds__(256) void colsum_partial(const float* __restrict__ x, int64_t rows,
-                                                      int dim, int64_t ldx, int64_t chunk,
+                                                      int dim, int64_t ldx,
+                                                      const float* __restrict__ w, int64_t ldw,
+                                                      int group, int64_t chunk,
                                                       float* __restrict__ part) {
   const int64_t r0 = (int64_t)blockIdx.x * chunk;
   const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
   for (int f = threadIdx.x; f < dim; f += 256) {
+    const int wf = WEIGHTED ? f / group : 0;
+    auto val = [&](int64_t r) {
+      const float v = x[r * ldx + f];
+      if constexpr (WEIGHTED) return v * w[r * ldw + wf];
+      else return v;
+    };
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     int64_t r = r0;
     for (; r + 4 <= r1; r += 4) {
-      a0 += x[(r + 0) * ldx + f];
-      a1 += x[(r + 1) * ldx + f];
-      a2 += x[(r + 2) * ldx + f];
-      a3 += x[(r + 3) * ldx + f];
+      a0 += val(r + 0);
+      a1 += val(r + 1);
+      a2 += val(r + 2);
+      a3 += val(r + 3);
     }
-    for (; r < r1; ++r) a0 += x[r * ldx + f];
+    for (; r < r1; ++r) a0 += val(r);
     part[(int64_t)blockIdx.x * dim + f] = (a0 + a1) + (a2 + a3);
   }
 }
@@ -667,21 +678,30 @@ extern "C" int gr_gcn_aggregate(const int32_t* units, int64_t n_units, const int
   return GR_OK;
 }
 
-extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx, float* out,
+extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
+                             const float* w, int64_t ldw, int64_t group, float* out,
                              float* workspace, int64_t workspace_floats, void* stream) {
   gr::clear_error();
   GR_REQUIRE(rows >= 0 && dim >= 1 && ldx >= dim, "column_sum: bad shape");
   GR_REQUIRE(out != nullptr && (rows == 0 || x != nullptr), "column_sum: NULL pointer");
+  GR_REQUIRE(w == nullptr || (group >= 1 && ldw >= (dim + group - 1) / group),
+             "column_sum: weights need group >= 1 and ldw >= ceil(dim / group)");
   hipStream_t s = gr::as_stream(stream);
   const int64_t nblk_max = workspace_floats / dim;
   GR_REQUIRE(workspace != nullptr && nblk_max >= 1,
              "column_sum: workspace must hold at least dim floats");
-  int64_t nblk = rows == 0 ? 1 : (rows + 2047) / 2048;  // ~2048 rows per workgroup
-  if (nblk > 1024) nblk = 1024;
+  // ~256 rows per workgroup (enough loads in flight for small row counts),
+  // at most 4096 partial rows.
+  int64_t nblk = rows == 0 ? 1 : (rows + 255) / 256;
+  if (nblk > 4096) nblk = 4096;
   if (nblk > nblk_max) nblk = nblk_max;
   const int64_t chunk = rows == 0 ? 0 : (rows + nblk - 1) / nblk;
-  hipLaunchKernelGGL(gr_agg::colsum_partial, dim3((unsigned)nblk), dim3(256), 0, s, x, rows, (int)dim,
-                     ldx, chunk, workspace);
+  if (w != nullptr)
+    hipLaunchKernelGGL(gr_agg::colsum_partial<true>, dim3((unsigned)nblk), dim3(256), 0, s, x,
+                       rows, (int)dim, ldx, w, ldw, (int)group, chunk, workspace);
+  else
+    hipLaunchKernelGGL(gr_agg::colsum_partial<false>, dim3((unsigned)nblk), dim3(256), 0, s, x,
+                       rows, (int)dim, ldx, nullptr, 0, 1, chunk, workspace);
   GR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((dim + 15) / 16)), dim3(256), 0, s,
                      workspace, (int)nblk, (int)dim, out);

@@ -15,6 +15,14 @@
 // Work decomposition mirrors the GCN aggregation: one wavefront per plan
 // unit (row, edge range, slot); rows longer than the plan's segment length
 // are reduced by an ordered fixup pass, so results are deterministic.
+//
+// alpha is formed once per edge: the statistics pass stores
+// exp(v - m_k) with the unit's own max m_k, and after the split rows are
+// combined each unit rescales its edges in place,
+//   alpha = exp(v - m_k) * exp(m_k - m) / den     (exp(0) = 1 for whole rows),
+// so the aggregation (for one head: the GCN SpMM kernel with alpha as the
+// edge values) and the backward read alpha instead of re-deriving it.
+#include <algorithm>
 #include <cfloat>
 
 #include "gr_internal.h"
@@ -62,7 +70,9 @@ __device__ __forceinline__ void st(float* __restrict__ p, const float (&r)[VEC])
 
 // ------------------------------------------------------------- scores --
 
-// One wavefront per source row j: s[j,:] and, for j < B, d[j,:].
+// s[j,:] and, for j < B, d[j,:]: a wavefront covers a row's H*C features
+// in NCH chunks of VEC per lane and keeps U rows in flight; grid-stride.
+template <int VEC, int NCH, int U>
 __global__ __launch_bounds__(256) void gat_scores_kernel(const float* __restrict__ hs, int64_t ldh,
                                                          int64_t n_src, int64_t n_dst, int H,
                                                          int C, const float* __restrict__ att_src,
@@ -70,22 +80,54 @@ __global__ __launch_bounds__(256) void gat_scores_kernel(const float* __restrict
                                                          float* __restrict__ s,
                                                          float* __restrict__ d) {
   const int lane = threadIdx.x & 63;
-  const int64_t j = wave_id();
-  if (j >= n_src) return;
-  const float* row = hs + j * ldh;
-  const bool is_dst = j < n_dst;
-  for (int h = 0; h < H; ++h) {
-    float ps = 0.f, pd = 0.f;
-    for (int c = lane; c < C; c += 64) {
-      const float x = row[h * C + c];
-      ps = fmaf(x, att_src[h * C + c], ps);
-      if (is_dst) pd = fmaf(x, att_dst[h * C + c], pd);
+  const int64_t wid = wave_id();
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  const int HC = H * C;
+  int fld[NCH], hd[NCH];
+  float as[NCH][VEC], ad[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    const int foff = (ch * 64 + lane) * VEC;
+    const bool valid = foff < HC;
+    fld[ch] = valid ? foff : HC - VEC;
+    hd[ch] = fld[ch] / C;
+    ld<VEC>(att_src + fld[ch], as[ch]);
+    ld<VEC>(att_dst + fld[ch], ad[ch]);
+    if (!valid) {
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) as[ch][q] = ad[ch][q] = 0.f;
     }
-    ps = wave_sum(ps);
-    pd = wave_sum(pd);
-    if (lane == 0) {
-      s[j * H + h] = ps;
-      if (is_dst) d[j * H + h] = pd;
+  }
+  for (int64_t r0 = wid * U; r0 < n_src; r0 += nwaves * U) {
+    float x[U][NCH][VEC];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t r = r0 + k < n_src ? r0 + k : n_src - 1;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) ld<VEC>(hs + r * ldh + fld[ch], x[k][ch]);
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t r = r0 + k;
+      if (r >= n_src) break;
+      for (int h = 0; h < H; ++h) {
+        float ps = 0.f, pd = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+          if (hd[ch] != h) continue;
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            ps = fmaf(x[k][ch][q], as[ch][q], ps);
+            pd = fmaf(x[k][ch][q], ad[ch][q], pd);
+          }
+        }
+        ps = wave_sum(ps);
+        if (lane == 0) s[r * H + h] = ps;
+        if (r < n_dst) {
+          pd = wave_sum(pd);
+          if (lane == 0) d[r * H + h] = pd;
+        }
+      }
     }
   }
 }
@@ -93,8 +135,9 @@ __global__ __launch_bounds__(256) void gat_scores_kernel(const float* __restrict
 // ------------------------------------------------------ softmax stats --
 
 // Per unit: m = max_e v_e and sum_e exp(v_e - m) for each head (two passes
-// over the unit's edges, lanes parallel over edges).  Unsplit rows write
-// m[i,h] and den[i,h] = sum + 1e-16; split rows write (m_k, sum_k) partials.
+// over the unit's edges, lanes parallel over edges); ex[e,h] = exp(v_e - m)
+// with this unit's max.  Unsplit rows write m[i,h] and den[i,h] = sum +
+// 1e-16; split rows write (m_k, sum_k) partials.
 __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__ units,
                                                         int64_t n_units,
                                                         const int32_t* __restrict__ idx,
@@ -102,6 +145,7 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
                                                         const float* __restrict__ d, int H,
                                                         float* __restrict__ m,
                                                         float* __restrict__ den,
+                                                        float* __restrict__ ex,
                                                         float* __restrict__ ws) {
   const int lane = threadIdx.x & 63;
   const int64_t wid = wave_id();
@@ -119,7 +163,9 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
     float sum = 0.f;
     for (int e = w.y + lane; e < w.z; e += 64) {
       const float v = leaky(s[(int64_t)idx[e] * H + h] + di);
-      sum += expf(v - mx);
+      const float x = expf(v - mx);
+      ex[(int64_t)e * H + h] = x;
+      sum += x;
     }
     sum = wave_sum(sum);
     if (lane == 0) {
@@ -158,17 +204,55 @@ __global__ __launch_bounds__(256) void gat_stats_fixup(const int32_t* __restrict
   }
 }
 
+// In place over ex: alpha[e,h] = ex[e,h] * exp(m_k - m[i,h]) / den[i,h], with
+// m_k the unit's own max (the row max for whole rows, where the factor is 1).
+__global__ __launch_bounds__(256) void gat_alpha_kernel(const int4* __restrict__ units,
+                                                        int64_t n_units, int H,
+                                                        const float* __restrict__ m,
+                                                        const float* __restrict__ den,
+                                                        const float* __restrict__ ws,
+                                                        float* __restrict__ ex) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = wave_id();
+  if (wid >= n_units) return;
+  const int4 w = units[wid];
+  for (int h = 0; h < H; ++h) {
+    const int64_t ih = (int64_t)w.x * H + h;
+    const float mi = m[ih];
+    const float mk = w.w < 0 ? mi : ws[(int64_t)w.w * 2 * H + h];
+    const float corr = expf(mk - mi);
+    const float dn = den[ih];
+    for (int e = w.y + lane; e < w.z; e += 64) {
+      float* p = ex + (int64_t)e * H + h;
+      *p = (*p * corr) / dn;
+    }
+  }
+}
+
+// y[r, f] = o[r, f] + bias[f] (bias may be NULL) for r < rows, f < HC.
+__global__ __launch_bounds__(256) void gat_add_bias(const float* __restrict__ o, int64_t rows,
+                                                    int HC, const float* __restrict__ bias,
+                                                    float* __restrict__ y, int64_t ldy) {
+  const int64_t n = rows * HC;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < n; k += stride) {
+    const int64_t r = k / HC;
+    const int f = (int)(k - r * HC);
+    y[r * ldy + f] = o[k] + (bias != nullptr ? bias[f] : 0.f);
+  }
+}
+
 // ---------------------------------------------------------- aggregate --
 
-// O[i,:] = sum_e alpha_e Hs[col_e,:]; alpha recomputed from (s, d, m, den).
-// Writes O (no bias) and, if y != NULL, Y = O + bias.
+// O[i,:] = sum_e alpha[e, h(f)] Hs[col_e,:] for several heads (one head goes
+// through the GCN SpMM kernel).  Writes O (no bias) and, if y != NULL,
+// Y = O + bias.
 template <int VEC, int NCH, int U>
 __global__ __launch_bounds__(256) void gat_aggregate_kernel(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
-    const float* __restrict__ hs, int64_t ldh, const float* __restrict__ s,
-    const float* __restrict__ d, const float* __restrict__ m, const float* __restrict__ den,
-    int H, int C, const float* __restrict__ bias, float* __restrict__ o,
-    float* __restrict__ y, int64_t ldy, float* __restrict__ ws) {
+    const float* __restrict__ hs, int64_t ldh, const float* __restrict__ alpha, int H, int C,
+    const float* __restrict__ bias, float* __restrict__ o, float* __restrict__ y, int64_t ldy,
+    float* __restrict__ ws) {
   const int lane = threadIdx.x & 63;
   const int64_t wid = wave_id();
   if (wid >= n_units) return;
@@ -178,16 +262,12 @@ __global__ __launch_bounds__(256) void gat_aggregate_kernel(
 
   int foff[NCH], fld[NCH], hd[NCH];
   bool fvalid[NCH];
-  float dh[NCH], mh[NCH], rden[NCH];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     foff[ch] = (ch * 64 + lane) * VEC;
     fvalid[ch] = foff[ch] < HC;
     fld[ch] = fvalid[ch] ? foff[ch] : HC - VEC;
     hd[ch] = fld[ch] / C;
-    dh[ch] = d[i * H + hd[ch]];
-    mh[ch] = m[i * H + hd[ch]];
-    rden[ch] = den[i * H + hd[ch]];
   }
   float acc[NCH][VEC];
 #pragma unroll
@@ -206,21 +286,21 @@ __global__ __launch_bounds__(256) void gat_aggregate_kernel(
       c[k] = ok[k] ? idx[e + k] : idx[e];
     }
     float r[U][NCH][VEC];
-    float sv[U][NCH];
+    float av[U][NCH];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const float* row = hs + (int64_t)c[k] * ldh;
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch) {
         ld<VEC>(row + fld[ch], r[k][ch]);
-        sv[k][ch] = s[(int64_t)c[k] * H + hd[ch]];
+        av[k][ch] = alpha[(int64_t)(ok[k] ? e + k : e) * H + hd[ch]];
       }
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch) {
-        const float a = ok[k] ? expf(leaky(sv[k][ch] + dh[ch]) - mh[ch]) / rden[ch] : 0.f;
+        const float a = ok[k] ? av[k][ch] : 0.f;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) acc[ch][j] = fmaf(a, r[k][ch][j], acc[ch][j]);
       }
@@ -272,8 +352,8 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 
 // ----------------------------------------------------------- backward --
 
-// Column-parallel (CSC) pass over source rows j.  For each edge (i, j):
-//   alpha = exp(LeakyReLU(s_j + d_i) - m_i) / den_i
+// Column-parallel (CSC) pass over source rows j.  For each edge (i, j), with
+// alpha read through the CSC -> CSR permutation:
 //   g_alpha = <GO_i, Hs_j>  (per head);  g_e = alpha (g_alpha - c_i)
 //   g_t = g_e * (t > 0 ? 1 : 0.2)
 //   dHs_j += alpha GO_i;  ds_j += g_t;  gdd[csr position of e] = g_e * (t > 0 ? 0 : -0.8)
@@ -285,15 +365,30 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 // exactly; summing g_t directly would cancel to fp32 noise.  The destination
 // pass therefore forms dd_i = sum_j g_e,ij (slope_ij - 1) + c_i * 1e-16 / den_i,
 // the same value without the cancellation.
-template <int VEC, int NCH, int U>
+//
+// G lanes per edge: with one head and rows of at most G vectors, a wavefront
+// takes 64 / G edges of the unit at once (slot `sub` takes edges sub,
+// sub + 64/G, ...); the slots' partial dHs_j and ds_j are combined in a fixed
+// butterfly order at the end.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int VEC, int NCH, int U, int G>
 __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
     const int32_t* __restrict__ perm, const float* __restrict__ hs, int64_t ldh,
     const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
-    const float* __restrict__ m, const float* __restrict__ den, const float* __restrict__ cdot,
+    const float* __restrict__ alpha, const float* __restrict__ cdot,
     const float* __restrict__ att_src, int H, int C, float* __restrict__ dhs,
     float* __restrict__ ds, float* __restrict__ gt, float* __restrict__ ws) {
+  constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
+  const int sub = lane / G;
+  const int li = lane % G;
   const int64_t wid = wave_id();
   if (wid >= n_units) return;
   const int4 w = units[wid];
@@ -305,7 +400,7 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
   float hsj[NCH][VEC], sj[NCH];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
-    foff[ch] = (ch * 64 + lane) * VEC;
+    foff[ch] = (ch * G + li) * VEC;
     fvalid[ch] = foff[ch] < HC;
     fld[ch] = fvalid[ch] ? foff[ch] : HC - VEC;
     hd[ch] = fld[ch] / C;
@@ -326,13 +421,16 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
     for (int q = 0; q < VEC; ++q) acc[ch][q] = 0.f;
   }
 
-  for (int e = w.y; e < w.z; e += U) {
-    int ii[U];
+  for (int e = w.y; e < w.z; e += U * EPI) {
+    int ii[U], pe[U];
     bool ok[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      ok[k] = e + k < w.z;
-      ii[k] = ok[k] ? row_idx[e + k] : row_idx[e];
+      const int ek = e + k * EPI + sub;
+      ok[k] = ek < w.z;
+      const int el = ok[k] ? ek : w.y;
+      ii[k] = row_idx[el];
+      pe[k] = perm[el];
     }
     float g[U][NCH][VEC];
 #pragma unroll
@@ -341,7 +439,7 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
       for (int ch = 0; ch < NCH; ++ch) ld<VEC>(go + (int64_t)ii[k] * HC + fld[ch], g[k][ch]);
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      // Per-lane partial dot products, then one wave reduction per head.
+      // Per-lane partial dot products, then one reduction per head.
       float pd[NCH];
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch) {
@@ -355,10 +453,11 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
         float t = 0.f;
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) t += pd[ch];
-        t = wave_sum(t);
+        t = group_sum<G>(t);
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) ga[ch] = t;
       } else {
+        // Several heads: G == 64 (one edge per wavefront).
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) ga[ch] = 0.f;
         for (int h = 0; h < H; ++h) {
@@ -376,18 +475,29 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
       for (int ch = 0; ch < NCH; ++ch) {
         const int64_t ih = i * H + hd[ch];
         const float tt = sj[ch] + d[ih];
-        const float a = expf(leaky(tt) - m[ih]) / den[ih];
+        const float a = alpha[(int64_t)pe[k] * H + hd[ch]];
         const float ge = a * (ga[ch] - cdot[ih]);
         const bool pos = tt > 0.f;
         if (ok[k]) {
           dsl[ch] += pos ? ge : 0.2f * ge;
 #pragma unroll
           for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a, g[k][ch][q], acc[ch][q]);
-          if (head_lead[ch]) gt[(int64_t)perm[e + k] * H + hd[ch]] = pos ? 0.f : -0.8f * ge;
+          if (head_lead[ch]) gt[(int64_t)pe[k] * H + hd[ch]] = pos ? 0.f : -0.8f * ge;
         }
       }
     }
   }
+  // Combine the edge slots (no-op for G == 64).
+#pragma unroll
+  for (int off = G; off < 64; off <<= 1) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      dsl[ch] += __shfl_xor(dsl[ch], off, 64);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[ch][q] += __shfl_xor(acc[ch][q], off, 64);
+    }
+  }
+  if (sub != 0) return;
 
   if (w.w < 0) {
 #pragma unroll
@@ -556,9 +666,27 @@ extern "C" int gr_gat_scores(const float* hs, int64_t ldh, int64_t n_src, int64_
   GR_REQUIRE(ldh >= heads * channels, "gat_scores: ldh < H*C");
   if (n_src == 0) return GR_OK;
   GR_REQUIRE(hs && att_src && att_dst && s && (d || n_dst == 0), "gat_scores: NULL pointer");
-  hipLaunchKernelGGL(gat_scores_kernel, dim3(blocks_for(n_src)), dim3(256), 0,
-                     gr::as_stream(stream), hs, ldh, n_src, n_dst, (int)heads, (int)channels,
-                     att_src, att_dst, s, d);
+  const int64_t HC = heads * channels;
+  const bool al = aligned16(hs) && ldh % 4 == 0 && aligned16(att_src) && aligned16(att_dst);
+  int vec, nch;
+  pick_shape(HC, channels, al, &vec, &nch);
+  hipStream_t st = gr::as_stream(stream);
+  const int H = (int)heads, C = (int)channels;
+  // U rows in flight per wavefront; enough wavefronts to fill the chip.
+  auto grid = [&](int u) {
+    const int64_t waves = (n_src + u - 1) / u;
+    return dim3((unsigned)std::min<int64_t>(4096, (waves + 3) / 4));
+  };
+#define GR_SC(V, N, U)                                                                   \
+  hipLaunchKernelGGL((gat_scores_kernel<V, N, U>), grid(U), dim3(256), 0, st, hs, ldh, n_src, \
+                     n_dst, H, C, att_src, att_dst, s, d)
+  if (vec == 4) {
+    if (nch == 1) GR_SC(4, 1, 4); else if (nch == 2) GR_SC(4, 2, 2); else GR_SC(4, 4, 1);
+  } else {
+    if (nch == 1) GR_SC(1, 1, 4); else if (nch == 2) GR_SC(1, 2, 2); else if (nch == 4) GR_SC(1, 4, 1);
+    else if (nch == 8) GR_SC(1, 8, 1); else GR_SC(1, 16, 1);
+  }
+#undef GR_SC
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
@@ -566,73 +694,90 @@ extern "C" int gr_gat_scores(const float* hs, int64_t ldh, int64_t n_src, int64_
 extern "C" int gr_gat_softmax_stats(const int32_t* units, int64_t n_units, const int32_t* fixups,
                                     int64_t n_fix, const int32_t* idx, const float* s,
                                     const float* d, int64_t heads, float* m, float* den,
-                                    float* workspace, int64_t n_slots, void* stream) {
+                                    float* alpha, float* workspace, int64_t n_slots,
+                                    void* stream) {
   gr::clear_error();
   GR_REQUIRE(heads >= 1 && heads <= kMaxHeads, "gat_softmax_stats: bad heads");
   GR_REQUIRE(n_units >= 0 && n_fix >= 0 && n_slots >= 0, "gat_softmax_stats: negative extent");
   GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_softmax_stats: NULL fixups/workspace");
   if (n_units == 0) return GR_OK;
-  GR_REQUIRE(units && aligned16(units) && s && d && m && den,
+  GR_REQUIRE(units && aligned16(units) && s && d && m && den && alpha,
              "gat_softmax_stats: NULL or misaligned pointer");
   hipStream_t st = gr::as_stream(stream);
-  hipLaunchKernelGGL(gat_stats_kernel, dim3(blocks_for(n_units)), dim3(256), 0, st,
-                     reinterpret_cast<const int4*>(units), n_units, idx, s, d, (int)heads, m, den,
-                     workspace);
+  const int4* u4 = reinterpret_cast<const int4*>(units);
+  hipLaunchKernelGGL(gat_stats_kernel, dim3(blocks_for(n_units)), dim3(256), 0, st, u4, n_units,
+                     idx, s, d, (int)heads, m, den, alpha, workspace);
   GR_HIP_CHECK(hipGetLastError());
   if (n_fix > 0) {
     hipLaunchKernelGGL(gat_stats_fixup, dim3(blocks_for(n_fix)), dim3(256), 0, st, fixups, n_fix,
                        workspace, (int)heads, m, den);
     GR_HIP_CHECK(hipGetLastError());
   }
+  hipLaunchKernelGGL(gat_alpha_kernel, dim3(blocks_for(n_units)), dim3(256), 0, st, u4, n_units,
+                     (int)heads, m, den, workspace, alpha);
+  GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
 
 template <int VEC, int NCH>
 static hipError_t launch_gat_agg(hipStream_t st, const int4* units, int64_t n_units,
-                                 const int32_t* idx, const float* hs, int64_t ldh, const float* s,
-                                 const float* d, const float* m, const float* den, int H, int C,
-                                 const float* bias, float* o, float* y, int64_t ldy, float* ws) {
+                                 const int32_t* idx, const float* hs, int64_t ldh,
+                                 const float* alpha, int H, int C, const float* bias, float* o,
+                                 float* y, int64_t ldy, float* ws) {
   constexpr int U = NCH == 1 ? 8 : (NCH == 2 ? 4 : (NCH == 4 ? 2 : 1));
   hipLaunchKernelGGL((gat_aggregate_kernel<VEC, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
-                     st, units, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, ws);
+                     st, units, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, ws);
   return hipGetLastError();
 }
 
 extern "C" int gr_gat_aggregate(const int32_t* units, int64_t n_units, const int32_t* fixups,
                                 int64_t n_fix, const int32_t* idx, const float* hs, int64_t ldh,
-                                const float* s, const float* d, const float* m, const float* den,
-                                int64_t heads, int64_t channels, const float* bias, float* o,
-                                float* y, int64_t ldy, float* workspace, int64_t n_slots,
-                                void* stream) {
+                                const float* alpha, int64_t n_dst, int64_t heads,
+                                int64_t channels, const float* bias, float* o, float* y,
+                                int64_t ldy, float* workspace, int64_t n_slots, void* stream) {
   gr::clear_error();
   int rc = check_heads(heads, channels);
   if (rc) return rc;
   const int64_t HC = heads * channels;
+  GR_REQUIRE(n_dst >= 0, "gat_aggregate: negative row count");
   GR_REQUIRE(ldh >= HC && (y == nullptr || ldy >= HC), "gat_aggregate: bad leading dims");
   GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_aggregate: NULL fixups/workspace");
   if (n_units == 0) return GR_OK;
-  GR_REQUIRE(units && aligned16(units) && idx && hs && s && d && m && den && o,
+  GR_REQUIRE(units && aligned16(units) && idx && hs && alpha && o,
              "gat_aggregate: NULL or misaligned pointer");
+  hipStream_t st = gr::as_stream(stream);
+  const int H = (int)heads, C = (int)channels;
+  if (H == 1) {
+    // One head: O = A_alpha Hs is the GCN SpMM with alpha as edge values.
+    rc = gr_gcn_aggregate(units, n_units, fixups, n_fix, idx, alpha, hs, ldh, o, HC, nullptr,
+                          n_dst, HC, workspace, n_slots, stream);
+    if (rc) return rc;
+    if (y != nullptr && n_dst > 0) {
+      const int64_t n = n_dst * HC;
+      hipLaunchKernelGGL(gat_add_bias, dim3((unsigned)std::min<int64_t>(8192, (n + 255) / 256)),
+                         dim3(256), 0, st, o, n_dst, (int)HC, bias, y, ldy);
+      GR_HIP_CHECK(hipGetLastError());
+    }
+    return GR_OK;
+  }
   const bool al = aligned16(hs) && aligned16(o) && ldh % 4 == 0 &&
                   (y == nullptr || (aligned16(y) && ldy % 4 == 0)) &&
                   (bias == nullptr || aligned16(bias)) &&
                   (workspace == nullptr || aligned16(workspace));
   int vec, nch;
   pick_shape(HC, channels, al, &vec, &nch);
-  hipStream_t st = gr::as_stream(stream);
   const int4* u4 = reinterpret_cast<const int4*>(units);
-  const int H = (int)heads, C = (int)channels;
   hipError_t err;
   if (vec == 4) {
-    if (nch == 1) err = launch_gat_agg<4, 1>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else if (nch == 2) err = launch_gat_agg<4, 2>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else err = launch_gat_agg<4, 4>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
+    if (nch == 1) err = launch_gat_agg<4, 1>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
+    else if (nch == 2) err = launch_gat_agg<4, 2>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
+    else err = launch_gat_agg<4, 4>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
   } else {
-    if (nch == 1) err = launch_gat_agg<1, 1>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else if (nch == 2) err = launch_gat_agg<1, 2>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else if (nch == 4) err = launch_gat_agg<1, 4>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else if (nch == 8) err = launch_gat_agg<1, 8>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
-    else err = launch_gat_agg<1, 16>(st, u4, n_units, idx, hs, ldh, s, d, m, den, H, C, bias, o, y, ldy, workspace);
+    if (nch == 1) err = launch_gat_agg<1, 1>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
+    else if (nch == 2) err = launch_gat_agg<1, 2>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
+    else if (nch == 4) err = launch_gat_agg<1, 4>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
+    else if (nch == 8) err = launch_gat_agg<1, 8>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
+    else err = launch_gat_agg<1, 16>(st, u4, n_units, idx, hs, ldh, alpha, H, C, bias, o, y, ldy, workspace);
   }
   GR_HIP_CHECK(err);
   if (n_fix > 0) {
@@ -643,16 +788,15 @@ extern "C" int gr_gat_aggregate(const int32_t* units, int64_t n_units, const int
   return GR_OK;
 }
 
-template <int VEC, int NCH>
+template <int VEC, int NCH, int G = 64>
 static hipError_t launch_gat_bwd(hipStream_t st, const int4* units, int64_t n_units,
                                  const int32_t* row_idx, const int32_t* perm, const float* hs,
                                  int64_t ldh, const float* go, const float* s, const float* d,
-                                 const float* m, const float* den, const float* cdot,
-                                 const float* att_src, int H, int C, float* dhs, float* ds,
-                                 float* gt, float* ws) {
-  constexpr int U = NCH == 1 ? 4 : (NCH <= 4 ? 2 : 1);
-  hipLaunchKernelGGL((gat_bwd_src_kernel<VEC, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
-                     st, units, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src,
+                                 const float* alpha, const float* cdot, const float* att_src,
+                                 int H, int C, float* dhs, float* ds, float* gt, float* ws) {
+  constexpr int U = G < 64 ? 2 : (NCH == 1 ? 4 : (NCH <= 4 ? 2 : 1));
+  hipLaunchKernelGGL((gat_bwd_src_kernel<VEC, NCH, U, G>), dim3(blocks_for(n_units)), dim3(256), 0,
+                     st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src,
                      H, C, dhs, ds, gt, ws);
   return hipGetLastError();
 }
@@ -660,7 +804,7 @@ static hipError_t launch_gat_bwd(hipStream_t st, const int4* units, int64_t n_un
 extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const int32_t* fixups,
                                    int64_t n_fix, const int32_t* row_idx, const int32_t* perm,
                                    const float* hs, int64_t ldh, const float* go, const float* s,
-                                   const float* d, const float* m, const float* den,
+                                   const float* d, const float* alpha,
                                    const float* cdot, const float* att_src, int64_t heads,
                                    int64_t channels, float* dhs, float* ds, float* gt,
                                    float* workspace, int64_t n_slots, void* stream) {
@@ -671,7 +815,7 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   GR_REQUIRE(ldh >= HC, "gat_backward_src: ldh < H*C");
   GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_backward_src: NULL fixups/workspace");
   if (n_units == 0) return GR_OK;
-  GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && go && s && d && m && den &&
+  GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && go && s && d && alpha &&
                  cdot && att_src && dhs && ds && gt,
              "gat_backward_src: NULL or misaligned pointer");
   const bool al = aligned16(hs) && aligned16(go) && aligned16(dhs) && aligned16(att_src) &&
@@ -682,16 +826,28 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   const int4* u4 = reinterpret_cast<const int4*>(units);
   const int H = (int)heads, C = (int)channels;
   hipError_t err;
-  if (vec == 4) {
-    if (nch == 1) err = launch_gat_bwd<4, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else if (nch == 2) err = launch_gat_bwd<4, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else err = launch_gat_bwd<4, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
+  const int64_t chunks = (HC + vec - 1) / vec;
+  if (H == 1 && chunks <= 32) {
+    // Narrow single-head rows: several edges per wavefront.
+    if (vec == 4) {
+      if (chunks <= 8) err = launch_gat_bwd<4, 1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+      else if (chunks <= 16) err = launch_gat_bwd<4, 1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+      else err = launch_gat_bwd<4, 1, 32>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    } else {
+      if (chunks <= 8) err = launch_gat_bwd<1, 1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+      else if (chunks <= 16) err = launch_gat_bwd<1, 1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+      else err = launch_gat_bwd<1, 1, 32>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    }
+  } else if (vec == 4) {
+    if (nch == 1) err = launch_gat_bwd<4, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else if (nch == 2) err = launch_gat_bwd<4, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else err = launch_gat_bwd<4, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
   } else {
-    if (nch == 1) err = launch_gat_bwd<1, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else if (nch == 2) err = launch_gat_bwd<1, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else if (nch == 4) err = launch_gat_bwd<1, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else if (nch == 8) err = launch_gat_bwd<1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    else err = launch_gat_bwd<1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, m, den, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    if (nch == 1) err = launch_gat_bwd<1, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else if (nch == 2) err = launch_gat_bwd<1, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else if (nch == 4) err = launch_gat_bwd<1, 4>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else if (nch == 8) err = launch_gat_bwd<1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
+    else err = launch_gat_bwd<1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
   }
   GR_HIP_CHECK(err);
   if (n_fix > 0) {

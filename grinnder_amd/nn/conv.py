@@ -14,6 +14,7 @@ import math
 from typing import Tuple, Union
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import Linear, Module, Parameter
 
@@ -125,6 +126,20 @@ class GATConv(Module):
                 raise ValueError("GATConv expects (x, x[:num_dst]) with a shared projection")
         else:
             x_src = x
+        if self.heads == 1 and self.out_channels % 4 != 0:
+            # One head of C channels, C not a multiple of 4: run the attention
+            # on C rounded up to 4 with zero-padded W, att_src, att_dst and
+            # bias.  The pad channel is zero in Hs and in both attention
+            # vectors, so the logits, alpha and the first C output channels
+            # are unchanged; the kernels then move 16-byte row vectors.
+            pad = (-self.out_channels) % 4
+            w = F.pad(self.lin.weight, (0, 0, 0, pad))
+            a_s = F.pad(self.att_src, (0, pad))
+            a_d = F.pad(self.att_dst, (0, pad))
+            b = F.pad(self.bias, (0, pad)) if self.bias is not None else None
+            hs = linear(x_src, w)
+            y = gat_attention(hs, adj, a_s, a_d, b, 1, self.out_channels + pad, self.concat)
+            return y[:, :self.out_channels]
         hs = linear(x_src, self.lin.weight)
         return gat_attention(hs, adj, self.att_src, self.att_dst, self.bias, self.heads,
                              self.out_channels, self.concat)

@@ -238,13 +238,16 @@ int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
                         float* dbeta, float* dbias, float* workspace,
                         int64_t workspace_floats, void* stream);
 
-/* Bias gradient of the GCN layer, db = sum_i G[i, :D] (fp32, deterministic:
- * fixed row chunks, partials reduced in chunk order).  Replaces the bias
- * gradient of PyG GCNConv's "+ bias" (grinnder/nn/gcn.py:53-56).
- * workspace: at least D floats (up to 1024 * D are used for parallelism). */
+/* Column sums out[f] = sum_i X[i, f] (w == NULL), or weighted sums
+ * out[f] = sum_i w[i * ldw + f / group] * X[i, f] (fp32, deterministic: fixed
+ * row chunks, partials reduced in chunk order).  Replaces the bias gradient of
+ * PyG GCNConv's / GATConv's "+ bias" (grinnder/nn/gcn.py:53-56,
+ * grinnder/nn/gat.py:54-61) and, weighted by ds / dd with group = C, GATConv's
+ * attention-vector gradients d att_src[h] = sum_j ds[j,h] Hs[j,h,:].
+ * workspace: at least D floats (up to 4096 * D are used for parallelism). */
 int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
-                  float* out, float* workspace, int64_t workspace_floats,
-                  void* stream);
+                  const float* w, int64_t ldw, int64_t group, float* out,
+                  float* workspace, int64_t workspace_floats, void* stream);
 
 /* Dense form of the fused epilogue, for a layer whose product Z was formed
  * outside the aggregation (aggregate-first GCN: Z = (A X) W^T):
@@ -320,29 +323,29 @@ int gr_gat_scores(const float* hs, int64_t ldh, int64_t n_src, int64_t n_dst,
                   int64_t heads, int64_t channels, const float* att_src,
                   const float* att_dst, float* s, float* d, void* stream);
 
-/* Row max m[i,h] of LeakyReLU(s_j + d_i) over the CSR row and
- * den[i,h] = sum exp(v - m) + 1e-16 (rows without edges: m = 0, den = 1).
+/* Edge softmax over each CSR row: m[i,h] = max_j LeakyReLU(s_j + d_i),
+ * den[i,h] = sum exp(v - m) + 1e-16 (rows without edges: m = 0, den = 1) and
+ * the attention weights alpha[e,h] = exp(v_e - m) / den [nnz, H] (CSR order).
  * Uses the CSR plan of gr_spmm_plan; workspace: n_slots * 2H floats. */
 int gr_gat_softmax_stats(const int32_t* units, int64_t n_units,
                          const int32_t* fixups, int64_t n_fix,
                          const int32_t* idx, const float* s, const float* d,
-                         int64_t heads, float* m, float* den, float* workspace,
-                         int64_t n_slots, void* stream);
+                         int64_t heads, float* m, float* den, float* alpha,
+                         float* workspace, int64_t n_slots, void* stream);
 
-/* O[i,:] = sum_e alpha_e Hs[idx[e],:] with
- * alpha_e = exp(LeakyReLU(s + d) - m) / den, written to o [B, H*C]; when y is
- * not NULL also Y = O + bias (bias may be NULL) with row stride ldy.
- * workspace: n_slots * H*C floats. */
+/* O[i,:] = sum_e alpha[e, h] Hs[idx[e],:] (alpha from gr_gat_softmax_stats),
+ * written to o [n_dst, H*C]; when y is not NULL also Y = O + bias (bias may be
+ * NULL) with row stride ldy.  workspace: n_slots * H*C floats. */
 int gr_gat_aggregate(const int32_t* units, int64_t n_units,
                      const int32_t* fixups, int64_t n_fix, const int32_t* idx,
-                     const float* hs, int64_t ldh, const float* s,
-                     const float* d, const float* m, const float* den,
-                     int64_t heads, int64_t channels, const float* bias,
-                     float* o, float* y, int64_t ldy, float* workspace,
-                     int64_t n_slots, void* stream);
+                     const float* hs, int64_t ldh, const float* alpha,
+                     int64_t n_dst, int64_t heads, int64_t channels,
+                     const float* bias, float* o, float* y, int64_t ldy,
+                     float* workspace, int64_t n_slots, void* stream);
 
 /* Backward over source rows j (CSC plan, row_idx/perm from
- * gr_csr_transpose).  go = dL/dO [B, H*C]; cdot[i,h] = <go_i,h, O_i,h>.
+ * gr_csr_transpose; alpha [nnz, H] in CSR order from gr_gat_softmax_stats).
+ * go = dL/dO [B, H*C]; cdot[i,h] = <go_i,h, O_i,h>.
  * With g_e = alpha (<go_i, Hs_j> - cdot_i) and g_t = g_e * (t > 0 ? 1 : 0.2),
  * writes dhs [E, H*C] = sum_i alpha_ij go_i + ds_j * att_src,
  * ds [E,H] = sum_i g_t,ij and gt [nnz,H] (CSR order) = g_e * (t > 0 ? 0 : -0.8),
@@ -353,8 +356,8 @@ int gr_gat_backward_src(const int32_t* units, int64_t n_units,
                         const int32_t* fixups, int64_t n_fix,
                         const int32_t* row_idx, const int32_t* perm,
                         const float* hs, int64_t ldh, const float* go,
-                        const float* s, const float* d, const float* m,
-                        const float* den, const float* cdot,
+                        const float* s, const float* d, const float* alpha,
+                        const float* cdot,
                         const float* att_src, int64_t heads, int64_t channels,
                         float* dhs, float* ds, float* gt, float* workspace,
                         int64_t n_slots, void* stream);

@@ -201,11 +201,13 @@ def _vanilla_gat(data, state, make_model):
     return float(loss), {k: p.grad for k, p in model.named_parameters()}
 
 
-@pytest.mark.parametrize("heads", [1, 2])
-def test_gat_matches_dense_vanilla(gpu, heads):
-    data = _graph_data(n=40, reach=3, feat=12, classes=4, train_all=False)
+@pytest.mark.parametrize("heads,hidden,classes", [(1, 8, 4), (2, 8, 4), (1, 6, 3)])
+def test_gat_matches_dense_vanilla(gpu, heads, hidden, classes):
+    """(1, 6, 3): single-head layers of 6 and 3 channels run padded to 8 and 4."""
+    data = _graph_data(n=40, reach=3, feat=12, classes=classes, train_all=False)
     torch.manual_seed(11)
-    make = lambda: GAT(12, 8, 4, num_layers=3, heads=heads, dropout=0.0, norm=True)  # noqa
+    make = lambda: GAT(12, hidden, classes, num_layers=3, heads=heads, dropout=0.0,  # noqa
+                       norm=True)
     state = make().state_dict()
     ref_loss, ref_grads = _vanilla_gat(data, state, make)
     for parts, mode in [(1, "grinnder"), (4, "grinnder"), (4, "hongtu")]:
