@@ -438,15 +438,41 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     }
   }
   const float inv_d = 1.0f / (float)dim;
+  // The next row's loads are issued before the current row is reduced.
+  float gn[NCH][VEC], hn[NCH][VEC], mu_n = 0.f, rs_n = 0.f;
+  if (wid < rows) {
+    mu_n = mean[wid];
+    rs_n = rstd[wid];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      load_vec<VEC>(g + wid * dim + fld[ch], gn[ch]);
+      load_vec<VEC>(h + wid * dim + fld[ch], hn[ch]);
+    }
+  }
   for (int64_t r = wid; r < rows; r += nwaves) {
-    const float mu = mean[r], rs = rstd[r];
-    float gv[NCH][VEC], xh[NCH][VEC], gx[NCH][VEC];
+    const float mu = mu_n, rs = rs_n;
+    float gv[NCH][VEC], hc[NCH][VEC], xh[NCH][VEC], gx[NCH][VEC];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        gv[ch][j] = gn[ch][j];
+        hc[ch][j] = hn[ch][j];
+      }
+    const int64_t rn = r + nwaves;
+    if (rn < rows) {
+      mu_n = mean[rn];
+      rs_n = rstd[rn];
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) {
+        load_vec<VEC>(g + rn * dim + fld[ch], gn[ch]);
+        load_vec<VEC>(h + rn * dim + fld[ch], hn[ch]);
+      }
+    }
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
-      float hv[VEC];
-      load_vec<VEC>(g + r * dim + fld[ch], gv[ch]);
-      load_vec<VEC>(h + r * dim + fld[ch], hv);
+      const float* hv = hc[ch];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const float y = ln_affine(hv[j], mu, rs, gam[ch][j], bet[ch][j]);
@@ -512,13 +538,22 @@ __global__ __launch_bounds__(256) void bias_ln_relu_rows(
       for (int j = 0; j < VEC; ++j) bv[ch][j] = 0.f;
     }
   }
+  // The next row's load is issued before the current row is reduced.
+  float zn[NCH][VEC];
+  if (wid < rows) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) load_vec<VEC>(z + wid * ldz + fld[ch], zn[ch]);
+  }
   for (int64_t r = wid; r < rows; r += nwaves) {
     float acc[NCH][VEC];
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      load_vec<VEC>(z + r * ldz + fld[ch], acc[ch]);
+    for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) acc[ch][j] += bv[ch][j];
+      for (int j = 0; j < VEC; ++j) acc[ch][j] = zn[ch][j] + bv[ch][j];
+    const int64_t rn = r + nwaves;
+    if (rn < rows) {
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) load_vec<VEC>(z + rn * ldz + fld[ch], zn[ch]);
     }
     ln_relu_store_row<VEC, NCH>(acc, fvalid, foff, dim, gamma, beta, eps, h + r * dim,
                                 out + r * dim, mean + r, rstd + r, lane);
@@ -559,37 +594,43 @@ __global__ __launch_bounds__(256) void colsum_partial(const float* __restrict__ 
 }
 
 // Column sums of part[nblk, dim] over nblk, deterministic: a workgroup owns
-// 16 columns; its 16 row groups each sum rows g, g+16, ... of their column in
-// order, then the 16 group sums are added in group order.
+// 4 columns; its 64 row groups each sum rows g, g+64, ... of their column in
+// order, then the 64 group sums are added in group order.
+constexpr int kFinalCols = 4;
+constexpr int kFinalGroups = 64;
+
 __global__ __launch_bounds__(256) void colsum_final(const float* __restrict__ part, int nblk,
                                                     int dim, float* __restrict__ out) {
-  __shared__ float red[16][17];
-  const int cl = threadIdx.x & 15;
-  const int grp = threadIdx.x >> 4;
-  const int f = blockIdx.x * 16 + cl;
+  __shared__ float red[kFinalGroups][kFinalCols + 1];
+  const int cl = threadIdx.x % kFinalCols;
+  const int grp = threadIdx.x / kFinalCols;
+  const int f = blockIdx.x * kFinalCols + cl;
   float s = 0.f;
   if (f < dim) {
     int b = grp;
-    for (; b + 48 < nblk; b += 64) {
+    for (; b + 3 * kFinalGroups < nblk; b += 4 * kFinalGroups) {
       const float a0 = part[(int64_t)b * dim + f];
-      const float a1 = part[(int64_t)(b + 16) * dim + f];
-      const float a2 = part[(int64_t)(b + 32) * dim + f];
-      const float a3 = part[(int64_t)(b + 48) * dim + f];
+      const float a1 = part[(int64_t)(b + kFinalGroups) * dim + f];
+      const float a2 = part[(int64_t)(b + 2 * kFinalGroups) * dim + f];
+      const float a3 = part[(int64_t)(b + 3 * kFinalGroups) * dim + f];
       s += a0;
       s += a1;
       s += a2;
       s += a3;
     }
-    for (; b < nblk; b += 16) s += part[(int64_t)b * dim + f];
+    for (; b < nblk; b += kFinalGroups) s += part[(int64_t)b * dim + f];
   }
   red[grp][cl] = s;
   __syncthreads();
   if (grp == 0 && f < dim) {
     float t = 0.f;
-#pragma unroll
-    for (int g = 0; g < 16; ++g) t += red[g][cl];
+    for (int g = 0; g < kFinalGroups; ++g) t += red[g][cl];
     out[f] = t;
   }
+}
+
+inline unsigned final_blocks(int64_t dim) {
+  return (unsigned)((dim + kFinalCols - 1) / kFinalCols);
 }
 
 template <int VEC, int G, int NCH>
@@ -703,7 +744,7 @@ extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t 
     hipLaunchKernelGGL(gr_agg::colsum_partial<false>, dim3((unsigned)nblk), dim3(256), 0, s, x,
                        rows, (int)dim, ldx, nullptr, 0, 1, chunk, workspace);
   GR_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((dim + 15) / 16)), dim3(256), 0, s,
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(dim)), dim3(256), 0, s,
                      workspace, (int)nblk, (int)dim, out);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
@@ -833,12 +874,12 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
 #undef GR_LNB
   GR_HIP_CHECK(hipGetLastError());
   // dgamma / dbeta = column sums of the partials, in wavefront order.
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s, pg,
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(d)), dim3(256), 0, s, pg,
                      (int)nwaves, d, dgamma);
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s, pb,
+  hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(d)), dim3(256), 0, s, pb,
                      (int)nwaves, d, dbeta);
   if (dbias != nullptr)
-    hipLaunchKernelGGL(gr_agg::colsum_final, dim3((unsigned)((d + 15) / 16)), dim3(256), 0, s,
+    hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(d)), dim3(256), 0, s,
                        ph, (int)nwaves, d, dbias);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;

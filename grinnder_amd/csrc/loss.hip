@@ -103,10 +103,32 @@ __global__ __launch_bounds__(256) void xent_rows_small(const float* __restrict__
   const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock;
   const int nr = (int)min<int64_t>(kRowsPerBlock, rows - row0);
   const int n = nr * C;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const int r = i / C;
-    const int c = i - r * C;
-    tile[r * CP + c] = x[(row0 + r) * ld + c];
+  // Dense rows of odd width: the tile is a straight copy (16-byte accesses
+  // when aligned); otherwise element by element into the padded layout.
+  const bool linear = CP == C && ld == C;
+  if (linear) {
+    const float* src = x + row0 * C;
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+      const int n4 = n / 4;
+      for (int i = threadIdx.x; i < n4; i += 256)
+        reinterpret_cast<float4*>(tile)[i] = reinterpret_cast<const float4*>(src)[i];
+      for (int i = n4 * 4 + threadIdx.x; i < n; i += 256) tile[i] = src[i];
+    } else {
+      for (int i = threadIdx.x; i < n; i += 256) tile[i] = src[i];
+    }
+  } else {
+    // (r, c) of element i advance by (256 / C, 256 % C) per step.
+    const int dq = 256 / C, dr = 256 - dq * C;
+    int r = threadIdx.x / C, c = threadIdx.x - r * C;
+    for (int i = threadIdx.x; i < n; i += 256) {
+      tile[r * CP + c] = x[(row0 + r) * ld + c];
+      r += dq;
+      c += dr;
+      if (c >= C) {
+        c -= C;
+        ++r;
+      }
+    }
   }
   __syncthreads();
   double acc[kStats];
@@ -142,10 +164,28 @@ __global__ __launch_bounds__(256) void xent_rows_small(const float* __restrict__
   }
   if (grad != nullptr) {
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) {
-      const int r = i / C;
-      const int c = i - r * C;
-      grad[(row0 + r) * ldg + c] = tile[r * CP + c];
+    float* dst = grad + row0 * ldg;
+    if (CP == C && ldg == C) {
+      if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        const int n4 = n / 4;
+        for (int i = threadIdx.x; i < n4; i += 256)
+          reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(tile)[i];
+        for (int i = n4 * 4 + threadIdx.x; i < n; i += 256) dst[i] = tile[i];
+      } else {
+        for (int i = threadIdx.x; i < n; i += 256) dst[i] = tile[i];
+      }
+    } else {
+      const int dq = 256 / C, dr = 256 - dq * C;
+      int r = threadIdx.x / C, c = threadIdx.x - r * C;
+      for (int i = threadIdx.x; i < n; i += 256) {
+        dst[(int64_t)r * ldg + c] = tile[r * CP + c];
+        r += dq;
+        c += dr;
+        if (c >= C) {
+          c -= C;
+          ++r;
+        }
+      }
     }
   }
   block_stats(acc, part);
