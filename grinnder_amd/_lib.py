@@ -23,6 +23,9 @@ _dbl = ctypes.c_double
 _f32 = ctypes.c_float
 _P = ctypes.c_void_p  # every pointer crosses as void*
 
+# Activations of the LayerNorm epilogues (GR_ACT_* in include/grinnder_amd.h).
+ACTIVATIONS = {"relu": 0, "elu": 1}
+
 # name -> argument types (all return int status)
 _SIGNATURES = {
     "gr_h2d_copy_async": [_P, _P, _i64, _P],
@@ -43,8 +46,9 @@ _SIGNATURES = {
     "gr_column_sum": [_P, _i64, _i64, _i64, _P, _i64, _i64, _P, _P, _i64, _P],
     "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,
                                  _i64, _P, _P, _P, _P, _P, _i64, _P],
-    "gr_ln_relu_backward": [_P, _P, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _P, _P, _i64, _P],
-    "gr_bias_ln_relu": [_P, _i64, _P, _P, _P, _f32, _i64, _i64, _P, _P, _P, _P, _P],
+    "gr_ln_act_backward": [_P, _P, _P, _P, _P, _P, _i32, _i64, _i64, _P, _P, _P, _P, _P, _i64,
+                           _P],
+    "gr_bias_ln_act": [_P, _i64, _P, _P, _P, _f32, _i32, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_gemm_tn_workspace": [_i64, _i64, _i64, _P, _P],
     "gr_xent_forward": [_P, _i64, _i64, _i64, _P, _P, _i32, _P, _P, _i64, _P, _P, _P, _i64, _P],
     "gr_gemm_tn": [_P, _i64, _P, _i64, _i64, _i64, _i64, _f32, _P, _P, _i64, _i64, _P],

@@ -213,9 +213,9 @@ def gcn_linear_aggregate(x: Tensor, weight: Tensor, adj: Adjacency,
     return _GCNLinearAggregatePadded.apply(x, weight, bias, plan)
 
 
-def ln_relu_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: Tensor,
-                     beta: Tensor, with_bias: bool = False):
-    """(dL/dh, dgamma, dbeta, dbias or None) of out = ReLU(LayerNorm(h)) given
+def ln_act_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: Tensor,
+                    beta: Tensor, with_bias: bool = False, act: str = "relu"):
+    """(dL/dh, dgamma, dbeta, dbias or None) of out = act(LayerNorm(h)) given
     dL/dout (GPU); dbias = the column sums of dL/dh, formed in the same pass."""
     gout = gout.contiguous()
     B, D = h.shape
@@ -228,8 +228,9 @@ def ln_relu_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma:
     nwaves = (nwaves + 3) // 4 * 4
     ws = torch.empty(((3 if with_bias else 2) * nwaves + 1) * D, dtype=torch.float32,
                      device=dev)
-    _lib.call("gr_ln_relu_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
-              rstd.data_ptr(), gamma.data_ptr(), beta.data_ptr(), B, D, gh.data_ptr(),
+    _lib.call("gr_ln_act_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
+              rstd.data_ptr(), gamma.data_ptr(), beta.data_ptr(), _lib.ACTIVATIONS[act], B, D,
+              gh.data_ptr(),
               dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias), ws.data_ptr(), ws.numel(),
               _lib.stream_handle())
     return gh, dgamma, dbeta, dbias
@@ -270,7 +271,7 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
     def backward(ctx, gout: Tensor):
         h, mean, rstd, g, bt = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
-        gh, dgamma, dbeta, db = ln_relu_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
+        gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
         dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd") \
             if ctx.needs_input_grad[0] else None
         return dz, db, dgamma, dbeta, None, None

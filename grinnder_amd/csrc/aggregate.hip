@@ -204,12 +204,26 @@ __device__ __forceinline__ float wave_sum64(float v) {
 }
 
 // y = (h - mean) * rstd * gamma + beta; the backward recomputes it with the
-// same expression so the ReLU mask is bit-identical.
+// same expression so the activation's branch is bit-identical.
 __device__ __forceinline__ float ln_affine(float h, float mean, float rstd, float g, float b) {
   return fmaf((h - mean) * rstd, g, b);
 }
 
-template <int VEC, int NCH>
+// Activations after the LayerNorm: ReLU (GCN) and ELU with alpha = 1 (GAT),
+// and their derivatives as functions of the pre-activation y.
+template <int ACT>
+__device__ __forceinline__ float act_fwd(float y) {
+  if constexpr (ACT == GR_ACT_RELU) return fmaxf(y, 0.f);
+  else return y > 0.f ? y : expm1f(y);
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_grad(float y) {
+  if constexpr (ACT == GR_ACT_RELU) return y > 0.f ? 1.f : 0.f;
+  else return y > 0.f ? 1.f : expf(y);
+}
+
+template <int VEC, int NCH, int ACT = GR_ACT_RELU>
 __device__ __forceinline__ void ln_relu_store_row(float (&acc)[NCH][VEC], const bool (&fvalid)[NCH],
                                                   const int (&foff)[NCH], int dim,
                                                   const float* __restrict__ gamma,
@@ -240,7 +254,7 @@ __device__ __forceinline__ void ln_relu_store_row(float (&acc)[NCH][VEC], const 
     load_vec<VEC>(gamma + foff[ch], g);
     load_vec<VEC>(beta + foff[ch], b);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) o[j] = fmaxf(ln_affine(acc[ch][j], mean, rstd, g[j], b[j]), 0.f);
+    for (int j = 0; j < VEC; ++j) o[j] = act_fwd<ACT>(ln_affine(acc[ch][j], mean, rstd, g[j], b[j]));
     store_vec<VEC>(hrow + foff[ch], acc[ch]);
     store_vec<VEC>(orow + foff[ch], o);
   }
@@ -401,15 +415,15 @@ __global__ __launch_bounds__(256) void aggregate_ln_relu_fixup(
   }
 }
 
-// Backward of ReLU(LayerNorm(h)): for each row, with xh = (h - mean) * rstd,
-// y = xh * gamma + beta and gy = g * (y > 0):
+// Backward of act(LayerNorm(h)): for each row, with xh = (h - mean) * rstd,
+// y = xh * gamma + beta and gy = g * act'(y):
 //   gh = rstd * (gy*gamma - mean(gy*gamma) - xh * mean(gy*gamma*xh)),
 // and per-wavefront partial sums of dgamma = sum gy*xh, dbeta = sum gy
 // (reduced afterwards in wavefront order).  With part_bias != NULL the
 // per-wavefront column sums of gh itself are kept too: the gradient of the
 // bias added before the LayerNorm, without a second read of gh.
 // Grid-stride over rows.
-template <int VEC, int NCH>
+template <int VEC, int NCH, int ACT>
 __global__ __launch_bounds__(256) void ln_relu_backward(
     const float* __restrict__ g, const float* __restrict__ h, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
@@ -476,7 +490,7 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const float y = ln_affine(hv[j], mu, rs, gam[ch][j], bet[ch][j]);
-        const float gy = (fvalid[ch] && y > 0.f) ? gv[ch][j] : 0.f;
+        const float gy = fvalid[ch] ? gv[ch][j] * act_grad<ACT>(y) : 0.f;
         xh[ch][j] = (hv[j] - mu) * rs;
         gx[ch][j] = gy * gam[ch][j];
         dg[ch][j] = fmaf(gy, xh[ch][j], dg[ch][j]);
@@ -508,12 +522,12 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
   }
 }
 
-// Dense epilogue of a layer whose product was formed outside the aggregation:
-// h = z + bias, out = ReLU(LayerNorm(h)), with the same row statistics and
-// affine expression as the fused aggregation epilogue.  One wavefront per row,
+// Dense epilogue of a layer whose product was formed outside the aggregation
+// (or by the GAT aggregation): h = z + bias, out = act(LayerNorm(h)), with the
+// same row statistics and affine expression as the fused aggregation epilogue.  One wavefront per row,
 // grid-stride.  h may be z itself (ldz == dim): each lane reads its elements
 // of the row before the row statistics are reduced, and writes them after.
-template <int VEC, int NCH>
+template <int VEC, int NCH, int ACT>
 __global__ __launch_bounds__(256) void bias_ln_relu_rows(
     const float* z, int64_t ldz, const float* __restrict__ bias,
     const float* __restrict__ gamma, const float* __restrict__ beta, float eps, int dim,
@@ -555,8 +569,8 @@ __global__ __launch_bounds__(256) void bias_ln_relu_rows(
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch) load_vec<VEC>(z + rn * ldz + fld[ch], zn[ch]);
     }
-    ln_relu_store_row<VEC, NCH>(acc, fvalid, foff, dim, gamma, beta, eps, h + r * dim,
-                                out + r * dim, mean + r, rstd + r, lane);
+    ln_relu_store_row<VEC, NCH, ACT>(acc, fvalid, foff, dim, gamma, beta, eps, h + r * dim,
+                                     out + r * dim, mean + r, rstd + r, lane);
   }
 }
 
@@ -828,9 +842,9 @@ extern "C" int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
   return GR_OK;
 }
 
-extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
-                                   const float* rstd, const float* gamma, const float* beta,
-                                   int64_t rows, int64_t dim, float* gh, float* dgamma,
+extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* mean,
+                                  const float* rstd, const float* gamma, const float* beta,
+                                  int32_t act, int64_t rows, int64_t dim, float* gh, float* dgamma,
                                    float* dbeta, float* dbias, float* workspace,
                                    int64_t workspace_floats,
                                    void* stream) {
@@ -838,6 +852,8 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
   int vec, nch;
   GR_REQUIRE(rows >= 0 && dim >= 1 && fused_shape(dim, &vec, &nch),
              "ln_relu_backward: dim %lld unsupported", (long long)dim);
+  GR_REQUIRE(act == GR_ACT_RELU || act == GR_ACT_ELU, "ln_act_backward: unknown activation %d",
+             act);
   GR_REQUIRE(gamma && beta && dgamma && dbeta && workspace &&
                  (rows == 0 || (g && h && mean && rstd && gh)),
              "ln_relu_backward: NULL pointer");
@@ -863,9 +879,15 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
   hipStream_t s = gr::as_stream(stream);
   const int d = (int)dim;
   const unsigned blocks = (unsigned)(nwaves / 4);
-#define GR_LNB(V, N)                                                                        \
-  hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N>), dim3(blocks), dim3(256), 0, s, g, h, \
-                     mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph)
+#define GR_LNB(V, N)                                                                         \
+  do {                                                                                       \
+    if (act == GR_ACT_RELU)                                                                  \
+      hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N, GR_ACT_RELU>), dim3(blocks), dim3(256), \
+                         0, s, g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);      \
+    else                                                                                     \
+      hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N, GR_ACT_ELU>), dim3(blocks), dim3(256),  \
+                         0, s, g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);      \
+  } while (0)
   if (vec == 4) {
     if (nch == 1) GR_LNB(4, 1); else if (nch == 2) GR_LNB(4, 2); else GR_LNB(4, 4);
   } else {
@@ -885,15 +907,16 @@ extern "C" int gr_ln_relu_backward(const float* g, const float* h, const float* 
   return GR_OK;
 }
 
-extern "C" int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
-                               const float* gamma, const float* beta, float eps, int64_t rows,
-                               int64_t dim, float* h, float* out, float* mean, float* rstd,
-                               void* stream) {
+extern "C" int gr_bias_ln_act(const float* z, int64_t ldz, const float* bias,
+                              const float* gamma, const float* beta, float eps, int32_t act,
+                              int64_t rows, int64_t dim, float* h, float* out, float* mean,
+                              float* rstd, void* stream) {
   gr::clear_error();
   int vec, nch;
   GR_REQUIRE(rows >= 0 && dim >= 1 && fused_shape(dim, &vec, &nch),
              "bias_ln_relu: dim %lld unsupported (max 1024)", (long long)dim);
   GR_REQUIRE(ldz >= dim, "bias_ln_relu: ldz < dim");
+  GR_REQUIRE(act == GR_ACT_RELU || act == GR_ACT_ELU, "bias_ln_act: unknown activation %d", act);
   GR_REQUIRE(h != z || ldz == dim, "bias_ln_relu: in-place h needs ldz == dim");
   if (rows == 0) return GR_OK;
   GR_REQUIRE(z && gamma && beta && h && out && mean && rstd, "bias_ln_relu: NULL pointer");
@@ -910,9 +933,17 @@ extern "C" int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
   hipStream_t s = gr::as_stream(stream);
   const int d = (int)dim;
   const unsigned blocks = (unsigned)std::min<int64_t>(8192, (rows + 3) / 4);
-#define GR_BLR(V, N)                                                                    \
-  hipLaunchKernelGGL((gr_agg::bias_ln_relu_rows<V, N>), dim3(blocks), dim3(256), 0, s, z, \
-                     ldz, bias, gamma, beta, eps, d, rows, h, out, mean, rstd)
+#define GR_BLR(V, N)                                                                        \
+  do {                                                                                      \
+    if (act == GR_ACT_RELU)                                                                 \
+      hipLaunchKernelGGL((gr_agg::bias_ln_relu_rows<V, N, GR_ACT_RELU>), dim3(blocks),      \
+                         dim3(256), 0, s, z, ldz, bias, gamma, beta, eps, d, rows, h, out,  \
+                         mean, rstd);                                                       \
+    else                                                                                    \
+      hipLaunchKernelGGL((gr_agg::bias_ln_relu_rows<V, N, GR_ACT_ELU>), dim3(blocks),       \
+                         dim3(256), 0, s, z, ldz, bias, gamma, beta, eps, d, rows, h, out,  \
+                         mean, rstd);                                                       \
+  } while (0)
   if (vec == 4) {
     if (nch == 1) GR_BLR(4, 1); else if (nch == 2) GR_BLR(4, 2); else GR_BLR(4, 4);
   } else {

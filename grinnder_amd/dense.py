@@ -8,8 +8,9 @@ partition with M, N <= a few hundred, a shape the library GEMMs split poorly.
 ``linear`` keeps the forward on torch and computes dW with ``gr_gemm_tn``
 (split-K fp32 MFMA, partials summed in a fixed order).
 
-``bias_ln_relu`` is the dense counterpart of the fused aggregation epilogue,
-used when a layer aggregates first and multiplies afterwards.
+``bias_ln_act`` is the dense counterpart of the fused aggregation epilogue:
+LayerNorm + ReLU after a GCN layer that aggregates first and multiplies
+afterwards, and LayerNorm + ELU after a GAT layer.
 """
 
 from __future__ import annotations
@@ -103,12 +104,12 @@ def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
     return _Linear.apply(x, weight, bias)
 
 
-class _BiasLNReLU(torch.autograd.Function):
-    """out = ReLU(LayerNorm(z + b)); backward with gr_ln_relu_backward."""
+class _BiasLNAct(torch.autograd.Function):
+    """out = act(LayerNorm(z + b)); backward with gr_ln_act_backward."""
 
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                eps: float) -> Tensor:
+                eps: float, act: str) -> Tensor:
         z = z.contiguous()
         rows, dim = z.shape
         dev = z.device
@@ -118,23 +119,34 @@ class _BiasLNReLU(torch.autograd.Function):
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         b = bias.contiguous() if bias is not None else None
         g, bt = gamma.contiguous(), beta.contiguous()
-        _lib.call("gr_bias_ln_relu", z.data_ptr(), z.stride(0), _lib.ptr(b), g.data_ptr(),
-                  bt.data_ptr(), float(eps), rows, dim, h.data_ptr(), out.data_ptr(),
-                  mean.data_ptr(), rstd.data_ptr(), _lib.stream_handle())
+        _lib.call("gr_bias_ln_act", z.data_ptr(), z.stride(0), _lib.ptr(b), g.data_ptr(),
+                  bt.data_ptr(), float(eps), _lib.ACTIVATIONS[act], rows, dim, h.data_ptr(),
+                  out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), _lib.stream_handle())
         ctx.save_for_backward(h, mean, rstd, g, bt)
         ctx.has_bias = bias is not None
+        ctx.act = act
         return out
 
     @staticmethod
     def backward(ctx, gout: Tensor):
-        from grinnder_amd.aggregation import ln_relu_backward
+        from grinnder_amd.aggregation import ln_act_backward
         h, mean, rstd, g, bt = ctx.saved_tensors
-        gh, dgamma, dbeta, db = ln_relu_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
-        return gh, db, dgamma, dbeta, None
+        gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias,
+                                                ctx.act)
+        return gh, db, dgamma, dbeta, None, None
+
+
+def bias_ln_act(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
+                eps: float = 1e-5, act: str = "relu") -> Tensor:
+    """act(LayerNorm(z + bias)) over the rows of z (GPU, one pass); act is
+    "relu" or "elu" (alpha = 1)."""
+    _check("z", z)
+    if act not in _lib.ACTIVATIONS:
+        raise ValueError(f"unknown activation {act!r}")
+    return _BiasLNAct.apply(z, bias, gamma, beta, eps, act)
 
 
 def bias_ln_relu(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
                  eps: float = 1e-5) -> Tensor:
     """ReLU(LayerNorm(z + bias)) over the rows of z (GPU, one pass)."""
-    _check("z", z)
-    return _BiasLNReLU.apply(z, bias, gamma, beta, eps)
+    return bias_ln_act(z, bias, gamma, beta, eps, "relu")

@@ -8,6 +8,7 @@ import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
 
+from grinnder_amd.dense import bias_ln_act
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.nn.conv import GATConv
 
@@ -43,7 +44,12 @@ class GAT(GriNNderModel):
         x = self.convs[layer]((x, x[:num_dst]), adj)
         if layer < self.num_layers - 1:
             if self.norms is not None:
-                x = self.norms[layer](x)
+                norm = self.norms[layer]
+                if (x.is_cuda and norm.elementwise_affine and norm.bias is not None
+                        and tuple(norm.normalized_shape) == (x.size(-1),)):
+                    # LayerNorm + ELU in one pass over the attention output.
+                    return bias_ln_act(x, None, norm.weight, norm.bias, norm.eps, "elu")
+                x = norm(x)
             x = F.elu(x)
         return x
 

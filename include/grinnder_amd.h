@@ -45,6 +45,10 @@ extern "C" {
 #define GR_ENOMEM (-3)   /* host allocation failed */
 #define GR_EUNSUP (-4)   /* shape or dtype not supported */
 
+/* Activations of the LayerNorm epilogues. */
+#define GR_ACT_RELU 0    /* max(y, 0): GCN.forward_layer, grinnder/nn/gcn.py:64-72 */
+#define GR_ACT_ELU 1     /* y > 0 ? y : exp(y) - 1: GAT.forward_layer, gat.py:74-78 */
+
 /* Message of the last failure on this thread ("" if none). */
 const char* gr_last_error(void);
 
@@ -226,17 +230,18 @@ int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
                              float* mean, float* rstd, float* workspace,
                              int64_t n_slots, void* stream);
 
-/* Backward of out = ReLU(LayerNorm(h)) given g = dL/dout: writes
+/* Backward of out = act(LayerNorm(h)) (act = GR_ACT_RELU or GR_ACT_ELU) given
+ * g = dL/dout: writes
  * gh = dL/dh [rows, dim], dgamma [dim], dbeta [dim] and, when dbias != NULL,
  * dbias = sum_rows gh (the gradient of a bias added before the LayerNorm)
  * (deterministic: per-wavefront partials reduced in order).  workspace: at
  * least (k * 4 + 1) * dim floats with k = 3 when dbias != NULL, else 2; up to
  * (k * 8192 + 1) * dim are used. */
-int gr_ln_relu_backward(const float* g, const float* h, const float* mean,
-                        const float* rstd, const float* gamma, const float* beta,
-                        int64_t rows, int64_t dim, float* gh, float* dgamma,
-                        float* dbeta, float* dbias, float* workspace,
-                        int64_t workspace_floats, void* stream);
+int gr_ln_act_backward(const float* g, const float* h, const float* mean,
+                       const float* rstd, const float* gamma, const float* beta,
+                       int32_t act, int64_t rows, int64_t dim, float* gh,
+                       float* dgamma, float* dbeta, float* dbias, float* workspace,
+                       int64_t workspace_floats, void* stream);
 
 /* Column sums out[f] = sum_i X[i, f] (w == NULL), or weighted sums
  * out[f] = sum_i w[i * ldw + f / group] * X[i, f] (fp32, deterministic: fixed
@@ -250,16 +255,17 @@ int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
                   float* workspace, int64_t workspace_floats, void* stream);
 
 /* Dense form of the fused epilogue, for a layer whose product Z was formed
- * outside the aggregation (aggregate-first GCN: Z = (A X) W^T):
- *   h = Z + bias, out = ReLU(LayerNorm(h)), mean, rstd
- * with the same expressions as gr_gcn_aggregate_ln_relu, so gr_ln_relu_backward
+ * outside the aggregation (aggregate-first GCN: Z = (A X) W^T; GAT output):
+ *   h = Z + bias, out = act(LayerNorm(h)), mean, rstd
+ * with the same expressions as gr_gcn_aggregate_ln_relu, so gr_ln_act_backward
  * is its backward.  Z is ldz-strided; h, out dense [rows, dim]; h may be Z
  * itself when ldz == dim.  Replaces the LayerNorm + ReLU that follow the conv
- * in grinnder/nn/gcn.py:64-72. */
-int gr_bias_ln_relu(const float* z, int64_t ldz, const float* bias,
-                    const float* gamma, const float* beta, float eps,
-                    int64_t rows, int64_t dim, float* h, float* out,
-                    float* mean, float* rstd, void* stream);
+ * in grinnder/nn/gcn.py:64-72 (act = GR_ACT_RELU) and the LayerNorm + ELU of
+ * grinnder/nn/gat.py:74-78 (act = GR_ACT_ELU). */
+int gr_bias_ln_act(const float* z, int64_t ldz, const float* bias,
+                   const float* gamma, const float* beta, float eps, int32_t act,
+                   int64_t rows, int64_t dim, float* h, float* out, float* mean,
+                   float* rstd, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Loss and accuracy                                                         */

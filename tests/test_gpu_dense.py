@@ -1,13 +1,13 @@
 """GPU: the dense per-layer transform — split-K weight-gradient GEMM
 (gr_gemm_tn), the Linear autograd function built on it, and the dense
-bias + LayerNorm + ReLU epilogue (gr_bias_ln_relu) — against float64 torch.
+bias + LayerNorm + ReLU/ELU epilogue (gr_bias_ln_act) — against float64 torch.
 fp32 tolerance: max-abs-normalised error <= 1e-5 (TOL)."""
 
 import pytest
 import torch
 
 from grinnder_amd import _lib
-from grinnder_amd.dense import bias_ln_relu, gemm_tn, gemm_tn_splits, linear
+from grinnder_amd.dense import bias_ln_act, bias_ln_relu, gemm_tn, gemm_tn_splits, linear
 from tests.graphs import TOL, max_abs_norm_err
 
 pytestmark = pytest.mark.gpu
@@ -130,8 +130,8 @@ def test_bias_ln_relu_in_place_h(gpu):
         out = torch.empty_like(z)
         mean = torch.empty(rows, device=gpu)
         rstd = torch.empty(rows, device=gpu)
-        _lib.call("gr_bias_ln_relu", zz.data_ptr(), dim, bias.data_ptr(), gamma.data_ptr(),
-                  beta.data_ptr(), 1e-5, rows, dim, h.data_ptr(), out.data_ptr(),
+        _lib.call("gr_bias_ln_act", zz.data_ptr(), dim, bias.data_ptr(), gamma.data_ptr(),
+                  beta.data_ptr(), 1e-5, 0, rows, dim, h.data_ptr(), out.data_ptr(),
                   mean.data_ptr(), rstd.data_ptr(), _lib.stream_handle())
         outs.append((h.clone(), out.clone()))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
@@ -141,3 +141,28 @@ def test_bias_ln_relu_in_place_h(gpu):
 def test_default_splits_shape(gpu):
     s, ws = gemm_tn_splits(256, 256, 2_449_029)
     assert s % 8 == 0 and ws == s * 256 * 256
+
+
+@pytest.mark.parametrize("rows,dim,bias", [(3000, 256, True), (800, 20, False)])
+def test_bias_ln_elu_matches_fp64(gpu, rows, dim, bias):
+    """The GAT epilogue: ELU(LayerNorm(z + b)) and its gradients."""
+    z = _randn(rows, dim, seed=dim + 1, dev=gpu).requires_grad_(True)
+    b = _randn(dim, seed=5, dev=gpu).requires_grad_(True) if bias else None
+    gamma = (1 + 0.1 * _randn(dim, seed=6, dev=gpu)).requires_grad_(True)
+    beta = (0.1 * _randn(dim, seed=7, dev=gpu)).requires_grad_(True)
+    go = _randn(rows, dim, seed=8, dev=gpu)
+    out = bias_ln_act(z, b, gamma, beta, 1e-5, "elu")
+    out.backward(go)
+    zd = z.detach().double().requires_grad_(True)
+    bd = b.detach().double().requires_grad_(True) if bias else None
+    gd = gamma.detach().double().requires_grad_(True)
+    btd = beta.detach().double().requires_grad_(True)
+    h = zd + bd if bias else zd
+    ref = torch.nn.functional.elu(torch.nn.functional.layer_norm(h, (dim,), gd, btd, 1e-5))
+    ref.backward(go.double())
+    assert max_abs_norm_err(out, ref) <= TOL
+    assert max_abs_norm_err(z.grad, zd.grad) <= TOL
+    assert max_abs_norm_err(gamma.grad, gd.grad) <= TOL
+    assert max_abs_norm_err(beta.grad, btd.grad) <= TOL
+    if bias:
+        assert max_abs_norm_err(b.grad, bd.grad) <= TOL

@@ -309,7 +309,10 @@ def test_gemm_tn_split_heuristic_and_argument_checks():
     with pytest.raises(_lib.GrError, match="leading dimension"):
         _lib.call("gr_gemm_tn", fake, 4, fake, 8, 8, 8, 100, 0.0, fake, fake, 10**6, 1, None)
     with pytest.raises(_lib.GrError, match="in-place"):
-        _lib.call("gr_bias_ln_relu", fake, 12, None, fake, fake, 1e-5, 4, 8, fake, fake, fake,
+        _lib.call("gr_bias_ln_act", fake, 12, None, fake, fake, 1e-5, 0, 4, 8, fake, fake, fake,
+                  fake, None)
+    with pytest.raises(_lib.GrError, match="activation"):
+        _lib.call("gr_bias_ln_act", fake, 8, None, fake, fake, 1e-5, 7, 4, 8, fake, fake, fake,
                   fake, None)
 
 
