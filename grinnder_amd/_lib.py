@@ -50,6 +50,8 @@ _SIGNATURES = {
                            _P],
     "gr_bias_ln_act": [_P, _i64, _P, _P, _P, _f32, _i32, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_gemm_tn_workspace": [_i64, _i64, _i64, _P, _P],
+    "gr_linear_ln_act": [_P, _i64, _i64, _i64, _P, _i64, _P, _P, _P, _f32, _i32, _P, _P, _P, _P,
+                         _P],
     "gr_xent_forward": [_P, _i64, _i64, _i64, _P, _P, _i32, _P, _P, _i64, _P, _P, _P, _i64, _P],
     "gr_gemm_tn": [_P, _i64, _P, _i64, _i64, _i64, _i64, _f32, _P, _P, _i64, _i64, _P],
     "gr_gat_scores": [_P, _i64, _i64, _i64, _i64, _i64, _P, _P, _P, _P, _P],

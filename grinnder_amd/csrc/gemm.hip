@@ -247,3 +247,205 @@ extern "C" int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t l
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Dense layer transform with the LayerNorm epilogue in the accumulators:
+//   z = x W^T, h = z + bias, out = act(LayerNorm(h)), mean, rstd
+// for x [rows, din] (ldx-strided) and W^T [din, dout] (row-major, the
+// transposed weight) with dout = 16 * NB <= 256.
+// A workgroup takes 64 rows; each wavefront owns 16 complete output rows
+// (NB blocks of v_mfma_f32_16x16x4_f32 across the row), so the row statistics
+// are reduced inside the wavefront.  K is walked in chunks of 16 columns of x
+// and W staged through LDS.  The epilogue uses the same expressions as the
+// other LayerNorm epilogues (biased variance, y = (h - mean) * rstd * gamma +
+// beta), so the LayerNorm backward applies unchanged.
+namespace gr_gemm {
+
+constexpr int LT_ROWS = 64;
+constexpr int LT_K = 16;
+
+template <int ACT>
+__device__ __forceinline__ float lt_act(float y) {
+  if constexpr (ACT == GR_ACT_RELU) return fmaxf(y, 0.f);
+  else return y > 0.f ? y : expm1f(y);
+}
+
+template <int NB, int ACT>
+__global__ __launch_bounds__(256) void linear_ln_act_kernel(
+    const float* __restrict__ x, int64_t ldx, int64_t rows, int din,
+    const float* __restrict__ wt, const float* __restrict__ bias,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+    float* __restrict__ h, float* __restrict__ out, float* __restrict__ mean,
+    float* __restrict__ rstd) {
+  constexpr int DOUT = 16 * NB;
+  constexpr int WPT = DOUT * LT_K / 256;  // W^T chunk floats per thread (NB)
+  __shared__ __align__(16) float Ws[LT_K][DOUT + 16];  // Ws[k][c] = W^T[k0 + k][c]
+  static_assert(16 * (DOUT + 4) <= LT_K * (DOUT + 16), "epilogue stage must fit the W tile");
+  __shared__ float Xs[LT_ROWS][LT_K + 1];  // Xs[r][k] = x[row0 + r][k0 + k]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lr = lane & 15;
+  const int lk = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * LT_ROWS;
+
+  floatx4 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // Chunk loads: W^T rows k0..k0+15 (contiguous DOUT floats each) and the
+  // 64 x 16 block of x; element e of this thread is e * 256 + tid.
+  float wr[WPT], xr[4];
+  auto load_chunk = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < WPT; ++e) {
+      const int i = e * 256 + tid;
+      const int k = i / DOUT, c = i % DOUT;
+      wr[e] = (k0 + k < din) ? wt[(int64_t)(k0 + k) * DOUT + c] : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = e * 256 + tid;
+      const int r = i / LT_K, k = i % LT_K;
+      xr[e] = (row0 + r < rows && k0 + k < din) ? x[(row0 + r) * ldx + k0 + k] : 0.f;
+    }
+  };
+  load_chunk(0);
+  for (int k0 = 0; k0 < din; k0 += LT_K) {
+    __syncthreads();  // the previous chunk's reads of Ws / Xs are done
+#pragma unroll
+    for (int e = 0; e < WPT; ++e) {
+      const int i = e * 256 + tid;
+      Ws[i / DOUT][i % DOUT] = wr[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = e * 256 + tid;
+      Xs[i / LT_K][i % LT_K] = xr[e];
+    }
+    __syncthreads();
+    if (k0 + LT_K < din) load_chunk(k0 + LT_K);
+    const int kmax = din - k0 < LT_K ? din - k0 : LT_K;
+    for (int kk = 0; kk < kmax; kk += 4) {
+      const float a = Xs[wave * 16 + lr][kk + lk];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Ws[kk + lk][b * 16 + lr], acc[b], 0, 0,
+                                                       0);
+    }
+  }
+
+  // Lane holds rows 4 * lk + q (q = 0..3) of the wavefront's 16, columns
+  // b * 16 + lr.  Row reductions: the 16 lanes sharing lk.
+  if (bias != nullptr) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float bb = bias[b * 16 + lr];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[b][q] += bb;
+    }
+  }
+  const float inv_d = 1.0f / (float)DOUT;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t row = row0 + wave * 16 + lk * 4 + q;
+    float s = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s += acc[b][q];
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
+    const float mu = s * inv_d;
+    float v = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float dlt = acc[b][q] - mu;
+      v += dlt * dlt;
+    }
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 64);
+    const float rs = 1.0f / sqrtf(v * inv_d + eps);
+    // Stage the 4 rows {4 * lk + q} of this wavefront in LDS (reusing the W
+    // tile), then store them with 16-byte accesses along each row.
+    __syncthreads();
+    float* stage = &Ws[0][0] + wave * 4 * (DOUT + 4);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) stage[lk * (DOUT + 4) + b * 16 + lr] = acc[b][q];
+    __syncthreads();
+    if (row < rows) {
+      const float* srow = stage + lk * (DOUT + 4);
+      for (int c = lr * 4; c < DOUT; c += 64) {
+        const float4 hv = *reinterpret_cast<const float4*>(srow + c);
+        const float4 gg = *reinterpret_cast<const float4*>(gamma + c);
+        const float4 bt = *reinterpret_cast<const float4*>(beta + c);
+        float4 o;
+        o.x = lt_act<ACT>(fmaf((hv.x - mu) * rs, gg.x, bt.x));
+        o.y = lt_act<ACT>(fmaf((hv.y - mu) * rs, gg.y, bt.y));
+        o.z = lt_act<ACT>(fmaf((hv.z - mu) * rs, gg.z, bt.z));
+        o.w = lt_act<ACT>(fmaf((hv.w - mu) * rs, gg.w, bt.w));
+        *reinterpret_cast<float4*>(h + row * DOUT + c) = hv;
+        *reinterpret_cast<float4*>(out + row * DOUT + c) = o;
+      }
+      if (lr == 0) {
+        mean[row] = mu;
+        rstd[row] = rs;
+      }
+    }
+  }
+}
+
+}  // namespace gr_gemm
+
+extern "C" int gr_linear_ln_act(const float* x, int64_t ldx, int64_t rows, int64_t din,
+                                const float* wt, int64_t dout, const float* bias,
+                                const float* gamma, const float* beta, float eps, int32_t act,
+                                float* h, float* out, float* mean, float* rstd, void* stream) {
+  using namespace gr_gemm;
+  gr::clear_error();
+  GR_REQUIRE(rows >= 0 && din >= 1 && ldx >= din, "linear_ln_act: bad shape");
+  GR_REQUIRE(dout >= 16 && dout <= 256 && dout % 16 == 0,
+             "linear_ln_act: dout %lld must be a multiple of 16 in [16, 256]", (long long)dout);
+  GR_REQUIRE(act == GR_ACT_RELU || act == GR_ACT_ELU, "linear_ln_act: unknown activation %d",
+             act);
+  if (rows == 0) return GR_OK;
+  GR_REQUIRE(x && wt && gamma && beta && h && out && mean && rstd,
+             "linear_ln_act: NULL pointer");
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  GR_REQUIRE(al16(gamma) && al16(beta) && al16(h) && al16(out),
+             "linear_ln_act: gamma, beta, h and out must be 16-byte aligned");
+  const int64_t blocks = (rows + LT_ROWS - 1) / LT_ROWS;
+  GR_REQUIRE(blocks <= INT32_MAX, "linear_ln_act: too many rows");
+  hipStream_t s = gr::as_stream(stream);
+  const int nb = (int)(dout / 16);
+#define GR_LT(NB)                                                                              \
+  do {                                                                                         \
+    if (act == GR_ACT_RELU)                                                                    \
+      hipLaunchKernelGGL((linear_ln_act_kernel<NB, GR_ACT_RELU>), dim3((unsigned)blocks),      \
+                         dim3(256), 0, s, x, ldx, rows, (int)din, wt, bias, gamma, beta, eps, h, \
+                         out, mean, rstd);                                                     \
+    else                                                                                       \
+      hipLaunchKernelGGL((linear_ln_act_kernel<NB, GR_ACT_ELU>), dim3((unsigned)blocks),       \
+                         dim3(256), 0, s, x, ldx, rows, (int)din, wt, bias, gamma, beta, eps, h, \
+                         out, mean, rstd);                                                     \
+  } while (0)
+  switch (nb) {
+    case 1: GR_LT(1); break;
+    case 2: GR_LT(2); break;
+    case 3: GR_LT(3); break;
+    case 4: GR_LT(4); break;
+    case 5: GR_LT(5); break;
+    case 6: GR_LT(6); break;
+    case 7: GR_LT(7); break;
+    case 8: GR_LT(8); break;
+    case 9: GR_LT(9); break;
+    case 10: GR_LT(10); break;
+    case 11: GR_LT(11); break;
+    case 12: GR_LT(12); break;
+    case 13: GR_LT(13); break;
+    case 14: GR_LT(14); break;
+    case 15: GR_LT(15); break;
+    default: GR_LT(16); break;
+  }
+#undef GR_LT
+  GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}

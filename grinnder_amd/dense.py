@@ -150,3 +150,57 @@ def bias_ln_relu(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
                  eps: float = 1e-5) -> Tensor:
     """ReLU(LayerNorm(z + bias)) over the rows of z (GPU, one pass)."""
     return bias_ln_act(z, bias, gamma, beta, eps, "relu")
+
+
+class _LinearLNAct(torch.autograd.Function):
+    """out = act(LayerNorm(x Wᵀ + b)) with the LayerNorm in the GEMM epilogue
+    (gr_linear_ln_act); backward: gr_ln_act_backward, then dW = ghᵀ x on the
+    split-K kernel and dx = gh W."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor], gamma: Tensor,
+                beta: Tensor, eps: float, act: str) -> Tensor:
+        x = x.contiguous()
+        rows, din = x.shape
+        dout = weight.size(0)
+        dev = x.device
+        w = weight.contiguous()
+        wt = w.t().contiguous()
+        h = torch.empty((rows, dout), dtype=torch.float32, device=dev)
+        out = torch.empty_like(h)
+        mean = torch.empty(rows, dtype=torch.float32, device=dev)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        b = bias.contiguous() if bias is not None else None
+        g, bt = gamma.contiguous(), beta.contiguous()
+        _lib.call("gr_linear_ln_act", x.data_ptr(), x.stride(0), rows, din, wt.data_ptr(), dout,
+                  _lib.ptr(b), g.data_ptr(), bt.data_ptr(), float(eps), _lib.ACTIVATIONS[act],
+                  h.data_ptr(), out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                  _lib.stream_handle())
+        ctx.save_for_backward(x, w, h, mean, rstd, g, bt)
+        ctx.has_bias = bias is not None
+        ctx.act = act
+        return out
+
+    @staticmethod
+    def backward(ctx, gout: Tensor):
+        from grinnder_amd.aggregation import ln_act_backward
+        x, w, h, mean, rstd, g, bt = ctx.saved_tensors
+        gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias,
+                                                ctx.act)
+        dx = torch.mm(gh, w) if ctx.needs_input_grad[0] else None
+        dw = gemm_tn(gh, x) if ctx.needs_input_grad[1] else None
+        return dx, dw, db, dgamma, dbeta, None, None
+
+
+def linear_ln_act(x: Tensor, weight: Tensor, bias: Optional[Tensor], gamma: Tensor,
+                  beta: Tensor, eps: float = 1e-5, act: str = "relu") -> Tensor:
+    """act(LayerNorm(x Wᵀ + bias)) (GPU).  One fused MFMA pass when the output
+    width is a multiple of 16 up to 256; otherwise the product and the
+    epilogue run as two passes."""
+    _check("x", x)
+    if act not in _lib.ACTIVATIONS:
+        raise ValueError(f"unknown activation {act!r}")
+    dout = weight.size(0)
+    if dout % 16 == 0 and dout <= 256 and x.dim() == 2:
+        return _LinearLNAct.apply(x, weight, bias, gamma, beta, eps, act)
+    return bias_ln_act(linear(x, weight), bias, gamma, beta, eps, act)

@@ -9,7 +9,7 @@ from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
 
 from grinnder_amd.aggregation import gcn_aggregate, gcn_aggregate_ln_relu
-from grinnder_amd.dense import bias_ln_relu, linear
+from grinnder_amd.dense import linear, linear_ln_act
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.nn.conv import GCNConv
 
@@ -54,8 +54,8 @@ class GCN(GriNNderModel):
         if self._fusable(layer, x, adj):
             conv, norm = self.convs[layer], self.norms[layer]
             if conv.aggregate_first():
-                z = linear(gcn_aggregate(x, adj), conv.lin.weight)
-                return bias_ln_relu(z, conv.bias, norm.weight, norm.bias, norm.eps)
+                return linear_ln_act(gcn_aggregate(x, adj), conv.lin.weight, conv.bias,
+                                     norm.weight, norm.bias, norm.eps, "relu")
             return gcn_aggregate_ln_relu(linear(x, conv.lin.weight), adj, conv.bias,
                                          norm.weight, norm.bias, norm.eps)
         h = self.convs[layer](x, adj)

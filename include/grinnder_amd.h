@@ -293,7 +293,7 @@ int gr_xent_forward(const float* logits, int64_t ld, int64_t rows,
                     int64_t workspace_doubles, void* stream);
 
 /* ------------------------------------------------------------------------ */
-/* Dense weight gradient                                                     */
+/* Dense transform                                                           */
 /* ------------------------------------------------------------------------ */
 
 /* C[M, N] = A^T B (+ beta * C) with A [K, M] (lda-strided rows) and B [K, N]
@@ -310,6 +310,20 @@ int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t ldb,
                int64_t m, int64_t n, int64_t k, float beta, float* c,
                float* workspace, int64_t workspace_floats, int64_t splits,
                void* stream);
+
+/* Dense layer transform with the LayerNorm epilogue in the GEMM accumulators:
+ *   h = x W^T + bias, out = act(LayerNorm(h; gamma, beta, eps)), mean, rstd
+ * for x [rows, din] (ldx-strided), wt = W^T [din, dout] row-major (the
+ * transposed [dout, din] weight), dout a multiple of 16 in [16, 256]; h, out
+ * dense [rows, dout]; gamma, beta, h and out 16-byte aligned.  fp32 on the matrix cores.  The
+ * epilogue's expressions are those of gr_bias_ln_act, so gr_ln_act_backward is
+ * its backward.  Replaces the Linear of an aggregate-first GCNConv (PyG
+ * GCNConv's lin, grinnder/nn/gcn.py:53-56) followed by the LayerNorm and ReLU
+ * of grinnder/nn/gcn.py:64-72. */
+int gr_linear_ln_act(const float* x, int64_t ldx, int64_t rows, int64_t din,
+                     const float* wt, int64_t dout, const float* bias,
+                     const float* gamma, const float* beta, float eps, int32_t act,
+                     float* h, float* out, float* mean, float* rstd, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* GAT attention (device)                                                    */

@@ -166,3 +166,29 @@ def test_bias_ln_elu_matches_fp64(gpu, rows, dim, bias):
     assert max_abs_norm_err(beta.grad, btd.grad) <= TOL
     if bias:
         assert max_abs_norm_err(b.grad, bd.grad) <= TOL
+
+
+@pytest.mark.parametrize("rows,din,dout,act", [(5000, 100, 256, "relu"), (777, 37, 48, "elu"),
+                                               (64, 3, 16, "relu"), (0, 8, 32, "relu")])
+def test_linear_ln_act_matches_fp64(gpu, rows, din, dout, act):
+    """act(LayerNorm(x Wᵀ + b)) with the LayerNorm in the MFMA GEMM epilogue."""
+    from grinnder_amd.dense import linear_ln_act
+    x = _randn(rows, din, seed=din, dev=gpu).requires_grad_(True)
+    w = (0.2 * _randn(dout, din, seed=dout, dev=gpu)).requires_grad_(True)
+    b = _randn(dout, seed=1, dev=gpu).requires_grad_(True)
+    gamma = (1 + 0.1 * _randn(dout, seed=2, dev=gpu)).requires_grad_(True)
+    beta = (0.1 * _randn(dout, seed=3, dev=gpu)).requires_grad_(True)
+    go = _randn(rows, dout, seed=4, dev=gpu)
+    out = linear_ln_act(x, w, b, gamma, beta, 1e-5, act)
+    out.backward(go)
+    ps = [t.detach().double().requires_grad_(True) for t in (x, w, b, gamma, beta)]
+    f = torch.relu if act == "relu" else torch.nn.functional.elu
+    ref = f(torch.nn.functional.layer_norm(ps[0] @ ps[1].t() + ps[2], (dout,), ps[3], ps[4],
+                                           1e-5))
+    ref.backward(go.double())
+    if rows == 0:
+        assert out.shape == (0, dout)
+        return
+    assert max_abs_norm_err(out, ref) <= TOL
+    for got, want in zip((x, w, b, gamma, beta), ps):
+        assert max_abs_norm_err(got.grad, want.grad) <= TOL
