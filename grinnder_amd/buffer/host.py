@@ -99,6 +99,9 @@ class HostBuffer:
         self._pin_memory = pin_memory
         self._zero_initialized = [False] * num_parts
         self._tensors: List[Tensor] = []
+        # D2H entries (fills, scatters) this buffer queued and nobody waited
+        # for yet; the library's D2H completion queue is FIFO.
+        self.d2h_queued = 0
         for i in range(num_parts):
             t = _empty_host_tensor(part_sizes[i], embedding_dim, pin_memory=pin_memory,
                                    allocate=not lazy)
@@ -168,12 +171,18 @@ class HostBuffer:
         stream.wait_stream(torch.cuda.current_stream(gpu_data.device))
         with torch.cuda.stream(stream):
             _C.d2h_copy_async(gpu_data.contiguous(), self._tensors[pid])
+        self.d2h_queued += 1
         self._zero_initialized[pid] = True
 
     def d2h_synchronize(self, stream: torch.cuda.Stream) -> None:
         """Waits for the oldest queued D2H entry, then for `stream` itself."""
-        _C.d2h_synchronize()
+        self.d2h_wait_oldest()
         stream.synchronize()
+
+    def d2h_wait_oldest(self) -> None:
+        """Waits for the oldest queued D2H entry only (no stream synchronize)."""
+        _C.d2h_synchronize()
+        self.d2h_queued = max(0, self.d2h_queued - 1)
 
     # ---------------------------------------------------------- host -> GPU
 
@@ -222,6 +231,7 @@ class HostBuffer:
         bnd = _none_to_empty(pid, boundaries, self.num_parts)
         with torch.cuda.stream(stream):
             _C.scatter_partitions(pid, gpu_source, self._tensors, bnd)
+        self.d2h_queued += 1
 
     # ------------------------------------------------------------- utilities
 

@@ -216,12 +216,18 @@ class Trainer:
             x, layer_id, pid,
             self.host_gradients[layer_id] if layer_id > 0 else None,
             self.graph.boundaries[pid],
-            self.streams.d2h[pid % self.config.pool_size],
+            self._scatter_stream(),
             self.streams.compute,
         )
         # Activations are stored, freed and re-uploaded as dense [B, D] blocks;
         # a layer may return a strided view (a padded product), made dense here.
         return self.model.forward_layer(layer_id, x, self.graph.adjacency(pid)).contiguous()
+
+    def _scatter_stream(self) -> torch.cuda.Stream:
+        """All halo-gradient scatters of a backward phase share one stream:
+        partitions' halos overlap in the host write-back buffer, and the
+        read-add-write of consecutive partitions must not interleave."""
+        return self.streams.d2h[0]
 
     def _checkpointed(self, layer: int, pid: int, slot: int) -> Tensor:
         x = self.device_features[layer][pid]
@@ -367,6 +373,10 @@ class Trainer:
             self._gather(layer, pids[0], s.act_h2d[0])
         if upload_grad:
             self._upload_grad(layer + 1, pids[0], s.h2d[0])
+        # The scatters of partition p are waited for after partition p+1's
+        # backward ran, so they overlap that compute and the next gather; at
+        # most two partitions' scatters are in flight (one stream, in order).
+        hg = self.host_gradients[layer]
         for i, pid in enumerate(pids):
             k = i % pool
             if regather:
@@ -381,6 +391,7 @@ class Trainer:
                         self._gather(layer, pids[i + 1], s.act_h2d[(i + 1) % pool])
                     if upload_grad:
                         self._upload_grad(layer + 1, pids[i + 1], s.h2d[(i + 1) % pool])
+                queued_before = hg.d2h_queued if hg is not None else 0
                 run(pid)
                 s.compute.synchronize()
                 act = self.activations[layer][pid]
@@ -392,11 +403,15 @@ class Trainer:
                     self.device_gradients) else None
                 if gbuf is not None:
                     gbuf.release(pid)
-                if self.host_gradients[layer] is not None:
-                    self.host_gradients[layer].d2h_synchronize(s.d2h[pid % pool])
+                for _ in range(queued_before):
+                    hg.d2h_wait_oldest()  # the previous partition's scatters
                 self.device_features[layer].release(pid)
             if pool == 1 and i + 1 < len(pids):
                 if regather:
                     self._gather(layer, pids[i + 1], s.act_h2d[0])
                 if upload_grad:
                     self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])
+        if hg is not None:
+            while hg.d2h_queued > 0:
+                hg.d2h_wait_oldest()
+            self._scatter_stream().synchronize()
