@@ -27,19 +27,21 @@ constexpr int TN = 128;
 constexpr int TK = 16;
 constexpr int PAD = 16;  // LDS row padding: rows k and k+1 land 16 banks apart
 
-// Loads rows [k, k + TK) x columns [c0, c0 + 128) of a row-major [K, ld]
-// matrix into registers: 2048 floats per workgroup, 8 per thread.  Out-of-range
-// elements read as 0.
-template <int VEC>
+// Loads rows [k, k + TK) x columns [c0, c0 + W) of a row-major [K, ld] matrix
+// into registers: 16 * W floats per workgroup, W / 16 per thread (W = 128 or
+// 64).  Out-of-range elements read as 0.
+template <int VEC, int W>
 __device__ __forceinline__ void load_tile(const float* __restrict__ src, int64_t ld, int64_t k,
-                                          int64_t k_end, int c0, int cols, float (&r)[8]) {
+                                          int64_t k_end, int c0, int cols,
+                                          float (&r)[W / 16]) {
   const int tid = threadIdx.x;
   if constexpr (VEC == 4) {
+    constexpr int Q = W / 4;  // float4 slots per row
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = tid + i * 256;  // 512 float4 slots: 16 rows x 32
-      const int row = idx >> 5;
-      const int c = c0 + (idx & 31) * 4;
+    for (int i = 0; i < W / 64; ++i) {
+      const int idx = tid + i * 256;
+      const int row = idx / Q;
+      const int c = c0 + (idx % Q) * 4;
       const int64_t kr = k + row;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (kr < k_end && c < cols) v = *reinterpret_cast<const float4*>(src + kr * ld + c);
@@ -50,92 +52,95 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ src, int64_t
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int idx = tid + i * 256;  // 2048 slots: 16 rows x 128
-      const int row = idx >> 7;
-      const int c = c0 + (idx & 127);
+    for (int i = 0; i < W / 16; ++i) {
+      const int idx = tid + i * 256;
+      const int row = idx / W;
+      const int c = c0 + (idx % W);
       const int64_t kr = k + row;
       r[i] = (kr < k_end && c < cols) ? src[kr * ld + c] : 0.f;
     }
   }
 }
 
-template <int VEC>
-__device__ __forceinline__ void store_tile(float (*lds)[TM + PAD], const float (&r)[8]) {
+template <int VEC, int W>
+__device__ __forceinline__ void store_tile(float (*lds)[W + PAD], const float (&r)[W / 16]) {
   const int tid = threadIdx.x;
   if constexpr (VEC == 4) {
+    constexpr int Q = W / 4;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < W / 64; ++i) {
       const int idx = tid + i * 256;
-      const int row = idx >> 5;
-      const int c = (idx & 31) * 4;
+      const int row = idx / Q;
+      const int c = (idx % Q) * 4;
       *reinterpret_cast<float4*>(&lds[row][c]) =
           make_float4(r[i * 4 + 0], r[i * 4 + 1], r[i * 4 + 2], r[i * 4 + 3]);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < W / 16; ++i) {
       const int idx = tid + i * 256;
-      lds[idx >> 7][idx & 127] = r[i];
+      lds[idx / W][idx % W] = r[i];
     }
   }
 }
 
 constexpr int kXcds = 8;
 
-template <int VA, int VB>
+// BN = 128 or 64 output columns per workgroup (64 for narrow N).
+template <int VA, int VB, int BN>
 __global__ __launch_bounds__(256) void gemm_tn_splitk(const float* __restrict__ A, int64_t lda,
                                                       const float* __restrict__ B, int64_t ldb,
                                                       int M, int N, int64_t K, int64_t kchunk,
                                                       int nchunks, int tiles_m, int tiles,
                                                       float* __restrict__ part) {
+  constexpr int NJ = BN / 32;  // 16-column blocks per wavefront
   __shared__ float As[TK][TM + PAD];
-  __shared__ float Bs[TK][TN + PAD];
+  __shared__ float Bs[TK][BN + PAD];
   const int w = blockIdx.x;
   const int q = w / kXcds;
   const int t = q % tiles;
   const int z = (q / tiles) * kXcds + w % kXcds;
   if (z >= nchunks) return;  // whole workgroup: no barrier is pending
   const int m0 = (t % tiles_m) * TM;
-  const int n0 = (t / tiles_m) * TN;
+  const int n0 = (t / tiles_m) * BN;
   const int64_t k_begin = (int64_t)z * kchunk;
   const int64_t k_end = k_begin + kchunk < K ? k_begin + kchunk : K;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = (wave & 1) * 64;
-  const int wn = (wave >> 1) * 64;
+  const int wn = (wave >> 1) * (BN / 2);
   const int lr = lane & 15;  // row (A) / column (B) inside a 16-block
   const int lk = lane >> 4;  // k inside a 4-step
 
-  floatx4 acc[4][4];
+  floatx4 acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  float ra[8], rb[8];
-  load_tile<VA>(A, lda, k_begin, k_end, m0, M, ra);
-  load_tile<VB>(B, ldb, k_begin, k_end, n0, N, rb);
+  float ra[TM / 16], rb[BN / 16];
+  load_tile<VA, TM>(A, lda, k_begin, k_end, m0, M, ra);
+  load_tile<VB, BN>(B, ldb, k_begin, k_end, n0, N, rb);
   for (int64_t k = k_begin; k < k_end; k += TK) {
     __syncthreads();  // previous step's MFMA reads of the LDS tiles are done
-    store_tile<VA>(As, ra);
-    store_tile<VB>(Bs, rb);
+    store_tile<VA, TM>(As, ra);
+    store_tile<VB, BN>(Bs, rb);
     __syncthreads();
     if (k + TK < k_end) {
-      load_tile<VA>(A, lda, k + TK, k_end, m0, M, ra);
-      load_tile<VB>(B, ldb, k + TK, k_end, n0, N, rb);
+      load_tile<VA, TM>(A, lda, k + TK, k_end, m0, M, ra);
+      load_tile<VB, BN>(B, ldb, k + TK, k_end, n0, N, rb);
     }
 #pragma unroll
     for (int kk = 0; kk < TK; kk += 4) {
-      float a[4], b[4];
+      float a[4], b[NJ];
 #pragma unroll
       for (int i = 0; i < 4; ++i) a[i] = As[kk + lk][wm + i * 16 + lr];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[kk + lk][wn + j * 16 + lr];
+      for (int j = 0; j < NJ; ++j) b[j] = Bs[kk + lk][wn + j * 16 + lr];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
   }
@@ -145,7 +150,7 @@ __global__ __launch_bounds__(256) void gemm_tn_splitk(const float* __restrict__ 
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int n = n0 + wn + j * 16 + lr;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -155,10 +160,13 @@ __global__ __launch_bounds__(256) void gemm_tn_splitk(const float* __restrict__ 
     }
 }
 
-// C[e] = sum_z part[z][e] in z order (e over M*N elements, grid-stride).
+// C = sum_z part[z] in z order over the rows x cols partial tiles
+// (grid-stride).  With `trans` the partial holds C^T: element (r, q) goes to
+// c[q * rows + r].
 __global__ __launch_bounds__(256) void sum_partials(const float* __restrict__ part, int splits,
-                                                    int64_t elems, float beta,
-                                                    float* __restrict__ c) {
+                                                    int64_t rows, int64_t cols, float beta,
+                                                    int trans, float* __restrict__ c) {
+  const int64_t elems = rows * cols;
   const int64_t stride = (int64_t)gridDim.x * 256;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < elems; e += stride) {
     float s = 0.f;
@@ -174,7 +182,8 @@ __global__ __launch_bounds__(256) void sum_partials(const float* __restrict__ pa
       s += a3;
     }
     for (; z < splits; ++z) s += part[(int64_t)z * elems + e];
-    c[e] = beta != 0.f ? fmaf(beta, c[e], s) : s;
+    const int64_t d = trans ? (e % cols) * rows + e / cols : e;
+    c[d] = beta != 0.f ? fmaf(beta, c[d], s) : s;
   }
 }
 
@@ -220,30 +229,39 @@ extern "C" int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t l
   GR_REQUIRE(workspace_floats >= used * m * n,
              "gemm_tn: workspace of %lld floats, %lld needed", (long long)workspace_floats,
              (long long)(used * m * n));
-  const bool va = (lda % 4 == 0) && (m % 4 == 0) && (reinterpret_cast<uintptr_t>(a) % 16 == 0);
-  const bool vb = (ldb % 4 == 0) && (n % 4 == 0) && (reinterpret_cast<uintptr_t>(b) % 16 == 0);
-  const int tiles_m = (int)((m + TM - 1) / TM);
-  const int tiles = tiles_m * (int)((n + TN - 1) / TN);
+  // A narrow product (m <= 64 < n) runs as C^T = B^T A, so the narrow side
+  // falls on 64-column tiles instead of wasting rows of 128-row tiles; the
+  // partials are summed into C with a transposed store.
+  const bool swap = m <= 64 && n > 64;
+  const float* pa = swap ? b : a;
+  const float* pb = swap ? a : b;
+  const int64_t pm = swap ? n : m, pn = swap ? m : n;
+  const int64_t plda = swap ? ldb : lda, pldb = swap ? lda : ldb;
+  const bool va = (plda % 4 == 0) && (pm % 4 == 0) && (reinterpret_cast<uintptr_t>(pa) % 16 == 0);
+  const bool vb = (pldb % 4 == 0) && (pn % 4 == 0) && (reinterpret_cast<uintptr_t>(pb) % 16 == 0);
+  const bool narrow = pn <= 64;
+  const int bn = narrow ? 64 : TN;
+  const int tiles_m = (int)((pm + TM - 1) / TM);
+  const int tiles = tiles_m * (int)((pn + bn - 1) / bn);
   const int64_t nwg = (used + kXcds - 1) / kXcds * kXcds * tiles;
   GR_REQUIRE(nwg <= INT32_MAX, "gemm_tn: too many workgroups");
   const dim3 grid((unsigned)nwg);
-  if (va && vb)
-    hipLaunchKernelGGL((gemm_tn_splitk<4, 4>), grid, dim3(256), 0, s, a, lda, b, ldb, (int)m,
-                       (int)n, k, kchunk, (int)used, tiles_m, tiles, workspace);
-  else if (va)
-    hipLaunchKernelGGL((gemm_tn_splitk<4, 1>), grid, dim3(256), 0, s, a, lda, b, ldb, (int)m,
-                       (int)n, k, kchunk, (int)used, tiles_m, tiles, workspace);
-  else if (vb)
-    hipLaunchKernelGGL((gemm_tn_splitk<1, 4>), grid, dim3(256), 0, s, a, lda, b, ldb, (int)m,
-                       (int)n, k, kchunk, (int)used, tiles_m, tiles, workspace);
-  else
-    hipLaunchKernelGGL((gemm_tn_splitk<1, 1>), grid, dim3(256), 0, s, a, lda, b, ldb, (int)m,
-                       (int)n, k, kchunk, (int)used, tiles_m, tiles, workspace);
+#define GR_GT(VA_, VB_, BN_)                                                                   \
+  hipLaunchKernelGGL((gemm_tn_splitk<VA_, VB_, BN_>), grid, dim3(256), 0, s, pa, plda, pb, pldb, \
+                     (int)pm, (int)pn, k, kchunk, (int)used, tiles_m, tiles, workspace)
+  if (narrow) {
+    if (va && vb) GR_GT(4, 4, 64); else if (va) GR_GT(4, 1, 64);
+    else if (vb) GR_GT(1, 4, 64); else GR_GT(1, 1, 64);
+  } else {
+    if (va && vb) GR_GT(4, 4, 128); else if (va) GR_GT(4, 1, 128);
+    else if (vb) GR_GT(1, 4, 128); else GR_GT(1, 1, 128);
+  }
+#undef GR_GT
   GR_HIP_CHECK(hipGetLastError());
   const int64_t elems = m * n;
   const unsigned blocks = (unsigned)std::min<int64_t>(4096, (elems + 255) / 256);
-  hipLaunchKernelGGL(sum_partials, dim3(blocks), dim3(256), 0, s, workspace, (int)used, elems,
-                     beta, c);
+  hipLaunchKernelGGL(sum_partials, dim3(blocks), dim3(256), 0, s, workspace, (int)used, pm, pn,
+                     beta, (int)swap, c);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }

@@ -20,8 +20,10 @@ def _randn(*shape, seed, dev):
 
 @pytest.mark.parametrize("k,m,n", [(0, 5, 7), (1, 1, 1), (37, 3, 5), (1000, 47, 256),
                                    (5000, 256, 100), (3001, 130, 129), (200_000, 256, 256),
-                                   (70_000, 47, 256)])
+                                   (70_000, 47, 256), (20_000, 256, 48), (20_000, 48, 100),
+                                   (5000, 64, 256), (0, 48, 256)])
 def test_gemm_tn_matches_fp64(gpu, k, m, n):
+    """Covers 128- and 64-column tiles and the transposed narrow path (m <= 64 < n)."""
     a = _randn(k, m, seed=k + m, dev=gpu)
     b = _randn(k, n, seed=k + n + 1, dev=gpu)
     c = gemm_tn(a, b)
