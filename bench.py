@@ -32,6 +32,7 @@ import time
 from typing import Optional
 
 HBM_PEAK_GBPS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 CALIBRATION_KIB = 1 << 20      # bytes read (and written) by one calibration launch, in KiB
 CALIBRATION_KERNEL = "bitwise_not"
 # PMC summary whose FETCH_SIZE / WRITE_SIZE rows give roofline.traffic for C2.
@@ -315,6 +316,8 @@ def main():
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     per_pass = {}
     for r in recs:
+        if r.name.startswith("dense_"):
+            continue
         key = f"{r.name}_d{r.dim}"
         e = per_pass.setdefault(key, [0, 0.0, 0])
         e[0] += 1
@@ -323,6 +326,18 @@ def main():
     passes = {k: {"launches": v[0], "avg_ms": round(v[1] / v[0], 4),
                   "GBps": round(v[2] / (v[1] / 1e3) / 1e9, 1)} for k, v in per_pass.items()}
     log(f"passes: {json.dumps(passes)}")
+
+    dense = [r for r in recs if r.name.startswith("dense_")]
+    dense_ms = sum(r.ms() for r in dense)
+    dense_flops = sum(r.flops for r in dense)
+    dense_stats = None
+    if dense_ms > 0:
+        tf = dense_flops / (dense_ms / 1e3) / 1e12
+        dense_stats = {"ms_per_epoch": round(dense_ms / args.steps, 3),
+                       "tflops": round(tf, 1), "peak_tflops": FP32_MFMA_PEAK_TFLOPS,
+                       "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                       "tflop_per_epoch": round(dense_flops / args.steps / 1e12, 4)}
+        log(f"dense transform: {dense_stats}")
 
     traffic = None
     if args.config == "c2":
@@ -370,6 +385,7 @@ def main():
                      "kernel": (f"aggregate_units (GCN SpMM, D={cfg['hidden']}, fwd CSR + bwd CSC)"
                                 if cfg["model"] == "gcn" else
                                 f"GAT attention fwd+bwd kernels, H*C={cfg['hidden']}")},
+        "dense_mfma": dense_stats,
         "cpu_baseline": cpu,
         "passes": passes,
     }

@@ -29,13 +29,15 @@ class KernelRecord:
     dim: int
     start: "torch.cuda.Event"
     end: "torch.cuda.Event"
+    flops: int = 0
 
     def ms(self) -> float:
         return self.start.elapsed_time(self.end)
 
 
 class KernelTimer:
-    """Records HIP events around every aggregation pass while active.
+    """Records HIP events around every aggregation pass (and, as "dense_*"
+    regions with their flop counts, every dense product) while active.
 
     Events are recorded on the stream the kernels are launched on (the
     current stream), so elapsed times are the passes' device durations.
@@ -61,7 +63,7 @@ class KernelTimer:
 
     @staticmethod
     @contextlib.contextmanager
-    def region(name: str, nbytes: int, edges: int, dim: int):
+    def region(name: str, nbytes: int, edges: int, dim: int, flops: int = 0):
         timer = KernelTimer.active
         if timer is None:
             yield
@@ -71,7 +73,12 @@ class KernelTimer:
         start.record()
         yield
         end.record()
-        timer.records.append(KernelRecord(name, nbytes, edges, dim, start, end))
+        timer.records.append(KernelRecord(name, nbytes, edges, dim, start, end, flops))
+
+
+def dense_region(name: str, rows: int, k: int, n: int):
+    """Timer region of a dense product of 2 * rows * k * n flops."""
+    return KernelTimer.region("dense_" + name, 0, 0, n, 2 * rows * k * n)
 
 
 def _check_device_tensor(name: str, t: Tensor) -> None:
@@ -175,7 +182,8 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
         dp = (d + 3) // 4 * 4
         x = x.contiguous()
         wp = pad(weight, (0, 0, 0, dp - d))
-        z = torch.mm(x, wp.t())
+        with dense_region("fwd", x.size(0), x.size(1), dp):
+            z = torch.mm(x, wp.t())
         bp = pad(bias, (0, dp - d)).contiguous() if bias is not None else None
         y = spmm(plan.fwd, plan.idx, plan.val, z, plan.num_dst, bp, name="gcn_fwd")
         ctx.save_for_backward(x, wp)
@@ -194,8 +202,13 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
         d, dp = ctx.d, wp.size(0)
         gyp = pad(gy, (0, dp - d)).contiguous()
         dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gyp, plan.num_src, name="gcn_bwd")
-        dx = torch.mm(dz, wp) if ctx.needs_input_grad[0] else None
-        dw = gemm_tn(dz, x)[:d] if ctx.needs_input_grad[1] else None
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            with dense_region("dx", dz.size(0), dp, wp.size(1)):
+                dx = torch.mm(dz, wp)
+        if ctx.needs_input_grad[1]:
+            with dense_region("dw", dz.size(0), dp, x.size(1)):
+                dw = gemm_tn(dz, x)[:d]
         db = column_sum(gyp)[:d] if (ctx.has_bias and ctx.needs_input_grad[2]) else None
         return dx, dw, db, None
 

@@ -72,11 +72,13 @@ class _Linear(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+        from grinnder_amd.aggregation import dense_region
         x2 = x.reshape(-1, x.size(-1))
-        if bias is not None:
-            y = torch.addmm(bias, x2, weight.t())
-        else:
-            y = torch.mm(x2, weight.t())
+        with dense_region("fwd", x2.size(0), x2.size(1), weight.size(0)):
+            if bias is not None:
+                y = torch.addmm(bias, x2, weight.t())
+            else:
+                y = torch.mm(x2, weight.t())
         ctx.save_for_backward(x2, weight)
         ctx.in_shape = x.shape
         ctx.has_bias = bias is not None
@@ -84,13 +86,17 @@ class _Linear(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gy: Tensor):
+        from grinnder_amd.aggregation import dense_region
         x2, weight = ctx.saved_tensors
         gy2 = gy.reshape(-1, weight.size(0)).contiguous()
         dx = dw = db = None
+        rows, dout, din = gy2.size(0), weight.size(0), weight.size(1)
         if ctx.needs_input_grad[0]:
-            dx = torch.mm(gy2, weight).reshape(ctx.in_shape)
+            with dense_region("dx", rows, dout, din):
+                dx = torch.mm(gy2, weight).reshape(ctx.in_shape)
         if ctx.needs_input_grad[1]:
-            dw = gemm_tn(gy2, x2)
+            with dense_region("dw", rows, dout, din):
+                dw = gemm_tn(gy2, x2)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             from grinnder_amd.aggregation import column_sum
             db = column_sum(gy2)
@@ -172,10 +178,12 @@ class _LinearLNAct(torch.autograd.Function):
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         b = bias.contiguous() if bias is not None else None
         g, bt = gamma.contiguous(), beta.contiguous()
-        _lib.call("gr_linear_ln_act", x.data_ptr(), x.stride(0), rows, din, wt.data_ptr(), dout,
-                  _lib.ptr(b), g.data_ptr(), bt.data_ptr(), float(eps), _lib.ACTIVATIONS[act],
-                  h.data_ptr(), out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
-                  _lib.stream_handle())
+        from grinnder_amd.aggregation import dense_region
+        with dense_region("fwd_ln", rows, din, dout):
+            _lib.call("gr_linear_ln_act", x.data_ptr(), x.stride(0), rows, din, wt.data_ptr(),
+                      dout, _lib.ptr(b), g.data_ptr(), bt.data_ptr(), float(eps),
+                      _lib.ACTIVATIONS[act], h.data_ptr(), out.data_ptr(), mean.data_ptr(),
+                      rstd.data_ptr(), _lib.stream_handle())
         ctx.save_for_backward(x, w, h, mean, rstd, g, bt)
         ctx.has_bias = bias is not None
         ctx.act = act
@@ -183,12 +191,18 @@ class _LinearLNAct(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gout: Tensor):
-        from grinnder_amd.aggregation import ln_act_backward
+        from grinnder_amd.aggregation import dense_region, ln_act_backward
         x, w, h, mean, rstd, g, bt = ctx.saved_tensors
         gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias,
                                                 ctx.act)
-        dx = torch.mm(gh, w) if ctx.needs_input_grad[0] else None
-        dw = gemm_tn(gh, x) if ctx.needs_input_grad[1] else None
+        dx = dw = None
+        rows, din, dout = x.size(0), x.size(1), w.size(0)
+        if ctx.needs_input_grad[0]:
+            with dense_region("dx", rows, dout, din):
+                dx = torch.mm(gh, w)
+        if ctx.needs_input_grad[1]:
+            with dense_region("dw", rows, dout, din):
+                dw = gemm_tn(gh, x)
         return dx, dw, db, dgamma, dbeta, None, None
 
 
