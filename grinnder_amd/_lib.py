@@ -58,6 +58,8 @@ _SIGNATURES = {
     "gr_gat_softmax_stats": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_aggregate": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _i64, _i64, _i64, _P, _P, _P,
                          _i64, _P, _i64, _P],
+    "gr_gat_forward": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _P, _i64, _i64, _i64, _P, _P, _P,
+                       _P, _P, _P, _i64, _P, _i64, _i64, _P],
     "gr_gat_backward_src": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,

@@ -326,22 +326,22 @@ class _GATAttention(torch.autograd.Function):
         den = torch.empty((B, H), dtype=torch.float32, device=dev)
         alpha = torch.empty((max(nnz, 1), H), dtype=torch.float32, device=dev)
         f = plan.fwd
-        ws = _workspace(f.n_slots, 2 * H, dev)
-        _lib.call("gr_gat_softmax_stats", f.units.data_ptr(), f.n_units,
-                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
-                  s.data_ptr(), d.data_ptr(), H, m.data_ptr(), den.data_ptr(), alpha.data_ptr(),
-                  _lib.ptr(ws), f.n_slots, stream)
         o = torch.empty((B, HC), dtype=torch.float32, device=dev)
-        fused_bias = concat or H == 1
+        fused_bias = (concat or H == 1) and bias is not None
         y = torch.empty((B, HC), dtype=torch.float32, device=dev) if fused_bias else None
-        b = bias.contiguous() if (bias is not None and fused_bias) else None
-        ws = _workspace(f.n_slots, HC, dev)
-        _lib.call("gr_gat_aggregate", f.units.data_ptr(), f.n_units,
+        b = bias.contiguous() if fused_bias else None
+        ws_width = (HC + 3) // 4 * 4 + (2 * H + 3) // 4 * 4
+        ws = _workspace(f.n_slots, ws_width, dev)
+        _lib.call("gr_gat_forward", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
-                  hs.data_ptr(), hs.stride(0), alpha.data_ptr(), B, H, C, _lib.ptr(b),
-                  o.data_ptr(), _lib.ptr(y), HC, _lib.ptr(ws), f.n_slots, stream)
+                  hs.data_ptr(), hs.stride(0), s.data_ptr(), d.data_ptr(), B, H, C, _lib.ptr(b),
+                  m.data_ptr(), den.data_ptr(), alpha.data_ptr(), o.data_ptr(), _lib.ptr(y), HC,
+                  _lib.ptr(ws), 0 if ws is None else ws.numel(), f.n_slots, stream)
         region.__exit__(None, None, None)
-        if not fused_bias:
+        if concat or H == 1:
+            if y is None:
+                y = o  # no bias: the output is O itself, also saved for the backward
+        else:
             y = o.view(B, H, C).mean(dim=1)
             if bias is not None:
                 y = y + bias

@@ -20,28 +20,22 @@
 // exp(v - m_k) with the unit's own max m_k, and after the split rows are
 // combined each unit rescales its edges in place,
 //   alpha = exp(v - m_k) * exp(m_k - m) / den     (exp(0) = 1 for whole rows),
-// so the aggregation (for one head: the GCN SpMM kernel with alpha as the
-// edge values) and the backward read alpha instead of re-deriving it.
+// so the aggregation and the backward read alpha instead of re-deriving it.
+// With one head the statistics, alpha and the aggregation run as one fused
+// pass per unit (gat_fwd_fused); several heads use the statistics kernel and
+// then gat_aggregate_kernel.
 #include <algorithm>
 #include <cfloat>
 
 #include "gr_internal.h"
+#include "wave.h"
 
 namespace gr_gat {
 
 constexpr int kMaxHeads = 16;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
+using gr_wave::wave_max;
+using gr_wave::wave_sum;
 
 __device__ __forceinline__ float leaky(float t) { return t > 0.f ? t : 0.2f * t; }
 
@@ -350,6 +344,278 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
   }
 }
 
+// ------------------------------------------------ fused forward, H = 1 --
+
+// One head: the edge softmax and the weighted aggregation in one pass per
+// plan unit (row i, edges [y, z), slot).
+//   Pass 1, lanes parallel over the unit's edges: m = max_e v_e and
+//   sum = sum_e exp(v_e - m); the first 64 edges keep (col, v) in registers.
+//   Pass 2, in 64-edge chunks: lane l forms the weight of edge l of the chunk,
+//   exp(v - m) / den for a whole row (den = sum + 1e-16) or the unscaled
+//   exp(v - m_k) of a split row's unit, stores it as alpha, and the wavefront
+//   aggregates the chunk's rows with column ids and weights taken from the
+//   owning lanes (readlane when the whole wavefront takes one edge, a
+//   cross-lane permute for G-lane edge slots).
+// Edges are assigned to slots and summed in the same order as in the GCN
+// SpMM kernel, so whole rows give the same bits as gr_gat_softmax_stats
+// followed by gr_gat_aggregate.  Split rows leave (acc_k, m_k, sum_k) in
+// their workspace slot for gat_fused_fixup.
+template <int VEC, int G, int NCH, int U>
+__global__ __launch_bounds__(256) void gat_fwd_fused(
+    const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
+    const float* __restrict__ hs, int64_t ldh, const float* __restrict__ s,
+    const float* __restrict__ d, int C, const float* __restrict__ bias, float* __restrict__ m,
+    float* __restrict__ den, float* __restrict__ alpha, float* __restrict__ o,
+    float* __restrict__ y, int64_t ldy, float* __restrict__ ws, int64_t ws_stride) {
+  constexpr int EPI = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = wave_id();
+  if (wid >= n_units) return;
+  const int4 w = units[wid];
+  const int slot = (EPI == 1) ? 0 : lane / G;
+  const int sub = (EPI == 1) ? lane : lane % G;
+  const int64_t i = w.x;
+  const int len = w.z - w.y;
+
+  int foff[NCH], fld[NCH];
+  bool fvalid[NCH];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    foff[ch] = (ch * G + sub) * VEC;
+    fvalid[ch] = foff[ch] < C;
+    fld[ch] = fvalid[ch] ? foff[ch] : C - VEC;
+  }
+
+  if (len <= 0) {
+    // A row without edges (never a split unit): m = 0, den = 1, O = 0.
+    if (lane == 0) {
+      m[i] = 0.f;
+      den[i] = 1.f;
+    }
+    if (slot != 0) return;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      if (!fvalid[ch]) continue;
+      float z[VEC];
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) z[q] = 0.f;
+      st<VEC>(o + i * C + foff[ch], z);
+      if (y != nullptr) {
+        if (bias != nullptr) ld<VEC>(bias + foff[ch], z);
+        st<VEC>(y + i * ldy + foff[ch], z);
+      }
+    }
+    return;
+  }
+
+  // Every load below is unconditional (indices clamped into the unit), so
+  // the compiler can wait for each one alone: lanes past the unit's end read
+  // its last edge and get weight 0.  The column ids of the first 64 edges and
+  // their logits go out first; vector loads return in issue order, so the
+  // statistics can run while the first iteration's row loads (issued next,
+  // independent of the statistics) are still in flight.  Later iterations
+  // reuse the same registers.
+  const float di = d[i];
+  const int c0 = idx[w.y + min(lane, len - 1)];
+  const float s0 = s[c0];
+  float r[U][NCH][VEC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int c;
+    if constexpr (EPI == 1) {
+      c = __builtin_amdgcn_readlane(c0, u);
+    } else {
+      c = __shfl(c0, u * EPI + slot, 64);
+    }
+    const float* row = hs + (int64_t)c * ldh;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) ld<VEC>(row + fld[ch], r[u][ch]);
+  }
+
+  // Pass 1.
+  const float v0 = lane < len ? leaky(s0 + di) : -FLT_MAX;
+  float mx = v0;
+  for (int b = w.y + 64; b < w.z; b += 64) {
+    const float v = leaky(s[idx[min(b + lane, w.z - 1)]] + di);
+    if (b + lane < w.z) mx = fmaxf(mx, v);
+  }
+  mx = wave_max(mx);
+  float sum = lane < len ? expf(v0 - mx) : 0.f;
+  for (int b = w.y + 64; b < w.z; b += 64) {
+    const float v = leaky(s[idx[min(b + lane, w.z - 1)]] + di);
+    if (b + lane < w.z) sum += expf(v - mx);
+  }
+  sum = wave_sum(sum);
+  const bool whole = w.w < 0;
+  const float dn = whole ? sum + 1e-16f : 1.f;
+
+  // Pass 2.  Stores wait until a chunk's row loads are consumed: on gfx9 a
+  // wait for a load also waits for every store issued before it.
+  float acc[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[ch][q] = 0.f;
+
+  for (int b = w.y; b < w.z; b += 64) {
+    const int n = min(64, w.z - b);
+    const bool ok = lane < n;
+    const bool first = b == w.y;
+    int cl;
+    float al;
+    if (first) {
+      cl = c0;
+      al = ok ? expf(v0 - mx) / dn : 0.f;
+    } else {
+      cl = idx[b + min(lane, n - 1)];
+      const float v = leaky(s[cl] + di);
+      al = ok ? expf(v - mx) / dn : 0.f;
+    }
+    for (int k = 0; k < n; k += EPI * U) {
+      int c[U];
+      float a[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if constexpr (EPI == 1) {
+          c[u] = __builtin_amdgcn_readlane(cl, k + u);
+          a[u] = __builtin_bit_cast(float,
+                                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, al), k + u));
+        } else {
+          const int t = k + u * EPI + slot;
+          c[u] = __shfl(cl, t, 64);
+          a[u] = __shfl(al, t, 64);
+        }
+      }
+      if (!(first && k == 0)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float* row = hs + (int64_t)c[u] * ldh;
+#pragma unroll
+          for (int ch = 0; ch < NCH; ++ch) ld<VEC>(row + fld[ch], r[u][ch]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a[u], r[u][ch][q], acc[ch][q]);
+    }
+    if (ok) alpha[b + lane] = al;
+  }
+
+  if (lane == 0) {
+    if (whole) {
+      m[i] = mx;
+      den[i] = dn;
+    } else {
+      float* stt = ws + (int64_t)w.w * ws_stride + ws_stride - 4;
+      stt[0] = mx;
+      stt[1] = sum;
+    }
+  }
+  if constexpr (EPI > 1) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[ch][q] = gr_wave::slot_sum<G>(acc[ch][q]);
+  }
+  if (slot != 0) return;
+  if (whole) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      if (!fvalid[ch]) continue;
+      st<VEC>(o + i * C + foff[ch], acc[ch]);
+      if (y != nullptr) {
+        float b[VEC];
+        if (bias != nullptr) {
+          ld<VEC>(bias + foff[ch], b);
+        } else {
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) b[q] = 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) b[q] += acc[ch][q];
+        st<VEC>(y + i * ldy + foff[ch], b);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+      if (fvalid[ch]) st<VEC>(ws + (int64_t)w.w * ws_stride + foff[ch], acc[ch]);
+  }
+}
+
+// Split rows of the fused forward: one workgroup per (split row, 256
+// features).  m = max_k m_k, den = sum_k sum_k exp(m_k - m) + 1e-16 and
+// O = sum_k acc_k exp(m_k - m) / den, in slot order.
+__global__ __launch_bounds__(256) void gat_fused_fixup(const int32_t* __restrict__ fix,
+                                                       const float* __restrict__ ws,
+                                                       int64_t ws_stride, int C,
+                                                       const float* __restrict__ bias,
+                                                       float* __restrict__ m,
+                                                       float* __restrict__ den,
+                                                       float* __restrict__ o,
+                                                       float* __restrict__ y, int64_t ldy) {
+  const int64_t r = blockIdx.x;
+  const int row = fix[3 * r + 0], first = fix[3 * r + 1], n = fix[3 * r + 2];
+  const float* stats = ws + ws_stride - 4;  // (m_k, sum_k) of slot k at stats[k * ws_stride]
+  float mx = -FLT_MAX;
+  for (int k = 0; k < n; ++k) mx = fmaxf(mx, stats[(int64_t)(first + k) * ws_stride]);
+  float sum = 0.f;
+  for (int k = 0; k < n; ++k) {
+    const float* st = stats + (int64_t)(first + k) * ws_stride;
+    sum += st[1] * expf(st[0] - mx);
+  }
+  const float dn = sum + 1e-16f;
+  const int f = blockIdx.y * 256 + threadIdx.x;
+  if (f < C) {
+    float acc = 0.f;
+    int k = 0;
+    for (; k + 4 <= n; k += 4) {
+      const float* p = ws + (int64_t)(first + k) * ws_stride;
+      const float a0 = p[f], a1 = p[ws_stride + f], a2 = p[2 * ws_stride + f],
+                  a3 = p[3 * ws_stride + f];
+      acc = fmaf(a0, expf(p[ws_stride - 4] - mx), acc);
+      acc = fmaf(a1, expf(p[2 * ws_stride - 4] - mx), acc);
+      acc = fmaf(a2, expf(p[3 * ws_stride - 4] - mx), acc);
+      acc = fmaf(a3, expf(p[4 * ws_stride - 4] - mx), acc);
+    }
+    for (; k < n; ++k) {
+      const float* p = ws + (int64_t)(first + k) * ws_stride;
+      acc = fmaf(p[f], expf(p[ws_stride - 4] - mx), acc);
+    }
+    acc /= dn;
+    o[(int64_t)row * C + f] = acc;
+    if (y != nullptr) y[(int64_t)row * ldy + f] = acc + (bias != nullptr ? bias[f] : 0.f);
+  }
+  if (blockIdx.y == 0 && threadIdx.x == 0) {
+    m[row] = mx;
+    den[row] = dn;
+  }
+}
+
+// Split units of the fused forward, one wavefront per unit, after the fixup:
+// alpha = exp(v - m_k) * exp(m_k - m) / den.  Launched over the first n_slots
+// units, which gr_spmm_plan fills with the split rows' units (unit k holds
+// slot k).
+__global__ __launch_bounds__(256) void gat_fused_alpha_split(const int4* __restrict__ units,
+                                                             int64_t n_split,
+                                                             const float* __restrict__ m,
+                                                             const float* __restrict__ den,
+                                                             const float* __restrict__ ws,
+                                                             int64_t ws_stride,
+                                                             float* __restrict__ alpha) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = wave_id();
+  if (wid >= n_split) return;
+  const int4 w = units[wid];
+  if (w.w < 0) return;
+  const float corr = expf(ws[(int64_t)w.w * ws_stride + ws_stride - 4] - m[w.x]);
+  const float dn = den[w.x];
+  for (int e = w.y + lane; e < w.z; e += 64) alpha[e] = (alpha[e] * corr) / dn;
+}
+
 // ----------------------------------------------------------- backward --
 
 // Column-parallel (CSC) pass over source rows j.  For each edge (i, j), with
@@ -370,12 +636,7 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 // takes 64 / G edges of the unit at once (slot `sub` takes edges sub,
 // sub + 64/G, ...); the slots' partial dHs_j and ds_j are combined in a fixed
 // butterfly order at the end.
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+using gr_wave::group_sum;
 
 template <int VEC, int NCH, int U, int G>
 __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
@@ -489,13 +750,10 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
   }
   // Combine the edge slots (no-op for G == 64).
 #pragma unroll
-  for (int off = G; off < 64; off <<= 1) {
+  for (int ch = 0; ch < NCH; ++ch) {
+    dsl[ch] = gr_wave::slot_sum<G>(dsl[ch]);
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      dsl[ch] += __shfl_xor(dsl[ch], off, 64);
-#pragma unroll
-      for (int q = 0; q < VEC; ++q) acc[ch][q] += __shfl_xor(acc[ch][q], off, 64);
-    }
+    for (int q = 0; q < VEC; ++q) acc[ch][q] = gr_wave::slot_sum<G>(acc[ch][q]);
   }
   if (sub != 0) return;
 
@@ -546,6 +804,150 @@ __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restri
     }
     dhs[(int64_t)row * HC + f] = fmaf(dsum, att_src[f], acc);
     if (f == h * C) ds[(int64_t)row * H + h] = dsum;
+  }
+}
+
+// One head: the same pass as gat_bwd_src_kernel with the per-edge scalars
+// batched.  For each 64-edge chunk of the unit, lane l loads edge l's
+// destination row, CSR position, alpha, d and cdot (two coalesced loads and
+// three gathers, all issued before the chunk's go-row loads), and the
+// wavefront takes them from the owning lane (readlane when the whole
+// wavefront works on one edge, a cross-lane permute for G-lane edge slots).
+// The chunk's gdd values are collected in lane l and stored once, after the
+// chunk's row loads have been consumed: on gfx9 a wait for a load also waits
+// for every store issued before it.  Edges are assigned to slots and summed
+// in the same order as in gat_bwd_src_kernel.
+template <int VEC, int G, int NCH, int U>
+__global__ __launch_bounds__(256) void gat_bwd_src_h1(
+    const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
+    const int32_t* __restrict__ perm, const float* __restrict__ hs, int64_t ldh,
+    const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
+    const float* __restrict__ alpha, const float* __restrict__ cdot,
+    const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
+    float* __restrict__ gt, float* __restrict__ ws) {
+  constexpr int EPI = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int slot = (EPI == 1) ? 0 : lane / G;
+  const int sub = (EPI == 1) ? lane : lane % G;
+  const int64_t wid = wave_id();
+  if (wid >= n_units) return;
+  const int4 w = units[wid];
+  const int64_t j = w.x;
+
+  int foff[NCH], fld[NCH];
+  bool fvalid[NCH];
+  float hsj[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    foff[ch] = (ch * G + sub) * VEC;
+    fvalid[ch] = foff[ch] < C;
+    fld[ch] = fvalid[ch] ? foff[ch] : C - VEC;
+    ld<VEC>(hs + j * ldh + fld[ch], hsj[ch]);
+    if (!fvalid[ch]) {
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) hsj[ch][q] = 0.f;
+    }
+  }
+  const float sj = s[j];
+  float acc[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[ch][q] = 0.f;
+  float dsl = 0.f;
+
+  for (int b = w.y; b < w.z; b += 64) {
+    const int n = min(64, w.z - b);
+    const int el = b + min(lane, n - 1);
+    const int il = row_idx[el];
+    const int pl = perm[el];
+    const float al = alpha[pl];
+    const float dl = d[il];
+    const float cl = cdot[il];
+    float gtv = 0.f;
+    for (int k = 0; k < n; k += EPI * U) {
+      int ii[U];
+      float a[U], dv[U], cv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if constexpr (EPI == 1) {
+          ii[u] = __builtin_amdgcn_readlane(il, k + u);
+          a[u] = __builtin_bit_cast(float,
+                                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, al), k + u));
+          dv[u] = __builtin_bit_cast(float,
+                                     __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k + u));
+          cv[u] = __builtin_bit_cast(float,
+                                     __builtin_amdgcn_readlane(__builtin_bit_cast(int, cl), k + u));
+        } else {
+          const int t = k + u * EPI + slot;
+          ii[u] = __shfl(il, t, 64);
+          a[u] = __shfl(al, t, 64);
+          dv[u] = __shfl(dl, t, 64);
+          cv[u] = __shfl(cl, t, 64);
+        }
+      }
+      float g[U][NCH][VEC];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) ld<VEC>(go + (int64_t)ii[u] * C + fld[ch], g[u][ch]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float t = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) t = fmaf(g[u][ch][q], hsj[ch][q], t);
+        const float ga = gr_wave::group_sum<G>(t);
+        const float ge = a[u] * (ga - cv[u]);
+        const bool pos = sj + dv[u] > 0.f;
+        const int te = k + u * EPI + slot;  // this slot's edge in the chunk
+        if (te < n) {
+          dsl += pos ? ge : 0.2f * ge;
+#pragma unroll
+          for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a[u], g[u][ch][q], acc[ch][q]);
+        }
+        const float gv = pos ? 0.f : -0.8f * ge;
+        // Lane k + u * EPI + s collects the value of slot s.
+        const int src = lane - k - u * EPI;
+        if constexpr (EPI == 1) {
+          if (src == 0) gtv = gv;
+        } else {
+          const float v = __shfl(gv, (src & (EPI - 1)) * G, 64);
+          if (src >= 0 && src < EPI) gtv = v;
+        }
+      }
+    }
+    if (lane < n) gt[pl] = gtv;
+  }
+
+  dsl = gr_wave::slot_sum<G>(dsl);
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[ch][q] = gr_wave::slot_sum<G>(acc[ch][q]);
+  if (slot != 0) return;
+  if (w.w < 0) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      if (!fvalid[ch]) continue;
+      float av[VEC];
+      ld<VEC>(att_src + foff[ch], av);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) av[q] = fmaf(dsl, av[q], acc[ch][q]);
+      st<VEC>(dhs + j * C + foff[ch], av);
+    }
+    if (lane == 0) ds[j] = dsl;
+  } else {
+    // Slot layout [acc (C) | ds], each part padded to 4 floats.
+    const int c4 = ((C + 3) / 4) * 4;
+    float* p = ws + (int64_t)w.w * (c4 + 4);
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+      if (fvalid[ch]) st<VEC>(p + foff[ch], acc[ch]);
+    if (lane == 0) p[c4] = dsl;
   }
 }
 
@@ -747,7 +1149,11 @@ extern "C" int gr_gat_aggregate(const int32_t* units, int64_t n_units, const int
              "gat_aggregate: NULL or misaligned pointer");
   hipStream_t st = gr::as_stream(stream);
   const int H = (int)heads, C = (int)channels;
-  if (H == 1) {
+  // The GCN kernel takes rows of up to 256 vectors: any C <= 256, wider rows
+  // only as float4 vectors.
+  const bool gcn_ok = C <= 256 || (C % 4 == 0 && aligned16(hs) && ldh % 4 == 0 && aligned16(o) &&
+                                   (workspace == nullptr || aligned16(workspace)));
+  if (H == 1 && gcn_ok) {
     // One head: O = A_alpha Hs is the GCN SpMM with alpha as edge values.
     rc = gr_gcn_aggregate(units, n_units, fixups, n_fix, idx, alpha, hs, ldh, o, HC, nullptr,
                           n_dst, HC, workspace, n_slots, stream);
@@ -788,6 +1194,106 @@ extern "C" int gr_gat_aggregate(const int32_t* units, int64_t n_units, const int
   return GR_OK;
 }
 
+template <int VEC, int G, int NCH>
+static hipError_t launch_fused(hipStream_t st, const int4* units, int64_t n_units,
+                               const int32_t* idx, const float* hs, int64_t ldh, const float* s,
+                               const float* d, int C, const float* bias, float* m, float* den,
+                               float* alpha, float* o, float* y, int64_t ldy, float* ws,
+                               int64_t ws_stride) {
+  constexpr int EPI = 64 / G;
+  constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
+  hipLaunchKernelGGL((gat_fwd_fused<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
+                     st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha, o, y, ldy,
+                     ws, ws_stride);
+  return hipGetLastError();
+}
+
+template <int VEC>
+static hipError_t dispatch_fused(int chunks, hipStream_t st, const int4* units, int64_t n_units,
+                                 const int32_t* idx, const float* hs, int64_t ldh,
+                                 const float* s, const float* d, int C, const float* bias,
+                                 float* m, float* den, float* alpha, float* o, float* y,
+                                 int64_t ldy, float* ws, int64_t ws_stride) {
+#define GR_FU(G, N)                                                                       \
+  return launch_fused<VEC, G, N>(st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, \
+                                 alpha, o, y, ldy, ws, ws_stride)
+  if (chunks <= 8) GR_FU(8, 1);
+  if (chunks <= 16) GR_FU(16, 1);
+  if (chunks <= 32) GR_FU(32, 1);
+  if (chunks <= 64) GR_FU(64, 1);
+  if (chunks <= 128) GR_FU(64, 2);
+  GR_FU(64, 4);
+#undef GR_FU
+}
+
+extern "C" int gr_gat_forward(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                              int64_t n_fix, const int32_t* idx, const float* hs, int64_t ldh,
+                              const float* s, const float* d, int64_t n_dst, int64_t heads,
+                              int64_t channels, const float* bias, float* m, float* den,
+                              float* alpha, float* o, float* y, int64_t ldy, float* workspace,
+                              int64_t ws_floats, int64_t n_slots, void* stream) {
+  gr::clear_error();
+  int rc = check_heads(heads, channels);
+  if (rc) return rc;
+  const int64_t HC = heads * channels;
+  GR_REQUIRE(n_units >= 0 && n_fix >= 0 && n_slots >= 0 && n_dst >= 0,
+             "gat_forward: negative extent");
+  GR_REQUIRE(ldh >= HC && (y == nullptr || ldy >= HC), "gat_forward: bad leading dims");
+  const int64_t hc4 = (HC + 3) / 4 * 4;
+  const int64_t need = n_slots * (hc4 + (2 * heads + 3) / 4 * 4);
+  GR_REQUIRE(n_fix == 0 || (fixups && workspace && ws_floats >= need),
+             "gat_forward: workspace of %lld floats, %lld needed",
+             (long long)ws_floats, (long long)need);
+  if (n_units == 0) return GR_OK;
+  GR_REQUIRE(units && aligned16(units) && idx && hs && s && d && m && den && alpha && o,
+             "gat_forward: NULL or misaligned pointer");
+  hipStream_t st = gr::as_stream(stream);
+  if (heads > 1) {
+    // Several heads: statistics, then the aggregation.
+    rc = gr_gat_softmax_stats(units, n_units, fixups, n_fix, idx, s, d, heads, m, den, alpha,
+                              workspace, n_slots, stream);
+    if (rc) return rc;
+    return gr_gat_aggregate(units, n_units, fixups, n_fix, idx, hs, ldh, alpha, n_dst, heads,
+                            channels, bias, o, y, ldy, workspace, n_slots, stream);
+  }
+  const int C = (int)channels;
+  const bool al = aligned16(hs) && ldh % 4 == 0 && aligned16(o) &&
+                  (y == nullptr || (aligned16(y) && ldy % 4 == 0)) &&
+                  (bias == nullptr || aligned16(bias)) &&
+                  (workspace == nullptr || aligned16(workspace));
+  const int vec = (C % 4 == 0 && al) ? 4 : 1;
+  const int chunks = (C + vec - 1) / vec;
+  const int64_t ws_stride = hc4 + 4;
+  const int4* u4 = reinterpret_cast<const int4*>(units);
+  hipError_t err;
+  if (vec == 4) {
+    err = dispatch_fused<4>(chunks, st, u4, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha,
+                            o, y, ldy, workspace, ws_stride);
+  } else if (chunks <= 256) {
+    err = dispatch_fused<1>(chunks, st, u4, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha,
+                            o, y, ldy, workspace, ws_stride);
+  } else {
+    // Unaligned rows wider than 256 floats: statistics, then the aggregation.
+    rc = gr_gat_softmax_stats(units, n_units, fixups, n_fix, idx, s, d, 1, m, den, alpha,
+                              workspace, n_slots, stream);
+    if (rc) return rc;
+    return gr_gat_aggregate(units, n_units, fixups, n_fix, idx, hs, ldh, alpha, n_dst, 1,
+                            channels, bias, o, y, ldy, workspace, n_slots, stream);
+  }
+  GR_HIP_CHECK(err);
+  if (n_fix > 0) {
+    GR_REQUIRE(n_fix <= INT32_MAX && n_slots <= n_units, "gat_forward: inconsistent plan");
+    hipLaunchKernelGGL(gat_fused_fixup, dim3((unsigned)n_fix, (unsigned)((C + 255) / 256)),
+                       dim3(256), 0, st, fixups, workspace, ws_stride, C, bias, m, den, o, y,
+                       ldy);
+    GR_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(gat_fused_alpha_split, dim3(blocks_for(n_slots)), dim3(256), 0, st, u4,
+                       n_slots, m, den, workspace, ws_stride, alpha);
+    GR_HIP_CHECK(hipGetLastError());
+  }
+  return GR_OK;
+}
+
 template <int VEC, int NCH, int G = 64>
 static hipError_t launch_gat_bwd(hipStream_t st, const int4* units, int64_t n_units,
                                  const int32_t* row_idx, const int32_t* perm, const float* hs,
@@ -799,6 +1305,39 @@ static hipError_t launch_gat_bwd(hipStream_t st, const int4* units, int64_t n_un
                      st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src,
                      H, C, dhs, ds, gt, ws);
   return hipGetLastError();
+}
+
+template <int VEC, int G, int NCH>
+static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_units,
+                                const int32_t* row_idx, const int32_t* perm, const float* hs,
+                                int64_t ldh, const float* go, const float* s, const float* d,
+                                const float* alpha, const float* cdot, const float* att_src,
+                                int C, float* dhs, float* ds, float* gt, float* ws) {
+  constexpr int EPI = 64 / G;
+  constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
+  hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
+                     st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src,
+                     C, dhs, ds, gt, ws);
+  return hipGetLastError();
+}
+
+template <int VEC>
+static hipError_t dispatch_bwd_h1(int chunks, hipStream_t st, const int4* units,
+                                  int64_t n_units, const int32_t* row_idx, const int32_t* perm,
+                                  const float* hs, int64_t ldh, const float* go, const float* s,
+                                  const float* d, const float* alpha, const float* cdot,
+                                  const float* att_src, int C, float* dhs, float* ds, float* gt,
+                                  float* ws) {
+#define GR_BH(G, N)                                                                      \
+  return launch_bwd_h1<VEC, G, N>(st, units, n_units, row_idx, perm, hs, ldh, go, s, d,  \
+                                  alpha, cdot, att_src, C, dhs, ds, gt, ws)
+  if (chunks <= 8) GR_BH(8, 1);
+  if (chunks <= 16) GR_BH(16, 1);
+  if (chunks <= 32) GR_BH(32, 1);
+  if (chunks <= 64) GR_BH(64, 1);
+  if (chunks <= 128) GR_BH(64, 2);
+  GR_BH(64, 4);
+#undef GR_BH
 }
 
 extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const int32_t* fixups,
@@ -827,7 +1366,14 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   const int H = (int)heads, C = (int)channels;
   hipError_t err;
   const int64_t chunks = (HC + vec - 1) / vec;
-  if (H == 1 && chunks <= 32) {
+  if (H == 1 && chunks <= 256) {
+    if (vec == 4)
+      err = dispatch_bwd_h1<4>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
+                               alpha, cdot, att_src, C, dhs, ds, gt, workspace);
+    else
+      err = dispatch_bwd_h1<1>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
+                               alpha, cdot, att_src, C, dhs, ds, gt, workspace);
+  } else if (H == 1 && chunks <= 32) {
     // Narrow single-head rows: several edges per wavefront.
     if (vec == 4) {
       if (chunks <= 8) err = launch_gat_bwd<4, 1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);

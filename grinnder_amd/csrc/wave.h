@@ -1,0 +1,77 @@
+// Cross-lane sums and maxima of a 64-lane gfx950 wavefront without the LDS
+// crossbar: DPP within rows of 16 lanes (quad_perm, row_half_mirror,
+// row_mirror, row_ror:8) and the gfx950 v_permlane16_swap /
+// v_permlane32_swap across rows.  Each step combines a lane with its partner
+// by a commutative operation, so every lane of a group ends with the same
+// bits, and the order is fixed, so results do not vary between runs.
+//
+// Call these with all 64 lanes active (uniform control flow).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace gr_wave {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Value of lane ^ 16 (rows 0 <-> 1, 2 <-> 3), through v_permlane16_swap.
+__device__ __forceinline__ float xor16(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  // r[0] holds rows (0, 0, 2, 2) and r[1] rows (1, 1, 3, 3) of x.
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+
+// Value of lane ^ 32, through v_permlane32_swap.
+__device__ __forceinline__ float xor32(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  // r[0] holds halves (0, 0) and r[1] halves (1, 1) of x.
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// Sum over aligned groups of G consecutive lanes (G a power of two, 1..64);
+// every lane of a group gets the group's sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G must be a power of two <= 64");
+  if constexpr (G >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (G >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (G >= 8) v += dpp<0x141>(v);  // row_half_mirror: the other quad
+  if constexpr (G >= 16) v += dpp<0x140>(v); // row_mirror: the other half-row
+  if constexpr (G >= 32) v += xor16(v);
+  if constexpr (G >= 64) v += xor32(v);
+  return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G must be a power of two <= 64");
+  if constexpr (G >= 2) v = fmaxf(v, dpp<0xB1>(v));
+  if constexpr (G >= 4) v = fmaxf(v, dpp<0x4E>(v));
+  if constexpr (G >= 8) v = fmaxf(v, dpp<0x141>(v));
+  if constexpr (G >= 16) v = fmaxf(v, dpp<0x140>(v));
+  if constexpr (G >= 32) v = fmaxf(v, xor16(v));
+  if constexpr (G >= 64) v = fmaxf(v, xor32(v));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
+
+// Sum over the lanes that share lane % G (the 64 / G edge slots of G lanes
+// each, G in 8..64); every such lane gets the sum.
+template <int G>
+__device__ __forceinline__ float slot_sum(float v) {
+  static_assert(G >= 8 && G <= 64 && (G & (G - 1)) == 0, "G must be 8, 16, 32 or 64");
+  if constexpr (G <= 8) v += dpp<0x128>(v);  // row_ror:8 = lane ^ 8 within a row
+  if constexpr (G <= 16) v += xor16(v);
+  if constexpr (G <= 32) v += xor32(v);
+  return v;
+}
+
+}  // namespace gr_wave

@@ -116,7 +116,11 @@ class GATConv(Module):
             state_dict.pop(prefix + "lin_dst.weight", None)
         super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
 
-    def forward(self, x: Union[Tensor, Tuple[Tensor, Tensor]], adj: Adjacency) -> Tensor:
+    def forward(self, x: Union[Tensor, Tuple[Tensor, Tensor]], adj: Adjacency,
+                add_bias: bool = True) -> Tensor:
+        """add_bias=False leaves the bias out of the output, for a caller that
+        adds it in a fused epilogue (the LayerNorm of GAT.forward_layer)."""
+        bias = self.bias if add_bias else None
         num_dst = adj.sparse_sizes()[0]
         if isinstance(x, tuple):
             x_src, x_dst = x
@@ -136,12 +140,12 @@ class GATConv(Module):
             w = F.pad(self.lin.weight, (0, 0, 0, pad))
             a_s = F.pad(self.att_src, (0, pad))
             a_d = F.pad(self.att_dst, (0, pad))
-            b = F.pad(self.bias, (0, pad)) if self.bias is not None else None
+            b = F.pad(bias, (0, pad)) if bias is not None else None
             hs = linear(x_src, w)
             y = gat_attention(hs, adj, a_s, a_d, b, 1, self.out_channels + pad, self.concat)
             return y[:, :self.out_channels]
         hs = linear(x_src, self.lin.weight)
-        return gat_attention(hs, adj, self.att_src, self.att_dst, self.bias, self.heads,
+        return gat_attention(hs, adj, self.att_src, self.att_dst, bias, self.heads,
                              self.out_channels, self.concat)
 
     def __repr__(self) -> str:

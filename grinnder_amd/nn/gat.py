@@ -41,15 +41,20 @@ class GAT(GriNNderModel):
     def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
         x = F.dropout(x, p=self.dropout, training=self.training)
         num_dst = adj.sparse_sizes()[0]
-        x = self.convs[layer]((x, x[:num_dst]), adj)
+        conv = self.convs[layer]
+        if layer < self.num_layers - 1 and self.norms is not None:
+            norm = self.norms[layer]
+            if (x.is_cuda and norm.elementwise_affine and norm.bias is not None
+                    and tuple(norm.normalized_shape) == (conv.out_channels * conv.heads,)
+                    and conv.concat):
+                # The conv bias, LayerNorm and ELU in one pass over the
+                # attention output.
+                x = conv((x, x[:num_dst]), adj, add_bias=False)
+                return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
+        x = conv((x, x[:num_dst]), adj)
         if layer < self.num_layers - 1:
             if self.norms is not None:
-                norm = self.norms[layer]
-                if (x.is_cuda and norm.elementwise_affine and norm.bias is not None
-                        and tuple(norm.normalized_shape) == (x.size(-1),)):
-                    # LayerNorm + ELU in one pass over the attention output.
-                    return bias_ln_act(x, None, norm.weight, norm.bias, norm.eps, "elu")
-                x = norm(x)
+                x = self.norms[layer](x)
             x = F.elu(x)
         return x
 

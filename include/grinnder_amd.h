@@ -363,6 +363,24 @@ int gr_gat_aggregate(const int32_t* units, int64_t n_units,
                      const float* bias, float* o, float* y, int64_t ldy,
                      float* workspace, int64_t n_slots, void* stream);
 
+/* The whole attention forward after the scores: edge softmax (m, den, alpha
+ * as gr_gat_softmax_stats) and O = sum_e alpha Hs[idx[e]] into o [n_dst, H*C],
+ * plus Y = O + bias into y when y is not NULL (bias may be NULL).  One head
+ * runs as one fused pass per plan unit (the softmax statistics, the weights
+ * and the weighted row sums together); whole rows give the same bits as
+ * gr_gat_softmax_stats followed by gr_gat_aggregate.  Several heads run those
+ * two.  units / fixups as gr_spmm_plan lays them out (split rows' units first,
+ * unit k holding slot k).
+ * workspace: ws_floats >= n_slots * (round_up(H*C, 4) + round_up(2H, 4)).
+ * Replaces the attention / softmax / propagate sequence of PyG GATConv as
+ * grinnder/nn/gat.py:54-61,73 calls it. */
+int gr_gat_forward(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                   int64_t n_fix, const int32_t* idx, const float* hs, int64_t ldh,
+                   const float* s, const float* d, int64_t n_dst, int64_t heads,
+                   int64_t channels, const float* bias, float* m, float* den,
+                   float* alpha, float* o, float* y, int64_t ldy, float* workspace,
+                   int64_t ws_floats, int64_t n_slots, void* stream);
+
 /* Backward over source rows j (CSC plan, row_idx/perm from
  * gr_csr_transpose; alpha [nnz, H] in CSR order from gr_gat_softmax_stats).
  * go = dL/dO [B, H*C]; cdot[i,h] = <go_i,h, O_i,h>.

@@ -70,3 +70,111 @@ def test_gat_deterministic(gpu):
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0])
     assert torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("C,long_len,seg", [(256, 1200, 512), (19, 700, 256), (3, 300, 128),
+                                            (64, 2000, 512), (300, 900, 512), (301, 600, 512),
+                                            (1024, 0, 512)])
+def test_gat_forward_fused_matches_two_pass(gpu, C, long_len, seg):
+    """gr_gat_forward (one fused pass for one head) against gr_gat_softmax_stats
+    + gr_gat_aggregate through the C ABI: m, den, alpha and O bit-identical on
+    whole rows; split rows (combined with rescaled partials) within TOL."""
+    from grinnder_amd import _lib
+    B, E = 300, 420
+    print(f"case C={C} long_len={long_len} seg={seg}", flush=True)
+    rowptr, col, val = random_bipartite(B, E, 9, seed=C, long_rows=3 if long_len else 0,
+                                        long_len=long_len)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=seg)
+    plan = adj.device_plan(gpu)
+    f = plan.fwd
+    g = torch.Generator().manual_seed(C)
+    hs = torch.randn(E, C, generator=g).to(gpu)
+    s = (torch.randn(E, 1, generator=g) * 2).to(gpu)
+    d = (torch.randn(B, 1, generator=g) * 2).to(gpu)
+    bias = torch.randn(C, generator=g).to(gpu)
+    nnz = plan.nnz
+    st = _lib.stream_handle()
+    fixp = f.fixups.data_ptr() if f.n_fix else None
+    c4 = (C + 3) // 4 * 4
+    outs = []
+    for fused in (False, True):
+        m = torch.full((B, 1), float("nan"), device=gpu)
+        den = torch.full((B, 1), float("nan"), device=gpu)
+        alpha = torch.full((max(nnz, 1), 1), float("nan"), device=gpu)
+        o = torch.full((B, C), float("nan"), device=gpu)
+        y = torch.full((B, C), float("nan"), device=gpu)
+        ws = torch.empty(max(1, f.n_slots) * (c4 + 4), device=gpu)
+        if fused:
+            _lib.call("gr_gat_forward", f.units.data_ptr(), f.n_units, fixp, f.n_fix,
+                      plan.idx.data_ptr(), hs.data_ptr(), C, s.data_ptr(), d.data_ptr(), B, 1, C,
+                      bias.data_ptr(), m.data_ptr(), den.data_ptr(), alpha.data_ptr(),
+                      o.data_ptr(), y.data_ptr(), C, ws.data_ptr(), ws.numel(), f.n_slots, st)
+        else:
+            _lib.call("gr_gat_softmax_stats", f.units.data_ptr(), f.n_units, fixp, f.n_fix,
+                      plan.idx.data_ptr(), s.data_ptr(), d.data_ptr(), 1, m.data_ptr(),
+                      den.data_ptr(), alpha.data_ptr(), ws.data_ptr(), f.n_slots, st)
+            _lib.call("gr_gat_aggregate", f.units.data_ptr(), f.n_units, fixp, f.n_fix,
+                      plan.idx.data_ptr(), hs.data_ptr(), C, alpha.data_ptr(), B, 1, C,
+                      bias.data_ptr(), o.data_ptr(), y.data_ptr(), C, ws.data_ptr(), f.n_slots,
+                      st)
+        torch.cuda.synchronize()
+        outs.append([t.cpu() for t in (m, den, alpha[:nnz], o, y)])
+    deg = rowptr[1:] - rowptr[:-1]
+    split = deg > seg
+    edge_split = torch.repeat_interleave(split, deg)
+    assert (f.n_fix > 0) == bool(split.any())
+    (m0, den0, a0, o0, y0), (m1, den1, a1, o1, y1) = outs
+    for t in (m1, den1, a1, o1, y1):
+        assert not torch.isnan(t).any()
+    whole = ~split
+    assert torch.equal(m0[whole], m1[whole]) and torch.equal(den0[whole], den1[whole])
+    assert torch.equal(a0[~edge_split], a1[~edge_split])
+    assert torch.equal(o0[whole], o1[whole]) and torch.equal(y0[whole], y1[whole])
+    # Split rows: the same statistics formula, O from rescaled partial sums.
+    assert torch.equal(m0[split], m1[split]) and torch.equal(den0[split], den1[split])
+    assert max_abs_norm_err(a1[edge_split], a0[edge_split].double()) <= TOL
+    assert max_abs_norm_err(o1, o0.double()) <= TOL
+    assert max_abs_norm_err(y1, y0.double()) <= TOL
+    # Rows without edges: m = 0, den = 1, O = 0, Y = bias.
+    empty = deg == 0
+    assert bool(empty.any())
+    assert torch.equal(m1[empty], torch.zeros(int(empty.sum()), 1))
+    assert torch.equal(den1[empty], torch.ones(int(empty.sum()), 1))
+    assert torch.equal(o1[empty], torch.zeros(int(empty.sum()), C))
+    assert torch.equal(y1[empty], bias.cpu().expand(int(empty.sum()), C))
+
+
+@pytest.mark.parametrize("H,C", [(1, 256), (1, 20), (1, 7), (2, 16)])
+def test_gat_hub_source_matches_oracle(gpu, H, C):
+    """A source column shared by most destination rows (an R-MAT hub):
+    its CSC column is longer than the segment length, so the backward's
+    split-column fixup runs, next to short columns."""
+    print(f"case hub H={H} C={C}", flush=True)
+    B, E = 900, 1500
+    rowptr, col, val = random_bipartite(B, E, 6, seed=C + H, long_rows=1, long_len=700)
+    rows = torch.repeat_interleave(torch.arange(B), rowptr[1:] - rowptr[:-1])
+    g = torch.Generator().manual_seed(3)
+    hub = (torch.rand(col.numel(), generator=g) < 0.5) & (rows % 3 != 0)
+    col = torch.where(hub, torch.full_like(col, 11), col)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=128)
+    assert int((col == 11).sum()) > 128
+    hs = torch.randn(E, H * C, generator=g)
+    att_src = torch.randn(1, H, C, generator=g) * 0.5
+    att_dst = torch.randn(1, H, C, generator=g) * 0.5
+    bias = torch.randn(H * C, generator=g)
+    gy = torch.randn(B, H * C, generator=g)
+    hs_d = hs.to(gpu).requires_grad_(True)
+    as_d = att_src.to(gpu).requires_grad_(True)
+    ad_d = att_dst.to(gpu).requires_grad_(True)
+    b_d = bias.to(gpu).requires_grad_(True)
+    y = gat_attention(hs_d, adj, as_d, ad_d, b_d, H, C, True)
+    y.backward(gy.to(gpu))
+    torch.cuda.synchronize()
+    ref_y, alpha, tpre = oracle.gat_forward(rowptr, col, hs, H, C, att_src, att_dst, bias, True)
+    dhs, das, dad, db = oracle.gat_backward(rowptr, col, hs, H, C, att_src, att_dst, True,
+                                            alpha, tpre, gy)
+    assert max_abs_norm_err(y.detach(), ref_y) <= TOL
+    assert max_abs_norm_err(hs_d.grad, dhs) <= TOL
+    assert max_abs_norm_err(as_d.grad.reshape(-1), das) <= TOL
+    assert max_abs_norm_err(ad_d.grad.reshape(-1), dad) <= TOL
+    assert max_abs_norm_err(b_d.grad, db) <= TOL
