@@ -366,8 +366,10 @@ class _GATAttention(torch.autograd.Function):
         else:
             go = (gy / H).unsqueeze(1).expand(B, H, C).reshape(B, HC).contiguous()
         db = column_sum(gy) if ctx.has_bias else None
-        cdot = (go.view(B, H, C) * o.view(B, H, C)).sum(-1).contiguous()
         stream = _lib.stream_handle()
+        cdot = torch.empty((B, H), dtype=torch.float32, device=dev)
+        _lib.call("gr_gat_row_dot", go.data_ptr(), go.stride(0), o.data_ptr(), o.stride(0), B,
+                  H, C, cdot.data_ptr(), stream)
         nnz = plan.nnz
         region = KernelTimer.region(
             "gat_bwd", nnz * (8 * HC + 16 * H + 8) + E * (4 * HC + 4 * H) + B * (4 * HC + 4 * H),

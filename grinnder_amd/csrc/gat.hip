@@ -126,6 +126,58 @@ __global__ __launch_bounds__(256) void gat_scores_kernel(const float* __restrict
   }
 }
 
+// cdot[i,h] = <a[i,h,:], b[i,h,:]> (the backward's c_i = <GO_i, O_i>): the
+// same row walk as the scores kernel with a second row in place of the
+// attention vectors.
+template <int VEC, int NCH, int U>
+__global__ __launch_bounds__(256) void gat_row_dot_kernel(const float* __restrict__ a,
+                                                          int64_t lda,
+                                                          const float* __restrict__ b,
+                                                          int64_t ldb, int64_t rows, int H,
+                                                          int C, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = wave_id();
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  const int HC = H * C;
+  int fld[NCH], hd[NCH];
+  bool valid[NCH];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    const int foff = (ch * 64 + lane) * VEC;
+    valid[ch] = foff < HC;
+    fld[ch] = valid[ch] ? foff : HC - VEC;
+    hd[ch] = fld[ch] / C;
+  }
+  for (int64_t r0 = wid * U; r0 < rows; r0 += nwaves * U) {
+    float x[U][NCH][VEC], z[U][NCH][VEC];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t r = r0 + k < rows ? r0 + k : rows - 1;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) {
+        ld<VEC>(a + r * lda + fld[ch], x[k][ch]);
+        ld<VEC>(b + r * ldb + fld[ch], z[k][ch]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int64_t r = r0 + k;
+      if (r >= rows) break;
+      for (int h = 0; h < H; ++h) {
+        float p = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+          if (hd[ch] != h || !valid[ch]) continue;
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) p = fmaf(x[k][ch][q], z[k][ch][q], p);
+        }
+        p = wave_sum(p);
+        if (lane == 0) out[r * H + h] = p;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------ softmax stats --
 
 // Per unit: m = max_e v_e and sum_e exp(v_e - m) for each head (two passes
@@ -1089,6 +1141,40 @@ extern "C" int gr_gat_scores(const float* hs, int64_t ldh, int64_t n_src, int64_
     else if (nch == 8) GR_SC(1, 8, 1); else GR_SC(1, 16, 1);
   }
 #undef GR_SC
+  GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}
+
+extern "C" int gr_gat_row_dot(const float* a, int64_t lda, const float* b, int64_t ldb,
+                              int64_t rows, int64_t heads, int64_t channels, float* out,
+                              void* stream) {
+  gr::clear_error();
+  int rc = check_heads(heads, channels);
+  if (rc) return rc;
+  GR_REQUIRE(rows >= 0, "gat_row_dot: negative row count");
+  GR_REQUIRE(lda >= heads * channels && ldb >= heads * channels, "gat_row_dot: bad leading dims");
+  if (rows == 0) return GR_OK;
+  GR_REQUIRE(a && b && out, "gat_row_dot: NULL pointer");
+  const int64_t HC = heads * channels;
+  const bool al = aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0;
+  int vec, nch;
+  pick_shape(HC, channels, al, &vec, &nch);
+  hipStream_t st = gr::as_stream(stream);
+  const int H = (int)heads, C = (int)channels;
+  auto grid = [&](int u) {
+    const int64_t waves = (rows + u - 1) / u;
+    return dim3((unsigned)std::min<int64_t>(4096, (waves + 3) / 4));
+  };
+#define GR_RD(V, N, U)                                                                 \
+  hipLaunchKernelGGL((gat_row_dot_kernel<V, N, U>), grid(U), dim3(256), 0, st, a, lda, b, ldb, \
+                     rows, H, C, out)
+  if (vec == 4) {
+    if (nch == 1) GR_RD(4, 1, 4); else if (nch == 2) GR_RD(4, 2, 2); else GR_RD(4, 4, 1);
+  } else {
+    if (nch == 1) GR_RD(1, 1, 4); else if (nch == 2) GR_RD(1, 2, 2); else if (nch == 4) GR_RD(1, 4, 1);
+    else if (nch == 8) GR_RD(1, 8, 1); else GR_RD(1, 16, 1);
+  }
+#undef GR_RD
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }

@@ -343,6 +343,13 @@ int gr_gat_scores(const float* hs, int64_t ldh, int64_t n_src, int64_t n_dst,
                   int64_t heads, int64_t channels, const float* att_src,
                   const float* att_dst, float* s, float* d, void* stream);
 
+/* out[r,h] = <a[r, h*C:(h+1)*C], b[r, h*C:(h+1)*C]> for r < rows: the
+ * backward's cdot_i = <go_i, O_i> per head (PyG GATConv backward through
+ * softmax, grinnder/nn/gat.py:54-61). */
+int gr_gat_row_dot(const float* a, int64_t lda, const float* b, int64_t ldb,
+                   int64_t rows, int64_t heads, int64_t channels, float* out,
+                   void* stream);
+
 /* Edge softmax over each CSR row: m[i,h] = max_j LeakyReLU(s_j + d_i),
  * den[i,h] = sum exp(v - m) + 1e-16 (rows without edges: m = 0, den = 1) and
  * the attention weights alpha[e,h] = exp(v_e - m) / den [nnz, H] (CSR order).

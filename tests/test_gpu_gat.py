@@ -178,3 +178,22 @@ def test_gat_hub_source_matches_oracle(gpu, H, C):
     assert max_abs_norm_err(as_d.grad.reshape(-1), das) <= TOL
     assert max_abs_norm_err(ad_d.grad.reshape(-1), dad) <= TOL
     assert max_abs_norm_err(b_d.grad, db) <= TOL
+
+
+@pytest.mark.parametrize("rows,H,C", [(1000, 1, 256), (777, 1, 20), (500, 4, 64), (300, 3, 7),
+                                      (5, 1, 1024), (0, 1, 8)])
+def test_gat_row_dot_matches_fp64(gpu, rows, H, C):
+    """cdot[r,h] = <a[r,h,:], b[r,h,:]> (the backward's <GO_i, O_i>)."""
+    from grinnder_amd import _lib
+    g = torch.Generator().manual_seed(rows + C)
+    a = torch.randn(rows, H * C + 4, generator=g)[:, :H * C]   # row stride H*C + 4
+    b = torch.randn(rows, H * C, generator=g)
+    a_d, b_d = a.to(gpu), b.to(gpu)
+    out = torch.full((max(rows, 1), H), float("nan"), device=gpu)
+    _lib.call("gr_gat_row_dot", a_d.data_ptr(), a_d.stride(0), b_d.data_ptr(), H * C, rows, H,
+              C, out.data_ptr(), _lib.stream_handle())
+    torch.cuda.synchronize()
+    if rows == 0:
+        return
+    ref = (a.double().view(rows, H, C) * b.double().view(rows, H, C)).sum(-1)
+    assert max_abs_norm_err(out.cpu(), ref) <= TOL
