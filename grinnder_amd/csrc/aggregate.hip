@@ -10,6 +10,7 @@
 // plan's segment length are summed by a second, ordered pass, so results do
 // not depend on scheduling (no atomics).
 #include "gr_internal.h"
+#include "wave.h"
 
 namespace gr_agg {
 
@@ -130,11 +131,9 @@ __global__ __launch_bounds__(256) void aggregate_units(
   // Combine the EPI edge slots (lanes sub, sub+G, sub+2G, ...).
   if constexpr (EPI > 1) {
 #pragma unroll
-    for (int off = G; off < 64; off <<= 1)
+    for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
-      for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) acc[ch][j] += __shfl_xor(acc[ch][j], off, 64);
+      for (int j = 0; j < VEC; ++j) acc[ch][j] = gr_wave::slot_sum<G>(acc[ch][j]);
   }
   if (slot != 0) return;
 
@@ -197,11 +196,7 @@ __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict
 // Writes h (kept for the backward), out = ReLU(LN(h)) and the row statistics
 // mean / rstd.  LayerNorm uses the biased variance of the row, as torch does.
 
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum64(float v) { return gr_wave::wave_sum(v); }
 
 // y = (h - mean) * rstd * gamma + beta; the backward recomputes it with the
 // same expression so the activation's branch is bit-identical.

@@ -17,6 +17,7 @@
 #include <algorithm>
 
 #include "gr_internal.h"
+#include "wave.h"
 
 namespace gr_gemm {
 
@@ -370,8 +371,7 @@ __global__ __launch_bounds__(256) void linear_ln_act_kernel(
     float s = 0.f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) s += acc[b][q];
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
+    s = gr_wave::group_sum<16>(s);  // the 16 lanes of this row block
     const float mu = s * inv_d;
     float v = 0.f;
 #pragma unroll
@@ -379,8 +379,7 @@ __global__ __launch_bounds__(256) void linear_ln_act_kernel(
       const float dlt = acc[b][q] - mu;
       v += dlt * dlt;
     }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 64);
+    v = gr_wave::group_sum<16>(v);
     const float rs = 1.0f / sqrtf(v * inv_d + eps);
     // Stage the 4 rows {4 * lk + q} of this wavefront in LDS (reusing the W
     // tile), then store them with 16-byte accesses along each row.

@@ -15,31 +15,15 @@
 #include <algorithm>
 
 #include "gr_internal.h"
+#include "wave.h"
 
 namespace gr_loss {
 
 constexpr int kStats = 7;  // nll_sum, train_n, val_ok, val_n, test_ok, test_n, bad_labels
 
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, G));
-  return v;
-}
-
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, G);
-  return v;
-}
-
-template <int G>
-__device__ __forceinline__ int group_min_int(int v) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off >>= 1) v = min(v, __shfl_xor(v, off, G));
-  return v;
-}
+using gr_wave::group_max;
+using gr_wave::group_min_int;
+using gr_wave::group_sum;
 
 // Accumulates one row's contribution to the seven statistics.
 __device__ __forceinline__ void add_row_stats(double (&acc)[kStats], uint8_t mk, bool ok_label,

@@ -60,6 +60,34 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+__device__ __forceinline__ int xor16_int(int x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return (threadIdx.x & 16) ? r[0] : r[1];
+}
+
+__device__ __forceinline__ int xor32_int(int x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_int(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+
+// Minimum over aligned groups of G consecutive lanes, for ints.
+template <int G>
+__device__ __forceinline__ int group_min_int(int v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G must be a power of two <= 64");
+  if constexpr (G >= 2) v = min(v, dpp_int<0xB1>(v));
+  if constexpr (G >= 4) v = min(v, dpp_int<0x4E>(v));
+  if constexpr (G >= 8) v = min(v, dpp_int<0x141>(v));
+  if constexpr (G >= 16) v = min(v, dpp_int<0x140>(v));
+  if constexpr (G >= 32) v = min(v, xor16_int(v));
+  if constexpr (G >= 64) v = min(v, xor32_int(v));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
