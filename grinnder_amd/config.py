@@ -32,6 +32,12 @@ class GriNNderConfig:
         the storage tier; this package keeps every layer host-resident, which
         is what 'auto' resolves to when the working set fits).
     device: GPU device string; pool_size: transfer double-buffering depth.
+    project_first: 'auto' lets the partitioned trainer project layer 0's
+        input rows once per partition and gather projected rows, held in HBM,
+        when the layer starts with a narrowing bias-free projection and they
+        fit (same results up to fp32 summation order); 'off' always gathers
+        input rows as the reference does.  Not a field of the reference's
+        config.
     """
 
     mode: Literal["hongtu", "grinnder"] = "grinnder"
@@ -58,3 +64,5 @@ class GriNNderConfig:
     preprocess_workers: int = field(default_factory=_default_threads)
 
     num_gpus: int = 1
+
+    project_first: Literal["auto", "off"] = "auto"

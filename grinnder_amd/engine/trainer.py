@@ -24,6 +24,19 @@ Differences by design: host buffers are pinned so halo traffic moves by
 device kernels; waits are per stream, not device-wide; the NVMe storage tier
 and its partition-LRU cache are out of scope (every layer stays in host RAM,
 which is what the reference's 'auto' cache resolves to when it fits).
+
+Projected first layer (config.project_first = 'auto'): when layer 0 starts
+by multiplying every gathered input row by a narrowing W (a GCNConv that
+multiplies first, a GATConv with inactive dropout), gather(X) Wᵀ =
+gather(X Wᵀ) row by row.  Each partition's own rows are then uploaded once
+and projected into Z = X Wᵀ, which stays in HBM with its gradient dZ; every
+partition gathers its rows of Z on the device instead of input rows from the
+host.  The backward recomputes the layer from the gathered Z, adds dL/dZ of
+the gathered rows into dZ (partitions in order, so sums are deterministic),
+and finally forms dL/dW = sum_p dZ_pᵀ X_p with a second upload of each
+partition's rows.  For 1024-wide inputs projected to 256 this replaces the
+two host gathers of ~(halo amplification) x N x 4 KiB per epoch by two
+N x 4 KiB uploads.
 """
 
 from __future__ import annotations
@@ -37,8 +50,10 @@ from torch.utils.checkpoint import checkpoint
 from grinnder_amd.autograd.checkpoint import HongtuCheckpoint, ScatteredCheckpoint
 from grinnder_amd.autograd.grad_offload import GradOffload
 from grinnder_amd.buffer.device import DeviceBuffer
+from grinnder_amd.aggregation import KernelTimer, dense_region
 from grinnder_amd.buffer.host import HostBuffer
 from grinnder_amd.config import GriNNderConfig
+from grinnder_amd.dense import gemm_tn
 from grinnder_amd.data.graph import PartitionedGraph
 from grinnder_amd.engine.streams import StreamManager
 from grinnder_amd.nn.base import GriNNderModel
@@ -84,6 +99,14 @@ class Trainer:
         self._pid_to_loss_idx: Dict[int, int] = {}
         self._resident: Dict[str, Tensor] = {}
         self._label_cache: Dict[int, tuple] = {}
+        # Projected layers: their W this epoch; Z, dZ per layer and two upload
+        # buffers per input width, kept across epochs; the device row ids of
+        # each partition's gathered rows.
+        self._proj: Dict[int, Tensor] = {}
+        self._zbufs: Dict[int, Tensor] = {}
+        self._dzbufs: Dict[int, Tensor] = {}
+        self._xbufs: Dict[int, List[Tensor]] = {}
+        self._grow: Dict[int, Tensor] = {}
         if not self._fast:
             for l in range(L + 1):
                 self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
@@ -123,6 +146,7 @@ class Trainer:
         self.model.train()
         if self._fast:
             return self._train_fast(optimizer)
+        self._proj = self._plan_projection()
         self.reset_epoch()
         optimizer.zero_grad()
         for l in range(self.model.num_layers):
@@ -146,6 +170,7 @@ class Trainer:
             out = self._fast_logits()
             _, metrics = self._fast_metrics(out)
             return metrics
+        self._proj = self._plan_projection()
         self.reset_epoch()
         for l in range(self.model.num_layers):
             self._forward_layer(l)
@@ -245,24 +270,239 @@ class Trainer:
         if t is not None:
             t.untyped_storage().resize_(0)
 
+    # --------------------------------------------------- projected layers
+
+    @property
+    def projected(self) -> bool:
+        """Whether the current epoch runs any layer on projected rows."""
+        return bool(self._proj)
+
+    @property
+    def projected_layers(self) -> List[int]:
+        return sorted(self._proj)
+
+    def _plan_projection(self) -> Dict[int, Tensor]:
+        """Layers this epoch runs projected, with their input projection W:
+        grinnder mode, every partition on this trainer, a narrowing
+        projection, and room in HBM for Z, dZ and the upload buffers (plus
+        8 GiB for the per-partition working set)."""
+        cfg, g = self.config, self.graph
+        if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
+                or (self._pid_start, self._pid_end) != (0, g.num_parts)):
+            return {}
+        n, maxb = int(g.ptr[-1]), max(g.partition_sizes)
+        free = None
+        plan: Dict[int, Tensor] = {}
+        for layer in range(self.model.num_layers):
+            w = self.model.input_projection(layer)
+            if w is None or w.size(0) >= w.size(1):
+                continue
+            if layer not in self._zbufs:
+                if free is None:
+                    free, _ = torch.cuda.mem_get_info(self.device)
+                need = 4 * (2 * n * w.size(0) + 2 * maxb * w.size(1))
+                if need + (8 << 30) > free:
+                    continue
+                free -= need
+            plan[layer] = w
+        return plan
+
+    def _zbuf(self, layer: int) -> Tensor:
+        z = self._zbufs.get(layer)
+        if z is None:
+            with torch.cuda.stream(self.streams.compute):
+                z = torch.empty(int(self.graph.ptr[-1]), self._proj[layer].size(0),
+                                device=self.device)
+            self._zbufs[layer] = z
+        return z
+
+    def _dzbuf(self, layer: int) -> Tensor:
+        dz = self._dzbufs.get(layer)
+        if dz is None:
+            with torch.cuda.stream(self.streams.compute):
+                dz = torch.empty_like(self._zbuf(layer))
+            self._dzbufs[layer] = dz
+        return dz
+
+    def _global_rows(self, pid: int) -> Tensor:
+        """Device int64 ids (in partition order) of partition pid's gathered
+        rows, laid out [intra | halo from p' = 0..P-1] like the host gather."""
+        idx = self._grow.get(pid)
+        if idx is None:
+            g = self.graph
+            lo, hi = g._range(pid)
+            parts = [torch.arange(lo, hi, dtype=torch.int64)]
+            for q, b in enumerate(g.boundaries[pid]):
+                if q != pid and b is not None and b.numel() > 0:
+                    parts.append(b.to(torch.int64) + int(g.ptr[q]))
+            idx = torch.cat(parts).to(self.device)
+            if idx.numel() != g.expanded_sizes[pid]:
+                raise RuntimeError(f"partition {pid}: {idx.numel()} gathered rows, "
+                                   f"expected {g.expanded_sizes[pid]}")
+            self._grow[pid] = idx
+        return idx
+
+    def _gather_projected(self, layer: int, pid: int) -> Tensor:
+        rows = self._global_rows(pid)
+        z = self._zbufs[layer]
+        d = z.size(1)
+        with KernelTimer.region("z_gather", 2 * 4 * rows.numel() * d, 0, d):
+            return z.index_select(0, rows)
+
+    def _project_rows(self, layer: int, x: Tensor, lo: int, hi: int) -> None:
+        """Z_layer[lo:hi] = x Wᵀ (no autograd)."""
+        w = self._proj[layer]
+        with torch.no_grad(), dense_region("fwd", hi - lo, w.size(1), w.size(0)):
+            torch.mm(x.detach(), w.detach().t(), out=self._zbuf(layer)[lo:hi])
+
+    def _each_input_partition(self, layer: int, fn) -> None:
+        """fn(pid, x_p, lo, hi) on the compute stream for every partition,
+        x_p = the partition's rows of the host buffer of layer `layer`'s
+        inputs, uploaded to HBM; two buffers, so the next upload overlaps fn."""
+        g, s, pids = self.graph, self.streams, self._my_pids
+        host = self.host_features[layer]
+        din = host.embedding_dim
+        bufs = self._xbufs.get(din)
+        if bufs is None:
+            with torch.cuda.stream(s.compute):
+                bufs = [torch.empty(max(g.partition_sizes), din, device=self.device)
+                        for _ in range(2)]
+            self._xbufs[din] = bufs
+        freed: List[Optional[torch.cuda.Event]] = [None, None]
+
+        def upload(i: int) -> torch.cuda.Event:
+            k, pid = i % 2, pids[i]
+            b = g.partition_sizes[pid]
+            st = s.h2d[k % len(s.h2d)]
+            if freed[k] is not None:
+                st.wait_event(freed[k])
+            with torch.cuda.stream(st):
+                with KernelTimer.region("x_upload", 4 * b * din, 0, din):
+                    bufs[k][:b].copy_(host[pid], non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record(st)
+            return ev
+
+        ready = upload(0)
+        for i, pid in enumerate(pids):
+            k = i % 2
+            nxt = upload(i + 1) if i + 1 < len(pids) else None
+            s.compute.wait_event(ready)
+            with torch.cuda.stream(s.compute):
+                lo, hi = g._range(pid)
+                fn(pid, bufs[k][:hi - lo], lo, hi)
+                ev = torch.cuda.Event()
+                ev.record(s.compute)
+                freed[k] = ev
+            ready = nxt
+
+    def _device_grad(self, layer: int, pid: int) -> Tensor:
+        """dL/d(x_layer) of partition pid's rows when layer `layer` runs
+        projected: dZ_layer[rows] W (the halo contributions of every partition
+        are already summed in dZ)."""
+        lo, hi = self.graph._range(pid)
+        w = self._proj[layer]
+        with dense_region("dx", hi - lo, w.size(0), w.size(1)):
+            return torch.mm(self._dzbufs[layer][lo:hi], w.detach())
+
+    def _backward_projected(self, layer: int) -> None:
+        """Backward of a projected layer: per partition, recompute the layer
+        from its gathered rows of Z and backpropagate into the layer's
+        parameters and into dZ; then dW = sum_p dZ_pᵀ x_p."""
+        g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
+        if not pids:
+            return
+        last = layer == self.model.num_layers - 1
+        w = self._proj[layer]
+        dz = self._dzbuf(layer)
+        with torch.cuda.stream(s.compute):
+            dz.zero_()
+        from_device = (layer + 1) in self._proj
+        from_host = not last and not from_device
+        gbuf = self.device_gradients[layer + 1] if not last else None
+        if from_host:
+            self._upload_grad(layer + 1, pids[0], s.h2d[0])
+        for i, pid in enumerate(pids):
+            k = i % pool
+            if from_host:
+                self.host_gradients[layer + 1].h2d_synchronize(s.h2d[k])
+                s.compute.wait_stream(s.h2d[k])
+            with torch.cuda.stream(s.compute):
+                if from_host and i + 1 < len(pids) and pool > 1:
+                    self._upload_grad(layer + 1, pids[i + 1], s.h2d[(i + 1) % pool])
+                z = self._gather_projected(layer, pid).requires_grad_(True)
+                with torch.enable_grad():
+                    out = self.model.forward_projected(layer, z, g.adjacency(pid))
+                    if last:
+                        y, codes = self._labels_and_codes(pid)
+                        loss, _ = masked_cross_entropy(out, y, codes, "sum")
+                if last:
+                    loss.backward()
+                elif from_device:
+                    out.backward(self._device_grad(layer + 1, pid))
+                else:
+                    out.backward(gbuf[pid])
+                    gbuf.release(pid)
+                # Rows are distinct within one partition, so each element of
+                # dZ gets one addition per partition, in partition order.
+                dz.index_add_(0, self._global_rows(pid), z.grad)
+                del z, out
+                self.activations[layer][pid] = None
+            if from_host and pool == 1 and i + 1 < len(pids):
+                self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])
+        with torch.cuda.stream(s.compute):
+            dw = torch.zeros_like(w)
+
+        def accumulate(pid, xp, lo, hi):
+            with dense_region("dw", hi - lo, w.size(0), w.size(1)):
+                gemm_tn(dz[lo:hi], xp, out=dw, beta=1.0)
+
+        self._each_input_partition(layer, accumulate)
+        with torch.cuda.stream(s.compute):
+            if w.grad is None:
+                w.grad = dw
+            else:
+                w.grad.add_(dw)
+        s.compute.synchronize()
+
     # ------------------------------------------------------------- forward
 
     def _forward_layer(self, layer: int) -> None:
-        pids, pool, s = self._my_pids, self.config.pool_size, self.streams
+        """Per partition: the layer's output from gathered input rows (the
+        reference's flow) or from gathered rows of Z (a projected layer), D2H
+        into the next layer's host buffer, and, when the next layer runs
+        projected, its rows of Z_{layer+1} = out Wᵀ formed right away."""
+        g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
-        self._gather(layer, pids[0], s.h2d[0])
+        projected = layer in self._proj
+        w_next = self._proj.get(layer + 1)
+        if projected and layer == 0:
+            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+        if not projected:
+            self._gather(layer, pids[0], s.h2d[0])
         for i, pid in enumerate(pids):
             k = i % pool
-            self.device_features[layer].h2d_synchronize(s.h2d[k])
-            s.compute.wait_stream(s.h2d[k])
+            if not projected:
+                self.device_features[layer].h2d_synchronize(s.h2d[k])
+                s.compute.wait_stream(s.h2d[k])
             with torch.cuda.stream(s.compute):
-                if i + 1 < len(pids) and pool > 1:
-                    self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
-                out = self._checkpointed(layer, pid, k)
+                if not projected:
+                    if i + 1 < len(pids) and pool > 1:
+                        self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
+                    out = self._checkpointed(layer, pid, k)
+                else:
+                    with torch.no_grad():
+                        out = self.model.forward_projected(
+                            layer, self._gather_projected(layer, pid),
+                            g.adjacency(pid)).contiguous()
+                if w_next is not None:
+                    lo, hi = g._range(pid)
+                    self._project_rows(layer + 1, out, lo, hi)
                 self.activations[layer][pid] = out
                 self.host_features[layer + 1].async_fill(pid, out, s.d2h[k])
-                self.device_features[layer].release(pid)
+                if not projected:
+                    self.device_features[layer].release(pid)
                 if i > 0 and pool > 1:
                     prev, pk = pids[i - 1], (i - 1) % pool
                     self.host_features[layer + 1].d2h_synchronize(s.d2h[pk])
@@ -270,7 +510,7 @@ class Trainer:
             if pool == 1:
                 self.host_features[layer + 1].d2h_synchronize(s.d2h[0])
                 self._free(self.activations[layer][pid])
-                if i + 1 < len(pids):
+                if not projected and i + 1 < len(pids):
                     self._gather(layer, pids[i + 1], s.h2d[0])
         if pool > 1:
             last = (len(pids) - 1) % pool
@@ -345,21 +585,33 @@ class Trainer:
 
     def _backward_last_layer(self, losses: List[Tensor]) -> None:
         layer = self.model.num_layers - 1
-        self._backward_pass(layer, lambda pid: losses[self._pid_to_loss_idx[pid]].backward())
+        if layer in self._proj:
+            self._backward_projected(layer)
+        else:
+            self._backward_pass(layer,
+                                lambda pid: losses[self._pid_to_loss_idx[pid]].backward())
         for i in range(len(losses)):
             losses[i] = None
 
     def _backward_layer(self, layer: int) -> None:
+        if layer in self._proj:
+            self._backward_projected(layer)
+            return
+        from_device = (layer + 1) in self._proj
+
         def run(pid: int) -> None:
             act = self.activations[layer][pid]
             if act is None or act.grad_fn is None:
+                return
+            if from_device:
+                act.backward(self._device_grad(layer + 1, pid))
                 return
             gbuf = self.device_gradients[layer + 1]
             if gbuf is not None and gbuf.is_allocated(pid):
                 act.backward(gbuf[pid])
             else:
                 act.backward()
-        self._backward_pass(layer, run, upload_grad=True)
+        self._backward_pass(layer, run, upload_grad=not from_device)
 
     def _backward_pass(self, layer: int, run, upload_grad: bool = False) -> None:
         """Per partition: re-gather x_layer, upload dL/d(out) if needed, backprop."""

@@ -3,7 +3,7 @@
 from __future__ import annotations
 
 from abc import abstractmethod
-from typing import List
+from typing import List, Optional
 
 import torch
 from torch import Tensor
@@ -33,3 +33,17 @@ class GriNNderModel(torch.nn.Module):
     @abstractmethod
     def layer_dims(self) -> List[int]:
         ...
+
+    def input_projection(self, layer: int) -> Optional[Tensor]:
+        """The weight W [out, in] when ``forward_layer(layer, x, adj)`` starts
+        by multiplying every gathered row of x by Wᵀ, with nothing applied to x
+        before, so that it equals ``forward_projected(layer, x Wᵀ, adj)``.  A
+        partitioned trainer may then project each partition's own rows once
+        and gather projected rows (narrower when out < in).  None when the
+        layer has no such form (the default)."""
+        return None
+
+    def forward_projected(self, layer: int, z: Tensor, adj) -> Tensor:
+        """forward_layer(layer, x, adj) given z = x Wᵀ for the W of
+        input_projection(layer)."""
+        raise NotImplementedError(f"{type(self).__name__} has no projected form of layer {layer}")

@@ -144,7 +144,21 @@ class GATConv(Module):
             hs = linear(x_src, w)
             y = gat_attention(hs, adj, a_s, a_d, b, 1, self.out_channels + pad, self.concat)
             return y[:, :self.out_channels]
-        hs = linear(x_src, self.lin.weight)
+        return self.attend(linear(x_src, self.lin.weight), adj, add_bias)
+
+    def attend(self, hs: Tensor, adj: Adjacency, add_bias: bool = True) -> Tensor:
+        """The layer after its projection: attention over hs = lin(x) for all
+        source rows.  One head of C channels, C not a multiple of 4, runs on hs
+        and the attention parameters zero-padded to a multiple of 4 (as in
+        forward)."""
+        bias = self.bias if add_bias else None
+        if self.heads == 1 and self.out_channels % 4 != 0:
+            pad = (-self.out_channels) % 4
+            b = F.pad(bias, (0, pad)) if bias is not None else None
+            y = gat_attention(F.pad(hs, (0, pad)), adj, F.pad(self.att_src, (0, pad)),
+                              F.pad(self.att_dst, (0, pad)), b, 1, self.out_channels + pad,
+                              self.concat)
+            return y[:, :self.out_channels]
         return gat_attention(hs, adj, self.att_src, self.att_dst, bias, self.heads,
                              self.out_channels, self.concat)
 

@@ -38,25 +38,47 @@ class GAT(GriNNderModel):
             self.norms = ModuleList(LayerNorm(hidden_channels * heads)
                                     for _ in range(num_layers - 1))
 
-    def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
-        x = F.dropout(x, p=self.dropout, training=self.training)
-        num_dst = adj.sparse_sizes()[0]
-        conv = self.convs[layer]
-        if layer < self.num_layers - 1 and self.norms is not None:
-            norm = self.norms[layer]
-            if (x.is_cuda and norm.elementwise_affine and norm.bias is not None
-                    and tuple(norm.normalized_shape) == (conv.out_channels * conv.heads,)
-                    and conv.concat):
-                # The conv bias, LayerNorm and ELU in one pass over the
-                # attention output.
-                x = conv((x, x[:num_dst]), adj, add_bias=False)
-                return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
-        x = conv((x, x[:num_dst]), adj)
+    def _fused_norm(self, layer: int, x: Tensor) -> bool:
+        """The conv bias, LayerNorm and ELU can run as one pass over the
+        attention output."""
+        if layer >= self.num_layers - 1 or self.norms is None or not x.is_cuda:
+            return False
+        conv, norm = self.convs[layer], self.norms[layer]
+        return (norm.elementwise_affine and norm.bias is not None
+                and tuple(norm.normalized_shape) == (conv.out_channels * conv.heads,)
+                and conv.concat)
+
+    def _finish(self, layer: int, x: Tensor) -> Tensor:
         if layer < self.num_layers - 1:
             if self.norms is not None:
                 x = self.norms[layer](x)
             x = F.elu(x)
         return x
+
+    def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
+        x = F.dropout(x, p=self.dropout, training=self.training)
+        num_dst = adj.sparse_sizes()[0]
+        conv = self.convs[layer]
+        if self._fused_norm(layer, x):
+            norm = self.norms[layer]
+            x = conv((x, x[:num_dst]), adj, add_bias=False)
+            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
+        return self._finish(layer, conv((x, x[:num_dst]), adj))
+
+    def input_projection(self, layer: int):
+        """GATConv multiplies every source row by lin first; the dropout before
+        it must be inactive."""
+        if self.dropout != 0.0 and self.training:
+            return None
+        return self.convs[layer].lin.weight
+
+    def forward_projected(self, layer: int, hs: Tensor, adj) -> Tensor:
+        conv = self.convs[layer]
+        if self._fused_norm(layer, hs):
+            norm = self.norms[layer]
+            x = conv.attend(hs, adj, add_bias=False)
+            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
+        return self._finish(layer, conv.attend(hs, adj))
 
     def layer_dims(self) -> List[int]:
         dims = [self.convs[0].in_channels]

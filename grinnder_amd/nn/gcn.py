@@ -36,19 +36,55 @@ class GCN(GriNNderModel):
         if norm:
             self.norms = ModuleList(LayerNorm(hidden_channels) for _ in range(num_layers - 1))
 
-    def _fusable(self, layer: int, x: Tensor, adj) -> bool:
-        """conv -> LayerNorm -> ReLU runs as one fused kernel when nothing else
-        sits between them: no residual add, no active dropout, affine LayerNorm
-        over the full feature width."""
+    def _fusable_norm(self, layer: int, x: Tensor) -> bool:
+        """conv -> LayerNorm -> ReLU can run as one fused kernel: affine
+        LayerNorm over the full feature width, no active dropout after it."""
         if self.norms is None or layer >= self.num_layers - 1 or not x.is_cuda:
             return False
         norm = self.norms[layer]
         conv = self.convs[layer]
-        out_shape = (adj.sparse_sizes()[0], conv.out_channels)
         return (norm.elementwise_affine and norm.bias is not None
                 and tuple(norm.normalized_shape) == (conv.out_channels,)
-                and not (self.residual and tuple(x.shape) == out_shape)
                 and (self.dropout == 0.0 or not self.training))
+
+    def _fusable(self, layer: int, x: Tensor, adj) -> bool:
+        """As _fusable_norm, and no residual add between the conv and the LayerNorm."""
+        out_shape = (adj.sparse_sizes()[0], self.convs[layer].out_channels)
+        return (self._fusable_norm(layer, x)
+                and not (self.residual and tuple(x.shape) == out_shape))
+
+    def input_projection(self, layer: int):
+        """A GCNConv that multiplies first applies lin to every gathered row
+        before anything else (dropout acts on layer outputs).  Not for
+        aggregate-first layers, or when the residual add could need x itself
+        (in == out)."""
+        conv = self.convs[layer]
+        if conv.aggregate_first():
+            return None
+        if self.residual and conv.in_channels == conv.out_channels:
+            return None
+        return conv.lin.weight
+
+    def forward_projected(self, layer: int, z: Tensor, adj) -> Tensor:
+        conv = self.convs[layer]
+        d = conv.out_channels
+        if d % 4 != 0:
+            # Widths that are not a multiple of 4 aggregate zero-padded rows
+            # (16-byte vectors), as GCNConv does; the pad column stays zero.
+            pad = (-d) % 4
+            b = F.pad(conv.bias, (0, pad)) if conv.bias is not None else None
+            h = gcn_aggregate(F.pad(z, (0, pad)), adj, b)[:, :d]
+        elif self._fusable_norm(layer, z):
+            norm = self.norms[layer]
+            return gcn_aggregate_ln_relu(z, adj, conv.bias, norm.weight, norm.bias, norm.eps)
+        else:
+            h = gcn_aggregate(z, adj, conv.bias)
+        if layer < self.num_layers - 1:
+            if self.norms is not None:
+                h = self.norms[layer](h)
+            h = F.relu(h)
+            h = F.dropout(h, p=self.dropout, training=self.training)
+        return h
 
     def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
         if self._fusable(layer, x, adj):

@@ -265,3 +265,56 @@ def test_buffers_released_and_loss_decreases(gpu):
                 assert buf.allocated_pids() == []
         ev = trainer.evaluate(torch.nn.CrossEntropyLoss())
         assert 0.0 <= ev["val_acc"] <= 1.0
+
+
+@pytest.mark.parametrize("model_kind", ["gcn", "gat"])
+@pytest.mark.parametrize("pool_size", [1, 2])
+def test_projected_layers_match_gathered(gpu, model_kind, pool_size):
+    """config.project_first: layers that start with a narrowing projection
+    (here layer 0, 24 -> 16 or 8, and the last layer, 16 or 8 -> 4) run on
+    projected rows Z = x Wᵀ held in HBM; loss and gradients equal those of the
+    reference flow that gathers input rows (project_first='off') within the
+    1e-5 bound, and evaluate() agrees too."""
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    torch.manual_seed(3)
+    if model_kind == "gcn":
+        make = lambda: GCN(24, 16, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
+    else:
+        make = lambda: GAT(24, 8, 4, num_layers=3, heads=1, dropout=0.0, norm=True)  # noqa
+    state = make().state_dict()
+    ei, x, y, tr, va, te = data
+    runs = {}
+    for proj in ("off", "auto"):
+        config = GriNNderConfig(num_parts=4, pool_size=pool_size, project_first=proj)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        metrics = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
+        assert trainer.projected_layers == ([0, 2] if proj == "auto" else [])
+        grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()
+                 if p.grad is not None}
+        ev = trainer.evaluate(torch.nn.CrossEntropyLoss())
+        runs[proj] = (metrics["loss"], grads, ev)
+    (l0, g0, e0), (l1, g1, e1) = runs["off"], runs["auto"]
+    assert abs(l0 - l1) < 1e-5
+    assert set(g0) == set(g1)
+    for k, err in grad_errs(g1, g0).items():
+        assert err <= 1e-5, (k, err)
+    assert e0["val_acc"] == e1["val_acc"]
+
+
+def test_projected_layers_match_dense_vanilla(gpu):
+    """The projected flow (layer 0 24 -> 16, last layer 16 -> 3, padded to 4)
+    against the float64 dense GCN."""
+    data = _graph_data(feat=24)
+    torch.manual_seed(7)
+    make = lambda: GCN(24, 16, 3, num_layers=2, dropout=0.0, norm=True)  # noqa: E731
+    state = make().state_dict()
+    ref_loss, ref_grads = _vanilla(data, state, make)
+    loss, grads, trainer, _ = _step(data, state, make, 4, "grinnder")
+    assert trainer.projected_layers == [0, 1]
+    assert abs(loss - ref_loss) < 1e-5
+    for k, err in grad_errs(grads, ref_grads).items():
+        assert err <= 1e-5, (k, err)
