@@ -54,6 +54,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", choices=sorted(CONFIGS_NAMES), default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--project-first", choices=("auto", "off"), default="auto",
+                    help="partitioned configs: run layers on projected rows held in HBM "
+                         "('auto', GriNNderConfig.project_first) or gather every layer's "
+                         "input rows from the host buffers as the reference does ('off')")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
                     help="print a text summary of the rocprofv3 CSV output under DIR and exit")
@@ -85,7 +89,7 @@ CONFIGS = {
 }
 
 
-def build_graph(cfg, device):
+def build_graph(cfg, device, project_first="auto"):
     import torch
 
     from grinnder_amd.config import GriNNderConfig
@@ -107,7 +111,8 @@ def build_graph(cfg, device):
     else:
         nd = synthetic.node_data(n, cfg["feat_dim"], cfg["num_classes"], seed=42)
         x = nd.x
-    config = GriNNderConfig(num_parts=cfg["num_parts"], device=device)
+    config = GriNNderConfig(num_parts=cfg["num_parts"], device=device,
+                            project_first=project_first)
     graph = build_partitioned_graph(ei, x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
                                     config)
     del ei
@@ -259,7 +264,7 @@ def main():
             f"MemAvailable {int(meminfo['MemAvailable']) / 2**20:.1f} GiB, cpus {os.cpu_count()}")
     except OSError:
         pass
-    graph, config = build_graph(cfg, device)
+    graph, config = build_graph(cfg, device, args.project_first)
     nnz = sum(int(a[1].numel()) for a in graph.adj_csr)
 
     torch.manual_seed(42)
@@ -297,7 +302,8 @@ def main():
             metrics = trainer.train_epoch(opt, crit)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f})")
+    log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f}); "
+        f"projected layers {trainer.projected_layers}")
     if cfg["num_parts"] > 1:
         from grinnder_amd.buffer.host import PINNED_STATS
         log(f"pinned host memory {PINNED_STATS['bytes'] / 2**30:.1f} GiB, "
@@ -373,7 +379,8 @@ def main():
                    "nnz": nnz, "feat_dim": cfg["feat_dim"], "hidden": cfg["hidden"],
                    "num_classes": cfg["num_classes"], "num_layers": cfg["num_layers"],
                    "num_parts": cfg["num_parts"], "model": cfg["model"],
-                   "halo_amplification": round(graph.halo_amplification(), 4)},
+                   "halo_amplification": round(graph.halo_amplification(), 4),
+                   "projected_layers": trainer.projected_layers},
         "epoch_s": round(epoch_s, 5),
         "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,
         "agg_kernel_gteps": round(sum(r.edges for r in recs_agg) / (agg_ms / 1e3) / 1e9, 4),

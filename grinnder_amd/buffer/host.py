@@ -22,7 +22,12 @@ PINNED_STATS = {"bytes": 0, "blocks": 0, "fallbacks": 0, "fallback_bytes": 0}
 
 
 class _PinnedBlock:
-    """Owns one exact-size pinned host allocation (gr_host_alloc)."""
+    """Owns one exact-size pinned host allocation (gr_host_alloc).
+
+    Ownership runs one way, tensor -> ctypes array -> block, so the
+    allocation is released as soon as the last tensor over it dies, not at
+    some later cyclic garbage collection (a dropped Trainer would otherwise
+    keep tens of GB pinned)."""
 
     def __init__(self, nbytes: int):
         ptr = ctypes.c_void_p()
@@ -31,8 +36,12 @@ class _PinnedBlock:
         PINNED_STATS["bytes"] += nbytes
         PINNED_STATS["blocks"] += 1
         self.nbytes = nbytes
-        self.array = (ctypes.c_char * nbytes).from_address(self.ptr)
-        self.array._owner = self  # the tensor keeps the array, the array keeps us
+
+    def array(self) -> ctypes.Array:
+        """A ctypes view of the block that keeps the block alive."""
+        arr = (ctypes.c_char * self.nbytes).from_address(self.ptr)
+        arr._owner = self
+        return arr
 
     def __del__(self):
         ptr = getattr(self, "ptr", None)
@@ -58,7 +67,7 @@ def pinned_empty(rows: int, cols: int) -> Tensor:
         PINNED_STATS["fallbacks"] += 1
         PINNED_STATS["fallback_bytes"] += nbytes
         return torch.empty((rows, cols), dtype=torch.float32)
-    return torch.frombuffer(block.array, dtype=torch.float32).view(rows, cols)
+    return torch.frombuffer(block.array(), dtype=torch.float32).view(rows, cols)
 
 
 def _empty_host_tensor(rows: int, cols: int, *, pin_memory: bool, allocate: bool) -> Tensor:

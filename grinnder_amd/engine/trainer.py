@@ -25,18 +25,19 @@ device kernels; waits are per stream, not device-wide; the NVMe storage tier
 and its partition-LRU cache are out of scope (every layer stays in host RAM,
 which is what the reference's 'auto' cache resolves to when it fits).
 
-Projected first layer (config.project_first = 'auto'): when layer 0 starts
-by multiplying every gathered input row by a narrowing W (a GCNConv that
-multiplies first, a GATConv with inactive dropout), gather(X) Wᵀ =
-gather(X Wᵀ) row by row.  Each partition's own rows are then uploaded once
-and projected into Z = X Wᵀ, which stays in HBM with its gradient dZ; every
-partition gathers its rows of Z on the device instead of input rows from the
-host.  The backward recomputes the layer from the gathered Z, adds dL/dZ of
-the gathered rows into dZ (partitions in order, so sums are deterministic),
-and finally forms dL/dW = sum_p dZ_pᵀ X_p with a second upload of each
-partition's rows.  For 1024-wide inputs projected to 256 this replaces the
-two host gathers of ~(halo amplification) x N x 4 KiB per epoch by two
-N x 4 KiB uploads.
+Projected layers (config.project_first = 'auto'): when a layer's input
+enters only through x Wᵀ (GCNConv; GATConv with inactive dropout),
+gather(x) Wᵀ = gather(x Wᵀ) row by row.  Z = x Wᵀ is then formed once per
+partition from its own rows (layer 0: uploaded input rows; above: the
+previous layer's output, right after it is computed) and stays in HBM with
+its gradient dZ; every partition gathers its rows of Z on the device instead
+of input rows from the host.  The backward recomputes the layer from the
+gathered Z, adds dL/dZ of the gathered rows into dZ (partitions in order, so
+sums are deterministic), hands dZ_p W to the layer below as the gradient of
+its outputs (no host scatter), and forms dL/dW = sum_p dZ_pᵀ x_p from a
+second upload of each partition's input rows.  Per layer this replaces two
+host gathers and a read-add-write scatter of ~E x d_in rows by two N x d_in
+uploads.
 """
 
 from __future__ import annotations
@@ -283,20 +284,25 @@ class Trainer:
 
     def _plan_projection(self) -> Dict[int, Tensor]:
         """Layers this epoch runs projected, with their input projection W:
-        grinnder mode, every partition on this trainer, a narrowing
-        projection, and room in HBM for Z, dZ and the upload buffers (plus
-        8 GiB for the per-partition working set)."""
+        grinnder mode, every partition on this trainer, and room in HBM for
+        Z, dZ and the upload buffers (plus 8 GiB for the per-partition
+        working set).  A projected layer moves 2 N d_in bytes over the host
+        link (two uploads of its input rows) instead of 2 E d_in of gathers
+        and, above layer 0, an E d_in read-add-write scatter; when HBM is
+        short, layers with the most input width per byte of Z go first."""
         cfg, g = self.config, self.graph
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
             return {}
         n, maxb = int(g.ptr[-1]), max(g.partition_sizes)
-        free = None
-        plan: Dict[int, Tensor] = {}
+        cands = []
         for layer in range(self.model.num_layers):
             w = self.model.input_projection(layer)
-            if w is None or w.size(0) >= w.size(1):
-                continue
+            if w is not None:
+                cands.append((w.size(1) / w.size(0), layer, w))
+        free = None
+        plan: Dict[int, Tensor] = {}
+        for _, layer, w in sorted(cands, key=lambda c: (-c[0], c[1])):
             if layer not in self._zbufs:
                 if free is None:
                     free, _ = torch.cuda.mem_get_info(self.device)
@@ -305,7 +311,7 @@ class Trainer:
                     continue
                 free -= need
             plan[layer] = w
-        return plan
+        return dict(sorted(plan.items()))
 
     def _zbuf(self, layer: int) -> Tensor:
         z = self._zbufs.get(layer)
@@ -368,14 +374,20 @@ class Trainer:
                 bufs = [torch.empty(max(g.partition_sizes), din, device=self.device)
                         for _ in range(2)]
             self._xbufs[din] = bufs
-        freed: List[Optional[torch.cuda.Event]] = [None, None]
+        # The first upload into each buffer waits for the compute stream's
+        # queued work: a buffer allocated just now may occupy memory that
+        # queued compute kernels still read (the caching allocator reuses a
+        # block as soon as its stream has queued the last use), and a cached
+        # one may still be read by the previous call's last fn.
+        entry = torch.cuda.Event()
+        entry.record(s.compute)
+        freed: List[torch.cuda.Event] = [entry, entry]
 
         def upload(i: int) -> torch.cuda.Event:
             k, pid = i % 2, pids[i]
             b = g.partition_sizes[pid]
             st = s.h2d[k % len(s.h2d)]
-            if freed[k] is not None:
-                st.wait_event(freed[k])
+            st.wait_event(freed[k])
             with torch.cuda.stream(st):
                 with KernelTimer.region("x_upload", 4 * b * din, 0, din):
                     bufs[k][:b].copy_(host[pid], non_blocking=True)

@@ -54,13 +54,11 @@ class GCN(GriNNderModel):
                 and not (self.residual and tuple(x.shape) == out_shape))
 
     def input_projection(self, layer: int):
-        """A GCNConv that multiplies first applies lin to every gathered row
-        before anything else (dropout acts on layer outputs).  Not for
-        aggregate-first layers, or when the residual add could need x itself
-        (in == out)."""
+        """GCNConv computes A (x Wᵀ) + b (in the order PyG uses; an
+        aggregate-first layer's (A x) Wᵀ + b is the same function), and
+        dropout acts on layer outputs, so x enters only through x Wᵀ - unless
+        the residual add needs x itself (in == out)."""
         conv = self.convs[layer]
-        if conv.aggregate_first():
-            return None
         if self.residual and conv.in_channels == conv.out_channels:
             return None
         return conv.lin.weight

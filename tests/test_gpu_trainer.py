@@ -270,11 +270,10 @@ def test_buffers_released_and_loss_decreases(gpu):
 @pytest.mark.parametrize("model_kind", ["gcn", "gat"])
 @pytest.mark.parametrize("pool_size", [1, 2])
 def test_projected_layers_match_gathered(gpu, model_kind, pool_size):
-    """config.project_first: layers that start with a narrowing projection
-    (here layer 0, 24 -> 16 or 8, and the last layer, 16 or 8 -> 4) run on
-    projected rows Z = x Wᵀ held in HBM; loss and gradients equal those of the
-    reference flow that gathers input rows (project_first='off') within the
-    1e-5 bound, and evaluate() agrees too."""
+    """config.project_first: every layer runs on projected rows Z = x Wᵀ held
+    in HBM (narrowing, equal and widening projections); loss and gradients
+    equal those of the reference flow that gathers input rows
+    (project_first='off') within the 1e-5 bound, and evaluate() agrees too."""
     data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
     torch.manual_seed(3)
     if model_kind == "gcn":
@@ -292,7 +291,7 @@ def test_projected_layers_match_gathered(gpu, model_kind, pool_size):
         trainer = Trainer(model, graph, config)
         opt = torch.optim.SGD(model.parameters(), lr=0.0)
         metrics = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
-        assert trainer.projected_layers == ([0, 2] if proj == "auto" else [])
+        assert trainer.projected_layers == ([0, 1, 2] if proj == "auto" else [])
         grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()
                  if p.grad is not None}
         ev = trainer.evaluate(torch.nn.CrossEntropyLoss())
@@ -307,7 +306,7 @@ def test_projected_layers_match_gathered(gpu, model_kind, pool_size):
 
 def test_projected_layers_match_dense_vanilla(gpu):
     """The projected flow (layer 0 24 -> 16, last layer 16 -> 3, padded to 4)
-    against the float64 dense GCN."""
+    against the float64 dense GCN, and a widening first layer (8 -> 16)."""
     data = _graph_data(feat=24)
     torch.manual_seed(7)
     make = lambda: GCN(24, 16, 3, num_layers=2, dropout=0.0, norm=True)  # noqa: E731
@@ -318,3 +317,44 @@ def test_projected_layers_match_dense_vanilla(gpu):
     assert abs(loss - ref_loss) < 1e-5
     for k, err in grad_errs(grads, ref_grads).items():
         assert err <= 1e-5, (k, err)
+    data = _graph_data(feat=8)
+    make = lambda: GCN(8, 16, 3, num_layers=2, dropout=0.0, norm=True)  # noqa: E731
+    state = make().state_dict()
+    ref_loss, ref_grads = _vanilla(data, state, make)
+    loss, grads, trainer, _ = _step(data, state, make, 4, "grinnder")
+    assert trainer.projected_layers == [0, 1]
+    assert abs(loss - ref_loss) < 1e-5
+    for k, err in grad_errs(grads, ref_grads).items():
+        assert err <= 1e-5, (k, err)
+
+
+@pytest.mark.parametrize("project_first", ["off", "auto"])
+def test_dropped_trainer_releases_pinned_memory(gpu, project_first):
+    """A Trainer's pinned host buffers are released when the last reference
+    to it goes, by reference counting alone (the cyclic collector is off
+    here), so a second trainer in the same process does not find the
+    first one's pinned memory still mapped."""
+    import gc
+
+    from grinnder_amd.buffer.host import PINNED_STATS
+
+    data = _graph_data(n=60, reach=3, feat=24, classes=4)
+    make = lambda: GCN(24, 16, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
+    gc.collect()
+    before = dict(PINNED_STATS)
+    gc.disable()
+    try:
+        ei, x, y, tr, va, te = data
+        config = GriNNderConfig(num_parts=4, project_first=project_first)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        trainer = Trainer(model, graph, config)
+        trainer.train_epoch(torch.optim.SGD(model.parameters(), lr=0.1),
+                            torch.nn.CrossEntropyLoss())
+        torch.cuda.synchronize()
+        assert PINNED_STATS["bytes"] > before["bytes"]
+        del trainer, model, graph
+        assert PINNED_STATS["bytes"] == before["bytes"]
+        assert PINNED_STATS["blocks"] == before["blocks"]
+    finally:
+        gc.enable()
