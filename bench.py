@@ -303,7 +303,7 @@ def main():
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f}); "
-        f"projected layers {trainer.projected_layers}")
+        f"projected layers {trainer.projected_layers}, inputs kept in HBM {trainer.resident_inputs}")
     if cfg["num_parts"] > 1:
         from grinnder_amd.buffer.host import PINNED_STATS
         log(f"pinned host memory {PINNED_STATS['bytes'] / 2**30:.1f} GiB, "
@@ -380,7 +380,8 @@ def main():
                    "num_classes": cfg["num_classes"], "num_layers": cfg["num_layers"],
                    "num_parts": cfg["num_parts"], "model": cfg["model"],
                    "halo_amplification": round(graph.halo_amplification(), 4),
-                   "projected_layers": trainer.projected_layers},
+                   "projected_layers": trainer.projected_layers,
+                   "resident_inputs": trainer.resident_inputs},
         "epoch_s": round(epoch_s, 5),
         "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,
         "agg_kernel_gteps": round(sum(r.edges for r in recs_agg) / (agg_ms / 1e3) / 1e9, 4),

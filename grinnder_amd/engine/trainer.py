@@ -42,7 +42,7 @@ uploads.
 
 from __future__ import annotations
 
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Set
 
 import torch
 from torch import Tensor
@@ -100,13 +100,16 @@ class Trainer:
         self._pid_to_loss_idx: Dict[int, int] = {}
         self._resident: Dict[str, Tensor] = {}
         self._label_cache: Dict[int, tuple] = {}
-        # Projected layers: their W this epoch; Z, dZ per layer and two upload
-        # buffers per input width, kept across epochs; the device row ids of
-        # each partition's gathered rows.
+        # Projected layers: their W this epoch; Z, dZ per layer, two upload
+        # buffers per input width and the HBM-resident inputs, kept across
+        # epochs; the layers whose inputs stay in HBM this epoch; the device
+        # row ids of each partition's gathered rows.
         self._proj: Dict[int, Tensor] = {}
         self._zbufs: Dict[int, Tensor] = {}
         self._dzbufs: Dict[int, Tensor] = {}
         self._xbufs: Dict[int, List[Tensor]] = {}
+        self._xres: Dict[int, Tensor] = {}
+        self._xin: Set[int] = set()
         self._grow: Dict[int, Tensor] = {}
         if not self._fast:
             for l in range(L + 1):
@@ -282,6 +285,11 @@ class Trainer:
     def projected_layers(self) -> List[int]:
         return sorted(self._proj)
 
+    @property
+    def resident_inputs(self) -> List[int]:
+        """Projected layers whose input rows stay in HBM this epoch."""
+        return sorted(self._xin)
+
     def _plan_projection(self) -> Dict[int, Tensor]:
         """Layers this epoch runs projected, with their input projection W:
         grinnder mode, every partition on this trainer, and room in HBM for
@@ -289,8 +297,14 @@ class Trainer:
         working set).  A projected layer moves 2 N d_in bytes over the host
         link (two uploads of its input rows) instead of 2 E d_in of gathers
         and, above layer 0, an E d_in read-add-write scatter; when HBM is
-        short, layers with the most input width per byte of Z go first."""
+        short, layers with the most input width per byte of Z go first.
+
+        Also decides self._xin: the projected layers above layer 0 whose input
+        rows x (produced on the device by the layer below) stay in HBM with
+        what room is left, so that neither the D2H of x nor the upload for
+        dW = sum_p dZ_pᵀ x_p crosses the host link."""
         cfg, g = self.config, self.graph
+        self._xin = set()
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
             return {}
@@ -311,7 +325,28 @@ class Trainer:
                     continue
                 free -= need
             plan[layer] = w
+        for layer in sorted(plan):
+            if layer == 0:
+                continue
+            if layer not in self._xres:
+                if free is None:
+                    free, _ = torch.cuda.mem_get_info(self.device)
+                need = 4 * n * plan[layer].size(1)
+                if need + (8 << 30) > free:
+                    continue
+                free -= need
+            self._xin.add(layer)
         return dict(sorted(plan.items()))
+
+    def _xres_buf(self, layer: int) -> Tensor:
+        """HBM copy of layer `layer`'s input rows (all partitions, in order)."""
+        x = self._xres.get(layer)
+        if x is None:
+            with torch.cuda.stream(self.streams.compute):
+                x = torch.empty(int(self.graph.ptr[-1]), self._proj[layer].size(1),
+                                device=self.device)
+            self._xres[layer] = x
+        return x
 
     def _zbuf(self, layer: int) -> Tensor:
         z = self._zbufs.get(layer)
@@ -469,7 +504,14 @@ class Trainer:
             with dense_region("dw", hi - lo, w.size(0), w.size(1)):
                 gemm_tn(dz[lo:hi], xp, out=dw, beta=1.0)
 
-        self._each_input_partition(layer, accumulate)
+        if layer in self._xin:
+            x = self._xres[layer]
+            with torch.cuda.stream(s.compute):
+                for pid in pids:
+                    lo, hi = g._range(pid)
+                    accumulate(pid, x[lo:hi], lo, hi)
+        else:
+            self._each_input_partition(layer, accumulate)
         with torch.cuda.stream(s.compute):
             if w.grad is None:
                 w.grad = dw
@@ -482,13 +524,17 @@ class Trainer:
     def _forward_layer(self, layer: int) -> None:
         """Per partition: the layer's output from gathered input rows (the
         reference's flow) or from gathered rows of Z (a projected layer), D2H
-        into the next layer's host buffer, and, when the next layer runs
+        into the next layer's host buffer (or, when the next layer's input
+        stays in HBM, a device copy into it), and, when the next layer runs
         projected, its rows of Z_{layer+1} = out Wᵀ formed right away."""
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
         projected = layer in self._proj
         w_next = self._proj.get(layer + 1)
+        if (layer + 1) in self._xin:
+            self._forward_layer_resident(layer)
+            return
         if projected and layer == 0:
             self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
         if not projected:
@@ -528,6 +574,46 @@ class Trainer:
             last = (len(pids) - 1) % pool
             self.host_features[layer + 1].d2h_synchronize(s.d2h[last])
             self._free(self.activations[layer][pids[-1]])
+
+    def _forward_layer_resident(self, layer: int) -> None:
+        """_forward_layer when the next layer is projected and its input rows
+        stay in HBM: each partition's output goes to Z_{layer+1} and to the
+        resident copy of x_{layer+1}, and nothing crosses to the host."""
+        g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
+        projected = layer in self._proj
+        x_next = self._xres_buf(layer + 1)
+        if projected and layer == 0:
+            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+        if not projected:
+            self._gather(layer, pids[0], s.h2d[0])
+        for i, pid in enumerate(pids):
+            k = i % pool
+            if not projected:
+                self.device_features[layer].h2d_synchronize(s.h2d[k])
+                s.compute.wait_stream(s.h2d[k])
+            with torch.cuda.stream(s.compute):
+                if not projected:
+                    if i + 1 < len(pids) and pool > 1:
+                        self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
+                    out = self._checkpointed(layer, pid, k)
+                else:
+                    with torch.no_grad():
+                        out = self.model.forward_projected(
+                            layer, self._gather_projected(layer, pid),
+                            g.adjacency(pid)).contiguous()
+                lo, hi = g._range(pid)
+                self._project_rows(layer + 1, out, lo, hi)
+                with torch.no_grad():
+                    x_next[lo:hi].copy_(out)
+                # The storage goes back to the allocator in stream order; a
+                # reference-flow layer keeps the tensor for its backward, which
+                # recomputes it.
+                self.activations[layer][pid] = out
+                self._free(out)
+                if not projected:
+                    self.device_features[layer].release(pid)
+            if pool == 1 and not projected and i + 1 < len(pids):
+                self._gather(layer, pids[i + 1], s.h2d[0])
 
     # ---------------------------------------------------------------- loss
 
