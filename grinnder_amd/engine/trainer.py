@@ -299,10 +299,13 @@ class Trainer:
         and, above layer 0, an E d_in read-add-write scatter; when HBM is
         short, layers with the most input width per byte of Z go first.
 
-        Also decides self._xin: the projected layers above layer 0 whose input
-        rows x (produced on the device by the layer below) stay in HBM with
-        what room is left, so that neither the D2H of x nor the upload for
-        dW = sum_p dZ_pᵀ x_p crosses the host link."""
+        Also decides self._xin, with what room is left: the projected layers
+        whose input rows x stay in HBM for the epoch.  Above layer 0, x is
+        produced on the device by the layer below, so neither its D2H nor the
+        upload for dW = sum_p dZ_pᵀ x_p crosses the host link; layer 0's rows
+        are uploaded once per epoch, for the projection, and kept for dW
+        instead of being uploaded a second time.  Layers above 0 go first
+        (each of their bytes saves two crossings)."""
         cfg, g = self.config, self.graph
         self._xin = set()
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
@@ -325,9 +328,7 @@ class Trainer:
                     continue
                 free -= need
             plan[layer] = w
-        for layer in sorted(plan):
-            if layer == 0:
-                continue
+        for layer in sorted(plan, key=lambda l: (l == 0, l)):
             if layer not in self._xres:
                 if free is None:
                     free, _ = torch.cuda.mem_get_info(self.device)
@@ -399,10 +400,15 @@ class Trainer:
     def _each_input_partition(self, layer: int, fn) -> None:
         """fn(pid, x_p, lo, hi) on the compute stream for every partition,
         x_p = the partition's rows of the host buffer of layer `layer`'s
-        inputs, uploaded to HBM; two buffers, so the next upload overlaps fn."""
+        inputs, uploaded to HBM: into the layer's resident input buffer when
+        it has one this epoch, else through two buffers, so that the next
+        upload overlaps fn."""
         g, s, pids = self.graph, self.streams, self._my_pids
         host = self.host_features[layer]
         din = host.embedding_dim
+        if layer in self._xin:
+            self._upload_resident(layer, fn)
+            return
         bufs = self._xbufs.get(din)
         if bufs is None:
             with torch.cuda.stream(s.compute):
@@ -442,6 +448,37 @@ class Trainer:
                 ev.record(s.compute)
                 freed[k] = ev
             ready = nxt
+
+    def _upload_resident(self, layer: int, fn) -> None:
+        """_each_input_partition into the resident input buffer: every
+        partition has its own rows there, so the uploads run back to back on
+        the two H2D streams and fn(p) waits only for partition p's upload."""
+        g, s, pids = self.graph, self.streams, self._my_pids
+        host = self.host_features[layer]
+        x = self._xres_buf(layer)
+        din = x.size(1)
+        # The buffer may be new (its memory just freed by queued compute work)
+        # or still read by the previous epoch's dW pass: uploads wait for the
+        # compute stream's queued work first.
+        entry = torch.cuda.Event()
+        entry.record(s.compute)
+        for st in s.h2d[:2]:
+            st.wait_event(entry)
+        ready: List[torch.cuda.Event] = []
+        for i, pid in enumerate(pids):
+            lo, hi = g._range(pid)
+            st = s.h2d[i % min(2, len(s.h2d))]
+            with torch.cuda.stream(st):
+                with KernelTimer.region("x_upload", 4 * (hi - lo) * din, 0, din):
+                    x[lo:hi].copy_(host[pid], non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record(st)
+            ready.append(ev)
+        for i, pid in enumerate(pids):
+            s.compute.wait_event(ready[i])
+            with torch.cuda.stream(s.compute):
+                lo, hi = g._range(pid)
+                fn(pid, x[lo:hi], lo, hi)
 
     def _device_grad(self, layer: int, pid: int) -> Tensor:
         """dL/d(x_layer) of partition pid's rows when layer `layer` runs

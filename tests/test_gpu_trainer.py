@@ -267,29 +267,32 @@ def test_buffers_released_and_loss_decreases(gpu):
         assert 0.0 <= ev["val_acc"] <= 1.0
 
 
-def _without_resident_inputs(monkeypatch):
-    """Plans projected layers as usual but keeps every layer input on the
-    host, as when HBM has no room for them: dW then comes from uploads."""
+def _limit_resident_inputs(monkeypatch, keep):
+    """Plans projected layers as usual but keeps only the inputs of layers in
+    `keep` in HBM, as when HBM has no room for the others: their dW then
+    comes from uploads (a second one, for layer 0)."""
     plan = Trainer._plan_projection
 
-    def no_resident(self):
+    def limited(self):
         out = plan(self)
-        self._xin = set()
+        self._xin = {l for l in self._xin if l in keep}
         return out
-    monkeypatch.setattr(Trainer, "_plan_projection", no_resident)
+    monkeypatch.setattr(Trainer, "_plan_projection", limited)
 
 
 @pytest.mark.parametrize("model_kind", ["gcn", "gat"])
 @pytest.mark.parametrize("pool_size", [1, 2])
-@pytest.mark.parametrize("resident", [True, False])
+@pytest.mark.parametrize("resident", ["all", "above0", "none"])
 def test_projected_layers_match_gathered(gpu, model_kind, pool_size, resident, monkeypatch):
     """config.project_first: every layer runs on projected rows Z = x Wᵀ held
-    in HBM (narrowing, equal and widening projections), with the inputs of
-    layers 1 and 2 kept in HBM or taken from the host; loss and gradients
-    equal those of the reference flow that gathers input rows
-    (project_first='off') within the 1e-5 bound, and evaluate() agrees too."""
-    if not resident:
-        _without_resident_inputs(monkeypatch)
+    in HBM (narrowing, equal and widening projections), with the layer inputs
+    kept in HBM for the epoch (all, those above layer 0, or none: uploads);
+    loss and gradients equal those of the reference flow that gathers input
+    rows (project_first='off') within the 1e-5 bound, and evaluate() agrees
+    too."""
+    kept = {"all": [0, 1, 2], "above0": [1, 2], "none": []}[resident]
+    if resident != "all":
+        _limit_resident_inputs(monkeypatch, set(kept))
     data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
     torch.manual_seed(3)
     if model_kind == "gcn":
@@ -308,7 +311,7 @@ def test_projected_layers_match_gathered(gpu, model_kind, pool_size, resident, m
         opt = torch.optim.SGD(model.parameters(), lr=0.0)
         metrics = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
         assert trainer.projected_layers == ([0, 1, 2] if proj == "auto" else [])
-        assert trainer.resident_inputs == ([1, 2] if proj == "auto" and resident else [])
+        assert trainer.resident_inputs == (kept if proj == "auto" else [])
         grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()
                  if p.grad is not None}
         ev = trainer.evaluate(torch.nn.CrossEntropyLoss())
@@ -382,8 +385,8 @@ def test_dropped_trainer_releases_pinned_memory(gpu, project_first):
 def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, monkeypatch):
     """The projected flow against the reference flow on a graph large enough
     that the dW pass's uploads run while compute work is still queued
-    (300k nodes, 8 partitions, widths 128/256), with the inputs of layers
-    above 0 kept in HBM or uploaded from the host: the loss agrees to 1e-6,
+    (300k nodes, 8 partitions, widths 128/256), with the layer inputs kept
+    in HBM for the epoch or uploaded again for dW: the loss agrees to 1e-6,
     gradients to 1e-3 of their largest entry (sums over 180k training rows in
     fp32 on both sides: the reference flow itself differs from a float64
     computation by up to ~3e-4 at this scale), and two projected epochs give
@@ -391,7 +394,7 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     from grinnder_amd.data import synthetic
 
     if not resident:
-        _without_resident_inputs(monkeypatch)
+        _limit_resident_inputs(monkeypatch, set())
     n = 300_000
     ei = synthetic.uniform_graph(n, 3_000_000, seed=5)
     nd = synthetic.node_data(n, 128, 16, seed=5)
