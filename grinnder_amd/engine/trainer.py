@@ -61,6 +61,23 @@ from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.loss import check_stats, mask_codes, masked_cross_entropy
 
 
+class _GatherRows(torch.autograd.Function):
+    """z = Z[rows] for a projected layer; the backward adds dL/dz into the
+    layer's dZ buffer at the same rows (distinct within a partition) instead
+    of returning a gradient for Z.  `token` is a zero-element tensor that
+    requires grad, so that autograd records the gather although Z does not."""
+
+    @staticmethod
+    def forward(ctx, token: Tensor, z: Tensor, rows: Tensor, dz: Tensor) -> Tensor:
+        ctx.rows, ctx.dz = rows, dz
+        return z.index_select(0, rows)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        ctx.dz.index_add_(0, ctx.rows, grad)
+        return None, None, None, None
+
+
 class Trainer:
     def __init__(self, model: GriNNderModel, graph: PartitionedGraph, config: GriNNderConfig,
                  partition_range: Optional[tuple] = None):
@@ -111,6 +128,13 @@ class Trainer:
         self._xres: Dict[int, Tensor] = {}
         self._xin: Set[int] = set()
         self._grow: Dict[int, Tensor] = {}
+        # Projected layers whose forward graphs are kept until their backward
+        # this epoch (instead of being recomputed), the kept outputs, and the
+        # RNG state each recomputed partition's forward started from.
+        self._keep: Set[int] = set()
+        self._graphs: Dict[int, Dict[int, Tensor]] = {}
+        self._rng: Dict[tuple, Tensor] = {}
+        self._token: Optional[Tensor] = None
         if not self._fast:
             for l in range(L + 1):
                 self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
@@ -144,6 +168,8 @@ class Trainer:
         for acts in self.activations:
             for i in range(len(acts)):
                 acts[i] = None
+        self._graphs = {}
+        self._rng = {}
 
     def train_epoch(self, optimizer: torch.optim.Optimizer,
                     criterion: torch.nn.Module) -> Dict[str, float]:
@@ -337,6 +363,27 @@ class Trainer:
                     continue
                 free -= need
             self._xin.add(layer)
+        # Kept forward graphs (training only): a projected layer below the
+        # last whose output feeds a resident input keeps each partition's
+        # autograd graph until its backward, which then skips the recompute
+        # (an aggregation pass and a gather of Z per partition).  What the
+        # graph holds is bounded by the gathered rows, three [N, d_out]
+        # tensors and one float per edge.
+        self._keep = set()
+        if self.model.training:
+            sum_e = sum(g.expanded_sizes)
+            nnz = sum(int(a[1].numel()) for a in g.adj_csr)
+            for layer in sorted(plan):
+                if layer + 1 not in self._xin:
+                    continue
+                d = plan[layer].size(0)
+                if free is None:
+                    free, _ = torch.cuda.mem_get_info(self.device)
+                need = 4 * (sum_e * d + 3 * n * d + nnz)
+                if need + (8 << 30) > free:
+                    continue
+                free -= need
+                self._keep.add(layer)
         return dict(sorted(plan.items()))
 
     def _xres_buf(self, layer: int) -> Tensor:
@@ -384,12 +431,52 @@ class Trainer:
             self._grow[pid] = idx
         return idx
 
-    def _gather_projected(self, layer: int, pid: int) -> Tensor:
+    def _gather_projected(self, layer: int, pid: int, grad: bool = False) -> Tensor:
+        """Partition pid's gathered rows of Z_layer; with grad, the backward
+        adds their gradient into dZ_layer."""
         rows = self._global_rows(pid)
         z = self._zbufs[layer]
         d = z.size(1)
         with KernelTimer.region("z_gather", 2 * 4 * rows.numel() * d, 0, d):
-            return z.index_select(0, rows)
+            if not grad:
+                return z.index_select(0, rows)
+            if self._token is None:
+                self._token = torch.zeros(0, device=self.device, requires_grad=True)
+            return _GatherRows.apply(self._token, z, rows, self._dzbuf(layer))
+
+    def _projected_forward(self, layer: int, pid: int) -> Tensor:
+        """The forward of a projected layer on partition pid: with its graph
+        kept when the layer is in self._keep, else without autograd, noting
+        the RNG state so that the backward's recompute draws the same dropout
+        masks (as torch.utils.checkpoint does in the reference's flow)."""
+        adj = self.graph.adjacency(pid)
+        if layer in self._keep:
+            with torch.enable_grad():
+                out = self.model.forward_projected(
+                    layer, self._gather_projected(layer, pid, grad=True), adj)
+            self._graphs.setdefault(layer, {})[pid] = out
+            return out
+        if self.model.training:
+            self._rng[(layer, pid)] = torch.cuda.get_rng_state(self._device_index())
+        with torch.no_grad():
+            return self.model.forward_projected(
+                layer, self._gather_projected(layer, pid), adj).contiguous()
+
+    def _device_index(self) -> int:
+        return self.device.index if self.device.index is not None else torch.cuda.current_device()
+
+    def _projected_recompute(self, layer: int, pid: int) -> Tensor:
+        """The partition's forward again, with autograd, from the RNG state
+        its first forward started from; the global RNG stream is left as it
+        was."""
+        state = self._rng.pop((layer, pid), None)
+        dev = self._device_index()
+        with torch.random.fork_rng(devices=[dev]), torch.enable_grad():
+            if state is not None:
+                torch.cuda.set_rng_state(state, dev)
+            return self.model.forward_projected(
+                layer, self._gather_projected(layer, pid, grad=True),
+                self.graph.adjacency(pid))
 
     def _project_rows(self, layer: int, x: Tensor, lo: int, hi: int) -> None:
         """Z_layer[lo:hi] = x Wᵀ (no autograd)."""
@@ -490,9 +577,10 @@ class Trainer:
             return torch.mm(self._dzbufs[layer][lo:hi], w.detach())
 
     def _backward_projected(self, layer: int) -> None:
-        """Backward of a projected layer: per partition, recompute the layer
-        from its gathered rows of Z and backpropagate into the layer's
-        parameters and into dZ; then dW = sum_p dZ_pᵀ x_p."""
+        """Backward of a projected layer: per partition, take the forward's
+        kept graph or recompute the layer from its gathered rows of Z, and
+        backpropagate into the layer's parameters and into dZ; then
+        dW = sum_p dZ_pᵀ x_p."""
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
@@ -514,23 +602,23 @@ class Trainer:
             with torch.cuda.stream(s.compute):
                 if from_host and i + 1 < len(pids) and pool > 1:
                     self._upload_grad(layer + 1, pids[i + 1], s.h2d[(i + 1) % pool])
-                z = self._gather_projected(layer, pid).requires_grad_(True)
-                with torch.enable_grad():
-                    out = self.model.forward_projected(layer, z, g.adjacency(pid))
-                    if last:
-                        y, codes = self._labels_and_codes(pid)
-                        loss, _ = masked_cross_entropy(out, y, codes, "sum")
+                out = self._graphs.get(layer, {}).pop(pid, None)
+                if out is None:
+                    out = self._projected_recompute(layer, pid)
                 if last:
+                    y, codes = self._labels_and_codes(pid)
+                    with torch.enable_grad():
+                        loss, _ = masked_cross_entropy(out, y, codes, "sum")
                     loss.backward()
                 elif from_device:
                     out.backward(self._device_grad(layer + 1, pid))
                 else:
                     out.backward(gbuf[pid])
                     gbuf.release(pid)
-                # Rows are distinct within one partition, so each element of
-                # dZ gets one addition per partition, in partition order.
-                dz.index_add_(0, self._global_rows(pid), z.grad)
-                del z, out
+                # The gather's backward added dL/dz into dZ at the partition's
+                # rows (distinct within one partition): each element of dZ
+                # gets one addition per partition, in partition order.
+                del out
                 self.activations[layer][pid] = None
             if from_host and pool == 1 and i + 1 < len(pids):
                 self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])
@@ -587,10 +675,7 @@ class Trainer:
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
                 else:
-                    with torch.no_grad():
-                        out = self.model.forward_projected(
-                            layer, self._gather_projected(layer, pid),
-                            g.adjacency(pid)).contiguous()
+                    out = self._projected_forward(layer, pid)
                 if w_next is not None:
                     lo, hi = g._range(pid)
                     self._project_rows(layer + 1, out, lo, hi)
@@ -634,19 +719,17 @@ class Trainer:
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
                 else:
-                    with torch.no_grad():
-                        out = self.model.forward_projected(
-                            layer, self._gather_projected(layer, pid),
-                            g.adjacency(pid)).contiguous()
+                    out = self._projected_forward(layer, pid)
                 lo, hi = g._range(pid)
                 self._project_rows(layer + 1, out, lo, hi)
                 with torch.no_grad():
                     x_next[lo:hi].copy_(out)
-                # The storage goes back to the allocator in stream order; a
-                # reference-flow layer keeps the tensor for its backward, which
-                # recomputes it.
-                self.activations[layer][pid] = out
-                self._free(out)
+                if layer not in self._keep:
+                    # The storage goes back to the allocator in stream order; a
+                    # reference-flow layer keeps the tensor for its backward,
+                    # which recomputes it.  A kept graph keeps its output.
+                    self.activations[layer][pid] = out
+                    self._free(out)
                 if not projected:
                     self.device_features[layer].release(pid)
             if pool == 1 and not projected and i + 1 < len(pids):

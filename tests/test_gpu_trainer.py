@@ -423,3 +423,62 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     for k, err in grad_errs(g1, g0).items():
         assert err <= 1e-3, (k, err)
     assert all(torch.equal(g1[k], g2[k]) for k in g1)
+
+
+def _no_kept_graphs(monkeypatch):
+    """Plans as usual but recomputes every projected layer in its backward."""
+    plan = Trainer._plan_projection
+
+    def recompute(self):
+        out = plan(self)
+        self._keep = set()
+        return out
+    monkeypatch.setattr(Trainer, "_plan_projection", recompute)
+
+
+@pytest.mark.parametrize("flow", ["reference", "kept_graph", "recompute"])
+def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
+    """With dropout active, the backward must see the masks the forward drew:
+    the reference flow's checkpoint restores the RNG state, a projected layer
+    either keeps its forward graph or recomputes from the RNG state its
+    forward started from.  Every epoch below starts from the same seed, so
+    its forward draws the same masks and the reported loss is one smooth
+    function of the weights: its central difference along the gradient must
+    equal the gradient's norm (a backward that drew new masks is off by tens
+    of percent)."""
+    data = _graph_data(n=60, reach=3, feat=24, classes=4)
+    ei, x, y, tr, va, te = data
+    if flow == "recompute":
+        _no_kept_graphs(monkeypatch)
+    torch.manual_seed(5)
+    model = GCN(24, 32, 4, num_layers=3, dropout=0.5, norm=True).cuda()
+    config = GriNNderConfig(num_parts=4, project_first="off" if flow == "reference" else "auto")
+    graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+    trainer = Trainer(model, graph, config)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    crit = torch.nn.CrossEntropyLoss()
+
+    def epoch():
+        torch.manual_seed(123)
+        return trainer.train_epoch(opt, crit)["loss"]
+
+    epoch()
+    if flow == "reference":
+        assert trainer.projected_layers == []
+    else:
+        assert trainer.projected_layers == [0, 1, 2]
+        assert sorted(trainer._keep) == ([0, 1] if flow == "kept_graph" else [])
+    w = model.convs[1].lin.weight
+    g = w.grad.detach().clone()
+    v = g / g.norm()
+    delta = 1e-2
+    with torch.no_grad():
+        w.add_(delta * v)
+    up = epoch()
+    with torch.no_grad():
+        w.sub_(2 * delta * v)
+    down = epoch()
+    with torch.no_grad():
+        w.add_(delta * v)
+    fd = (up - down) / (2 * delta)
+    assert abs(fd - float(g.norm())) <= 2e-3 * float(g.norm()) + 1e-4, (fd, float(g.norm()))
