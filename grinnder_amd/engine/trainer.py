@@ -363,18 +363,20 @@ class Trainer:
                     continue
                 free -= need
             self._xin.add(layer)
-        # Kept forward graphs (training only): a projected layer below the
-        # last whose output feeds a resident input keeps each partition's
+        # Kept forward graphs (training only): a projected layer whose output
+        # feeds a resident input, or the last layer, keeps each partition's
         # autograd graph until its backward, which then skips the recompute
-        # (an aggregation pass and a gather of Z per partition).  What the
-        # graph holds is bounded by the gathered rows, three [N, d_out]
-        # tensors and one float per edge.
+        # (an aggregation pass and a gather of Z per partition); the last
+        # layer's loss is then taken from the kept logits, which no longer
+        # go through host memory.  What a graph holds is bounded by the
+        # gathered rows, three [N, d_out] tensors and one float per edge.
         self._keep = set()
         if self.model.training:
             sum_e = sum(g.expanded_sizes)
             nnz = sum(int(a[1].numel()) for a in g.adj_csr)
+            last = self.model.num_layers - 1
             for layer in sorted(plan):
-                if layer + 1 not in self._xin:
+                if layer + 1 not in self._xin and layer != last:
                     continue
                 d = plan[layer].size(0)
                 if free is None:
@@ -444,13 +446,13 @@ class Trainer:
                 self._token = torch.zeros(0, device=self.device, requires_grad=True)
             return _GatherRows.apply(self._token, z, rows, self._dzbuf(layer))
 
-    def _projected_forward(self, layer: int, pid: int) -> Tensor:
+    def _projected_forward(self, layer: int, pid: int, keep: bool) -> Tensor:
         """The forward of a projected layer on partition pid: with its graph
-        kept when the layer is in self._keep, else without autograd, noting
-        the RNG state so that the backward's recompute draws the same dropout
-        masks (as torch.utils.checkpoint does in the reference's flow)."""
+        kept for the backward (keep), else without autograd, noting the RNG
+        state so that the backward's recompute draws the same dropout masks
+        (as torch.utils.checkpoint does in the reference's flow)."""
         adj = self.graph.adjacency(pid)
-        if layer in self._keep:
+        if keep:
             with torch.enable_grad():
                 out = self.model.forward_projected(
                     layer, self._gather_projected(layer, pid, grad=True), adj)
@@ -576,7 +578,7 @@ class Trainer:
         with dense_region("dx", hi - lo, w.size(0), w.size(1)):
             return torch.mm(self._dzbufs[layer][lo:hi], w.detach())
 
-    def _backward_projected(self, layer: int) -> None:
+    def _backward_projected(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
         """Backward of a projected layer: per partition, take the forward's
         kept graph or recompute the layer from its gathered rows of Z, and
         backpropagate into the layer's parameters and into dZ; then
@@ -603,18 +605,23 @@ class Trainer:
                 if from_host and i + 1 < len(pids) and pool > 1:
                     self._upload_grad(layer + 1, pids[i + 1], s.h2d[(i + 1) % pool])
                 out = self._graphs.get(layer, {}).pop(pid, None)
-                if out is None:
+                if last and out is not None:
+                    # Kept logits: _compute_losses formed the loss from them.
+                    losses[self._pid_to_loss_idx[pid]].backward()
+                elif last:
                     out = self._projected_recompute(layer, pid)
-                if last:
                     y, codes = self._labels_and_codes(pid)
                     with torch.enable_grad():
                         loss, _ = masked_cross_entropy(out, y, codes, "sum")
                     loss.backward()
-                elif from_device:
-                    out.backward(self._device_grad(layer + 1, pid))
                 else:
-                    out.backward(gbuf[pid])
-                    gbuf.release(pid)
+                    if out is None:
+                        out = self._projected_recompute(layer, pid)
+                    if from_device:
+                        out.backward(self._device_grad(layer + 1, pid))
+                    else:
+                        out.backward(gbuf[pid])
+                        gbuf.release(pid)
                 # The gather's backward added dL/dz into dZ at the partition's
                 # rows (distinct within one partition): each element of dZ
                 # gets one addition per partition, in partition order.
@@ -662,6 +669,13 @@ class Trainer:
             return
         if projected and layer == 0:
             self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+        if layer in self._keep and layer == self.model.num_layers - 1:
+            # The last layer with its graphs kept: the loss reads the logits
+            # from them (_compute_losses), so nothing goes to the host.
+            for pid in pids:
+                with torch.cuda.stream(s.compute):
+                    self._projected_forward(layer, pid, keep=True)
+            return
         if not projected:
             self._gather(layer, pids[0], s.h2d[0])
         for i, pid in enumerate(pids):
@@ -675,7 +689,7 @@ class Trainer:
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
                 else:
-                    out = self._projected_forward(layer, pid)
+                    out = self._projected_forward(layer, pid, keep=False)
                 if w_next is not None:
                     lo, hi = g._range(pid)
                     self._project_rows(layer + 1, out, lo, hi)
@@ -719,12 +733,12 @@ class Trainer:
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
                 else:
-                    out = self._projected_forward(layer, pid)
+                    out = self._projected_forward(layer, pid, keep=layer in self._keep)
                 lo, hi = g._range(pid)
                 self._project_rows(layer + 1, out, lo, hi)
                 with torch.no_grad():
                     x_next[lo:hi].copy_(out)
-                if layer not in self._keep:
+                if not (projected and layer in self._keep):
                     # The storage goes back to the allocator in stream order; a
                     # reference-flow layer keeps the tensor for its backward,
                     # which recomputes it.  A kept graph keeps its output.
@@ -754,15 +768,20 @@ class Trainer:
                 act.untyped_storage().resize_(act.numel() * act.element_size())
             self.host_features[-1].async_upload(pid, act, stream)
 
+        kept = last in self._keep and last in self._graphs
         with torch.cuda.stream(s.compute):
-            upload(pids[0], s.h2d[0])
+            if not kept:
+                upload(pids[0], s.h2d[0])
             for i, pid in enumerate(pids):
                 k = i % pool
-                self.host_features[-1].h2d_synchronize(s.h2d[k])
-                s.compute.wait_stream(s.h2d[k])
-                if i + 1 < len(pids):
-                    upload(pids[i + 1], s.h2d[(i + 1) % pool])
-                out = self.activations[last][pid]
+                if kept:
+                    out = self._graphs[last][pid]
+                else:
+                    self.host_features[-1].h2d_synchronize(s.h2d[k])
+                    s.compute.wait_stream(s.h2d[k])
+                    if i + 1 < len(pids):
+                        upload(pids[i + 1], s.h2d[(i + 1) % pool])
+                    out = self.activations[last][pid]
                 y, codes = self._labels_and_codes(pid)
                 # Sum over the partition's train rows (zero, with a zero
                 # gradient, when it has none); the accuracy counts ride along.
@@ -771,7 +790,8 @@ class Trainer:
                 losses.append(loss)
                 loss_sums.append(loss.detach())
                 stat_rows.append(stats)
-                self._free(out)
+                if not kept:
+                    self._free(out)
             st = torch.stack(stat_rows).sum(0).tolist()
             total_loss = float(torch.stack(loss_sums).double().sum())
         check_stats(st)
@@ -804,7 +824,7 @@ class Trainer:
     def _backward_last_layer(self, losses: List[Tensor]) -> None:
         layer = self.model.num_layers - 1
         if layer in self._proj:
-            self._backward_projected(layer)
+            self._backward_projected(layer, losses)
         else:
             self._backward_pass(layer,
                                 lambda pid: losses[self._pid_to_loss_idx[pid]].backward())

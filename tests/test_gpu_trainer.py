@@ -276,6 +276,8 @@ def _limit_resident_inputs(monkeypatch, keep):
     def limited(self):
         out = plan(self)
         self._xin = {l for l in self._xin if l in keep}
+        last = self.model.num_layers - 1
+        self._keep = {l for l in self._keep if l + 1 in self._xin or l == last}
         return out
     monkeypatch.setattr(Trainer, "_plan_projection", limited)
 
@@ -467,7 +469,7 @@ def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
         assert trainer.projected_layers == []
     else:
         assert trainer.projected_layers == [0, 1, 2]
-        assert sorted(trainer._keep) == ([0, 1] if flow == "kept_graph" else [])
+        assert sorted(trainer._keep) == ([0, 1, 2] if flow == "kept_graph" else [])
     w = model.convs[1].lin.weight
     g = w.grad.detach().clone()
     v = g / g.norm()
