@@ -133,15 +133,53 @@ def spmm(plan, idx: Tensor, val: Tensor, x: Tensor, rows: int,
     return out
 
 
+@dataclass
+class ProjectedSink:
+    """Where a projected layer's source rows live: the aggregation reads the
+    layer's whole Z (all partitions' rows, [N, d]) through `gidx`, the global
+    row of each CSR edge's source, instead of a gathered copy; the backward
+    adds Aᵀ G into `dz` ([N, d]) at `rows`, the global row of each of the
+    partition's E source rows (distinct), instead of returning a gradient for
+    Z.  `token` is a zero-element tensor that requires grad, so that autograd
+    records the aggregation although Z does not."""
+
+    dz: Tensor
+    gidx: Tensor
+    rows: Tensor
+    token: Tensor
+
+
+def spmm_into(plan, idx: Tensor, val: Tensor, x: Tensor, sink: ProjectedSink,
+              name: str = "gcn_bwd") -> None:
+    """sink.dz[sink.rows[r]] += sum_e val[e] * x[idx[e]] for the rows of `plan`."""
+    dim = x.size(1)
+    dz = sink.dz
+    if dz.size(1) != dim or not dz.is_contiguous():
+        raise ValueError("spmm_into: dz must be contiguous with the width of x")
+    rows = plan.rows
+    if sink.rows.numel() != rows:
+        raise ValueError(f"spmm_into: {sink.rows.numel()} row ids for {rows} rows")
+    ws = _workspace(plan.n_slots, dim, x.device)
+    nnz = idx.numel()
+    with KernelTimer.region(name, nnz * (4 * dim + 8) + rows * (8 * dim + 4), nnz, dim):
+        _lib.call("gr_gcn_aggregate_into", plan.units.data_ptr(), plan.n_units,
+                  plan.fixups.data_ptr() if plan.n_fix else None, plan.n_fix,
+                  idx.data_ptr(), val.data_ptr(), x.data_ptr(), x.stride(0),
+                  sink.rows.data_ptr(), dz.data_ptr(), dz.stride(0), rows, dim, _lib.ptr(ws),
+                  plan.n_slots, _lib.stream_handle())
+
+
 class _GCNAggregate(torch.autograd.Function):
     """Y = A Z + b forward; dZ = A^T G (CSC plan) and db = sum G backward."""
 
     @staticmethod
-    def forward(ctx, z: Tensor, bias: Optional[Tensor], plan: DevicePlan) -> Tensor:
+    def forward(ctx, z: Tensor, bias: Optional[Tensor], plan: DevicePlan,
+                sink: Optional[ProjectedSink] = None, token: Optional[Tensor] = None) -> Tensor:
         z = z.contiguous()
-        y = spmm(plan.fwd, plan.idx, plan.val, z, plan.num_dst,
+        y = spmm(plan.fwd, plan.idx if sink is None else sink.gidx, plan.val, z, plan.num_dst,
                  bias.contiguous() if bias is not None else None, name="gcn_fwd")
         ctx.plan = plan
+        ctx.sink = sink
         ctx.has_bias = bias is not None
         return y
 
@@ -150,19 +188,36 @@ class _GCNAggregate(torch.autograd.Function):
         plan: DevicePlan = ctx.plan
         gy = gy.contiguous()
         dz = None
-        if ctx.needs_input_grad[0]:
+        if ctx.sink is not None:
+            spmm_into(plan.bwd, plan.row_idx, plan.val_t, gy, ctx.sink)
+        elif ctx.needs_input_grad[0]:
             dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gy, plan.num_src, name="gcn_bwd")
         db = column_sum(gy) if (ctx.has_bias and ctx.needs_input_grad[1]) else None
-        return dz, db, None
+        return dz, db, None, None, None
 
 
-def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None) -> Tensor:
-    """GCN neighbour aggregation A·Z (+ bias) of one partition, on the GPU."""
+def _check_source(z: Tensor, plan: DevicePlan, sink: Optional[ProjectedSink]) -> None:
+    if sink is None:
+        if z.size(0) != plan.num_src:
+            raise ValueError(f"z has {z.size(0)} rows, adjacency has {plan.num_src} columns")
+        return
+    if sink.gidx.numel() != plan.nnz or sink.rows.numel() != plan.num_src:
+        raise ValueError("sink: gidx / rows do not match the adjacency")
+    if sink.dz.shape != z.shape:
+        raise ValueError(f"sink: dz {tuple(sink.dz.shape)} vs Z {tuple(z.shape)}")
+
+
+def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None,
+                  sink: Optional[ProjectedSink] = None) -> Tensor:
+    """GCN neighbour aggregation A·Z (+ bias) of one partition, on the GPU.
+    With a sink, z is the layer's whole Z read through sink.gidx, and the
+    backward adds into sink.dz."""
     _check_device_tensor("z", z)
     plan = adj.device_plan(z.device)
-    if z.size(0) != plan.num_src:
-        raise ValueError(f"z has {z.size(0)} rows, adjacency has {plan.num_src} columns")
-    return _GCNAggregate.apply(z, bias, plan)
+    _check_source(z, plan, sink)
+    if sink is None:
+        return _GCNAggregate.apply(z, bias, plan)
+    return _GCNAggregate.apply(z, bias, plan, sink, sink.token)
 
 
 class _GCNLinearAggregatePadded(torch.autograd.Function):
@@ -255,8 +310,10 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                plan: DevicePlan, eps: float) -> Tensor:
+                plan: DevicePlan, eps: float, sink: Optional[ProjectedSink] = None,
+                token: Optional[Tensor] = None) -> Tensor:
         z = z.contiguous()
+        idx = plan.idx if sink is None else sink.gidx
         dev = z.device
         B, D = plan.num_dst, z.size(1)
         f = plan.fwd
@@ -270,13 +327,14 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
         nnz = plan.nnz
         with KernelTimer.region("gcn_fwd", nnz * (4 * D + 8) + B * (4 * D + 4), nnz, D):
             _lib.call("gr_gcn_aggregate_ln_relu", f.units.data_ptr(), f.n_units,
-                      f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
+                      f.fixups.data_ptr() if f.n_fix else None, f.n_fix, idx.data_ptr(),
                       plan.val.data_ptr(), z.data_ptr(), z.stride(0), _lib.ptr(b), g.data_ptr(),
                       bt.data_ptr(), float(eps), B, D, h.data_ptr(), out.data_ptr(),
                       mean.data_ptr(), rstd.data_ptr(), _lib.ptr(ws), f.n_slots,
                       _lib.stream_handle())
         ctx.save_for_backward(h, mean, rstd, g, bt)
         ctx.plan = plan
+        ctx.sink = sink
         ctx.has_bias = bias is not None
         return out
 
@@ -285,19 +343,25 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
         h, mean, rstd, g, bt = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
         gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
-        dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd") \
-            if ctx.needs_input_grad[0] else None
-        return dz, db, dgamma, dbeta, None, None
+        dz = None
+        if ctx.sink is not None:
+            spmm_into(plan.bwd, plan.row_idx, plan.val_t, gh, ctx.sink)
+        elif ctx.needs_input_grad[0]:
+            dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd")
+        return dz, db, dgamma, dbeta, None, None, None, None
 
 
 def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gamma: Tensor,
-                          beta: Tensor, eps: float = 1e-5) -> Tensor:
-    """ReLU(LayerNorm(A·Z + bias)) of one partition in one fused pass (GPU)."""
+                          beta: Tensor, eps: float = 1e-5,
+                          sink: Optional[ProjectedSink] = None) -> Tensor:
+    """ReLU(LayerNorm(A·Z + bias)) of one partition in one fused pass (GPU);
+    a sink as in gcn_aggregate."""
     _check_device_tensor("z", z)
     plan = adj.device_plan(z.device)
-    if z.size(0) != plan.num_src:
-        raise ValueError(f"z has {z.size(0)} rows, adjacency has {plan.num_src} columns")
-    return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps)
+    _check_source(z, plan, sink)
+    if sink is None:
+        return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps)
+    return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, sink.token)
 
 
 class _GATAttention(torch.autograd.Function):

@@ -39,12 +39,14 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&r
 }
 
 // One wavefront per plan unit; 4 wavefronts per 256-thread workgroup.
+// With orow, output row r goes to y row orow[r] and is added to what that row
+// holds (the rows of one launch are distinct, so each element has one writer).
 template <int VEC, int G, int NCH, int U>
 __global__ __launch_bounds__(256) void aggregate_units(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
     const float* __restrict__ val, const float* __restrict__ x, int64_t ldx,
     float* __restrict__ y, int64_t ldy, const float* __restrict__ bias, int dim,
-    float* __restrict__ ws) {
+    float* __restrict__ ws, const int32_t* __restrict__ orow) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int64_t wid =
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256) void aggregate_units(
   if (slot != 0) return;
 
   if (w.w < 0) {
-    float* out = y + (int64_t)w.x * ldy;
+    float* out = y + (int64_t)(orow != nullptr ? orow[w.x] : w.x) * ldy;
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
       if (!fvalid[ch]) continue;
@@ -147,6 +149,12 @@ __global__ __launch_bounds__(256) void aggregate_units(
         load_vec<VEC>(bias + foff[ch], b);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) acc[ch][j] += b[j];
+      }
+      if (orow != nullptr) {
+        float o[VEC];
+        load_vec<VEC>(out + foff[ch], o);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[ch][j] = o[j] + acc[ch][j];
       }
       store_vec<VEC>(out + foff[ch], acc[ch]);
     }
@@ -165,7 +173,8 @@ __global__ __launch_bounds__(256) void aggregate_units(
 __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict__ fix,
                                                        const float* __restrict__ ws, int dim,
                                                        float* __restrict__ y, int64_t ldy,
-                                                       const float* __restrict__ bias) {
+                                                       const float* __restrict__ bias,
+                                                       const int32_t* __restrict__ orow) {
   const int64_t r = blockIdx.x;
   const int f = blockIdx.y * 256 + threadIdx.x;
   if (f >= dim) return;
@@ -187,7 +196,12 @@ __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict
   }
   for (; k < n; ++k) s += p[(int64_t)k * dim];
   if (bias != nullptr) s += bias[f];
-  y[(int64_t)row * ldy + f] = s;
+  if (orow != nullptr) {
+    float* o = y + (int64_t)orow[row] * ldy + f;
+    *o = *o + s;
+  } else {
+    y[(int64_t)row * ldy + f] = s;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -645,30 +659,32 @@ inline unsigned final_blocks(int64_t dim) {
 template <int VEC, int G, int NCH>
 hipError_t launch_units(const int4* units, int64_t n_units, const int32_t* idx,
                         const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
-                        const float* bias, int dim, float* ws, hipStream_t s) {
+                        const float* bias, int dim, float* ws, const int32_t* orow,
+                        hipStream_t s) {
   constexpr int EPI = 64 / G;
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
   const int64_t blocks = (n_units + 3) / 4;
   hipLaunchKernelGGL((aggregate_units<VEC, G, NCH, U>), dim3((unsigned)blocks), dim3(256), 0, s,
-                     units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws);
+                     units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow);
   return hipGetLastError();
 }
 
 template <int VEC>
 hipError_t dispatch_g(int chunks, const int4* units, int64_t n_units, const int32_t* idx,
                       const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
-                      const float* bias, int dim, float* ws, hipStream_t s) {
+                      const float* bias, int dim, float* ws, const int32_t* orow,
+                      hipStream_t s) {
   if (chunks <= 8)
-    return launch_units<VEC, 8, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, s);
+    return launch_units<VEC, 8, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
   if (chunks <= 16)
-    return launch_units<VEC, 16, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, s);
+    return launch_units<VEC, 16, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
   if (chunks <= 32)
-    return launch_units<VEC, 32, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, s);
+    return launch_units<VEC, 32, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
   if (chunks <= 64)
-    return launch_units<VEC, 64, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, s);
+    return launch_units<VEC, 64, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
   if (chunks <= 128)
-    return launch_units<VEC, 64, 2>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, s);
-  return launch_units<VEC, 64, 4>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, s);
+    return launch_units<VEC, 64, 2>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
+  return launch_units<VEC, 64, 4>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
 }
 
 inline bool aligned(const void* p, int bytes) {
@@ -677,13 +693,43 @@ inline bool aligned(const void* p, int bytes) {
 
 }  // namespace gr_agg
 
+namespace gr_agg {
+
+int aggregate_entry(const int32_t* units, int64_t n_units, const int32_t* fixups, int64_t n_fix,
+                    const int32_t* idx, const float* val, const float* x, int64_t ldx,
+                    float* y, int64_t ldy, const float* bias, int64_t rows, int64_t dim,
+                    float* workspace, int64_t n_slots, const int32_t* orow, void* stream);
+
+}  // namespace gr_agg
+
 extern "C" int gr_gcn_aggregate(const int32_t* units, int64_t n_units, const int32_t* fixups,
                                 int64_t n_fix, const int32_t* idx, const float* val,
                                 const float* x, int64_t ldx, float* y, int64_t ldy,
                                 const float* bias, int64_t rows, int64_t dim, float* workspace,
                                 int64_t n_slots, void* stream) {
-  using namespace gr_agg;
   gr::clear_error();
+  return gr_agg::aggregate_entry(units, n_units, fixups, n_fix, idx, val, x, ldx, y, ldy, bias,
+                                 rows, dim, workspace, n_slots, nullptr, stream);
+}
+
+extern "C" int gr_gcn_aggregate_into(const int32_t* units, int64_t n_units,
+                                     const int32_t* fixups, int64_t n_fix, const int32_t* idx,
+                                     const float* val, const float* x, int64_t ldx,
+                                     const int32_t* out_rows, float* y, int64_t ldy,
+                                     int64_t rows, int64_t dim, float* workspace,
+                                     int64_t n_slots, void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(out_rows != nullptr || n_units == 0, "gcn_aggregate_into: NULL out_rows");
+  return gr_agg::aggregate_entry(units, n_units, fixups, n_fix, idx, val, x, ldx, y, ldy,
+                                 nullptr, rows, dim, workspace, n_slots, out_rows, stream);
+}
+
+int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                            int64_t n_fix, const int32_t* idx, const float* val,
+                            const float* x, int64_t ldx, float* y, int64_t ldy,
+                            const float* bias, int64_t rows, int64_t dim, float* workspace,
+                            int64_t n_slots, const int32_t* orow, void* stream) {
+  using namespace gr_agg;
   GR_REQUIRE(n_units >= 0 && n_fix >= 0 && n_slots >= 0 && rows >= 0,
              "gcn_aggregate: negative extent");
   GR_REQUIRE(dim >= 1 && dim <= 1024, "gcn_aggregate: dim %lld outside [1, 1024]",
@@ -712,17 +758,20 @@ extern "C" int gr_gcn_aggregate(const int32_t* units, int64_t n_units, const int
   const int4* u4 = reinterpret_cast<const int4*>(units);
   hipError_t err;
   if (vec == 4)
-    err = dispatch_g<4>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, s);
+    err = dispatch_g<4>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, orow,
+                        s);
   else if (vec == 2)
-    err = dispatch_g<2>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, s);
+    err = dispatch_g<2>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, orow,
+                        s);
   else
-    err = dispatch_g<1>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, s);
+    err = dispatch_g<1>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, orow,
+                        s);
   GR_HIP_CHECK(err);
   if (n_fix > 0) {
     GR_REQUIRE(n_fix <= INT32_MAX, "gcn_aggregate: too many split rows");
     const int threads = d >= 256 ? 256 : ((d + 63) / 64) * 64;
     hipLaunchKernelGGL(aggregate_fixup, dim3((unsigned)n_fix, (unsigned)((d + 255) / 256)),
-                       dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias);
+                       dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias, orow);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;

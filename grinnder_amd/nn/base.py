@@ -43,7 +43,15 @@ class GriNNderModel(torch.nn.Module):
         layer has no such form (the default)."""
         return None
 
-    def forward_projected(self, layer: int, z: Tensor, adj) -> Tensor:
+    def forward_projected(self, layer: int, z: Tensor, adj, sink=None) -> Tensor:
         """forward_layer(layer, x, adj) given z = x Wᵀ for the W of
-        input_projection(layer)."""
+        input_projection(layer).  With a sink (grinnder_amd.aggregation.
+        ProjectedSink; only where projected_sink_ok(layer)), z is the whole
+        projected matrix of all partitions, read in place through the sink's
+        global ids, and the gradient of the partition's rows is added into
+        the sink's dZ."""
         raise NotImplementedError(f"{type(self).__name__} has no projected form of layer {layer}")
+
+    def projected_sink_ok(self, layer: int) -> bool:
+        """Whether forward_projected(layer, ...) accepts a sink."""
+        return False

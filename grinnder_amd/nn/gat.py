@@ -72,7 +72,9 @@ class GAT(GriNNderModel):
             return None
         return self.convs[layer].lin.weight
 
-    def forward_projected(self, layer: int, hs: Tensor, adj) -> Tensor:
+    def forward_projected(self, layer: int, hs: Tensor, adj, sink=None) -> Tensor:
+        if sink is not None:
+            raise ValueError("GAT layers read gathered rows; they take no sink")
         conv = self.convs[layer]
         if self._fused_norm(layer, hs):
             norm = self.norms[layer]

@@ -63,9 +63,14 @@ class GCN(GriNNderModel):
             return None
         return conv.lin.weight
 
-    def forward_projected(self, layer: int, z: Tensor, adj) -> Tensor:
+    def projected_sink_ok(self, layer: int) -> bool:
+        return self.convs[layer].out_channels % 4 == 0
+
+    def forward_projected(self, layer: int, z: Tensor, adj, sink=None) -> Tensor:
         conv = self.convs[layer]
         d = conv.out_channels
+        if sink is not None and d % 4 != 0:
+            raise ValueError(f"layer {layer}: a sink needs an output width divisible by 4")
         if d % 4 != 0:
             # Widths that are not a multiple of 4 aggregate zero-padded rows
             # (16-byte vectors), as GCNConv does; the pad column stays zero.
@@ -74,9 +79,10 @@ class GCN(GriNNderModel):
             h = gcn_aggregate(F.pad(z, (0, pad)), adj, b)[:, :d]
         elif self._fusable_norm(layer, z):
             norm = self.norms[layer]
-            return gcn_aggregate_ln_relu(z, adj, conv.bias, norm.weight, norm.bias, norm.eps)
+            return gcn_aggregate_ln_relu(z, adj, conv.bias, norm.weight, norm.bias, norm.eps,
+                                         sink=sink)
         else:
-            h = gcn_aggregate(z, adj, conv.bias)
+            h = gcn_aggregate(z, adj, conv.bias, sink=sink)
         if layer < self.num_layers - 1:
             if self.norms is not None:
                 h = self.norms[layer](h)

@@ -213,6 +213,21 @@ int gr_gcn_aggregate(const int32_t* units, int64_t n_units,
                      int64_t rows, int64_t dim, float* workspace,
                      int64_t n_slots, void* stream);
 
+/* No counterpart in the reference: gr_gcn_aggregate with an output row map,
+ * for the backward of projected layers (grinnder_amd/engine/trainer.py),
+ * which add the gradient of a partition's gathered rows straight into the
+ * layer's dZ instead of materialising it and scattering it afterwards:
+ *   y[out_rows[r]] += sum_e val[e] * X[idx[e]]   for each plan row r.
+ * out_rows must be distinct within one call (each y row has one writer, so
+ * the result is deterministic); the sum is formed exactly as by
+ * gr_gcn_aggregate and then added once.  No bias. */
+int gr_gcn_aggregate_into(const int32_t* units, int64_t n_units,
+                          const int32_t* fixups, int64_t n_fix,
+                          const int32_t* idx, const float* val, const float* x,
+                          int64_t ldx, const int32_t* out_rows, float* y,
+                          int64_t ldy, int64_t rows, int64_t dim,
+                          float* workspace, int64_t n_slots, void* stream);
+
 /* Fused GCN layer epilogue (bias + LayerNorm + ReLU of grinnder/nn/gcn.py:
  * 64-72, LayerNorm of torch with biased variance and eps):
  *   h[r]   = sum_e val[e] * X[idx[e]] + bias       (written, kept for backward)
