@@ -303,7 +303,8 @@ def main():
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f}); "
-        f"projected layers {trainer.projected_layers}, inputs kept in HBM {trainer.resident_inputs}")
+        f"projected layers {trainer.projected_layers}, in place {trainer.inplace_layers}, "
+        f"inputs kept in HBM {trainer.resident_inputs}")
     if cfg["num_parts"] > 1:
         from grinnder_amd.buffer.host import PINNED_STATS
         log(f"pinned host memory {PINNED_STATS['bytes'] / 2**30:.1f} GiB, "
@@ -381,6 +382,7 @@ def main():
                    "num_parts": cfg["num_parts"], "model": cfg["model"],
                    "halo_amplification": round(graph.halo_amplification(), 4),
                    "projected_layers": trainer.projected_layers,
+                   "inplace_layers": trainer.inplace_layers,
                    "resident_inputs": trainer.resident_inputs},
         "epoch_s": round(epoch_s, 5),
         "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,

@@ -135,18 +135,20 @@ def spmm(plan, idx: Tensor, val: Tensor, x: Tensor, rows: int,
 
 @dataclass
 class ProjectedSink:
-    """Where a projected layer's source rows live: the aggregation reads the
-    layer's whole Z (all partitions' rows, [N, d]) through `gidx`, the global
-    row of each CSR edge's source, instead of a gathered copy; the backward
-    adds Aᵀ G into `dz` ([N, d]) at `rows`, the global row of each of the
-    partition's E source rows (distinct), instead of returning a gradient for
-    Z.  `token` is a zero-element tensor that requires grad, so that autograd
-    records the aggregation although Z does not."""
+    """Where a partition's source rows live when they are read in place: the
+    aggregation reads the whole matrix of all partitions' rows ([N, d])
+    through `gidx`, the global row of each CSR edge's source, instead of a
+    gathered copy.  With `dz`, the backward adds Aᵀ G into dz ([N, d]) at
+    `rows`, the global row of each of the partition's E source rows
+    (distinct), instead of returning a gradient for the matrix; `token` is
+    then a zero-element tensor that requires grad, so that autograd records
+    the aggregation although the matrix does not.  Without dz the source
+    gets no gradient (a layer's input features)."""
 
-    dz: Tensor
+    dz: Optional[Tensor]
     gidx: Tensor
-    rows: Tensor
-    token: Tensor
+    rows: Optional[Tensor] = None
+    token: Optional[Tensor] = None
 
 
 def spmm_into(plan, idx: Tensor, val: Tensor, x: Tensor, sink: ProjectedSink,
@@ -189,7 +191,8 @@ class _GCNAggregate(torch.autograd.Function):
         gy = gy.contiguous()
         dz = None
         if ctx.sink is not None:
-            spmm_into(plan.bwd, plan.row_idx, plan.val_t, gy, ctx.sink)
+            if ctx.sink.dz is not None:
+                spmm_into(plan.bwd, plan.row_idx, plan.val_t, gy, ctx.sink)
         elif ctx.needs_input_grad[0]:
             dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gy, plan.num_src, name="gcn_bwd")
         db = column_sum(gy) if (ctx.has_bias and ctx.needs_input_grad[1]) else None
@@ -201,8 +204,12 @@ def _check_source(z: Tensor, plan: DevicePlan, sink: Optional[ProjectedSink]) ->
         if z.size(0) != plan.num_src:
             raise ValueError(f"z has {z.size(0)} rows, adjacency has {plan.num_src} columns")
         return
-    if sink.gidx.numel() != plan.nnz or sink.rows.numel() != plan.num_src:
-        raise ValueError("sink: gidx / rows do not match the adjacency")
+    if sink.gidx.numel() != plan.nnz:
+        raise ValueError("sink: gidx does not match the adjacency")
+    if sink.dz is None:
+        return
+    if sink.rows is None or sink.rows.numel() != plan.num_src or sink.token is None:
+        raise ValueError("sink: a sink with dz needs rows for every source and a token")
     if sink.dz.shape != z.shape:
         raise ValueError(f"sink: dz {tuple(sink.dz.shape)} vs Z {tuple(z.shape)}")
 
@@ -215,8 +222,8 @@ def gcn_aggregate(z: Tensor, adj: Adjacency, bias: Optional[Tensor] = None,
     _check_device_tensor("z", z)
     plan = adj.device_plan(z.device)
     _check_source(z, plan, sink)
-    if sink is None:
-        return _GCNAggregate.apply(z, bias, plan)
+    if sink is None or sink.dz is None:
+        return _GCNAggregate.apply(z, bias, plan, sink)
     return _GCNAggregate.apply(z, bias, plan, sink, sink.token)
 
 
@@ -345,7 +352,8 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
         gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
         dz = None
         if ctx.sink is not None:
-            spmm_into(plan.bwd, plan.row_idx, plan.val_t, gh, ctx.sink)
+            if ctx.sink.dz is not None:
+                spmm_into(plan.bwd, plan.row_idx, plan.val_t, gh, ctx.sink)
         elif ctx.needs_input_grad[0]:
             dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd")
         return dz, db, dgamma, dbeta, None, None, None, None
@@ -359,8 +367,8 @@ def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gam
     _check_device_tensor("z", z)
     plan = adj.device_plan(z.device)
     _check_source(z, plan, sink)
-    if sink is None:
-        return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps)
+    if sink is None or sink.dz is None:
+        return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink)
     return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, sink.token)
 
 

@@ -136,6 +136,9 @@ class Trainer:
         self._rng: Dict[tuple, Tensor] = {}
         self._token: Optional[Tensor] = None
         self._gsrc: Dict[int, tuple] = {}
+        # Layers that read their resident input rows in place this epoch
+        # (model.forward_inplace), in place of running projected.
+        self._inplace: Set[int] = set()
         if not self._fast:
             for l in range(L + 1):
                 self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
@@ -178,6 +181,7 @@ class Trainer:
         if self._fast:
             return self._train_fast(optimizer)
         self._proj = self._plan_projection()
+        self._plan_inplace()
         self.reset_epoch()
         optimizer.zero_grad()
         for l in range(self.model.num_layers):
@@ -202,6 +206,7 @@ class Trainer:
             _, metrics = self._fast_metrics(out)
             return metrics
         self._proj = self._plan_projection()
+        self._plan_inplace()
         self.reset_epoch()
         for l in range(self.model.num_layers):
             self._forward_layer(l)
@@ -389,12 +394,30 @@ class Trainer:
                 self._keep.add(layer)
         return dict(sorted(plan.items()))
 
+    def _plan_inplace(self) -> None:
+        """Moves a planned layer from projected to in place when its input
+        rows stay in HBM this epoch and the model has a cheaper in-place form
+        (GCN's widening first layer aggregates its narrower input, and the
+        input needs no gradient): no Z, dZ or dW pass for it then."""
+        self._inplace = set()
+        for layer in sorted(self._proj):
+            if layer in self._xin and self.model.inplace_ok(layer) \
+                    and int(self.graph.ptr[-1]) < 2 ** 31:
+                self._inplace.add(layer)
+        for layer in self._inplace:
+            del self._proj[layer]
+
+    @property
+    def inplace_layers(self) -> List[int]:
+        """Layers that read their HBM-resident input rows in place this epoch."""
+        return sorted(self._inplace)
+
     def _xres_buf(self, layer: int) -> Tensor:
         """HBM copy of layer `layer`'s input rows (all partitions, in order)."""
         x = self._xres.get(layer)
         if x is None:
             with torch.cuda.stream(self.streams.compute):
-                x = torch.empty(int(self.graph.ptr[-1]), self._proj[layer].size(1),
+                x = torch.empty(int(self.graph.ptr[-1]), self.host_features[layer].embedding_dim,
                                 device=self.device)
             self._xres[layer] = x
         return x
@@ -447,18 +470,24 @@ class Trainer:
                 self._token = torch.zeros(0, device=self.device, requires_grad=True)
             return _GatherRows.apply(self._token, z, rows, self._dzbuf(layer))
 
-    def _sink(self, layer: int, pid: int):
-        """A ProjectedSink for partition pid of a layer whose model reads Z in
-        place (projected_sink_ok), or None: the global id of each CSR edge's
-        source and of each gathered row, as int32 (cached per partition)."""
-        if not self.model.projected_sink_ok(layer) or int(self.graph.ptr[-1]) >= 2 ** 31:
-            return None
+    def _gids(self, pid: int) -> tuple:
+        """(global row of each CSR edge's source, global row of each gathered
+        row) of partition pid, int32 on the device, cached."""
         ids = self._gsrc.get(pid)
         if ids is None:
             rows = self._global_rows(pid)
             plan = self.graph.adjacency(pid).device_plan(self.device)
             ids = (rows[plan.idx.long()].to(torch.int32), rows.to(torch.int32))
             self._gsrc[pid] = ids
+        return ids
+
+    def _sink(self, layer: int, pid: int):
+        """A ProjectedSink for partition pid of a layer whose model reads Z in
+        place (projected_sink_ok), or None: the global id of each CSR edge's
+        source and of each gathered row, as int32 (cached per partition)."""
+        if not self.model.projected_sink_ok(layer) or int(self.graph.ptr[-1]) >= 2 ** 31:
+            return None
+        ids = self._gids(pid)
         if self._token is None:
             self._token = torch.zeros(0, device=self.device, requires_grad=True)
         return ProjectedSink(self._dzbuf(layer), ids[0], ids[1], self._token)
@@ -468,6 +497,8 @@ class Trainer:
         sink where the model allows it, else on gathered rows of Z (whose
         gradient the gather adds into dZ when grad)."""
         adj = self.graph.adjacency(pid)
+        if layer in self._inplace:
+            return self.model.forward_inplace(layer, self._xres[layer], adj, self._gids(pid)[0])
         sink = self._sink(layer, pid)
         if sink is not None:
             return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
@@ -605,15 +636,19 @@ class Trainer:
         """Backward of a projected layer: per partition, take the forward's
         kept graph or recompute the layer from its gathered rows of Z, and
         backpropagate into the layer's parameters and into dZ; then
-        dW = sum_p dZ_pᵀ x_p."""
+        dW = sum_p dZ_pᵀ x_p.  An in-place layer backpropagates the same way
+        into all its parameters (its input gets no gradient), with no dZ and
+        no dW pass."""
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
         last = layer == self.model.num_layers - 1
-        w = self._proj[layer]
-        dz = self._dzbuf(layer)
-        with torch.cuda.stream(s.compute):
-            dz.zero_()
+        inplace = layer in self._inplace
+        if not inplace:
+            w = self._proj[layer]
+            dz = self._dzbuf(layer)
+            with torch.cuda.stream(s.compute):
+                dz.zero_()
         from_device = (layer + 1) in self._proj
         from_host = not last and not from_device
         gbuf = self.device_gradients[layer + 1] if not last else None
@@ -652,6 +687,9 @@ class Trainer:
                 self.activations[layer][pid] = None
             if from_host and pool == 1 and i + 1 < len(pids):
                 self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])
+        if inplace:
+            s.compute.synchronize()
+            return
         with torch.cuda.stream(s.compute):
             dw = torch.zeros_like(w)
 
@@ -676,6 +714,19 @@ class Trainer:
 
     # ------------------------------------------------------------- forward
 
+    def _layer0_inputs(self, layer: int) -> None:
+        """Before the first layer's loop: its input rows uploaded into their
+        HBM copy (in place) or projected into Z_0 as they arrive (projected);
+        nothing for the reference flow, which gathers per partition."""
+        if layer != 0:
+            return
+        if layer in self._inplace:
+            # Every partition reads halo rows of the others: all uploads land
+            # before the compute stream goes on.
+            self._upload_resident(0, lambda pid, x, lo, hi: None)
+        elif layer in self._proj:
+            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+
     def _forward_layer(self, layer: int) -> None:
         """Per partition: the layer's output from gathered input rows (the
         reference's flow) or from gathered rows of Z (a projected layer), D2H
@@ -685,13 +736,12 @@ class Trainer:
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
-        projected = layer in self._proj
+        projected = layer in self._proj or layer in self._inplace
         w_next = self._proj.get(layer + 1)
         if (layer + 1) in self._xin:
             self._forward_layer_resident(layer)
             return
-        if projected and layer == 0:
-            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+        self._layer0_inputs(layer)
         if layer in self._keep and layer == self.model.num_layers - 1:
             # The last layer with its graphs kept: the loss reads the logits
             # from them (_compute_losses), so nothing goes to the host.
@@ -739,10 +789,9 @@ class Trainer:
         stay in HBM: each partition's output goes to Z_{layer+1} and to the
         resident copy of x_{layer+1}, and nothing crosses to the host."""
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
-        projected = layer in self._proj
+        projected = layer in self._proj or layer in self._inplace
         x_next = self._xres_buf(layer + 1)
-        if projected and layer == 0:
-            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+        self._layer0_inputs(layer)
         if not projected:
             self._gather(layer, pids[0], s.h2d[0])
         for i, pid in enumerate(pids):
@@ -846,7 +895,7 @@ class Trainer:
 
     def _backward_last_layer(self, losses: List[Tensor]) -> None:
         layer = self.model.num_layers - 1
-        if layer in self._proj:
+        if layer in self._proj or layer in self._inplace:
             self._backward_projected(layer, losses)
         else:
             self._backward_pass(layer,
@@ -855,7 +904,7 @@ class Trainer:
             losses[i] = None
 
     def _backward_layer(self, layer: int) -> None:
-        if layer in self._proj:
+        if layer in self._proj or layer in self._inplace:
             self._backward_projected(layer)
             return
         from_device = (layer + 1) in self._proj

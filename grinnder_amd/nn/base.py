@@ -55,3 +55,15 @@ class GriNNderModel(torch.nn.Module):
     def projected_sink_ok(self, layer: int) -> bool:
         """Whether forward_projected(layer, ...) accepts a sink."""
         return False
+
+    def inplace_ok(self, layer: int) -> bool:
+        """Whether forward_inplace(layer, ...) exists and is the cheaper form
+        of the layer when all partitions' input rows are in device memory
+        (the default: no)."""
+        return False
+
+    def forward_inplace(self, layer: int, x: Tensor, adj, gidx: Tensor) -> Tensor:
+        """forward_layer(layer, x[rows], adj) for the partition's gathered rows,
+        with x the input rows of all partitions read in place through gidx
+        (the global row of each CSR edge's source); x gets no gradient."""
+        raise NotImplementedError(f"{type(self).__name__} has no in-place form of layer {layer}")

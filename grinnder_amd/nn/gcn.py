@@ -8,7 +8,7 @@ import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
 
-from grinnder_amd.aggregation import gcn_aggregate, gcn_aggregate_ln_relu
+from grinnder_amd.aggregation import ProjectedSink, gcn_aggregate, gcn_aggregate_ln_relu
 from grinnder_amd.dense import linear, linear_ln_act
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.nn.conv import GCNConv
@@ -65,6 +65,30 @@ class GCN(GriNNderModel):
 
     def projected_sink_ok(self, layer: int) -> bool:
         return self.convs[layer].out_channels % 4 == 0
+
+    def inplace_ok(self, layer: int) -> bool:
+        """The first layer, when it aggregates first (it widens): (A x) Wᵀ
+        aggregates the narrower input, and its input needs no gradient."""
+        conv = self.convs[layer]
+        return (layer == 0 and conv.aggregate_first()
+                and not (self.residual and conv.in_channels == conv.out_channels))
+
+    def forward_inplace(self, layer: int, x: Tensor, adj, gidx: Tensor) -> Tensor:
+        if not self.inplace_ok(layer):
+            raise ValueError(f"layer {layer} has no in-place form")
+        conv = self.convs[layer]
+        h = gcn_aggregate(x, adj, sink=ProjectedSink(None, gidx))
+        if self._fusable_norm(layer, x):
+            norm = self.norms[layer]
+            return linear_ln_act(h, conv.lin.weight, conv.bias, norm.weight, norm.bias,
+                                 norm.eps, "relu")
+        h = linear(h, conv.lin.weight, conv.bias)
+        if layer < self.num_layers - 1:
+            if self.norms is not None:
+                h = self.norms[layer](h)
+            h = F.relu(h)
+            h = F.dropout(h, p=self.dropout, training=self.training)
+        return h
 
     def forward_projected(self, layer: int, z: Tensor, adj, sink=None) -> Tensor:
         conv = self.convs[layer]
