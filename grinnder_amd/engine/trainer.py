@@ -25,19 +25,33 @@ device kernels; waits are per stream, not device-wide; the NVMe storage tier
 and its partition-LRU cache are out of scope (every layer stays in host RAM,
 which is what the reference's 'auto' cache resolves to when it fits).
 
-Projected layers (config.project_first = 'auto'): when a layer's input
-enters only through x Wᵀ (GCNConv; GATConv with inactive dropout),
-gather(x) Wᵀ = gather(x Wᵀ) row by row.  Z = x Wᵀ is then formed once per
-partition from its own rows (layer 0: uploaded input rows; above: the
-previous layer's output, right after it is computed) and stays in HBM with
-its gradient dZ; every partition gathers its rows of Z on the device instead
-of input rows from the host.  The backward recomputes the layer from the
-gathered Z, adds dL/dZ of the gathered rows into dZ (partitions in order, so
-sums are deterministic), hands dZ_p W to the layer below as the gradient of
-its outputs (no host scatter), and forms dL/dW = sum_p dZ_pᵀ x_p from a
-second upload of each partition's input rows.  Per layer this replaces two
-host gathers and a read-add-write scatter of ~E x d_in rows by two N x d_in
-uploads.
+Projected layers (config.project_first = 'auto', planned per epoch against
+free HBM; 'off' keeps the reference's data movement):
+
+- A layer whose input enters only through x Wᵀ (GCNConv; GATConv with
+  inactive dropout) satisfies gather(x) Wᵀ = gather(x Wᵀ) row by row.  Z =
+  x Wᵀ is formed once per partition from its own rows and stays in HBM with
+  its gradient dZ, and partitions take their gathered rows from Z on the
+  device instead of input rows from the host.  A GCN layer reads Z in place
+  through global row ids (aggregation.ProjectedSink); a GAT layer gathers.
+- The backward adds dL/dZ of a partition's rows into dZ (partitions in
+  order, so sums are deterministic), hands dZ_p W to the layer below as the
+  gradient of its outputs (no host scatter), and forms dL/dW = sum_p
+  dZ_pᵀ x_p at the end.
+- Layer inputs stay in HBM for the epoch when there is room
+  (resident_inputs): layer 0's rows are uploaded once per epoch, those above
+  come from the layer below and never reach the host.  Without room they are
+  uploaded again for dW.
+- The forward's autograd graphs are kept for the backward when there is
+  room; otherwise the backward recomputes each partition from the RNG state
+  its forward started from, as the reference's checkpoint does.
+- A widening first GCN layer whose input rows stay in HBM runs in place
+  instead (inplace_layers): it aggregates the narrower input first, reading
+  it through global row ids, and needs no backward aggregation.
+
+Per layer this replaces two host gathers and a read-add-write scatter of
+~E x d_in rows (plus the D2H of the output and the upload of its gradient)
+with at most one N x d_in upload per epoch.
 """
 
 from __future__ import annotations
@@ -337,7 +351,9 @@ class Trainer:
         upload for dW = sum_p dZ_pᵀ x_p crosses the host link; layer 0's rows
         are uploaded once per epoch, for the projection, and kept for dW
         instead of being uploaded a second time.  Layers above 0 go first
-        (each of their bytes saves two crossings)."""
+        (each of their bytes saves two crossings).  Then self._keep: the
+        layers whose per-partition forward graphs are kept for the backward
+        (training only)."""
         cfg, g = self.config, self.graph
         self._xin = set()
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
