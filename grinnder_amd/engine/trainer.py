@@ -153,6 +153,14 @@ class Trainer:
         # Layers that read their resident input rows in place this epoch
         # (model.forward_inplace), in place of running projected.
         self._inplace: Set[int] = set()
+        # Layer 0's resident input rows are double-buffered across epochs when
+        # there is room: the next epoch's rows stream into the other buffer
+        # (on streams of their own) while this epoch computes.
+        self._x0bufs: List[Tensor] = []
+        self._x0cur = 0
+        self._x0double = False
+        self._x0pending: Optional[tuple] = None
+        self._pf_streams: List[torch.cuda.Stream] = []
         if not self._fast:
             for l in range(L + 1):
                 self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
@@ -356,8 +364,11 @@ class Trainer:
         (training only)."""
         cfg, g = self.config, self.graph
         self._xin = set()
+        self._keep = set()
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
+            self._x0double = False
+            self._drop_prefetch()
             return {}
         n, maxb = int(g.ptr[-1]), max(g.partition_sizes)
         cands = []
@@ -408,6 +419,21 @@ class Trainer:
                     continue
                 free -= need
                 self._keep.add(layer)
+        # A second copy of layer 0's input rows for the next epoch's upload to
+        # stream into while this epoch computes.
+        self._x0double = False
+        if 0 in self._xin:
+            if len(self._x0bufs) >= 2:
+                self._x0double = True
+            else:
+                if free is None:
+                    free, _ = torch.cuda.mem_get_info(self.device)
+                need = 4 * n * plan[0].size(1)
+                if need + (8 << 30) <= free:
+                    free -= need
+                    self._x0double = True
+        if not self._x0double:
+            self._drop_prefetch()
         return dict(sorted(plan.items()))
 
     def _plan_inplace(self) -> None:
@@ -609,35 +635,69 @@ class Trainer:
             ready = nxt
 
     def _upload_resident(self, layer: int, fn) -> None:
-        """_each_input_partition into the resident input buffer: every
-        partition has its own rows there, so the uploads run back to back on
-        the two H2D streams and fn(p) waits only for partition p's upload."""
+        """_each_input_partition for layer 0's resident input buffer: every
+        partition has its own rows there, so fn(p) waits only for partition
+        p's upload.  The rows come from the upload the previous epoch started
+        into this buffer when there is one, else from one started now; with
+        two buffers, the next epoch's upload then starts into the other."""
+        if layer != 0:
+            raise ValueError("only layer 0's input rows are uploaded to a resident buffer")
         g, s, pids = self.graph, self.streams, self._my_pids
-        host = self.host_features[layer]
-        x = self._xres_buf(layer)
-        din = x.size(1)
-        # The buffer may be new (its memory just freed by queued compute work)
-        # or still read by the previous epoch's dW pass: uploads wait for the
-        # compute stream's queued work first.
+        if self._x0pending is not None:
+            idx, ready = self._x0pending
+            self._x0pending = None
+        else:
+            idx = self._x0cur
+            ready = self._issue_layer0_upload(idx)
+        self._x0cur = idx
+        x = self._xres[0] = self._x0bufs[idx]
+        for i, pid in enumerate(pids):
+            s.compute.wait_event(ready[i])
+            with torch.cuda.stream(s.compute):
+                lo, hi = g._range(pid)
+                fn(pid, x[lo:hi], lo, hi)
+        if self._x0double:
+            self._x0pending = (1 - idx, self._issue_layer0_upload(1 - idx))
+
+    def _issue_layer0_upload(self, idx: int) -> List[torch.cuda.Event]:
+        """Starts uploading every partition's layer-0 input rows into buffer
+        idx on the two prefetch streams; returns each partition's ready event.
+        The uploads first wait for the compute stream's queued work: the
+        buffer may be new (its memory just freed by queued compute work) or
+        still read by an earlier epoch."""
+        g, s, pids = self.graph, self.streams, self._my_pids
+        host = self.host_features[0]
+        n, din = int(g.ptr[-1]), host.embedding_dim
+        while len(self._x0bufs) <= idx:
+            with torch.cuda.stream(s.compute):
+                self._x0bufs.append(torch.empty(n, din, device=self.device))
+        x = self._x0bufs[idx]
+        if not self._pf_streams:
+            self._pf_streams = [torch.cuda.Stream(self.device) for _ in range(2)]
         entry = torch.cuda.Event()
         entry.record(s.compute)
-        for st in s.h2d[:2]:
+        for st in self._pf_streams:
             st.wait_event(entry)
+            x.record_stream(st)
         ready: List[torch.cuda.Event] = []
         for i, pid in enumerate(pids):
             lo, hi = g._range(pid)
-            st = s.h2d[i % min(2, len(s.h2d))]
+            st = self._pf_streams[i % 2]
             with torch.cuda.stream(st):
                 with KernelTimer.region("x_upload", 4 * (hi - lo) * din, 0, din):
                     x[lo:hi].copy_(host[pid], non_blocking=True)
                 ev = torch.cuda.Event()
                 ev.record(st)
             ready.append(ev)
-        for i, pid in enumerate(pids):
-            s.compute.wait_event(ready[i])
-            with torch.cuda.stream(s.compute):
-                lo, hi = g._range(pid)
-                fn(pid, x[lo:hi], lo, hi)
+        return ready
+
+    def _drop_prefetch(self) -> None:
+        """Forgets an upload started for an epoch that will not use it; later
+        compute work (and uploads, which wait for it) is ordered after it."""
+        if self._x0pending is not None:
+            for ev in self._x0pending[1]:
+                self.streams.compute.wait_event(ev)
+            self._x0pending = None
 
     def _device_grad(self, layer: int, pid: int) -> Tensor:
         """dL/d(x_layer) of partition pid's rows when layer `layer` runs

@@ -490,3 +490,43 @@ def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
         w.add_(delta * v)
     fd = (up - down) / (2 * delta)
     assert abs(fd - float(g.norm())) <= 2e-3 * float(g.norm()) + 1e-4, (fd, float(g.norm()))
+
+
+@pytest.mark.parametrize("model_kind", ["gcn", "gat"])
+def test_layer0_prefetch_across_epochs_is_exact(gpu, model_kind, monkeypatch):
+    """Layer 0's input rows for the next epoch stream into a second buffer
+    while an epoch computes: three training epochs (weights changing) and an
+    evaluate() in between give bit-identical weights and metrics with and
+    without that prefetch."""
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    ei, x, y, tr, va, te = data
+    torch.manual_seed(4)
+    if model_kind == "gcn":
+        make = lambda: GCN(24, 32, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
+    else:
+        make = lambda: GAT(24, 8, 4, num_layers=2, heads=1, dropout=0.0, norm=True)  # noqa
+    state = make().state_dict()
+    plan = Trainer._plan_projection
+    runs = []
+    for prefetch in (True, False):
+        if not prefetch:
+            def single(self):
+                out = plan(self)
+                self._x0double = False
+                self._drop_prefetch()
+                return out
+            monkeypatch.setattr(Trainer, "_plan_projection", single)
+        config = GriNNderConfig(num_parts=4)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.SGD(model.parameters(), lr=0.5)
+        crit = torch.nn.CrossEntropyLoss()
+        metrics = [trainer.train_epoch(opt, crit), trainer.evaluate(crit),
+                   trainer.train_epoch(opt, crit), trainer.train_epoch(opt, crit)]
+        assert len(trainer._x0bufs) == (2 if prefetch else 1)
+        runs.append((metrics, {k: v.detach().clone() for k, v in model.state_dict().items()}))
+    (m0, w0), (m1, w1) = runs
+    assert [m["loss"] for m in m0] == [m["loss"] for m in m1]
+    assert all(torch.equal(w0[k], w1[k]) for k in w0)
