@@ -530,3 +530,45 @@ def test_layer0_prefetch_across_epochs_is_exact(gpu, model_kind, monkeypatch):
     (m0, w0), (m1, w1) = runs
     assert [m["loss"] for m in m0] == [m["loss"] for m in m1]
     assert all(torch.equal(w0[k], w1[k]) for k in w0)
+
+
+@pytest.mark.parametrize("pool_size", [1, 2])
+@pytest.mark.parametrize("resident", ["all", "none"])
+def test_mixed_flows_match_reference(gpu, pool_size, resident, monkeypatch):
+    """A residual GCN whose 16 -> 16 layers cannot be projected (the residual
+    add needs x itself): layers 0 and 3 run projected, layers 1 and 2 the
+    reference flow, so outputs and gradients cross between the two flows in
+    both directions (device Z rows and host buffers forward; host gradient
+    buffers and dZ W backward).  Loss, gradients and evaluate() equal those of
+    the reference flow throughout within the 1e-5 bound, over two epochs."""
+    kept = {"all": [0, 1, 2, 3], "none": []}[resident]
+    if resident == "none":
+        _limit_resident_inputs(monkeypatch, set())
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    ei, x, y, tr, va, te = data
+    torch.manual_seed(6)
+    make = lambda: GCN(24, 16, 4, num_layers=4, dropout=0.0, norm=True,  # noqa: E731
+                       residual=True)
+    state = make().state_dict()
+    runs = {}
+    for proj in ("off", "auto"):
+        config = GriNNderConfig(num_parts=4, pool_size=pool_size, project_first=proj)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        crit = torch.nn.CrossEntropyLoss()
+        losses = [trainer.train_epoch(opt, crit)["loss"]]
+        grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()}
+        losses.append(trainer.train_epoch(opt, crit)["loss"])
+        ev = trainer.evaluate(crit)
+        if proj == "auto":
+            assert trainer.projected_layers == [0, 3]
+            assert trainer.resident_inputs == [l for l in kept if l in (0, 3)]
+        runs[proj] = (losses, grads, ev)
+    (l0, g0, e0), (l1, g1, e1) = runs["off"], runs["auto"]
+    assert all(abs(a - b) < 1e-5 for a, b in zip(l0, l1))
+    for k, err in grad_errs(g1, g0).items():
+        assert err <= 1e-5, (k, err)
+    assert e0["val_acc"] == e1["val_acc"]
