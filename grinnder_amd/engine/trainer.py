@@ -56,7 +56,7 @@ with at most one N x d_in upload per epoch.
 
 from __future__ import annotations
 
-from typing import Dict, List, Optional, Set
+from typing import Dict, List, Optional
 
 import torch
 from torch import Tensor
@@ -65,34 +65,16 @@ from torch.utils.checkpoint import checkpoint
 from grinnder_amd.autograd.checkpoint import HongtuCheckpoint, ScatteredCheckpoint
 from grinnder_amd.autograd.grad_offload import GradOffload
 from grinnder_amd.buffer.device import DeviceBuffer
-from grinnder_amd.aggregation import KernelTimer, ProjectedSink, dense_region
 from grinnder_amd.buffer.host import HostBuffer
 from grinnder_amd.config import GriNNderConfig
-from grinnder_amd.dense import gemm_tn
 from grinnder_amd.data.graph import PartitionedGraph
+from grinnder_amd.engine.projected import ProjectedLayers
 from grinnder_amd.engine.streams import StreamManager
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.loss import check_stats, mask_codes, masked_cross_entropy
 
 
-class _GatherRows(torch.autograd.Function):
-    """z = Z[rows] for a projected layer; the backward adds dL/dz into the
-    layer's dZ buffer at the same rows (distinct within a partition) instead
-    of returning a gradient for Z.  `token` is a zero-element tensor that
-    requires grad, so that autograd records the gather although Z does not."""
-
-    @staticmethod
-    def forward(ctx, token: Tensor, z: Tensor, rows: Tensor, dz: Tensor) -> Tensor:
-        ctx.rows, ctx.dz = rows, dz
-        return z.index_select(0, rows)
-
-    @staticmethod
-    def backward(ctx, grad: Tensor):
-        ctx.dz.index_add_(0, ctx.rows, grad)
-        return None, None, None, None
-
-
-class Trainer:
+class Trainer(ProjectedLayers):
     def __init__(self, model: GriNNderModel, graph: PartitionedGraph, config: GriNNderConfig,
                  partition_range: Optional[tuple] = None):
         if config.mode not in ("hongtu", "grinnder"):
@@ -131,36 +113,7 @@ class Trainer:
         self._pid_to_loss_idx: Dict[int, int] = {}
         self._resident: Dict[str, Tensor] = {}
         self._label_cache: Dict[int, tuple] = {}
-        # Projected layers: their W this epoch; Z, dZ per layer, two upload
-        # buffers per input width and the HBM-resident inputs, kept across
-        # epochs; the layers whose inputs stay in HBM this epoch; the device
-        # row ids of each partition's gathered rows.
-        self._proj: Dict[int, Tensor] = {}
-        self._zbufs: Dict[int, Tensor] = {}
-        self._dzbufs: Dict[int, Tensor] = {}
-        self._xbufs: Dict[int, List[Tensor]] = {}
-        self._xres: Dict[int, Tensor] = {}
-        self._xin: Set[int] = set()
-        self._grow: Dict[int, Tensor] = {}
-        # Projected layers whose forward graphs are kept until their backward
-        # this epoch (instead of being recomputed), the kept outputs, and the
-        # RNG state each recomputed partition's forward started from.
-        self._keep: Set[int] = set()
-        self._graphs: Dict[int, Dict[int, Tensor]] = {}
-        self._rng: Dict[tuple, Tensor] = {}
-        self._token: Optional[Tensor] = None
-        self._gsrc: Dict[int, tuple] = {}
-        # Layers that read their resident input rows in place this epoch
-        # (model.forward_inplace), in place of running projected.
-        self._inplace: Set[int] = set()
-        # Layer 0's resident input rows are double-buffered across epochs when
-        # there is room: the next epoch's rows stream into the other buffer
-        # (on streams of their own) while this epoch computes.
-        self._x0bufs: List[Tensor] = []
-        self._x0cur = 0
-        self._x0double = False
-        self._x0pending: Optional[tuple] = None
-        self._pf_streams: List[torch.cuda.Stream] = []
+        self._init_projected()
         if not self._fast:
             for l in range(L + 1):
                 self.host_features.append(HostBuffer(P, graph.partition_sizes, dims[l],
@@ -328,480 +281,7 @@ class Trainer:
         if t is not None:
             t.untyped_storage().resize_(0)
 
-    # --------------------------------------------------- projected layers
-
-    @property
-    def projected(self) -> bool:
-        """Whether the current epoch runs any layer on projected rows."""
-        return bool(self._proj)
-
-    @property
-    def projected_layers(self) -> List[int]:
-        return sorted(self._proj)
-
-    @property
-    def resident_inputs(self) -> List[int]:
-        """Projected layers whose input rows stay in HBM this epoch."""
-        return sorted(self._xin)
-
-    def _plan_projection(self) -> Dict[int, Tensor]:
-        """Layers this epoch runs projected, with their input projection W:
-        grinnder mode, every partition on this trainer, and room in HBM for
-        Z, dZ and the upload buffers (plus 8 GiB for the per-partition
-        working set).  A projected layer moves 2 N d_in bytes over the host
-        link (two uploads of its input rows) instead of 2 E d_in of gathers
-        and, above layer 0, an E d_in read-add-write scatter; when HBM is
-        short, layers with the most input width per byte of Z go first.
-
-        Also decides self._xin, with what room is left: the projected layers
-        whose input rows x stay in HBM for the epoch.  Above layer 0, x is
-        produced on the device by the layer below, so neither its D2H nor the
-        upload for dW = sum_p dZ_pᵀ x_p crosses the host link; layer 0's rows
-        are uploaded once per epoch, for the projection, and kept for dW
-        instead of being uploaded a second time.  Layers above 0 go first
-        (each of their bytes saves two crossings).  Then self._keep: the
-        layers whose per-partition forward graphs are kept for the backward
-        (training only)."""
-        cfg, g = self.config, self.graph
-        self._xin = set()
-        self._keep = set()
-        if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
-                or (self._pid_start, self._pid_end) != (0, g.num_parts)):
-            self._x0double = False
-            self._drop_prefetch()
-            return {}
-        n, maxb = int(g.ptr[-1]), max(g.partition_sizes)
-        cands = []
-        for layer in range(self.model.num_layers):
-            w = self.model.input_projection(layer)
-            if w is not None:
-                cands.append((w.size(1) / w.size(0), layer, w))
-        free = None
-        plan: Dict[int, Tensor] = {}
-        for _, layer, w in sorted(cands, key=lambda c: (-c[0], c[1])):
-            if layer not in self._zbufs:
-                if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
-                need = 4 * (2 * n * w.size(0) + 2 * maxb * w.size(1))
-                if need + (8 << 30) > free:
-                    continue
-                free -= need
-            plan[layer] = w
-        for layer in sorted(plan, key=lambda l: (l == 0, l)):
-            if layer not in self._xres:
-                if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
-                need = 4 * n * plan[layer].size(1)
-                if need + (8 << 30) > free:
-                    continue
-                free -= need
-            self._xin.add(layer)
-        # Kept forward graphs (training only): a projected layer whose output
-        # feeds a resident input, or the last layer, keeps each partition's
-        # autograd graph until its backward, which then skips the recompute
-        # (an aggregation pass and a gather of Z per partition); the last
-        # layer's loss is then taken from the kept logits, which no longer
-        # go through host memory.  What a graph holds is bounded by the
-        # gathered rows, three [N, d_out] tensors and one float per edge.
-        self._keep = set()
-        if self.model.training:
-            sum_e = sum(g.expanded_sizes)
-            nnz = sum(int(a[1].numel()) for a in g.adj_csr)
-            last = self.model.num_layers - 1
-            for layer in sorted(plan):
-                if layer + 1 not in self._xin and layer != last:
-                    continue
-                d = plan[layer].size(0)
-                if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
-                need = 4 * (sum_e * d + 3 * n * d + nnz)
-                if need + (8 << 30) > free:
-                    continue
-                free -= need
-                self._keep.add(layer)
-        # A second copy of layer 0's input rows for the next epoch's upload to
-        # stream into while this epoch computes.
-        self._x0double = False
-        if 0 in self._xin:
-            if len(self._x0bufs) >= 2:
-                self._x0double = True
-            else:
-                if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
-                need = 4 * n * plan[0].size(1)
-                if need + (8 << 30) <= free:
-                    free -= need
-                    self._x0double = True
-        if not self._x0double:
-            self._drop_prefetch()
-        return dict(sorted(plan.items()))
-
-    def _plan_inplace(self) -> None:
-        """Moves a planned layer from projected to in place when its input
-        rows stay in HBM this epoch and the model has a cheaper in-place form
-        (GCN's widening first layer aggregates its narrower input, and the
-        input needs no gradient): no Z, dZ or dW pass for it then."""
-        self._inplace = set()
-        for layer in sorted(self._proj):
-            if layer in self._xin and self.model.inplace_ok(layer) \
-                    and int(self.graph.ptr[-1]) < 2 ** 31:
-                self._inplace.add(layer)
-        for layer in self._inplace:
-            del self._proj[layer]
-
-    @property
-    def inplace_layers(self) -> List[int]:
-        """Layers that read their HBM-resident input rows in place this epoch."""
-        return sorted(self._inplace)
-
-    def _xres_buf(self, layer: int) -> Tensor:
-        """HBM copy of layer `layer`'s input rows (all partitions, in order)."""
-        x = self._xres.get(layer)
-        if x is None:
-            with torch.cuda.stream(self.streams.compute):
-                x = torch.empty(int(self.graph.ptr[-1]), self.host_features[layer].embedding_dim,
-                                device=self.device)
-            self._xres[layer] = x
-        return x
-
-    def _zbuf(self, layer: int) -> Tensor:
-        z = self._zbufs.get(layer)
-        if z is None:
-            with torch.cuda.stream(self.streams.compute):
-                z = torch.empty(int(self.graph.ptr[-1]), self._proj[layer].size(0),
-                                device=self.device)
-            self._zbufs[layer] = z
-        return z
-
-    def _dzbuf(self, layer: int) -> Tensor:
-        dz = self._dzbufs.get(layer)
-        if dz is None:
-            with torch.cuda.stream(self.streams.compute):
-                dz = torch.empty_like(self._zbuf(layer))
-            self._dzbufs[layer] = dz
-        return dz
-
-    def _global_rows(self, pid: int) -> Tensor:
-        """Device int64 ids (in partition order) of partition pid's gathered
-        rows, laid out [intra | halo from p' = 0..P-1] like the host gather."""
-        idx = self._grow.get(pid)
-        if idx is None:
-            g = self.graph
-            lo, hi = g._range(pid)
-            parts = [torch.arange(lo, hi, dtype=torch.int64)]
-            for q, b in enumerate(g.boundaries[pid]):
-                if q != pid and b is not None and b.numel() > 0:
-                    parts.append(b.to(torch.int64) + int(g.ptr[q]))
-            idx = torch.cat(parts).to(self.device)
-            if idx.numel() != g.expanded_sizes[pid]:
-                raise RuntimeError(f"partition {pid}: {idx.numel()} gathered rows, "
-                                   f"expected {g.expanded_sizes[pid]}")
-            self._grow[pid] = idx
-        return idx
-
-    def _gather_projected(self, layer: int, pid: int, grad: bool = False) -> Tensor:
-        """Partition pid's gathered rows of Z_layer; with grad, the backward
-        adds their gradient into dZ_layer."""
-        rows = self._global_rows(pid)
-        z = self._zbufs[layer]
-        d = z.size(1)
-        with KernelTimer.region("z_gather", 2 * 4 * rows.numel() * d, 0, d):
-            if not grad:
-                return z.index_select(0, rows)
-            if self._token is None:
-                self._token = torch.zeros(0, device=self.device, requires_grad=True)
-            return _GatherRows.apply(self._token, z, rows, self._dzbuf(layer))
-
-    def _gids(self, pid: int) -> tuple:
-        """(global row of each CSR edge's source, global row of each gathered
-        row) of partition pid, int32 on the device, cached."""
-        ids = self._gsrc.get(pid)
-        if ids is None:
-            rows = self._global_rows(pid)
-            plan = self.graph.adjacency(pid).device_plan(self.device)
-            ids = (rows[plan.idx.long()].to(torch.int32), rows.to(torch.int32))
-            self._gsrc[pid] = ids
-        return ids
-
-    def _sink(self, layer: int, pid: int):
-        """A ProjectedSink for partition pid of a layer whose model reads Z in
-        place (projected_sink_ok), or None: the global id of each CSR edge's
-        source and of each gathered row, as int32 (cached per partition)."""
-        if not self.model.projected_sink_ok(layer) or int(self.graph.ptr[-1]) >= 2 ** 31:
-            return None
-        ids = self._gids(pid)
-        if self._token is None:
-            self._token = torch.zeros(0, device=self.device, requires_grad=True)
-        return ProjectedSink(self._dzbuf(layer), ids[0], ids[1], self._token)
-
-    def _projected_call(self, layer: int, pid: int, grad: bool) -> Tensor:
-        """forward_projected on partition pid: reading Z in place through a
-        sink where the model allows it, else on gathered rows of Z (whose
-        gradient the gather adds into dZ when grad)."""
-        adj = self.graph.adjacency(pid)
-        if layer in self._inplace:
-            return self.model.forward_inplace(layer, self._xres[layer], adj, self._gids(pid)[0])
-        sink = self._sink(layer, pid)
-        if sink is not None:
-            return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
-        return self.model.forward_projected(
-            layer, self._gather_projected(layer, pid, grad=grad), adj)
-
-    def _projected_forward(self, layer: int, pid: int, keep: bool) -> Tensor:
-        """The forward of a projected layer on partition pid: with its graph
-        kept for the backward (keep), else without autograd, noting the RNG
-        state so that the backward's recompute draws the same dropout masks
-        (as torch.utils.checkpoint does in the reference's flow)."""
-        if keep:
-            with torch.enable_grad():
-                out = self._projected_call(layer, pid, grad=True)
-            self._graphs.setdefault(layer, {})[pid] = out
-            return out
-        if self.model.training:
-            self._rng[(layer, pid)] = torch.cuda.get_rng_state(self._device_index())
-        with torch.no_grad():
-            return self._projected_call(layer, pid, grad=False).contiguous()
-
-    def _device_index(self) -> int:
-        return self.device.index if self.device.index is not None else torch.cuda.current_device()
-
-    def _projected_recompute(self, layer: int, pid: int) -> Tensor:
-        """The partition's forward again, with autograd, from the RNG state
-        its first forward started from; the global RNG stream is left as it
-        was."""
-        state = self._rng.pop((layer, pid), None)
-        dev = self._device_index()
-        with torch.random.fork_rng(devices=[dev]), torch.enable_grad():
-            if state is not None:
-                torch.cuda.set_rng_state(state, dev)
-            return self._projected_call(layer, pid, grad=True)
-
-    def _project_rows(self, layer: int, x: Tensor, lo: int, hi: int) -> None:
-        """Z_layer[lo:hi] = x Wᵀ (no autograd)."""
-        w = self._proj[layer]
-        with torch.no_grad(), dense_region("fwd", hi - lo, w.size(1), w.size(0)):
-            torch.mm(x.detach(), w.detach().t(), out=self._zbuf(layer)[lo:hi])
-
-    def _each_input_partition(self, layer: int, fn) -> None:
-        """fn(pid, x_p, lo, hi) on the compute stream for every partition,
-        x_p = the partition's rows of the host buffer of layer `layer`'s
-        inputs, uploaded to HBM: into the layer's resident input buffer when
-        it has one this epoch, else through two buffers, so that the next
-        upload overlaps fn."""
-        g, s, pids = self.graph, self.streams, self._my_pids
-        host = self.host_features[layer]
-        din = host.embedding_dim
-        if layer in self._xin:
-            self._upload_resident(layer, fn)
-            return
-        bufs = self._xbufs.get(din)
-        if bufs is None:
-            with torch.cuda.stream(s.compute):
-                bufs = [torch.empty(max(g.partition_sizes), din, device=self.device)
-                        for _ in range(2)]
-            self._xbufs[din] = bufs
-        # The first upload into each buffer waits for the compute stream's
-        # queued work: a buffer allocated just now may occupy memory that
-        # queued compute kernels still read (the caching allocator reuses a
-        # block as soon as its stream has queued the last use), and a cached
-        # one may still be read by the previous call's last fn.
-        entry = torch.cuda.Event()
-        entry.record(s.compute)
-        freed: List[torch.cuda.Event] = [entry, entry]
-
-        def upload(i: int) -> torch.cuda.Event:
-            k, pid = i % 2, pids[i]
-            b = g.partition_sizes[pid]
-            st = s.h2d[k % len(s.h2d)]
-            st.wait_event(freed[k])
-            with torch.cuda.stream(st):
-                with KernelTimer.region("x_upload", 4 * b * din, 0, din):
-                    bufs[k][:b].copy_(host[pid], non_blocking=True)
-                ev = torch.cuda.Event()
-                ev.record(st)
-            return ev
-
-        ready = upload(0)
-        for i, pid in enumerate(pids):
-            k = i % 2
-            nxt = upload(i + 1) if i + 1 < len(pids) else None
-            s.compute.wait_event(ready)
-            with torch.cuda.stream(s.compute):
-                lo, hi = g._range(pid)
-                fn(pid, bufs[k][:hi - lo], lo, hi)
-                ev = torch.cuda.Event()
-                ev.record(s.compute)
-                freed[k] = ev
-            ready = nxt
-
-    def _upload_resident(self, layer: int, fn) -> None:
-        """_each_input_partition for layer 0's resident input buffer: every
-        partition has its own rows there, so fn(p) waits only for partition
-        p's upload.  The rows come from the upload the previous epoch started
-        into this buffer when there is one, else from one started now; with
-        two buffers, the next epoch's upload then starts into the other."""
-        if layer != 0:
-            raise ValueError("only layer 0's input rows are uploaded to a resident buffer")
-        g, s, pids = self.graph, self.streams, self._my_pids
-        if self._x0pending is not None:
-            idx, ready = self._x0pending
-            self._x0pending = None
-        else:
-            idx = self._x0cur
-            ready = self._issue_layer0_upload(idx)
-        self._x0cur = idx
-        x = self._xres[0] = self._x0bufs[idx]
-        for i, pid in enumerate(pids):
-            s.compute.wait_event(ready[i])
-            with torch.cuda.stream(s.compute):
-                lo, hi = g._range(pid)
-                fn(pid, x[lo:hi], lo, hi)
-        if self._x0double:
-            self._x0pending = (1 - idx, self._issue_layer0_upload(1 - idx))
-
-    def _issue_layer0_upload(self, idx: int) -> List[torch.cuda.Event]:
-        """Starts uploading every partition's layer-0 input rows into buffer
-        idx on the two prefetch streams; returns each partition's ready event.
-        The uploads first wait for the compute stream's queued work: the
-        buffer may be new (its memory just freed by queued compute work) or
-        still read by an earlier epoch."""
-        g, s, pids = self.graph, self.streams, self._my_pids
-        host = self.host_features[0]
-        n, din = int(g.ptr[-1]), host.embedding_dim
-        while len(self._x0bufs) <= idx:
-            with torch.cuda.stream(s.compute):
-                self._x0bufs.append(torch.empty(n, din, device=self.device))
-        x = self._x0bufs[idx]
-        if not self._pf_streams:
-            self._pf_streams = [torch.cuda.Stream(self.device) for _ in range(2)]
-        entry = torch.cuda.Event()
-        entry.record(s.compute)
-        for st in self._pf_streams:
-            st.wait_event(entry)
-            x.record_stream(st)
-        ready: List[torch.cuda.Event] = []
-        for i, pid in enumerate(pids):
-            lo, hi = g._range(pid)
-            st = self._pf_streams[i % 2]
-            with torch.cuda.stream(st):
-                with KernelTimer.region("x_upload", 4 * (hi - lo) * din, 0, din):
-                    x[lo:hi].copy_(host[pid], non_blocking=True)
-                ev = torch.cuda.Event()
-                ev.record(st)
-            ready.append(ev)
-        return ready
-
-    def _drop_prefetch(self) -> None:
-        """Forgets an upload started for an epoch that will not use it; later
-        compute work (and uploads, which wait for it) is ordered after it."""
-        if self._x0pending is not None:
-            for ev in self._x0pending[1]:
-                self.streams.compute.wait_event(ev)
-            self._x0pending = None
-
-    def _device_grad(self, layer: int, pid: int) -> Tensor:
-        """dL/d(x_layer) of partition pid's rows when layer `layer` runs
-        projected: dZ_layer[rows] W (the halo contributions of every partition
-        are already summed in dZ)."""
-        lo, hi = self.graph._range(pid)
-        w = self._proj[layer]
-        with dense_region("dx", hi - lo, w.size(0), w.size(1)):
-            return torch.mm(self._dzbufs[layer][lo:hi], w.detach())
-
-    def _backward_projected(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
-        """Backward of a projected layer: per partition, take the forward's
-        kept graph or recompute the layer from its gathered rows of Z, and
-        backpropagate into the layer's parameters and into dZ; then
-        dW = sum_p dZ_pᵀ x_p.  An in-place layer backpropagates the same way
-        into all its parameters (its input gets no gradient), with no dZ and
-        no dW pass."""
-        g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
-        if not pids:
-            return
-        last = layer == self.model.num_layers - 1
-        inplace = layer in self._inplace
-        if not inplace:
-            w = self._proj[layer]
-            dz = self._dzbuf(layer)
-            with torch.cuda.stream(s.compute):
-                dz.zero_()
-        from_device = (layer + 1) in self._proj
-        from_host = not last and not from_device
-        gbuf = self.device_gradients[layer + 1] if not last else None
-        if from_host:
-            self._upload_grad(layer + 1, pids[0], s.h2d[0])
-        for i, pid in enumerate(pids):
-            k = i % pool
-            if from_host:
-                self.host_gradients[layer + 1].h2d_synchronize(s.h2d[k])
-                s.compute.wait_stream(s.h2d[k])
-            with torch.cuda.stream(s.compute):
-                if from_host and i + 1 < len(pids) and pool > 1:
-                    self._upload_grad(layer + 1, pids[i + 1], s.h2d[(i + 1) % pool])
-                out = self._graphs.get(layer, {}).pop(pid, None)
-                if last and out is not None:
-                    # Kept logits: _compute_losses formed the loss from them.
-                    losses[self._pid_to_loss_idx[pid]].backward()
-                elif last:
-                    out = self._projected_recompute(layer, pid)
-                    y, codes = self._labels_and_codes(pid)
-                    with torch.enable_grad():
-                        loss, _ = masked_cross_entropy(out, y, codes, "sum")
-                    loss.backward()
-                else:
-                    if out is None:
-                        out = self._projected_recompute(layer, pid)
-                    if from_device:
-                        out.backward(self._device_grad(layer + 1, pid))
-                    else:
-                        out.backward(gbuf[pid])
-                        gbuf.release(pid)
-                # The gather's backward added dL/dz into dZ at the partition's
-                # rows (distinct within one partition): each element of dZ
-                # gets one addition per partition, in partition order.
-                del out
-                self.activations[layer][pid] = None
-            if from_host and pool == 1 and i + 1 < len(pids):
-                self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])
-        if inplace:
-            s.compute.synchronize()
-            return
-        with torch.cuda.stream(s.compute):
-            dw = torch.zeros_like(w)
-
-        def accumulate(pid, xp, lo, hi):
-            with dense_region("dw", hi - lo, w.size(0), w.size(1)):
-                gemm_tn(dz[lo:hi], xp, out=dw, beta=1.0)
-
-        if layer in self._xin:
-            x = self._xres[layer]
-            with torch.cuda.stream(s.compute):
-                for pid in pids:
-                    lo, hi = g._range(pid)
-                    accumulate(pid, x[lo:hi], lo, hi)
-        else:
-            self._each_input_partition(layer, accumulate)
-        with torch.cuda.stream(s.compute):
-            if w.grad is None:
-                w.grad = dw
-            else:
-                w.grad.add_(dw)
-        s.compute.synchronize()
-
     # ------------------------------------------------------------- forward
-
-    def _layer0_inputs(self, layer: int) -> None:
-        """Before the first layer's loop: its input rows uploaded into their
-        HBM copy (in place) or projected into Z_0 as they arrive (projected);
-        nothing for the reference flow, which gathers per partition."""
-        if layer != 0:
-            return
-        if layer in self._inplace:
-            # Every partition reads halo rows of the others: all uploads land
-            # before the compute stream goes on.
-            self._upload_resident(0, lambda pid, x, lo, hi: None)
-        elif layer in self._proj:
-            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
 
     def _forward_layer(self, layer: int) -> None:
         """Per partition: the layer's output from gathered input rows (the
@@ -859,43 +339,6 @@ class Trainer:
             last = (len(pids) - 1) % pool
             self.host_features[layer + 1].d2h_synchronize(s.d2h[last])
             self._free(self.activations[layer][pids[-1]])
-
-    def _forward_layer_resident(self, layer: int) -> None:
-        """_forward_layer when the next layer is projected and its input rows
-        stay in HBM: each partition's output goes to Z_{layer+1} and to the
-        resident copy of x_{layer+1}, and nothing crosses to the host."""
-        g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
-        projected = layer in self._proj or layer in self._inplace
-        x_next = self._xres_buf(layer + 1)
-        self._layer0_inputs(layer)
-        if not projected:
-            self._gather(layer, pids[0], s.h2d[0])
-        for i, pid in enumerate(pids):
-            k = i % pool
-            if not projected:
-                self.device_features[layer].h2d_synchronize(s.h2d[k])
-                s.compute.wait_stream(s.h2d[k])
-            with torch.cuda.stream(s.compute):
-                if not projected:
-                    if i + 1 < len(pids) and pool > 1:
-                        self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
-                    out = self._checkpointed(layer, pid, k)
-                else:
-                    out = self._projected_forward(layer, pid, keep=layer in self._keep)
-                lo, hi = g._range(pid)
-                self._project_rows(layer + 1, out, lo, hi)
-                with torch.no_grad():
-                    x_next[lo:hi].copy_(out)
-                if not (projected and layer in self._keep):
-                    # The storage goes back to the allocator in stream order; a
-                    # reference-flow layer keeps the tensor for its backward,
-                    # which recomputes it.  A kept graph keeps its output.
-                    self.activations[layer][pid] = out
-                    self._free(out)
-                if not projected:
-                    self.device_features[layer].release(pid)
-            if pool == 1 and not projected and i + 1 < len(pids):
-                self._gather(layer, pids[i + 1], s.h2d[0])
 
     # ---------------------------------------------------------------- loss
 
