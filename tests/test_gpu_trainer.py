@@ -282,7 +282,7 @@ def _limit_resident_inputs(monkeypatch, keep):
     monkeypatch.setattr(Trainer, "_plan_projection", limited)
 
 
-@pytest.mark.parametrize("model_kind", ["gcn", "gat"])
+@pytest.mark.parametrize("model_kind", ["gcn", "gat", "gat2"])
 @pytest.mark.parametrize("pool_size", [1, 2])
 @pytest.mark.parametrize("resident", ["all", "above0", "none"])
 def test_projected_layers_match_gathered(gpu, model_kind, pool_size, resident, monkeypatch):
@@ -300,7 +300,8 @@ def test_projected_layers_match_gathered(gpu, model_kind, pool_size, resident, m
     if model_kind == "gcn":
         make = lambda: GCN(24, 16, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
     else:
-        make = lambda: GAT(24, 8, 4, num_layers=3, heads=1, dropout=0.0, norm=True)  # noqa
+        heads = 2 if model_kind == "gat2" else 1
+        make = lambda: GAT(24, 8, 4, num_layers=3, heads=heads, dropout=0.0, norm=True)  # noqa
     state = make().state_dict()
     ei, x, y, tr, va, te = data
     runs = {}
