@@ -88,14 +88,22 @@ class ProjectedLayers:
         """Projected layers whose input rows stay in HBM this epoch."""
         return sorted(self._xin)
 
+    def _free_device_memory(self) -> int:
+        """Bytes new tensors can take: the device's free memory plus the
+        blocks torch's caching allocator holds unused (an earlier epoch's
+        kept graphs and temporaries, which the allocator hands out again)."""
+        free, _ = torch.cuda.mem_get_info(self.device)
+        return free + torch.cuda.memory_reserved(self.device) - torch.cuda.memory_allocated(self.device)
+
     def _plan_projection(self) -> Dict[int, Tensor]:
         """Layers this epoch runs projected, with their input projection W:
         grinnder mode, every partition on this trainer, and room in HBM for
         Z, dZ and the upload buffers (plus 8 GiB for the per-partition
-        working set).  A projected layer moves 2 N d_in bytes over the host
-        link (two uploads of its input rows) instead of 2 E d_in of gathers
-        and, above layer 0, an E d_in read-add-write scatter; when HBM is
-        short, layers with the most input width per byte of Z go first.
+        working set).  A projected layer moves at most two N d_in uploads of
+        its input rows over the host link (one, or none above layer 0, when
+        they stay in HBM) instead of 2 E d_in of gathers and, above layer 0,
+        an E d_in read-add-write scatter; when HBM is short, layers with the
+        most input width per byte of Z go first.
 
         Also decides self._xin, with what room is left: the projected layers
         whose input rows x stay in HBM for the epoch.  Above layer 0, x is
@@ -125,7 +133,7 @@ class ProjectedLayers:
         for _, layer, w in sorted(cands, key=lambda c: (-c[0], c[1])):
             if layer not in self._zbufs:
                 if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
+                    free = self._free_device_memory()
                 need = 4 * (2 * n * w.size(0) + 2 * maxb * w.size(1))
                 if need + (8 << 30) > free:
                     continue
@@ -134,7 +142,7 @@ class ProjectedLayers:
         for layer in sorted(plan, key=lambda l: (l == 0, l)):
             if layer not in self._xres:
                 if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
+                    free = self._free_device_memory()
                 need = 4 * n * plan[layer].size(1)
                 if need + (8 << 30) > free:
                     continue
@@ -157,7 +165,7 @@ class ProjectedLayers:
                     continue
                 d = plan[layer].size(0)
                 if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
+                    free = self._free_device_memory()
                 need = 4 * (sum_e * d + 3 * n * d + nnz)
                 if need + (8 << 30) > free:
                     continue
@@ -171,7 +179,7 @@ class ProjectedLayers:
                 self._x0double = True
             else:
                 if free is None:
-                    free, _ = torch.cuda.mem_get_info(self.device)
+                    free = self._free_device_memory()
                 need = 4 * n * plan[0].size(1)
                 if need + (8 << 30) <= free:
                     free -= need
