@@ -573,3 +573,38 @@ def test_mixed_flows_match_reference(gpu, pool_size, resident, monkeypatch):
     for k, err in grad_errs(g1, g0).items():
         assert err <= 1e-5, (k, err)
     assert e0["val_acc"] == e1["val_acc"]
+
+
+@pytest.mark.parametrize("model_kind", ["gcn_widening", "gcn_narrowing"])
+def test_training_trajectory_matches_reference_flow(gpu, model_kind):
+    """Three Adam epochs (weight decay, dropout 0.5 on layer outputs) from the
+    same weights in the reference flow and the default (projected / in place)
+    flow: every epoch's loss agrees within 1e-5 and the final weights within
+    1e-4 of their largest entry.  Each partition draws its dropout mask over
+    its own output rows in partition order in both flows, so the masks agree."""
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    ei, x, y, tr, va, te = data
+    hidden = 32 if model_kind == "gcn_widening" else 16
+    torch.manual_seed(8)
+    make = lambda: GCN(24, hidden, 4, num_layers=3, dropout=0.5, norm=True)  # noqa: E731
+    state = make().state_dict()
+    runs = {}
+    for proj in ("off", "auto"):
+        config = GriNNderConfig(num_parts=4, project_first=proj)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.Adam(model.parameters(), lr=0.01, weight_decay=5e-4)
+        crit = torch.nn.CrossEntropyLoss()
+        losses = []
+        for ep in range(3):
+            torch.manual_seed(100 + ep)
+            losses.append(trainer.train_epoch(opt, crit)["loss"])
+        if proj == "auto":
+            assert trainer.projected_layers + trainer.inplace_layers != []
+        runs[proj] = (losses, {k: v.detach().clone() for k, v in model.state_dict().items()})
+    (l0, w0), (l1, w1) = runs["off"], runs["auto"]
+    assert all(abs(a - b) < 1e-5 for a, b in zip(l0, l1)), (l0, l1)
+    for k, err in grad_errs(w1, w0).items():
+        assert err <= 1e-4, (k, err)
