@@ -377,7 +377,8 @@ class _GATAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hs: Tensor, att_src: Tensor, att_dst: Tensor, bias: Optional[Tensor],
-                plan: DevicePlan, heads: int, channels: int, concat: bool) -> Tensor:
+                plan: DevicePlan, heads: int, channels: int, concat: bool,
+                s_pre: Optional[Tensor] = None, d_pre: Optional[Tensor] = None) -> Tensor:
         hs = hs.contiguous()
         dev = hs.device
         H, C = heads, channels
@@ -390,10 +391,15 @@ class _GATAttention(torch.autograd.Function):
         region = KernelTimer.region(
             "gat_fwd", nnz * (4 * HC + 8 * H + 4) + B * (4 * HC + 4 * H + 4), nnz, HC)
         region.__enter__()
-        s = torch.empty((E, H), dtype=torch.float32, device=dev)
-        d = torch.empty((B, H), dtype=torch.float32, device=dev)
-        _lib.call("gr_gat_scores", hs.data_ptr(), hs.stride(0), E, B, H, C, a_src.data_ptr(),
-                  a_dst.data_ptr(), s.data_ptr(), d.data_ptr(), stream)
+        if s_pre is not None:
+            # Scores formed beforehand (once per layer for all rows of a
+            # projected matrix, by the same kernel): s_pre [E, H], d_pre [B, H].
+            s, d = s_pre.contiguous(), d_pre.contiguous()
+        else:
+            s = torch.empty((E, H), dtype=torch.float32, device=dev)
+            d = torch.empty((B, H), dtype=torch.float32, device=dev)
+            _lib.call("gr_gat_scores", hs.data_ptr(), hs.stride(0), E, B, H, C, a_src.data_ptr(),
+                      a_dst.data_ptr(), s.data_ptr(), d.data_ptr(), stream)
         m = torch.empty((B, H), dtype=torch.float32, device=dev)
         den = torch.empty((B, H), dtype=torch.float32, device=dev)
         alpha = torch.empty((max(nnz, 1), H), dtype=torch.float32, device=dev)
@@ -471,16 +477,39 @@ class _GATAttention(torch.autograd.Function):
         datt_src = column_sum(hs, ds, C)
         datt_dst = column_sum(hs[:B], dd, C)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
-                None, None, None, None)
+                None, None, None, None, None, None)
+
+
+def gat_scores(hs: Tensor, att_src: Tensor, att_dst: Tensor, heads: int, channels: int,
+               num_dst: int) -> Tuple[Tensor, Tensor]:
+    """The attention logits' two halves of GATConv (no autograd): s[r, h] =
+    <hs[r, h], att_src[h]> for every row and d[r, h] = <hs[r, h], att_dst[h]>
+    for the first num_dst rows, by the kernel gat_attention uses."""
+    _check_device_tensor("hs", hs)
+    hs = hs.contiguous()
+    E, H = hs.size(0), heads
+    if hs.size(1) != heads * channels or not 0 <= num_dst <= E:
+        raise ValueError("gat_scores: bad shape")
+    s = torch.empty((E, H), dtype=torch.float32, device=hs.device)
+    d = torch.empty((num_dst, H), dtype=torch.float32, device=hs.device)
+    a_src = att_src.detach().reshape(-1).contiguous()
+    a_dst = att_dst.detach().reshape(-1).contiguous()
+    _lib.call("gr_gat_scores", hs.data_ptr(), hs.stride(0), E, num_dst, H, channels,
+              a_src.data_ptr(), a_dst.data_ptr(), s.data_ptr(), d.data_ptr(),
+              _lib.stream_handle())
+    return s, d
 
 
 def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
                   bias: Optional[Tensor], heads: int, channels: int,
-                  concat: bool = True) -> Tensor:
+                  concat: bool = True,
+                  scores: Optional[Tuple[Tensor, Tensor]] = None) -> Tensor:
     """GATConv attention over a bipartite partition adjacency, on the GPU.
 
     hs = lin(x) for all E source rows; destination features are hs[:B].
     Returns [B, H*C] (concat) or [B, C] (mean over heads), bias added.
+    `scores`, when given, are the logit halves (s [E, H], d [B, H]) formed
+    beforehand by gat_scores, so they are not formed again here.
     """
     _check_device_tensor("hs", hs)
     plan = adj.device_plan(hs.device)
@@ -488,4 +517,9 @@ def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
         raise ValueError(f"hs has {hs.size(0)} rows, adjacency has {plan.num_src} columns")
     if hs.size(1) != heads * channels:
         raise ValueError(f"hs has {hs.size(1)} features, expected {heads * channels}")
-    return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat)
+    if scores is None:
+        return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat)
+    s, d = scores
+    if tuple(s.shape) != (plan.num_src, heads) or tuple(d.shape) != (plan.num_dst, heads):
+        raise ValueError("gat_attention: scores do not match the adjacency and heads")
+    return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat, s, d)

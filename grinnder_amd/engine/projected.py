@@ -73,6 +73,9 @@ class ProjectedLayers:
         self._x0double = False
         self._x0pending: Optional[tuple] = None
         self._pf_streams: List[torch.cuda.Stream] = []
+        # Per-row quantities of each projected layer's Z formed once for all
+        # partitions this epoch (GAT's attention scores), by layer.
+        self._scores: Dict[int, tuple] = {}
 
     @property
     def projected(self) -> bool:
@@ -296,8 +299,13 @@ class ProjectedLayers:
         sink = self._sink(layer, pid)
         if sink is not None:
             return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
-        return self.model.forward_projected(
-            layer, self._gather_projected(layer, pid, grad=grad), adj)
+        z = self._gather_projected(layer, pid, grad=grad)
+        sc = self._scores.get(layer)
+        if sc is None:
+            return self.model.forward_projected(layer, z, adj)
+        lo, hi = self.graph._range(pid)
+        s_rows = sc[0].index_select(0, self._global_rows(pid))
+        return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]))
 
     def _projected_forward(self, layer: int, pid: int, keep: bool) -> Tensor:
         """The forward of a projected layer on partition pid: with its graph
@@ -541,18 +549,27 @@ class ProjectedLayers:
         s.compute.synchronize()
 
 
-    def _layer0_inputs(self, layer: int) -> None:
-        """Before the first layer's loop: its input rows uploaded into their
-        HBM copy (in place) or projected into Z_0 as they arrive (projected);
-        nothing for the reference flow, which gathers per partition."""
-        if layer != 0:
-            return
-        if layer in self._inplace:
-            # Every partition reads halo rows of the others: all uploads land
-            # before the compute stream goes on.
-            self._upload_resident(0, lambda pid, x, lo, hi: None)
-        elif layer in self._proj:
-            self._each_input_partition(0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+    def _prepare_layer(self, layer: int) -> None:
+        """Before a layer's partition loop: the first layer's input rows
+        uploaded into their HBM copy (in place) or projected into Z_0 as they
+        arrive (projected); and, for a projected layer whose model takes
+        per-row quantities of Z precomputed (GAT's attention scores), those
+        formed once for all rows.  Nothing for the reference flow, which
+        gathers per partition."""
+        if layer == 0:
+            if layer in self._inplace:
+                # Every partition reads halo rows of the others: all uploads
+                # land before the compute stream goes on.
+                self._upload_resident(0, lambda pid, x, lo, hi: None)
+            elif layer in self._proj:
+                self._each_input_partition(
+                    0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+        self._scores.pop(layer, None)
+        if layer in self._proj:
+            with torch.cuda.stream(self.streams.compute):
+                sc = self.model.projected_scores(layer, self._zbufs[layer])
+            if sc is not None:
+                self._scores[layer] = sc
 
     def _forward_layer_resident(self, layer: int) -> None:
         """_forward_layer when the next layer is projected and its input rows
@@ -561,7 +578,7 @@ class ProjectedLayers:
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         projected = layer in self._proj or layer in self._inplace
         x_next = self._xres_buf(layer + 1)
-        self._layer0_inputs(layer)
+        self._prepare_layer(layer)
         if not projected:
             self._gather(layer, pids[0], s.h2d[0])
         for i, pid in enumerate(pids):

@@ -149,6 +149,7 @@ class Trainer(ProjectedLayers):
                 acts[i] = None
         self._graphs = {}
         self._rng = {}
+        self._scores = {}
 
     def train_epoch(self, optimizer: torch.optim.Optimizer,
                     criterion: torch.nn.Module) -> Dict[str, float]:
@@ -297,7 +298,7 @@ class Trainer(ProjectedLayers):
         if (layer + 1) in self._xin:
             self._forward_layer_resident(layer)
             return
-        self._layer0_inputs(layer)
+        self._prepare_layer(layer)
         if layer in self._keep and layer == self.model.num_layers - 1:
             # The last layer with its graphs kept: the loss reads the logits
             # from them (_compute_losses), so nothing goes to the host.

@@ -56,6 +56,13 @@ class GriNNderModel(torch.nn.Module):
         """Whether forward_projected(layer, ...) accepts a sink."""
         return False
 
+    def projected_scores(self, layer: int, z: Tensor):
+        """Per-row quantities of the projected matrix z that
+        forward_projected(layer, ...) can take precomputed for a partition's
+        gathered rows (its `scores` argument), formed once for all rows; None
+        when the layer has none (the default)."""
+        return None
+
     def inplace_ok(self, layer: int) -> bool:
         """Whether forward_inplace(layer, ...) exists and is the cheaper form
         of the layer when all partitions' input rows are in device memory

@@ -11,14 +11,15 @@ projection ``lin_src``/``lin_dst``; both spellings load.
 from __future__ import annotations
 
 import math
-from typing import Tuple, Union
+from typing import Optional, Tuple, Union
 
 import torch
 import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import Linear, Module, Parameter
 
-from grinnder_amd.aggregation import gat_attention, gcn_aggregate, gcn_linear_aggregate
+from grinnder_amd.aggregation import (gat_attention, gat_scores, gcn_aggregate,
+                                      gcn_linear_aggregate)
 from grinnder_amd.data.adjacency import Adjacency
 from grinnder_amd.dense import linear
 
@@ -146,21 +147,37 @@ class GATConv(Module):
             return y[:, :self.out_channels]
         return self.attend(linear(x_src, self.lin.weight), adj, add_bias)
 
-    def attend(self, hs: Tensor, adj: Adjacency, add_bias: bool = True) -> Tensor:
+    def _padded(self) -> int:
+        """Zero columns added to one head of C channels, C not a multiple of 4."""
+        return (-self.out_channels) % 4 if self.heads == 1 else 0
+
+    def attend(self, hs: Tensor, adj: Adjacency, add_bias: bool = True,
+               scores: Optional[Tuple[Tensor, Tensor]] = None) -> Tensor:
         """The layer after its projection: attention over hs = lin(x) for all
         source rows.  One head of C channels, C not a multiple of 4, runs on hs
         and the attention parameters zero-padded to a multiple of 4 (as in
-        forward)."""
+        forward).  `scores`: the logit halves of these rows from scores()."""
         bias = self.bias if add_bias else None
-        if self.heads == 1 and self.out_channels % 4 != 0:
-            pad = (-self.out_channels) % 4
+        pad = self._padded()
+        if pad:
             b = F.pad(bias, (0, pad)) if bias is not None else None
             y = gat_attention(F.pad(hs, (0, pad)), adj, F.pad(self.att_src, (0, pad)),
                               F.pad(self.att_dst, (0, pad)), b, 1, self.out_channels + pad,
-                              self.concat)
+                              self.concat, scores)
             return y[:, :self.out_channels]
         return gat_attention(hs, adj, self.att_src, self.att_dst, bias, self.heads,
-                             self.out_channels, self.concat)
+                             self.out_channels, self.concat, scores)
+
+    def scores(self, hs: Tensor) -> Tuple[Tensor, Tensor]:
+        """The logit halves (s, d) of every row of hs, as attend forms them
+        (padding included), for callers that hold hs for many partitions."""
+        pad = self._padded()
+        if pad:
+            return gat_scores(F.pad(hs, (0, pad)), F.pad(self.att_src, (0, pad)),
+                              F.pad(self.att_dst, (0, pad)), 1, self.out_channels + pad,
+                              hs.size(0))
+        return gat_scores(hs, self.att_src, self.att_dst, self.heads, self.out_channels,
+                          hs.size(0))
 
     def __repr__(self) -> str:
         return (f"{self.__class__.__name__}({self.in_channels}, {self.out_channels}, "

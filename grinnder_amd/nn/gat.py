@@ -4,6 +4,7 @@ from __future__ import annotations
 
 from typing import List
 
+import torch
 import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
@@ -72,15 +73,23 @@ class GAT(GriNNderModel):
             return None
         return self.convs[layer].lin.weight
 
-    def forward_projected(self, layer: int, hs: Tensor, adj, sink=None) -> Tensor:
+    def forward_projected(self, layer: int, hs: Tensor, adj, sink=None,
+                          scores=None) -> Tensor:
         if sink is not None:
             raise ValueError("GAT layers read gathered rows; they take no sink")
         conv = self.convs[layer]
         if self._fused_norm(layer, hs):
             norm = self.norms[layer]
-            x = conv.attend(hs, adj, add_bias=False)
+            x = conv.attend(hs, adj, add_bias=False, scores=scores)
             return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
-        return self._finish(layer, conv.attend(hs, adj))
+        return self._finish(layer, conv.attend(hs, adj, scores=scores))
+
+    def projected_scores(self, layer: int, z: Tensor):
+        """The attention logit halves of every row of the projected matrix z,
+        formed once for all partitions (no autograd: the attention-vector
+        gradients come from the attention's own backward)."""
+        with torch.no_grad():
+            return self.convs[layer].scores(z)
 
     def layer_dims(self) -> List[int]:
         dims = [self.convs[0].in_channels]
