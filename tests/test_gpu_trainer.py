@@ -608,3 +608,63 @@ def test_training_trajectory_matches_reference_flow(gpu, model_kind):
     assert all(abs(a - b) < 1e-5 for a, b in zip(l0, l1)), (l0, l1)
     for k, err in grad_errs(w1, w0).items():
         assert err <= 1e-4, (k, err)
+
+
+def _random_config(seed):
+    import random
+    r = random.Random(seed)
+    kind = r.choice(["gcn", "gat"])
+    layers = r.randint(2, 4)
+    feat = r.choice([3, 8, 12, 20])
+    hidden = r.choice([4, 8, 12, 16])
+    classes = r.choice([3, 4, 5])
+    norm = r.random() < 0.7
+    parts = r.choice([2, 3, 5])
+    pool = r.choice([1, 2])
+    if kind == "gcn":
+        residual = r.random() < 0.4
+        make = lambda: GCN(feat, hidden, classes, num_layers=layers, dropout=0.0,  # noqa: E731
+                           norm=norm, residual=residual)
+        desc = f"gcn L={layers} {feat}->{hidden}->{classes} norm={norm} residual={residual}"
+    else:
+        heads = r.choice([1, 2])
+        make = lambda: GAT(feat, hidden, classes, num_layers=layers, heads=heads,  # noqa: E731
+                           dropout=0.0, norm=norm)
+        desc = f"gat L={layers} {feat}->{hidden}x{heads}->{classes} norm={norm}"
+    return make, feat, classes, parts, pool, f"{desc} P={parts} pool={pool}"
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configs_match_reference_flow(gpu, seed):
+    """Seeded random models and partitionings (GCN / GAT, 2-4 layers, widths
+    that are and are not multiples of 4, widening and narrowing first layers,
+    residual layers that cannot be projected, 1-2 heads, 2-5 partitions, both
+    pool sizes): the default flow's loss, gradients and evaluate() equal the
+    reference flow's within the 1e-5 bound."""
+    make, feat, classes, parts, pool, desc = _random_config(seed)
+    print(f"config {seed}: {desc}", flush=True)
+    data = _graph_data(n=50, reach=3, feat=feat, classes=classes, seed=seed,
+                       train_all=False)
+    ei, x, y, tr, va, te = data
+    torch.manual_seed(seed)
+    state = make().state_dict()
+    runs = {}
+    for proj in ("off", "auto"):
+        config = GriNNderConfig(num_parts=parts, pool_size=pool, project_first=proj)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        crit = torch.nn.CrossEntropyLoss()
+        loss = trainer.train_epoch(opt, crit)["loss"]
+        grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()
+                 if p.grad is not None}
+        ev = trainer.evaluate(crit)
+        runs[proj] = (loss, grads, ev)
+    (l0, g0, e0), (l1, g1, e1) = runs["off"], runs["auto"]
+    assert abs(l0 - l1) < 1e-5, desc
+    assert set(g0) == set(g1), desc
+    for k, err in grad_errs(g1, g0).items():
+        assert err <= 1e-5, (desc, k, err)
+    assert e0["val_acc"] == e1["val_acc"], desc
