@@ -58,6 +58,9 @@ def parse_args():
                     help="partitioned configs: run layers on projected rows held in HBM "
                          "('auto', GriNNderConfig.project_first) or gather every layer's "
                          "input rows from the host buffers as the reference does ('off')")
+    ap.add_argument("--dropout", type=float, default=0.0,
+                    help="model dropout (the reference's own benchmarks use 0; GAT's input "
+                         "dropout, when active, rules out the projected flow)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
                     help="print a text summary of the rocprofv3 CSV output under DIR and exit")
@@ -270,10 +273,10 @@ def main():
     torch.manual_seed(42)
     if cfg["model"] == "gcn":
         model = GCN(cfg["feat_dim"], cfg["hidden"], cfg["num_classes"], cfg["num_layers"],
-                    dropout=0.0, norm=True).to(device)
+                    dropout=args.dropout, norm=True).to(device)
     else:
         model = GAT(cfg["feat_dim"], cfg["hidden"], cfg["num_classes"], cfg["num_layers"],
-                    heads=1, dropout=0.0, norm=True).to(device)
+                    heads=1, dropout=args.dropout, norm=True).to(device)
     t0 = time.perf_counter()
     trainer = Trainer(model, graph, config)
     from grinnder_amd.buffer.host import PINNED_STATS
@@ -304,6 +307,7 @@ def main():
         wall = time.perf_counter() - t0
     log(f"timed {args.steps} epochs in {wall:.3f}s (loss {metrics.get('loss', 0):.4f}); "
         f"projected layers {trainer.projected_layers}, in place {trainer.inplace_layers}, "
+        f"gathered from HBM {trainer.gathered_layers}, "
         f"inputs kept in HBM {trainer.resident_inputs}")
     if cfg["num_parts"] > 1:
         from grinnder_amd.buffer.host import PINNED_STATS
@@ -380,9 +384,11 @@ def main():
                    "nnz": nnz, "feat_dim": cfg["feat_dim"], "hidden": cfg["hidden"],
                    "num_classes": cfg["num_classes"], "num_layers": cfg["num_layers"],
                    "num_parts": cfg["num_parts"], "model": cfg["model"],
+                   "dropout": args.dropout,
                    "halo_amplification": round(graph.halo_amplification(), 4),
                    "projected_layers": trainer.projected_layers,
                    "inplace_layers": trainer.inplace_layers,
+                   "gathered_layers": trainer.gathered_layers,
                    "resident_inputs": trainer.resident_inputs},
         "epoch_s": round(epoch_s, 5),
         "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,

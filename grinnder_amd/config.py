@@ -32,12 +32,14 @@ class GriNNderConfig:
         the storage tier; this package keeps every layer host-resident, which
         is what 'auto' resolves to when the working set fits).
     device: GPU device string; pool_size: transfer double-buffering depth.
-    project_first: 'auto' lets the partitioned trainer project layer 0's
-        input rows once per partition and gather projected rows, held in HBM,
-        when the layer starts with a narrowing bias-free projection and they
-        fit (same results up to fp32 summation order); 'off' always gathers
-        input rows as the reference does.  Not a field of the reference's
-        config.
+    project_first: 'auto' lets the partitioned trainer (grinnder mode, all
+        partitions) keep layer data in HBM where it fits, planned per epoch:
+        a layer that starts with a bias-free input projection forms Z = x Wᵀ
+        once per partition and gathers (or reads in place) rows of Z; any
+        other layer gathers its input rows from an HBM copy and adds their
+        gradient into one (same results up to fp32 summation order).  'off'
+        gathers every layer's input rows from the host buffers as the
+        reference does.  Not a field of the reference's config.
     """
 
     mode: Literal["hongtu", "grinnder"] = "grinnder"

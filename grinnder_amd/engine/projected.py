@@ -1,9 +1,10 @@
 """Projected layers of the partitioned Trainer (grinnder_amd.engine.trainer).
 
-Mixin of Trainer: planning (which layers run projected or in place, which
-inputs and forward graphs stay in HBM, the layer-0 double buffer), the
-device buffers Z, dZ and resident inputs, the per-partition forward and
-backward of projected and in-place layers, and the layer-0 uploads.  The
+Mixin of Trainer: planning (which layers run projected, in place or
+gathered from HBM, which inputs and forward graphs stay in HBM, the layer-0
+double buffer), the device buffers Z, dZ, resident inputs and their
+gradients, the per-partition forward and backward of those layers, and the
+layer-0 uploads.  The
 trainer's module docstring describes the flow; the reference has no
 counterpart (its trainer gathers every layer's input rows from the host,
 grinnder/engine/trainer.py:477-1138).
@@ -22,9 +23,10 @@ from grinnder_amd.loss import masked_cross_entropy
 
 
 class _GatherRows(torch.autograd.Function):
-    """z = Z[rows] for a projected layer; the backward adds dL/dz into the
-    layer's dZ buffer at the same rows (distinct within a partition) instead
-    of returning a gradient for Z.  `token` is a zero-element tensor that
+    """z = Z[rows] of an HBM-resident matrix Z (a projected layer's Z, or a
+    gathered layer's input rows); the backward adds dL/dz into Z's gradient
+    buffer dz at the same rows (distinct within a partition) instead of
+    returning a gradient for Z.  `token` is a zero-element tensor that
     requires grad, so that autograd records the gather although Z does not."""
 
     @staticmethod
@@ -76,6 +78,12 @@ class ProjectedLayers:
         # Per-row quantities of each projected layer's Z formed once for all
         # partitions this epoch (GAT's attention scores), by layer.
         self._scores: Dict[int, tuple] = {}
+        # HBM buffers of dL/dx for the gathered layers above layer 0 (layers
+        # in self._xin that run neither projected nor in place), by layer.
+        self._gxbufs: Dict[int, Tensor] = {}
+        # Whether HBM has room this epoch for the logits of every partition
+        # (self._xres[num_layers]); see _logits_on_device.
+        self._out_room = False
 
     @property
     def projected(self) -> bool:
@@ -88,8 +96,38 @@ class ProjectedLayers:
 
     @property
     def resident_inputs(self) -> List[int]:
-        """Projected layers whose input rows stay in HBM this epoch."""
+        """Layers whose input rows stay in HBM this epoch."""
         return sorted(self._xin)
+
+    @property
+    def gathered_layers(self) -> List[int]:
+        """Layers that run the reference's per-partition forward this epoch
+        (no input projection) on input rows gathered from HBM: their input
+        rows stay there, and so does the gradient of those above layer 0."""
+        return sorted(self._gathered())
+
+    def _gathered(self) -> Set[int]:
+        return {l for l in self._xin if l not in self._proj and l not in self._inplace}
+
+    def _device_flow(self, layer: int) -> bool:
+        """Whether layer `layer` runs this epoch without host buffers:
+        projected, in place or gathered from HBM."""
+        return layer in self._proj or layer in self._inplace or layer in self._xin
+
+    def _grad_on_device(self, layer: int) -> bool:
+        """Whether dL/d(x_layer) of every partition is in HBM once layer
+        `layer`'s backward is done (projected: dZ W; gathered: its buffer)."""
+        return layer in self._proj or (layer in self._xin and layer not in self._inplace)
+
+    def _logits_on_device(self) -> bool:
+        """Whether the last layer's outputs go to an HBM buffer for the loss
+        this epoch instead of a D2H and an upload per partition: when that
+        layer runs without host buffers and keeps no forward graphs (kept
+        graphs hold the logits already).  Besides the two transfers, this
+        keeps the forward off the copy engines while the next epoch's layer-0
+        rows stream in: a D2H queued behind that upload waits for all of it."""
+        last = self.model.num_layers - 1
+        return self._out_room and self._device_flow(last) and last not in self._keep
 
     def _free_device_memory(self) -> int:
         """Bytes new tensors can take: the device's free memory plus the
@@ -114,12 +152,16 @@ class ProjectedLayers:
         upload for dW = sum_p dZ_pᵀ x_p crosses the host link; layer 0's rows
         are uploaded once per epoch, for the projection, and kept for dW
         instead of being uploaded a second time.  Layers above 0 go first
-        (each of their bytes saves two crossings).  Then self._keep: the
+        (each of their bytes saves two crossings).  Then, with what room is
+        still left, the gathered layers (added to self._xin): layers without
+        an input projection whose input rows (and, above layer 0, their
+        gradient) stay in HBM.  Then self._keep: the
         layers whose per-partition forward graphs are kept for the backward
         (training only)."""
         cfg, g = self.config, self.graph
         self._xin = set()
         self._keep = set()
+        self._out_room = False
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
             self._x0double = False
@@ -147,6 +189,28 @@ class ProjectedLayers:
                 if free is None:
                     free = self._free_device_memory()
                 need = 4 * n * plan[layer].size(1)
+                if need + (8 << 30) > free:
+                    continue
+                free -= need
+            self._xin.add(layer)
+        # Gathered layers: a layer with no input projection (GAT with active
+        # input dropout, a model without one) runs the reference's
+        # per-partition forward, but with its input rows kept in HBM when
+        # there is room: each partition gathers its rows there, and the
+        # backward adds dL/dx into an HBM buffer (above layer 0) instead of a
+        # host read-add-write over the link.  Layers above 0 first (their
+        # rows would cross the link four times, layer 0's twice).
+        for layer in sorted((l for l in range(self.model.num_layers) if l not in plan),
+                            key=lambda l: (l == 0, l)):
+            din = self.host_features[layer].embedding_dim
+            need = 0
+            if layer not in self._xres:
+                need += 4 * n * din
+            if layer > 0 and layer not in self._gxbufs:
+                need += 4 * n * din
+            if need:
+                if free is None:
+                    free = self._free_device_memory()
                 if need + (8 << 30) > free:
                     continue
                 free -= need
@@ -183,12 +247,20 @@ class ProjectedLayers:
             else:
                 if free is None:
                     free = self._free_device_memory()
-                need = 4 * n * plan[0].size(1)
+                need = 4 * n * self.host_features[0].embedding_dim
                 if need + (8 << 30) <= free:
                     free -= need
                     self._x0double = True
         if not self._x0double:
             self._drop_prefetch()
+        # Room for the logits of every partition (used when the last layer
+        # runs without host buffers; see _logits_on_device).
+        nl = self.model.num_layers
+        self._out_room = nl in self._xres
+        if not self._out_room:
+            if free is None:
+                free = self._free_device_memory()
+            self._out_room = 4 * n * self.host_features[nl].embedding_dim + (8 << 30) <= free
         return dict(sorted(plan.items()))
 
     def _plan_inplace(self) -> None:
@@ -218,6 +290,16 @@ class ProjectedLayers:
                                 device=self.device)
             self._xres[layer] = x
         return x
+
+    def _gxbuf(self, layer: int) -> Tensor:
+        """HBM buffer of dL/dx for a gathered layer's input rows."""
+        gx = self._gxbufs.get(layer)
+        if gx is None:
+            with torch.cuda.stream(self.streams.compute):
+                gx = torch.empty(int(self.graph.ptr[-1]), self.host_features[layer].embedding_dim,
+                                 device=self.device)
+            self._gxbufs[layer] = gx
+        return gx
 
     def _zbuf(self, layer: int) -> Tensor:
         z = self._zbufs.get(layer)
@@ -257,15 +339,20 @@ class ProjectedLayers:
     def _gather_projected(self, layer: int, pid: int, grad: bool = False) -> Tensor:
         """Partition pid's gathered rows of Z_layer; with grad, the backward
         adds their gradient into dZ_layer."""
+        return self._gather_rows("z_gather", pid, self._zbufs[layer],
+                                 self._dzbuf(layer) if grad else None)
+
+    def _gather_rows(self, name: str, pid: int, z: Tensor, dz: Optional[Tensor]) -> Tensor:
+        """Partition pid's gathered rows of the HBM matrix z; with dz, the
+        backward adds their gradient into dz."""
         rows = self._global_rows(pid)
-        z = self._zbufs[layer]
         d = z.size(1)
-        with KernelTimer.region("z_gather", 2 * 4 * rows.numel() * d, 0, d):
-            if not grad:
+        with KernelTimer.region(name, 2 * 4 * rows.numel() * d, 0, d):
+            if dz is None:
                 return z.index_select(0, rows)
             if self._token is None:
                 self._token = torch.zeros(0, device=self.device, requires_grad=True)
-            return _GatherRows.apply(self._token, z, rows, self._dzbuf(layer))
+            return _GatherRows.apply(self._token, z, rows, dz)
 
     def _gids(self, pid: int) -> tuple:
         """(global row of each CSR edge's source, global row of each gathered
@@ -289,13 +376,19 @@ class ProjectedLayers:
             self._token = torch.zeros(0, device=self.device, requires_grad=True)
         return ProjectedSink(self._dzbuf(layer), ids[0], ids[1], self._token)
 
-    def _projected_call(self, layer: int, pid: int, grad: bool) -> Tensor:
+    def _device_call(self, layer: int, pid: int, grad: bool) -> Tensor:
         """forward_projected on partition pid: reading Z in place through a
         sink where the model allows it, else on gathered rows of Z (whose
         gradient the gather adds into dZ when grad)."""
         adj = self.graph.adjacency(pid)
         if layer in self._inplace:
             return self.model.forward_inplace(layer, self._xres[layer], adj, self._gids(pid)[0])
+        if layer not in self._proj:
+            # A gathered layer: the reference's forward on the partition's
+            # input rows, gathered from HBM (layer 0's get no gradient).
+            gx = self._gxbuf(layer) if grad and layer > 0 else None
+            x = self._gather_rows("x_gather", pid, self._xres[layer], gx)
+            return self.model.forward_layer(layer, x, adj)
         sink = self._sink(layer, pid)
         if sink is not None:
             return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
@@ -307,25 +400,25 @@ class ProjectedLayers:
         s_rows = sc[0].index_select(0, self._global_rows(pid))
         return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]))
 
-    def _projected_forward(self, layer: int, pid: int, keep: bool) -> Tensor:
+    def _device_forward(self, layer: int, pid: int, keep: bool) -> Tensor:
         """The forward of a projected layer on partition pid: with its graph
         kept for the backward (keep), else without autograd, noting the RNG
         state so that the backward's recompute draws the same dropout masks
         (as torch.utils.checkpoint does in the reference's flow)."""
         if keep:
             with torch.enable_grad():
-                out = self._projected_call(layer, pid, grad=True)
+                out = self._device_call(layer, pid, grad=True)
             self._graphs.setdefault(layer, {})[pid] = out
             return out
         if self.model.training:
             self._rng[(layer, pid)] = torch.cuda.get_rng_state(self._device_index())
         with torch.no_grad():
-            return self._projected_call(layer, pid, grad=False).contiguous()
+            return self._device_call(layer, pid, grad=False).contiguous()
 
     def _device_index(self) -> int:
         return self.device.index if self.device.index is not None else torch.cuda.current_device()
 
-    def _projected_recompute(self, layer: int, pid: int) -> Tensor:
+    def _device_recompute(self, layer: int, pid: int) -> Tensor:
         """The partition's forward again, with autograd, from the RNG state
         its first forward started from; the global RNG stream is left as it
         was."""
@@ -334,7 +427,7 @@ class ProjectedLayers:
         with torch.random.fork_rng(devices=[dev]), torch.enable_grad():
             if state is not None:
                 torch.cuda.set_rng_state(state, dev)
-            return self._projected_call(layer, pid, grad=True)
+            return self._device_call(layer, pid, grad=True)
 
     def _project_rows(self, layer: int, x: Tensor, lo: int, hi: int) -> None:
         """Z_layer[lo:hi] = x Wᵀ (no autograd)."""
@@ -460,32 +553,42 @@ class ProjectedLayers:
             self._x0pending = None
 
     def _device_grad(self, layer: int, pid: int) -> Tensor:
-        """dL/d(x_layer) of partition pid's rows when layer `layer` runs
-        projected: dZ_layer[rows] W (the halo contributions of every partition
-        are already summed in dZ)."""
+        """dL/d(x_layer) of partition pid's rows when layer `layer` keeps that
+        gradient in HBM: dZ_layer[rows] W when it runs projected, else (a
+        gathered layer) its rows of the layer's dL/dx buffer.  The halo
+        contributions of every partition are already summed in either."""
         lo, hi = self.graph._range(pid)
+        if layer not in self._proj:
+            return self._gxbufs[layer][lo:hi]
         w = self._proj[layer]
         with dense_region("dx", hi - lo, w.size(0), w.size(1)):
             return torch.mm(self._dzbufs[layer][lo:hi], w.detach())
 
-    def _backward_projected(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
+    def _backward_device(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
         """Backward of a projected layer: per partition, take the forward's
         kept graph or recompute the layer from its gathered rows of Z, and
         backpropagate into the layer's parameters and into dZ; then
         dW = sum_p dZ_pᵀ x_p.  An in-place layer backpropagates the same way
         into all its parameters (its input gets no gradient), with no dZ and
-        no dW pass."""
+        no dW pass; so does a gathered layer, whose recompute regathers its
+        input rows in HBM and adds their gradient into the layer's dL/dx
+        buffer (above layer 0)."""
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
         last = layer == self.model.num_layers - 1
         inplace = layer in self._inplace
-        if not inplace:
+        gathered = layer not in self._proj and not inplace
+        if gathered:
+            if layer > 0:
+                with torch.cuda.stream(s.compute):
+                    self._gxbuf(layer).zero_()
+        elif not inplace:
             w = self._proj[layer]
             dz = self._dzbuf(layer)
             with torch.cuda.stream(s.compute):
                 dz.zero_()
-        from_device = (layer + 1) in self._proj
+        from_device = not last and self._grad_on_device(layer + 1)
         from_host = not last and not from_device
         gbuf = self.device_gradients[layer + 1] if not last else None
         if from_host:
@@ -503,14 +606,14 @@ class ProjectedLayers:
                     # Kept logits: _compute_losses formed the loss from them.
                     losses[self._pid_to_loss_idx[pid]].backward()
                 elif last:
-                    out = self._projected_recompute(layer, pid)
+                    out = self._device_recompute(layer, pid)
                     y, codes = self._labels_and_codes(pid)
                     with torch.enable_grad():
                         loss, _ = masked_cross_entropy(out, y, codes, "sum")
                     loss.backward()
                 else:
                     if out is None:
-                        out = self._projected_recompute(layer, pid)
+                        out = self._device_recompute(layer, pid)
                     if from_device:
                         out.backward(self._device_grad(layer + 1, pid))
                     else:
@@ -523,7 +626,7 @@ class ProjectedLayers:
                 self.activations[layer][pid] = None
             if from_host and pool == 1 and i + 1 < len(pids):
                 self._upload_grad(layer + 1, pids[i + 1], s.h2d[0])
-        if inplace:
+        if inplace or gathered:
             s.compute.synchronize()
             return
         with torch.cuda.stream(s.compute):
@@ -551,13 +654,13 @@ class ProjectedLayers:
 
     def _prepare_layer(self, layer: int) -> None:
         """Before a layer's partition loop: the first layer's input rows
-        uploaded into their HBM copy (in place) or projected into Z_0 as they
-        arrive (projected); and, for a projected layer whose model takes
-        per-row quantities of Z precomputed (GAT's attention scores), those
-        formed once for all rows.  Nothing for the reference flow, which
-        gathers per partition."""
+        uploaded into their HBM copy (in place, gathered) or projected into
+        Z_0 as they arrive (projected); and, for a projected layer whose model
+        takes per-row quantities of Z precomputed (GAT's attention scores),
+        those formed once for all rows.  Nothing for the reference flow, which
+        gathers per partition from the host."""
         if layer == 0:
-            if layer in self._inplace:
+            if layer in self._inplace or (layer in self._xin and layer not in self._proj):
                 # Every partition reads halo rows of the others: all uploads
                 # land before the compute stream goes on.
                 self._upload_resident(0, lambda pid, x, lo, hi: None)
@@ -572,11 +675,12 @@ class ProjectedLayers:
                 self._scores[layer] = sc
 
     def _forward_layer_resident(self, layer: int) -> None:
-        """_forward_layer when the next layer is projected and its input rows
-        stay in HBM: each partition's output goes to Z_{layer+1} and to the
-        resident copy of x_{layer+1}, and nothing crosses to the host."""
+        """_forward_layer when the next layer's input rows stay in HBM: each
+        partition's output goes to the resident copy of x_{layer+1} (and to
+        Z_{layer+1} when that layer runs projected), and nothing crosses to
+        the host."""
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
-        projected = layer in self._proj or layer in self._inplace
+        projected = self._device_flow(layer)
         x_next = self._xres_buf(layer + 1)
         self._prepare_layer(layer)
         if not projected:
@@ -592,9 +696,10 @@ class ProjectedLayers:
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
                 else:
-                    out = self._projected_forward(layer, pid, keep=layer in self._keep)
+                    out = self._device_forward(layer, pid, keep=layer in self._keep)
                 lo, hi = g._range(pid)
-                self._project_rows(layer + 1, out, lo, hi)
+                if (layer + 1) in self._proj:
+                    self._project_rows(layer + 1, out, lo, hi)
                 with torch.no_grad():
                     x_next[lo:hi].copy_(out)
                 if not (projected and layer in self._keep):

@@ -48,6 +48,12 @@ free HBM; 'off' keeps the reference's data movement):
 - A widening first GCN layer whose input rows stay in HBM runs in place
   instead (inplace_layers): it aggregates the narrower input first, reading
   it through global row ids, and needs no backward aggregation.
+- A layer with no input projection (GATConv with active input dropout, a
+  model without one) runs the reference's per-partition forward and
+  recompute, but when there is room its input rows stay in HBM
+  (gathered_layers): each partition gathers its rows there, and the
+  backward adds dL/dx into an HBM buffer, partitions in order, in place of
+  the host scatter.
 
 Per layer this replaces two host gathers and a read-add-write scatter of
 ~E x d_in rows (plus the D2H of the output and the upload of its gradient)
@@ -293,9 +299,10 @@ class Trainer(ProjectedLayers):
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         if not pids:
             return
-        projected = layer in self._proj or layer in self._inplace
+        projected = self._device_flow(layer)
         w_next = self._proj.get(layer + 1)
-        if (layer + 1) in self._xin:
+        last = layer == self.model.num_layers - 1
+        if (layer + 1) in self._xin or (last and self._logits_on_device()):
             self._forward_layer_resident(layer)
             return
         self._prepare_layer(layer)
@@ -304,7 +311,7 @@ class Trainer(ProjectedLayers):
             # from them (_compute_losses), so nothing goes to the host.
             for pid in pids:
                 with torch.cuda.stream(s.compute):
-                    self._projected_forward(layer, pid, keep=True)
+                    self._device_forward(layer, pid, keep=True)
             return
         if not projected:
             self._gather(layer, pids[0], s.h2d[0])
@@ -319,7 +326,7 @@ class Trainer(ProjectedLayers):
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
                 else:
-                    out = self._projected_forward(layer, pid, keep=False)
+                    out = self._device_forward(layer, pid, keep=False)
                 if w_next is not None:
                     lo, hi = g._range(pid)
                     self._project_rows(layer + 1, out, lo, hi)
@@ -361,13 +368,17 @@ class Trainer(ProjectedLayers):
             self.host_features[-1].async_upload(pid, act, stream)
 
         kept = last in self._keep and last in self._graphs
+        on_device = not kept and self._logits_on_device()
         with torch.cuda.stream(s.compute):
-            if not kept:
+            if not kept and not on_device:
                 upload(pids[0], s.h2d[0])
             for i, pid in enumerate(pids):
                 k = i % pool
                 if kept:
                     out = self._graphs[last][pid]
+                elif on_device:
+                    lo, hi = self.graph._range(pid)
+                    out = self._xres[last + 1][lo:hi]
                 else:
                     self.host_features[-1].h2d_synchronize(s.h2d[k])
                     s.compute.wait_stream(s.h2d[k])
@@ -382,7 +393,7 @@ class Trainer(ProjectedLayers):
                 losses.append(loss)
                 loss_sums.append(loss.detach())
                 stat_rows.append(stats)
-                if not kept:
+                if not kept and not on_device:
                     self._free(out)
             st = torch.stack(stat_rows).sum(0).tolist()
             total_loss = float(torch.stack(loss_sums).double().sum())
@@ -415,8 +426,8 @@ class Trainer(ProjectedLayers):
 
     def _backward_last_layer(self, losses: List[Tensor]) -> None:
         layer = self.model.num_layers - 1
-        if layer in self._proj or layer in self._inplace:
-            self._backward_projected(layer, losses)
+        if self._device_flow(layer):
+            self._backward_device(layer, losses)
         else:
             self._backward_pass(layer,
                                 lambda pid: losses[self._pid_to_loss_idx[pid]].backward())
@@ -424,10 +435,10 @@ class Trainer(ProjectedLayers):
             losses[i] = None
 
     def _backward_layer(self, layer: int) -> None:
-        if layer in self._proj or layer in self._inplace:
-            self._backward_projected(layer)
+        if self._device_flow(layer):
+            self._backward_device(layer)
             return
-        from_device = (layer + 1) in self._proj
+        from_device = self._grad_on_device(layer + 1)
 
         def run(pid: int) -> None:
             act = self.activations[layer][pid]

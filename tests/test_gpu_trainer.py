@@ -444,23 +444,29 @@ def _no_kept_graphs(monkeypatch):
     monkeypatch.setattr(Trainer, "_plan_projection", recompute)
 
 
-@pytest.mark.parametrize("flow", ["reference", "kept_graph", "recompute"])
+@pytest.mark.parametrize("flow", ["reference", "kept_graph", "recompute", "gathered",
+                                  "gat_reference"])
 def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
     """With dropout active, the backward must see the masks the forward drew:
     the reference flow's checkpoint restores the RNG state, a projected layer
     either keeps its forward graph or recomputes from the RNG state its
-    forward started from.  Every epoch below starts from the same seed, so
-    its forward draws the same masks and the reported loss is one smooth
-    function of the weights: its central difference along the gradient must
-    equal the gradient's norm (a backward that drew new masks is off by tens
-    of percent)."""
+    forward started from, and so does a gathered layer (GAT with input
+    dropout, gathered from HBM).  Every epoch below starts from the same
+    seed, so its forward draws the same masks and the reported loss is one
+    smooth function of the weights: its central difference along the
+    gradient must equal the gradient's norm (a backward that drew new masks
+    is off by tens of percent)."""
     data = _graph_data(n=60, reach=3, feat=24, classes=4)
     ei, x, y, tr, va, te = data
     if flow == "recompute":
         _no_kept_graphs(monkeypatch)
     torch.manual_seed(5)
-    model = GCN(24, 32, 4, num_layers=3, dropout=0.5, norm=True).cuda()
-    config = GriNNderConfig(num_parts=4, project_first="off" if flow == "reference" else "auto")
+    if flow in ("gathered", "gat_reference"):
+        model = GAT(24, 8, 4, num_layers=3, heads=2, dropout=0.5, norm=True).cuda()
+    else:
+        model = GCN(24, 32, 4, num_layers=3, dropout=0.5, norm=True).cuda()
+    reference = flow in ("reference", "gat_reference")
+    config = GriNNderConfig(num_parts=4, project_first="off" if reference else "auto")
     graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
     trainer = Trainer(model, graph, config)
     opt = torch.optim.SGD(model.parameters(), lr=0.0)
@@ -471,8 +477,10 @@ def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
         return trainer.train_epoch(opt, crit)["loss"]
 
     epoch()
-    if flow == "reference":
-        assert trainer.projected_layers == []
+    if reference:
+        assert trainer.projected_layers == [] and trainer.gathered_layers == []
+    elif flow == "gathered":
+        assert trainer.projected_layers == [] and trainer.gathered_layers == [0, 1, 2]
     else:
         # 24 -> 32 widens: the first layer reads its input rows in place.
         assert trainer.projected_layers == [1, 2] and trainer.inplace_layers == [0]
@@ -480,7 +488,9 @@ def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
     w = model.convs[1].lin.weight
     g = w.grad.detach().clone()
     v = g / g.norm()
-    delta = 1e-2
+    # GAT's attention logits pass a LeakyReLU, whose kinks the step can
+    # cross: at 1e-2 the central difference is 0.8% off in both flows alike.
+    delta = 1e-3 if model.__class__ is GAT else 1e-2
     with torch.no_grad():
         w.add_(delta * v)
     up = epoch()
@@ -493,19 +503,21 @@ def test_dropout_gradient_matches_finite_difference(gpu, flow, monkeypatch):
     assert abs(fd - float(g.norm())) <= 2e-3 * float(g.norm()) + 1e-4, (fd, float(g.norm()))
 
 
-@pytest.mark.parametrize("model_kind", ["gcn", "gat"])
+@pytest.mark.parametrize("model_kind", ["gcn", "gat", "gat_dropout"])
 def test_layer0_prefetch_across_epochs_is_exact(gpu, model_kind, monkeypatch):
     """Layer 0's input rows for the next epoch stream into a second buffer
     while an epoch computes: three training epochs (weights changing) and an
     evaluate() in between give bit-identical weights and metrics with and
-    without that prefetch."""
+    without that prefetch.  With GAT's input dropout, layer 0 is gathered
+    from those rows in training and projected from them in evaluate()."""
     data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
     ei, x, y, tr, va, te = data
     torch.manual_seed(4)
     if model_kind == "gcn":
         make = lambda: GCN(24, 32, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
     else:
-        make = lambda: GAT(24, 8, 4, num_layers=2, heads=1, dropout=0.0, norm=True)  # noqa
+        p = 0.5 if model_kind == "gat_dropout" else 0.0
+        make = lambda: GAT(24, 8, 4, num_layers=2, heads=1, dropout=p, norm=True)  # noqa
     state = make().state_dict()
     plan = Trainer._plan_projection
     runs = []
@@ -524,9 +536,14 @@ def test_layer0_prefetch_across_epochs_is_exact(gpu, model_kind, monkeypatch):
         trainer = Trainer(model, graph, config)
         opt = torch.optim.SGD(model.parameters(), lr=0.5)
         crit = torch.nn.CrossEntropyLoss()
-        metrics = [trainer.train_epoch(opt, crit), trainer.evaluate(crit),
-                   trainer.train_epoch(opt, crit), trainer.train_epoch(opt, crit)]
+        metrics = []
+        for i, step in enumerate(("train", "eval", "train", "train")):
+            torch.manual_seed(300 + i)
+            metrics.append(trainer.train_epoch(opt, crit) if step == "train"
+                           else trainer.evaluate(crit))
         assert len(trainer._x0bufs) == (2 if prefetch else 1)
+        if model_kind == "gat_dropout":
+            assert trainer.gathered_layers == [0, 1]
         runs.append((metrics, {k: v.detach().clone() for k, v in model.state_dict().items()}))
     (m0, w0), (m1, w1) = runs
     assert [m["loss"] for m in m0] == [m["loss"] for m in m1]
@@ -534,17 +551,19 @@ def test_layer0_prefetch_across_epochs_is_exact(gpu, model_kind, monkeypatch):
 
 
 @pytest.mark.parametrize("pool_size", [1, 2])
-@pytest.mark.parametrize("resident", ["all", "none"])
+@pytest.mark.parametrize("resident", ["all", "projected", "none"])
 def test_mixed_flows_match_reference(gpu, pool_size, resident, monkeypatch):
     """A residual GCN whose 16 -> 16 layers cannot be projected (the residual
-    add needs x itself): layers 0 and 3 run projected, layers 1 and 2 the
-    reference flow, so outputs and gradients cross between the two flows in
-    both directions (device Z rows and host buffers forward; host gradient
+    add needs x itself): layers 0 and 3 run projected, layers 1 and 2 are
+    gathered from HBM (all inputs resident) or take the reference flow's host
+    buffers (only the projected layers' inputs resident, or none), so outputs
+    and gradients cross between the flows in both directions (device Z rows,
+    resident inputs and host buffers forward; host gradient buffers, dL/dx
     buffers and dZ W backward).  Loss, gradients and evaluate() equal those of
     the reference flow throughout within the 1e-5 bound, over two epochs."""
-    kept = {"all": [0, 1, 2, 3], "none": []}[resident]
-    if resident == "none":
-        _limit_resident_inputs(monkeypatch, set())
+    kept = {"all": [0, 1, 2, 3], "projected": [0, 3], "none": []}[resident]
+    if resident != "all":
+        _limit_resident_inputs(monkeypatch, set(kept))
     data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
     ei, x, y, tr, va, te = data
     torch.manual_seed(6)
@@ -566,10 +585,57 @@ def test_mixed_flows_match_reference(gpu, pool_size, resident, monkeypatch):
         ev = trainer.evaluate(crit)
         if proj == "auto":
             assert trainer.projected_layers == [0, 3]
-            assert trainer.resident_inputs == [l for l in kept if l in (0, 3)]
+            assert trainer.resident_inputs == kept
+            assert trainer.gathered_layers == [l for l in kept if l in (1, 2)]
         runs[proj] = (losses, grads, ev)
     (l0, g0, e0), (l1, g1, e1) = runs["off"], runs["auto"]
     assert all(abs(a - b) < 1e-5 for a, b in zip(l0, l1))
+    for k, err in grad_errs(g1, g0).items():
+        assert err <= 1e-5, (k, err)
+    assert e0["val_acc"] == e1["val_acc"]
+
+
+@pytest.mark.parametrize("heads", [1, 2])
+@pytest.mark.parametrize("pool_size", [1, 2])
+@pytest.mark.parametrize("resident", ["all", "above0", "none"])
+def test_gathered_layers_match_reference_flow(gpu, heads, pool_size, resident, monkeypatch):
+    """GAT with input dropout (0.6, the model's default): no layer can run
+    projected in training, so every layer is gathered from HBM when its input
+    rows stay there (all layers, those above layer 0, or none: the reference
+    flow's host buffers).  Over two seeded epochs the loss, the gradients and
+    evaluate() (which runs projected: dropout is off) equal the reference
+    flow's within the 1e-5 bound."""
+    kept = {"all": [0, 1, 2], "above0": [1, 2], "none": []}[resident]
+    if resident != "all":
+        _limit_resident_inputs(monkeypatch, set(kept))
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    ei, x, y, tr, va, te = data
+    torch.manual_seed(9)
+    make = lambda: GAT(24, 8, 4, num_layers=3, heads=heads, norm=True)  # noqa: E731
+    state = make().state_dict()
+    runs = {}
+    for proj in ("off", "auto"):
+        config = GriNNderConfig(num_parts=4, pool_size=pool_size, project_first=proj)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        assert model.dropout == 0.6
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        crit = torch.nn.CrossEntropyLoss()
+        torch.manual_seed(200)
+        losses = [trainer.train_epoch(opt, crit)["loss"]]
+        grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()}
+        if proj == "auto":
+            assert trainer.projected_layers == [] and trainer.gathered_layers == kept
+        torch.manual_seed(201)
+        losses.append(trainer.train_epoch(opt, crit)["loss"])
+        ev = trainer.evaluate(crit)
+        if proj == "auto":
+            assert trainer.projected_layers == [0, 1, 2] and trainer.gathered_layers == []
+        runs[proj] = (losses, grads, ev)
+    (l0, g0, e0), (l1, g1, e1) = runs["off"], runs["auto"]
+    assert all(abs(a - b) < 1e-5 for a, b in zip(l0, l1)), (l0, l1)
     for k, err in grad_errs(g1, g0).items():
         assert err <= 1e-5, (k, err)
     assert e0["val_acc"] == e1["val_acc"]
@@ -628,9 +694,12 @@ def _random_config(seed):
         desc = f"gcn L={layers} {feat}->{hidden}->{classes} norm={norm} residual={residual}"
     else:
         heads = r.choice([1, 2])
+        # Active input dropout keeps GAT layers off the projected flow: they
+        # run gathered from HBM.
+        dropout = r.choice([0.0, 0.0, 0.5])
         make = lambda: GAT(feat, hidden, classes, num_layers=layers, heads=heads,  # noqa: E731
-                           dropout=0.0, norm=norm)
-        desc = f"gat L={layers} {feat}->{hidden}x{heads}->{classes} norm={norm}"
+                           dropout=dropout, norm=norm)
+        desc = f"gat L={layers} {feat}->{hidden}x{heads}->{classes} norm={norm} dropout={dropout}"
     return make, feat, classes, parts, pool, f"{desc} P={parts} pool={pool}"
 
 
@@ -638,9 +707,10 @@ def _random_config(seed):
 def test_random_configs_match_reference_flow(gpu, seed):
     """Seeded random models and partitionings (GCN / GAT, 2-4 layers, widths
     that are and are not multiples of 4, widening and narrowing first layers,
-    residual layers that cannot be projected, 1-2 heads, 2-5 partitions, both
-    pool sizes): the default flow's loss, gradients and evaluate() equal the
-    reference flow's within the 1e-5 bound."""
+    residual layers that cannot be projected, GAT with and without input
+    dropout, 1-2 heads, 2-5 partitions, both pool sizes): the default flow's
+    loss, gradients and evaluate() equal the reference flow's within the 1e-5
+    bound."""
     make, feat, classes, parts, pool, desc = _random_config(seed)
     print(f"config {seed}: {desc}", flush=True)
     data = _graph_data(n=50, reach=3, feat=feat, classes=classes, seed=seed,
@@ -657,6 +727,7 @@ def test_random_configs_match_reference_flow(gpu, seed):
         trainer = Trainer(model, graph, config)
         opt = torch.optim.SGD(model.parameters(), lr=0.0)
         crit = torch.nn.CrossEntropyLoss()
+        torch.manual_seed(1000 + seed)
         loss = trainer.train_epoch(opt, crit)["loss"]
         grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()
                  if p.grad is not None}
