@@ -109,6 +109,26 @@ def column_sum(g: Tensor, weights: Optional[Tensor] = None, group: int = 1) -> T
     return out
 
 
+def scatter_add_rows(x: Tensor, rows: Tensor, y: Tensor) -> None:
+    """y[rows[r]] += x[r] in place on the current stream (HIP kernel, no
+    atomics): fp32 [n, D] rows into fp32 [*, D] y, rows int64 on the device
+    and distinct, which is what makes the result deterministic.  The same
+    values as y.index_add_(0, rows, x) for distinct rows."""
+    if x.dim() != 2 or y.dim() != 2 or x.size(1) != y.size(1) or rows.numel() != x.size(0):
+        raise ValueError("scatter_add_rows: x [n, D], rows [n], y [*, D]")
+    if x.dtype != torch.float32 or y.dtype != torch.float32 or rows.dtype != torch.int64:
+        raise ValueError("scatter_add_rows: fp32 x and y, int64 rows")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    if y.stride(-1) != 1:
+        raise ValueError("scatter_add_rows: y rows must be contiguous")
+    rows = rows.contiguous()
+    n, dim = x.shape
+    _lib.call("gr_scatter_add_rows", x.data_ptr(), n, dim, max(x.stride(0), dim),
+              rows.data_ptr(), y.data_ptr(), y.size(0), max(y.stride(0), dim),
+              _lib.stream_handle())
+
+
 def _workspace(n_slots: int, width: int, device) -> Optional[Tensor]:
     if n_slots == 0:
         return None

@@ -691,6 +691,55 @@ inline bool aligned(const void* p, int bytes) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
+// y[rows[r]][j] += x[r][j] over n rows of dv V-wide elements.  The rows are
+// distinct (the caller's contract), so every element of y has one writer: no
+// atomics, and the result is the same as adding the rows one at a time.  A
+// row id outside [0, y_rows) is skipped rather than written.  Flat over
+// elements (I: the index type), four independent read-add-writes in flight
+// per lane.
+template <typename V, typename I>
+__global__ __launch_bounds__(256) void scatter_add_rows(const V* __restrict__ x, I n, I dv,
+                                                       I ldx, const int64_t* __restrict__ rows,
+                                                       V* __restrict__ y, I ldy, int64_t y_rows) {
+  const I total = n * dv;
+  const I stride = (I)gridDim.x * 256;
+  for (I base = (I)blockIdx.x * 256 + (I)threadIdx.x; base < total; base += 4 * stride) {
+    V xv[4], yv[4];
+    V* dst[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const I i = base + u * stride;
+      dst[u] = nullptr;
+      if (i < total) {
+        const I r = i / dv;
+        const I j = i - r * dv;
+        const int64_t t = rows[r];
+        if (t >= 0 && t < y_rows) {
+          dst[u] = y + (I)t * ldy + j;
+          xv[u] = x[r * ldx + j];
+          yv[u] = *dst[u];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (dst[u] != nullptr) *dst[u] = yv[u] + xv[u];
+  }
+}
+
+template <typename V, typename I>
+void launch_scatter_add_rows(const float* x, int64_t n, int64_t dim, int64_t ldx,
+                             const int64_t* rows, float* y, int64_t ldy, int64_t y_rows,
+                             hipStream_t s) {
+  constexpr int W = sizeof(V) / sizeof(float);
+  const int64_t total = n * (dim / W);
+  const int64_t want = (total + 1023) / 1024;
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 1 << 20));
+  hipLaunchKernelGGL((scatter_add_rows<V, I>), dim3(grid), dim3(256), 0, s,
+                     reinterpret_cast<const V*>(x), (I)n, (I)(dim / W), (I)(ldx / W), rows,
+                     reinterpret_cast<V*>(y), (I)(ldy / W), y_rows);
+}
+
 }  // namespace gr_agg
 
 namespace gr_agg {
@@ -774,6 +823,33 @@ int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t
                        dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias, orow);
     GR_HIP_CHECK(hipGetLastError());
   }
+  return GR_OK;
+}
+
+extern "C" int gr_scatter_add_rows(const float* x, int64_t n, int64_t dim, int64_t ldx,
+                                   const int64_t* rows, float* y, int64_t y_rows, int64_t ldy,
+                                   void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(n >= 0 && dim >= 1 && ldx >= dim && ldy >= dim && y_rows >= 0,
+             "scatter_add_rows: bad shape");
+  if (n == 0) return GR_OK;
+  GR_REQUIRE(x != nullptr && rows != nullptr && y != nullptr, "scatter_add_rows: NULL pointer");
+  hipStream_t s = gr::as_stream(stream);
+  const bool vec = dim % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && gr_agg::aligned(x, 16) &&
+                   gr_agg::aligned(y, 16);
+  // 32-bit element indices when every offset fits: below 2^30 elements of x
+  // the loop's index (at most total + 4 grid strides, a stride at most 2^28)
+  // stays below 2^31 too.
+  const bool narrow = n * ldx < (int64_t(1) << 30) && y_rows * ldy < (int64_t(1) << 31);
+  if (vec && narrow)
+    gr_agg::launch_scatter_add_rows<float4, int32_t>(x, n, dim, ldx, rows, y, ldy, y_rows, s);
+  else if (vec)
+    gr_agg::launch_scatter_add_rows<float4, int64_t>(x, n, dim, ldx, rows, y, ldy, y_rows, s);
+  else if (narrow)
+    gr_agg::launch_scatter_add_rows<float, int32_t>(x, n, dim, ldx, rows, y, ldy, y_rows, s);
+  else
+    gr_agg::launch_scatter_add_rows<float, int64_t>(x, n, dim, ldx, rows, y, ldy, y_rows, s);
+  GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
 

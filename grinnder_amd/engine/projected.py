@@ -17,7 +17,7 @@ from typing import Dict, List, Optional, Set
 import torch
 from torch import Tensor
 
-from grinnder_amd.aggregation import KernelTimer, ProjectedSink, dense_region
+from grinnder_amd.aggregation import KernelTimer, ProjectedSink, dense_region, scatter_add_rows
 from grinnder_amd.dense import gemm_tn
 from grinnder_amd.loss import masked_cross_entropy
 
@@ -36,7 +36,9 @@ class _GatherRows(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad: Tensor):
-        ctx.dz.index_add_(0, ctx.rows, grad)
+        d = grad.size(1)
+        with KernelTimer.region("row_scatter_add", 3 * 4 * grad.size(0) * d, 0, d):
+            scatter_add_rows(grad, ctx.rows, ctx.dz)
         return None, None, None, None
 
 

@@ -228,6 +228,20 @@ int gr_gcn_aggregate_into(const int32_t* units, int64_t n_units,
                           int64_t ldy, int64_t rows, int64_t dim,
                           float* workspace, int64_t n_slots, void* stream);
 
+/* No counterpart in the reference: the backward of a row gather from an
+ * HBM-resident matrix (the trainer's projected and gathered layers, which
+ * take a partition's rows on the device where the reference gathers them
+ * from host buffers and scatters their gradient back with
+ * scatter_partitions, csrc/cuda/async_transfer.cu:122-186):
+ *   y[rows[r]][j] += x[r][j]   for r < n, j < dim,
+ * x [n, dim] with row stride ldx, y [y_rows, dim] with row stride ldy, rows
+ * device int64.  rows must be distinct within one call (each y row has one
+ * writer: no atomics, deterministic, the same as adding the rows one at a
+ * time); a row id outside [0, y_rows) is skipped. */
+int gr_scatter_add_rows(const float* x, int64_t n, int64_t dim, int64_t ldx,
+                        const int64_t* rows, float* y, int64_t y_rows, int64_t ldy,
+                        void* stream);
+
 /* Fused GCN layer epilogue (bias + LayerNorm + ReLU of grinnder/nn/gcn.py:
  * 64-72, LayerNorm of torch with biased variance and eps):
  *   h[r]   = sum_e val[e] * X[idx[e]] + bias       (written, kept for backward)

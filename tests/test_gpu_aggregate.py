@@ -156,6 +156,52 @@ def test_gcn_linear_aggregate_matches_oracle(gpu, B, E, fin, fout):
     assert max_abs_norm_err(bd.grad, gy.double().sum(0)) <= TOL
 
 
+@pytest.mark.parametrize("dim,ldx,ldy", [(1, 1, 1), (3, 3, 5), (19, 19, 19), (20, 24, 20),
+                                         (64, 64, 68), (256, 256, 256), (1024, 1028, 1024)])
+def test_scatter_add_rows_equals_index_add(gpu, dim, ldx, ldy):
+    """gr_scatter_add_rows (the backward of the trainer's device row gathers)
+    against torch's index_add_ for distinct rows, bit for bit: 16-byte and
+    scalar accesses, strided x and y, and row ids outside y skipped."""
+    from grinnder_amd.aggregation import scatter_add_rows
+    g = torch.Generator().manual_seed(dim)
+    y_rows, n = 5000, 3000
+    rows = torch.randperm(y_rows, generator=g)[:n]
+    xs = torch.randn(n, ldx, generator=g)[:, :dim].cuda()
+    ys = torch.randn(y_rows, ldy, generator=g)[:, :dim].cuda()
+    r = rows.cuda()
+    expect = ys.clone().index_add_(0, r, xs)
+    got = ys.clone()
+    scatter_add_rows(xs, r, got)
+    assert torch.equal(got, expect)
+    # Ids outside [0, y_rows) are skipped; the others still land.
+    bad = rows.clone()
+    bad[::7] = -1
+    bad[3::7] = y_rows
+    keep = (bad >= 0) & (bad < y_rows)
+    expect = ys.clone().index_add_(0, bad[keep].cuda(), xs[keep.cuda()])
+    got = ys.clone()
+    scatter_add_rows(xs, bad.cuda(), got)
+    assert torch.equal(got, expect)
+    scatter_add_rows(xs[:0], r[:0], got)  # no rows: nothing to do
+    assert torch.equal(got, expect)
+
+
+def test_scatter_add_rows_64bit_offsets(gpu):
+    """The 64-bit index path, which x of 2^30 elements (4 GiB) takes: every
+    chosen row of y gets its ones, the others stay zero."""
+    n, dim = 1 << 20, 1024
+    y_rows = n + 4096
+    rows = torch.randperm(y_rows, device="cuda")[:n]
+    x = torch.ones(n, dim, device="cuda")
+    y = torch.zeros(y_rows, dim, device="cuda")
+    from grinnder_amd.aggregation import scatter_add_rows
+    scatter_add_rows(x, rows, y)
+    hit = torch.zeros(y_rows, dtype=torch.bool, device="cuda")
+    hit[rows] = True
+    assert bool((y[hit] == 1).all()) and bool((y[~hit] == 0).all())
+    del x, y
+
+
 @pytest.mark.parametrize("dim", [3, 47, 64, 256, 300, 1024])
 def test_aggregate_into_equals_spmm_then_index_add(gpu, dim):
     """gr_gcn_aggregate_into (output row map, accumulate) against the plain
