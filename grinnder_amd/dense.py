@@ -68,17 +68,27 @@ def gemm_tn(a: Tensor, b: Tensor, out: Optional[Tensor] = None, beta: float = 0.
 
 
 class _Linear(torch.autograd.Function):
-    """y = x W^T (+ b); dx = dy W (torch), dW = dy^T x (gr_gemm_tn), db = sum dy."""
+    """y = x W^T (+ b); dx = dy W (torch), dW = dy^T x (gr_gemm_tn), db = sum dy.
+    `reuse` (a one-element list, or None) holds y as an earlier forward
+    computed it from the same x, W and b: it is returned instead of being
+    recomputed, and the backward is the same."""
 
     @staticmethod
-    def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor],
+                reuse: Optional[list] = None) -> Tensor:
         from grinnder_amd.aggregation import dense_region
         x2 = x.reshape(-1, x.size(-1))
-        with dense_region("fwd", x2.size(0), x2.size(1), weight.size(0)):
-            if bias is not None:
-                y = torch.addmm(bias, x2, weight.t())
-            else:
-                y = torch.mm(x2, weight.t())
+        if reuse is not None:
+            y = reuse[0].detach()
+            if y.shape != (x2.size(0), weight.size(0)):
+                raise ValueError(f"linear: reused product has shape {tuple(y.shape)}, "
+                                 f"expected {(x2.size(0), weight.size(0))}")
+        else:
+            with dense_region("fwd", x2.size(0), x2.size(1), weight.size(0)):
+                if bias is not None:
+                    y = torch.addmm(bias, x2, weight.t())
+                else:
+                    y = torch.mm(x2, weight.t())
         ctx.save_for_backward(x2, weight)
         ctx.in_shape = x.shape
         ctx.has_bias = bias is not None
@@ -100,14 +110,18 @@ class _Linear(torch.autograd.Function):
         if ctx.has_bias and ctx.needs_input_grad[2]:
             from grinnder_amd.aggregation import column_sum
             db = column_sum(gy2)
-        return dx, dw, db
+        return dx, dw, db, None
 
 
-def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
-    """``F.linear`` whose weight gradient runs on the split-K MFMA kernel (GPU)."""
+def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None,
+           reuse: Optional[Tensor] = None) -> Tensor:
+    """``F.linear`` whose weight gradient runs on the split-K MFMA kernel (GPU).
+    `reuse`: this product as an earlier forward formed it from the same
+    operands (rows [-1, out]); it is returned instead of recomputed, with the
+    same backward."""
     if not x.is_cuda:
         raise RuntimeError(f"linear: x must be a GPU tensor (HIP); got {x.device}")
-    return _Linear.apply(x, weight, bias)
+    return _Linear.apply(x, weight, bias, None if reuse is None else [reuse])
 
 
 class _BiasLNAct(torch.autograd.Function):

@@ -86,6 +86,11 @@ class ProjectedLayers:
         # Whether HBM has room this epoch for the logits of every partition
         # (self._xres[num_layers]); see _logits_on_device.
         self._out_room = False
+        # What a gathered layer's forward kept for its recompute
+        # (model.forward_gathered), by (layer, pid), and the bytes still free
+        # for that this epoch.
+        self._gkept: Dict[tuple, Tensor] = {}
+        self._gkept_left = 0
 
     @property
     def projected(self) -> bool:
@@ -262,7 +267,18 @@ class ProjectedLayers:
         if not self._out_room:
             if free is None:
                 free = self._free_device_memory()
-            self._out_room = 4 * n * self.host_features[nl].embedding_dim + (8 << 30) <= free
+            need = 4 * n * self.host_features[nl].embedding_dim
+            self._out_room = need + (8 << 30) <= free
+            if self._out_room:
+                free -= need
+        # What is left (training with gathered layers): what their forwards
+        # keep for the recompute, partition by partition while it fits.
+        self._gkept = {}
+        self._gkept_left = 0
+        if self.model.training and any(l not in plan for l in self._xin):
+            if free is None:
+                free = self._free_device_memory()
+            self._gkept_left = max(0, free - (8 << 30))
         return dict(sorted(plan.items()))
 
     def _plan_inplace(self) -> None:
@@ -387,10 +403,25 @@ class ProjectedLayers:
             return self.model.forward_inplace(layer, self._xres[layer], adj, self._gids(pid)[0])
         if layer not in self._proj:
             # A gathered layer: the reference's forward on the partition's
-            # input rows, gathered from HBM (layer 0's get no gradient).
+            # input rows, gathered from HBM (layer 0's get no gradient).  The
+            # first forward keeps what the model offers for the recompute
+            # (forward_gathered) while the epoch's budget allows; the
+            # recompute takes it back.
             gx = self._gxbuf(layer) if grad and layer > 0 else None
             x = self._gather_rows("x_gather", pid, self._xres[layer], gx)
-            return self.model.forward_layer(layer, x, adj)
+            if grad:
+                return self.model.forward_gathered(layer, x, adj,
+                                                   reuse=self._gkept.pop((layer, pid), None))
+            if not self.model.training or self._gkept_left <= 0:
+                return self.model.forward_layer(layer, x, adj)
+            keep: List[Tensor] = []
+            out = self.model.forward_gathered(layer, x, adj, keep=keep)
+            if len(keep) == 1:
+                nbytes = keep[0].numel() * keep[0].element_size()
+                if nbytes <= self._gkept_left:
+                    self._gkept[(layer, pid)] = keep[0]
+                    self._gkept_left -= nbytes
+            return out
         sink = self._sink(layer, pid)
         if sink is not None:
             return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)

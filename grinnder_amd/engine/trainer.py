@@ -155,6 +155,7 @@ class Trainer(ProjectedLayers):
                 acts[i] = None
         self._graphs = {}
         self._rng = {}
+        self._gkept = {}
         self._scores = {}
 
     def train_epoch(self, optimizer: torch.optim.Optimizer,

@@ -74,3 +74,13 @@ class GriNNderModel(torch.nn.Module):
         with x the input rows of all partitions read in place through gidx
         (the global row of each CSR edge's source); x gets no gradient."""
         raise NotImplementedError(f"{type(self).__name__} has no in-place form of layer {layer}")
+
+    def forward_gathered(self, layer: int, x: Tensor, adj, reuse=None, keep=None) -> Tensor:
+        """forward_layer(layer, x, adj), for a partitioned trainer that
+        recomputes the layer in its backward.  A model may append to the list
+        `keep` one tensor the forward forms from x (detached; e.g. its first
+        product), and take that tensor back as `reuse` in the recompute, which
+        runs on the same rows with the same weights and dropout masks, instead
+        of forming it again; the result must not change.  The default keeps
+        nothing and ignores `reuse`."""
+        return self.forward_layer(layer, x, adj)

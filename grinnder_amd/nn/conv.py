@@ -118,9 +118,14 @@ class GATConv(Module):
         super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
 
     def forward(self, x: Union[Tensor, Tuple[Tensor, Tensor]], adj: Adjacency,
-                add_bias: bool = True) -> Tensor:
+                add_bias: bool = True, reuse: Optional[Tensor] = None,
+                keep: Optional[list] = None) -> Tensor:
         """add_bias=False leaves the bias out of the output, for a caller that
-        adds it in a fused epilogue (the LayerNorm of GAT.forward_layer)."""
+        adds it in a fused epilogue (the LayerNorm of GAT.forward_layer).
+        keep: a list that receives this call's projection hs of the source
+        rows (detached); reuse: such an hs from an earlier call on the same
+        rows and weights, taken instead of the projection product (the
+        backward is unchanged)."""
         bias = self.bias if add_bias else None
         num_dst = adj.sparse_sizes()[0]
         if isinstance(x, tuple):
@@ -142,10 +147,15 @@ class GATConv(Module):
             a_s = F.pad(self.att_src, (0, pad))
             a_d = F.pad(self.att_dst, (0, pad))
             b = F.pad(bias, (0, pad)) if bias is not None else None
-            hs = linear(x_src, w)
+            hs = linear(x_src, w, reuse=reuse)
+            if keep is not None:
+                keep.append(hs.detach())
             y = gat_attention(hs, adj, a_s, a_d, b, 1, self.out_channels + pad, self.concat)
             return y[:, :self.out_channels]
-        return self.attend(linear(x_src, self.lin.weight), adj, add_bias)
+        hs = linear(x_src, self.lin.weight, reuse=reuse)
+        if keep is not None:
+            keep.append(hs.detach())
+        return self.attend(hs, adj, add_bias)
 
     def _padded(self) -> int:
         """Zero columns added to one head of C channels, C not a multiple of 4."""

@@ -57,14 +57,20 @@ class GAT(GriNNderModel):
         return x
 
     def forward_layer(self, layer: int, x: Tensor, adj) -> Tensor:
+        return self.forward_gathered(layer, x, adj)
+
+    def forward_gathered(self, layer: int, x: Tensor, adj, reuse=None, keep=None) -> Tensor:
+        """forward_layer, with GATConv's projection of the (dropped-out) input
+        rows appended to `keep`, or taken from `reuse` instead of recomputed
+        (a recompute from the same rows, weights and dropout mask)."""
         x = F.dropout(x, p=self.dropout, training=self.training)
         num_dst = adj.sparse_sizes()[0]
         conv = self.convs[layer]
         if self._fused_norm(layer, x):
             norm = self.norms[layer]
-            x = conv((x, x[:num_dst]), adj, add_bias=False)
+            x = conv((x, x[:num_dst]), adj, add_bias=False, reuse=reuse, keep=keep)
             return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
-        return self._finish(layer, conv((x, x[:num_dst]), adj))
+        return self._finish(layer, conv((x, x[:num_dst]), adj, reuse=reuse, keep=keep))
 
     def input_projection(self, layer: int):
         """GATConv multiplies every source row by lin first; the dropout before

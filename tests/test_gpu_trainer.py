@@ -433,15 +433,33 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     assert all(torch.equal(g1[k], g2[k]) for k in g1)
 
 
-def test_gathered_layers_match_reference_flow_at_scale(gpu):
+@pytest.mark.parametrize("keep_products", [True, False])
+def test_gathered_layers_match_reference_flow_at_scale(gpu, keep_products, monkeypatch):
     """GAT with input dropout 0.6 on the 300k-node graph (8 partitions,
     widths 128 -> 256 -> 16, two heads in the first layer): every layer is
     gathered from HBM, against the reference flow from the same seed.  The
     two flows run the same kernels on the same rows with the same dropout
     masks, and add each input-gradient row in the same partition order, so
-    the loss and every gradient are bit-identical."""
+    the loss and every gradient are bit-identical, whether the recompute
+    takes each partition's projection product kept by its forward
+    (forward_gathered) or forms it again."""
     from grinnder_amd.data import synthetic
 
+    plan = Trainer._plan_projection
+    compute_losses = Trainer._compute_losses
+    kept_counts = []
+
+    def planned(self):
+        out = plan(self)
+        if not keep_products:
+            self._gkept_left = 0
+        return out
+
+    def losses(self):
+        kept_counts.append(len(self._gkept))
+        return compute_losses(self)
+    monkeypatch.setattr(Trainer, "_plan_projection", planned)
+    monkeypatch.setattr(Trainer, "_compute_losses", losses)
     n = 300_000
     ei = synthetic.uniform_graph(n, 3_000_000, seed=6)
     nd = synthetic.node_data(n, 128, 16, seed=6)
@@ -460,9 +478,12 @@ def test_gathered_layers_match_reference_flow_at_scale(gpu):
         metrics = trainer.train_epoch(torch.optim.SGD(model.parameters(), lr=0.0),
                                       torch.nn.CrossEntropyLoss())
         assert trainer.gathered_layers == ([] if proj == "off" else [0, 1, 2])
+        assert trainer._gkept == {}
         runs[proj] = (metrics["loss"], {k: p.grad.detach().clone()
                                         for k, p in model.named_parameters()})
         del trainer, model, graph
+    # Every layer of every partition kept its product for the recompute.
+    assert kept_counts == [0, 3 * 8 if keep_products else 0]
     (l0, g0), (l1, g1) = runs["off"], runs["auto"]
     assert l0 == l1
     for k in g0:
