@@ -102,7 +102,11 @@ class Trainer(ProjectedLayers):
             self._pid_start, self._pid_end = partition_range
         else:
             self._pid_start, self._pid_end = 0, graph.num_parts
-        self._my_pids = list(range(self._pid_start, self._pid_end))
+        # A partition with no nodes has no rows to gather, compute or
+        # scatter (nor halo rows: it has no edges), and adds nothing to the
+        # loss, its gradient or the metrics: the partition loops skip it.
+        self._my_pids = [p for p in range(self._pid_start, self._pid_end)
+                         if graph.partition_sizes[p] > 0]
 
         dims = model.layer_dims()
         if len(dims) != model.num_layers + 1:

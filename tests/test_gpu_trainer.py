@@ -733,6 +733,53 @@ def test_training_trajectory_matches_reference_flow(gpu, model_kind):
         assert err <= 1e-4, (k, err)
 
 
+@pytest.mark.parametrize("model_kind", ["gcn", "gat", "gat_dropout", "gcn_residual"])
+def test_empty_partitions_match_reference_flow(gpu, model_kind):
+    """A 12-node graph cut into 8 partitions, two of them empty: every flow
+    (projected and in place for GCN, projected GAT, gathered GAT with input
+    dropout, gathered residual GCN) gives the reference flow's loss,
+    gradients and evaluate() within the 1e-5 bound, in both modes."""
+    n = 12
+    src = torch.tensor([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 0, 3])
+    dst = torch.tensor([1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 5, 9])
+    ei = torch.stack([torch.cat([src, dst]), torch.cat([dst, src])])
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(n, 8, generator=g)
+    y = torch.randint(0, 3, (n,), generator=g)
+    tr = torch.zeros(n, dtype=torch.bool)
+    tr[::2] = True
+    va, te = ~tr, torch.zeros(n, dtype=torch.bool)
+    torch.manual_seed(13)
+    make = {
+        "gcn": lambda: GCN(8, 16, 3, num_layers=2, dropout=0.0, norm=True),
+        "gat": lambda: GAT(8, 4, 3, num_layers=2, heads=2, dropout=0.0, norm=True),
+        "gat_dropout": lambda: GAT(8, 4, 3, num_layers=2, heads=2, dropout=0.5, norm=True),
+        "gcn_residual": lambda: GCN(8, 8, 3, num_layers=3, dropout=0.0, norm=True,
+                                    residual=True),
+    }[model_kind]
+    state = make().state_dict()
+    for mode in ("grinnder", "hongtu"):
+        runs = {}
+        for proj in ("off", "auto"):
+            config = GriNNderConfig(num_parts=8, mode=mode, project_first=proj)
+            graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+            assert 0 in graph.partition_sizes
+            model = make().cuda()
+            model.load_state_dict(state)
+            trainer = Trainer(model, graph, config)
+            torch.manual_seed(21)
+            loss = trainer.train_epoch(torch.optim.SGD(model.parameters(), lr=0.0),
+                                       torch.nn.CrossEntropyLoss())["loss"]
+            grads = {k: p.grad.detach().clone() for k, p in model.named_parameters()}
+            runs[proj] = (loss, grads, trainer.evaluate(torch.nn.CrossEntropyLoss()))
+        (l0, g0, e0), (l1, g1, e1) = runs["off"], runs["auto"]
+        assert abs(l0 - l1) < 1e-5, (mode, l0, l1)
+        for k, err in grad_errs(g1, g0).items():
+            assert err <= 1e-5, (mode, k, err)
+        assert abs(e0["loss"] - e1["loss"]) < 1e-5
+        assert (e0["val_acc"], e0["test_acc"]) == (e1["val_acc"], e1["test_acc"])
+
+
 def _random_config(seed):
     import random
     r = random.Random(seed)
