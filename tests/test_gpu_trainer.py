@@ -155,7 +155,7 @@ def _vanilla(data, state, make_model):
             h = torch.relu(h)
     loss = torch.nn.functional.cross_entropy(h[tr], y[tr])
     loss.backward()
-    return float(loss), {k: p.grad for k, p in model.named_parameters()}
+    return float(loss.detach()), {k: p.grad for k, p in model.named_parameters()}
 
 
 @pytest.mark.parametrize("norm", [False, True])
@@ -198,7 +198,7 @@ def _vanilla_gat(data, state, make_model):
             h = torch.nn.functional.elu(h)
     loss = torch.nn.functional.cross_entropy(h[tr], y[tr])
     loss.backward()
-    return float(loss), {k: p.grad for k, p in model.named_parameters()}
+    return float(loss.detach()), {k: p.grad for k, p in model.named_parameters()}
 
 
 @pytest.mark.parametrize("heads,hidden,classes", [(1, 8, 4), (2, 8, 4), (1, 6, 3)])
