@@ -80,6 +80,9 @@ class ProjectedLayers:
         # Per-row quantities of each projected layer's Z formed once for all
         # partitions this epoch (GAT's attention scores), by layer.
         self._scores: Dict[int, tuple] = {}
+        # W padded with zero rows to Z's width, per projected layer whose Z is
+        # wider than W's rows (formed once per epoch: W changes between).
+        self._wpad: Dict[int, Tensor] = {}
         # HBM buffers of dL/dx for the gathered layers above layer 0 (layers
         # in self._xin that run neither projected nor in place), by layer.
         self._gxbufs: Dict[int, Tensor] = {}
@@ -169,6 +172,7 @@ class ProjectedLayers:
         self._xin = set()
         self._keep = set()
         self._out_room = False
+        self._wpad = {}
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
             self._x0double = False
@@ -186,7 +190,7 @@ class ProjectedLayers:
             if layer not in self._zbufs:
                 if free is None:
                     free = self._free_device_memory()
-                need = 4 * (2 * n * w.size(0) + 2 * maxb * w.size(1))
+                need = 4 * (2 * n * self.model.projected_width(layer) + 2 * maxb * w.size(1))
                 if need + (8 << 30) > free:
                     continue
                 free -= need
@@ -320,10 +324,12 @@ class ProjectedLayers:
         return gx
 
     def _zbuf(self, layer: int) -> Tensor:
+        """Z of a projected layer, [N, model.projected_width(layer)]: the
+        columns past W's rows (zero padding the model reads) stay zero."""
         z = self._zbufs.get(layer)
         if z is None:
             with torch.cuda.stream(self.streams.compute):
-                z = torch.empty(int(self.graph.ptr[-1]), self._proj[layer].size(0),
+                z = torch.empty(int(self.graph.ptr[-1]), self.model.projected_width(layer),
                                 device=self.device)
             self._zbufs[layer] = z
         return z
@@ -463,10 +469,19 @@ class ProjectedLayers:
             return self._device_call(layer, pid, grad=True)
 
     def _project_rows(self, layer: int, x: Tensor, lo: int, hi: int) -> None:
-        """Z_layer[lo:hi] = x Wᵀ (no autograd)."""
-        w = self._proj[layer]
+        """Z_layer[lo:hi] = x Wᵀ (no autograd); with Z wider than W's rows,
+        through W padded with zero rows, which writes the pad columns' zeros."""
+        z = self._zbuf(layer)
+        w = self._proj[layer].detach()
+        if z.size(1) != w.size(0):
+            wp = self._wpad.get(layer)
+            if wp is None:
+                with torch.no_grad():
+                    wp = torch.nn.functional.pad(w, (0, 0, 0, z.size(1) - w.size(0)))
+                self._wpad[layer] = wp
+            w = wp
         with torch.no_grad(), dense_region("fwd", hi - lo, w.size(1), w.size(0)):
-            torch.mm(x.detach(), w.detach().t(), out=self._zbuf(layer)[lo:hi])
+            torch.mm(x.detach(), w.t(), out=z[lo:hi])
 
     def _each_input_partition(self, layer: int, fn) -> None:
         """fn(pid, x_p, lo, hi) on the compute stream for every partition,
@@ -595,7 +610,7 @@ class ProjectedLayers:
             return self._gxbufs[layer][lo:hi]
         w = self._proj[layer]
         with dense_region("dx", hi - lo, w.size(0), w.size(1)):
-            return torch.mm(self._dzbufs[layer][lo:hi], w.detach())
+            return torch.mm(self._dzbufs[layer][lo:hi, :w.size(0)], w.detach())
 
     def _backward_device(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
         """Backward of a projected layer: per partition, take the forward's
@@ -667,7 +682,7 @@ class ProjectedLayers:
 
         def accumulate(pid, xp, lo, hi):
             with dense_region("dw", hi - lo, w.size(0), w.size(1)):
-                gemm_tn(dz[lo:hi], xp, out=dw, beta=1.0)
+                gemm_tn(dz[lo:hi, :w.size(0)], xp, out=dw, beta=1.0)
 
         if layer in self._xin:
             x = self._xres[layer]

@@ -52,6 +52,13 @@ class GriNNderModel(torch.nn.Module):
         the sink's dZ."""
         raise NotImplementedError(f"{type(self).__name__} has no projected form of layer {layer}")
 
+    def projected_width(self, layer: int) -> int:
+        """Columns of the projected matrix Z that forward_projected(layer, ...)
+        reads: the rows of input_projection(layer)'s W (the default), or more
+        when the model reads Z zero-padded (the trainer then keeps the columns
+        past W's rows at zero)."""
+        return self.input_projection(layer).size(0)
+
     def projected_sink_ok(self, layer: int) -> bool:
         """Whether forward_projected(layer, ...) accepts a sink."""
         return False

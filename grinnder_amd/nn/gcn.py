@@ -63,7 +63,17 @@ class GCN(GriNNderModel):
             return None
         return conv.lin.weight
 
+    def projected_width(self, layer: int) -> int:
+        """Z rounded up to a multiple of 4 columns (16-byte rows; the pad
+        columns are zero), so that gathered rows of Z need no padding copy."""
+        d = self.convs[layer].out_channels
+        return d + (-d) % 4
+
     def projected_sink_ok(self, layer: int) -> bool:
+        """Z read in place for widths that are multiples of 4.  A narrower,
+        padded layer gathers its rows: at C3 the 48-wide Z (470 MB) read in
+        place over the whole graph cost more than gathering each partition's
+        rows into a compact copy that stays in the caches."""
         return self.convs[layer].out_channels % 4 == 0
 
     def inplace_ok(self, layer: int) -> bool:
@@ -93,9 +103,18 @@ class GCN(GriNNderModel):
     def forward_projected(self, layer: int, z: Tensor, adj, sink=None) -> Tensor:
         conv = self.convs[layer]
         d = conv.out_channels
-        if sink is not None and d % 4 != 0:
+        w = z.size(1)
+        if w != d:
+            # Z zero-padded to w columns (projected_width): aggregate all of
+            # them (16-byte rows) with the bias padded alike; the pad columns
+            # of the output are zero and are dropped.
+            if w < d or w % 4 != 0:
+                raise ValueError(f"layer {layer}: Z has {w} columns for a width of {d}")
+            b = F.pad(conv.bias, (0, w - d)) if conv.bias is not None else None
+            h = gcn_aggregate(z, adj, b, sink=sink)[:, :d]
+        elif sink is not None and d % 4 != 0:
             raise ValueError(f"layer {layer}: a sink needs an output width divisible by 4")
-        if d % 4 != 0:
+        elif d % 4 != 0:
             # Widths that are not a multiple of 4 aggregate zero-padded rows
             # (16-byte vectors), as GCNConv does; the pad column stays zero.
             pad = (-d) % 4
