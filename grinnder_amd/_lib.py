@@ -45,6 +45,7 @@ _SIGNATURES = {
                          _i64, _P],
     "gr_gcn_aggregate_into": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _i64, _i64, _i64,
                               _P, _i64, _P],
+    "gr_gather_rows": [_P, _i64, _i64, _P, _i64, _i64, _P, _i64, _P],
     "gr_scatter_add_rows": [_P, _i64, _i64, _i64, _P, _P, _i64, _i64, _P],
     "gr_column_sum": [_P, _i64, _i64, _i64, _P, _i64, _i64, _P, _P, _i64, _P],
     "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,

@@ -109,6 +109,24 @@ def column_sum(g: Tensor, weights: Optional[Tensor] = None, group: int = 1) -> T
     return out
 
 
+def gather_rows(x: Tensor, rows: Tensor) -> Tensor:
+    """x[rows] for fp32 [*, D] device rows x and int64 device row ids (HIP
+    kernel, flat over elements, so narrow rows run near copy speed too);
+    the same values as x.index_select(0, rows)."""
+    if x.dim() != 2 or rows.dim() != 1:
+        raise ValueError("gather_rows: x [*, D], rows [n]")
+    if x.dtype != torch.float32 or rows.dtype != torch.int64:
+        raise ValueError("gather_rows: fp32 x, int64 rows")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    rows = rows.contiguous()
+    n, dim = rows.numel(), x.size(1)
+    y = torch.empty(n, dim, dtype=torch.float32, device=x.device)
+    _lib.call("gr_gather_rows", x.data_ptr(), x.size(0), max(x.stride(0), dim),
+              rows.data_ptr(), n, dim, y.data_ptr(), dim, _lib.stream_handle())
+    return y
+
+
 def scatter_add_rows(x: Tensor, rows: Tensor, y: Tensor) -> None:
     """y[rows[r]] += x[r] in place on the current stream (HIP kernel, no
     atomics): fp32 [n, D] rows into fp32 [*, D] y, rows int64 on the device

@@ -727,6 +727,54 @@ __global__ __launch_bounds__(256) void scatter_add_rows(const V* __restrict__ x,
   }
 }
 
+// y[r][j] = x[rows[r]][j] over n rows of dv V-wide elements; a row id
+// outside [0, x_rows) yields a zero row.  Flat over elements, as
+// scatter_add_rows, so narrow rows still keep every lane busy.
+template <typename V, typename I>
+__global__ __launch_bounds__(256) void gather_rows(const V* __restrict__ x, I ldx,
+                                                  const int64_t* __restrict__ rows,
+                                                  int64_t x_rows, I n, I dv,
+                                                  V* __restrict__ y, I ldy) {
+  const I total = n * dv;
+  const I stride = (I)gridDim.x * 256;
+  for (I base = (I)blockIdx.x * 256 + (I)threadIdx.x; base < total; base += 4 * stride) {
+    V v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const I i = base + u * stride;
+      if (i < total) {
+        const I r = i / dv;
+        const I j = i - r * dv;
+        const int64_t t = rows[r];
+        if (t >= 0 && t < x_rows)
+          v[u] = x[(I)t * ldx + j];
+        else
+          v[u] = V{};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const I i = base + u * stride;
+      if (i < total) {
+        const I r = i / dv;
+        y[r * ldy + (i - r * dv)] = v[u];
+      }
+    }
+  }
+}
+
+template <typename V, typename I>
+void launch_gather_rows(const float* x, int64_t ldx, const int64_t* rows, int64_t x_rows,
+                        int64_t n, int64_t dim, float* y, int64_t ldy, hipStream_t s) {
+  constexpr int W = sizeof(V) / sizeof(float);
+  const int64_t total = n * (dim / W);
+  const int64_t want = (total + 1023) / 1024;
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 1 << 20));
+  hipLaunchKernelGGL((gather_rows<V, I>), dim3(grid), dim3(256), 0, s,
+                     reinterpret_cast<const V*>(x), (I)(ldx / W), rows, x_rows, (I)n,
+                     (I)(dim / W), reinterpret_cast<V*>(y), (I)(ldy / W));
+}
+
 template <typename V, typename I>
 void launch_scatter_add_rows(const float* x, int64_t n, int64_t dim, int64_t ldx,
                              const int64_t* rows, float* y, int64_t ldy, int64_t y_rows,
@@ -823,6 +871,32 @@ int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t
                        dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias, orow);
     GR_HIP_CHECK(hipGetLastError());
   }
+  return GR_OK;
+}
+
+extern "C" int gr_gather_rows(const float* x, int64_t x_rows, int64_t ldx,
+                              const int64_t* rows, int64_t n, int64_t dim, float* y,
+                              int64_t ldy, void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(n >= 0 && dim >= 1 && ldx >= dim && ldy >= dim && x_rows >= 0,
+             "gather_rows: bad shape");
+  if (n == 0) return GR_OK;
+  GR_REQUIRE(rows != nullptr && y != nullptr && (x != nullptr || x_rows == 0),
+             "gather_rows: NULL pointer");
+  hipStream_t s = gr::as_stream(stream);
+  const bool vec = dim % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && gr_agg::aligned(x, 16) &&
+                   gr_agg::aligned(y, 16);
+  // 32-bit element indices when every offset fits (see gr_scatter_add_rows).
+  const bool narrow = n * ldy < (int64_t(1) << 30) && x_rows * ldx < (int64_t(1) << 31);
+  if (vec && narrow)
+    gr_agg::launch_gather_rows<float4, int32_t>(x, ldx, rows, x_rows, n, dim, y, ldy, s);
+  else if (vec)
+    gr_agg::launch_gather_rows<float4, int64_t>(x, ldx, rows, x_rows, n, dim, y, ldy, s);
+  else if (narrow)
+    gr_agg::launch_gather_rows<float, int32_t>(x, ldx, rows, x_rows, n, dim, y, ldy, s);
+  else
+    gr_agg::launch_gather_rows<float, int64_t>(x, ldx, rows, x_rows, n, dim, y, ldy, s);
+  GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
 

@@ -17,7 +17,8 @@ from typing import Dict, List, Optional, Set
 import torch
 from torch import Tensor
 
-from grinnder_amd.aggregation import KernelTimer, ProjectedSink, dense_region, scatter_add_rows
+from grinnder_amd.aggregation import (KernelTimer, ProjectedSink, dense_region, gather_rows,
+                                     scatter_add_rows)
 from grinnder_amd.dense import gemm_tn
 from grinnder_amd.loss import masked_cross_entropy
 
@@ -32,7 +33,7 @@ class _GatherRows(torch.autograd.Function):
     @staticmethod
     def forward(ctx, token: Tensor, z: Tensor, rows: Tensor, dz: Tensor) -> Tensor:
         ctx.rows, ctx.dz = rows, dz
-        return z.index_select(0, rows)
+        return gather_rows(z, rows)
 
     @staticmethod
     def backward(ctx, grad: Tensor):
@@ -373,7 +374,7 @@ class ProjectedLayers:
         d = z.size(1)
         with KernelTimer.region(name, 2 * 4 * rows.numel() * d, 0, d):
             if dz is None:
-                return z.index_select(0, rows)
+                return gather_rows(z, rows)
             if self._token is None:
                 self._token = torch.zeros(0, device=self.device, requires_grad=True)
             return _GatherRows.apply(self._token, z, rows, dz)
@@ -436,7 +437,7 @@ class ProjectedLayers:
         if sc is None:
             return self.model.forward_projected(layer, z, adj)
         lo, hi = self.graph._range(pid)
-        s_rows = sc[0].index_select(0, self._global_rows(pid))
+        s_rows = gather_rows(sc[0], self._global_rows(pid))
         return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]))
 
     def _device_forward(self, layer: int, pid: int, keep: bool) -> Tensor:

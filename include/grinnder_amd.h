@@ -228,6 +228,16 @@ int gr_gcn_aggregate_into(const int32_t* units, int64_t n_units,
                           int64_t ldy, int64_t rows, int64_t dim,
                           float* workspace, int64_t n_slots, void* stream);
 
+/* No counterpart in the reference: the row gather from an HBM-resident
+ * matrix that the trainer's projected and gathered layers do on the device
+ * where the reference gathers halo rows from host buffers
+ * (gather_partitions, csrc/cuda/async_transfer.cu:60-120):
+ *   y[r][j] = x[rows[r]][j]   for r < n, j < dim,
+ * x [x_rows, dim] with row stride ldx, y [n, dim] with row stride ldy, rows
+ * device int64; a row id outside [0, x_rows) gives a zero row. */
+int gr_gather_rows(const float* x, int64_t x_rows, int64_t ldx, const int64_t* rows,
+                   int64_t n, int64_t dim, float* y, int64_t ldy, void* stream);
+
 /* No counterpart in the reference: the backward of a row gather from an
  * HBM-resident matrix (the trainer's projected and gathered layers, which
  * take a partition's rows on the device where the reference gathers them

@@ -186,6 +186,29 @@ def test_scatter_add_rows_equals_index_add(gpu, dim, ldx, ldy):
     assert torch.equal(got, expect)
 
 
+@pytest.mark.parametrize("dim,ldx", [(1, 1), (3, 5), (19, 19), (20, 24), (48, 48), (256, 260),
+                                     (1024, 1024)])
+def test_gather_rows_equals_index_select(gpu, dim, ldx):
+    """gr_gather_rows (the trainer's device row gathers) against torch's
+    index_select, bit for bit: 16-byte and scalar accesses, strided x,
+    repeated ids, and ids outside x giving zero rows."""
+    from grinnder_amd.aggregation import gather_rows
+    g = torch.Generator().manual_seed(dim)
+    x_rows, n = 4000, 6000
+    xs = torch.randn(x_rows, ldx, generator=g)[:, :dim].cuda()
+    rows = torch.randint(0, x_rows, (n,), generator=g)
+    got = gather_rows(xs, rows.cuda())
+    assert torch.equal(got, xs.index_select(0, rows.cuda()))
+    bad = rows.clone()
+    bad[::5] = -3
+    bad[2::5] = x_rows
+    got = gather_rows(xs, bad.cuda())
+    keep = ((bad >= 0) & (bad < x_rows)).cuda()
+    assert torch.equal(got[keep], xs.index_select(0, bad.cuda()[keep]))
+    assert bool((got[~keep] == 0).all())
+    assert gather_rows(xs, rows[:0].cuda()).shape == (0, dim)
+
+
 def test_scatter_add_rows_64bit_offsets(gpu):
     """The 64-bit index path, which x of 2^30 elements (4 GiB) takes: every
     chosen row of y gets its ones, the others stay zero."""
@@ -199,7 +222,13 @@ def test_scatter_add_rows_64bit_offsets(gpu):
     hit = torch.zeros(y_rows, dtype=torch.bool, device="cuda")
     hit[rows] = True
     assert bool((y[hit] == 1).all()) and bool((y[~hit] == 0).all())
-    del x, y
+    # And back through the gather's 64-bit path (n * dim = 2^30 elements).
+    from grinnder_amd.aggregation import gather_rows
+    del x
+    y[rows[::2]] = 2.0
+    back = gather_rows(y, rows)
+    assert bool((back[::2] == 2).all()) and bool((back[1::2] == 1).all())
+    del y, back
 
 
 @pytest.mark.parametrize("dim", [3, 47, 64, 256, 300, 1024])
