@@ -35,8 +35,8 @@ def random_bipartite(num_dst: int, num_src: int, avg_deg: float, seed: int,
 
 def max_abs_norm_err(got, ref) -> float:
     """max|got - ref| / max|ref| (the north-star tolerance metric)."""
-    got = torch.as_tensor(got, dtype=torch.float64).cpu()
-    ref = torch.as_tensor(ref, dtype=torch.float64).cpu()
+    got = torch.as_tensor(got, dtype=torch.float64).detach().cpu()
+    ref = torch.as_tensor(ref, dtype=torch.float64).detach().cpu()
     if ref.numel() == 0:
         return 0.0
     scale = float(ref.abs().max())
