@@ -50,8 +50,19 @@ class KernelTimer:
 
     active: Optional["KernelTimer"] = None
 
-    def __init__(self):
+    def __init__(self, capacity: int = 0):
+        """capacity: events to create (and record once) up front, so that
+        regions timed later take ready events instead of creating them; a
+        timed epoch of many short kernels otherwise pays for event creation
+        on the host between its launches."""
         self.records: List[KernelRecord] = []
+        self._pool: List["torch.cuda.Event"] = []
+        for _ in range(capacity):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self._pool.append(ev)
+        if capacity:
+            torch.cuda.synchronize()
 
     def __enter__(self):
         KernelTimer.active = self
@@ -61,6 +72,9 @@ class KernelTimer:
         KernelTimer.active = None
         return False
 
+    def _event(self) -> "torch.cuda.Event":
+        return self._pool.pop() if self._pool else torch.cuda.Event(enable_timing=True)
+
     @staticmethod
     @contextlib.contextmanager
     def region(name: str, nbytes: int, edges: int, dim: int, flops: int = 0):
@@ -68,8 +82,8 @@ class KernelTimer:
         if timer is None:
             yield
             return
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        start = timer._event()
+        end = timer._event()
         start.record()
         yield
         end.record()
