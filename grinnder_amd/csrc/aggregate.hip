@@ -652,6 +652,45 @@ __global__ __launch_bounds__(256) void colsum_final(const float* __restrict__ pa
   }
 }
 
+// colsum_final over up to three partial matrices of the same shape, laid out
+// one after the other (part + y * nblk * dim for y = blockIdx.y), into out0,
+// out1, out2: one launch for the LayerNorm backward's dgamma, dbeta and dbias,
+// with the same sums in the same order as three colsum_final launches.
+__global__ __launch_bounds__(256) void colsum_final3(const float* __restrict__ part, int nblk,
+                                                     int dim, float* __restrict__ out0,
+                                                     float* __restrict__ out1,
+                                                     float* __restrict__ out2) {
+  __shared__ float red[kFinalGroups][kFinalCols + 1];
+  const int y = blockIdx.y;
+  const float* __restrict__ p = part + (int64_t)y * nblk * dim;
+  float* __restrict__ out = y == 0 ? out0 : (y == 1 ? out1 : out2);
+  const int cl = threadIdx.x % kFinalCols;
+  const int grp = threadIdx.x / kFinalCols;
+  const int f = blockIdx.x * kFinalCols + cl;
+  float s = 0.f;
+  if (f < dim) {
+    int b = grp;
+    for (; b + 3 * kFinalGroups < nblk; b += 4 * kFinalGroups) {
+      const float a0 = p[(int64_t)b * dim + f];
+      const float a1 = p[(int64_t)(b + kFinalGroups) * dim + f];
+      const float a2 = p[(int64_t)(b + 2 * kFinalGroups) * dim + f];
+      const float a3 = p[(int64_t)(b + 3 * kFinalGroups) * dim + f];
+      s += a0;
+      s += a1;
+      s += a2;
+      s += a3;
+    }
+    for (; b < nblk; b += kFinalGroups) s += p[(int64_t)b * dim + f];
+  }
+  red[grp][cl] = s;
+  __syncthreads();
+  if (grp == 0 && f < dim) {
+    float t = 0.f;
+    for (int g = 0; g < kFinalGroups; ++g) t += red[g][cl];
+    out[f] = t;
+  }
+}
+
 inline unsigned final_blocks(int64_t dim) {
   return (unsigned)((dim + kFinalCols - 1) / kFinalCols);
 }
@@ -1089,14 +1128,11 @@ extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* m
   }
 #undef GR_LNB
   GR_HIP_CHECK(hipGetLastError());
-  // dgamma / dbeta = column sums of the partials, in wavefront order.
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(d)), dim3(256), 0, s, pg,
-                     (int)nwaves, d, dgamma);
-  hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(d)), dim3(256), 0, s, pb,
-                     (int)nwaves, d, dbeta);
-  if (dbias != nullptr)
-    hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(d)), dim3(256), 0, s,
-                       ph, (int)nwaves, d, dbias);
+  // dgamma / dbeta (/ dbias) = column sums of the partials, in wavefront
+  // order: the partial matrices follow one another in the workspace, and
+  // one launch reduces all of them.
+  hipLaunchKernelGGL(gr_agg::colsum_final3, dim3(gr_agg::final_blocks(d), (unsigned)nparts),
+                     dim3(256), 0, s, pg, (int)nwaves, d, dgamma, dbeta, dbias);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
