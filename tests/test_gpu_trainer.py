@@ -698,6 +698,57 @@ def test_gathered_layers_match_reference_flow(gpu, heads, pool_size, resident, m
     assert e0["val_acc"] == e1["val_acc"]
 
 
+@pytest.mark.parametrize("budget_parts", [0, 1, 3])
+def test_gathered_partial_keep_budget_is_exact(gpu, budget_parts, monkeypatch):
+    """When HBM holds the forward's projection products of only some
+    partitions (a budget of 0, 1 or 3 partitions' worth), those recompute
+    from the kept product and the others form it again: the loss and the
+    gradients are bit-identical to keeping every partition's product."""
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    ei, x, y, tr, va, te = data
+    torch.manual_seed(19)
+    make = lambda: GAT(24, 8, 4, num_layers=2, heads=2, dropout=0.6, norm=True)  # noqa
+    state = make().state_dict()
+    plan = Trainer._plan_projection
+    compute_losses = Trainer._compute_losses
+    budget = {"bytes": None}
+    kept = []
+
+    def planned(self):
+        out = plan(self)
+        if budget["bytes"] is not None:
+            self._gkept_left = budget["bytes"]
+        return out
+
+    def losses(self):
+        kept.append(len(self._gkept))
+        return compute_losses(self)
+    monkeypatch.setattr(Trainer, "_plan_projection", planned)
+    monkeypatch.setattr(Trainer, "_compute_losses", losses)
+    runs = []
+    for limited in (False, True):
+        config = GriNNderConfig(num_parts=4)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        if limited:
+            # Layer 0's products of `budget_parts` average partitions.
+            per_part = sum(graph.expanded_sizes) // graph.num_parts * 16 * 4
+            budget["bytes"] = budget_parts * per_part
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        torch.manual_seed(33)
+        loss = trainer.train_epoch(torch.optim.SGD(model.parameters(), lr=0.0),
+                                   torch.nn.CrossEntropyLoss())["loss"]
+        assert trainer.gathered_layers == [0, 1]
+        runs.append((loss, {k: p.grad.detach().clone() for k, p in model.named_parameters()}))
+    (l0, g0), (l1, g1) = runs
+    # Two layers of four partitions: all eight kept without a limit, fewer
+    # with one (none for a zero budget).
+    assert kept[0] == 8 and (kept[1] == 0 if budget_parts == 0 else 0 < kept[1] < 8)
+    assert l0 == l1
+    assert all(torch.equal(g0[k], g1[k]) for k in g0)
+
+
 @pytest.mark.parametrize("model_kind", ["gcn_widening", "gcn_narrowing"])
 def test_training_trajectory_matches_reference_flow(gpu, model_kind):
     """Three Adam epochs (weight decay, dropout 0.5 on layer outputs) from the
