@@ -13,6 +13,8 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must be loaded first: provides the HIP runtime)
 
+from grinnder_amd.build import source_hash
+
 LIB_PATH = Path(__file__).resolve().parent / "libgrinnder_amd.so"
 
 _c_void_p = ctypes.c_void_p
@@ -73,7 +75,7 @@ _SIGNATURES = {
     "gr_gaussian_rows": [_u64, _P, _i64, _i64, _P, _i32],
 }
 
-EXPORTED = tuple(_SIGNATURES) + ("gr_last_error", "gr_abi_version")
+EXPORTED = tuple(_SIGNATURES) + ("gr_last_error", "gr_abi_version", "gr_source_hash")
 
 _lock = threading.Lock()
 _lib = None
@@ -105,6 +107,15 @@ def load():
         lib.gr_last_error.restype = ctypes.c_char_p
         lib.gr_abi_version.argtypes = []
         lib.gr_abi_version.restype = ctypes.c_int
+        lib.gr_source_hash.argtypes = []
+        lib.gr_source_hash.restype = ctypes.c_char_p
+        built = lib.gr_source_hash().decode()
+        current = source_hash()
+        if built != current:
+            raise ImportError(
+                f"{LIB_PATH} was built from other sources (hash {built[:12]}, the sources "
+                f"here hash to {current[:12]}); rebuild it with `python -m grinnder_amd.build` "
+                "in a fresh process")
         _lib = lib
     return _lib
 

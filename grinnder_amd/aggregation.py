@@ -131,7 +131,9 @@ def gather_rows(x: Tensor, rows: Tensor) -> Tensor:
         raise ValueError("gather_rows: x [*, D], rows [n]")
     if x.dtype != torch.float32 or rows.dtype != torch.int64:
         raise ValueError("gather_rows: fp32 x, int64 rows")
-    if x.stride(-1) != 1:
+    if x.stride(-1) != 1 or (x.size(0) > 1 and x.stride(0) < x.size(1)):
+        # Rows that overlap (a broadcast or expanded view) are made dense:
+        # the kernel reads row r at r * stride(0).
         x = x.contiguous()
     rows = rows.contiguous()
     n, dim = rows.numel(), x.size(1)
@@ -150,10 +152,10 @@ def scatter_add_rows(x: Tensor, rows: Tensor, y: Tensor) -> None:
         raise ValueError("scatter_add_rows: x [n, D], rows [n], y [*, D]")
     if x.dtype != torch.float32 or y.dtype != torch.float32 or rows.dtype != torch.int64:
         raise ValueError("scatter_add_rows: fp32 x and y, int64 rows")
-    if x.stride(-1) != 1:
+    if x.stride(-1) != 1 or (x.size(0) > 1 and x.stride(0) < x.size(1)):
         x = x.contiguous()
-    if y.stride(-1) != 1:
-        raise ValueError("scatter_add_rows: y rows must be contiguous")
+    if y.stride(-1) != 1 or (y.size(0) > 1 and y.stride(0) < y.size(1)):
+        raise ValueError("scatter_add_rows: y must hold distinct, contiguous rows")
     rows = rows.contiguous()
     n, dim = x.shape
     _lib.call("gr_scatter_add_rows", x.data_ptr(), n, dim, max(x.stride(0), dim),

@@ -8,6 +8,7 @@ process which imports torch holds exactly one HIP runtime.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -35,6 +36,19 @@ SOURCES = [
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+def source_hash() -> str:
+    """Hex SHA-256 over the library's sources (csrc/*, the public header), the
+    target architecture and the device flags.  Embedded in the library as
+    gr_source_hash(); the loader compares the two."""
+    h = hashlib.sha256()
+    files = sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp", ".h"))
+    files.append(PKG_DIR.parent / "include" / "grinnder_amd.h")
+    for p in files:
+        h.update(p.name.encode() + b"\0" + p.read_bytes() + b"\0")
+    h.update(ARCH.encode() + b"\0" + " ".join(DEVICE_FLAGS).encode())
+    return h.hexdigest()
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -48,9 +62,10 @@ def _torch_lib_dir() -> Path:
     return Path(torch.__file__).resolve().parent / "lib"
 
 
-def _compile(src: Path, obj: Path) -> None:
+def _compile(src: Path, obj: Path, digest: str) -> None:
     cmd = [_hipcc(), "-std=c++17", "-O3", "-fPIC", "-Wall", "-Wno-unused-result",
-           f"-I{PKG_DIR.parent / 'include'}", "-c", str(src), "-o", str(obj)]
+           f"-I{PKG_DIR.parent / 'include'}", f'-DGR_SOURCE_HASH="{digest}"', "-c", str(src),
+           "-o", str(obj)]
     if src.suffix == ".hip":
         cmd[1:1] = ["-x", "hip", f"--offload-arch={ARCH}", *DEVICE_FLAGS]
     else:
@@ -63,6 +78,7 @@ def _compile(src: Path, obj: Path) -> None:
 def build(verbose: bool = True) -> Path:
     """Compiles every source and links the shared library; returns its path."""
     BUILD_DIR.mkdir(exist_ok=True)
+    digest = source_hash()
     objs = []
     jobs = []
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
@@ -70,7 +86,7 @@ def build(verbose: bool = True) -> Path:
             src = CSRC / name
             obj = BUILD_DIR / (name + ".o")
             objs.append(obj)
-            jobs.append(ex.submit(_compile, src, obj))
+            jobs.append(ex.submit(_compile, src, obj, digest))
         for j in jobs:
             j.result()
     torch_lib = _torch_lib_dir()

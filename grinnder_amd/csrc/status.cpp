@@ -24,3 +24,9 @@ const char* last_error_cstr() { return g_last_error.c_str(); }
 extern "C" const char* gr_last_error(void) { return gr::last_error_cstr(); }
 
 extern "C" int gr_abi_version(void) { return 100; }
+
+#ifndef GR_SOURCE_HASH
+#error "GR_SOURCE_HASH must be defined by the build (grinnder_amd/build.py)"
+#endif
+
+extern "C" const char* gr_source_hash(void) { return GR_SOURCE_HASH; }

@@ -218,31 +218,51 @@ class Trainer(ProjectedLayers):
             out = self.model.forward_layer(l, out, adj)
         return out
 
-    def _fast_metrics(self, out: Tensor):
+    def _fast_loss(self, out: Tensor):
+        """(loss, stats) of the resident logits; no host synchronisation."""
         g = self.graph
-        y = self._res("y", lambda: g.partition_labels(0).to(self.device))
+
+        def labels():
+            y = g.partition_labels(0)
+            train = g.partition_train_mask(0)
+            sel = train | g.partition_val_mask(0) | g.partition_test_mask(0)
+            # The labels stay resident, so an out-of-range label among the
+            # selected rows is reported once here, before any step is taken,
+            # instead of by a host read of the statistics every epoch.
+            bad = int((sel & ((y < 0) | (y >= out.size(1)))).sum())
+            check_stats([0, 0, 0, 0, 0, bad])
+            return y.to(self.device)
+
+        y = self._res("y", labels)
         train = self._res("train", lambda: g.partition_train_mask(0).to(self.device))
         codes = self._res("codes", lambda: mask_codes(
             train, g.partition_val_mask(0), g.partition_test_mask(0)))
-        loss, stats = masked_cross_entropy(out, y, codes, "mean")
+        return masked_cross_entropy(out, y, codes, "mean")
+
+    @staticmethod
+    def _fast_metrics_from(loss: Tensor, stats: Tensor) -> Dict[str, float]:
         st = stats.tolist()
         check_stats(st)
         n_train = st[0]
-        metrics = {
-            "loss": float(loss) if n_train > 0 else 0.0,
+        return {
+            "loss": float(loss.detach()) if n_train > 0 else 0.0,
             "val_acc": st[1] / st[2] if st[2] else 0.0,
             "test_acc": st[3] / st[4] if st[4] else 0.0,
             "_n_train": n_train,
         }
-        return loss, metrics
+
+    def _fast_metrics(self, out: Tensor):
+        loss, stats = self._fast_loss(out)
+        return loss, self._fast_metrics_from(loss, stats)
 
     def _train_fast(self, optimizer) -> Dict[str, float]:
         optimizer.zero_grad()
         out = self._fast_logits()
-        loss, metrics = self._fast_metrics(out)
+        loss, stats = self._fast_loss(out)
         loss.backward()
         optimizer.step()
-        return metrics
+        # The statistics are read once the whole step is queued.
+        return self._fast_metrics_from(loss, stats)
 
     # ------------------------------------------------- partitioned helpers
 

@@ -55,6 +55,11 @@ const char* gr_last_error(void);
 /* ABI version of this library (major * 100 + minor). */
 int gr_abi_version(void);
 
+/* Hex SHA-256 of the sources and device flags this library was built from
+ * (build identity, no reference counterpart): a loader compares it with the
+ * sources beside it and refuses a stale binary. */
+const char* gr_source_hash(void);
+
 /* ------------------------------------------------------------------------ */
 /* Host <-> device transfers (grinnder._C transfer ops)                      */
 /* ------------------------------------------------------------------------ */

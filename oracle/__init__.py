@@ -70,6 +70,7 @@ def lib():
         i32 = ctypes.c_int32
         L.orc_spmm_csr.argtypes = [i64, P, P, P, P, i64, i64, P, P]
         L.orc_spmm_csr_t.argtypes = [i64, i64, P, P, P, P, i64, P]
+        L.orc_spmm_rows.argtypes = [i64, P, P, P, P, P, i64, i64, P, P]
         L.orc_gat_forward.argtypes = [i64, i64, P, P, P, i64, i64, P, P, P, i32, P, P, P]
         L.orc_gat_backward.argtypes = [i64, i64, P, P, P, i64, i64, P, P, i32, P, P, P, P, P,
                                        P, P]
@@ -206,6 +207,38 @@ def spmm(rowptr: Tensor, col: Tensor, val: Optional[Tensor], x: Tensor,
     out = np.zeros((rows, xx.shape[1]), dtype=np.float64)
     lib().orc_spmm_csr(rows, _p(rp), _p(cl), _p(v), _p(xx), xx.shape[1], xx.shape[1], _p(b),
                        _p(out))
+    return out
+
+
+def spmm_rows(rowptr: Tensor, col: Tensor, val: Optional[Tensor], x: Tensor, rows: Tensor,
+              bias: Optional[Tensor] = None, threads: int = 16) -> np.ndarray:
+    """Rows `rows` of A X (+ bias), float64 accumulation (oracle.c
+    orc_spmm_rows), split over `threads` host threads (ctypes releases the
+    GIL).  The inputs are converted once, so X may be a full-size matrix."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    rp, cl = _np(rowptr, np.int64), _np(col, np.int64)
+    v = None if val is None else _np(val, np.float32)
+    xx = _np(x, np.float32)
+    b = None if bias is None else _np(bias, np.float32)
+    sel = _np(rows, np.int64)
+    dim = xx.shape[1]
+    out = np.zeros((sel.size, dim), dtype=np.float64)
+    if sel.size and (sel.min() < 0 or sel.max() >= rp.size - 1):
+        raise IndexError("spmm_rows: row id out of range")
+    if cl.size and (cl.min() < 0 or cl.max() >= xx.shape[0]):
+        raise IndexError("spmm_rows: column id out of range")
+    chunks = np.array_split(np.arange(sel.size), max(1, min(threads, sel.size)))
+
+    def run(idx):
+        if idx.size == 0:
+            return
+        k0 = int(idx[0])
+        lib().orc_spmm_rows(idx.size, sel.ctypes.data + 8 * k0, _p(rp), _p(cl), _p(v), _p(xx),
+                            dim, dim, _p(b), out.ctypes.data + 8 * dim * k0)
+
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        list(ex.map(run, chunks))
     return out
 
 

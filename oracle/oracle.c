@@ -34,6 +34,24 @@ void orc_spmm_csr(int64_t rows, const int64_t* rowptr, const int64_t* col,
   }
 }
 
+/* orc_spmm_csr restricted to the n_sel rows listed in `sel`: out row k is
+ * row sel[k] of A Z (+ b).  Lets a caller check sampled rows of a pass at
+ * full size without running every row. */
+void orc_spmm_rows(int64_t n_sel, const int64_t* sel, const int64_t* rowptr,
+                   const int64_t* col, const float* val, const float* x,
+                   int64_t ldx, int64_t dim, const float* bias, double* out) {
+  for (int64_t k = 0; k < n_sel; ++k) {
+    const int64_t i = sel[k];
+    double* o = out + k * dim;
+    for (int64_t f = 0; f < dim; ++f) o[f] = bias ? (double)bias[f] : 0.0;
+    for (int64_t e = rowptr[i]; e < rowptr[i + 1]; ++e) {
+      const double w = val ? (double)val[e] : 1.0;
+      const float* xr = x + col[e] * ldx;
+      for (int64_t f = 0; f < dim; ++f) o[f] += w * (double)xr[f];
+    }
+  }
+}
+
 /* Transposed aggregation dZ[c] = sum_{(r,c)} val * G[r] computed directly
  * from the CSR (scatter form), independent of any CSC construction. */
 void orc_spmm_csr_t(int64_t rows, int64_t cols, const int64_t* rowptr,

@@ -175,6 +175,23 @@ def test_gcn_matches_dense_vanilla(gpu, norm, feat, hidden):
             assert err <= 1e-5, (parts, mode, k, err)
 
 
+def test_fast_path_rejects_bad_labels_before_stepping(gpu):
+    """A selected row whose label is outside [0, C) raises, as F.cross_entropy
+    does, before the optimizer changes any weight."""
+    ei, x, y, tr, va, te = _graph_data()
+    y = y.clone()
+    y[3] = 99
+    config = GriNNderConfig(num_parts=1)
+    graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+    model = GCN(8, 16, 3, num_layers=2).cuda()
+    before = {k: v.clone() for k, v in model.state_dict().items()}
+    trainer = Trainer(model, graph, config)
+    with pytest.raises(IndexError):
+        trainer.train_epoch(torch.optim.SGD(model.parameters(), lr=0.1),
+                            torch.nn.CrossEntropyLoss())
+    assert all(torch.equal(before[k], v) for k, v in model.state_dict().items())
+
+
 def _vanilla_gat(data, state, make_model):
     """Dense float64 full-batch GAT with the same layer structure."""
     from tests.test_oracle import _dense_gat

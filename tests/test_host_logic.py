@@ -38,6 +38,19 @@ def test_library_exports_every_declared_symbol():
     assert _lib.load().gr_abi_version() == 100
 
 
+def test_loader_refuses_a_stale_library(monkeypatch):
+    """The library carries the hash of the sources it was built from; the
+    loader refuses it when the sources beside it hash differently."""
+    lib = _lib.load()
+    assert lib.gr_source_hash().decode() == _lib.source_hash()
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "source_hash", lambda: "0" * 64)
+    with pytest.raises(ImportError, match="other sources"):
+        _lib.load()
+    monkeypatch.undo()
+    assert _lib.load() is lib
+
+
 def test_errors_are_reported_not_swallowed():
     with pytest.raises(_lib.GrError, match="spmm_plan"):
         _lib.call("gr_spmm_plan", None, 5, 16, None, None, None, None, None)
@@ -116,6 +129,20 @@ def test_partition_subgraph_and_pipeline_bit_exact():
     for pid in range(3):
         for a, b in zip(g.adj_csr[pid], ref[pid][1]):
             assert torch.equal(a, b)
+
+
+def test_native_partition_subgraph_halo_order_known_answer():
+    """The hand-derived halo layout of grinnder/data/partition.py:195-225."""
+    from tests.test_oracle import check_halo_known_answer
+
+    check_halo_known_answer(_build_partition_subgraph)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_native_partition_subgraph_halo_layout_property(seed):
+    from tests.test_oracle import check_halo_layout_property
+
+    check_halo_layout_property(_build_partition_subgraph, seed)
 
 
 def test_partition_cache_round_trip(tmp_path):

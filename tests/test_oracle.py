@@ -193,6 +193,113 @@ def test_partition_subgraph_gather_invariant():
         assert np.allclose(part, full[int(ptr[pid]):int(ptr[pid + 1])], rtol=0, atol=1e-12)
 
 
+# Hand-derived known answer for the halo layout of
+# grinnder/data/partition.py:195-225 (derivation written out below).
+# 8 nodes, 3 partitions ptr=[0,3,5,8]: p0={0,1,2}, p1={3,4}, p2={5,6,7}.
+# Neighbour lists are chosen so that discovery order within an owner is
+# NOT ascending (a sorted-within-owner restatement gives different lists).
+HALO_ROWS = [[7, 3, 5], [4, 6, 0], [5, 3, 7, 1], [6, 1, 3, 0], [2, 7, 5, 1], [5, 4, 0], [],
+             [2, 7, 3, 0, 4]]
+HALO_PTR = [0, 3, 5, 8]
+# pid 0: first-seen halo ids 7,3,5,4,6 -> owner p1: 3,4 ; owner p2: 7,5,6
+#   layout [0,1,2 | 3,4 | 7,5,6]; row 0 (7,3,5) -> (5,3,6) ...
+# pid 1: first-seen 6,1,0,2,7,5 -> p0: 1,0,2 ; p2: 6,7,5
+#   layout [3,4 | 1,0,2 | 6,7,5]
+# pid 2: first-seen 4,0,2,3 -> p0: 0,2 ; p1: 4,3
+#   layout [5,6,7 | 0,2 | 4,3]
+HALO_EXPECTED = {
+    0: dict(rowptr=[0, 3, 6, 10], col=[5, 3, 6, 4, 7, 0, 6, 3, 5, 1],
+            boundaries=[None, [0, 1], [2, 0, 1]], expanded=8, batch=3),
+    1: dict(rowptr=[0, 4, 8], col=[5, 2, 0, 3, 4, 6, 7, 2],
+            boundaries=[[1, 0, 2], None, [1, 2, 0]], expanded=8, batch=2),
+    2: dict(rowptr=[0, 3, 3, 8], col=[0, 5, 3, 4, 2, 6, 3, 5],
+            boundaries=[[0, 2], [1, 0], None], expanded=7, batch=3),
+}
+
+
+def _halo_csr():
+    rowptr = torch.tensor([0] + np.cumsum([len(r) for r in HALO_ROWS]).tolist())
+    col = torch.tensor([c for r in HALO_ROWS for c in r])
+    val = torch.arange(col.numel(), dtype=torch.float32) + 0.5
+    return rowptr, col, val
+
+
+def check_halo_known_answer(fn):
+    """Checks fn(pid, ptr, rowptr, col, w, P) against HALO_EXPECTED."""
+    rowptr, col, val = _halo_csr()
+    ptr = torch.tensor(HALO_PTR)
+    for pid, exp in HALO_EXPECTED.items():
+        got_pid, (rp, c, v), bnd, expanded, batch = fn(pid, ptr, rowptr, col, val, 3)
+        assert got_pid == pid
+        assert rp.tolist() == exp["rowptr"], pid
+        assert c.tolist() == exp["col"], pid
+        seeds = range(HALO_PTR[pid], HALO_PTR[pid + 1])
+        assert v.tolist() == [float(val[j]) for s in seeds
+                              for j in range(int(rowptr[s]), int(rowptr[s + 1]))]
+        assert [None if b is None else b.tolist() for b in bnd] == exp["boundaries"], pid
+        assert (expanded, batch) == (exp["expanded"], exp["batch"])
+
+
+def check_halo_layout_property(fn, seed):
+    """Independent restatement of the layout: the concatenated global ids of
+    the boundaries are n_id[B:] stably sorted by owning partition, and each
+    remapped column addresses the same global node as before the remap."""
+    g = torch.Generator().manual_seed(seed)
+    n, parts = 120, 5
+    ei = torch.randint(0, n, (2, 900), generator=g)
+    rowptr, col, _ = oracle.edge_index_to_csr(ei, n)
+    val = torch.rand(col.numel(), generator=g)
+    cuts = torch.sort(torch.randperm(n - 1, generator=g)[:parts - 1] + 1).values
+    ptr = torch.cat([torch.tensor([0]), cuts, torch.tensor([n])])
+    for pid in range(parts):
+        lo, hi = int(ptr[pid]), int(ptr[pid + 1])
+        _, _, _, n_id = oracle.build_subgraph(rowptr, col, val, torch.arange(lo, hi), True)
+        halo = n_id[hi - lo:]
+        owner = torch.searchsorted(ptr, halo, right=True) - 1
+        order = torch.sort(owner, stable=True).indices
+        _, (rp, c, v), bnd, expanded, batch = fn(pid, ptr, rowptr, col, val, parts)
+        got = [b + ptr[p] for p, b in enumerate(bnd) if b is not None]
+        got = torch.cat(got) if got else torch.zeros(0, dtype=torch.long)
+        assert torch.equal(got, halo[order])
+        layout = torch.cat([torch.arange(lo, hi), got])
+        assert expanded == layout.numel() and batch == hi - lo
+        assert torch.equal(layout[c], col[int(rowptr[lo]):int(rowptr[hi])])
+        for p, b in enumerate(bnd):
+            assert (b is None) == (p == pid or not bool((owner == p).any()))
+
+
+def _sorted_within_owner(pid, ptr, rowptr, col, w, parts):
+    """A plausible slip: the oracle with halo ids sorted within each owner."""
+    out = oracle.build_partition_subgraph(pid, ptr, rowptr, col, w, parts)
+    _, (rp, c, v), bnd, expanded, batch = out
+    layout_old = torch.cat([torch.arange(int(ptr[pid]), int(ptr[pid + 1]))]
+                           + [b + ptr[p] for p, b in enumerate(bnd) if b is not None])
+    bnd = [None if b is None else torch.sort(b).values for b in bnd]
+    layout = torch.cat([torch.arange(int(ptr[pid]), int(ptr[pid + 1]))]
+                       + [b + ptr[p] for p, b in enumerate(bnd) if b is not None])
+    pos = {int(g): i for i, g in enumerate(layout.tolist())}
+    c = torch.tensor([pos[int(layout_old[k])] for k in c.tolist()], dtype=torch.long)
+    return pid, (rp, c, v), bnd, expanded, batch
+
+
+def test_partition_subgraph_halo_order_known_answer():
+    check_halo_known_answer(oracle.build_partition_subgraph)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_partition_subgraph_halo_layout_property(seed):
+    check_halo_layout_property(oracle.build_partition_subgraph, seed)
+
+
+def test_halo_checks_reject_sorted_within_owner():
+    """The two checks above fail for an oracle that sorts halo ids within an
+    owner (the mistake is planted in a copy of the oracle, on the CPU)."""
+    with pytest.raises(AssertionError):
+        check_halo_known_answer(_sorted_within_owner)
+    with pytest.raises(AssertionError):
+        check_halo_layout_property(_sorted_within_owner, 0)
+
+
 # ----------------------------------------------------------- arithmetic --
 
 def _dense(rowptr, col, val, rows, cols):
@@ -214,6 +321,21 @@ def test_spmm_matches_dense_brute_force():
     g = torch.randn(40, 9)
     got_t = oracle.spmm_t(rowptr, col, val, g, 55)
     assert np.allclose(got_t, (a.t() @ g.double()).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_rows_matches_dense_brute_force():
+    """The row-subset driver (used at full size on sampled rows): repeated and
+    unordered row ids, empty rows, a bias, and any thread count."""
+    rowptr, col, val = random_bipartite(60, 70, 7, seed=12, long_rows=2, long_len=150)
+    x = torch.randn(70, 6, generator=torch.Generator().manual_seed(1))
+    b = torch.randn(6)
+    ref = (_dense(rowptr, col, val, 60, 70) @ x.double() + b.double()).numpy()
+    rows = torch.tensor([59, 3, 3, 0, 17, 42, 8, 8, 31])
+    for threads in (1, 4, 16):
+        got = oracle.spmm_rows(rowptr, col, val, x, rows, b, threads=threads)
+        assert np.allclose(got, ref[rows.numpy()], rtol=0, atol=1e-12)
+    with pytest.raises(IndexError):
+        oracle.spmm_rows(rowptr, col, val, x, torch.tensor([60]))
 
 
 def test_spmm_special_cases():
