@@ -45,6 +45,8 @@ _SIGNATURES = {
     "gr_spmm_plan": [_P, _i64, _i32, _P, _P, _P, _P, _P],
     "gr_gcn_aggregate": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64, _i64, _P,
                          _i64, _P],
+    "gr_gcn_aggregate_noalloc": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64,
+                                 _i64, _i64, _P],
     "gr_gcn_aggregate_into": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _i64, _i64, _i64,
                               _P, _i64, _P],
     "gr_gather_rows": [_P, _i64, _i64, _P, _i64, _i64, _P, _i64, _P],

@@ -9,6 +9,8 @@
 // the EPI slots are combined with cross-lane shuffles; rows longer than the
 // plan's segment length are summed by a second, ordered pass, so results do
 // not depend on scheduling (no atomics).
+#include <mutex>
+
 #include "gr_internal.h"
 #include "wave.h"
 
@@ -846,6 +848,62 @@ extern "C" int gr_gcn_aggregate(const int32_t* units, int64_t n_units, const int
   gr::clear_error();
   return gr_agg::aggregate_entry(units, n_units, fixups, n_fix, idx, val, x, ldx, y, ldy, bias,
                                  rows, dim, workspace, n_slots, nullptr, stream);
+}
+
+// Scratch of gr_gcn_aggregate_noalloc: the split-row partial sums live in
+// this file-scope device array instead of a caller workspace.  Each GPU the
+// library runs on holds its own copy until the process ends.  Host code
+// never uses the array's name as a device address: its address on each
+// device comes from hipGetSymbolAddress, taken once per device with that
+// device current, and only that address reaches kernels.
+__device__ __align__(256) float scratch[GR_NOALLOC_SCRATCH_FLOATS];
+
+namespace gr_agg {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once).
+int scratch_address(float** out) {
+  int dev = -1;
+  GR_HIP_CHECK(hipGetDevice(&dev));
+  GR_REQUIRE(dev >= 0 && dev < kMaxDevices, "gcn_aggregate_noalloc: device %d unsupported",
+             dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    GR_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    GR_REQUIRE(p != nullptr, "gcn_aggregate_noalloc: no device address for the scratch");
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return GR_OK;
+}
+
+}  // namespace gr_agg
+
+extern "C" int gr_gcn_aggregate_noalloc(const int32_t* units, int64_t n_units,
+                                        const int32_t* fixups, int64_t n_fix,
+                                        const int32_t* idx, const float* val, const float* x,
+                                        int64_t ldx, float* y, int64_t ldy, const float* bias,
+                                        int64_t rows, int64_t dim, int64_t n_slots,
+                                        void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(dim >= 1 && n_slots >= 0, "gcn_aggregate_noalloc: bad dim or n_slots");
+  GR_REQUIRE(n_slots <= GR_NOALLOC_SCRATCH_FLOATS / dim,
+             "gcn_aggregate_noalloc: %lld split slots of %lld floats exceed the scratch of "
+             "%lld floats; use gr_gcn_aggregate with a workspace",
+             (long long)n_slots, (long long)dim, (long long)GR_NOALLOC_SCRATCH_FLOATS);
+  float* ws = nullptr;
+  if (n_fix > 0 && n_units > 0) {
+    const int rc = gr_agg::scratch_address(&ws);
+    if (rc != GR_OK) return rc;
+  }
+  // Split units store every element of their slot before the fixup reads
+  // it, so nothing in the scratch needs clearing between calls.
+  return gr_agg::aggregate_entry(units, n_units, fixups, n_fix, idx, val, x, ldx, y, ldy, bias,
+                                 rows, dim, ws, n_slots, nullptr, stream);
 }
 
 extern "C" int gr_gcn_aggregate_into(const int32_t* units, int64_t n_units,

@@ -218,6 +218,25 @@ int gr_gcn_aggregate(const int32_t* units, int64_t n_units,
                      int64_t rows, int64_t dim, float* workspace,
                      int64_t n_slots, void* stream);
 
+/* Floats of the per-GPU scratch behind gr_gcn_aggregate_noalloc (32 MiB). */
+#define GR_NOALLOC_SCRATCH_FLOATS (8LL << 20)
+
+/* No counterpart in the reference.  gr_gcn_aggregate for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same kernels and results, with the
+ * split-row partial sums in a static per-GPU scratch of
+ * GR_NOALLOC_SCRATCH_FLOATS floats instead of a caller workspace.  Rejects
+ * n_slots * dim above that maximum (use gr_gcn_aggregate then).  Allocates
+ * nothing; the scratch address is looked up once per GPU on the first call
+ * there.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (two streams, two threads) race.  No clearing is
+ * needed between calls: each call writes every slot element it reads. */
+int gr_gcn_aggregate_noalloc(const int32_t* units, int64_t n_units,
+                             const int32_t* fixups, int64_t n_fix,
+                             const int32_t* idx, const float* val, const float* x,
+                             int64_t ldx, float* y, int64_t ldy, const float* bias,
+                             int64_t rows, int64_t dim, int64_t n_slots, void* stream);
+
 /* No counterpart in the reference: gr_gcn_aggregate with an output row map,
  * for the backward of projected layers (grinnder_amd/engine/trainer.py),
  * which add the gradient of a partition's gathered rows straight into the
