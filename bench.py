@@ -4,22 +4,28 @@ Default workload ("products-scale GCN"): seeded
 R-MAT graph (a,b,c,d = .57,.19,.19,.05; scale 22), 2,449,029 nodes,
 61,859,140 undirected edges (123,718,280 directed + 2,449,029 self-loops),
 fp32 features N(0,1) dim 100, 47 classes, 3-layer GCN hidden 256 with
-LayerNorm and full-graph symmetric normalisation, num_parts=1 (all resident),
-Adam(lr=0.01, wd=5e-4).  A step is one Trainer.train_epoch (forward +
-backward of all layers + optimizer step) with every input resident in HBM.
+LayerNorm and full-graph symmetric normalisation, num_parts=1, Adam(lr=0.01,
+wd=5e-4).  A step is one Trainer.train_epoch (forward + backward of all
+layers + optimizer step).  Graph plans, labels and masks are in HBM when the
+timed region starts; the input features follow --inputs: 'stream' (default,
+the reference's data movement: uploaded from pinned host memory every epoch,
+the next epoch's upload overlapped with this one) or 'resident' (kept in HBM
+across epochs).  The policy is the same for every configuration and is
+recorded in config.inputs.
 
-Printed JSON line (rank 0): metric/value/unit = aggregation fwd+bwd GTEPS of
-the whole epoch: the reference model's 2 x num_layers aggregation passes of
-nnz edges each per epoch, divided by the epoch wall time.  (A layer that
-widens aggregates first here, so its backward needs no aggregation; the
-edges actually traversed per epoch are reported as `edges_per_epoch`.)  The
-kernel-level aggregation GTEPS (edges traversed / time inside the aggregation
-passes), HBM fraction and epoch time go alongside, with the
-roofline of the dominant kernel (the D=256 GCN aggregation passes, timed with
-HIP events on their stream) and a CPU baseline (the oracle's sequential
-aggregation on a bounded row sample).
+Printed JSON line (rank 0): value = aggregation GTEPS of the whole epoch:
+the edges the aggregation kernels traverse per epoch (forward and backward
+passes; a widening first layer aggregates first, so its backward traverses
+none) divided by the epoch wall time.  `model_edges_per_epoch` is the
+reference model's 2 x num_layers passes of nnz edges, given beside it.  The
+kernel-level aggregation GTEPS and HBM fraction (time inside the aggregation
+passes), the roofline of the dominant kernel (the D=256 passes, HIP events on
+their stream) and the CPU baselines (torch sparse CSR on the host's threads;
+the reference's halo gather/scatter for partitioned configs; the oracle)
+go alongside.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c1]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1..c5]
+       [--inputs stream|resident]
 """
 
 from __future__ import annotations
@@ -62,6 +68,10 @@ def parse_args():
     ap.add_argument("--dropout", type=float, default=0.0,
                     help="model dropout (the reference's own benchmarks use 0; GAT's input "
                          "dropout, when active, rules out the projected flow)")
+    ap.add_argument("--inputs", choices=("stream", "resident"), default="stream",
+                    help="input features uploaded from host memory every epoch, overlapped "
+                         "('stream', the reference's data movement) or kept in HBM across "
+                         "epochs ('resident'); GriNNderConfig.input_residency")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
                     help="print a text summary of the rocprofv3 CSV output under DIR and exit")
@@ -93,7 +103,7 @@ CONFIGS = {
 }
 
 
-def build_graph(cfg, device, project_first="auto"):
+def build_graph(cfg, device, project_first="auto", inputs="stream"):
     import torch
 
     from grinnder_amd.config import GriNNderConfig
@@ -116,7 +126,7 @@ def build_graph(cfg, device, project_first="auto"):
         nd = synthetic.node_data(n, cfg["feat_dim"], cfg["num_classes"], seed=42)
         x = nd.x
     config = GriNNderConfig(num_parts=cfg["num_parts"], device=device,
-                            project_first=project_first)
+                            project_first=project_first, input_residency=inputs)
     graph = build_partitioned_graph(ei, x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
                                     config)
     del ei
@@ -126,10 +136,131 @@ def build_graph(cfg, device, project_first="auto"):
     return graph, config
 
 
-def cpu_baseline(graph, dim: int, seconds: float):
-    """Oracle (sequential C, float64 accumulation, 1 thread) on a row sample
-    of one D=dim aggregation pass of partition 0; returns (GTEPS, sample)."""
-    import numpy as np
+def host_info() -> dict:
+    """CPU model, core counts and RAM of this machine (lscpu, /proc/meminfo)."""
+    import subprocess
+
+    info = {"threads": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = {k.strip(): v.strip() for k, _, v in (l.partition(":") for l in out.splitlines())}
+        info["model"] = kv.get("Model name")
+        per_socket = int(kv.get("Core(s) per socket", "0") or 0)
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        if per_socket and sockets:
+            info["physical_cores"] = per_socket * sockets
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    try:
+        mem = {l.split(":")[0]: l.split()[1] for l in open("/proc/meminfo")}
+        info["ram_gib"] = round(int(mem["MemTotal"]) / 2**20, 1)
+    except (OSError, KeyError, ValueError):
+        pass
+    return info
+
+
+def host_threads() -> int:
+    """Host threads this process may use: OMP_NUM_THREADS when set (the GPU
+    box's CPU share), else every CPU."""
+    try:
+        return max(1, min(os.cpu_count() or 1, int(os.environ["OMP_NUM_THREADS"])))
+    except (KeyError, ValueError):
+        return os.cpu_count() or 1
+
+
+def _median_time(fn, runs: int = 5) -> float:
+    import statistics
+
+    fn()  # warm-up
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def cpu_baseline(graph, dim: int, sample_edges: int = 24_000_000) -> dict:
+    """The reference's CPU arithmetic for this path, on
+    every host thread: torch's sparse CSR product for the GCN forward A Z and
+    for the backward Aᵀ G (the transposed CSR, built outside the timing), at
+    width `dim`.  Bounded sample: the first rows of partition 0 up to
+    `sample_edges` edges, with their source columns relabelled to the
+    distinct sources, i.e. a partition-shaped [B, E] block.  One warm-up,
+    then the median of 5 runs of each pass.  GTEPS = (fwd + bwd edges) /
+    (fwd + bwd median time)."""
+    import torch
+
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    rowptr, col, val = graph.adj_csr[0]
+    r1 = int(torch.searchsorted(rowptr, torch.tensor(sample_edges)).clamp(max=rowptr.numel() - 1))
+    e1 = int(rowptr[r1])
+    src, local = torch.unique(col[:e1], return_inverse=True)
+    a = torch.sparse_csr_tensor(rowptr[:r1 + 1].clone(), local, val[:e1].clone(),
+                                (r1, src.numel()))
+    at = a.t().to_sparse_csr()
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(src.numel(), dim, generator=g)
+    gy = torch.randn(r1, dim, generator=g)
+    t_fwd = _median_time(lambda: a @ z)
+    t_bwd = _median_time(lambda: at @ gy)
+    return {"value": round(2 * e1 / (t_fwd + t_bwd) / 1e9, 6), "unit": "GTEPS",
+            "cores": threads, "kind": "port",
+            "sample": (f"torch.sparse_csr (CPU, {threads} threads) A @ Z and A^T @ G at D={dim} "
+                       f"on rows [0, {r1}) of partition 0 with their {src.numel()} distinct "
+                       f"sources ({e1} edges); median of 5 after a warm-up: fwd {t_fwd:.4f} s, "
+                       f"bwd {t_bwd:.4f} s"),
+            "host": host_info()}
+
+
+def cpu_halo_baseline(graph, dim: int, max_parts: int = 4) -> Optional[dict]:
+    """The reference's CPU halo movement (csrc/cuda/async_transfer.cu:60-186):
+    per partition, index_select of the boundary rows of every other
+    partition's host buffer (the gather) and index_put_(accumulate=True) of
+    their gradient rows back (the scatter), partitions in order, at width
+    `dim`, on every host thread.  Bounded: the first `max_parts` partitions.
+    Median of 5 after a warm-up; rates in GB/s of halo rows moved."""
+    import torch
+
+    if graph.num_parts < 2:
+        return None
+    torch.set_num_threads(host_threads())
+    g = torch.Generator().manual_seed(1)
+    host = [torch.randn(b, dim, generator=g) for b in graph.partition_sizes]
+    pids = list(range(min(max_parts, graph.num_parts)))
+    rows = sum(int(b.numel()) for p in pids for q, b in enumerate(graph.boundaries[p])
+               if b is not None and q != p)
+    grads = {p: torch.randn(graph.expanded_sizes[p] - graph.partition_sizes[p], dim,
+                            generator=g) for p in pids}
+
+    def gather():
+        for p in pids:
+            torch.cat([host[q].index_select(0, b) for q, b in enumerate(graph.boundaries[p])
+                       if b is not None and q != p])
+
+    def scatter():
+        for p in pids:
+            off = 0
+            for q, b in enumerate(graph.boundaries[p]):
+                if b is None or q == p:
+                    continue
+                host[q].index_put_((b,), grads[p][off:off + b.numel()], accumulate=True)
+                off += b.numel()
+
+    t_g = _median_time(gather)
+    t_s = _median_time(scatter)
+    nbytes = rows * dim * 4
+    return {"gather_GBps": round(nbytes / t_g / 1e9, 2), "scatter_GBps": round(nbytes / t_s / 1e9, 2),
+            "sample": (f"index_select / index_put_(accumulate=True) of the halo rows of "
+                       f"partitions {pids} ({rows} rows of {dim} floats), "
+                       f"{host_threads()} threads, median of 5: gather {t_g:.4f} s, scatter "
+                       f"{t_s:.4f} s")}
+
+
+def oracle_baseline(graph, dim: int, seconds: float):
+    """Secondary CPU figure: the oracle (sequential C, float64 accumulation,
+    1 thread) on a row sample of one D=dim forward pass of partition 0."""
     import torch
 
     import oracle
@@ -151,9 +282,10 @@ def cpu_baseline(graph, dim: int, seconds: float):
         edges_done += e1 - e0
         start_row = r1
         rows *= 2
-    sample = (f"oracle orc_spmm_csr (C, 1 thread, fp64 accumulate), D={dim}, rows "
-              f"[0, {start_row}) of the forward pass = {edges_done} edges in {elapsed:.1f}s")
-    return edges_done / elapsed / 1e9, sample
+    return {"value": round(edges_done / elapsed / 1e9, 6), "unit": "GTEPS", "cores": 1,
+            "sample": (f"oracle orc_spmm_csr (C, 1 thread, fp64 accumulate), D={dim}, rows "
+                       f"[0, {start_row}) of the forward pass = {edges_done} edges in "
+                       f"{elapsed:.1f}s")}
 
 
 def summarize_profile(root: str) -> None:
@@ -268,7 +400,7 @@ def main():
             f"MemAvailable {int(meminfo['MemAvailable']) / 2**20:.1f} GiB, cpus {os.cpu_count()}")
     except OSError:
         pass
-    graph, config = build_graph(cfg, device, args.project_first)
+    graph, config = build_graph(cfg, device, args.project_first, args.inputs)
     nnz = sum(int(a[1].numel()) for a in graph.adj_csr)
 
     torch.manual_seed(42)
@@ -326,7 +458,7 @@ def main():
     recs = timer.records
     agg_ms = sum(r.ms() for r in recs if r.name.startswith(("gcn_", "gat_")))
     agg_bytes = sum(r.nbytes for r in recs if r.name.startswith(("gcn_", "gat_")))
-    useful_edges = 2 * cfg["num_layers"] * nnz * args.steps
+    model_edges = 2 * cfg["num_layers"] * nnz
     epoch_s = wall / args.steps
     recs_agg = [r for r in recs if r.name.startswith(("gcn_", "gat_"))]
     dom = [r for r in recs_agg if r.dim == cfg["hidden"]]
@@ -368,16 +500,25 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
+        # Reported baselines, never fatal for the GPU number.
         try:
-            gteps, sample = cpu_baseline(graph, cfg["hidden"], args.cpu_seconds)
-            cpu = {"value": round(gteps, 6), "unit": "GTEPS", "cores": 1, "kind": "port",
-                   "sample": sample}
-        except Exception as exc:  # reported, never fatal for the GPU number
+            cpu = cpu_baseline(graph, cfg["hidden"])
+            log(f"cpu baseline: {cpu}")
+        except Exception as exc:
             log(f"cpu baseline failed: {exc!r}")
+        if cpu is not None:
+            try:
+                cpu["halo"] = cpu_halo_baseline(graph, cfg["hidden"])
+            except Exception as exc:
+                log(f"cpu halo baseline failed: {exc!r}")
+            try:
+                cpu["oracle"] = oracle_baseline(graph, cfg["hidden"], args.cpu_seconds)
+            except Exception as exc:
+                log(f"oracle baseline failed: {exc!r}")
 
     out = {
         "metric": "agg fwd+bwd GTEPS & % peak HBM GB/s on 1 MI355X; epoch time (s)",
-        "value": round(useful_edges / wall / 1e9, 4),
+        "value": round(sum(r.edges for r in recs_agg) / wall / 1e9, 4),
         "unit": "GTEPS",
         "n_gpus": 1,
         "steps": args.steps,
@@ -393,6 +534,10 @@ def main():
                    "num_classes": cfg["num_classes"], "num_layers": cfg["num_layers"],
                    "num_parts": cfg["num_parts"], "model": cfg["model"],
                    "dropout": args.dropout,
+                   "inputs": ("features uploaded from pinned host memory every epoch, the "
+                              "next epoch's upload overlapped; plans, labels and masks in HBM"
+                              if args.inputs == "stream" else
+                              "features, plans, labels and masks kept in HBM across epochs"),
                    "halo_amplification": round(graph.halo_amplification(), 4),
                    "projected_layers": trainer.projected_layers,
                    "inplace_layers": trainer.inplace_layers,
@@ -400,6 +545,8 @@ def main():
                    "resident_inputs": trainer.resident_inputs},
         "epoch_s": round(epoch_s, 5),
         "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,
+        "model_edges_per_epoch": model_edges,
+        "model_edge_gteps": round(model_edges * args.steps / wall / 1e9, 4),
         "agg_kernel_gteps": round(sum(r.edges for r in recs_agg) / (agg_ms / 1e3) / 1e9, 4),
         "agg_hbm_frac": round(agg_bytes / (agg_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "agg_ms_per_epoch": round(agg_ms / args.steps, 3),

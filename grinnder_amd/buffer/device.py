@@ -1,12 +1,17 @@
-"""DeviceBuffer: per-partition GPU tensors with lazy allocation (grinnder/buffer/device.py).
+"""HBM blocks of one layer's per-partition rows (the role of grinnder/buffer/device.py).
 
-Tensor objects keep their logical shape; storage is resized to zero on
-release so only the partitions in flight (double buffering) occupy HBM.
+A partition's block exists only while the partition is in flight.
+``allocate`` creates it from torch's caching allocator, on the current
+stream like any tensor; ``release`` drops it and returns its storage at
+once, even if a stale Python reference to the tensor is still around.  A
+double-buffered epoch therefore holds at most a few partitions of a layer
+in HBM.  Blocks are fp32 [rows, dim], rows = the partition's size in this
+buffer (expanded sizes for gathered inputs, partition sizes for gradients).
 """
 
 from __future__ import annotations
 
-from typing import List, Optional
+from typing import Dict, List, Optional
 
 import torch
 from torch import Tensor
@@ -18,53 +23,67 @@ from grinnder_amd.buffer.host import HostBuffer
 class DeviceBuffer:
     def __init__(self, num_parts: int, part_sizes: List[int], embedding_dim: int,
                  device: str = "cuda:0"):
+        if len(part_sizes) != num_parts:
+            raise ValueError(f"{len(part_sizes)} partition sizes for {num_parts} partitions")
         self.num_parts = num_parts
-        self.part_sizes = list(part_sizes)
-        self.embedding_dim = embedding_dim
-        self.device = device
-        self._tensors: List[Tensor] = []
-        for i in range(num_parts):
-            t = torch.empty(part_sizes[i], embedding_dim, dtype=torch.float32, device=device)
-            t.untyped_storage().resize_(0)
-            self._tensors.append(t)
-
-    def __getitem__(self, pid: int) -> Tensor:
-        return self._tensors[pid]
+        self.part_sizes = [int(s) for s in part_sizes]
+        self.embedding_dim = int(embedding_dim)
+        self.device = torch.device(device)
+        self._blocks: Dict[int, Tensor] = {}
 
     def __len__(self) -> int:
         return self.num_parts
 
+    def __getitem__(self, pid: int) -> Tensor:
+        """The partition's block; without one, a shape-only (meta) tensor of
+        the partition's logical shape, which holds no memory."""
+        block = self._blocks.get(pid)
+        if block is not None:
+            return block
+        if not 0 <= pid < self.num_parts:
+            raise IndexError(f"partition {pid} outside [0, {self.num_parts})")
+        return torch.empty((self.part_sizes[pid], self.embedding_dim), dtype=torch.float32,
+                           device="meta")
+
     def allocate(self, pid: int) -> Tensor:
-        t = self._tensors[pid]
-        nbytes = t.numel() * t.element_size()
-        if t.untyped_storage().size() < nbytes:
-            t.untyped_storage().resize_(nbytes)
-        return t
+        """The partition's block, created on first use."""
+        block = self._blocks.get(pid)
+        if block is None:
+            if not 0 <= pid < self.num_parts:
+                raise IndexError(f"partition {pid} outside [0, {self.num_parts})")
+            block = torch.empty((self.part_sizes[pid], self.embedding_dim),
+                                dtype=torch.float32, device=self.device)
+            self._blocks[pid] = block
+        return block
 
     def release(self, pid: int) -> None:
-        t = self._tensors[pid]
-        t.untyped_storage().resize_(0)
-        t.grad = None
+        block = self._blocks.pop(pid, None)
+        if block is not None:
+            block.grad = None
+            block.untyped_storage().resize_(0)
 
     def is_allocated(self, pid: int) -> bool:
-        return self._tensors[pid].untyped_storage().size() > 0
+        return pid in self._blocks
 
     def allocated_pids(self) -> List[int]:
-        return [p for p in range(self.num_parts) if self.is_allocated(p)]
+        return sorted(self._blocks)
 
     @property
     def resident_bytes(self) -> int:
-        return sum(t.untyped_storage().size() for t in self._tensors)
+        return sum(b.untyped_storage().nbytes() for b in self._blocks.values())
 
     def async_gather(self, pid: int, host_buffer: HostBuffer,
                      boundaries: List[Optional[Tensor]], stream: torch.cuda.Stream) -> None:
-        self.allocate(pid)
-        host_buffer.async_gather(pid, self._tensors[pid], boundaries, stream)
+        """Queues the partition's [intra | halo] rows from the host buffers
+        into its block on `stream` (see HostBuffer.async_gather)."""
+        host_buffer.async_gather(pid, self.allocate(pid), boundaries, stream)
 
     def h2d_synchronize(self, stream: torch.cuda.Stream) -> None:
+        """Waits for the oldest queued upload (errors are raised, not
+        swallowed) and for `stream`."""
         _C.h2d_synchronize()
         stream.synchronize()
 
     def reset(self) -> None:
-        for i in range(self.num_parts):
-            self.release(i)
+        for pid in list(self._blocks):
+            self.release(pid)

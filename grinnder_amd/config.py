@@ -40,6 +40,13 @@ class GriNNderConfig:
         gradient into one (same results up to fp32 summation order).  'off'
         gathers every layer's input rows from the host buffers as the
         reference does.  Not a field of the reference's config.
+    input_residency: 'stream' (the reference's data movement) uploads the
+        input features from pinned host memory every epoch, the next epoch's
+        upload running on a side stream while this epoch computes (the
+        single-partition path and the layer-0 rows of projected / in-place
+        layers).  'resident' uploads them once and keeps them in HBM across
+        epochs (the features are static).  Not a field of the reference's
+        config.
     """
 
     mode: Literal["hongtu", "grinnder"] = "grinnder"
@@ -68,3 +75,4 @@ class GriNNderConfig:
     num_gpus: int = 1
 
     project_first: Literal["auto", "off"] = "auto"
+    input_residency: Literal["stream", "resident"] = "stream"

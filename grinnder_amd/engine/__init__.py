@@ -1,14 +1,6 @@
-"""Training engine: layer-wise, partition-wise orchestration."""
+"""Training engine: the layer-wise, partition-wise Trainer and its streams."""
 
+from grinnder_amd.engine.streams import StreamManager
+from grinnder_amd.engine.trainer import Trainer
 
-def __getattr__(name):
-    if name == "Trainer":
-        from grinnder_amd.engine.trainer import Trainer
-        return Trainer
-    if name == "StreamManager":
-        from grinnder_amd.engine.streams import StreamManager
-        return StreamManager
-    raise AttributeError(f"module 'grinnder_amd.engine' has no attribute {name!r}")
-
-
-__all__ = ["Trainer", "StreamManager"]
+__all__ = ["StreamManager", "Trainer"]

@@ -77,6 +77,9 @@ class ProjectedLayers:
         self._x0cur = 0
         self._x0double = False
         self._x0pending: Optional[tuple] = None
+        # input_residency 'resident': the index of the buffer that holds the
+        # layer-0 rows already (uploaded in an earlier epoch), else -1.
+        self._x0loaded = -1
         self._pf_streams: List[torch.cuda.Stream] = []
         # Per-row quantities of each projected layer's Z formed once for all
         # partitions this epoch (GAT's attention scores), by layer.
@@ -253,7 +256,7 @@ class ProjectedLayers:
         # A second copy of layer 0's input rows for the next epoch's upload to
         # stream into while this epoch computes.
         self._x0double = False
-        if 0 in self._xin:
+        if 0 in self._xin and cfg.input_residency == "stream":
             if len(self._x0bufs) >= 2:
                 self._x0double = True
             else:
@@ -545,16 +548,23 @@ class ProjectedLayers:
         if layer != 0:
             raise ValueError("only layer 0's input rows are uploaded to a resident buffer")
         g, s, pids = self.graph, self.streams, self._my_pids
+        resident = self.config.input_residency == "resident"
         if self._x0pending is not None:
             idx, ready = self._x0pending
             self._x0pending = None
+        elif resident and self._x0loaded == self._x0cur:
+            # Uploaded in an earlier epoch; compute work is ordered after it.
+            idx, ready = self._x0cur, None
         else:
             idx = self._x0cur
             ready = self._issue_layer0_upload(idx)
         self._x0cur = idx
+        if resident:
+            self._x0loaded = idx
         x = self._xres[0] = self._x0bufs[idx]
         for i, pid in enumerate(pids):
-            s.compute.wait_event(ready[i])
+            if ready is not None:
+                s.compute.wait_event(ready[i])
             with torch.cuda.stream(s.compute):
                 lo, hi = g._range(pid)
                 fn(pid, x[lo:hi], lo, hi)

@@ -80,6 +80,43 @@ from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.loss import check_stats, mask_codes, masked_cross_entropy
 
 
+class _EpochUploads:
+    """Input features uploaded from pinned host memory once per epoch into
+    two HBM buffers in turn: while an epoch computes on one buffer, the next
+    epoch's upload runs on a side stream into the other.  An upload waits
+    for the compute work queued before it, which includes the last epoch
+    that read its buffer."""
+
+    def __init__(self, host: Tensor, device: torch.device):
+        self.host = host
+        self.bufs = [torch.empty(host.shape, dtype=host.dtype, device=device) for _ in range(2)]
+        self.stream = torch.cuda.Stream(device)
+        self.pending: Optional[tuple] = None
+        self.cur = 0
+
+    def _issue(self, idx: int, compute: torch.cuda.Stream) -> torch.cuda.Event:
+        entry = torch.cuda.Event()
+        entry.record(compute)
+        self.stream.wait_event(entry)
+        with torch.cuda.stream(self.stream):
+            from grinnder_amd.aggregation import KernelTimer
+            with KernelTimer.region("x_upload", self.host.numel() * 4, 0, self.host.size(1)):
+                self.bufs[idx].copy_(self.host, non_blocking=True)
+            done = torch.cuda.Event()
+            done.record(self.stream)
+        return done
+
+    def next(self, compute: torch.cuda.Stream) -> Tensor:
+        if self.pending is None:
+            idx, done = self.cur, self._issue(self.cur, compute)
+        else:
+            idx, done = self.pending
+        compute.wait_event(done)
+        self.cur = idx
+        self.pending = (1 - idx, self._issue(1 - idx, compute))
+        return self.bufs[idx]
+
+
 class Trainer(ProjectedLayers):
     def __init__(self, model: GriNNderModel, graph: PartitionedGraph, config: GriNNderConfig,
                  partition_range: Optional[tuple] = None):
@@ -122,6 +159,7 @@ class Trainer(ProjectedLayers):
         self.activations: List[List[Optional[Tensor]]] = [[None] * P for _ in range(L)]
         self._pid_to_loss_idx: Dict[int, int] = {}
         self._resident: Dict[str, Tensor] = {}
+        self._uploads: Optional[_EpochUploads] = None
         self._label_cache: Dict[int, tuple] = {}
         self._init_projected()
         if not self._fast:
@@ -209,9 +247,26 @@ class Trainer(ProjectedLayers):
             self._resident[name] = t
         return t
 
+    def _fast_features(self) -> Tensor:
+        """This epoch's input features in HBM.  'resident': uploaded once.
+        'stream': uploaded from pinned host memory every epoch, as the
+        reference does (trainer.py:421-428), the next epoch's upload queued
+        on a side stream as soon as this epoch has its rows."""
+        g = self.graph
+        if self.config.input_residency == "resident":
+            return self._res("x", lambda: g.partition_features(0).to(self.device))
+        up = self._uploads
+        if up is None:
+            feats = g.partition_features(0)
+            host = torch.empty(feats.shape, dtype=torch.float32, pin_memory=True)
+            host.copy_(feats)
+            del feats
+            up = self._uploads = _EpochUploads(host, self.device)
+        return up.next(torch.cuda.current_stream())
+
     def _fast_logits(self) -> Tensor:
         g = self.graph
-        x = self._res("x", lambda: g.partition_features(0).to(self.device))
+        x = self._fast_features()
         adj = g.adjacency(0)
         out = x
         for l in range(self.model.num_layers):

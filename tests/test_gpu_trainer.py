@@ -624,6 +624,46 @@ def test_layer0_prefetch_across_epochs_is_exact(gpu, model_kind, monkeypatch):
     assert all(torch.equal(w0[k], w1[k]) for k in w0)
 
 
+@pytest.mark.parametrize("num_parts,model_kind", [(1, "gcn"), (1, "gcn_narrow"), (4, "gcn"),
+                                                  (4, "gat")])
+def test_input_residency_stream_equals_resident(gpu, num_parts, model_kind):
+    """input_residency 'stream' (features uploaded every epoch, the next
+    epoch's upload overlapped) and 'resident' (uploaded once): four steps
+    with the weights changing and an evaluate() in between give
+    bit-identical metrics and weights, on the single-partition path and on
+    the partitioned projected flow."""
+    data = _graph_data(n=60, reach=3, feat=24, classes=4, train_all=False)
+    ei, x, y, tr, va, te = data
+    torch.manual_seed(5)
+    if model_kind == "gcn":
+        make = lambda: GCN(24, 32, 4, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
+    elif model_kind == "gcn_narrow":  # layer 0 projects first: autograd keeps x for dW
+        make = lambda: GCN(24, 16, 4, num_layers=2, dropout=0.0, norm=True)  # noqa: E731
+    else:
+        make = lambda: GAT(24, 8, 4, num_layers=2, heads=1, dropout=0.0, norm=True)  # noqa
+    state = make().state_dict()
+    runs = []
+    for residency in ("stream", "resident"):
+        config = GriNNderConfig(num_parts=num_parts, input_residency=residency)
+        graph = build_partitioned_graph(ei, x, y, tr, va, te, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.Adam(model.parameters(), lr=0.05)
+        crit = torch.nn.CrossEntropyLoss()
+        metrics = [trainer.train_epoch(opt, crit) if step == "train" else trainer.evaluate(crit)
+                   for step in ("train", "eval", "train", "train")]
+        if num_parts == 1:
+            assert (trainer._uploads is not None) == (residency == "stream")
+        else:
+            assert 0 in trainer.resident_inputs or 0 in trainer.inplace_layers
+            assert len(trainer._x0bufs) == (2 if residency == "stream" else 1)
+        runs.append((metrics, {k: v.detach().clone() for k, v in model.state_dict().items()}))
+    (m0, w0), (m1, w1) = runs
+    assert m0 == m1
+    assert all(torch.equal(w0[k], w1[k]) for k in w0)
+
+
 @pytest.mark.parametrize("pool_size", [1, 2])
 @pytest.mark.parametrize("resident", ["all", "projected", "none"])
 def test_mixed_flows_match_reference(gpu, pool_size, resident, monkeypatch):
