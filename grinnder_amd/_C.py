@@ -13,9 +13,14 @@ buffer and autograd layers call them unchanged:
 Differences by design: work is enqueued on the current stream from the
 calling thread (no worker thread is needed for pinned buffers), errors are
 raised immediately or by the next *_synchronize (never swallowed), and
-pinned host partitions are moved by device kernels over PCIe.  The
-io_uring engine (IoUringEngine) belongs to the storage tier and is not
-provided.
+pinned host partitions are moved by device kernels over PCIe.
+
+  IoUringEngine(queue_depth)                 csrc/cpu/io_uring_engine.cpp:15-245
+      submit_read / submit_write(path, tensor, offset, nbytes) -> handle,
+      wait(handle), wait_all(), poll(handle), pending(), has_io_uring()
+      The storage tier's host <-> file engine.  liburing is absent, so
+      requests run on a pread/pwrite thread pool (gr_io_*); has_io_uring()
+      is therefore False.  Failed or short transfers raise at wait().
 """
 
 from __future__ import annotations
@@ -31,7 +36,7 @@ from grinnder_amd.data.partition import build_subgraph  # noqa: F401  (re-export
 
 __all__ = [
     "h2d_copy_async", "d2h_copy_async", "h2d_synchronize", "d2h_synchronize",
-    "gather_partitions", "scatter_partitions", "build_subgraph",
+    "gather_partitions", "scatter_partitions", "build_subgraph", "IoUringEngine",
 ]
 
 
@@ -145,3 +150,82 @@ def scatter_partitions(pid: int, src: Tensor, dsts: List[Tensor],
         _lib.call("gr_scatter_partitions", pid, P, src.data_ptr(), src.size(0), max(dim, 1),
                   dst_ptrs, dst_rows, bptr, blen, stream.cuda_stream)
     del keep
+
+
+class IoUringEngine:
+    """Asynchronous host <-> file I/O (the reference's IoUringEngine API).
+
+    `queue_depth` bounds the worker threads (at most 16): each request is
+    split into 8 MiB chunks that the workers read or write in parallel.
+    A submitted tensor must stay alive, and unchanged for a write, until
+    the request is waited for; the engine keeps a reference to it until then.
+    """
+
+    def __init__(self, queue_depth: int = 64):
+        import ctypes
+
+        if queue_depth < 1:
+            raise ValueError("queue_depth must be >= 1")
+        handle = ctypes.c_void_p()
+        _lib.call("gr_io_create", max(1, min(16, int(queue_depth))), ctypes.byref(handle))
+        self._engine = handle.value
+        self._inflight = {}
+
+    def has_io_uring(self) -> bool:
+        return False
+
+    def _submit(self, write: bool, path: str, tensor: Tensor, offset: int, nbytes: int) -> int:
+        import ctypes
+
+        what = "submit_write" if write else "submit_read"
+        _require(not tensor.is_cuda, f"{what}: tensor must be on CPU")
+        _require(tensor.is_contiguous(), f"{what}: tensor must be contiguous")
+        _require(0 <= nbytes <= tensor.numel() * tensor.element_size(),
+                 f"{what}: {nbytes} bytes do not fit the tensor")
+        h = ctypes.c_int64()
+        _lib.call("gr_io_submit", self._engine, int(write), str(path).encode(),
+                  tensor.data_ptr() if nbytes else None, int(offset), int(nbytes),
+                  ctypes.byref(h))
+        self._inflight[h.value] = tensor
+        return h.value
+
+    def submit_read(self, path: str, tensor: Tensor, offset: int, nbytes: int) -> int:
+        return self._submit(False, path, tensor, offset, nbytes)
+
+    def submit_write(self, path: str, tensor: Tensor, offset: int, nbytes: int) -> int:
+        return self._submit(True, path, tensor, offset, nbytes)
+
+    def wait(self, handle: int) -> None:
+        try:
+            _lib.call("gr_io_wait", self._engine, int(handle))
+        finally:
+            self._inflight.pop(handle, None)
+
+    def wait_all(self) -> None:
+        try:
+            _lib.call("gr_io_wait_all", self._engine)
+        finally:
+            self._inflight.clear()
+
+    def poll(self, handle: int) -> bool:
+        import ctypes
+
+        done = ctypes.c_int32()
+        _lib.call("gr_io_poll", self._engine, int(handle), ctypes.byref(done))
+        return bool(done.value)
+
+    def pending(self) -> int:
+        import ctypes
+
+        n = ctypes.c_int64()
+        _lib.call("gr_io_pending", self._engine, ctypes.byref(n))
+        return int(n.value)
+
+    def __del__(self):
+        engine = getattr(self, "_engine", None)
+        if engine:
+            self._engine = None
+            try:
+                _lib.load().gr_io_destroy(engine)
+            except Exception:  # interpreter shutdown
+                pass

@@ -73,6 +73,13 @@ _SIGNATURES = {
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],
+    "gr_io_create": [_i32, _P],
+    "gr_io_destroy": [_P],
+    "gr_io_submit": [_P, _i32, ctypes.c_char_p, _P, _i64, _i64, _P],
+    "gr_io_wait": [_P, _i64],
+    "gr_io_wait_all": [_P],
+    "gr_io_poll": [_P, _i64, _P],
+    "gr_io_pending": [_P, _P],
     "gr_rmat_sample": [_u64, _i32, _dbl, _dbl, _dbl, _i64, _i64, _P, _P, _i32],
     "gr_gaussian_rows": [_u64, _P, _i64, _i64, _P, _i32],
 }

@@ -97,8 +97,7 @@ class HostBuffer:
     def __init__(self, num_parts: int, part_sizes: List[int], embedding_dim: int,
                  backend=None, file_prefix: str = "host", lazy: bool = True,
                  pin_memory: bool = False):
-        if backend is not None:
-            raise NotImplementedError("the NVMe storage tier is outside this package's scope")
+        self._backend = backend
         self.num_parts = num_parts
         self.part_sizes = list(part_sizes)
         self.embedding_dim = embedding_dim
@@ -107,6 +106,9 @@ class HostBuffer:
         self._lazy = lazy
         self._pin_memory = pin_memory
         self._zero_initialized = [False] * num_parts
+        # Partitions whose host rows may differ from their storage copy (the
+        # copy is rewritten before such a partition is evicted).
+        self._dirty = [False] * num_parts
         self._tensors: List[Tensor] = []
         # D2H entries (fills, scatters) this buffer queued and nobody waited
         # for yet; the library's D2H completion queue is FIFO.
@@ -121,6 +123,7 @@ class HostBuffer:
 
     def __getitem__(self, pid: int) -> Tensor:
         self.allocate(pid)
+        self._dirty[pid] = True  # the caller may write through the tensor
         return self._tensors[pid]
 
     def __len__(self) -> int:
@@ -151,6 +154,7 @@ class HostBuffer:
         self._tensors[pid] = _empty_host_tensor(self.part_sizes[pid], self.embedding_dim,
                                                 pin_memory=self._pin_memory, allocate=False)
         self._zero_initialized[pid] = False
+        self._dirty[pid] = False
 
     def release_all(self) -> None:
         for pid in range(self.num_parts):
@@ -165,6 +169,7 @@ class HostBuffer:
     def zero_partition(self, pid: int) -> None:
         self.allocate(pid).zero_()
         self._zero_initialized[pid] = True
+        self._dirty[pid] = True
 
     @property
     def resident_bytes(self) -> int:
@@ -182,6 +187,7 @@ class HostBuffer:
             _C.d2h_copy_async(gpu_data.contiguous(), self._tensors[pid])
         self.d2h_queued += 1
         self._zero_initialized[pid] = True
+        self._dirty[pid] = True
 
     def d2h_synchronize(self, stream: torch.cuda.Stream) -> None:
         """Waits for the oldest queued D2H entry, then for `stream` itself."""
@@ -237,6 +243,7 @@ class HostBuffer:
                 if not self._zero_initialized[p]:
                     self._tensors[p].zero_()
                     self._zero_initialized[p] = True
+                self._dirty[p] = True
         bnd = _none_to_empty(pid, boundaries, self.num_parts)
         with torch.cuda.stream(stream):
             _C.scatter_partitions(pid, gpu_source, self._tensors, bnd)
@@ -245,15 +252,88 @@ class HostBuffer:
     # ------------------------------------------------------------- utilities
 
     def initialize_zeros(self, lazy: bool = False) -> None:
+        """Every partition becomes zero: now, or (lazy) when first touched;
+        storage copies of the old values are dropped."""
         if lazy:
             self.release_all()
+            if self._backend is not None:
+                for pid in range(self.num_parts):
+                    self._backend.remove(self._file_id(pid))
             return
         for pid in range(self.num_parts):
             self.allocate(pid).zero_()
             self._zero_initialized[pid] = True
+            self._dirty[pid] = True
 
     def reset(self) -> None:
         self.initialize_zeros()
 
+    # ------------------------------------------------- host <-> storage files
+
+    def attach_backend(self, backend) -> None:
+        """Gives the buffer a storage backend after construction (the
+        trainer sets up the storage tier only when host memory is short)."""
+        self._backend = backend
+
+    def _file_id(self, pid: int) -> str:
+        return f"{self._file_prefix}_p{pid}"
+
+    def _require_backend(self, what: str):
+        if self._backend is None:
+            raise RuntimeError(f"HostBuffer.{what}: no storage backend")
+        return self._backend
+
     def storage_exists(self, pid: int) -> bool:
-        return False
+        """Whether partition pid has a copy in storage."""
+        return self._backend is not None and self._backend.exists(self._file_id(pid))
+
+    def ensure_storage_copy(self, pid: int) -> None:
+        """Writes a resident partition to storage unless an up-to-date copy
+        exists there (the reference skips the write whenever any copy exists,
+        which would drop rows that changed since it was written)."""
+        if self._backend is None:
+            return
+        if self.storage_exists(pid) and not (self.is_allocated(pid) and self._dirty[pid]):
+            return
+        if not self.is_allocated(pid):
+            raise RuntimeError(f"HostBuffer partition {pid} is neither resident nor in storage")
+        self.cpu_to_storage(pid)
+
+    def _pids(self, pid: Optional[int]) -> List[int]:
+        return list(range(self.num_parts)) if pid is None else [pid]
+
+    def storage_to_cpu(self, pid: Optional[int] = None) -> None:
+        """Loads partition pid (all partitions with a storage copy, when pid is
+        None) from storage into host memory, allocating it again if it was
+        released.  The reads run in parallel; returns when they are done."""
+        backend = self._require_backend("storage_to_cpu")
+        pids = self._pids(pid)
+        if pid is None:
+            pids = [p for p in pids if self.storage_exists(p)]
+        handles = [backend.host_read(self._file_id(p), self.allocate(p)) for p in pids]
+        for h in handles:
+            backend.wait(h)
+        for p in pids:
+            self._zero_initialized[p] = True
+            self._dirty[p] = False
+
+    def cpu_to_storage(self, pid: Optional[int] = None) -> None:
+        """Writes partition pid (every partition, when pid is None) to storage;
+        returns when the writes are done.  Host memory is kept."""
+        backend = self._require_backend("cpu_to_storage")
+        pids = self._pids(pid)
+        handles = [backend.host_write(self.allocate(p), self._file_id(p)) for p in pids]
+        for h in handles:
+            backend.wait(h)
+        for p in pids:
+            self._dirty[p] = False
+
+    def async_bypass_to_storage(self, pid: int, gpu_data: Tensor,
+                                stream: torch.cuda.Stream) -> None:
+        """Writes a partition's device rows straight to storage, without a
+        resident host copy (the reference's GPUDirect bypass,
+        grinnder/buffer/host.py:392-405): ordered after the current stream's
+        work, on `stream`, complete on return."""
+        backend = self._require_backend("async_bypass_to_storage")
+        stream.wait_stream(torch.cuda.current_stream(gpu_data.device))
+        backend.gpu_write(gpu_data, self._file_id(pid), stream)

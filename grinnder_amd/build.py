@@ -25,6 +25,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 SOURCES = [
     "status.cpp",
     "graph_prep.cpp",
+    "io_engine.cpp",
     "transfer.hip",
     "aggregate.hip",
     "gat.hip",

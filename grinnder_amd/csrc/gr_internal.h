@@ -23,6 +23,9 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Clears the last error message of this thread.
 void clear_error();
 
+// The last error message of this thread ("" if none).
+const char* last_error_cstr();
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace gr

@@ -156,6 +156,19 @@ def _reorder_graph_payload(x: Any, y: Tensor, train_mask: Tensor, val_mask: Tens
     return x, y[perm], train_mask[perm], val_mask[perm], test_mask[perm]
 
 
+def _store_adjacency(backend, adj_csr) -> None:
+    """With a storage backend, each partition's CSR is also written to
+    storage as adj_rowptr_p{pid}, adj_col_p{pid}, adj_val_p{pid} (raw int64 /
+    fp32; grinnder/data/partition.py:373-379); the graph keeps them in RAM."""
+    if backend is None:
+        return
+    for pid, (rp, c, v) in enumerate(adj_csr):
+        backend.host_write(rp.contiguous(), f"adj_rowptr_p{pid}", async_=False)
+        backend.host_write(c.contiguous(), f"adj_col_p{pid}", async_=False)
+        if v is not None:
+            backend.host_write(v.contiguous(), f"adj_val_p{pid}", async_=False)
+
+
 def _cache_matches(cache: Dict[str, Any], *, num_nodes: int, num_edges: int, num_parts: int,
                    partitioner: str) -> bool:
     return (cache.get("version") == PARTITION_CACHE_VERSION
@@ -170,8 +183,6 @@ def build_partitioned_graph(edge_index: Tensor, x: Any, y: Tensor, train_mask: T
                             backend=None, cache_path: Optional[Union[str, Path]] = None,
                             save_cache: bool = True) -> PartitionedGraph:
     """Partitions a graph and builds every partition's adjacency and boundaries."""
-    if backend is not None:
-        raise NotImplementedError("the NVMe storage backend is outside this package's scope")
     num_nodes = int(x.size(0))
     input_num_edges = int(edge_index.size(1))
 
@@ -182,6 +193,7 @@ def build_partitioned_graph(edge_index: Tensor, x: Any, y: Tensor, train_mask: T
             perm = cache["perm"]
             x, y, train_mask, val_mask, test_mask = _reorder_graph_payload(
                 x, y, train_mask, val_mask, test_mask, perm)
+            _store_adjacency(backend, cache["adj_csr"])
             return PartitionedGraph(
                 num_nodes=cache["num_nodes"], num_edges=cache["num_edges"],
                 num_parts=cache["num_parts"], partition_sizes=cache["partition_sizes"],
@@ -224,6 +236,7 @@ def build_partitioned_graph(edge_index: Tensor, x: Any, y: Tensor, train_mask: T
         expanded_sizes.append(expanded)
         partition_sizes.append(batch)
 
+    _store_adjacency(backend, adj_csr)
     graph_num_edges = int(edge_index.size(1))
     if cache_path is not None and save_cache:
         path = Path(cache_path)

@@ -178,6 +178,7 @@ class ProjectedLayers:
         self._out_room = False
         self._wpad = {}
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
+                or self.cache is not None
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
             self._x0double = False
             self._drop_prefetch()

@@ -21,9 +21,12 @@ plain full-graph forward/backward.  Here its inputs (features, labels, masks,
 adjacency plans) stay resident in HBM across epochs.
 
 Differences by design: host buffers are pinned so halo traffic moves by
-device kernels; waits are per stream, not device-wide; the NVMe storage tier
-and its partition-LRU cache are out of scope (every layer stays in host RAM,
-which is what the reference's 'auto' cache resolves to when it fits).
+device kernels; waits are per stream, not device-wide.  The storage tier
+(grinnder mode, trainer.py:73-160) is set up only when the host buffers do
+not fit the host-memory budget or a cache mode is asked for: then a
+PartitionCache keeps layers (lru_layer) or dependency sets of partitions
+(partition_lru) in host memory and the rest in files under
+config.storage_dir, and the layers run with the reference's data movement.
 
 Projected layers (config.project_first = 'auto', planned per epoch against
 free HBM; 'off' keeps the reference's data movement):
@@ -124,10 +127,6 @@ class Trainer(ProjectedLayers):
             raise ValueError(f"unknown mode {config.mode!r}")
         if config.cache_mode not in ("auto", "lru_layer", "partition_lru"):
             raise ValueError(f"Unsupported cache mode {config.cache_mode!r}")
-        if config.cache_mode == "partition_lru":
-            raise NotImplementedError(
-                "cache_mode='partition_lru' needs the NVMe storage tier, which is outside "
-                "this package's scope")
         if config.pool_size < 1:
             raise ValueError("pool_size must be >= 1")
         self.model = model
@@ -150,7 +149,12 @@ class Trainer(ProjectedLayers):
             raise ValueError("layer_dims() must have num_layers + 1 entries")
         L, P = model.num_layers, graph.num_parts
         self.streams = StreamManager(pool_size=config.pool_size, device=config.device)
-        self._fast = graph.num_parts == 1 and partition_range is None
+        # One partition runs the reference's full-graph fast path, except
+        # under the partition-wise storage cache (trainer.py:148-160).
+        self._fast = (graph.num_parts == 1 and partition_range is None
+                      and not (config.mode == "grinnder"
+                               and config.cache_mode == "partition_lru"))
+        self.backend = None
 
         self.host_features: List[HostBuffer] = []
         self.host_gradients: List[Optional[HostBuffer]] = [None]
@@ -176,14 +180,93 @@ class Trainer(ProjectedLayers):
             for l in range(1, L):
                 self.device_gradients.append(DeviceBuffer(P, graph.partition_sizes, dims[l],
                                                           device=config.device))
+            self._setup_storage()
             for pid in range(P):
                 feats = graph.partition_features(pid)
                 self.host_features[0][pid].copy_(feats)
                 del feats
+                if self._uses_partition_lru():
+                    # Inputs wait in storage until a gather needs them.
+                    self.host_features[0].cpu_to_storage(pid)
+                    self.host_features[0].release(pid)
 
     # ------------------------------------------------------------ public API
 
+    # ------------------------------------------------------- storage tier
+
+    def _setup_storage(self) -> None:
+        """The storage tier (grinnder mode): a StorageBackend under
+        config.storage_dir and a PartitionCache over the host buffers.  With
+        cache_mode 'auto' it is set up only when the host buffers of every
+        layer do not fit the host-memory budget (host_memory_budget_gb, or the
+        available memory), less the graph's resident metadata and the safety
+        margin; when they fit, every layer stays in host memory, which is
+        what the reference's lru_layer cache does without evicting."""
+        from grinnder_amd.cache.partition_cache import PartitionCache, fixed_resident_bytes
+        from grinnder_amd.utils import get_available_host_memory
+
+        cfg, g = self.config, self.graph
+        if cfg.mode != "grinnder":
+            return
+        fixed = fixed_resident_bytes(g)
+        margin = int(cfg.runtime_safety_margin_gb * (1 << 30))
+        if cfg.cache_mode == "auto":
+            budget = (int(cfg.host_memory_budget_gb * (1 << 30)) if cfg.host_memory_budget_gb > 0
+                      else get_available_host_memory())
+            need = sum(b.total_nbytes for b in self.host_features)
+            need += sum(b.total_nbytes for b in self.host_gradients if b is not None)
+            if need <= budget - fixed - margin:
+                return
+        from grinnder_amd.storage.backend import StorageBackend
+
+        self.backend = StorageBackend(cfg.storage_dir)
+        for buf in self.host_features + [b for b in self.host_gradients if b is not None]:
+            buf.attach_backend(self.backend)
+        deps = [{p} | {q for q, b in enumerate(bnd) if q != p and b is not None and b.numel()}
+                for p, bnd in enumerate(g.boundaries)]
+        self.cache = PartitionCache(
+            num_parts=g.num_parts, num_layers=self.model.num_layers,
+            layer_dims=self.model.layer_dims(), num_nodes=g.num_nodes,
+            host_buffers=self.host_features, grad_buffers=self.host_gradients,
+            backend=self.backend, mode=cfg.cache_mode,
+            host_memory_budget_gb=cfg.host_memory_budget_gb, fixed_resident_bytes=fixed,
+            safety_margin_bytes=margin, dependency_sets=deps)
+
+    def _uses_partition_lru(self) -> bool:
+        return self.cache is not None and self.cache.mode == "partition_lru"
+
+    def _cache_layer(self, layer: int) -> None:
+        """lru_layer: the whole layer resident before its gathers."""
+        if self.cache is not None and self.cache.mode == "lru_layer":
+            self.cache.ensure_in_host(layer)
+
+    def _spill_output(self, layer: int, pid: int) -> None:
+        """partition_lru: a forward output partition goes to storage once its
+        D2H is done (the reference writes it from the GPU directly,
+        trainer.py:549-560), so host memory holds at most pool_size of them."""
+        if self._uses_partition_lru():
+            self.host_features[layer].cpu_to_storage(pid)
+            self.host_features[layer].release(pid)
+
+    def _gradient_partition_resident(self, layer: int, pid: int) -> None:
+        """partition_lru: a gradient partition flushed by the layer above is
+        loaded back for its upload, or zeroed if it has no copy (trainer.py:266-274)."""
+        buf = self.host_gradients[layer]
+        if buf is None or buf.is_allocated(pid) or not self._uses_partition_lru():
+            return
+        if buf.storage_exists(pid):
+            buf.storage_to_cpu(pid)
+        else:
+            buf.zero_partition(pid)
+
     def reset_epoch(self) -> None:
+        if self._uses_partition_lru():
+            self.cache.reset()
+            for buf in self.host_features[1:]:
+                buf.release_all()
+            for buf in self.host_gradients:
+                if buf is not None:
+                    buf.release_all()
         # Host activation buffers of layers >= 1 are fully overwritten by the
         # forward D2H fills and gradient buffers are zeroed before each
         # backward phase, so neither needs clearing here.
@@ -322,6 +405,12 @@ class Trainer(ProjectedLayers):
     # ------------------------------------------------- partitioned helpers
 
     def _gather(self, layer: int, pid: int, stream: torch.cuda.Stream) -> None:
+        if self._uses_partition_lru():
+            # The partitions this gather reads, made resident first (loaded
+            # from storage; least recently used others evicted).  Earlier
+            # gathers reading evicted partitions were waited for already.
+            self.cache.ensure_dependencies_in_host(layer, pid,
+                                                   boundaries=self.graph.boundaries[pid])
         with torch.cuda.stream(self.streams.compute):
             self.device_features[layer].async_gather(
                 pid, self.host_features[layer], self.graph.boundaries[pid], stream)
@@ -330,6 +419,7 @@ class Trainer(ProjectedLayers):
         buf = self.device_gradients[layer]
         if buf is None or self.host_gradients[layer] is None:
             return
+        self._gradient_partition_resident(layer, pid)
         with torch.cuda.stream(self.streams.compute):
             buf.allocate(pid)
             self.host_gradients[layer].async_upload(pid, buf[pid], stream)
@@ -394,6 +484,7 @@ class Trainer(ProjectedLayers):
                     self._device_forward(layer, pid, keep=True)
             return
         if not projected:
+            self._cache_layer(layer)
             self._gather(layer, pids[0], s.h2d[0])
         for i, pid in enumerate(pids):
             k = i % pool
@@ -418,15 +509,20 @@ class Trainer(ProjectedLayers):
                     prev, pk = pids[i - 1], (i - 1) % pool
                     self.host_features[layer + 1].d2h_synchronize(s.d2h[pk])
                     self._free(self.activations[layer][prev])
+                    self._spill_output(layer + 1, prev)
             if pool == 1:
                 self.host_features[layer + 1].d2h_synchronize(s.d2h[0])
                 self._free(self.activations[layer][pid])
+                self._spill_output(layer + 1, pid)
                 if not projected and i + 1 < len(pids):
                     self._gather(layer, pids[i + 1], s.h2d[0])
         if pool > 1:
             last = (len(pids) - 1) % pool
             self.host_features[layer + 1].d2h_synchronize(s.d2h[last])
             self._free(self.activations[layer][pids[-1]])
+            self._spill_output(layer + 1, pids[-1])
+        if self.cache is not None:
+            self.cache.on_layer_complete(layer)
 
     # ---------------------------------------------------------------- loss
 
@@ -443,9 +539,14 @@ class Trainer(ProjectedLayers):
 
         def upload(pid: int, stream) -> None:
             act = self.activations[last][pid]
+            if self._uses_partition_lru():
+                self.host_features[-1].storage_to_cpu(pid)
             with torch.cuda.stream(s.compute):
                 act.untyped_storage().resize_(act.numel() * act.element_size())
             self.host_features[-1].async_upload(pid, act, stream)
+
+        if self.cache is not None and self.cache.mode == "lru_layer":
+            self.cache.ensure_in_host(self.model.num_layers)
 
         kept = last in self._keep and last in self._graphs
         on_device = not kept and self._logits_on_device()
@@ -540,9 +641,11 @@ class Trainer(ProjectedLayers):
         if not pids:
             return
         if self.host_gradients[layer] is not None:
-            self.host_gradients[layer].initialize_zeros()
+            # partition_lru: partitions are zeroed when first touched.
+            self.host_gradients[layer].initialize_zeros(lazy=self._uses_partition_lru())
         regather = self._regathers(layer)
         if regather:
+            self._cache_layer(layer)
             self._gather(layer, pids[0], s.act_h2d[0])
         if upload_grad:
             self._upload_grad(layer + 1, pids[0], s.h2d[0])
@@ -588,3 +691,8 @@ class Trainer(ProjectedLayers):
             while hg.d2h_queued > 0:
                 hg.d2h_wait_oldest()
             self._scatter_stream().synchronize()
+        if self.cache is not None and (layer < self.model.num_layers - 1
+                                       or self._uses_partition_lru()):
+            # The layer's gradient write-back buffer goes to storage
+            # (trainer.py:889-890, :1137-1138).
+            self.cache.on_backward_layer_complete(layer)

@@ -30,3 +30,29 @@ def compute_micro_f1(pred: Tensor, target: Tensor, mask: Optional[Tensor] = None
     if target.numel() == 0:
         return 0.0
     return (pred == target.to(pred.device)).float().mean().item()
+
+
+def ensure_dir(path: str) -> str:
+    """Creates `path` (and parents) if missing; returns it."""
+    import os
+
+    os.makedirs(path, exist_ok=True)
+    return path
+
+
+def get_available_host_memory() -> int:
+    """Bytes of host memory available to new allocations: MemAvailable from
+    /proc/meminfo (grinnder/utils.py:47-64), else psutil, else 0."""
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemAvailable:"):
+                    return int(line.split()[1]) * 1024
+    except (OSError, ValueError):
+        pass
+    try:
+        import psutil
+
+        return int(psutil.virtual_memory().available)
+    except ImportError:
+        return 0

@@ -482,6 +482,43 @@ int gr_gat_backward_dst(const int32_t* units, int64_t n_units,
                         int64_t n_slots, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Host <-> storage I/O (grinnder._C.IoUringEngine)                          */
+/* ------------------------------------------------------------------------ */
+
+/* Asynchronous file engine replacing IoUringEngine (csrc/cpu/
+ * io_uring_engine.cpp:15-245; constructor :227-230).  liburing is absent, so
+ * requests run on `threads` worker threads with pread/pwrite, each request
+ * cut into 8 MiB chunks processed in parallel.  Host only. */
+int gr_io_create(int32_t threads, void** engine);
+
+/* Waits for every request, then frees the engine (~IoUringEngineImpl,
+ * io_uring_engine.cpp:25-28).  Reports the first failed request. */
+int gr_io_destroy(void* engine);
+
+/* submit_read / submit_write (io_uring_engine.cpp:32-108): nbytes at
+ * file `offset` into / from `buf`, which must stay valid until the request
+ * is waited for.  A write creates or truncates the file to offset + nbytes
+ * (the reference opens with O_TRUNC).  Returns the request's handle.  Open
+ * failures are reported here; I/O failures by gr_io_wait. */
+int gr_io_submit(void* engine, int32_t write, const char* path, void* buf,
+                 int64_t offset, int64_t nbytes, int64_t* handle);
+
+/* wait (io_uring_engine.cpp:110-136): blocks until the request is done and
+ * forgets the handle; a failed or short transfer is returned as an error
+ * (the reference throws). */
+int gr_io_wait(void* engine, int64_t handle);
+
+/* wait_all (io_uring_engine.cpp:138-160). */
+int gr_io_wait_all(void* engine);
+
+/* poll (io_uring_engine.cpp:162-178): *done = 1 once the request finished
+ * (it still has to be waited for). */
+int gr_io_poll(void* engine, int64_t handle, int32_t* done);
+
+/* pending (io_uring_engine.cpp:180-187): requests submitted and not done. */
+int gr_io_pending(void* engine, int64_t* count);
+
+/* ------------------------------------------------------------------------ */
 /* Synthetic inputs (no reference counterpart)                               */
 /* ------------------------------------------------------------------------ */
 
