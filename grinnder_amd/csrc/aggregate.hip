@@ -697,6 +697,119 @@ inline unsigned final_blocks(int64_t dim) {
   return (unsigned)((dim + kFinalCols - 1) / kFinalCols);
 }
 
+// Narrow rows (at most G * VEC floats, G <= 16): 64 / G whole rows per
+// wavefront, one per group of G lanes, each lane owning VEC consecutive
+// floats of its row.  A wavefront per row would spend most of its time in
+// the dependent loads that start a row (unit, column ids, first rows) for a
+// handful of short gathers; here 64 / G rows share that latency.  Each group
+// keeps U of its row's edges in flight; the plan lists whole rows by length
+// class, so the groups of a wavefront run similar trip counts.  All lanes of
+// a group read the same column id and weight (one broadcast load).  A row's
+// edges are summed in edge order; the result is deterministic.
+template <int VEC, int G, int U>
+__global__ __launch_bounds__(256) void aggregate_rows(
+    const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
+    const float* __restrict__ val, const float* __restrict__ x, int64_t ldx,
+    float* __restrict__ y, int64_t ldy, const float* __restrict__ bias, int dim,
+    const int32_t* __restrict__ orow) {
+  constexpr int RPW = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane / G;
+  const int sub = lane % G;
+  const int64_t wid =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t u = wid * RPW + grp;
+  if (wid * RPW >= n_units) return;
+  // When G does not divide 64 the last 64 % G lanes form no group.
+  const bool active = grp < RPW && u < n_units;
+  const int4 w = active ? units[u] : make_int4(0, 0, 0, -1);
+  const int foff = sub * VEC;
+  const bool fvalid = foff < dim;
+  const int fld = fvalid ? foff : dim - VEC;
+
+  float acc[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) acc[j] = 0.f;
+  int e = w.y;
+  const int end = w.z;
+  for (; e + U <= end; e += U) {
+    int c[U];
+    float v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      c[k] = idx[e + k];
+      v[k] = val[e + k];
+    }
+    float r[U][VEC];
+#pragma unroll
+    for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld, r[k]);
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v[k], r[k][j], acc[j]);
+  }
+  if (e < end) {
+    // Fewer than U edges left: the missing ones re-read the last edge's row
+    // (in bounds, cached) with weight 0.
+    int c[U];
+    float v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int ee = min(e + k, end - 1);
+      c[k] = idx[ee];
+      v[k] = e + k < end ? val[ee] : 0.f;
+    }
+    float r[U][VEC];
+#pragma unroll
+    for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld, r[k]);
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v[k], r[k][j], acc[j]);
+  }
+  if (!active || !fvalid) return;
+  float* out = y + (int64_t)(orow != nullptr ? orow[w.x] : w.x) * ldy + foff;
+  if (orow != nullptr) {
+    float o[VEC];
+    load_vec<VEC>(out, o);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc[j] = o[j] + acc[j];
+  } else if (bias != nullptr) {
+    float b[VEC];
+    load_vec<VEC>(bias + foff, b);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc[j] += b[j];
+  }
+  store_vec<VEC>(out, acc);
+}
+
+template <int VEC, int G>
+hipError_t launch_rows(const int4* units, int64_t n_units, const int32_t* idx, const float* val,
+                       const float* x, int64_t ldx, float* y, int64_t ldy, const float* bias,
+                       int dim, const int32_t* orow, hipStream_t s) {
+  constexpr int RPW = 64 / G;
+  const int64_t waves = (n_units + RPW - 1) / RPW;
+  const int64_t blocks = (waves + 3) / 4;
+  hipLaunchKernelGGL((aggregate_rows<VEC, G, 8>), dim3((unsigned)blocks), dim3(256), 0, s, units,
+                     n_units, idx, val, x, ldx, y, ldy, bias, dim, orow);
+  return hipGetLastError();
+}
+
+// Whole rows of a narrow pass: groups of exactly `chunks` lanes (any count
+// up to 16; the kernel needs no cross-lane reduction), so 64 / chunks rows
+// share a wavefront (12 for 20-float rows).
+template <int VEC, int G = 1>
+hipError_t dispatch_rows(int chunks, const int4* units, int64_t n_units, const int32_t* idx,
+                         const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
+                         const float* bias, int dim, const int32_t* orow, hipStream_t s) {
+  if constexpr (G < 16) {
+    if (chunks > G)
+      return dispatch_rows<VEC, G + 1>(chunks, units, n_units, idx, val, x, ldx, y, ldy, bias,
+                                       dim, orow, s);
+  }
+  return launch_rows<VEC, G>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, orow, s);
+}
+
 template <int VEC, int G, int NCH>
 hipError_t launch_units(const int4* units, int64_t n_units, const int32_t* idx,
                         const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
@@ -950,17 +1063,37 @@ int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t
   const int chunks = (d + vec - 1) / vec;
   GR_REQUIRE(chunks <= 256, "gcn_aggregate: dim %d too wide for vector width %d", d, vec);
   const int4* u4 = reinterpret_cast<const int4*>(units);
-  hipError_t err;
-  if (vec == 4)
-    err = dispatch_g<4>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, orow,
-                        s);
-  else if (vec == 2)
-    err = dispatch_g<2>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, orow,
-                        s);
-  else
-    err = dispatch_g<1>(chunks, u4, n_units, idx, val, x, ldx, y, ldy, bias, d, workspace, orow,
-                        s);
-  GR_HIP_CHECK(err);
+  // Narrow widths: the plan's n_slots split units come first (gr_spmm_plan)
+  // and run one per wavefront; the whole rows after them run several per
+  // wavefront (aggregate_rows).  Unlike the attention kernels, a group here
+  // takes a long row in one pass with U edges in flight, which measured
+  // faster than handing long rows back to aggregate_units.
+  const bool narrow = chunks <= 16;
+  const int64_t n_wide = narrow ? std::min(n_slots, n_units) : n_units;
+  hipError_t err = hipSuccess;
+  if (n_wide > 0) {
+    if (vec == 4)
+      err = dispatch_g<4>(chunks, u4, n_wide, idx, val, x, ldx, y, ldy, bias, d, workspace,
+                          orow, s);
+    else if (vec == 2)
+      err = dispatch_g<2>(chunks, u4, n_wide, idx, val, x, ldx, y, ldy, bias, d, workspace,
+                          orow, s);
+    else
+      err = dispatch_g<1>(chunks, u4, n_wide, idx, val, x, ldx, y, ldy, bias, d, workspace,
+                          orow, s);
+    GR_HIP_CHECK(err);
+  }
+  if (narrow && n_units > n_wide) {
+    const int4* rows = u4 + n_wide;
+    const int64_t n_rows = n_units - n_wide;
+    if (vec == 4)
+      err = dispatch_rows<4>(chunks, rows, n_rows, idx, val, x, ldx, y, ldy, bias, d, orow, s);
+    else if (vec == 2)
+      err = dispatch_rows<2>(chunks, rows, n_rows, idx, val, x, ldx, y, ldy, bias, d, orow, s);
+    else
+      err = dispatch_rows<1>(chunks, rows, n_rows, idx, val, x, ldx, y, ldy, bias, d, orow, s);
+    GR_HIP_CHECK(err);
+  }
   if (n_fix > 0) {
     GR_REQUIRE(n_fix <= INT32_MAX, "gcn_aggregate: too many split rows");
     const int threads = d >= 256 ? 256 : ((d + 63) / 64) * 64;

@@ -418,7 +418,8 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
     const float* __restrict__ hs, int64_t ldh, const float* __restrict__ s,
     const float* __restrict__ d, int C, const float* __restrict__ bias, float* __restrict__ m,
     float* __restrict__ den, float* __restrict__ alpha, float* __restrict__ o,
-    float* __restrict__ y, int64_t ldy, float* __restrict__ ws, int64_t ws_stride) {
+    float* __restrict__ y, int64_t ldy, float* __restrict__ ws, int64_t ws_stride,
+    int min_len) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int64_t wid = wave_id();
@@ -428,6 +429,8 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
   const int sub = (EPI == 1) ? lane : lane % G;
   const int64_t i = w.x;
   const int len = w.z - w.y;
+  // Whole rows shorter than min_len are gat_fwd_rows' work.
+  if (w.w < 0 && len < min_len) return;
 
   int foff[NCH], fld[NCH];
   bool fvalid[NCH];
@@ -876,7 +879,7 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
     const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
     const float* __restrict__ alpha, const float* __restrict__ cdot,
     const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
-    float* __restrict__ gt, float* __restrict__ ws) {
+    float* __restrict__ gt, float* __restrict__ ws, int min_len) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int slot = (EPI == 1) ? 0 : lane / G;
@@ -884,6 +887,8 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
   const int64_t wid = wave_id();
   if (wid >= n_units) return;
   const int4 w = units[wid];
+  // Whole columns shorter than min_len are gat_bwd_src_rows' work.
+  if (w.w < 0 && w.z - w.y < min_len) return;
   const int64_t j = w.x;
 
   int foff[NCH], fld[NCH];
@@ -1001,6 +1006,263 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
       if (fvalid[ch]) st<VEC>(p + foff[ch], acc[ch]);
     if (lane == 0) p[c4] = dsl;
   }
+}
+
+// ------------------------------------------------- narrow single-head rows --
+//
+// One head of at most G * VEC channels (G <= 16): 64 / G whole plan units
+// per wavefront, one per group of G lanes, each lane owning VEC channels.  A
+// wavefront per unit would spend most of its time in the dependent loads
+// that start a unit, for a handful of short gathers (C5's 20-wide layer has
+// 13 edges per destination row and 4.4 per source column); here 64 / G
+// units share that latency.  The members of a wavefront are stepped to the
+// longest member's length, so the group reductions (DPP within 16-lane rows)
+// and the shuffles always run with every lane active; loads and stores of
+// edges past a member's end are masked.  The plan lists whole units by
+// length class, so the members have similar lengths.
+
+// Longest unit of the wavefront (every lane gets it).
+__device__ __forceinline__ int wave_longest(int len) {
+  return (int)gr_wave::wave_max((float)len);
+}
+
+// Forward: softmax statistics over the row, then the aggregation
+// O_i = sum_e alpha_e Hs[col_e]; alpha, m, den and O as gat_fwd_fused writes
+// them for a whole row.  Lane sub of a group holds edges sub, G + sub, ...
+// of at most R * G: their column ids and logits are loaded once and kept in
+// registers, so a row costs one dependent index load, one logit load and one
+// round of U-wide row gathers per G edges.  Longer rows are left to
+// gat_fwd_fused.
+template <int VEC, int G, int R, int U>
+__global__ __launch_bounds__(256) void gat_fwd_rows(
+    const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
+    const float* __restrict__ hs, int64_t ldh, const float* __restrict__ s,
+    const float* __restrict__ d, int C, const float* __restrict__ bias, float* __restrict__ m,
+    float* __restrict__ den, float* __restrict__ alpha, float* __restrict__ o,
+    float* __restrict__ y, int64_t ldy) {
+  constexpr int RPW = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane / G, sub = lane % G, base = grp * G;
+  const int64_t wid = wave_id();
+  if (wid * RPW >= n_units) return;
+  const int64_t u = wid * RPW + grp;
+  const int4 wu = u < n_units ? units[u] : make_int4(0, 0, 0, -1);
+  const bool active = u < n_units && wu.z - wu.y <= R * G;
+  const int4 w = active ? wu : make_int4(0, 0, 0, -1);
+  const int64_t i = w.x;
+  const int len = w.z - w.y;
+  const int steps = wave_longest(len);
+  const int foff = sub * VEC;
+  const bool fvalid = foff < C;
+  const int fld = fvalid ? foff : C - VEC;
+  const float di = len > 0 ? d[i] : 0.f;
+
+  int cr[R];
+  float vr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) cr[r] = r * G + sub < len ? idx[w.y + r * G + sub] : 0;
+  // The first U row gathers need only column ids: they go out before the
+  // logits, so the two loads' latencies overlap.
+  float rp[U][VEC];
+#pragma unroll
+  for (int q = 0; q < U; ++q) {
+    const int c = __shfl(cr[0], base + q, 64);
+    if (q < len) {
+      ld<VEC>(hs + (int64_t)c * ldh + fld, rp[q]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) rp[q][v] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    vr[r] = r * G + sub < len ? leaky(s[cr[r]] + di) : -FLT_MAX;
+
+  // Pass 1: max, then the sum of exp(v - max).
+  float mx = vr[0];
+#pragma unroll
+  for (int r = 1; r < R; ++r) mx = fmaxf(mx, vr[r]);
+  mx = gr_wave::group_max<G>(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r * G + sub < len) sum += expf(vr[r] - mx);
+  sum = gr_wave::group_sum<G>(sum);
+  const float dn = sum + 1e-16f;
+
+  // Pass 2: the group takes edge k + q's column and weight from lane q.
+  float acc[VEC];
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) acc[q] = 0.f;
+  auto gather = [&](int k, int cl, float al) {
+    const int n = min(G, steps - k);
+    for (int q0 = 0; q0 < n; q0 += U) {
+      int c[U];
+      float a[U];
+#pragma unroll
+      for (int q = 0; q < U; ++q) {
+        const int src = base + min(q0 + q, G - 1);
+        c[q] = __shfl(cl, src, 64);
+        const float aq = __shfl(al, src, 64);
+        a[q] = k + q0 + q < len ? aq : 0.f;
+      }
+      float rr[U][VEC];
+#pragma unroll
+      for (int q = 0; q < U; ++q) {
+        if (k + q0 == 0) {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) rr[q][v] = rp[q][v];
+        } else if (k + q0 + q < len) {
+          ld<VEC>(hs + (int64_t)c[q] * ldh + fld, rr[q]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) rr[q][v] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < U; ++q)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = fmaf(a[q], rr[q][v], acc[v]);
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int k = r * G;
+    if (k >= steps) break;
+    const bool ok = k + sub < len;
+    const float al = ok ? expf(vr[r] - mx) / dn : 0.f;
+    gather(k, cr[r], al);
+    if (ok) alpha[w.y + k + sub] = al;
+  }
+
+  if (!active) return;
+  if (sub == 0) {
+    m[i] = len > 0 ? mx : 0.f;
+    den[i] = len > 0 ? dn : 1.f;
+  }
+  if (!fvalid) return;
+  st<VEC>(o + i * C + foff, acc);
+  if (y != nullptr) {
+    float b[VEC];
+    if (bias != nullptr) {
+      ld<VEC>(bias + foff, b);
+    } else {
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) b[q] = 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) b[q] += acc[q];
+    st<VEC>(y + i * ldy + foff, b);
+  }
+}
+
+// Backward, column-parallel (CSC) over source rows j: for each edge (i, j),
+// g_alpha = <GO_i, Hs_j> (a group sum), g_e = alpha (g_alpha - c_i),
+// ds_j += slope * g_e, dHs_j += alpha GO_i; the destination part of g_t is
+// collected in the lane that owns the edge and stored at its CSR position.
+// Writes dHs_j = acc + ds_j att_src and ds_j, as gat_bwd_src_h1 does for a
+// whole column.  Columns of more than max_len edges are left to
+// gat_bwd_src_h1.
+template <int VEC, int G, int U>
+__global__ __launch_bounds__(256) void gat_bwd_src_rows(
+    const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
+    const int32_t* __restrict__ perm, const float* __restrict__ hs, int64_t ldh,
+    const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
+    const float* __restrict__ alpha, const float* __restrict__ cdot,
+    const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
+    float* __restrict__ gt, int max_len) {
+  constexpr int RPW = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane / G, sub = lane % G, base = grp * G;
+  const int64_t wid = wave_id();
+  if (wid * RPW >= n_units) return;
+  const int64_t u = wid * RPW + grp;
+  const int4 wu = u < n_units ? units[u] : make_int4(0, 0, 0, -1);
+  const bool active = u < n_units && wu.z - wu.y <= max_len;
+  const int4 w = active ? wu : make_int4(0, 0, 0, -1);
+  const int64_t j = w.x;
+  const int len = w.z - w.y;
+  const int steps = wave_longest(len);
+  const int foff = sub * VEC;
+  const bool fvalid = foff < C;
+  const int fld = fvalid ? foff : C - VEC;
+
+  float hsj[VEC];
+  if (active && fvalid) {
+    ld<VEC>(hs + j * ldh + fld, hsj);
+  } else {
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) hsj[q] = 0.f;
+  }
+  const float sj = active ? s[j] : 0.f;
+  float acc[VEC];
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) acc[q] = 0.f;
+  float dsl = 0.f;
+
+  for (int k = 0; k < steps; k += G) {
+    const int t = k + sub;
+    const bool ok = t < len;
+    int il = 0, pl = 0;
+    float al = 0.f, dl = 0.f, cl = 0.f;
+    if (ok) {
+      il = row_idx[w.y + t];
+      pl = perm[w.y + t];
+      al = alpha[pl];
+      dl = d[il];
+      cl = cdot[il];
+    }
+    float gtv = 0.f;
+    const int n = min(G, steps - k);
+    for (int q0 = 0; q0 < n; q0 += U) {
+      // The row gathers need only the destination ids: they go out before
+      // the per-edge scalars are shuffled (which waits for their loads).
+      float g[U][VEC];
+#pragma unroll
+      for (int q = 0; q < U; ++q) {
+        const int iq = __shfl(il, base + min(q0 + q, G - 1), 64);
+        if (k + q0 + q < len) {
+          ld<VEC>(go + (int64_t)iq * C + fld, g[q]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) g[q][v] = 0.f;
+        }
+      }
+      float a[U], dv[U], cv[U];
+#pragma unroll
+      for (int q = 0; q < U; ++q) {
+        const int src = base + min(q0 + q, G - 1);
+        a[q] = __shfl(al, src, 64);
+        dv[q] = __shfl(dl, src, 64);
+        cv[q] = __shfl(cl, src, 64);
+      }
+#pragma unroll
+      for (int q = 0; q < U; ++q) {
+        float tdot = 0.f;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) tdot = fmaf(g[q][v], hsj[v], tdot);
+        const float ga = gr_wave::group_sum<G>(tdot);
+        const bool valid = q0 + q < n && k + q0 + q < len;
+        const float ge = valid ? a[q] * (ga - cv[q]) : 0.f;
+        const bool pos = sj + dv[q] > 0.f;
+        dsl += pos ? ge : 0.2f * ge;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = fmaf(valid ? a[q] : 0.f, g[q][v], acc[v]);
+        if (sub == q0 + q) gtv = pos ? 0.f : -0.8f * ge;
+      }
+    }
+    if (ok) gt[pl] = gtv;
+  }
+
+  if (!active) return;
+  if (fvalid) {
+    float av[VEC];
+    ld<VEC>(att_src + foff, av);
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) av[q] = fmaf(dsl, av[q], acc[q]);
+    st<VEC>(dhs + j * C + foff, av);
+  }
+  if (sub == 0) ds[j] = dsl;
 }
 
 // Row-parallel (CSR) pass over destination rows i:
@@ -1285,12 +1547,12 @@ static hipError_t launch_fused(hipStream_t st, const int4* units, int64_t n_unit
                                const int32_t* idx, const float* hs, int64_t ldh, const float* s,
                                const float* d, int C, const float* bias, float* m, float* den,
                                float* alpha, float* o, float* y, int64_t ldy, float* ws,
-                               int64_t ws_stride) {
+                               int64_t ws_stride, int min_len) {
   constexpr int EPI = 64 / G;
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
   hipLaunchKernelGGL((gat_fwd_fused<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha, o, y, ldy,
-                     ws, ws_stride);
+                     ws, ws_stride, min_len);
   return hipGetLastError();
 }
 
@@ -1299,10 +1561,10 @@ static hipError_t dispatch_fused(int chunks, hipStream_t st, const int4* units, 
                                  const int32_t* idx, const float* hs, int64_t ldh,
                                  const float* s, const float* d, int C, const float* bias,
                                  float* m, float* den, float* alpha, float* o, float* y,
-                                 int64_t ldy, float* ws, int64_t ws_stride) {
+                                 int64_t ldy, float* ws, int64_t ws_stride, int min_len = 0) {
 #define GR_FU(G, N)                                                                       \
   return launch_fused<VEC, G, N>(st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, \
-                                 alpha, o, y, ldy, ws, ws_stride)
+                                 alpha, o, y, ldy, ws, ws_stride, min_len)
   if (chunks <= 8) GR_FU(8, 1);
   if (chunks <= 16) GR_FU(16, 1);
   if (chunks <= 32) GR_FU(32, 1);
@@ -1311,6 +1573,20 @@ static hipError_t dispatch_fused(int chunks, hipStream_t st, const int4* units, 
   GR_FU(64, 4);
 #undef GR_FU
 }
+
+template <int VEC>
+static hipError_t launch_fwd_rows(int chunks, hipStream_t st, const int4* units, int64_t n,
+                                  const int32_t* idx, const float* hs, int64_t ldh,
+                                  const float* s, const float* d, int C, const float* bias,
+                                  float* m, float* den, float* alpha, float* o, float* y,
+                                  int64_t ldy);
+
+// Longest whole row gat_fwd_rows takes (R * G of the instance launch_fwd_rows
+// picks for `chunks`).
+constexpr int fwd_rows_max_len(int chunks) { return chunks <= 4 ? 16 : 32; }
+
+// Longest whole column gat_bwd_src_rows takes.
+constexpr int kBwdRowsMaxLen = 32;
 
 extern "C" int gr_gat_forward(const int32_t* units, int64_t n_units, const int32_t* fixups,
                               int64_t n_fix, const int32_t* idx, const float* hs, int64_t ldh,
@@ -1352,7 +1628,28 @@ extern "C" int gr_gat_forward(const int32_t* units, int64_t n_units, const int32
   const int64_t ws_stride = hc4 + 4;
   const int4* u4 = reinterpret_cast<const int4*>(units);
   hipError_t err;
-  if (vec == 4) {
+  if (chunks <= 16) {
+    // Narrow: split rows and long whole rows one per wavefront
+    // (gat_fwd_fused), the other whole rows several per wavefront
+    // (gat_fwd_rows, after the plan's first n_slots units, the split ones).
+    const int64_t n_split = std::min(n_slots, n_units);
+    const int min_len = fwd_rows_max_len(chunks) + 1;
+    if (vec == 4)
+      err = dispatch_fused<4>(chunks, st, u4, n_units, idx, hs, ldh, s, d, C, bias, m, den,
+                              alpha, o, y, ldy, workspace, ws_stride, min_len);
+    else
+      err = dispatch_fused<1>(chunks, st, u4, n_units, idx, hs, ldh, s, d, C, bias, m, den,
+                              alpha, o, y, ldy, workspace, ws_stride, min_len);
+    GR_HIP_CHECK(err);
+    if (n_units > n_split) {
+      if (vec == 4)
+        err = launch_fwd_rows<4>(chunks, st, u4 + n_split, n_units - n_split, idx, hs, ldh, s, d,
+                                 C, bias, m, den, alpha, o, y, ldy);
+      else
+        err = launch_fwd_rows<1>(chunks, st, u4 + n_split, n_units - n_split, idx, hs, ldh, s, d,
+                                 C, bias, m, den, alpha, o, y, ldy);
+    }
+  } else if (vec == 4) {
     err = dispatch_fused<4>(chunks, st, u4, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha,
                             o, y, ldy, workspace, ws_stride);
   } else if (chunks <= 256) {
@@ -1398,12 +1695,12 @@ static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_uni
                                 const int32_t* row_idx, const int32_t* perm, const float* hs,
                                 int64_t ldh, const float* go, const float* s, const float* d,
                                 const float* alpha, const float* cdot, const float* att_src,
-                                int C, float* dhs, float* ds, float* gt, float* ws) {
+                                int C, float* dhs, float* ds, float* gt, float* ws, int min_len) {
   constexpr int EPI = 64 / G;
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
   hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src,
-                     C, dhs, ds, gt, ws);
+                     C, dhs, ds, gt, ws, min_len);
   return hipGetLastError();
 }
 
@@ -1413,10 +1710,10 @@ static hipError_t dispatch_bwd_h1(int chunks, hipStream_t st, const int4* units,
                                   const float* hs, int64_t ldh, const float* go, const float* s,
                                   const float* d, const float* alpha, const float* cdot,
                                   const float* att_src, int C, float* dhs, float* ds, float* gt,
-                                  float* ws) {
+                                  float* ws, int min_len = 0) {
 #define GR_BH(G, N)                                                                      \
   return launch_bwd_h1<VEC, G, N>(st, units, n_units, row_idx, perm, hs, ldh, go, s, d,  \
-                                  alpha, cdot, att_src, C, dhs, ds, gt, ws)
+                                  alpha, cdot, att_src, C, dhs, ds, gt, ws, min_len)
   if (chunks <= 8) GR_BH(8, 1);
   if (chunks <= 16) GR_BH(16, 1);
   if (chunks <= 32) GR_BH(32, 1);
@@ -1424,6 +1721,47 @@ static hipError_t dispatch_bwd_h1(int chunks, hipStream_t st, const int4* units,
   if (chunks <= 128) GR_BH(64, 2);
   GR_BH(64, 4);
 #undef GR_BH
+}
+
+// Narrow single-head units (chunks <= 16 vectors): groups of 4, 8 or 16 lanes.
+template <int VEC>
+static hipError_t launch_fwd_rows(int chunks, hipStream_t st, const int4* units, int64_t n,
+                                  const int32_t* idx, const float* hs, int64_t ldh,
+                                  const float* s, const float* d, int C, const float* bias,
+                                  float* m, float* den, float* alpha, float* o, float* y,
+                                  int64_t ldy) {
+#define GR_FR(G, R, U)                                                                    \
+  static_assert(R * G == fwd_rows_max_len(G), "gat_fwd_rows takes R * G edges");           \
+  hipLaunchKernelGGL((gat_fwd_rows<VEC, G, R, U>),                                          \
+                     dim3(blocks_for((n + 64 / G - 1) / (64 / G))), dim3(256), 0, st, units, n, \
+                     idx, hs, ldh, s, d, C, bias, m, den, alpha, o, y, ldy)
+  if (chunks <= 4) {
+    GR_FR(4, 4, 4);
+  } else if (chunks <= 8) {
+    GR_FR(8, 4, 8);
+  } else {
+    GR_FR(16, 2, 8);
+  }
+#undef GR_FR
+  return hipGetLastError();
+}
+
+template <int VEC>
+static hipError_t launch_bwd_rows(int chunks, hipStream_t st, const int4* units, int64_t n,
+                                  const int32_t* row_idx, const int32_t* perm, const float* hs,
+                                  int64_t ldh, const float* go, const float* s, const float* d,
+                                  const float* alpha, const float* cdot, const float* att_src,
+                                  int C, float* dhs, float* ds, float* gt) {
+#define GR_BR(G)                                                                             \
+  hipLaunchKernelGGL((gat_bwd_src_rows<VEC, G, (G < 8 ? G : 8)>),                            \
+                     dim3(blocks_for((n + 64 / G - 1) / (64 / G))), dim3(256), 0, st, units, n, \
+                     row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, C, dhs, ds, gt, \
+                     kBwdRowsMaxLen)
+  if (chunks <= 4) GR_BR(4);
+  else if (chunks <= 8) GR_BR(8);
+  else GR_BR(16);
+#undef GR_BR
+  return hipGetLastError();
 }
 
 extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const int32_t* fixups,
@@ -1452,24 +1790,35 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   const int H = (int)heads, C = (int)channels;
   hipError_t err;
   const int64_t chunks = (HC + vec - 1) / vec;
-  if (H == 1 && chunks <= 256) {
+  if (H == 1 && chunks <= 16) {
+    // Narrow: split columns and long whole columns one per wavefront
+    // (gat_bwd_src_h1), the other whole columns several per wavefront
+    // (gat_bwd_src_rows, after the plan's first n_slots units).
+    const int64_t n_split = std::min(n_slots, n_units);
+    if (vec == 4)
+      err = dispatch_bwd_h1<4>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
+                               alpha, cdot, att_src, C, dhs, ds, gt, workspace,
+                               kBwdRowsMaxLen + 1);
+    else
+      err = dispatch_bwd_h1<1>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
+                               alpha, cdot, att_src, C, dhs, ds, gt, workspace,
+                               kBwdRowsMaxLen + 1);
+    GR_HIP_CHECK(err);
+    if (n_units > n_split) {
+      if (vec == 4)
+        err = launch_bwd_rows<4>((int)chunks, st, u4 + n_split, n_units - n_split, row_idx, perm,
+                                 hs, ldh, go, s, d, alpha, cdot, att_src, C, dhs, ds, gt);
+      else
+        err = launch_bwd_rows<1>((int)chunks, st, u4 + n_split, n_units - n_split, row_idx, perm,
+                                 hs, ldh, go, s, d, alpha, cdot, att_src, C, dhs, ds, gt);
+    }
+  } else if (H == 1 && chunks <= 256) {
     if (vec == 4)
       err = dispatch_bwd_h1<4>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
                                alpha, cdot, att_src, C, dhs, ds, gt, workspace);
     else
       err = dispatch_bwd_h1<1>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
                                alpha, cdot, att_src, C, dhs, ds, gt, workspace);
-  } else if (H == 1 && chunks <= 32) {
-    // Narrow single-head rows: several edges per wavefront.
-    if (vec == 4) {
-      if (chunks <= 8) err = launch_gat_bwd<4, 1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
-      else if (chunks <= 16) err = launch_gat_bwd<4, 1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
-      else err = launch_gat_bwd<4, 1, 32>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    } else {
-      if (chunks <= 8) err = launch_gat_bwd<1, 1, 8>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
-      else if (chunks <= 16) err = launch_gat_bwd<1, 1, 16>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
-      else err = launch_gat_bwd<1, 1, 32>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
-    }
   } else if (vec == 4) {
     if (nch == 1) err = launch_gat_bwd<4, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
     else if (nch == 2) err = launch_gat_bwd<4, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);

@@ -265,14 +265,28 @@ extern "C" int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len
     fixups[3 * f + 2] = k;
     ++f;
   }
-  for (int64_t r = 0; r < rows; ++r) {
-    const int64_t b = rowptr[r], e = rowptr[r + 1];
-    if (e - b > seg_len) continue;
-    units[4 * u + 0] = static_cast<int32_t>(r);
-    units[4 * u + 1] = static_cast<int32_t>(b);
-    units[4 * u + 2] = static_cast<int32_t>(e);
-    units[4 * u + 3] = -1;
-    ++u;
+  // Whole rows next, by length class (longest class first, row order within
+  // a class): kernels that give one wavefront several rows then get rows of
+  // similar length together, and the longest rows start first.
+  auto length_class = [](int64_t len) {
+    int c = 0;
+    while (len > 0) {
+      ++c;
+      len >>= 1;
+    }
+    return c;  // 0 for empty rows, floor(log2(len)) + 1 otherwise
+  };
+  const int top = length_class(seg_len);
+  for (int cls = top; cls >= 0; --cls) {
+    for (int64_t r = 0; r < rows; ++r) {
+      const int64_t b = rowptr[r], e = rowptr[r + 1];
+      if (e - b > seg_len || length_class(e - b) != cls) continue;
+      units[4 * u + 0] = static_cast<int32_t>(r);
+      units[4 * u + 1] = static_cast<int32_t>(b);
+      units[4 * u + 2] = static_cast<int32_t>(e);
+      units[4 * u + 3] = -1;
+      ++u;
+    }
   }
   return GR_OK;
 }

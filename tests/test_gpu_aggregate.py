@@ -24,6 +24,10 @@ CASES = [
     (700, 1300, 25, 3, 256),
     (200, 260, 10, 1, 300),
     (50, 64, 3, 0, 1024),
+    # narrow widths with rows and columns on both sides of the 32-edge limit
+    # of the several-rows-per-wavefront kernel
+    (600, 500, 32, 2, 20),
+    (500, 450, 30, 1, 7),
 ]
 
 
