@@ -62,6 +62,7 @@ _SIGNATURES = {
                          _P],
     "gr_xent_forward": [_P, _i64, _i64, _i64, _P, _P, _i32, _P, _P, _i64, _P, _P, _P, _i64, _P],
     "gr_gemm_tn": [_P, _i64, _P, _i64, _i64, _i64, _i64, _f32, _P, _P, _i64, _i64, _P],
+    "gr_gemm_nt": [_P, _i64, _P, _i64, _i64, _i64, _i64, _P, _P, _i64, _P],
     "gr_gat_scores": [_P, _i64, _i64, _i64, _i64, _i64, _P, _P, _P, _P, _P],
     "gr_gat_row_dot": [_P, _i64, _P, _i64, _i64, _i64, _i64, _P, _P],
     "gr_gat_softmax_stats": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _i64, _P],

@@ -294,12 +294,14 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
     def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor],
                 plan: DevicePlan) -> Tensor:
         from torch.nn.functional import pad
+
+        from grinnder_amd.dense import gemm_nt
         d = weight.size(0)
         dp = (d + 3) // 4 * 4
         x = x.contiguous()
         wp = pad(weight, (0, 0, 0, dp - d))
         with dense_region("fwd", x.size(0), x.size(1), dp):
-            z = torch.mm(x, wp.t())
+            z = gemm_nt(x, wp)
         bp = pad(bias, (0, dp - d)).contiguous() if bias is not None else None
         y = spmm(plan.fwd, plan.idx, plan.val, z, plan.num_dst, bp, name="gcn_fwd")
         ctx.save_for_backward(x, wp)
@@ -312,7 +314,7 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
     def backward(ctx, gy: Tensor):
         from torch.nn.functional import pad
 
-        from grinnder_amd.dense import gemm_tn
+        from grinnder_amd.dense import gemm_nt, gemm_tn
         x, wp = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
         d, dp = ctx.d, wp.size(0)
@@ -321,7 +323,7 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
         dx = dw = None
         if ctx.needs_input_grad[0]:
             with dense_region("dx", dz.size(0), dp, wp.size(1)):
-                dx = torch.mm(dz, wp)
+                dx = gemm_nt(dz, wp.t().contiguous())
         if ctx.needs_input_grad[1]:
             with dense_region("dw", dz.size(0), dp, x.size(1)):
                 dw = gemm_tn(dz, x)[:d]

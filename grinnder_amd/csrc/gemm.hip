@@ -15,6 +15,7 @@
 // of one K chunk are consecutive workgroups of the same XCD: the A and B rows
 // of that chunk are fetched from HBM once and re-read from that XCD's L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "gr_internal.h"
 #include "wave.h"
@@ -264,6 +265,284 @@ extern "C" int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t l
   hipLaunchKernelGGL(sum_partials, dim3(blocks), dim3(256), 0, s, workspace, (int)used, pm, pn,
                      beta, (int)swap, c);
   GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Row-block product C[M, N] = A[M, K] B[N, K]^T (+ bias[N]), all row-major:
+// the dense transform's forward y = x W^T + b (B = W) and its input gradient
+// dx = dy W (B = W^T).  M is the node count (millions), N and K at most a few
+// thousand.
+//
+// Both operands are K-contiguous, so a thread's 16-byte load takes 4
+// consecutive k of one row, and the tiles are staged in LDS as [row][k] with
+// a 4-float pad (row stride 20 or 36 floats: the 16 rows a quarter-wavefront
+// reads with ds_read_b128 fall on distinct banks).  For v_mfma_f32_16x16x4_f32 lane
+// (r, q) supplies row r of the 16-block at k = 4 step + q; here the lane
+// reads k = 4q .. 4q + 3 of a 16-k slice in one ds_read_b128 and feeds them
+// to four consecutive MFMAs, so MFMA s of the slice sums k = 4q + s over q.
+// A and B use the same order, so every k is paired correctly; only the
+// order of the fp32 sums differs from a k-ascending loop.
+//
+// Workgroup: 4 wavefronts as WMW x (4 / WMW), each owning MI x NJ blocks of
+// BLK x BLK; K in steps of KS with the next step's loads in registers while
+// the current step's MFMAs run.  The column tiles of one row tile are
+// consecutive workgroups of one XCD, so A is read from HBM once and from that
+// XCD's L2 after.  Each output element is one workgroup's sum over K in a
+// fixed order: the result is deterministic.
+namespace gr_gemm {
+
+// A [ROWS, KS] slice of a row-major matrix (rows r0.., columns k0..) into
+// registers; elements outside [rows) x [K) read as 0.  V = 4 needs K % 4 == 0,
+// ld % 4 == 0 and a 16-byte aligned base.
+template <int V, int ROWS, int KS>
+struct NtTile {
+  static constexpr int LDK = KS + 4;
+  static constexpr int SPR = KS / V;  // slots per row
+  static constexpr int SLOTS = ROWS * SPR;
+  static constexpr int PER = (SLOTS + 255) / 256;  // a 16 x 32 tile has 128 float4 slots
+  float r[PER][V];
+
+  __device__ __forceinline__ void load(const float* __restrict__ src, int64_t ld, int64_t r0,
+                                       int64_t rows, int k0, int K) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int slot = threadIdx.x + p * 256;
+      const int64_t row = r0 + slot / SPR;
+      const int k = k0 + (slot % SPR) * V;
+      const bool in = (SLOTS % 256 == 0 || slot < SLOTS) && row < rows && k < K;
+      if constexpr (V == 4) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (in) v = *reinterpret_cast<const float4*>(src + row * ld + k);
+        r[p][0] = v.x;
+        r[p][1] = v.y;
+        r[p][2] = v.z;
+        r[p][3] = v.w;
+      } else {
+        r[p][0] = in ? src[row * ld + k] : 0.f;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float (*lds)[LDK]) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int slot = threadIdx.x + p * 256;
+      if (SLOTS % 256 != 0 && slot >= SLOTS) continue;
+      float* d = &lds[slot / SPR][(slot % SPR) * V];
+      if constexpr (V == 4) {
+        *reinterpret_cast<float4*>(d) = make_float4(r[p][0], r[p][1], r[p][2], r[p][3]);
+      } else {
+        *d = r[p][0];
+      }
+    }
+  }
+};
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// BLK = 16: v_mfma_f32_16x16x4_f32 blocks; lane (r, q) = (lane % 16, lane / 16)
+// reads k = 4q .. 4q + 3 of a 16-k slice.  BLK = 32: v_mfma_f32_32x32x2_f32
+// blocks; lane (r, q) = (lane % 32, lane / 32) reads k = 4q .. 4q + 3 of an
+// 8-k slice, and MFMA s of the slice takes the k pair (s, 4 + s).
+// DB: two LDS buffers, one barrier per K step (step s computes from buffer
+// s % 2 while step s + 1's tile, already in registers, goes to the other).
+// OCC: the waves per SIMD the register allocation must allow.
+template <int VA, int VB, int MI, int NJ, int WMW, int KS, int BLK, int OCC, bool DB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) void gemm_nt_kernel(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
+    const float* __restrict__ bias, float* __restrict__ C, int64_t ldc, int64_t M, int N, int K,
+    int64_t tiles_m, int tiles_n) {
+  constexpr int WNW = 4 / WMW;
+  constexpr int TM = BLK * MI * WMW;
+  constexpr int TN = BLK * NJ * WNW;
+  constexpr int LDK = KS + 4;
+  constexpr int SLICE = BLK == 16 ? 16 : 8;  // k per fragment read
+  constexpr int NBUF = DB ? 2 : 1;
+  typedef typename std::conditional<BLK == 16, floatx4, floatx16>::type accx;
+  __shared__ __align__(16) float As[NBUF][TM][LDK];
+  __shared__ __align__(16) float Bs[NBUF][TN][LDK];
+
+  const int64_t w = blockIdx.x;
+  const int64_t q = w / kXcds;
+  const int64_t tm = (q / tiles_n) * kXcds + w % kXcds;
+  if (tm >= tiles_m) return;  // whole workgroup: no barrier is pending
+  const int tn = (int)(q % tiles_n);
+  const int64_t m0 = tm * TM;
+  const int n0 = tn * TN;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave % WMW) * (BLK * MI);
+  const int wn = (wave / WMW) * (BLK * NJ);
+  const int lr = lane % BLK;
+  const int lq = lane / BLK;
+
+  accx acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = accx{};
+
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < KS / SLICE; ++h) {
+      floatx4 a[MI], b[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        a[i] = *reinterpret_cast<const floatx4*>(&As[buf][wm + i * BLK + lr][h * SLICE + lq * 4]);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        b[j] = *reinterpret_cast<const floatx4*>(&Bs[buf][wn + j * BLK + lr][h * SLICE + lq * 4]);
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            if constexpr (BLK == 16)
+              acc[i][j] =
+                  __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], b[j][st], acc[i][j], 0, 0, 0);
+            else
+              acc[i][j] =
+                  __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][st], b[j][st], acc[i][j], 0, 0, 0);
+          }
+    }
+  };
+
+  NtTile<VA, TM, KS> ta;
+  NtTile<VB, TN, KS> tb;
+  ta.load(A, lda, m0, M, 0, K);
+  tb.load(B, ldb, n0, N, 0, K);
+  if constexpr (DB) {
+    // Buffer (s + 1) % 2 was last read in step s - 1, before the barrier
+    // that ended it.
+    ta.store(As[0]);
+    tb.store(Bs[0]);
+    if (KS < K) {
+      ta.load(A, lda, m0, M, KS, K);
+      tb.load(B, ldb, n0, N, KS, K);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < K; k0 += KS) {
+      compute(buf);
+      if (k0 + KS < K) {
+        ta.store(As[buf ^ 1]);
+        tb.store(Bs[buf ^ 1]);
+        if (k0 + 2 * KS < K) {
+          ta.load(A, lda, m0, M, k0 + 2 * KS, K);
+          tb.load(B, ldb, n0, N, k0 + 2 * KS, K);
+        }
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+  } else {
+    for (int k0 = 0; k0 < K; k0 += KS) {
+      __syncthreads();  // the previous step's reads of the LDS tiles are done
+      ta.store(As[0]);
+      tb.store(Bs[0]);
+      __syncthreads();
+      if (k0 + KS < K) {
+        ta.load(A, lda, m0, M, k0 + KS, K);
+        tb.load(B, ldb, n0, N, k0 + KS, K);
+      }
+      compute(0);
+    }
+  }
+
+  // BLK = 16: lane holds column lr, rows 4 lq + r (r < 4).  BLK = 32: lane
+  // holds column lr, rows 8 (r / 4) + 4 lq + r % 4 (r < 16).
+  constexpr int RPL = BLK == 16 ? 4 : 16;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = n0 + wn + j * BLK + lr;
+    if (n >= N) continue;
+    const float bn = bias != nullptr ? bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) {
+        const int row = BLK == 16 ? lq * 4 + r : (r / 4) * 8 + lq * 4 + r % 4;
+        const int64_t m = m0 + wm + i * BLK + row;
+        if (m < M) C[m * ldc + n] = acc[i][j][r] + bn;
+      }
+  }
+}
+
+template <int VA, int VB, int MI, int NJ, int WMW, int KS, int BLK, int OCC = 1, bool DB = false>
+static hipError_t launch_nt(const float* a, int64_t lda, const float* b, int64_t ldb,
+                            const float* bias, float* c, int64_t ldc, int64_t m, int n, int k,
+                            hipStream_t s) {
+  constexpr int TM = BLK * MI * WMW;
+  constexpr int TN = BLK * NJ * (4 / WMW);
+  const int64_t tiles_m = (m + TM - 1) / TM;
+  const int tiles_n = (n + TN - 1) / TN;
+  const int64_t nwg = (tiles_m + kXcds - 1) / kXcds * kXcds * tiles_n;
+  if (nwg > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nt_kernel<VA, VB, MI, NJ, WMW, KS, BLK, OCC, DB>), dim3((unsigned)nwg),
+                     dim3(256), 0, s, a, lda, b, ldb, bias, c, ldc, m, n, k, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+// Tile shape by the product's shape, as measured on the dense transform's
+// products (MI355X, fp32):
+//   n > 64, k > 256: 128 x 128 tiles of 16 x 16 blocks, 32-k steps (116 TFLOP/s
+//     for 625k x 256 x 1024);
+//   n > 64, k <= 256: 128 x 128 tiles of 32 x 32 blocks, 16-k double-buffered
+//     steps at 4 waves per SIMD (114-117 TFLOP/s for 2.45M x 256 x 256, and
+//     30% faster than the first form for k = 48 or 20);
+//   33..48 columns: 256 x 48 tiles (no padded columns); 49..64: 256 x 64;
+//   17..32 and <= 16 columns: 256 x 32 / 256 x 16.
+// hipBLASLt's own kernels run these products at 116-128 TFLOP/s with 82%
+// MFMA-busy cycles against 70-79% here.  A persistent grid, fragment reads
+// one slice ahead, explicit instruction interleaving and 64 x 128 wavefront
+// tiles were each measured and gained nothing; double-buffered LDS pays only
+// in the 16-k, 4-waves-per-SIMD form above.
+template <int VA, int VB>
+static hipError_t dispatch_nt(const float* a, int64_t lda, const float* b, int64_t ldb,
+                              const float* bias, float* c, int64_t ldc, int64_t m, int n, int k,
+                              hipStream_t s) {
+#define GR_NT(MI, NJ, WMW, KS, BLK, ...) \
+  return launch_nt<VA, VB, MI, NJ, WMW, KS, BLK, ##__VA_ARGS__>(a, lda, b, ldb, bias, c, ldc, m, n, k, s)
+  if (n > 64) {
+    if (k <= 256) GR_NT(2, 2, 2, 16, 32, 4, true);
+    GR_NT(4, 4, 2, 32, 16);
+  }
+  if (n > 48) GR_NT(4, 4, 4, 16, 16, 1, true);
+  if (n > 32) GR_NT(4, 3, 4, 32, 16);
+  if (n > 16) GR_NT(4, 2, 4, 32, 16);
+  GR_NT(4, 1, 4, 32, 16);
+#undef GR_NT
+}
+
+}  // namespace gr_gemm
+
+extern "C" int gr_gemm_nt(const float* a, int64_t lda, const float* b, int64_t ldb, int64_t m,
+                          int64_t n, int64_t k, const float* bias, float* c, int64_t ldc,
+                          void* stream) {
+  using namespace gr_gemm;
+  gr::clear_error();
+  GR_REQUIRE(m >= 0 && n >= 1 && k >= 1 && n <= (1 << 20) && k <= (1 << 24),
+             "gemm_nt: bad shape %lld x %lld x %lld", (long long)m, (long long)n, (long long)k);
+  GR_REQUIRE(lda >= k && ldb >= k && ldc >= n, "gemm_nt: leading dimension too small");
+  if (m == 0) return GR_OK;
+  GR_REQUIRE(a != nullptr && b != nullptr && c != nullptr, "gemm_nt: NULL pointer");
+  const bool va = k % 4 == 0 && lda % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0;
+  const bool vb = k % 4 == 0 && ldb % 4 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0;
+  hipStream_t s = gr::as_stream(stream);
+  hipError_t err;
+  if (va && vb)
+    err = dispatch_nt<4, 4>(a, lda, b, ldb, bias, c, ldc, m, (int)n, (int)k, s);
+  else if (va)
+    err = dispatch_nt<4, 1>(a, lda, b, ldb, bias, c, ldc, m, (int)n, (int)k, s);
+  else if (vb)
+    err = dispatch_nt<1, 4>(a, lda, b, ldb, bias, c, ldc, m, (int)n, (int)k, s);
+  else
+    err = dispatch_nt<1, 1>(a, lda, b, ldb, bias, c, ldc, m, (int)n, (int)k, s);
+  GR_REQUIRE(err != hipErrorInvalidValue, "gemm_nt: too many workgroups for %lld rows",
+             (long long)m);
+  GR_HIP_CHECK(err);
   return GR_OK;
 }
 

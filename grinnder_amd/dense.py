@@ -1,12 +1,12 @@
 """Dense per-layer transform of the conv layers, on the HIP kernels.
 
 PyG's GCNConv / GATConv (grinnder/nn/gcn.py:53-56, grinnder/nn/gat.py:54-61)
-apply a bias-free ``Linear`` to the node features.  Its forward and input
-gradient are plain tall-skinny matrix products (``torch.mm`` on hipBLASLt);
-its weight gradient dW = dZ^T X reduces over all K node rows of the
-partition with M, N <= a few hundred, a shape the library GEMMs split poorly.
-``linear`` keeps the forward on torch and computes dW with ``gr_gemm_tn``
-(split-K fp32 MFMA, partials summed in a fixed order).
+apply a bias-free ``Linear`` to the node features.  All three of its
+products run on this library's fp32 MFMA kernels: the forward x Wᵀ (+ b) and
+the input gradient dy W on ``gr_gemm_nt`` (row-block tiles, K-contiguous
+operands), the weight gradient dW = dyᵀ x, which reduces over all K node rows
+of the partition with M, N <= a few hundred, on ``gr_gemm_tn`` (split-K,
+partials summed in a fixed order).
 
 ``bias_ln_act`` is the dense counterpart of the fused aggregation epilogue:
 LayerNorm + ReLU after a GCN layer that aggregates first and multiplies
@@ -67,8 +67,47 @@ def gemm_tn(a: Tensor, b: Tensor, out: Optional[Tensor] = None, beta: float = 0.
     return out
 
 
+def gemm_nt(a: Tensor, b: Tensor, bias: Optional[Tensor] = None,
+            out: Optional[Tensor] = None) -> Tensor:
+    """C = a bᵀ (+ bias) for a [M, K] and b [N, K] fp32 device matrices with
+    unit column stride (rows may be strided) on the matrix cores; `out` is a
+    [M, N] matrix with unit column stride (for example a column slice of a
+    wider buffer), written in place."""
+    _check("a", a)
+    _check("b", b)
+    if a.dim() != 2 or b.dim() != 2 or a.size(1) != b.size(1):
+        raise ValueError(f"gemm_nt: a {tuple(a.shape)} and b {tuple(b.shape)} need equal columns")
+    if a.stride(1) != 1 or (a.size(0) > 1 and a.stride(0) < a.size(1)):
+        a = a.contiguous()
+    if b.stride(1) != 1 or (b.size(0) > 1 and b.stride(0) < b.size(1)):
+        b = b.contiguous()
+    m, k = a.shape
+    n = b.size(0)
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    else:
+        _check("out", out)
+        if out.shape != (m, n) or out.stride(1) != 1 or (m > 1 and out.stride(0) < n):
+            raise ValueError(f"gemm_nt: out must be a [{m}, {n}] matrix with unit column "
+                             f"stride; got {tuple(out.shape)} strides {out.stride()}")
+    if bias is not None:
+        _check("bias", bias)
+        bias = bias.contiguous()
+        if bias.numel() != n:
+            raise ValueError(f"gemm_nt: bias of {bias.numel()} elements, {n} expected")
+    if m == 0 or n == 0:
+        return out
+    if k == 0:
+        return out.copy_(bias.expand(m, n) if bias is not None else torch.zeros_like(out))
+    _lib.call("gr_gemm_nt", a.data_ptr(), max(a.stride(0), k), b.data_ptr(),
+              max(b.stride(0), k), m, n, k, _lib.ptr(bias), out.data_ptr(),
+              max(out.stride(0), n), _lib.stream_handle())
+    return out
+
+
 class _Linear(torch.autograd.Function):
-    """y = x W^T (+ b); dx = dy W (torch), dW = dy^T x (gr_gemm_tn), db = sum dy.
+    """y = x W^T (+ b) and dx = dy W (gr_gemm_nt), dW = dy^T x (gr_gemm_tn),
+    db = sum dy.
     `reuse` (a one-element list, or None) holds y as an earlier forward
     computed it from the same x, W and b: it is returned instead of being
     recomputed, and the backward is the same."""
@@ -85,10 +124,7 @@ class _Linear(torch.autograd.Function):
                                  f"expected {(x2.size(0), weight.size(0))}")
         else:
             with dense_region("fwd", x2.size(0), x2.size(1), weight.size(0)):
-                if bias is not None:
-                    y = torch.addmm(bias, x2, weight.t())
-                else:
-                    y = torch.mm(x2, weight.t())
+                y = gemm_nt(x2, weight, bias)
         ctx.save_for_backward(x2, weight)
         ctx.in_shape = x.shape
         ctx.has_bias = bias is not None
@@ -103,7 +139,7 @@ class _Linear(torch.autograd.Function):
         rows, dout, din = gy2.size(0), weight.size(0), weight.size(1)
         if ctx.needs_input_grad[0]:
             with dense_region("dx", rows, dout, din):
-                dx = torch.mm(gy2, weight).reshape(ctx.in_shape)
+                dx = gemm_nt(gy2, weight.t().contiguous()).reshape(ctx.in_shape)
         if ctx.needs_input_grad[1]:
             with dense_region("dw", rows, dout, din):
                 dw = gemm_tn(gy2, x2)
@@ -115,7 +151,8 @@ class _Linear(torch.autograd.Function):
 
 def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None,
            reuse: Optional[Tensor] = None) -> Tensor:
-    """``F.linear`` whose weight gradient runs on the split-K MFMA kernel (GPU).
+    """``F.linear`` on the library's MFMA kernels (GPU): forward and input
+    gradient on gr_gemm_nt, weight gradient on the split-K gr_gemm_tn.
     `reuse`: this product as an earlier forward formed it from the same
     operands (rows [-1, out]); it is returned instead of recomputed, with the
     same backward."""
@@ -213,7 +250,7 @@ class _LinearLNAct(torch.autograd.Function):
         rows, din, dout = x.size(0), x.size(1), w.size(0)
         if ctx.needs_input_grad[0]:
             with dense_region("dx", rows, dout, din):
-                dx = torch.mm(gh, w)
+                dx = gemm_nt(gh, w.t().contiguous())
         if ctx.needs_input_grad[1]:
             with dense_region("dw", rows, dout, din):
                 dw = gemm_tn(gh, x)

@@ -19,7 +19,7 @@ from torch import Tensor
 
 from grinnder_amd.aggregation import (KernelTimer, ProjectedSink, dense_region, gather_rows,
                                      scatter_add_rows)
-from grinnder_amd.dense import gemm_tn
+from grinnder_amd.dense import gemm_nt, gemm_tn
 from grinnder_amd.loss import masked_cross_entropy
 
 
@@ -486,7 +486,7 @@ class ProjectedLayers:
                 self._wpad[layer] = wp
             w = wp
         with torch.no_grad(), dense_region("fwd", hi - lo, w.size(1), w.size(0)):
-            torch.mm(x.detach(), w.t(), out=z[lo:hi])
+            gemm_nt(x.detach(), w, out=z[lo:hi])
 
     def _each_input_partition(self, layer: int, fn) -> None:
         """fn(pid, x_p, lo, hi) on the compute stream for every partition,
@@ -622,7 +622,7 @@ class ProjectedLayers:
             return self._gxbufs[layer][lo:hi]
         w = self._proj[layer]
         with dense_region("dx", hi - lo, w.size(0), w.size(1)):
-            return torch.mm(self._dzbufs[layer][lo:hi, :w.size(0)], w.detach())
+            return gemm_nt(self._dzbufs[layer][lo:hi, :w.size(0)], w.detach().t().contiguous())
 
     def _backward_device(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
         """Backward of a projected layer: per partition, take the forward's

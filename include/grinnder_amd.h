@@ -374,6 +374,17 @@ int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t ldb,
                float* workspace, int64_t workspace_floats, int64_t splits,
                void* stream);
 
+/* C[M, N] = A B^T (+ bias[N]) with A [M, K], B [N, K] and C [M, N] row-major
+ * (lda-, ldb-, ldc-strided rows), fp32 on the matrix cores; each element is
+ * one workgroup's sum over K (no split, deterministic).  With B = W [out, in]
+ * this is the forward x W^T + b of the conv's dense transform (the Linear of
+ * PyG GCNConv / GATConv, grinnder/nn/gcn.py:53-56, grinnder/nn/gat.py:54-61);
+ * with B = W^T it is the input gradient dx = dy W.  bias may be NULL; m may be
+ * 0 (nothing to do). */
+int gr_gemm_nt(const float* a, int64_t lda, const float* b, int64_t ldb,
+               int64_t m, int64_t n, int64_t k, const float* bias, float* c,
+               int64_t ldc, void* stream);
+
 /* Dense layer transform with the LayerNorm epilogue in the GEMM accumulators:
  *   h = x W^T + bias, out = act(LayerNorm(h; gamma, beta, eps)), mean, rstd
  * for x [rows, din] (ldx-strided), wt = W^T [din, dout] row-major (the

@@ -1,5 +1,6 @@
 """GPU: the dense per-layer transform — split-K weight-gradient GEMM
-(gr_gemm_tn), the Linear autograd function built on it, and the dense
+(gr_gemm_tn), the forward / input-gradient GEMM (gr_gemm_nt), the Linear
+autograd function built on them, and the dense
 bias + LayerNorm + ReLU/ELU epilogue (gr_bias_ln_act) — against float64 torch.
 fp32 tolerance: max-abs-normalised error <= 1e-5 (TOL)."""
 
@@ -7,7 +8,8 @@ import pytest
 import torch
 
 from grinnder_amd import _lib
-from grinnder_amd.dense import bias_ln_act, bias_ln_relu, gemm_tn, gemm_tn_splits, linear
+from grinnder_amd.dense import (bias_ln_act, bias_ln_relu, gemm_nt, gemm_tn, gemm_tn_splits,
+                                linear)
 from tests.graphs import TOL, max_abs_norm_err
 
 pytestmark = pytest.mark.gpu
@@ -64,6 +66,46 @@ def test_gemm_tn_workspace_checked(gpu):
     with pytest.raises(_lib.GrError, match="workspace"):
         _lib.call("gr_gemm_tn", a.data_ptr(), 8, b.data_ptr(), 8, 8, 8, 100, 0.0,
                   c.data_ptr(), ws.data_ptr(), ws.numel(), 7, _lib.stream_handle())
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (37, 7, 3), (1000, 20, 256), (777, 48, 100),
+                                   (5000, 256, 1024), (300, 300, 64), (129, 65, 33),
+                                   (4096, 16, 20), (70_000, 256, 48), (3000, 1024, 256),
+                                   (2500, 47, 256), (513, 130, 1)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
+    """Every tile shape (n > 64, 33..64, 17..32, <= 16), K not a multiple of
+    the 32-wide step or of 4 (scalar loads), ragged row and column tiles."""
+    a = _randn(m, k, seed=m + k, dev=gpu)
+    b = _randn(n, k, seed=n + k + 1, dev=gpu)
+    bv = _randn(n, seed=n, dev=gpu) if bias else None
+    c = gemm_nt(a, b, bv)
+    ref = a.double() @ b.double().t()
+    if bias:
+        ref += bv.double()
+    assert max_abs_norm_err(c, ref) <= TOL
+
+
+def test_gemm_nt_strided_and_in_place(gpu):
+    """Strided a and b rows, an unaligned a (scalar path), and a column slice
+    of a wider buffer as `out` (ldc > n): the columns around it are untouched;
+    the same call twice gives the same bits."""
+    big_a = _randn(9000, 300, seed=3, dev=gpu)
+    big_b = _randn(200, 260, seed=4, dev=gpu)
+    a, b = big_a[:, 16:272], big_b[:, :256]  # lda = 300, ldb = 260
+    buf = _randn(9000, 320, seed=5, dev=gpu)
+    before = buf.clone()
+    gemm_nt(a, b, out=buf[:, 40:240])
+    ref = a.double() @ b.double().t()
+    assert max_abs_norm_err(buf[:, 40:240], ref) <= TOL
+    assert torch.equal(buf[:, :40], before[:, :40]) and torch.equal(buf[:, 240:], before[:, 240:])
+    again = gemm_nt(a, b)
+    assert torch.equal(again, gemm_nt(a, b))
+    odd = big_a[:, 1:257]  # 4-byte aligned only
+    assert max_abs_norm_err(gemm_nt(odd, b), odd.double() @ b.double().t()) <= TOL
+    assert gemm_nt(a[:0], b).shape == (0, 200)
+    with pytest.raises(ValueError, match="out must be"):
+        gemm_nt(a, b, out=torch.empty(9000, 199, device=gpu))
 
 
 @pytest.mark.parametrize("rows,fin,fout,bias", [(5000, 100, 256, True), (777, 256, 47, False),
