@@ -1316,6 +1316,67 @@ __global__ __launch_bounds__(256) void gat_bwd_dst_kernel(const int4* __restrict
   }
 }
 
+// One head: the same sums, 64 / G units per wavefront (G lanes each, VEC
+// floats a lane, NCH chunks of G * VEC floats).  The row's dHs, att_dst, c_i
+// and den_i do not depend on the edge sum, so they are loaded first and their
+// latency overlaps the g_t loads; the edge loop keeps four loads in flight.
+template <int VEC, int G, int NCH>
+__global__ __launch_bounds__(256) void gat_bwd_dst_h1(
+    const int4* __restrict__ units, int64_t n_units, const float* __restrict__ gt, int C,
+    const float* __restrict__ att_dst, const float* __restrict__ cdot,
+    const float* __restrict__ den, float* __restrict__ dd, float* __restrict__ dhs,
+    float* __restrict__ ws) {
+  constexpr int RPW = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane / G, sub = lane % G;
+  const int64_t wid = wave_id();
+  if (wid * RPW >= n_units) return;
+  const int64_t u = wid * RPW + grp;
+  const bool active = u < n_units;
+  const int4 w = active ? units[u] : make_int4(0, 0, 0, -1);
+  const bool whole = active && w.w < 0;
+  const int64_t i = w.x;
+
+  int foff[NCH];
+  bool fvalid[NCH];
+  float hv[NCH][VEC], av[NCH][VEC];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    foff[ch] = (ch * G + sub) * VEC;
+    fvalid[ch] = foff[ch] < C;
+    const int fld = fvalid[ch] ? foff[ch] : C - VEC;
+    if (whole) {
+      ld<VEC>(dhs + i * C + fld, hv[ch]);
+      ld<VEC>(att_dst + fld, av[ch]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) hv[ch][q] = av[ch][q] = 0.f;
+    }
+  }
+  const float ci = whole ? cdot[i] : 0.f;
+  const float dn = whole ? den[i] : 1.f;
+
+  float p = 0.f;
+#pragma unroll 4
+  for (int e = w.y + sub; e < w.z; e += G) p += gt[e];
+  p = gr_wave::group_sum<G>(p);
+  if (!active) return;
+  if (whole) {
+    const float v = p + ci * (1e-16f / dn);
+    if (sub == 0) dd[i] = v;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      if (!fvalid[ch]) continue;
+      float o[VEC];
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) o[q] = fmaf(v, av[ch][q], hv[ch][q]);
+      st<VEC>(dhs + i * C + foff[ch], o);
+    }
+  } else if (sub == 0) {
+    ws[w.w] = p;
+  }
+}
+
 __global__ __launch_bounds__(256) void gat_bwd_dst_fixup(const int32_t* __restrict__ fix,
                                                          int64_t n_fix,
                                                          const float* __restrict__ ws, int H,
@@ -1852,9 +1913,34 @@ extern "C" int gr_gat_backward_dst(const int32_t* units, int64_t n_units, const 
   GR_REQUIRE(units && aligned16(units) && gt && att_dst && cdot && den && dd && dhs,
              "gat_backward_dst: NULL or misaligned pointer");
   hipStream_t st = gr::as_stream(stream);
-  hipLaunchKernelGGL(gat_bwd_dst_kernel, dim3(blocks_for(n_units)), dim3(256), 0, st,
-                     reinterpret_cast<const int4*>(units), n_units, gt, (int)heads, (int)channels,
-                     att_dst, cdot, den, dd, dhs, workspace);
+  const int4* u4 = reinterpret_cast<const int4*>(units);
+  const int C = (int)channels;
+  const int vec = (C % 4 == 0 && aligned16(dhs) && aligned16(att_dst)) ? 4 : 1;
+  const int chunks = (C + vec - 1) / vec;
+  if (heads == 1 && chunks <= 256) {
+    // G lanes a row: at least 16 (a long row's edge sum), else the smallest
+    // power of two that covers the row's vectors.
+#define GR_DH(V, G, N)                                                                        \
+  hipLaunchKernelGGL((gat_bwd_dst_h1<V, G, N>), dim3(blocks_for((n_units + 64 / G - 1) / (64 / G))), \
+                     dim3(256), 0, st, u4, n_units, gt, C, att_dst, cdot, den, dd, dhs, workspace)
+    if (vec == 4) {
+      if (chunks <= 16) GR_DH(4, 16, 1);
+      else if (chunks <= 32) GR_DH(4, 32, 1);
+      else if (chunks <= 64) GR_DH(4, 64, 1);
+      else if (chunks <= 128) GR_DH(4, 64, 2);
+      else GR_DH(4, 64, 4);
+    } else {
+      if (chunks <= 16) GR_DH(1, 16, 1);
+      else if (chunks <= 32) GR_DH(1, 32, 1);
+      else if (chunks <= 64) GR_DH(1, 64, 1);
+      else if (chunks <= 128) GR_DH(1, 64, 2);
+      else GR_DH(1, 64, 4);
+    }
+#undef GR_DH
+  } else {
+    hipLaunchKernelGGL(gat_bwd_dst_kernel, dim3(blocks_for(n_units)), dim3(256), 0, st, u4,
+                       n_units, gt, (int)heads, C, att_dst, cdot, den, dd, dhs, workspace);
+  }
   GR_HIP_CHECK(hipGetLastError());
   if (n_fix > 0) {
     hipLaunchKernelGGL(gat_bwd_dst_fixup, dim3(blocks_for(n_fix)), dim3(256), 0, st, fixups,
