@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void aggregate_ln_relu_fixup(
 // per-wavefront column sums of gh itself are kept too: the gradient of the
 // bias added before the LayerNorm, without a second read of gh.
 // Grid-stride over rows.
-template <int VEC, int NCH, int ACT>
+template <int VEC, int NCH, int ACT, int P>
 __global__ __launch_bounds__(256) void ln_relu_backward(
     const float* __restrict__ g, const float* __restrict__ h, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
@@ -463,65 +463,68 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     }
   }
   const float inv_d = 1.0f / (float)dim;
-  // The next row's loads are issued before the current row is reduced.
-  float gn[NCH][VEC], hn[NCH][VEC], mu_n = 0.f, rs_n = 0.f;
-  if (wid < rows) {
-    mu_n = mean[wid];
-    rs_n = rstd[wid];
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      load_vec<VEC>(g + wid * dim + fld[ch], gn[ch]);
-      load_vec<VEC>(h + wid * dim + fld[ch], hn[ch]);
-    }
-  }
-  for (int64_t r = wid; r < rows; r += nwaves) {
-    const float mu = mu_n, rs = rs_n;
-    float gv[NCH][VEC], hc[NCH][VEC], xh[NCH][VEC], gx[NCH][VEC];
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        gv[ch][j] = gn[ch][j];
-        hc[ch][j] = hn[ch][j];
-      }
-    const int64_t rn = r + nwaves;
-    if (rn < rows) {
-      mu_n = mean[rn];
-      rs_n = rstd[rn];
+  // A ring of P rows in flight: the wavefront's rows are r = wid + k nwaves;
+  // slot k % P holds row k's loads, issued P rows before its use (a loaded
+  // row's latency is several microseconds, one row's work a few hundred
+  // cycles).  Rows are consumed in the same order as with one row in flight.
+  float gn[P][NCH][VEC], hn[P][NCH][VEC], mu_n[P], rs_n[P];
+  auto issue = [&](int slot, int64_t r) {
+    if (r < rows) {
+      mu_n[slot] = mean[r];
+      rs_n[slot] = rstd[r];
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch) {
-        load_vec<VEC>(g + rn * dim + fld[ch], gn[ch]);
-        load_vec<VEC>(h + rn * dim + fld[ch], hn[ch]);
+        load_vec<VEC>(g + r * dim + fld[ch], gn[slot][ch]);
+        load_vec<VEC>(h + r * dim + fld[ch], hn[slot][ch]);
       }
     }
-    float s1 = 0.f, s2 = 0.f;
+  };
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      const float* hv = hc[ch];
+  for (int k = 0; k < P; ++k) issue(k, wid + k * nwaves);
+  for (int64_t r0 = wid; r0 < rows; r0 += P * nwaves) {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float y = ln_affine(hv[j], mu, rs, gam[ch][j], bet[ch][j]);
-        const float gy = fvalid[ch] ? gv[ch][j] * act_grad<ACT>(y) : 0.f;
-        xh[ch][j] = (hv[j] - mu) * rs;
-        gx[ch][j] = gy * gam[ch][j];
-        dg[ch][j] = fmaf(gy, xh[ch][j], dg[ch][j]);
-        db[ch][j] += gy;
-        s1 += gx[ch][j];
-        s2 = fmaf(gx[ch][j], xh[ch][j], s2);
+    for (int k = 0; k < P; ++k) {
+      const int64_t r = r0 + k * nwaves;
+      if (r >= rows) break;
+      const float mu = mu_n[k], rs = rs_n[k];
+      float gv[NCH][VEC], hc[NCH][VEC], xh[NCH][VEC], gx[NCH][VEC];
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          gv[ch][j] = gn[k][ch][j];
+          hc[ch][j] = hn[k][ch][j];
+        }
+      issue(k, r + P * nwaves);
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) {
+        const float* hv = hc[ch];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float y = ln_affine(hv[j], mu, rs, gam[ch][j], bet[ch][j]);
+          const float gy = fvalid[ch] ? gv[ch][j] * act_grad<ACT>(y) : 0.f;
+          xh[ch][j] = (hv[j] - mu) * rs;
+          gx[ch][j] = gy * gam[ch][j];
+          dg[ch][j] = fmaf(gy, xh[ch][j], dg[ch][j]);
+          db[ch][j] += gy;
+          s1 += gx[ch][j];
+          s2 = fmaf(gx[ch][j], xh[ch][j], s2);
+        }
       }
-    }
-    s1 = wave_sum64(s1) * inv_d;
-    s2 = wave_sum64(s2) * inv_d;
+      s1 = wave_sum64(s1) * inv_d;
+      s2 = wave_sum64(s2) * inv_d;
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      if (!fvalid[ch]) continue;
-      float o[VEC];
+      for (int ch = 0; ch < NCH; ++ch) {
+        if (!fvalid[ch]) continue;
+        float o[VEC];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        o[j] = rs * (gx[ch][j] - s1 - xh[ch][j] * s2);
-        dh[ch][j] += o[j];
+        for (int j = 0; j < VEC; ++j) {
+          o[j] = rs * (gx[ch][j] - s1 - xh[ch][j] * s2);
+          dh[ch][j] += o[j];
+        }
+        store_vec<VEC>(gh + r * dim + foff[ch], o);
       }
-      store_vec<VEC>(gh + r * dim + foff[ch], o);
     }
   }
 #pragma unroll
@@ -1266,6 +1269,81 @@ extern "C" int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
   return GR_OK;
 }
 
+namespace gr_agg {
+
+// Waves of `kernel` (256-thread workgroups) that the device holds at once.
+inline int64_t resident_waves(const void* kernel) {
+  int dev = 0, cus = 0, nb = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, 256, 0) != hipSuccess)
+    return 8192;
+  return (int64_t)std::max(nb, 1) * std::max(cus, 1) * 4;
+}
+
+// The LayerNorm/activation backward with the grid one resident wave per
+// slot (each wave keeps P rows in flight), then the ordered column sums of
+// the per-wave partials.
+template <int V, int N, int P>
+int run_ln_backward_p(int32_t act, const float* g, const float* h, const float* mean,
+                      const float* rstd, const float* gamma, const float* beta, int64_t rows,
+                      int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
+                      float* workspace, int64_t workspace_floats, hipStream_t s);
+
+template <int V, int N>
+int run_ln_backward(int32_t act, const float* g, const float* h, const float* mean,
+                    const float* rstd, const float* gamma, const float* beta, int64_t rows,
+                    int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
+                    float* workspace, int64_t workspace_floats, hipStream_t s) {
+  // Six rows in flight at 256 floats a row (measured: 1.52 ms for 2.45M rows at
+  // 4.96 TB/s against 1.68 ms with one, 5.05 against 4.55 TB/s for 625k rows).
+  return run_ln_backward_p<V, N, N == 1 ? 6 : 1>(act, g, h, mean, rstd, gamma, beta, rows, dim,
+                                                 gh, dgamma, dbeta, dbias, workspace,
+                                                 workspace_floats, s);
+}
+
+template <int V, int N, int P>
+int run_ln_backward_p(int32_t act, const float* g, const float* h, const float* mean,
+                      const float* rstd, const float* gamma, const float* beta, int64_t rows,
+                      int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
+                      float* workspace, int64_t workspace_floats, hipStream_t s) {
+  const void* kern = act == GR_ACT_RELU
+                         ? reinterpret_cast<const void*>(&ln_relu_backward<V, N, GR_ACT_RELU, P>)
+                         : reinterpret_cast<const void*>(&ln_relu_backward<V, N, GR_ACT_ELU, P>);
+  static int64_t resident[2] = {0, 0};
+  int64_t& res = resident[act == GR_ACT_RELU ? 0 : 1];
+  if (res == 0) res = resident_waves(kern);
+  // Wavefront count: the resident waves, fewer for few rows, bounded by the
+  // workspace (nparts * nwaves * dim floats of partials).
+  int64_t nwaves = std::min<int64_t>(res, std::max<int64_t>(4, (rows + 15) / 16));
+  nwaves = (nwaves + 3) / 4 * 4;
+  const int nparts = dbias != nullptr ? 3 : 2;
+  const int64_t cap = (workspace_floats / dim - 1) / nparts / 4 * 4;
+  GR_REQUIRE(cap >= 4, "ln_relu_backward: workspace too small");
+  if (nwaves > cap) nwaves = cap;
+  float* pg = workspace;
+  float* pb = workspace + nwaves * dim;
+  float* ph = dbias != nullptr ? workspace + 2 * nwaves * dim : nullptr;
+  const int d = (int)dim;
+  const unsigned blocks = (unsigned)(nwaves / 4);
+  if (act == GR_ACT_RELU)
+    hipLaunchKernelGGL((ln_relu_backward<V, N, GR_ACT_RELU, P>), dim3(blocks), dim3(256), 0, s,
+                       g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);
+  else
+    hipLaunchKernelGGL((ln_relu_backward<V, N, GR_ACT_ELU, P>), dim3(blocks), dim3(256), 0, s, g,
+                       h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);
+  GR_HIP_CHECK(hipGetLastError());
+  // dgamma / dbeta (/ dbias) = column sums of the partials, in wavefront
+  // order: the partial matrices follow one another in the workspace, and
+  // one launch reduces all of them.
+  hipLaunchKernelGGL(colsum_final3, dim3(final_blocks(d), (unsigned)nparts), dim3(256), 0, s, pg,
+                     (int)nwaves, d, dgamma, dbeta, dbias);
+  GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}
+
+}  // namespace gr_agg
+
 extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* mean,
                                   const float* rstd, const float* gamma, const float* beta,
                                   int32_t act, int64_t rows, int64_t dim, float* gh, float* dgamma,
@@ -1289,43 +1367,25 @@ extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* m
     vec = 1;
     nch = dim <= 64 ? 1 : (dim <= 128 ? 2 : 4);
   }
-  // Wavefront count: enough to fill the chip, bounded by the workspace
-  // (2 * nwaves * dim floats of partials + dim for the reduction pass).
-  int64_t nwaves = std::min<int64_t>(8192, std::max<int64_t>(4, (rows + 15) / 16));
-  nwaves = (nwaves + 3) / 4 * 4;
-  const int nparts = dbias != nullptr ? 3 : 2;
-  const int64_t cap = (workspace_floats / dim - 1) / nparts / 4 * 4;
-  GR_REQUIRE(cap >= 4, "ln_relu_backward: workspace too small");
-  if (nwaves > cap) nwaves = cap;
-  float* pg = workspace;
-  float* pb = workspace + nwaves * dim;
-  float* ph = dbias != nullptr ? workspace + 2 * nwaves * dim : nullptr;
   hipStream_t s = gr::as_stream(stream);
-  const int d = (int)dim;
-  const unsigned blocks = (unsigned)(nwaves / 4);
-#define GR_LNB(V, N)                                                                         \
-  do {                                                                                       \
-    if (act == GR_ACT_RELU)                                                                  \
-      hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N, GR_ACT_RELU>), dim3(blocks), dim3(256), \
-                         0, s, g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);      \
-    else                                                                                     \
-      hipLaunchKernelGGL((gr_agg::ln_relu_backward<V, N, GR_ACT_ELU>), dim3(blocks), dim3(256),  \
-                         0, s, g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);      \
-  } while (0)
   if (vec == 4) {
-    if (nch == 1) GR_LNB(4, 1); else if (nch == 2) GR_LNB(4, 2); else GR_LNB(4, 4);
-  } else {
-    if (nch == 1) GR_LNB(1, 1); else if (nch == 2) GR_LNB(1, 2); else GR_LNB(1, 4);
+    if (nch == 1)
+      return gr_agg::run_ln_backward<4, 1>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
+                                           dgamma, dbeta, dbias, workspace, workspace_floats, s);
+    if (nch == 2)
+      return gr_agg::run_ln_backward<4, 2>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
+                                           dgamma, dbeta, dbias, workspace, workspace_floats, s);
+    return gr_agg::run_ln_backward<4, 4>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
+                                         dgamma, dbeta, dbias, workspace, workspace_floats, s);
   }
-#undef GR_LNB
-  GR_HIP_CHECK(hipGetLastError());
-  // dgamma / dbeta (/ dbias) = column sums of the partials, in wavefront
-  // order: the partial matrices follow one another in the workspace, and
-  // one launch reduces all of them.
-  hipLaunchKernelGGL(gr_agg::colsum_final3, dim3(gr_agg::final_blocks(d), (unsigned)nparts),
-                     dim3(256), 0, s, pg, (int)nwaves, d, dgamma, dbeta, dbias);
-  GR_HIP_CHECK(hipGetLastError());
-  return GR_OK;
+  if (nch == 1)
+    return gr_agg::run_ln_backward<1, 1>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
+                                         dgamma, dbeta, dbias, workspace, workspace_floats, s);
+  if (nch == 2)
+    return gr_agg::run_ln_backward<1, 2>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
+                                         dgamma, dbeta, dbias, workspace, workspace_floats, s);
+  return gr_agg::run_ln_backward<1, 4>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
+                                       dgamma, dbeta, dbias, workspace, workspace_floats, s);
 }
 
 extern "C" int gr_bias_ln_act(const float* z, int64_t ldz, const float* bias,
