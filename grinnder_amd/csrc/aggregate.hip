@@ -819,7 +819,9 @@ hipError_t launch_units(const int4* units, int64_t n_units, const int32_t* idx,
                         const float* bias, int dim, float* ws, const int32_t* orow,
                         hipStream_t s) {
   constexpr int EPI = 64 / G;
-  constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
+  // Narrow rows (4 or more edge slots of at most 16 lanes) keep 8 edges a
+  // slot in flight: a 512-edge split unit then takes 8 rounds of loads, not 32.
+  constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 8);
   const int64_t blocks = (n_units + 3) / 4;
   hipLaunchKernelGGL((aggregate_units<VEC, G, NCH, U>), dim3((unsigned)blocks), dim3(256), 0, s,
                      units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow);
