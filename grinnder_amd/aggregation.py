@@ -344,10 +344,26 @@ def gcn_linear_aggregate(x: Tensor, weight: Tensor, adj: Adjacency,
     return _GCNLinearAggregatePadded.apply(x, weight, bias, plan)
 
 
+class RowDotSink:
+    """Carries c_i = <dL/dO_i, O_i> of a GAT attention output O from the
+    backward of the LayerNorm that consumes O + b (formed there while
+    dL/dO is in registers) to the attention's own backward, which uses it
+    only when the gradient it receives is that LayerNorm's output itself."""
+
+    __slots__ = ("cdot", "grad_ptr")
+
+    def __init__(self):
+        self.cdot: Optional[Tensor] = None
+        self.grad_ptr = 0
+
+
 def ln_act_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: Tensor,
-                    beta: Tensor, with_bias: bool = False, act: str = "relu"):
+                    beta: Tensor, with_bias: bool = False, act: str = "relu",
+                    shift: Optional[Tensor] = None, rowdot: Optional[Tensor] = None):
     """(dL/dh, dgamma, dbeta, dbias or None) of out = act(LayerNorm(h)) given
-    dL/dout (GPU); dbias = the column sums of dL/dh, formed in the same pass."""
+    dL/dout (GPU); dbias = the column sums of dL/dh, formed in the same pass.
+    With `rowdot` (a [rows] tensor) the pass also writes rowdot[r] =
+    <dL/dh_r, h_r - shift> (shift None: 0)."""
     gout = gout.contiguous()
     B, D = h.shape
     dev = h.device
@@ -361,9 +377,9 @@ def ln_act_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: 
                      device=dev)
     _lib.call("gr_ln_act_backward", gout.data_ptr(), h.data_ptr(), mean.data_ptr(),
               rstd.data_ptr(), gamma.data_ptr(), beta.data_ptr(), _lib.ACTIVATIONS[act], B, D,
-              gh.data_ptr(),
-              dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias), ws.data_ptr(), ws.numel(),
-              _lib.stream_handle())
+              gh.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias),
+              _lib.ptr(shift.contiguous() if shift is not None else None), _lib.ptr(rowdot),
+              ws.data_ptr(), ws.numel(), _lib.stream_handle())
     return gh, dgamma, dbeta, dbias
 
 
@@ -434,7 +450,8 @@ class _GATAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hs: Tensor, att_src: Tensor, att_dst: Tensor, bias: Optional[Tensor],
                 plan: DevicePlan, heads: int, channels: int, concat: bool,
-                s_pre: Optional[Tensor] = None, d_pre: Optional[Tensor] = None) -> Tensor:
+                s_pre: Optional[Tensor] = None, d_pre: Optional[Tensor] = None,
+                sink: Optional[RowDotSink] = None) -> Tensor:
         hs = hs.contiguous()
         dev = hs.device
         H, C = heads, channels
@@ -484,6 +501,7 @@ class _GATAttention(torch.autograd.Function):
         ctx.shape = (H, C, concat)
         ctx.has_bias = bias is not None
         ctx.att_shape = att_src.shape
+        ctx.sink = sink
         return y
 
     @staticmethod
@@ -501,9 +519,16 @@ class _GATAttention(torch.autograd.Function):
             go = (gy / H).unsqueeze(1).expand(B, H, C).reshape(B, HC).contiguous()
         db = column_sum(gy) if ctx.has_bias else None
         stream = _lib.stream_handle()
-        cdot = torch.empty((B, H), dtype=torch.float32, device=dev)
-        _lib.call("gr_gat_row_dot", go.data_ptr(), go.stride(0), o.data_ptr(), o.stride(0), B,
-                  H, C, cdot.data_ptr(), stream)
+        sink = ctx.sink
+        if (sink is not None and sink.cdot is not None and H == 1
+                and go.data_ptr() == sink.grad_ptr and sink.cdot.numel() == B):
+            # c_i came with this gradient from the LayerNorm that consumed O.
+            cdot = sink.cdot.view(B, 1)
+            sink.cdot = None
+        else:
+            cdot = torch.empty((B, H), dtype=torch.float32, device=dev)
+            _lib.call("gr_gat_row_dot", go.data_ptr(), go.stride(0), o.data_ptr(), o.stride(0),
+                      B, H, C, cdot.data_ptr(), stream)
         nnz = plan.nnz
         region = KernelTimer.region(
             "gat_bwd", nnz * (8 * HC + 16 * H + 8) + E * (4 * HC + 4 * H) + B * (4 * HC + 4 * H),
@@ -533,7 +558,7 @@ class _GATAttention(torch.autograd.Function):
         datt_src = column_sum(hs, ds, C)
         datt_dst = column_sum(hs[:B], dd, C)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
-                None, None, None, None, None, None)
+                None, None, None, None, None, None, None)
 
 
 def gat_scores(hs: Tensor, att_src: Tensor, att_dst: Tensor, heads: int, channels: int,
@@ -559,13 +584,16 @@ def gat_scores(hs: Tensor, att_src: Tensor, att_dst: Tensor, heads: int, channel
 def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
                   bias: Optional[Tensor], heads: int, channels: int,
                   concat: bool = True,
-                  scores: Optional[Tuple[Tensor, Tensor]] = None) -> Tensor:
+                  scores: Optional[Tuple[Tensor, Tensor]] = None,
+                  rowdot_sink: Optional[RowDotSink] = None) -> Tensor:
     """GATConv attention over a bipartite partition adjacency, on the GPU.
 
     hs = lin(x) for all E source rows; destination features are hs[:B].
     Returns [B, H*C] (concat) or [B, C] (mean over heads), bias added.
     `scores`, when given, are the logit halves (s [E, H], d [B, H]) formed
     beforehand by gat_scores, so they are not formed again here.
+    `rowdot_sink`: shared with the bias_ln_act that consumes this output, so
+    that its backward hands over c_i (one head).
     """
     _check_device_tensor("hs", hs)
     plan = adj.device_plan(hs.device)
@@ -574,8 +602,10 @@ def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
     if hs.size(1) != heads * channels:
         raise ValueError(f"hs has {hs.size(1)} features, expected {heads * channels}")
     if scores is None:
-        return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat)
+        return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat,
+                                   None, None, rowdot_sink)
     s, d = scores
     if tuple(s.shape) != (plan.num_src, heads) or tuple(d.shape) != (plan.num_dst, heads):
         raise ValueError("gat_attention: scores do not match the adjacency and heads")
-    return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat, s, d)
+    return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat, s, d,
+                               rowdot_sink)

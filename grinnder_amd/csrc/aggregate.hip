@@ -440,7 +440,8 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, int dim, int64_t rows, float* __restrict__ gh,
     float* __restrict__ part_gamma, float* __restrict__ part_beta,
-    float* __restrict__ part_bias) {
+    float* __restrict__ part_bias, const float* __restrict__ shift,
+    float* __restrict__ rowdot) {
   const int lane = threadIdx.x & 63;
   const int64_t wid =
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -448,6 +449,7 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
   bool fvalid[NCH];
   int foff[NCH], fld[NCH];
   float gam[NCH][VEC], bet[NCH][VEC], dg[NCH][VEC], db[NCH][VEC], dh[NCH][VEC];
+  float shf[NCH][VEC];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     foff[ch] = (ch * 64 + lane) * VEC;
@@ -455,6 +457,12 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     fld[ch] = fvalid[ch] ? foff[ch] : dim - VEC;
     load_vec<VEC>(gamma + fld[ch], gam[ch]);
     load_vec<VEC>(beta + fld[ch], bet[ch]);
+    if (shift != nullptr) {
+      load_vec<VEC>(shift + fld[ch], shf[ch]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) shf[ch][j] = 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
       dg[ch][j] = 0.f;
@@ -514,6 +522,7 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
       }
       s1 = wave_sum64(s1) * inv_d;
       s2 = wave_sum64(s2) * inv_d;
+      float dot = 0.f;
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch) {
         if (!fvalid[ch]) continue;
@@ -522,8 +531,13 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
         for (int j = 0; j < VEC; ++j) {
           o[j] = rs * (gx[ch][j] - s1 - xh[ch][j] * s2);
           dh[ch][j] += o[j];
+          dot = fmaf(o[j], hc[ch][j] - shf[ch][j], dot);
         }
         store_vec<VEC>(gh + r * dim + foff[ch], o);
+      }
+      if (rowdot != nullptr) {
+        dot = wave_sum64(dot);
+        if (lane == 0) rowdot[r] = dot;
       }
     }
   }
@@ -1290,25 +1304,28 @@ template <int V, int N, int P>
 int run_ln_backward_p(int32_t act, const float* g, const float* h, const float* mean,
                       const float* rstd, const float* gamma, const float* beta, int64_t rows,
                       int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
-                      float* workspace, int64_t workspace_floats, hipStream_t s);
+                      const float* shift, float* rowdot, float* workspace,
+                      int64_t workspace_floats, hipStream_t s);
 
 template <int V, int N>
 int run_ln_backward(int32_t act, const float* g, const float* h, const float* mean,
                     const float* rstd, const float* gamma, const float* beta, int64_t rows,
                     int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
-                    float* workspace, int64_t workspace_floats, hipStream_t s) {
+                    const float* shift, float* rowdot, float* workspace,
+                    int64_t workspace_floats, hipStream_t s) {
   // Six rows in flight at 256 floats a row (measured: 1.52 ms for 2.45M rows at
   // 4.96 TB/s against 1.68 ms with one, 5.05 against 4.55 TB/s for 625k rows).
   return run_ln_backward_p<V, N, N == 1 ? 6 : 1>(act, g, h, mean, rstd, gamma, beta, rows, dim,
-                                                 gh, dgamma, dbeta, dbias, workspace,
-                                                 workspace_floats, s);
+                                                 gh, dgamma, dbeta, dbias, shift, rowdot,
+                                                 workspace, workspace_floats, s);
 }
 
 template <int V, int N, int P>
 int run_ln_backward_p(int32_t act, const float* g, const float* h, const float* mean,
                       const float* rstd, const float* gamma, const float* beta, int64_t rows,
                       int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
-                      float* workspace, int64_t workspace_floats, hipStream_t s) {
+                      const float* shift, float* rowdot, float* workspace,
+                      int64_t workspace_floats, hipStream_t s) {
   const void* kern = act == GR_ACT_RELU
                          ? reinterpret_cast<const void*>(&ln_relu_backward<V, N, GR_ACT_RELU, P>)
                          : reinterpret_cast<const void*>(&ln_relu_backward<V, N, GR_ACT_ELU, P>);
@@ -1330,10 +1347,10 @@ int run_ln_backward_p(int32_t act, const float* g, const float* h, const float* 
   const unsigned blocks = (unsigned)(nwaves / 4);
   if (act == GR_ACT_RELU)
     hipLaunchKernelGGL((ln_relu_backward<V, N, GR_ACT_RELU, P>), dim3(blocks), dim3(256), 0, s,
-                       g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);
+                       g, h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph, shift, rowdot);
   else
     hipLaunchKernelGGL((ln_relu_backward<V, N, GR_ACT_ELU, P>), dim3(blocks), dim3(256), 0, s, g,
-                       h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph);
+                       h, mean, rstd, gamma, beta, d, rows, gh, pg, pb, ph, shift, rowdot);
   GR_HIP_CHECK(hipGetLastError());
   // dgamma / dbeta (/ dbias) = column sums of the partials, in wavefront
   // order: the partial matrices follow one another in the workspace, and
@@ -1349,9 +1366,8 @@ int run_ln_backward_p(int32_t act, const float* g, const float* h, const float* 
 extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* mean,
                                   const float* rstd, const float* gamma, const float* beta,
                                   int32_t act, int64_t rows, int64_t dim, float* gh, float* dgamma,
-                                   float* dbeta, float* dbias, float* workspace,
-                                   int64_t workspace_floats,
-                                   void* stream) {
+                                  float* dbeta, float* dbias, const float* shift, float* rowdot,
+                                  float* workspace, int64_t workspace_floats, void* stream) {
   gr::clear_error();
   int vec, nch;
   GR_REQUIRE(rows >= 0 && dim >= 1 && fused_shape(dim, &vec, &nch),
@@ -1363,7 +1379,7 @@ extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* m
              "ln_relu_backward: NULL pointer");
   const bool al = gr_agg::aligned(g, 16) && gr_agg::aligned(h, 16) && gr_agg::aligned(gh, 16) &&
                   gr_agg::aligned(gamma, 16) && gr_agg::aligned(beta, 16) &&
-                  gr_agg::aligned(workspace, 16);
+                  gr_agg::aligned(workspace, 16) && (shift == nullptr || gr_agg::aligned(shift, 16));
   if (vec == 4 && !al) {
     GR_REQUIRE(dim <= 256, "ln_relu_backward: misaligned rows wider than 256");
     vec = 1;
@@ -1373,21 +1389,21 @@ extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* m
   if (vec == 4) {
     if (nch == 1)
       return gr_agg::run_ln_backward<4, 1>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
-                                           dgamma, dbeta, dbias, workspace, workspace_floats, s);
+                                           dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
     if (nch == 2)
       return gr_agg::run_ln_backward<4, 2>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
-                                           dgamma, dbeta, dbias, workspace, workspace_floats, s);
+                                           dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
     return gr_agg::run_ln_backward<4, 4>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
-                                         dgamma, dbeta, dbias, workspace, workspace_floats, s);
+                                         dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
   }
   if (nch == 1)
     return gr_agg::run_ln_backward<1, 1>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
-                                         dgamma, dbeta, dbias, workspace, workspace_floats, s);
+                                         dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
   if (nch == 2)
     return gr_agg::run_ln_backward<1, 2>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
-                                         dgamma, dbeta, dbias, workspace, workspace_floats, s);
+                                         dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
   return gr_agg::run_ln_backward<1, 4>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
-                                       dgamma, dbeta, dbias, workspace, workspace_floats, s);
+                                       dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
 }
 
 extern "C" int gr_bias_ln_act(const float* z, int64_t ldz, const float* bias,

@@ -166,7 +166,7 @@ class _BiasLNAct(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                eps: float, act: str) -> Tensor:
+                eps: float, act: str, sink=None) -> Tensor:
         z = z.contiguous()
         rows, dim = z.shape
         dev = z.device
@@ -182,25 +182,36 @@ class _BiasLNAct(torch.autograd.Function):
         ctx.save_for_backward(h, mean, rstd, g, bt)
         ctx.has_bias = bias is not None
         ctx.act = act
+        ctx.sink = sink
+        ctx.bias = b
         return out
 
     @staticmethod
     def backward(ctx, gout: Tensor):
         from grinnder_amd.aggregation import ln_act_backward
         h, mean, rstd, g, bt = ctx.saved_tensors
+        rowdot = None
+        if ctx.sink is not None:
+            # <dL/dz_r, z_r> with z = h - b, for the attention that produced z.
+            rowdot = torch.empty(h.size(0), dtype=torch.float32, device=h.device)
         gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias,
-                                                ctx.act)
-        return gh, db, dgamma, dbeta, None, None
+                                                ctx.act, shift=ctx.bias, rowdot=rowdot)
+        if ctx.sink is not None:
+            ctx.sink.cdot = rowdot
+            ctx.sink.grad_ptr = gh.data_ptr()
+        return gh, db, dgamma, dbeta, None, None, None
 
 
 def bias_ln_act(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                eps: float = 1e-5, act: str = "relu") -> Tensor:
+                eps: float = 1e-5, act: str = "relu", rowdot_sink=None) -> Tensor:
     """act(LayerNorm(z + bias)) over the rows of z (GPU, one pass); act is
-    "relu" or "elu" (alpha = 1)."""
+    "relu" or "elu" (alpha = 1).  `rowdot_sink` (an aggregation.RowDotSink
+    shared with the GAT attention that produced z): the backward also forms
+    <dL/dz_r, z_r> and leaves it there."""
     _check("z", z)
     if act not in _lib.ACTIVATIONS:
         raise ValueError(f"unknown activation {act!r}")
-    return _BiasLNAct.apply(z, bias, gamma, beta, eps, act)
+    return _BiasLNAct.apply(z, bias, gamma, beta, eps, act, rowdot_sink)
 
 
 def bias_ln_relu(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,

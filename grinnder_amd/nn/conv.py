@@ -119,13 +119,13 @@ class GATConv(Module):
 
     def forward(self, x: Union[Tensor, Tuple[Tensor, Tensor]], adj: Adjacency,
                 add_bias: bool = True, reuse: Optional[Tensor] = None,
-                keep: Optional[list] = None) -> Tensor:
+                keep: Optional[list] = None, rowdot_sink=None) -> Tensor:
         """add_bias=False leaves the bias out of the output, for a caller that
         adds it in a fused epilogue (the LayerNorm of GAT.forward_layer).
         keep: a list that receives this call's projection hs of the source
         rows (detached); reuse: such an hs from an earlier call on the same
         rows and weights, taken instead of the projection product (the
-        backward is unchanged)."""
+        backward is unchanged).  rowdot_sink: see attend."""
         bias = self.bias if add_bias else None
         num_dst = adj.sparse_sizes()[0]
         if isinstance(x, tuple):
@@ -155,18 +155,21 @@ class GATConv(Module):
         hs = linear(x_src, self.lin.weight, reuse=reuse)
         if keep is not None:
             keep.append(hs.detach())
-        return self.attend(hs, adj, add_bias)
+        return self.attend(hs, adj, add_bias, rowdot_sink=rowdot_sink)
 
     def _padded(self) -> int:
         """Zero columns added to one head of C channels, C not a multiple of 4."""
         return (-self.out_channels) % 4 if self.heads == 1 else 0
 
     def attend(self, hs: Tensor, adj: Adjacency, add_bias: bool = True,
-               scores: Optional[Tuple[Tensor, Tensor]] = None) -> Tensor:
+               scores: Optional[Tuple[Tensor, Tensor]] = None, rowdot_sink=None) -> Tensor:
         """The layer after its projection: attention over hs = lin(x) for all
         source rows.  One head of C channels, C not a multiple of 4, runs on hs
         and the attention parameters zero-padded to a multiple of 4 (as in
-        forward).  `scores`: the logit halves of these rows from scores()."""
+        forward).  `scores`: the logit halves of these rows from scores().
+        `rowdot_sink` (aggregation.RowDotSink): shared with the bias_ln_act
+        that consumes this output, whose backward then hands the attention's
+        backward c_i = <dL/dO_i, O_i> instead of it being formed again."""
         bias = self.bias if add_bias else None
         pad = self._padded()
         if pad:
@@ -176,7 +179,7 @@ class GATConv(Module):
                               self.concat, scores)
             return y[:, :self.out_channels]
         return gat_attention(hs, adj, self.att_src, self.att_dst, bias, self.heads,
-                             self.out_channels, self.concat, scores)
+                             self.out_channels, self.concat, scores, rowdot_sink)
 
     def scores(self, hs: Tensor) -> Tuple[Tensor, Tensor]:
         """The logit halves (s, d) of every row of hs, as attend forms them

@@ -9,6 +9,7 @@ import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import LayerNorm, ModuleList
 
+from grinnder_amd.aggregation import RowDotSink
 from grinnder_amd.dense import bias_ln_act
 from grinnder_amd.nn.base import GriNNderModel
 from grinnder_amd.nn.conv import GATConv
@@ -68,8 +69,10 @@ class GAT(GriNNderModel):
         conv = self.convs[layer]
         if self._fused_norm(layer, x):
             norm = self.norms[layer]
-            x = conv((x, x[:num_dst]), adj, add_bias=False, reuse=reuse, keep=keep)
-            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
+            sink = RowDotSink()
+            x = conv((x, x[:num_dst]), adj, add_bias=False, reuse=reuse, keep=keep,
+                     rowdot_sink=sink)
+            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu", sink)
         return self._finish(layer, conv((x, x[:num_dst]), adj, reuse=reuse, keep=keep))
 
     def input_projection(self, layer: int):
@@ -86,8 +89,9 @@ class GAT(GriNNderModel):
         conv = self.convs[layer]
         if self._fused_norm(layer, hs):
             norm = self.norms[layer]
-            x = conv.attend(hs, adj, add_bias=False, scores=scores)
-            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu")
+            sink = RowDotSink()
+            x = conv.attend(hs, adj, add_bias=False, scores=scores, rowdot_sink=sink)
+            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu", sink)
         return self._finish(layer, conv.attend(hs, adj, scores=scores))
 
     def projected_scores(self, layer: int, z: Tensor):

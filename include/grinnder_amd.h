@@ -297,14 +297,19 @@ int gr_gcn_aggregate_ln_relu(const int32_t* units, int64_t n_units,
  * g = dL/dout: writes
  * gh = dL/dh [rows, dim], dgamma [dim], dbeta [dim] and, when dbias != NULL,
  * dbias = sum_rows gh (the gradient of a bias added before the LayerNorm)
- * (deterministic: per-wavefront partials reduced in order).  workspace: at
- * least (k * 4 + 1) * dim floats with k = 3 when dbias != NULL, else 2; up to
- * (k * 8192 + 1) * dim are used. */
+ * (deterministic: per-wavefront partials reduced in order).  When rowdot !=
+ * NULL it also writes rowdot[r] = sum_f gh[r, f] * (h[r, f] - shift[f])
+ * (shift NULL: 0): with h = o + b and shift = b this is <dL/do_r, o_r>, the
+ * c_i of the attention backward of a GATConv whose output feeds the
+ * LayerNorm (grinnder/nn/gat.py:74-78), formed while gh is in registers.
+ * workspace: at least (k * 4 + 1) * dim floats with k = 3 when dbias != NULL,
+ * else 2; up to (k * 8192 + 1) * dim are used. */
 int gr_ln_act_backward(const float* g, const float* h, const float* mean,
                        const float* rstd, const float* gamma, const float* beta,
                        int32_t act, int64_t rows, int64_t dim, float* gh,
-                       float* dgamma, float* dbeta, float* dbias, float* workspace,
-                       int64_t workspace_floats, void* stream);
+                       float* dgamma, float* dbeta, float* dbias, const float* shift,
+                       float* rowdot, float* workspace, int64_t workspace_floats,
+                       void* stream);
 
 /* Column sums out[f] = sum_i X[i, f] (w == NULL), or weighted sums
  * out[f] = sum_i w[i * ldw + f / group] * X[i, f] (fp32, deterministic: fixed

@@ -212,6 +212,64 @@ def test_bias_ln_elu_matches_fp64(gpu, rows, dim, bias):
         assert max_abs_norm_err(b.grad, bd.grad) <= TOL
 
 
+@pytest.mark.parametrize("rows,dim,shift", [(3000, 256, True), (777, 48, False), (50, 300, True),
+                                            (130, 7, True)])
+def test_ln_act_backward_row_dot(gpu, rows, dim, shift):
+    """gr_ln_act_backward's row dot <gh_r, h_r - shift> against the same dot of
+    its own gh in float64 (16-byte and scalar rows, several chunks a row)."""
+    from grinnder_amd.aggregation import ln_act_backward
+    h = _randn(rows, dim, seed=dim, dev=gpu)
+    g = _randn(rows, dim, seed=dim + 1, dev=gpu)
+    mean = h.mean(1)
+    rstd = 1.0 / (h.var(1, unbiased=False) + 1e-5).sqrt()
+    gamma = 1 + 0.1 * _randn(dim, seed=2, dev=gpu)
+    beta = 0.1 * _randn(dim, seed=3, dev=gpu)
+    sh = _randn(dim, seed=4, dev=gpu) if shift else None
+    rowdot = torch.empty(rows, device=gpu)
+    gh, dgamma, dbeta, _ = ln_act_backward(g, h, mean, rstd, gamma, beta, False, "elu",
+                                           shift=sh, rowdot=rowdot)
+    gh0, dgamma0, dbeta0, _ = ln_act_backward(g, h, mean, rstd, gamma, beta, False, "elu")
+    assert torch.equal(gh, gh0) and torch.equal(dgamma, dgamma0) and torch.equal(dbeta, dbeta0)
+    z = h.double() - (sh.double() if shift else 0.0)
+    terms = gh.double() * z
+    # Without a shift the dot cancels (a LayerNorm input gradient is
+    # orthogonal to its input up to eps), so the error is bounded by the
+    # size of the terms, as for any fp32 dot product.
+    err = (rowdot.double() - terms.sum(1)).abs() / terms.abs().sum(1).clamp_min(1e-30)
+    assert float(err.max()) <= TOL
+    if shift:
+        assert max_abs_norm_err(rowdot, terms.sum(1)) <= TOL
+
+
+def test_gat_layer_row_dot_handoff(gpu):
+    """A GAT attention whose output feeds bias_ln_act through a RowDotSink
+    takes c_i from the LayerNorm's backward: same gradients as without the
+    sink (where the attention forms c_i itself), and the hand-off is used."""
+    from grinnder_amd.aggregation import RowDotSink, gat_attention
+    from grinnder_amd.data.adjacency import Adjacency
+    from tests.graphs import random_bipartite
+    B, E, C = 600, 900, 64
+    rowptr, col, val = random_bipartite(B, E, 9, seed=3, long_rows=2, long_len=700)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=512)
+    grads = []
+    for use_sink in (False, True):
+        hs = _randn(E, C, seed=1, dev=gpu).requires_grad_(True)
+        a_s = (0.5 * _randn(1, 1, C, seed=2, dev=gpu)).requires_grad_(True)
+        a_d = (0.5 * _randn(1, 1, C, seed=3, dev=gpu)).requires_grad_(True)
+        b = _randn(C, seed=4, dev=gpu).requires_grad_(True)
+        gamma = (1 + 0.1 * _randn(C, seed=5, dev=gpu)).requires_grad_(True)
+        beta = (0.1 * _randn(C, seed=6, dev=gpu)).requires_grad_(True)
+        sink = RowDotSink() if use_sink else None
+        x = gat_attention(hs, adj, a_s, a_d, None, 1, C, True, rowdot_sink=sink)
+        out = bias_ln_act(x, b, gamma, beta, 1e-5, "elu", sink)
+        out.backward(_randn(B, C, seed=7, dev=gpu))
+        if use_sink:
+            assert sink.cdot is None  # handed over and consumed
+        grads.append([t.grad.clone() for t in (hs, a_s, a_d, b, gamma, beta)])
+    for g0, g1 in zip(*grads):
+        assert max_abs_norm_err(g1, g0.double()) <= TOL
+
+
 @pytest.mark.parametrize("rows,din,dout,act", [(5000, 100, 256, "relu"), (777, 37, 48, "elu"),
                                                (64, 3, 16, "relu"), (0, 8, 32, "relu")])
 def test_linear_ln_act_matches_fp64(gpu, rows, din, dout, act):
