@@ -51,7 +51,7 @@ _SIGNATURES = {
                               _P, _i64, _P],
     "gr_gather_rows": [_P, _i64, _i64, _P, _i64, _i64, _P, _i64, _P],
     "gr_scatter_add_rows": [_P, _i64, _i64, _i64, _P, _P, _i64, _i64, _P],
-    "gr_column_sum": [_P, _i64, _i64, _i64, _P, _i64, _i64, _P, _P, _i64, _P],
+    "gr_column_sum": [_P, _i64, _i64, _i64, _P, _P, _i64, _i64, _P, _P, _i64, _P],
     "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,
                                  _i64, _P, _P, _P, _P, _P, _i64, _P],
     "gr_ln_act_backward": [_P, _P, _P, _P, _P, _P, _i32, _i64, _i64, _P, _P, _P, _P, _P, _P,
@@ -72,6 +72,8 @@ _SIGNATURES = {
                        _P, _P, _P, _i64, _P, _i64, _i64, _P],
     "gr_gat_backward_src": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
+    "gr_gat_backward_src_into": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
+                                 _P, _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],
     "gr_io_create": [_i32, _P],

@@ -102,13 +102,19 @@ def _check_device_tensor(name: str, t: Tensor) -> None:
         raise RuntimeError(f"{name} must be float32; got {t.dtype}")
 
 
-def column_sum(g: Tensor, weights: Optional[Tensor] = None, group: int = 1) -> Tensor:
+def column_sum(g: Tensor, weights: Optional[Tensor] = None, group: int = 1,
+               rows_of: Optional[Tensor] = None) -> Tensor:
     """Sum over the rows of a [rows, D] fp32 device matrix (deterministic HIP
     kernel); with `weights` [rows, ceil(D / group)], row i of column f is
-    scaled by weights[i, f // group] first."""
+    scaled by weights[i, f // group] first.  With `rows_of` (int32, [n]) the
+    rows summed are g[rows_of[i]], i < n, read in place."""
     if g.stride(-1) != 1:
         g = g.contiguous()
     rows, dim = g.shape
+    if rows_of is not None:
+        if rows_of.dtype != torch.int32 or rows_of.dim() != 1:
+            raise ValueError("column_sum: rows_of must be a 1-D int32 tensor")
+        rows = rows_of.numel()
     out = torch.empty(dim, dtype=torch.float32, device=g.device)
     nblk = max(1, min(4096, (rows + 255) // 256))
     ws = torch.empty(nblk * dim, dtype=torch.float32, device=g.device)
@@ -117,7 +123,8 @@ def column_sum(g: Tensor, weights: Optional[Tensor] = None, group: int = 1) -> T
         w = weights.contiguous()
         if w.dim() != 2 or w.size(0) != rows or w.size(1) * group < dim:
             raise ValueError("column_sum: weights must be [rows, ceil(D / group)]")
-    _lib.call("gr_column_sum", g.data_ptr(), rows, dim, max(g.stride(0), dim), _lib.ptr(w),
+    _lib.call("gr_column_sum", g.data_ptr(), rows, dim, max(g.stride(0), dim),
+              _lib.ptr(rows_of), _lib.ptr(w),
               w.size(1) if w is not None else 0, group, out.data_ptr(), ws.data_ptr(),
               ws.numel(), _lib.stream_handle())
     return out
@@ -203,6 +210,9 @@ class ProjectedSink:
     gidx: Tensor
     rows: Optional[Tensor] = None
     token: Optional[Tensor] = None
+    # First global row of the partition's destination rows (its own rows,
+    # the first num_dst of `rows`); read by the attention backward.
+    lo: int = 0
 
 
 def spmm_into(plan, idx: Tensor, val: Tensor, x: Tensor, sink: ProjectedSink,
@@ -451,7 +461,11 @@ class _GATAttention(torch.autograd.Function):
     def forward(ctx, hs: Tensor, att_src: Tensor, att_dst: Tensor, bias: Optional[Tensor],
                 plan: DevicePlan, heads: int, channels: int, concat: bool,
                 s_pre: Optional[Tensor] = None, d_pre: Optional[Tensor] = None,
-                sink: Optional[RowDotSink] = None) -> Tensor:
+                sink: Optional[RowDotSink] = None, zsink: Optional[ProjectedSink] = None,
+                token: Optional[Tensor] = None) -> Tensor:
+        # zsink: hs is the matrix of all partitions' rows ([N, H*C], s_pre
+        # [N, H] alike), read in place through zsink.gidx; the backward adds
+        # dHs into zsink.dz at zsink.rows.
         hs = hs.contiguous()
         dev = hs.device
         H, C = heads, channels
@@ -483,8 +497,9 @@ class _GATAttention(torch.autograd.Function):
         b = bias.contiguous() if fused_bias else None
         ws_width = (HC + 3) // 4 * 4 + (2 * H + 3) // 4 * 4
         ws = _workspace(f.n_slots, ws_width, dev)
+        idx = plan.idx if zsink is None else zsink.gidx
         _lib.call("gr_gat_forward", f.units.data_ptr(), f.n_units,
-                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, plan.idx.data_ptr(),
+                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, idx.data_ptr(),
                   hs.data_ptr(), hs.stride(0), s.data_ptr(), d.data_ptr(), B, H, C, _lib.ptr(b),
                   m.data_ptr(), den.data_ptr(), alpha.data_ptr(), o.data_ptr(), _lib.ptr(y), HC,
                   _lib.ptr(ws), 0 if ws is None else ws.numel(), f.n_slots, stream)
@@ -502,6 +517,7 @@ class _GATAttention(torch.autograd.Function):
         ctx.has_bias = bias is not None
         ctx.att_shape = att_src.shape
         ctx.sink = sink
+        ctx.zsink = zsink
         return y
 
     @staticmethod
@@ -534,31 +550,51 @@ class _GATAttention(torch.autograd.Function):
             "gat_bwd", nnz * (8 * HC + 16 * H + 8) + E * (4 * HC + 4 * H) + B * (4 * HC + 4 * H),
             nnz, HC)
         region.__enter__()
-        dhs = torch.empty((E, HC), dtype=torch.float32, device=dev)
+        zsink = ctx.zsink
         ds = torch.empty((E, H), dtype=torch.float32, device=dev)
         gt = torch.empty((max(plan.nnz, 1), H), dtype=torch.float32, device=dev)
         bw = plan.bwd
         ws_stride = ((HC + 3) // 4) * 4 + ((H + 3) // 4) * 4
         ws = _workspace(bw.n_slots, ws_stride, dev)
-        _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
-                  bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
-                  plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(), hs.stride(0),
-                  go.data_ptr(), s.data_ptr(), d.data_ptr(), alpha.data_ptr(),
-                  cdot.data_ptr(), a_src.data_ptr(), H, C, dhs.data_ptr(), ds.data_ptr(),
-                  gt.data_ptr(), _lib.ptr(ws), bw.n_slots, stream)
+        if zsink is None:
+            dhs = torch.empty((E, HC), dtype=torch.float32, device=dev)
+            _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
+                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
+                      hs.stride(0), go.data_ptr(), s.data_ptr(), d.data_ptr(),
+                      alpha.data_ptr(), cdot.data_ptr(), a_src.data_ptr(), H, C,
+                      dhs.data_ptr(), ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws), bw.n_slots,
+                      stream)
+            dst_rows = dhs
+        else:
+            # dHs straight into dZ at the partition's global rows; the
+            # destination part below adds into its own rows dZ[lo:lo+B].
+            dhs = None
+            _lib.call("gr_gat_backward_src_into", bw.units.data_ptr(), bw.n_units,
+                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
+                      hs.stride(0), zsink.rows.data_ptr(), go.data_ptr(), s.data_ptr(),
+                      d.data_ptr(), alpha.data_ptr(), cdot.data_ptr(), a_src.data_ptr(), H, C,
+                      zsink.dz.data_ptr(), ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws),
+                      bw.n_slots, stream)
+            dst_rows = zsink.dz[zsink.lo:zsink.lo + B]
         dd = torch.empty((B, H), dtype=torch.float32, device=dev)
         f = plan.fwd
         ws = _workspace(f.n_slots, H, dev)
         _lib.call("gr_gat_backward_dst", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix, gt.data_ptr(),
                   a_dst.data_ptr(), cdot.data_ptr(), den.data_ptr(), H, C, dd.data_ptr(),
-                  dhs.data_ptr(), _lib.ptr(ws), f.n_slots, stream)
+                  dst_rows.data_ptr(), _lib.ptr(ws), f.n_slots, stream)
         region.__exit__(None, None, None)
         # Attention-vector gradients: per head, ds[:,h]^T Hs[:, h] and dd[:,h]^T Hs[:B, h].
-        datt_src = column_sum(hs, ds, C)
-        datt_dst = column_sum(hs[:B], dd, C)
+        if zsink is None:
+            datt_src = column_sum(hs, ds, C)
+            datt_dst = column_sum(hs[:B], dd, C)
+        else:
+            datt_src = column_sum(hs, ds, C, rows_of=zsink.rows)
+            datt_dst = column_sum(hs[zsink.lo:zsink.lo + B], dd, C)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
-                None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, None)
 
 
 def gat_scores(hs: Tensor, att_src: Tensor, att_dst: Tensor, heads: int, channels: int,
@@ -585,7 +621,8 @@ def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
                   bias: Optional[Tensor], heads: int, channels: int,
                   concat: bool = True,
                   scores: Optional[Tuple[Tensor, Tensor]] = None,
-                  rowdot_sink: Optional[RowDotSink] = None) -> Tensor:
+                  rowdot_sink: Optional[RowDotSink] = None,
+                  sink: Optional[ProjectedSink] = None) -> Tensor:
     """GATConv attention over a bipartite partition adjacency, on the GPU.
 
     hs = lin(x) for all E source rows; destination features are hs[:B].
@@ -594,13 +631,30 @@ def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
     beforehand by gat_scores, so they are not formed again here.
     `rowdot_sink`: shared with the bias_ln_act that consumes this output, so
     that its backward hands over c_i (one head).
+    `sink`: hs is the [N, H*C] matrix of all partitions' rows (one head of a
+    multiple of 4 in 68..1024 channels), read in place through sink.gidx with
+    `scores` = (s of all N rows, d of the partition's rows); the backward adds
+    dHs into sink.dz at sink.rows and returns no gradient for hs.
     """
     _check_device_tensor("hs", hs)
     plan = adj.device_plan(hs.device)
-    if hs.size(0) != plan.num_src:
-        raise ValueError(f"hs has {hs.size(0)} rows, adjacency has {plan.num_src} columns")
     if hs.size(1) != heads * channels:
         raise ValueError(f"hs has {hs.size(1)} features, expected {heads * channels}")
+    if sink is not None:
+        if heads != 1 or channels % 4 != 0 or not 64 < channels <= 1024 or scores is None:
+            raise ValueError("gat_attention: reading hs in place needs one head of 68..1024 "
+                             "channels (a multiple of 4) and precomputed scores")
+        s, d = scores
+        if (sink.gidx.numel() != plan.nnz or sink.rows.numel() != plan.num_src
+                or sink.dz is None or tuple(sink.dz.shape) != tuple(hs.shape)
+                or not sink.dz.is_contiguous() or s.size(0) != hs.size(0)
+                or tuple(d.shape) != (plan.num_dst, 1)
+                or not 0 <= sink.lo <= hs.size(0) - plan.num_dst):
+            raise ValueError("gat_attention: sink does not match the adjacency and hs")
+        return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat,
+                                   s, d, rowdot_sink, sink, sink.token)
+    if hs.size(0) != plan.num_src:
+        raise ValueError(f"hs has {hs.size(0)} rows, adjacency has {plan.num_src} columns")
     if scores is None:
         return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat,
                                    None, None, rowdot_sink)

@@ -612,13 +612,15 @@ __global__ __launch_bounds__(256) void colsum_partial(const float* __restrict__ 
                                                       int dim, int64_t ldx,
                                                       const float* __restrict__ w, int64_t ldw,
                                                       int group, int64_t chunk,
-                                                      float* __restrict__ part) {
+                                                      float* __restrict__ part,
+                                                      const int32_t* __restrict__ xrows) {
   const int64_t r0 = (int64_t)blockIdx.x * chunk;
   const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
   for (int f = threadIdx.x; f < dim; f += 256) {
     const int wf = WEIGHTED ? f / group : 0;
     auto val = [&](int64_t r) {
-      const float v = x[r * ldx + f];
+      const int64_t xr = xrows != nullptr ? (int64_t)xrows[r] : r;
+      const float v = x[xr * ldx + f];
       if constexpr (WEIGHTED) return v * w[r * ldw + wf];
       else return v;
     };
@@ -1177,8 +1179,9 @@ extern "C" int gr_scatter_add_rows(const float* x, int64_t n, int64_t dim, int64
 }
 
 extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
-                             const float* w, int64_t ldw, int64_t group, float* out,
-                             float* workspace, int64_t workspace_floats, void* stream) {
+                             const int32_t* xrows, const float* w, int64_t ldw, int64_t group,
+                             float* out, float* workspace, int64_t workspace_floats,
+                             void* stream) {
   gr::clear_error();
   GR_REQUIRE(rows >= 0 && dim >= 1 && ldx >= dim, "column_sum: bad shape");
   GR_REQUIRE(out != nullptr && (rows == 0 || x != nullptr), "column_sum: NULL pointer");
@@ -1196,10 +1199,10 @@ extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t 
   const int64_t chunk = rows == 0 ? 0 : (rows + nblk - 1) / nblk;
   if (w != nullptr)
     hipLaunchKernelGGL(gr_agg::colsum_partial<true>, dim3((unsigned)nblk), dim3(256), 0, s, x,
-                       rows, (int)dim, ldx, w, ldw, (int)group, chunk, workspace);
+                       rows, (int)dim, ldx, w, ldw, (int)group, chunk, workspace, xrows);
   else
     hipLaunchKernelGGL(gr_agg::colsum_partial<false>, dim3((unsigned)nblk), dim3(256), 0, s, x,
-                       rows, (int)dim, ldx, nullptr, 0, 1, chunk, workspace);
+                       rows, (int)dim, ldx, nullptr, 0, 1, chunk, workspace, xrows);
   GR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(gr_agg::colsum_final, dim3(gr_agg::final_blocks(dim)), dim3(256), 0, s,
                      workspace, (int)nblk, (int)dim, out);

@@ -836,12 +836,15 @@ __global__ __launch_bounds__(256) void gat_bwd_src_kernel(
   }
 }
 
+// With src_rows the row goes to dhs row src_rows[row] and is added to what
+// that row holds (accumulate into a gradient matrix of all partitions' rows).
 __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restrict__ fix,
                                                          int64_t n_fix,
                                                          const float* __restrict__ ws, int H,
                                                          int C, const float* __restrict__ att_src,
                                                          float* __restrict__ dhs,
-                                                         float* __restrict__ ds) {
+                                                         float* __restrict__ ds,
+                                                         const int32_t* __restrict__ src_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t wid = wave_id();
   if (wid >= n_fix) return;
@@ -857,7 +860,12 @@ __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restri
       acc += p[f];
       dsum += p[hc4 + h];
     }
-    dhs[(int64_t)row * HC + f] = fmaf(dsum, att_src[f], acc);
+    const float v = fmaf(dsum, att_src[f], acc);
+    if (src_rows != nullptr) {
+      dhs[(int64_t)src_rows[row] * HC + f] += v;
+    } else {
+      dhs[(int64_t)row * HC + f] = v;
+    }
     if (f == h * C) ds[(int64_t)row * H + h] = dsum;
   }
 }
@@ -879,7 +887,8 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
     const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
     const float* __restrict__ alpha, const float* __restrict__ cdot,
     const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
-    float* __restrict__ gt, float* __restrict__ ws, int min_len) {
+    float* __restrict__ gt, float* __restrict__ ws, int min_len,
+    const int32_t* __restrict__ src_rows) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int slot = (EPI == 1) ? 0 : lane / G;
@@ -890,6 +899,9 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
   // Whole columns shorter than min_len are gat_bwd_src_rows' work.
   if (w.w < 0 && w.z - w.y < min_len) return;
   const int64_t j = w.x;
+  // With src_rows, column j's rows of Hs, s and dHs are row src_rows[j] of
+  // matrices of all partitions' rows, and dHs is added to, not written.
+  const int64_t jr = src_rows != nullptr ? (int64_t)src_rows[j] : j;
 
   int foff[NCH], fld[NCH];
   bool fvalid[NCH];
@@ -899,13 +911,13 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
     foff[ch] = (ch * G + sub) * VEC;
     fvalid[ch] = foff[ch] < C;
     fld[ch] = fvalid[ch] ? foff[ch] : C - VEC;
-    ld<VEC>(hs + j * ldh + fld[ch], hsj[ch]);
+    ld<VEC>(hs + jr * ldh + fld[ch], hsj[ch]);
     if (!fvalid[ch]) {
 #pragma unroll
       for (int q = 0; q < VEC; ++q) hsj[ch][q] = 0.f;
     }
   }
-  const float sj = s[j];
+  const float sj = s[jr];
   float acc[NCH][VEC];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch)
@@ -994,7 +1006,15 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
       ld<VEC>(att_src + foff[ch], av);
 #pragma unroll
       for (int q = 0; q < VEC; ++q) av[q] = fmaf(dsl, av[q], acc[ch][q]);
-      st<VEC>(dhs + j * C + foff[ch], av);
+      if (src_rows != nullptr) {
+        float old[VEC];
+        ld<VEC>(dhs + jr * C + foff[ch], old);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) av[q] += old[q];
+        st<VEC>(dhs + jr * C + foff[ch], av);
+      } else {
+        st<VEC>(dhs + j * C + foff[ch], av);
+      }
     }
     if (lane == 0) ds[j] = dsl;
   } else {
@@ -1758,14 +1778,15 @@ static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_uni
                                 const int32_t* row_idx, const int32_t* perm, const float* hs,
                                 int64_t ldh, const float* go, const float* s, const float* d,
                                 const float* alpha, const float* cdot, const float* att_src,
-                                int C, float* dhs, float* ds, float* gt, float* ws, int min_len) {
+                                int C, float* dhs, float* ds, float* gt, float* ws, int min_len,
+                                const int32_t* src_rows) {
   constexpr int EPI = 64 / G;
   // Eight edges a slot in flight measured slower here (0.194 against 0.185 ms
   // for a C5 partition's 20-wide backward): each edge also does a group sum.
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
   hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src,
-                     C, dhs, ds, gt, ws, min_len);
+                     C, dhs, ds, gt, ws, min_len, src_rows);
   return hipGetLastError();
 }
 
@@ -1775,10 +1796,10 @@ static hipError_t dispatch_bwd_h1(int chunks, hipStream_t st, const int4* units,
                                   const float* hs, int64_t ldh, const float* go, const float* s,
                                   const float* d, const float* alpha, const float* cdot,
                                   const float* att_src, int C, float* dhs, float* ds, float* gt,
-                                  float* ws, int min_len = 0) {
+                                  float* ws, int min_len = 0, const int32_t* src_rows = nullptr) {
 #define GR_BH(G, N)                                                                      \
   return launch_bwd_h1<VEC, G, N>(st, units, n_units, row_idx, perm, hs, ldh, go, s, d,  \
-                                  alpha, cdot, att_src, C, dhs, ds, gt, ws, min_len)
+                                  alpha, cdot, att_src, C, dhs, ds, gt, ws, min_len, src_rows)
   if (chunks <= 8) GR_BH(8, 1);
   if (chunks <= 16) GR_BH(16, 1);
   if (chunks <= 32) GR_BH(32, 1);
@@ -1898,7 +1919,43 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   GR_HIP_CHECK(err);
   if (n_fix > 0) {
     hipLaunchKernelGGL(gat_bwd_src_fixup, dim3(blocks_for(n_fix)), dim3(256), 0, st, fixups,
-                       n_fix, workspace, H, C, att_src, dhs, ds);
+                       n_fix, workspace, H, C, att_src, dhs, ds, nullptr);
+    GR_HIP_CHECK(hipGetLastError());
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
+                                        const int32_t* fixups, int64_t n_fix,
+                                        const int32_t* row_idx, const int32_t* perm,
+                                        const float* hs, int64_t ldh, const int32_t* src_rows,
+                                        const float* go, const float* s, const float* d,
+                                        const float* alpha, const float* cdot,
+                                        const float* att_src, int64_t heads, int64_t channels,
+                                        float* dz, float* ds, float* gt, float* workspace,
+                                        int64_t n_slots, void* stream) {
+  gr::clear_error();
+  int rc = check_heads(heads, channels);
+  if (rc) return rc;
+  const int64_t C = channels;
+  GR_REQUIRE(heads == 1 && C % 4 == 0 && C > 64 && C <= 1024,
+             "gat_backward_src_into: one head of 68..1024 channels, a multiple of 4");
+  GR_REQUIRE(ldh >= C && ldh % 4 == 0, "gat_backward_src_into: bad ldh");
+  GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_backward_src_into: NULL fixups/workspace");
+  if (n_units == 0) return GR_OK;
+  GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && aligned16(hs) && src_rows &&
+                 go && aligned16(go) && s && d && alpha && cdot && att_src &&
+                 aligned16(att_src) && dz && aligned16(dz) && ds && gt &&
+                 (workspace == nullptr || aligned16(workspace)),
+             "gat_backward_src_into: NULL or misaligned pointer");
+  hipStream_t st = gr::as_stream(stream);
+  const int4* u4 = reinterpret_cast<const int4*>(units);
+  GR_HIP_CHECK(dispatch_bwd_h1<4>((int)(C / 4), st, u4, n_units, row_idx, perm, hs, ldh, go, s,
+                                  d, alpha, cdot, att_src, (int)C, dz, ds, gt, workspace, 0,
+                                  src_rows));
+  if (n_fix > 0) {
+    hipLaunchKernelGGL(gat_bwd_src_fixup, dim3(blocks_for(n_fix)), dim3(256), 0, st, fixups,
+                       n_fix, workspace, 1, (int)C, att_src, dz, ds, src_rows);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;

@@ -403,7 +403,8 @@ class ProjectedLayers:
         ids = self._gids(pid)
         if self._token is None:
             self._token = torch.zeros(0, device=self.device, requires_grad=True)
-        return ProjectedSink(self._dzbuf(layer), ids[0], ids[1], self._token)
+        return ProjectedSink(self._dzbuf(layer), ids[0], ids[1], self._token,
+                             self.graph._range(pid)[0])
 
     def _device_call(self, layer: int, pid: int, grad: bool) -> Tensor:
         """forward_projected on partition pid: reading Z in place through a
@@ -435,7 +436,12 @@ class ProjectedLayers:
             return out
         sink = self._sink(layer, pid)
         if sink is not None:
-            return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
+            sc = self._scores.get(layer)
+            if sc is None:
+                return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
+            lo, hi = self.graph._range(pid)
+            return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink,
+                                                scores=(sc[0], sc[1][lo:hi]))
         z = self._gather_projected(layer, pid, grad=grad)
         sc = self._scores.get(layer)
         if sc is None:

@@ -162,24 +162,29 @@ class GATConv(Module):
         return (-self.out_channels) % 4 if self.heads == 1 else 0
 
     def attend(self, hs: Tensor, adj: Adjacency, add_bias: bool = True,
-               scores: Optional[Tuple[Tensor, Tensor]] = None, rowdot_sink=None) -> Tensor:
+               scores: Optional[Tuple[Tensor, Tensor]] = None, rowdot_sink=None,
+               sink=None) -> Tensor:
         """The layer after its projection: attention over hs = lin(x) for all
         source rows.  One head of C channels, C not a multiple of 4, runs on hs
         and the attention parameters zero-padded to a multiple of 4 (as in
         forward).  `scores`: the logit halves of these rows from scores().
         `rowdot_sink` (aggregation.RowDotSink): shared with the bias_ln_act
         that consumes this output, whose backward then hands the attention's
-        backward c_i = <dL/dO_i, O_i> instead of it being formed again."""
+        backward c_i = <dL/dO_i, O_i> instead of it being formed again.
+        `sink` (aggregation.ProjectedSink): hs is the matrix of all
+        partitions' rows, read in place (gat_attention)."""
         bias = self.bias if add_bias else None
         pad = self._padded()
         if pad:
+            if sink is not None:
+                raise ValueError("GATConv.attend: a padded head reads gathered rows")
             b = F.pad(bias, (0, pad)) if bias is not None else None
             y = gat_attention(F.pad(hs, (0, pad)), adj, F.pad(self.att_src, (0, pad)),
                               F.pad(self.att_dst, (0, pad)), b, 1, self.out_channels + pad,
                               self.concat, scores)
             return y[:, :self.out_channels]
         return gat_attention(hs, adj, self.att_src, self.att_dst, bias, self.heads,
-                             self.out_channels, self.concat, scores, rowdot_sink)
+                             self.out_channels, self.concat, scores, rowdot_sink, sink)
 
     def scores(self, hs: Tensor) -> Tuple[Tensor, Tensor]:
         """The logit halves (s, d) of every row of hs, as attend forms them

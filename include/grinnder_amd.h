@@ -313,14 +313,15 @@ int gr_ln_act_backward(const float* g, const float* h, const float* mean,
 
 /* Column sums out[f] = sum_i X[i, f] (w == NULL), or weighted sums
  * out[f] = sum_i w[i * ldw + f / group] * X[i, f] (fp32, deterministic: fixed
- * row chunks, partials reduced in chunk order).  Replaces the bias gradient of
- * PyG GCNConv's / GATConv's "+ bias" (grinnder/nn/gcn.py:53-56,
- * grinnder/nn/gat.py:54-61) and, weighted by ds / dd with group = C, GATConv's
- * attention-vector gradients d att_src[h] = sum_j ds[j,h] Hs[j,h,:].
+ * row chunks, partials reduced in chunk order); with xrows != NULL, row i of
+ * X is row xrows[i] of x.  Replaces the bias gradient of PyG GCNConv's /
+ * GATConv's "+ bias" (grinnder/nn/gcn.py:53-56, grinnder/nn/gat.py:54-61)
+ * and, weighted by ds / dd with group = C, GATConv's attention-vector
+ * gradients d att_src[h] = sum_j ds[j,h] Hs[j,h,:].
  * workspace: at least D floats (up to 4096 * D are used for parallelism). */
 int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t ldx,
-                  const float* w, int64_t ldw, int64_t group, float* out,
-                  float* workspace, int64_t workspace_floats, void* stream);
+                  const int32_t* xrows, const float* w, int64_t ldw, int64_t group,
+                  float* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* Dense form of the fused epilogue, for a layer whose product Z was formed
  * outside the aggregation (aggregate-first GCN: Z = (A X) W^T; GAT output):
@@ -485,6 +486,24 @@ int gr_gat_backward_src(const int32_t* units, int64_t n_units,
                         const float* att_src, int64_t heads, int64_t channels,
                         float* dhs, float* ds, float* gt, float* workspace,
                         int64_t n_slots, void* stream);
+
+/* gr_gat_backward_src for one head of C channels (a multiple of 4 in
+ * 68..1024) read in place: source column j's rows of Hs and s are row
+ * src_rows[j] of hs ([N, ldh]) and s ([N]), matrices of all partitions' rows,
+ * and dHs_j is added into row src_rows[j] of dz ([N, C], dense) instead of
+ * being written (the src_rows of one partition are distinct).  Replaces the
+ * gather of the partition's rows of lin(x) before PyG GATConv's attention
+ * (grinnder/nn/gat.py:72-73) and the scatter of their gradient after it; ds
+ * and gt stay per partition.  workspace as gr_gat_backward_src. */
+int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
+                             const int32_t* fixups, int64_t n_fix,
+                             const int32_t* row_idx, const int32_t* perm,
+                             const float* hs, int64_t ldh, const int32_t* src_rows,
+                             const float* go, const float* s, const float* d,
+                             const float* alpha, const float* cdot,
+                             const float* att_src, int64_t heads, int64_t channels,
+                             float* dz, float* ds, float* gt, float* workspace,
+                             int64_t n_slots, void* stream);
 
 /* Backward over destination rows i (CSR plan):
  * dd[i,h] = sum_e gt[e,h] + cdot[i,h] * 1e-16 / den[i,h] (= sum_j g_t,ij) and

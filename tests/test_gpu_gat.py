@@ -218,3 +218,49 @@ def test_gat_row_dot_matches_fp64(gpu, rows, H, C):
         return
     ref = (a.double().view(rows, H, C) * b.double().view(rows, H, C)).sum(-1)
     assert max_abs_norm_err(out.cpu(), ref) <= TOL
+
+
+@pytest.mark.parametrize("C", [256, 128])
+def test_gat_attention_in_place_matches_gathered(gpu, C):
+    """One head read in place (the projected flow's ProjectedSink: edge
+    sources as global rows of Z, dHs added into dZ at the partition's rows)
+    gives the same output, dZ and attention-vector gradients, bit for bit,
+    as the same partition on its gathered rows of Z with the gradient
+    scattered back."""
+    from grinnder_amd.aggregation import ProjectedSink, gat_scores
+    N, B, E, lo = 3000, 500, 1400, 700
+    rowptr, col, val = random_bipartite(B, E, 9, seed=C, long_rows=2, long_len=900)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=512)
+    g = torch.Generator().manual_seed(C)
+    others = torch.cat([torch.arange(0, lo), torch.arange(lo + B, N)])
+    rows = torch.cat([torch.arange(lo, lo + B),
+                      others[torch.randperm(others.numel(), generator=g)[:E - B]]])
+    z = torch.randn(N, C, generator=g).to(gpu)
+    att_s = (0.5 * torch.randn(1, 1, C, generator=g)).to(gpu)
+    att_d = (0.5 * torch.randn(1, 1, C, generator=g)).to(gpu)
+    bias = torch.randn(C, generator=g).to(gpu)
+    gy = torch.randn(B, C, generator=g).to(gpu)
+    s_all, d_all = gat_scores(z, att_s, att_d, 1, C, N)
+    rg = rows.to(gpu)
+    outs = []
+    for in_place in (False, True):
+        a_s = att_s.clone().requires_grad_(True)
+        a_d = att_d.clone().requires_grad_(True)
+        b = bias.clone().requires_grad_(True)
+        dz = torch.zeros(N, C, device=gpu)
+        if in_place:
+            sink = ProjectedSink(dz, rows[col].to(torch.int32).to(gpu), rg.to(torch.int32),
+                                 torch.zeros(0, device=gpu, requires_grad=True), lo)
+            y = gat_attention(z, adj, a_s, a_d, b, 1, C, True,
+                              scores=(s_all, d_all[lo:lo + B]), sink=sink)
+            y.backward(gy)
+        else:
+            hs = z[rg].clone().requires_grad_(True)
+            y = gat_attention(hs, adj, a_s, a_d, b, 1, C, True,
+                              scores=(s_all[rg], d_all[lo:lo + B]))
+            y.backward(gy)
+            dz.index_add_(0, rg, hs.grad)
+        torch.cuda.synchronize()
+        outs.append((y.detach(), dz, a_s.grad, a_d.grad, b.grad))
+    for t0, t1 in zip(*outs):
+        assert torch.equal(t0, t1)
