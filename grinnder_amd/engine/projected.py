@@ -494,17 +494,18 @@ class ProjectedLayers:
         with torch.no_grad(), dense_region("fwd", hi - lo, w.size(1), w.size(0)):
             gemm_nt(x.detach(), w, out=z[lo:hi])
 
-    def _each_input_partition(self, layer: int, fn) -> None:
+    def _each_input_partition(self, layer: int, fn, whole=None) -> None:
         """fn(pid, x_p, lo, hi) on the compute stream for every partition,
         x_p = the partition's rows of the host buffer of layer `layer`'s
         inputs, uploaded to HBM: into the layer's resident input buffer when
         it has one this epoch, else through two buffers, so that the next
-        upload overlaps fn."""
+        upload overlaps fn.  `whole(x)`, when given, does the same work for
+        all rows at once; it runs instead when every row is already in HBM."""
         g, s, pids = self.graph, self.streams, self._my_pids
         host = self.host_features[layer]
         din = host.embedding_dim
         if layer in self._xin:
-            self._upload_resident(layer, fn)
+            self._upload_resident(layer, fn, whole)
             return
         bufs = self._xbufs.get(din)
         if bufs is None:
@@ -546,7 +547,7 @@ class ProjectedLayers:
                 freed[k] = ev
             ready = nxt
 
-    def _upload_resident(self, layer: int, fn) -> None:
+    def _upload_resident(self, layer: int, fn, whole=None) -> None:
         """_each_input_partition for layer 0's resident input buffer: every
         partition has its own rows there, so fn(p) waits only for partition
         p's upload.  The rows come from the upload the previous epoch started
@@ -569,14 +570,26 @@ class ProjectedLayers:
         if resident:
             self._x0loaded = idx
         x = self._xres[0] = self._x0bufs[idx]
+        if ready is None and whole is not None and len(pids) == g.num_parts:
+            # Every row is in HBM already: one call over all partitions'
+            # rows (contiguous in partition order) instead of one per
+            # partition, whose last partial wave of workgroups each launch
+            # would pay.
+            with torch.cuda.stream(s.compute):
+                whole(x)
+        else:
+            self._each_resident_partition(x, ready, fn)
+        if self._x0double:
+            self._x0pending = (1 - idx, self._issue_layer0_upload(1 - idx))
+
+    def _each_resident_partition(self, x: Tensor, ready, fn) -> None:
+        g, s, pids = self.graph, self.streams, self._my_pids
         for i, pid in enumerate(pids):
             if ready is not None:
                 s.compute.wait_event(ready[i])
             with torch.cuda.stream(s.compute):
                 lo, hi = g._range(pid)
                 fn(pid, x[lo:hi], lo, hi)
-        if self._x0double:
-            self._x0pending = (1 - idx, self._issue_layer0_upload(1 - idx))
 
     def _issue_layer0_upload(self, idx: int) -> List[torch.cuda.Event]:
         """Starts uploading every partition's layer-0 input rows into buffer
@@ -732,7 +745,8 @@ class ProjectedLayers:
                 self._upload_resident(0, lambda pid, x, lo, hi: None)
             elif layer in self._proj:
                 self._each_input_partition(
-                    0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi))
+                    0, lambda pid, x, lo, hi: self._project_rows(0, x, lo, hi),
+                    whole=lambda x: self._project_rows(0, x, 0, x.size(0)))
         self._scores.pop(layer, None)
         if layer in self._proj:
             with torch.cuda.stream(self.streams.compute):
