@@ -401,7 +401,9 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 // One head: the edge softmax and the weighted aggregation in one pass per
 // plan unit (row i, edges [y, z), slot).
 //   Pass 1, lanes parallel over the unit's edges: m = max_e v_e and
-//   sum = sum_e exp(v_e - m); the first 64 edges keep (col, v) in registers.
+//   sum = sum_e exp(v_e - m); a unit of up to kFwdChunks * 64 edges keeps
+//   every edge's (col, exp(v - m)) in registers, a longer one the first 64
+//   edges' (col, v).
 //   Pass 2, in 64-edge chunks: lane l forms the weight of edge l of the chunk,
 //   exp(v - m) / den for a whole row (den = sum + 1e-16) or the unscaled
 //   exp(v - m_k) of a split row's unit, stores it as alpha, and the wavefront
@@ -412,6 +414,10 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 // SpMM kernel, so whole rows give the same bits as gr_gat_softmax_stats
 // followed by gr_gat_aggregate.  Split rows leave (acc_k, m_k, sum_k) in
 // their workspace slot for gat_fused_fixup.
+// 64-edge chunks of a unit whose column ids and logits gat_fwd_fused keeps in
+// registers (gr_spmm_plan's units hold at most 512 edges).
+constexpr int kFwdChunks = 8;
+
 template <int VEC, int G, int NCH, int U>
 __global__ __launch_bounds__(256) void gat_fwd_fused(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
@@ -465,67 +471,35 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
 
   // Every load below is unconditional (indices clamped into the unit), so
   // the compiler can wait for each one alone: lanes past the unit's end read
-  // its last edge and get weight 0.  The column ids of the first 64 edges and
-  // their logits go out first; vector loads return in issue order, so the
-  // statistics can run while the first iteration's row loads (issued next,
-  // independent of the statistics) are still in flight.  Later iterations
-  // reuse the same registers.
+  // its last edge and get weight 0.  Vector loads return in issue order: the
+  // column ids and logits go out first, then the first U row gathers, which
+  // are independent of the statistics and stay in flight while they run.
   const float di = d[i];
-  const int c0 = idx[w.y + min(lane, len - 1)];
-  const float s0 = s[c0];
   float r[U][NCH][VEC];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    int c;
-    if constexpr (EPI == 1) {
-      c = __builtin_amdgcn_readlane(c0, u);
-    } else {
-      c = __shfl(c0, u * EPI + slot, 64);
-    }
-    const float* row = hs + (int64_t)c * ldh;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) ld<VEC>(row + fld[ch], r[u][ch]);
-  }
-
-  // Pass 1.
-  const float v0 = lane < len ? leaky(s0 + di) : -FLT_MAX;
-  float mx = v0;
-  for (int b = w.y + 64; b < w.z; b += 64) {
-    const float v = leaky(s[idx[min(b + lane, w.z - 1)]] + di);
-    if (b + lane < w.z) mx = fmaxf(mx, v);
-  }
-  mx = wave_max(mx);
-  float sum = lane < len ? expf(v0 - mx) : 0.f;
-  for (int b = w.y + 64; b < w.z; b += 64) {
-    const float v = leaky(s[idx[min(b + lane, w.z - 1)]] + di);
-    if (b + lane < w.z) sum += expf(v - mx);
-  }
-  sum = wave_sum(sum);
-  const bool whole = w.w < 0;
-  const float dn = whole ? sum + 1e-16f : 1.f;
-
-  // Pass 2.  Stores wait until a chunk's row loads are consumed: on gfx9 a
-  // wait for a load also waits for every store issued before it.
   float acc[NCH][VEC];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
     for (int q = 0; q < VEC; ++q) acc[ch][q] = 0.f;
-
-  for (int b = w.y; b < w.z; b += 64) {
-    const int n = min(64, w.z - b);
-    const bool ok = lane < n;
-    const bool first = b == w.y;
-    int cl;
-    float al;
-    if (first) {
-      cl = c0;
-      al = ok ? expf(v0 - mx) / dn : 0.f;
-    } else {
-      cl = idx[b + min(lane, n - 1)];
-      const float v = leaky(s[cl] + di);
-      al = ok ? expf(v - mx) / dn : 0.f;
+  // First U row gathers of the 64-edge chunk whose column ids are c0.
+  auto gather_first = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int c;
+      if constexpr (EPI == 1) {
+        c = __builtin_amdgcn_readlane(c0, u);
+      } else {
+        c = __shfl(c0, u * EPI + slot, 64);
+      }
+      const float* row = hs + (int64_t)c * ldh;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) ld<VEC>(row + fld[ch], r[u][ch]);
     }
+  };
+  // Aggregation of one 64-edge chunk: n edges from b, lane l holding column
+  // id cl and weight al of edge b + l; the first U gathers of the unit's
+  // first chunk are already in r.
+  auto aggregate_chunk = [&](int n, bool first, int cl, float al) {
     for (int k = 0; k < n; k += EPI * U) {
       int c[U];
       float a[U];
@@ -556,7 +530,99 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
 #pragma unroll
           for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a[u], r[u][ch][q], acc[ch][q]);
     }
-    if (ok) alpha[b + lane] = al;
+  };
+  const bool whole = w.w < 0;
+  float mx, sum, dn;
+  const int nchunks = (len + 63) >> 6;
+  if (nchunks <= kFwdChunks) {
+    // Units of up to kFwdChunks * 64 edges (every unit of gr_spmm_plan's
+    // 512-edge segments): all column ids and logits are loaded at once and
+    // kept in registers, so the unit costs one index load, one logit load
+    // and its row gathers in sequence, not three passes over the logits.
+    // Chunk k's values sit in cb[k] / eb[k]; the aggregation shifts them
+    // down one chunk at a time so that every register index is static.
+    int cb[kFwdChunks];
+    float eb[kFwdChunks];
+#pragma unroll
+    for (int k = 0; k < kFwdChunks; ++k) {
+      cb[k] = 0;
+      eb[k] = 0.f;
+      if (k < nchunks) cb[k] = idx[w.y + min(k * 64 + lane, len - 1)];
+    }
+#pragma unroll
+    for (int k = 0; k < kFwdChunks; ++k)
+      if (k < nchunks) eb[k] = s[cb[k]];
+    gather_first(cb[0]);
+    mx = -FLT_MAX;
+#pragma unroll
+    for (int k = 0; k < kFwdChunks; ++k)
+      if (k < nchunks) {
+        eb[k] = leaky(eb[k] + di);
+        if (k * 64 + lane < len) mx = fmaxf(mx, eb[k]);
+      }
+    mx = wave_max(mx);
+    sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kFwdChunks; ++k)
+      if (k < nchunks) {
+        eb[k] = k * 64 + lane < len ? expf(eb[k] - mx) : 0.f;
+        sum += eb[k];
+      }
+    sum = wave_sum(sum);
+    dn = whole ? sum + 1e-16f : 1.f;
+    for (int k = 0; k < nchunks; ++k) {
+      const int b = w.y + k * 64;
+      const int n = min(64, w.z - b);
+      const bool ok = lane < n;
+      const int cl = cb[0];
+      const float al = ok ? eb[0] / dn : 0.f;
+#pragma unroll
+      for (int q = 0; q + 1 < kFwdChunks; ++q) {
+        cb[q] = cb[q + 1];
+        eb[q] = eb[q + 1];
+      }
+      aggregate_chunk(n, k == 0, cl, al);
+      if (ok) alpha[b + lane] = al;
+    }
+  } else {
+    // Longer units: statistics in two passes over the logits, the first 64
+    // edges' (col, v) kept in registers.
+    const int c0 = idx[w.y + min(lane, len - 1)];
+    const float s0 = s[c0];
+    gather_first(c0);
+    const float v0 = lane < len ? leaky(s0 + di) : -FLT_MAX;
+    mx = v0;
+    for (int b = w.y + 64; b < w.z; b += 64) {
+      const float v = leaky(s[idx[min(b + lane, w.z - 1)]] + di);
+      if (b + lane < w.z) mx = fmaxf(mx, v);
+    }
+    mx = wave_max(mx);
+    sum = lane < len ? expf(v0 - mx) : 0.f;
+    for (int b = w.y + 64; b < w.z; b += 64) {
+      const float v = leaky(s[idx[min(b + lane, w.z - 1)]] + di);
+      if (b + lane < w.z) sum += expf(v - mx);
+    }
+    sum = wave_sum(sum);
+    dn = whole ? sum + 1e-16f : 1.f;
+    // Stores wait until a chunk's row loads are consumed: on gfx9 a wait for
+    // a load also waits for every store issued before it.
+    for (int b = w.y; b < w.z; b += 64) {
+      const int n = min(64, w.z - b);
+      const bool ok = lane < n;
+      const bool first = b == w.y;
+      int cl;
+      float al;
+      if (first) {
+        cl = c0;
+        al = ok ? expf(v0 - mx) / dn : 0.f;
+      } else {
+        cl = idx[b + min(lane, n - 1)];
+        const float v = leaky(s[cl] + di);
+        al = ok ? expf(v - mx) / dn : 0.f;
+      }
+      aggregate_chunk(n, first, cl, al);
+      if (ok) alpha[b + lane] = al;
+    }
   }
 
   if (lane == 0) {
@@ -1630,9 +1696,11 @@ static hipError_t launch_fused(hipStream_t st, const int4* units, int64_t n_unit
                                float* alpha, float* o, float* y, int64_t ldy, float* ws,
                                int64_t ws_stride, int min_len) {
   constexpr int EPI = 64 / G;
-  // Narrow rows (4 or more edge slots of at most 16 lanes) keep 8 edges a
-  // slot in flight: a 512-edge split unit then takes 8 rounds of loads, not 32.
-  constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 8);
+  // Narrow rows (4 or more edge slots of at most 16 lanes) keep 4 edges a
+  // slot in flight: with the unit's logits in registers this measured faster
+  // than 8 (5.58 against 5.75 ms for the 20-wide forward of C5's 64
+  // partitions) and than 2 (5.98 ms).
+  constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : 4;
   hipLaunchKernelGGL((gat_fwd_fused<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha, o, y, ldy,
                      ws, ws_stride, min_len);
