@@ -70,9 +70,10 @@ def gemm_tn(a: Tensor, b: Tensor, out: Optional[Tensor] = None, beta: float = 0.
 def gemm_nt(a: Tensor, b: Tensor, bias: Optional[Tensor] = None,
             out: Optional[Tensor] = None) -> Tensor:
     """C = a bᵀ (+ bias) for a [M, K] and b [N, K] fp32 device matrices with
-    unit column stride (rows may be strided) on the matrix cores; `out` is a
-    [M, N] matrix with unit column stride (for example a column slice of a
-    wider buffer), written in place."""
+    unit column stride (rows may be strided) on the matrix cores, or, for a
+    short reduction (K <= 64, N >= 64), as a stream of C's rows on the vector
+    units; `out` is a [M, N] matrix with unit column stride (for example a
+    column slice of a wider buffer), written in place."""
     _check("a", a)
     _check("b", b)
     if a.dim() != 2 or b.dim() != 2 or a.size(1) != b.size(1):

@@ -71,11 +71,15 @@ def test_gemm_tn_workspace_checked(gpu):
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (37, 7, 3), (1000, 20, 256), (777, 48, 100),
                                    (5000, 256, 1024), (300, 300, 64), (129, 65, 33),
                                    (4096, 16, 20), (70_000, 256, 48), (3000, 1024, 256),
-                                   (2500, 47, 256), (513, 130, 1)])
+                                   (2500, 47, 256), (513, 130, 1), (100_003, 256, 19),
+                                   (5000, 512, 20), (2001, 602, 47), (64, 64, 31), (1, 256, 63)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     """Every tile shape (n > 64, 33..64, 17..32, <= 16), K not a multiple of
-    the 32-wide step or of 4 (scalar loads), ragged row and column tiles."""
+    the 32-wide step or of 4 (scalar loads), ragged row and column tiles; the
+    short-reduction kernel (k <= 64 not a multiple of 4, n >= 64) with one to
+    five 128-column blocks, 8-byte and element stores, k just under its 32
+    and 64 register limits."""
     a = _randn(m, k, seed=m + k, dev=gpu)
     b = _randn(n, k, seed=n + k + 1, dev=gpu)
     bv = _randn(n, seed=n, dev=gpu) if bias else None
@@ -104,6 +108,17 @@ def test_gemm_nt_strided_and_in_place(gpu):
     odd = big_a[:, 1:257]  # 4-byte aligned only
     assert max_abs_norm_err(gemm_nt(odd, b), odd.double() @ b.double().t()) <= TOL
     assert gemm_nt(a[:0], b).shape == (0, 200)
+    # Short reduction (k = 19) with strided, unaligned a and b, into column
+    # slices whose start is 16-byte aligned (vector stores) or not.
+    sa, sb = big_a[:, 5:24], big_b[:, 3:22]
+    ref = sa.double() @ sb.double().t()
+    for c0 in (40, 41):
+        buf = _randn(9000, 320, seed=6, dev=gpu)
+        before = buf.clone()
+        gemm_nt(sa, sb, out=buf[:, c0:c0 + 200])
+        assert max_abs_norm_err(buf[:, c0:c0 + 200], ref) <= TOL
+        assert torch.equal(buf[:, :c0], before[:, :c0])
+        assert torch.equal(buf[:, c0 + 200:], before[:, c0 + 200:])
     with pytest.raises(ValueError, match="out must be"):
         gemm_nt(a, b, out=torch.empty(9000, 199, device=gpu))
 
