@@ -73,7 +73,7 @@ _SIGNATURES = {
     "gr_gat_backward_src": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_backward_src_into": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
-                                 _P, _i64, _i64, _P, _P, _P, _P, _i64, _P],
+                                 _P, _i64, _i64, _P, _P, _P, _P, _i64, _P, _i64, _P, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],
     "gr_io_create": [_i32, _P],

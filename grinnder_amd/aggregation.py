@@ -9,6 +9,7 @@ message aggregation (grinnder/nn/gat.py:54-61,73).
 from __future__ import annotations
 
 import contextlib
+import ctypes
 from dataclasses import dataclass
 from typing import List, Optional, Tuple
 
@@ -17,6 +18,7 @@ from torch import Tensor
 
 from grinnder_amd import _lib
 from grinnder_amd.data.adjacency import Adjacency, DevicePlan
+from grinnder_amd.dense import OutputRows, output_block
 
 
 @dataclass
@@ -400,14 +402,14 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
                 plan: DevicePlan, eps: float, sink: Optional[ProjectedSink] = None,
-                token: Optional[Tensor] = None) -> Tensor:
+                dest: Optional[OutputRows] = None, token: Optional[Tensor] = None) -> Tensor:
         z = z.contiguous()
         idx = plan.idx if sink is None else sink.gidx
         dev = z.device
         B, D = plan.num_dst, z.size(1)
         f = plan.fwd
         h = torch.empty((B, D), dtype=torch.float32, device=dev)
-        out = torch.empty((B, D), dtype=torch.float32, device=dev)
+        out = output_block(dest, B, D, dev)
         mean = torch.empty(B, dtype=torch.float32, device=dev)
         rstd = torch.empty(B, dtype=torch.float32, device=dev)
         ws = _workspace(f.n_slots, D, dev)
@@ -438,20 +440,28 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
                 spmm_into(plan.bwd, plan.row_idx, plan.val_t, gh, ctx.sink)
         elif ctx.needs_input_grad[0]:
             dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd")
-        return dz, db, dgamma, dbeta, None, None, None, None
+        return dz, db, dgamma, dbeta, None, None, None, None, None
 
 
 def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gamma: Tensor,
                           beta: Tensor, eps: float = 1e-5,
-                          sink: Optional[ProjectedSink] = None) -> Tensor:
+                          sink: Optional[ProjectedSink] = None,
+                          dest: Optional[OutputRows] = None) -> Tensor:
     """ReLU(LayerNorm(A·Z + bias)) of one partition in one fused pass (GPU);
-    a sink as in gcn_aggregate."""
+    a sink as in gcn_aggregate; `dest`: the output is written into that block
+    (dense.OutputRows) and returned as a view of it."""
     _check_device_tensor("z", z)
     plan = adj.device_plan(z.device)
     _check_source(z, plan, sink)
     if sink is None or sink.dz is None:
-        return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink)
-    return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, sink.token)
+        return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, dest)
+    return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, dest, sink.token)
+
+
+# Rows of per-wavefront partial sums the in-place GAT backward may use for the
+# attention-vector gradient (at most what the GPU holds at once is used; an
+# MI355X holds 256 CUs x 32 wavefronts): 8192 x C floats, 8 MB at C = 256.
+_ATT_PARTIAL_ROWS = 8192
 
 
 class _GATAttention(torch.autograd.Function):
@@ -569,14 +579,20 @@ class _GATAttention(torch.autograd.Function):
         else:
             # dHs straight into dZ at the partition's global rows; the
             # destination part below adds into its own rows dZ[lo:lo+B].
+            # The same pass forms per-wavefront partial sums of
+            # datt_src = sum_j ds_j Hs_j while Hs_j is in its registers.
             dhs = None
+            att_rows = min(bw.n_units, _ATT_PARTIAL_ROWS)
+            att_part = torch.empty((max(att_rows, 1), HC), dtype=torch.float32, device=dev)
+            att_waves = ctypes.c_int64(0)
             _lib.call("gr_gat_backward_src_into", bw.units.data_ptr(), bw.n_units,
                       bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
                       plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
                       hs.stride(0), zsink.rows.data_ptr(), go.data_ptr(), s.data_ptr(),
                       d.data_ptr(), alpha.data_ptr(), cdot.data_ptr(), a_src.data_ptr(), H, C,
                       zsink.dz.data_ptr(), ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws),
-                      bw.n_slots, stream)
+                      bw.n_slots, att_part.data_ptr(), att_part.size(0),
+                      ctypes.addressof(att_waves), stream)
             dst_rows = zsink.dz[zsink.lo:zsink.lo + B]
         dd = torch.empty((B, H), dtype=torch.float32, device=dev)
         f = plan.fwd
@@ -591,7 +607,10 @@ class _GATAttention(torch.autograd.Function):
             datt_src = column_sum(hs, ds, C)
             datt_dst = column_sum(hs[:B], dd, C)
         else:
-            datt_src = column_sum(hs, ds, C, rows_of=zsink.rows)
+            if att_waves.value > 0:
+                datt_src = column_sum(att_part[:att_waves.value])
+            else:  # no units: nothing summed
+                datt_src = torch.zeros(HC, dtype=torch.float32, device=dev)
             datt_dst = column_sum(hs[zsink.lo:zsink.lo + B], dd, C)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
                 None, None, None, None, None, None, None, None, None)

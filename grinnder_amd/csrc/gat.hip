@@ -25,6 +25,7 @@
 // pass per unit (gat_fwd_fused); several heads use the statistics kernel and
 // then gat_aggregate_kernel.
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 
 #include "gr_internal.h"
@@ -946,7 +947,16 @@ __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restri
 // chunk's row loads have been consumed: on gfx9 a wait for a load also waits
 // for every store issued before it.  Edges are assigned to slots and summed
 // in the same order as in gat_bwd_src_kernel.
-template <int VEC, int G, int NCH, int U>
+//
+// ATT: the wavefront also forms its share of the attention-vector gradient
+// datt_src = sum_j ds_j Hs_j while Hs_j is in its registers.  The grid is
+// then `waves` wavefronts (at most what the GPU holds at once); wavefront w
+// takes units w, w + waves, w + 2 waves, ..., adds each unit's (partial) ds
+// times Hs_j to its own sum, and writes that sum to att_part[w]; the caller
+// reduces the rows of att_part in order.  The result does not depend on
+// scheduling.  A split column's share is formed per unit from its partial ds
+// (the sum over its units is the same quantity, re-associated).
+template <int VEC, int G, int NCH, int U, bool ATT>
 __global__ __launch_bounds__(256) void gat_bwd_src_h1(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
     const int32_t* __restrict__ perm, const float* __restrict__ hs, int64_t ldh,
@@ -954,143 +964,168 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
     const float* __restrict__ alpha, const float* __restrict__ cdot,
     const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
     float* __restrict__ gt, float* __restrict__ ws, int min_len,
-    const int32_t* __restrict__ src_rows) {
+    const int32_t* __restrict__ src_rows, float* __restrict__ att_part, int64_t waves) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int slot = (EPI == 1) ? 0 : lane / G;
   const int sub = (EPI == 1) ? lane : lane % G;
-  const int64_t wid = wave_id();
-  if (wid >= n_units) return;
-  const int4 w = units[wid];
-  // Whole columns shorter than min_len are gat_bwd_src_rows' work.
-  if (w.w < 0 && w.z - w.y < min_len) return;
-  const int64_t j = w.x;
-  // With src_rows, column j's rows of Hs, s and dHs are row src_rows[j] of
-  // matrices of all partitions' rows, and dHs is added to, not written.
-  const int64_t jr = src_rows != nullptr ? (int64_t)src_rows[j] : j;
-
-  int foff[NCH], fld[NCH];
+  const int64_t first = wave_id();
+  if (first >= n_units || (ATT && first >= waves)) return;
+  int foff[NCH];
   bool fvalid[NCH];
-  float hsj[NCH][VEC];
+  float att[NCH][VEC];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     foff[ch] = (ch * G + sub) * VEC;
     fvalid[ch] = foff[ch] < C;
-    fld[ch] = fvalid[ch] ? foff[ch] : C - VEC;
-    ld<VEC>(hs + jr * ldh + fld[ch], hsj[ch]);
-    if (!fvalid[ch]) {
 #pragma unroll
-      for (int q = 0; q < VEC; ++q) hsj[ch][q] = 0.f;
-    }
+    for (int q = 0; q < VEC; ++q) att[ch][q] = 0.f;
   }
-  const float sj = s[jr];
-  float acc[NCH][VEC];
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[ch][q] = 0.f;
-  float dsl = 0.f;
+  const int64_t stride = ATT ? waves : n_units;
+  for (int64_t wid = first; wid < n_units; wid += stride) {
+    const int4 w = units[wid];
+    // Whole columns shorter than min_len are gat_bwd_src_rows' work.
+    if (w.w < 0 && w.z - w.y < min_len) continue;
+    const int64_t j = w.x;
+    // With src_rows, column j's rows of Hs, s and dHs are row src_rows[j] of
+    // matrices of all partitions' rows, and dHs is added to, not written.
+    const int64_t jr = src_rows != nullptr ? (int64_t)src_rows[j] : j;
 
-  for (int b = w.y; b < w.z; b += 64) {
-    const int n = min(64, w.z - b);
-    const int el = b + min(lane, n - 1);
-    const int il = row_idx[el];
-    const int pl = perm[el];
-    const float al = alpha[pl];
-    const float dl = d[il];
-    const float cl = cdot[il];
-    float gtv = 0.f;
-    for (int k = 0; k < n; k += EPI * U) {
-      int ii[U];
-      float a[U], dv[U], cv[U];
+    int fld[NCH];
+    float hsj[NCH][VEC];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if constexpr (EPI == 1) {
-          ii[u] = __builtin_amdgcn_readlane(il, k + u);
-          a[u] = __builtin_bit_cast(float,
-                                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, al), k + u));
-          dv[u] = __builtin_bit_cast(float,
-                                     __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k + u));
-          cv[u] = __builtin_bit_cast(float,
-                                     __builtin_amdgcn_readlane(__builtin_bit_cast(int, cl), k + u));
-        } else {
-          const int t = k + u * EPI + slot;
-          ii[u] = __shfl(il, t, 64);
-          a[u] = __shfl(al, t, 64);
-          dv[u] = __shfl(dl, t, 64);
-          cv[u] = __shfl(cl, t, 64);
-        }
+    for (int ch = 0; ch < NCH; ++ch) {
+      fld[ch] = fvalid[ch] ? foff[ch] : C - VEC;
+      ld<VEC>(hs + jr * ldh + fld[ch], hsj[ch]);
+      if (!fvalid[ch]) {
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) hsj[ch][q] = 0.f;
       }
-      float g[U][NCH][VEC];
+    }
+    const float sj = s[jr];
+    float acc[NCH][VEC];
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+    for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) ld<VEC>(go + (int64_t)ii[u] * C + fld[ch], g[u][ch]);
+      for (int q = 0; q < VEC; ++q) acc[ch][q] = 0.f;
+    float dsl = 0.f;
+
+    for (int b = w.y; b < w.z; b += 64) {
+      const int n = min(64, w.z - b);
+      const int el = b + min(lane, n - 1);
+      const int il = row_idx[el];
+      const int pl = perm[el];
+      const float al = alpha[pl];
+      const float dl = d[il];
+      const float cl = cdot[il];
+      float gtv = 0.f;
+      for (int k = 0; k < n; k += EPI * U) {
+        int ii[U];
+        float a[U], dv[U], cv[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float t = 0.f;
+        for (int u = 0; u < U; ++u) {
+          if constexpr (EPI == 1) {
+            ii[u] = __builtin_amdgcn_readlane(il, k + u);
+            a[u] = __builtin_bit_cast(float,
+                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, al), k + u));
+            dv[u] = __builtin_bit_cast(float,
+                                       __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k + u));
+            cv[u] = __builtin_bit_cast(float,
+                                       __builtin_amdgcn_readlane(__builtin_bit_cast(int, cl), k + u));
+          } else {
+            const int t = k + u * EPI + slot;
+            ii[u] = __shfl(il, t, 64);
+            a[u] = __shfl(al, t, 64);
+            dv[u] = __shfl(dl, t, 64);
+            cv[u] = __shfl(cl, t, 64);
+          }
+        }
+        float g[U][NCH][VEC];
 #pragma unroll
-        for (int ch = 0; ch < NCH; ++ch)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-          for (int q = 0; q < VEC; ++q) t = fmaf(g[u][ch][q], hsj[ch][q], t);
-        const float ga = gr_wave::group_sum<G>(t);
-        const float ge = a[u] * (ga - cv[u]);
-        const bool pos = sj + dv[u] > 0.f;
-        const int te = k + u * EPI + slot;  // this slot's edge in the chunk
-        if (te < n) {
-          dsl += pos ? ge : 0.2f * ge;
+          for (int ch = 0; ch < NCH; ++ch) ld<VEC>(go + (int64_t)ii[u] * C + fld[ch], g[u][ch]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float t = 0.f;
 #pragma unroll
           for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
-            for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a[u], g[u][ch][q], acc[ch][q]);
-        }
-        const float gv = pos ? 0.f : -0.8f * ge;
-        // Lane k + u * EPI + s collects the value of slot s.
-        const int src = lane - k - u * EPI;
-        if constexpr (EPI == 1) {
-          if (src == 0) gtv = gv;
-        } else {
-          const float v = __shfl(gv, (src & (EPI - 1)) * G, 64);
-          if (src >= 0 && src < EPI) gtv = v;
+            for (int q = 0; q < VEC; ++q) t = fmaf(g[u][ch][q], hsj[ch][q], t);
+          const float ga = gr_wave::group_sum<G>(t);
+          const float ge = a[u] * (ga - cv[u]);
+          const bool pos = sj + dv[u] > 0.f;
+          const int te = k + u * EPI + slot;  // this slot's edge in the chunk
+          if (te < n) {
+            dsl += pos ? ge : 0.2f * ge;
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+              for (int q = 0; q < VEC; ++q) acc[ch][q] = fmaf(a[u], g[u][ch][q], acc[ch][q]);
+          }
+          const float gv = pos ? 0.f : -0.8f * ge;
+          // Lane k + u * EPI + s collects the value of slot s.
+          const int src = lane - k - u * EPI;
+          if constexpr (EPI == 1) {
+            if (src == 0) gtv = gv;
+          } else {
+            const float v = __shfl(gv, (src & (EPI - 1)) * G, 64);
+            if (src >= 0 && src < EPI) gtv = v;
+          }
         }
       }
+      if (lane < n) gt[pl] = gtv;
     }
-    if (lane < n) gt[pl] = gtv;
-  }
 
-  dsl = gr_wave::slot_sum<G>(dsl);
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch)
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[ch][q] = gr_wave::slot_sum<G>(acc[ch][q]);
-  if (slot != 0) return;
-  if (w.w < 0) {
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      if (!fvalid[ch]) continue;
-      float av[VEC];
-      ld<VEC>(att_src + foff[ch], av);
-#pragma unroll
-      for (int q = 0; q < VEC; ++q) av[q] = fmaf(dsl, av[q], acc[ch][q]);
-      if (src_rows != nullptr) {
-        float old[VEC];
-        ld<VEC>(dhs + jr * C + foff[ch], old);
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) av[q] += old[q];
-        st<VEC>(dhs + jr * C + foff[ch], av);
-      } else {
-        st<VEC>(dhs + j * C + foff[ch], av);
-      }
-    }
-    if (lane == 0) ds[j] = dsl;
-  } else {
-    // Slot layout [acc (C) | ds], each part padded to 4 floats.
-    const int c4 = ((C + 3) / 4) * 4;
-    float* p = ws + (int64_t)w.w * (c4 + 4);
+    dsl = gr_wave::slot_sum<G>(dsl);
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch)
-      if (fvalid[ch]) st<VEC>(p + foff[ch], acc[ch]);
-    if (lane == 0) p[c4] = dsl;
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[ch][q] = gr_wave::slot_sum<G>(acc[ch][q]);
+    if constexpr (ATT) {
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) att[ch][q] = fmaf(dsl, hsj[ch][q], att[ch][q]);
+    }
+    if (slot == 0) {
+      if (w.w < 0) {
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+          if (!fvalid[ch]) continue;
+          float av[VEC];
+          ld<VEC>(att_src + foff[ch], av);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) av[q] = fmaf(dsl, av[q], acc[ch][q]);
+          if (src_rows != nullptr) {
+            float old[VEC];
+            ld<VEC>(dhs + jr * C + foff[ch], old);
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) av[q] += old[q];
+            st<VEC>(dhs + jr * C + foff[ch], av);
+          } else {
+            st<VEC>(dhs + j * C + foff[ch], av);
+          }
+        }
+        if (lane == 0) ds[j] = dsl;
+      } else {
+        // Slot layout [acc (C) | ds], each part padded to 4 floats.
+        const int c4 = ((C + 3) / 4) * 4;
+        float* p = ws + (int64_t)w.w * (c4 + 4);
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+          if (fvalid[ch]) st<VEC>(p + foff[ch], acc[ch]);
+        if (lane == 0) p[c4] = dsl;
+      }
+    }
+  }  // units of this wavefront
+  if constexpr (ATT) {
+    if (slot == 0) {
+      float* p = att_part + first * C;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+        if (fvalid[ch]) st<VEC>(p + foff[ch], att[ch]);
+    }
   }
 }
 
@@ -1841,20 +1876,58 @@ static hipError_t launch_gat_bwd(hipStream_t st, const int4* units, int64_t n_un
   return hipGetLastError();
 }
 
+// Wavefronts of gat_bwd_src_h1<VEC, G, NCH, U, true> the current device holds
+// at once (the kernel's occupancy times the CUs), counted once per device;
+// 0 when the query fails.
+template <int VEC, int G, int NCH, int U>
+static int64_t resident_waves_h1() {
+  constexpr int kDevices = 64;
+  static std::atomic<int64_t> cached[kDevices];
+  int dev = 0, cus = 0, blocks = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kDevices) {
+    const int64_t c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &blocks, gat_bwd_src_h1<VEC, G, NCH, U, true>, 256, 0) != hipSuccess ||
+      cus <= 0 || blocks <= 0)
+    return 0;
+  const int64_t waves = (int64_t)cus * blocks * 4;
+  if (dev < kDevices) cached[dev].store(waves, std::memory_order_relaxed);
+  return waves;
+}
+
+// att_part == nullptr: one wavefront per unit.  Otherwise the grid is
+// min(n_units, att_rows, resident waves) wavefronts that also form the
+// attention-vector gradient's partial sums (gat_bwd_src_h1's ATT); *att_waves
+// gets that count (0 when the occupancy query fails: an error).
 template <int VEC, int G, int NCH>
 static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_units,
                                 const int32_t* row_idx, const int32_t* perm, const float* hs,
                                 int64_t ldh, const float* go, const float* s, const float* d,
                                 const float* alpha, const float* cdot, const float* att_src,
                                 int C, float* dhs, float* ds, float* gt, float* ws, int min_len,
-                                const int32_t* src_rows) {
+                                const int32_t* src_rows, float* att_part = nullptr,
+                                int64_t att_rows = 0, int64_t* att_waves = nullptr) {
   constexpr int EPI = 64 / G;
   // Eight edges a slot in flight measured slower here (0.194 against 0.185 ms
   // for a C5 partition's 20-wide backward): each edge also does a group sum.
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 2);
-  hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
-                     st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src,
-                     C, dhs, ds, gt, ws, min_len, src_rows);
+  if (att_part == nullptr) {
+    hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U, false>), dim3(blocks_for(n_units)),
+                       dim3(256), 0, st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha,
+                       cdot, att_src, C, dhs, ds, gt, ws, min_len, src_rows, nullptr,
+                       (int64_t)0);
+    return hipGetLastError();
+  }
+  const int64_t waves = std::min(std::min(n_units, att_rows), resident_waves_h1<VEC, G, NCH, U>());
+  *att_waves = waves;
+  if (waves <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U, true>), dim3(blocks_for(waves)), dim3(256),
+                     0, st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot,
+                     att_src, C, dhs, ds, gt, ws, min_len, src_rows, att_part, waves);
   return hipGetLastError();
 }
 
@@ -1864,10 +1937,13 @@ static hipError_t dispatch_bwd_h1(int chunks, hipStream_t st, const int4* units,
                                   const float* hs, int64_t ldh, const float* go, const float* s,
                                   const float* d, const float* alpha, const float* cdot,
                                   const float* att_src, int C, float* dhs, float* ds, float* gt,
-                                  float* ws, int min_len = 0, const int32_t* src_rows = nullptr) {
-#define GR_BH(G, N)                                                                      \
-  return launch_bwd_h1<VEC, G, N>(st, units, n_units, row_idx, perm, hs, ldh, go, s, d,  \
-                                  alpha, cdot, att_src, C, dhs, ds, gt, ws, min_len, src_rows)
+                                  float* ws, int min_len = 0, const int32_t* src_rows = nullptr,
+                                  float* att_part = nullptr, int64_t att_rows = 0,
+                                  int64_t* att_waves = nullptr) {
+#define GR_BH(G, N)                                                                       \
+  return launch_bwd_h1<VEC, G, N>(st, units, n_units, row_idx, perm, hs, ldh, go, s, d,   \
+                                  alpha, cdot, att_src, C, dhs, ds, gt, ws, min_len, src_rows, \
+                                  att_part, att_rows, att_waves)
   if (chunks <= 8) GR_BH(8, 1);
   if (chunks <= 16) GR_BH(16, 1);
   if (chunks <= 32) GR_BH(32, 1);
@@ -2001,7 +2077,8 @@ extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
                                         const float* alpha, const float* cdot,
                                         const float* att_src, int64_t heads, int64_t channels,
                                         float* dz, float* ds, float* gt, float* workspace,
-                                        int64_t n_slots, void* stream) {
+                                        int64_t n_slots, float* att_part, int64_t att_rows,
+                                        int64_t* att_waves, void* stream) {
   gr::clear_error();
   int rc = check_heads(heads, channels);
   if (rc) return rc;
@@ -2010,6 +2087,11 @@ extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
              "gat_backward_src_into: one head of 68..1024 channels, a multiple of 4");
   GR_REQUIRE(ldh >= C && ldh % 4 == 0, "gat_backward_src_into: bad ldh");
   GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_backward_src_into: NULL fixups/workspace");
+  GR_REQUIRE(att_part == nullptr || (att_rows >= 1 && att_waves != nullptr &&
+                                     aligned16(att_part)),
+             "gat_backward_src_into: att_part needs att_rows >= 1, att_waves and 16-byte "
+             "alignment");
+  if (att_waves != nullptr) *att_waves = 0;
   if (n_units == 0) return GR_OK;
   GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && aligned16(hs) && src_rows &&
                  go && aligned16(go) && s && d && alpha && cdot && att_src &&
@@ -2018,9 +2100,13 @@ extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
              "gat_backward_src_into: NULL or misaligned pointer");
   hipStream_t st = gr::as_stream(stream);
   const int4* u4 = reinterpret_cast<const int4*>(units);
-  GR_HIP_CHECK(dispatch_bwd_h1<4>((int)(C / 4), st, u4, n_units, row_idx, perm, hs, ldh, go, s,
-                                  d, alpha, cdot, att_src, (int)C, dz, ds, gt, workspace, 0,
-                                  src_rows));
+  const hipError_t err = dispatch_bwd_h1<4>((int)(C / 4), st, u4, n_units, row_idx, perm, hs,
+                                            ldh, go, s, d, alpha, cdot, att_src, (int)C, dz, ds,
+                                            gt, workspace, 0, src_rows, att_part, att_rows,
+                                            att_waves);
+  GR_REQUIRE(att_part == nullptr || *att_waves > 0,
+             "gat_backward_src_into: occupancy query for the attention partials failed");
+  GR_HIP_CHECK(err);
   if (n_fix > 0) {
     hipLaunchKernelGGL(gat_bwd_src_fixup, dim3(blocks_for(n_fix)), dim3(256), 0, st, fixups,
                        n_fix, workspace, 1, (int)C, att_src, dz, ds, src_rows);

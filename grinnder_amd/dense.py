@@ -31,6 +31,37 @@ def _check(name: str, t: Tensor) -> None:
         raise RuntimeError(f"{name} must be float32; got {t.dtype}")
 
 
+class OutputRows:
+    """A caller's fp32 [rows, D] block of device memory (rows contiguous, no
+    gradient) that a fused layer epilogue writes its result into, instead of
+    a new tensor.  The epilogue returns a view of the block as the layer's
+    autograd output, so a caller that wanted the output there (the next
+    layer's HBM-resident input rows) needs no copy.  The block is passed
+    inside this holder, not as a tensor argument, so that autograd does not
+    take it for an input of the epilogue."""
+
+    __slots__ = ("rows",)
+
+    def __init__(self, rows: Tensor):
+        self.rows = rows
+
+
+def output_block(dest: Optional[OutputRows], rows: int, dim: int, device) -> Tensor:
+    """The tensor a fused epilogue writes its [rows, dim] result into:
+    dest's block when one is given (checked to be exactly that shape, fp32,
+    on the device and row-contiguous), else a new tensor."""
+    if dest is None:
+        return torch.empty((rows, dim), dtype=torch.float32, device=device)
+    t = dest.rows
+    if (t.dtype != torch.float32 or t.device != torch.device(device) or tuple(t.shape) != (rows, dim)
+            or (rows > 1 and t.stride(0) != dim) or (dim > 1 and t.stride(1) != 1)
+            or t.requires_grad):
+        raise ValueError(f"output block must be a contiguous fp32 [{rows}, {dim}] tensor on "
+                         f"{device} without gradient; got {tuple(t.shape)}, {t.dtype}, "
+                         f"strides {t.stride()}, on {t.device}")
+    return t
+
+
 def gemm_tn_splits(m: int, n: int, k: int) -> Tuple[int, int]:
     """Default K split count and workspace floats of ``gemm_tn`` for a shape."""
     splits = ctypes.c_int64(0)
@@ -167,12 +198,12 @@ class _BiasLNAct(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                eps: float, act: str, sink=None) -> Tensor:
+                eps: float, act: str, sink=None, dest: Optional[OutputRows] = None) -> Tensor:
         z = z.contiguous()
         rows, dim = z.shape
         dev = z.device
         h = torch.empty_like(z)
-        out = torch.empty_like(z)
+        out = output_block(dest, rows, dim, dev)
         mean = torch.empty(rows, dtype=torch.float32, device=dev)
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         b = bias.contiguous() if bias is not None else None
@@ -200,19 +231,21 @@ class _BiasLNAct(torch.autograd.Function):
         if ctx.sink is not None:
             ctx.sink.cdot = rowdot
             ctx.sink.grad_ptr = gh.data_ptr()
-        return gh, db, dgamma, dbeta, None, None, None
+        return gh, db, dgamma, dbeta, None, None, None, None
 
 
 def bias_ln_act(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                eps: float = 1e-5, act: str = "relu", rowdot_sink=None) -> Tensor:
+                eps: float = 1e-5, act: str = "relu", rowdot_sink=None,
+                dest: Optional[OutputRows] = None) -> Tensor:
     """act(LayerNorm(z + bias)) over the rows of z (GPU, one pass); act is
     "relu" or "elu" (alpha = 1).  `rowdot_sink` (an aggregation.RowDotSink
     shared with the GAT attention that produced z): the backward also forms
-    <dL/dz_r, z_r> and leaves it there."""
+    <dL/dz_r, z_r> and leaves it there.  `dest`: write the result into that
+    block and return a view of it."""
     _check("z", z)
     if act not in _lib.ACTIVATIONS:
         raise ValueError(f"unknown activation {act!r}")
-    return _BiasLNAct.apply(z, bias, gamma, beta, eps, act, rowdot_sink)
+    return _BiasLNAct.apply(z, bias, gamma, beta, eps, act, rowdot_sink, dest)
 
 
 def bias_ln_relu(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
@@ -228,7 +261,8 @@ class _LinearLNAct(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Optional[Tensor], gamma: Tensor,
-                beta: Tensor, eps: float, act: str) -> Tensor:
+                beta: Tensor, eps: float, act: str,
+                dest: Optional[OutputRows] = None) -> Tensor:
         x = x.contiguous()
         rows, din = x.shape
         dout = weight.size(0)
@@ -236,7 +270,7 @@ class _LinearLNAct(torch.autograd.Function):
         w = weight.contiguous()
         wt = w.t().contiguous()
         h = torch.empty((rows, dout), dtype=torch.float32, device=dev)
-        out = torch.empty_like(h)
+        out = output_block(dest, rows, dout, dev)
         mean = torch.empty(rows, dtype=torch.float32, device=dev)
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         b = bias.contiguous() if bias is not None else None
@@ -266,18 +300,19 @@ class _LinearLNAct(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             with dense_region("dw", rows, dout, din):
                 dw = gemm_tn(gh, x)
-        return dx, dw, db, dgamma, dbeta, None, None
+        return dx, dw, db, dgamma, dbeta, None, None, None
 
 
 def linear_ln_act(x: Tensor, weight: Tensor, bias: Optional[Tensor], gamma: Tensor,
-                  beta: Tensor, eps: float = 1e-5, act: str = "relu") -> Tensor:
+                  beta: Tensor, eps: float = 1e-5, act: str = "relu",
+                  dest: Optional[OutputRows] = None) -> Tensor:
     """act(LayerNorm(x Wᵀ + bias)) (GPU).  One fused MFMA pass when the output
     width is a multiple of 16 up to 256; otherwise the product and the
-    epilogue run as two passes."""
+    epilogue run as two passes.  `dest` as in bias_ln_act."""
     _check("x", x)
     if act not in _lib.ACTIVATIONS:
         raise ValueError(f"unknown activation {act!r}")
     dout = weight.size(0)
     if dout % 16 == 0 and dout <= 256 and x.dim() == 2:
-        return _LinearLNAct.apply(x, weight, bias, gamma, beta, eps, act)
-    return bias_ln_act(linear(x, weight), bias, gamma, beta, eps, act)
+        return _LinearLNAct.apply(x, weight, bias, gamma, beta, eps, act, dest)
+    return bias_ln_act(linear(x, weight), bias, gamma, beta, eps, act, dest=dest)

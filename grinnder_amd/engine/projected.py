@@ -19,7 +19,7 @@ from torch import Tensor
 
 from grinnder_amd.aggregation import (KernelTimer, ProjectedSink, dense_region, gather_rows,
                                      scatter_add_rows)
-from grinnder_amd.dense import gemm_nt, gemm_tn
+from grinnder_amd.dense import OutputRows, gemm_nt, gemm_tn
 from grinnder_amd.loss import masked_cross_entropy
 
 
@@ -406,13 +406,16 @@ class ProjectedLayers:
         return ProjectedSink(self._dzbuf(layer), ids[0], ids[1], self._token,
                              self.graph._range(pid)[0])
 
-    def _device_call(self, layer: int, pid: int, grad: bool) -> Tensor:
+    def _device_call(self, layer: int, pid: int, grad: bool,
+                     dest: Optional[OutputRows] = None) -> Tensor:
         """forward_projected on partition pid: reading Z in place through a
         sink where the model allows it, else on gathered rows of Z (whose
-        gradient the gather adds into dZ when grad)."""
+        gradient the gather adds into dZ when grad).  `dest`: where the
+        model may put the output (projected and in-place layers)."""
         adj = self.graph.adjacency(pid)
         if layer in self._inplace:
-            return self.model.forward_inplace(layer, self._xres[layer], adj, self._gids(pid)[0])
+            return self.model.forward_inplace(layer, self._xres[layer], adj, self._gids(pid)[0],
+                                              dest=dest)
         if layer not in self._proj:
             # A gathered layer: the reference's forward on the partition's
             # input rows, gathered from HBM (layer 0's get no gradient).  The
@@ -438,32 +441,38 @@ class ProjectedLayers:
         if sink is not None:
             sc = self._scores.get(layer)
             if sc is None:
-                return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink)
+                return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink,
+                                                    dest=dest)
             lo, hi = self.graph._range(pid)
             return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink,
-                                                scores=(sc[0], sc[1][lo:hi]))
+                                                scores=(sc[0], sc[1][lo:hi]), dest=dest)
         z = self._gather_projected(layer, pid, grad=grad)
         sc = self._scores.get(layer)
         if sc is None:
-            return self.model.forward_projected(layer, z, adj)
+            return self.model.forward_projected(layer, z, adj, dest=dest)
         lo, hi = self.graph._range(pid)
         s_rows = gather_rows(sc[0], self._global_rows(pid))
-        return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]))
+        return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]),
+                                            dest=dest)
 
-    def _device_forward(self, layer: int, pid: int, keep: bool) -> Tensor:
+    def _device_forward(self, layer: int, pid: int, keep: bool,
+                        dest: Optional[Tensor] = None) -> Tensor:
         """The forward of a projected layer on partition pid: with its graph
         kept for the backward (keep), else without autograd, noting the RNG
         state so that the backward's recompute draws the same dropout masks
-        (as torch.utils.checkpoint does in the reference's flow)."""
+        (as torch.utils.checkpoint does in the reference's flow).  `dest`: a
+        [B, D] block the output may be written into instead of a new tensor
+        (the returned tensor is then a view of it)."""
+        rows = OutputRows(dest) if dest is not None else None
         if keep:
             with torch.enable_grad():
-                out = self._device_call(layer, pid, grad=True)
+                out = self._device_call(layer, pid, grad=True, dest=rows)
             self._graphs.setdefault(layer, {})[pid] = out
             return out
         if self.model.training:
             self._rng[(layer, pid)] = torch.cuda.get_rng_state(self._device_index())
         with torch.no_grad():
-            return self._device_call(layer, pid, grad=False).contiguous()
+            return self._device_call(layer, pid, grad=False, dest=rows).contiguous()
 
     def _device_index(self) -> int:
         return self.device.index if self.device.index is not None else torch.cuda.current_device()
@@ -775,14 +784,22 @@ class ProjectedLayers:
                     if i + 1 < len(pids) and pool > 1:
                         self._gather(layer, pids[i + 1], s.h2d[(i + 1) % pool])
                     out = self._checkpointed(layer, pid, k)
-                else:
-                    out = self._device_forward(layer, pid, keep=layer in self._keep)
                 lo, hi = g._range(pid)
+                if projected:
+                    # The model may write the output into x_next's rows itself.
+                    out = self._device_forward(layer, pid, keep=layer in self._keep,
+                                               dest=x_next[lo:hi])
                 if (layer + 1) in self._proj:
                     self._project_rows(layer + 1, out, lo, hi)
-                with torch.no_grad():
-                    x_next[lo:hi].copy_(out)
-                if not (projected and layer in self._keep):
+                in_place = out.data_ptr() == x_next[lo:hi].data_ptr()
+                if not in_place:
+                    with torch.no_grad():
+                        x_next[lo:hi].copy_(out)
+                if in_place:
+                    # The storage is x_next's: it is never freed here.
+                    if layer not in self._keep:
+                        self.activations[layer][pid] = None
+                elif not (projected and layer in self._keep):
                     # The storage goes back to the allocator in stream order; a
                     # reference-flow layer keeps the tensor for its backward,
                     # which recomputes it.  A kept graph keeps its output.

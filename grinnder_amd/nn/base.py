@@ -43,13 +43,16 @@ class GriNNderModel(torch.nn.Module):
         layer has no such form (the default)."""
         return None
 
-    def forward_projected(self, layer: int, z: Tensor, adj, sink=None) -> Tensor:
+    def forward_projected(self, layer: int, z: Tensor, adj, sink=None, dest=None) -> Tensor:
         """forward_layer(layer, x, adj) given z = x Wᵀ for the W of
         input_projection(layer).  With a sink (grinnder_amd.aggregation.
         ProjectedSink; only where projected_sink_ok(layer)), z is the whole
         projected matrix of all partitions, read in place through the sink's
         global ids, and the gradient of the partition's rows is added into
-        the sink's dZ."""
+        the sink's dZ.  `dest` (grinnder_amd.dense.OutputRows): a block the
+        layer may write its output into, returning a view of it, when its
+        last step is a fused epilogue; a model may ignore it (the caller
+        then copies the output)."""
         raise NotImplementedError(f"{type(self).__name__} has no projected form of layer {layer}")
 
     def projected_width(self, layer: int) -> int:
@@ -76,10 +79,11 @@ class GriNNderModel(torch.nn.Module):
         (the default: no)."""
         return False
 
-    def forward_inplace(self, layer: int, x: Tensor, adj, gidx: Tensor) -> Tensor:
+    def forward_inplace(self, layer: int, x: Tensor, adj, gidx: Tensor, dest=None) -> Tensor:
         """forward_layer(layer, x[rows], adj) for the partition's gathered rows,
         with x the input rows of all partitions read in place through gidx
-        (the global row of each CSR edge's source); x gets no gradient."""
+        (the global row of each CSR edge's source); x gets no gradient.
+        `dest` as in forward_projected."""
         raise NotImplementedError(f"{type(self).__name__} has no in-place form of layer {layer}")
 
     def forward_gathered(self, layer: int, x: Tensor, adj, reuse=None, keep=None) -> Tensor:

@@ -94,7 +94,7 @@ class GAT(GriNNderModel):
         return conv.heads == 1 and c % 4 == 0 and 64 < c <= 1024
 
     def forward_projected(self, layer: int, hs: Tensor, adj, sink=None,
-                          scores=None) -> Tensor:
+                          scores=None, dest=None) -> Tensor:
         """The layer on hs = lin(x): the partition's gathered rows, or with
         `sink` the matrix of all partitions' rows read in place (then
         `scores` are the logit halves of all rows and of the partition's
@@ -106,7 +106,8 @@ class GAT(GriNNderModel):
             norm = self.norms[layer]
             dot = RowDotSink()
             x = conv.attend(hs, adj, add_bias=False, scores=scores, rowdot_sink=dot, sink=sink)
-            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu", dot)
+            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu", dot,
+                               dest=dest)
         return self._finish(layer, conv.attend(hs, adj, scores=scores, sink=sink))
 
     def projected_scores(self, layer: int, z: Tensor):

@@ -83,7 +83,7 @@ class GCN(GriNNderModel):
         return (layer == 0 and conv.aggregate_first()
                 and not (self.residual and conv.in_channels == conv.out_channels))
 
-    def forward_inplace(self, layer: int, x: Tensor, adj, gidx: Tensor) -> Tensor:
+    def forward_inplace(self, layer: int, x: Tensor, adj, gidx: Tensor, dest=None) -> Tensor:
         if not self.inplace_ok(layer):
             raise ValueError(f"layer {layer} has no in-place form")
         conv = self.convs[layer]
@@ -91,7 +91,7 @@ class GCN(GriNNderModel):
         if self._fusable_norm(layer, x):
             norm = self.norms[layer]
             return linear_ln_act(h, conv.lin.weight, conv.bias, norm.weight, norm.bias,
-                                 norm.eps, "relu")
+                                 norm.eps, "relu", dest=dest)
         h = linear(h, conv.lin.weight, conv.bias)
         if layer < self.num_layers - 1:
             if self.norms is not None:
@@ -100,7 +100,7 @@ class GCN(GriNNderModel):
             h = F.dropout(h, p=self.dropout, training=self.training)
         return h
 
-    def forward_projected(self, layer: int, z: Tensor, adj, sink=None) -> Tensor:
+    def forward_projected(self, layer: int, z: Tensor, adj, sink=None, dest=None) -> Tensor:
         conv = self.convs[layer]
         d = conv.out_channels
         w = z.size(1)
@@ -123,7 +123,7 @@ class GCN(GriNNderModel):
         elif self._fusable_norm(layer, z):
             norm = self.norms[layer]
             return gcn_aggregate_ln_relu(z, adj, conv.bias, norm.weight, norm.bias, norm.eps,
-                                         sink=sink)
+                                         sink=sink, dest=dest)
         else:
             h = gcn_aggregate(z, adj, conv.bias, sink=sink)
         if layer < self.num_layers - 1:

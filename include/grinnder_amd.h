@@ -494,7 +494,13 @@ int gr_gat_backward_src(const int32_t* units, int64_t n_units,
  * being written (the src_rows of one partition are distinct).  Replaces the
  * gather of the partition's rows of lin(x) before PyG GATConv's attention
  * (grinnder/nn/gat.py:72-73) and the scatter of their gradient after it; ds
- * and gt stay per partition.  workspace as gr_gat_backward_src. */
+ * and gt stay per partition.  workspace as gr_gat_backward_src.
+ * att_part (optional, 16-byte aligned, att_rows x C floats): the pass also
+ * forms the attention-vector gradient sum_j ds_j Hs_j (PyG GATConv's
+ * att_src gradient) while Hs_j is in registers: *att_waves (> 0) rows of
+ * att_part get per-wavefront partial sums, whose column sums taken in row
+ * order (gr_column_sum) are that gradient.  att_part NULL: att_rows and
+ * att_waves are ignored. */
 int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
                              const int32_t* fixups, int64_t n_fix,
                              const int32_t* row_idx, const int32_t* perm,
@@ -503,7 +509,8 @@ int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
                              const float* alpha, const float* cdot,
                              const float* att_src, int64_t heads, int64_t channels,
                              float* dz, float* ds, float* gt, float* workspace,
-                             int64_t n_slots, void* stream);
+                             int64_t n_slots, float* att_part, int64_t att_rows,
+                             int64_t* att_waves, void* stream);
 
 /* Backward over destination rows i (CSR plan):
  * dd[i,h] = sum_e gt[e,h] + cdot[i,h] * 1e-16 / den[i,h] (= sum_j g_t,ij) and

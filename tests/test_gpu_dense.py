@@ -309,3 +309,54 @@ def test_linear_ln_act_matches_fp64(gpu, rows, din, dout, act):
     assert max_abs_norm_err(out, ref) <= TOL
     for got, want in zip((x, w, b, gamma, beta), ps):
         assert max_abs_norm_err(got.grad, want.grad) <= TOL
+
+
+def test_fused_epilogues_write_into_output_block(gpu):
+    """The fused epilogues' `dest` (the trainer passes the next layer's
+    HBM-resident input rows): the output is a view of the block with the
+    same bits as a freshly allocated output, the gradients are unchanged,
+    and a block of the wrong shape is refused."""
+    from grinnder_amd.aggregation import gcn_aggregate_ln_relu
+    from grinnder_amd.data.adjacency import Adjacency
+    from grinnder_amd.dense import OutputRows, linear_ln_act
+    from tests.graphs import random_bipartite
+
+    rows, din, dout = 700, 64, 256
+    block = torch.full((rows + 300, dout), 7.0, device=gpu)
+    x = _randn(rows, din, seed=11, dev=gpu)
+    w = 0.2 * _randn(dout, din, seed=12, dev=gpu)
+    b = _randn(dout, seed=13, dev=gpu)
+    gamma = 1 + 0.1 * _randn(dout, seed=14, dev=gpu)
+    beta = 0.1 * _randn(dout, seed=15, dev=gpu)
+    go = _randn(rows, dout, seed=16, dev=gpu)
+    rowptr, col, val = random_bipartite(rows, 900, 12, seed=5, long_rows=2)
+    adj = Adjacency(rowptr, col, val, (rows, 900), seg_len=64)
+    z = _randn(900, dout, seed=17, dev=gpu)
+
+    def run(fn, inputs, dest):
+        ps = [t.clone().requires_grad_(True) for t in inputs]
+        out = fn(*ps, dest)
+        out.backward(go)
+        return out.detach().clone(), [p.grad for p in ps], out
+
+    cases = [
+        ("bias_ln_act", lambda zz, bb, dst: bias_ln_act(zz, bb, gamma, beta, 1e-5, "elu",
+                                                       dest=dst), (x @ w.t(), b)),
+        ("linear_ln_act", lambda xx, ww, dst: linear_ln_act(xx, ww, b, gamma, beta, 1e-5,
+                                                           "relu", dest=dst), (x, w)),
+        ("gcn_aggregate_ln_relu", lambda zz, bb, dst: gcn_aggregate_ln_relu(
+            zz, adj, bb, gamma, beta, 1e-5, dest=dst), (z, b)),
+    ]
+    for name, fn, inputs in cases:
+        print(f"case {name}", flush=True)
+        ref, ref_grads, _ = run(fn, inputs, None)
+        lo = 100
+        got, grads, view = run(fn, inputs, OutputRows(block[lo:lo + rows]))
+        assert view.data_ptr() == block[lo].data_ptr(), name
+        assert torch.equal(got, ref), name
+        assert torch.equal(block[lo:lo + rows], ref), name
+        for g0, g1 in zip(ref_grads, grads):
+            assert torch.equal(g0, g1), name
+        with pytest.raises(ValueError):
+            fn(*inputs, OutputRows(block[:rows, :dout - 4]))
+    assert torch.all(block[:100] == 7.0) and torch.all(block[100 + rows:] == 7.0)

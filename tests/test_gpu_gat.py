@@ -220,16 +220,30 @@ def test_gat_row_dot_matches_fp64(gpu, rows, H, C):
     assert max_abs_norm_err(out.cpu(), ref) <= TOL
 
 
-@pytest.mark.parametrize("C", [256, 128])
-def test_gat_attention_in_place_matches_gathered(gpu, C):
+@pytest.mark.parametrize("C,big", [(256, False), (128, False), (256, True)])
+def test_gat_attention_in_place_matches_gathered(gpu, C, big):
     """One head read in place (the projected flow's ProjectedSink: edge
     sources as global rows of Z, dHs added into dZ at the partition's rows)
-    gives the same output, dZ and attention-vector gradients, bit for bit,
-    as the same partition on its gathered rows of Z with the gradient
-    scattered back."""
+    gives the same output, dZ, att_dst and bias gradients, bit for bit, as
+    the same partition on its gathered rows of Z with the gradient scattered
+    back.  The in-place backward forms att_src's gradient from per-wavefront
+    partial sums (the same sum, re-associated): within TOL of the gathered
+    form's and of a float64 sum over the edges.  `big`: more source columns
+    than the GPU holds wavefronts, so each wavefront takes several, and hub
+    columns split into several units."""
     from grinnder_amd.aggregation import ProjectedSink, gat_scores
-    N, B, E, lo = 3000, 500, 1400, 700
+    if big:
+        N, B, E, lo = 150_000, 20_000, 70_000, 40_000
+    else:
+        N, B, E, lo = 3000, 500, 1400, 700
+    print(f"case C={C} N={N} B={B} E={E}", flush=True)
     rowptr, col, val = random_bipartite(B, E, 9, seed=C, long_rows=2, long_len=900)
+    if big:
+        # Three hub source columns of about 2,000 edges each (split in the CSC plan).
+        g0 = torch.Generator().manual_seed(7)
+        hub = torch.rand(col.numel(), generator=g0) < 6000 / col.numel()
+        col[hub] = torch.tensor([B + 11, B + 23, B + 37])[torch.randint(0, 3, (int(hub.sum()),),
+                                                                          generator=g0)]
     adj = Adjacency(rowptr, col, val, (B, E), seg_len=512)
     g = torch.Generator().manual_seed(C)
     others = torch.cat([torch.arange(0, lo), torch.arange(lo + B, N)])
@@ -262,5 +276,18 @@ def test_gat_attention_in_place_matches_gathered(gpu, C):
             dz.index_add_(0, rg, hs.grad)
         torch.cuda.synchronize()
         outs.append((y.detach(), dz, a_s.grad, a_d.grad, b.grad))
-    for t0, t1 in zip(*outs):
+    (y0, dz0, as0, ad0, b0), (y1, dz1, as1, ad1, b1) = outs
+    for t0, t1 in ((y0, y1), (dz0, dz1), (ad0, ad1), (b0, b1)):
         assert torch.equal(t0, t1)
+    assert max_abs_norm_err(as1, as0.double()) <= TOL
+    if big:
+        return
+    # float64: the oracle's backward on the gathered rows.  (The big case
+    # leaves it out: among its 190k edges a LeakyReLU tie, a logit within
+    # fp32 rounding of 0, may take the other slope in float64.)
+    hs64 = z[rg].cpu()
+    ref_o, alpha, tpre = oracle.gat_forward(rowptr, col, hs64, 1, C, att_s.cpu(), att_d.cpu(),
+                                            bias.cpu(), True)
+    back = oracle.gat_backward(rowptr, col, hs64, 1, C, att_s.cpu(), att_d.cpu(), True, alpha,
+                               tpre, gy.cpu())
+    assert max_abs_norm_err(as1.view(-1), torch.as_tensor(back[1]).view(-1)) <= TOL
