@@ -87,6 +87,7 @@ class ProjectedLayers:
         # W padded with zero rows to Z's width, per projected layer whose Z is
         # wider than W's rows (formed once per epoch: W changes between).
         self._wpad: Dict[int, Tensor] = {}
+        self._wtdx: Dict[int, Tensor] = {}
         # HBM buffers of dL/dx for the gathered layers above layer 0 (layers
         # in self._xin that run neither projected nor in place), by layer.
         self._gxbufs: Dict[int, Tensor] = {}
@@ -177,6 +178,7 @@ class ProjectedLayers:
         self._keep = set()
         self._out_room = False
         self._wpad = {}
+        self._wtdx = {}
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
                 or self.cache is not None
                 or (self._pid_start, self._pid_end) != (0, g.num_parts)):
@@ -649,8 +651,25 @@ class ProjectedLayers:
         if layer not in self._proj:
             return self._gxbufs[layer][lo:hi]
         w = self._proj[layer]
+        dz = self._dzbufs[layer][lo:hi]
         with dense_region("dx", hi - lo, w.size(0), w.size(1)):
-            return gemm_nt(self._dzbufs[layer][lo:hi, :w.size(0)], w.detach().t().contiguous())
+            return gemm_nt(dz, self._dx_weight(layer, dz.size(1)))
+
+    def _dx_weight(self, layer: int, width: int) -> Tensor:
+        """The B operand of dZ W for the layer's dZ rows of `width` columns:
+        Wᵀ, with zero columns for Z's zero pad columns, formed once per epoch.
+        Whole, 16-byte aligned dZ rows take the matrix-core product; the pad
+        columns of dZ and rows of W are zero, so the sum gains only exact
+        zero terms."""
+        wt = self._wtdx.get(layer)
+        if wt is None or wt.size(1) != width:
+            w = self._proj[layer].detach()
+            with torch.no_grad():
+                if width != w.size(0):
+                    w = torch.nn.functional.pad(w, (0, 0, 0, width - w.size(0)))
+                wt = w.t().contiguous()
+            self._wtdx[layer] = wt
+        return wt
 
     def _backward_device(self, layer: int, losses: Optional[List[Tensor]] = None) -> None:
         """Backward of a projected layer: per partition, take the forward's
@@ -717,12 +736,15 @@ class ProjectedLayers:
         if inplace or gathered:
             s.compute.synchronize()
             return
+        # dW over dZ's whole (16-byte) rows; the rows of dW for Z's zero pad
+        # columns are zero and are dropped.
         with torch.cuda.stream(s.compute):
-            dw = torch.zeros_like(w)
+            dwp = torch.zeros(dz.size(1), w.size(1), dtype=w.dtype, device=w.device)
+            dw = dwp[:w.size(0)]
 
         def accumulate(pid, xp, lo, hi):
             with dense_region("dw", hi - lo, w.size(0), w.size(1)):
-                gemm_tn(dz[lo:hi, :w.size(0)], xp, out=dw, beta=1.0)
+                gemm_tn(dz[lo:hi], xp, out=dwp, beta=1.0)
 
         if layer in self._xin:
             x = self._xres[layer]

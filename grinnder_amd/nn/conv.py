@@ -161,6 +161,17 @@ class GATConv(Module):
         """Zero columns added to one head of C channels, C not a multiple of 4."""
         return (-self.out_channels) % 4 if self.heads == 1 else 0
 
+    def _pad_rows(self, hs: Tensor) -> Tensor:
+        """hs with the padded head's zero columns: hs itself when it has them
+        already (a projected matrix held at the padded width, whose pad
+        columns the projection leaves zero)."""
+        width = self.out_channels + self._padded()
+        if hs.size(-1) == width:
+            return hs
+        if hs.size(-1) != self.out_channels:
+            raise ValueError(f"GATConv: rows of {hs.size(-1)} channels for {self.out_channels}")
+        return F.pad(hs, (0, width - self.out_channels))
+
     def attend(self, hs: Tensor, adj: Adjacency, add_bias: bool = True,
                scores: Optional[Tuple[Tensor, Tensor]] = None, rowdot_sink=None,
                sink=None) -> Tensor:
@@ -179,7 +190,7 @@ class GATConv(Module):
             if sink is not None:
                 raise ValueError("GATConv.attend: a padded head reads gathered rows")
             b = F.pad(bias, (0, pad)) if bias is not None else None
-            y = gat_attention(F.pad(hs, (0, pad)), adj, F.pad(self.att_src, (0, pad)),
+            y = gat_attention(self._pad_rows(hs), adj, F.pad(self.att_src, (0, pad)),
                               F.pad(self.att_dst, (0, pad)), b, 1, self.out_channels + pad,
                               self.concat, scores)
             return y[:, :self.out_channels]
@@ -191,7 +202,7 @@ class GATConv(Module):
         (padding included), for callers that hold hs for many partitions."""
         pad = self._padded()
         if pad:
-            return gat_scores(F.pad(hs, (0, pad)), F.pad(self.att_src, (0, pad)),
+            return gat_scores(self._pad_rows(hs), F.pad(self.att_src, (0, pad)),
                               F.pad(self.att_dst, (0, pad)), 1, self.out_channels + pad,
                               hs.size(0))
         return gat_scores(hs, self.att_src, self.att_dst, self.heads, self.out_channels,

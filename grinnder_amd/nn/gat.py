@@ -82,6 +82,14 @@ class GAT(GriNNderModel):
             return None
         return self.convs[layer].lin.weight
 
+    def projected_width(self, layer: int) -> int:
+        """One head of C channels, C not a multiple of 4, is held C rounded up
+        to 4 wide, the width its attention runs at (GATConv pads it): gathered
+        rows need no padding copy, and dZ's 16-byte rows take the matrix-core
+        dX product.  The pad columns of Z are zero."""
+        conv = self.convs[layer]
+        return conv.heads * conv.out_channels + conv._padded()
+
     def projected_sink_ok(self, layer: int) -> bool:
         """Z read in place for one head of 68..1024 channels (a multiple of
         4): the attention gathers each edge's source row of Z directly and
