@@ -637,6 +637,73 @@ __global__ __launch_bounds__(256) void colsum_partial(const float* __restrict__ 
   }
 }
 
+// The same sums with 16-byte loads, for dim % 4 == 0 (dim <= 1024), ldx % 4
+// == 0, a 16-byte aligned x and, weighted, group % 4 == 0 (the 4 columns of
+// a vector share one weight).  A workgroup takes RL = 256 / (dim / 4) rows at
+// a time: thread t owns the 4 columns of slot t % (dim / 4) in rows r0 + t /
+// (dim / 4) + k RL, with four accumulators (four rows in flight); the row
+// lanes' sums are then added in lane order through LDS.  Every step is in a
+// fixed order.
+template <bool WEIGHTED>
+__global__ __launch_bounds__(256) void colsum_partial4(const float* __restrict__ x, int64_t rows,
+                                                       int dim, int64_t ldx,
+                                                       const float* __restrict__ w,
+                                                       int64_t ldw, int group, int64_t chunk,
+                                                       float* __restrict__ part,
+                                                       const int32_t* __restrict__ xrows) {
+  __shared__ float4 red[256];
+  const int q = dim / 4;
+  const int rl_n = 256 / q;
+  const int slot = threadIdx.x % q;
+  const int rl = threadIdx.x / q;
+  const bool active = rl < rl_n;
+  const int64_t r0 = (int64_t)blockIdx.x * chunk;
+  const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
+  float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
+  if (active) {
+    const int f = slot * 4;
+    auto val = [&](int64_t r) {
+      const int64_t xr = xrows != nullptr ? (int64_t)xrows[r] : r;
+      float4 v = *reinterpret_cast<const float4*>(x + xr * ldx + f);
+      if constexpr (WEIGHTED) {
+        const float wt = w[r * ldw + f / group];
+        v.x *= wt;
+        v.y *= wt;
+        v.z *= wt;
+        v.w *= wt;
+      }
+      return v;
+    };
+    float4 a2 = a0, a3 = a0;
+    int64_t r = r0 + rl;
+    for (; r + 3 * rl_n < r1; r += 4 * rl_n) {
+      const float4 v0 = val(r), v1 = val(r + rl_n), v2 = val(r + 2 * rl_n),
+                   v3 = val(r + 3 * rl_n);
+      a0.x += v0.x; a0.y += v0.y; a0.z += v0.z; a0.w += v0.w;
+      a1.x += v1.x; a1.y += v1.y; a1.z += v1.z; a1.w += v1.w;
+      a2.x += v2.x; a2.y += v2.y; a2.z += v2.z; a2.w += v2.w;
+      a3.x += v3.x; a3.y += v3.y; a3.z += v3.z; a3.w += v3.w;
+    }
+    for (; r < r1; r += rl_n) {
+      const float4 v0 = val(r);
+      a0.x += v0.x; a0.y += v0.y; a0.z += v0.z; a0.w += v0.w;
+    }
+    a0.x += a1.x; a0.y += a1.y; a0.z += a1.z; a0.w += a1.w;
+    a2.x += a3.x; a2.y += a3.y; a2.z += a3.z; a2.w += a3.w;
+    a0.x += a2.x; a0.y += a2.y; a0.z += a2.z; a0.w += a2.w;
+  }
+  red[threadIdx.x] = a0;
+  __syncthreads();
+  if (rl == 0) {
+    float4 t = red[slot];
+    for (int k = 1; k < rl_n; ++k) {
+      const float4 v = red[k * q + slot];
+      t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+    }
+    *reinterpret_cast<float4*>(part + (int64_t)blockIdx.x * dim + slot * 4) = t;
+  }
+}
+
 // Column sums of part[nblk, dim] over nblk, deterministic: a workgroup owns
 // 4 columns; its 64 row groups each sum rows g, g+64, ... of their column in
 // order, then the 64 group sums are added in group order.
@@ -1197,7 +1264,17 @@ extern "C" int gr_column_sum(const float* x, int64_t rows, int64_t dim, int64_t 
   if (nblk > 4096) nblk = 4096;
   if (nblk > nblk_max) nblk = nblk_max;
   const int64_t chunk = rows == 0 ? 0 : (rows + nblk - 1) / nblk;
-  if (w != nullptr)
+  const bool vec4 = dim % 4 == 0 && dim <= 1024 && ldx % 4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
+                    (w == nullptr || group % 4 == 0);
+  if (vec4 && w != nullptr)
+    hipLaunchKernelGGL(gr_agg::colsum_partial4<true>, dim3((unsigned)nblk), dim3(256), 0, s, x,
+                       rows, (int)dim, ldx, w, ldw, (int)group, chunk, workspace, xrows);
+  else if (vec4)
+    hipLaunchKernelGGL(gr_agg::colsum_partial4<false>, dim3((unsigned)nblk), dim3(256), 0, s,
+                       x, rows, (int)dim, ldx, nullptr, 0, 4, chunk, workspace, xrows);
+  else if (w != nullptr)
     hipLaunchKernelGGL(gr_agg::colsum_partial<true>, dim3((unsigned)nblk), dim3(256), 0, s, x,
                        rows, (int)dim, ldx, w, ldw, (int)group, chunk, workspace, xrows);
   else

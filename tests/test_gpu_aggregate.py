@@ -100,6 +100,37 @@ def test_column_sum_matches_float64(gpu, rows, dim):
     assert torch.equal(got, again)
 
 
+@pytest.mark.parametrize("rows,dim,group,ld,indexed", [
+    (300000, 256, 256, 256, False), (300000, 256, 256, 260, True), (70000, 20, 20, 20, False),
+    (70000, 48, 4, 52, True), (5000, 1024, 256, 1024, False), (5000, 1028, 257, 1028, False),
+    (777, 76, 19, 76, True), (3, 8, 8, 8, False), (0, 256, 256, 256, False)])
+def test_weighted_column_sum_matches_float64(gpu, rows, dim, group, ld, indexed):
+    """Weighted (one weight per `group` columns) and row-indexed column sums,
+    with 16-byte rows (several rows per workgroup) and without (one thread
+    per column), against float64; repeated calls give the same bits."""
+    from grinnder_amd.aggregation import column_sum
+
+    g = torch.Generator().manual_seed(rows + dim)
+    n = rows + 100
+    xs = torch.randn(n, ld, generator=g)[:, :dim]
+    w = torch.randn(rows, (dim + group - 1) // group, generator=g)
+    rows_of = torch.randperm(n, generator=g)[:rows] if indexed else torch.arange(rows)
+    xd, wd = xs.to(gpu), w.to(gpu)
+    kw = dict(rows_of=rows_of.to(torch.int32).to(gpu)) if indexed else {}
+    src = xd if indexed else xd[:rows]
+    got = column_sum(src, wd, group, **kw)
+    again = column_sum(src, wd, group, **kw)
+    torch.cuda.synchronize()
+    sel = xs[rows_of].double()
+    wf = w.double().repeat_interleave(group, dim=1)[:, :dim]
+    ref = (sel * wf).sum(0)
+    if rows == 0:
+        assert torch.equal(got.cpu(), torch.zeros(dim))
+        return
+    assert max_abs_norm_err(got, ref) <= TOL
+    assert torch.equal(got, again)
+
+
 @pytest.mark.parametrize("B,E,deg,longs,dim", [(400, 600, 12, 2, 256), (300, 300, 8, 1, 64),
                                                (200, 350, 10, 1, 47), (120, 150, 6, 1, 1000)])
 def test_fused_ln_relu_matches_float64(gpu, B, E, deg, longs, dim):
