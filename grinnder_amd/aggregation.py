@@ -320,6 +320,8 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
         ctx.plan = plan
         ctx.d = d
         ctx.has_bias = bias is not None
+        ctx.ln_sink = LNProductSink.accepts(x, wp)
+        ctx.x_shape = x.shape
         return y[:, :d]
 
     @staticmethod
@@ -333,7 +335,10 @@ class _GCNLinearAggregatePadded(torch.autograd.Function):
         gyp = pad(gy, (0, dp - d)).contiguous()
         dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gyp, plan.num_src, name="gcn_bwd")
         dx = dw = None
-        if ctx.needs_input_grad[0]:
+        if ctx.needs_input_grad[0] and ctx.ln_sink is not None:
+            # dX = dZ Wp is formed inside the LayerNorm backward that consumes it.
+            dx = ctx.ln_sink.hand_over(dz, wp, ctx.x_shape)
+        elif ctx.needs_input_grad[0]:
             with dense_region("dx", dz.size(0), dp, wp.size(1)):
                 dx = gemm_nt(dz, wp.t().contiguous())
         if ctx.needs_input_grad[1]:
@@ -395,6 +400,80 @@ def ln_act_backward(gout: Tensor, h: Tensor, mean: Tensor, rstd: Tensor, gamma: 
     return gh, dgamma, dbeta, dbias
 
 
+class LNProductSink:
+    """Hands a fused LayerNorm/activation backward its incoming gradient as a
+    product.  The node that consumes the LayerNorm's output x (alone) and
+    forms x Wᵀ with W of at most 64 rows leaves dZ (its gradient of x Wᵀ) and
+    W here and returns `token`, a zero tensor of x's shape with zero strides,
+    as x's gradient.  The LayerNorm's backward, receiving exactly that token,
+    forms dL/dx = dZ W inside its own pass (gr_ln_act_backward_product)
+    instead of reading a [rows, D] gradient that a separate product wrote.
+    A gradient that is not the token (x had other consumers, whose gradients
+    autograd summed with the token's zeros) is completed with dZ W before the
+    usual backward."""
+
+    __slots__ = ("dz", "w", "token")
+
+    def __init__(self):
+        self.dz: Optional[Tensor] = None
+        self.w: Optional[Tensor] = None
+        self.token: Optional[Tensor] = None
+
+    @staticmethod
+    def accepts(x: Tensor, w: Tensor) -> Optional["LNProductSink"]:
+        """The sink of x when x's gradient can be handed over as dZ W for this
+        W ([K, D], K <= 64 and a multiple of 4, D = x's width), else None."""
+        sink = getattr(x, "_grinnder_ln_sink", None)
+        if sink is None or not isinstance(sink, LNProductSink):
+            return None
+        k, d = w.shape
+        if k > 64 or k % 4 != 0 or d != x.size(-1) or d not in (64, 128, 192, 256):
+            return None
+        return sink
+
+    def hand_over(self, dz: Tensor, w: Tensor, shape) -> Tensor:
+        self.dz, self.w = dz, w
+        self.token = torch.zeros((), dtype=dz.dtype, device=dz.device).expand(shape)
+        return self.token
+
+    def take(self, gout: Tensor):
+        """(dz, w, exact) left for this gradient, or None; clears the sink."""
+        if self.dz is None:
+            return None
+        tok = self.token
+        exact = (gout.data_ptr() == tok.data_ptr() and gout.stride() == tok.stride()
+                 and gout.shape == tok.shape)
+        out = (self.dz, self.w, exact)
+        self.dz = self.w = self.token = None
+        return out
+
+
+def ln_act_backward_product(dz: Tensor, w: Tensor, h: Tensor, mean: Tensor, rstd: Tensor,
+                            gamma: Tensor, beta: Tensor, with_bias: bool = False,
+                            act: str = "relu"):
+    """ln_act_backward with dL/dout = dz W formed inside the pass (GPU):
+    dz [rows, K] (K <= 64, a multiple of 4), w [K, D] with D in {64, 128, 192,
+    256}.  Returns (dL/dh, dgamma, dbeta, dbias or None)."""
+    B, D = h.shape
+    dz = dz.contiguous()
+    w = w.contiguous()
+    dev = h.device
+    gh = torch.empty_like(h)
+    dgamma = torch.empty(D, dtype=torch.float32, device=dev)
+    dbeta = torch.empty(D, dtype=torch.float32, device=dev)
+    dbias = torch.empty(D, dtype=torch.float32, device=dev) if with_bias else None
+    nwaves = min(8192, max(4, (B + 15) // 16))
+    nwaves = (nwaves + 3) // 4 * 4
+    ws = torch.empty(((3 if with_bias else 2) * nwaves + 1) * D, dtype=torch.float32,
+                     device=dev)
+    _lib.call("gr_ln_act_backward_product", dz.data_ptr(), dz.size(1), dz.size(1),
+              w.data_ptr(), h.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+              gamma.data_ptr(), beta.data_ptr(), _lib.ACTIVATIONS[act], B, D, gh.data_ptr(),
+              dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias), ws.data_ptr(),
+              ws.numel(), _lib.stream_handle())
+    return gh, dgamma, dbeta, dbias
+
+
 class _GCNAggregateLNReLU(torch.autograd.Function):
     """out = ReLU(LayerNorm(A Z + b)) with the LayerNorm/ReLU fused into the
     aggregation epilogue; backward: fused LN/ReLU gradient, then dZ = A^T gh."""
@@ -402,7 +481,8 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
                 plan: DevicePlan, eps: float, sink: Optional[ProjectedSink] = None,
-                dest: Optional[OutputRows] = None, token: Optional[Tensor] = None) -> Tensor:
+                dest: Optional[OutputRows] = None, ln_sink: Optional[LNProductSink] = None,
+                token: Optional[Tensor] = None) -> Tensor:
         z = z.contiguous()
         idx = plan.idx if sink is None else sink.gidx
         dev = z.device
@@ -426,6 +506,7 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
         ctx.save_for_backward(h, mean, rstd, g, bt)
         ctx.plan = plan
         ctx.sink = sink
+        ctx.ln_sink = ln_sink
         ctx.has_bias = bias is not None
         return out
 
@@ -433,14 +514,22 @@ class _GCNAggregateLNReLU(torch.autograd.Function):
     def backward(ctx, gout: Tensor):
         h, mean, rstd, g, bt = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
-        gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
+        prod = ctx.ln_sink.take(gout) if ctx.ln_sink is not None else None
+        if prod is not None and prod[2]:
+            gh, dgamma, dbeta, db = ln_act_backward_product(prod[0], prod[1], h, mean, rstd, g,
+                                                            bt, ctx.has_bias)
+        else:
+            if prod is not None:
+                from grinnder_amd.dense import gemm_nt
+                gout = gout + gemm_nt(prod[0], prod[1].t().contiguous())
+            gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias)
         dz = None
         if ctx.sink is not None:
             if ctx.sink.dz is not None:
                 spmm_into(plan.bwd, plan.row_idx, plan.val_t, gh, ctx.sink)
         elif ctx.needs_input_grad[0]:
             dz = spmm(plan.bwd, plan.row_idx, plan.val_t, gh, plan.num_src, name="gcn_bwd")
-        return dz, db, dgamma, dbeta, None, None, None, None, None
+        return dz, db, dgamma, dbeta, None, None, None, None, None, None
 
 
 def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gamma: Tensor,
@@ -453,9 +542,16 @@ def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gam
     _check_device_tensor("z", z)
     plan = adj.device_plan(z.device)
     _check_source(z, plan, sink)
+    ln_sink = LNProductSink()
     if sink is None or sink.dz is None:
-        return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, dest)
-    return _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, dest, sink.token)
+        out = _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, dest, ln_sink)
+    else:
+        out = _GCNAggregateLNReLU.apply(z, bias, gamma, beta, plan, eps, sink, dest, ln_sink,
+                                        sink.token)
+    # A product that consumes the output alone may hand its input gradient
+    # back as dZ W (LNProductSink).
+    out._grinnder_ln_sink = ln_sink
+    return out
 
 
 # Rows of per-wavefront partial sums the in-place GAT backward may use for the

@@ -9,6 +9,7 @@
 // the EPI slots are combined with cross-lane shuffles; rows longer than the
 // plan's segment length are summed by a second, ordered pass, so results do
 // not depend on scheduling (no atomics).
+#include <atomic>
 #include <mutex>
 
 #include "gr_internal.h"
@@ -547,6 +548,166 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
     store_vec<VEC>(part_gamma + wid * dim + foff[ch], dg[ch]);
     store_vec<VEC>(part_beta + wid * dim + foff[ch], db[ch]);
     if (part_bias != nullptr) store_vec<VEC>(part_bias + wid * dim + foff[ch], dh[ch]);
+  }
+}
+
+// The LayerNorm/activation backward of ln_relu_backward with its incoming
+// gradient formed in place: g = dz B (dz [rows, K] the next layer's gradient
+// of its projection, K <= 64; B [K, D] row-major, the next layer's W), on the
+// matrix cores, so g never goes to memory.  D = 16 NB.  A wavefront takes 16
+// rows at a time (grid-stride): it holds g for them as NB blocks of
+// v_mfma_f32_16x16x4_f32 (lane (lr, lk) holds columns b * 16 + lr of rows
+// 4 lk + q), reads h in the same layout (64 contiguous bytes per row per
+// instruction), reduces each row over the 16 lanes that share it, and writes
+// gh.  B is staged in LDS once per workgroup (row stride D + 16: the four rows
+// one instruction reads start 16 banks apart).  Partials of dgamma, dbeta and
+// dbias per wavefront, reduced in order afterwards (colsum_final3).  k runs in
+// slices of 16 with the k order of gemm_nt_kernel (MFMA s of a slice sums
+// k = 4 q + s over the lane quads q), zeros past K.
+constexpr int kLnpMaxK = 64;
+
+template <int NB, int ACT>
+__global__ __launch_bounds__(256) void ln_act_backward_product(
+    const float* __restrict__ dz, int64_t ldz, int K, const float* __restrict__ bmat,
+    const float* __restrict__ h, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ gamma,
+    const float* __restrict__ beta, int64_t rows, float* __restrict__ gh,
+    float* __restrict__ part_gamma, float* __restrict__ part_beta,
+    float* __restrict__ part_bias) {
+  typedef float floatx4 __attribute__((ext_vector_type(4)));
+  constexpr int D = 16 * NB;
+  constexpr int LDB = D + 16;
+  __shared__ float Bs[kLnpMaxK * LDB];
+  __shared__ float GB[2][D];  // gamma, beta
+  const int kpad = (K + 15) / 16 * 16;
+  for (int i = threadIdx.x; i < kpad * D; i += 256) {
+    const int k = i / D, c = i % D;
+    Bs[k * LDB + c] = k < K ? bmat[(int64_t)k * D + c] : 0.f;
+  }
+  for (int i = threadIdx.x; i < D; i += 256) {
+    GB[0][i] = gamma[i];
+    GB[1][i] = beta[i];
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 15;
+  const int lk = lane >> 4;
+  const int64_t wid =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  float pg[NB], pb[NB], ph[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    pg[b] = 0.f;
+    pb[b] = 0.f;
+    ph[b] = 0.f;
+  }
+  const float inv_d = 1.0f / (float)D;
+  const int nslices = kpad / 16;
+  // One wavefront per SIMD holds this kernel's registers, so nothing hides a
+  // load's latency but the wavefront's own work: the next row block's dz, h,
+  // mean and rstd are loaded while the current block is computed.
+  constexpr int kMaxSlices = kLnpMaxK / 16;
+  float4 dzn[kMaxSlices];
+  float hn[4][NB], mun[4], rsn[4];
+  auto prefetch = [&](int64_t r0) {
+    const int64_t ra = r0 + lr;
+#pragma unroll
+    for (int sl = 0; sl < kMaxSlices; ++sl) {
+      const int k0 = sl * 16 + lk * 4;
+      dzn[sl] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (sl < nslices && ra < rows && k0 < K)
+        dzn[sl] = *reinterpret_cast<const float4*>(dz + ra * ldz + k0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t row = r0 + lk * 4 + q;
+      const bool valid = row < rows;
+      mun[q] = valid ? mean[row] : 0.f;
+      rsn[q] = valid ? rstd[row] : 0.f;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) hn[q][b] = valid ? h[row * D + b * 16 + lr] : 0.f;
+    }
+  };
+  if (wid * 16 < rows) prefetch(wid * 16);
+  for (int64_t r0 = wid * 16; r0 < rows; r0 += nwaves * 16) {
+    float4 dzc[kMaxSlices];
+    float hv[4][NB], muv[4], rsv[4];
+#pragma unroll
+    for (int sl = 0; sl < kMaxSlices; ++sl) dzc[sl] = dzn[sl];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      muv[q] = mun[q];
+      rsv[q] = rsn[q];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) hv[q][b] = hn[q][b];
+    }
+    if (r0 + nwaves * 16 < rows) prefetch(r0 + nwaves * 16);
+    floatx4 acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sl = 0; sl < kMaxSlices; ++sl) {
+      if (sl >= nslices) break;
+      const int k0 = sl * 16 + lk * 4;
+      const float a[4] = {dzc[sl].x, dzc[sl].y, dzc[sl].z, dzc[sl].w};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const float* brow = Bs + (k0 + st) * LDB + lr;
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], brow[b * 16], acc[b], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t row = r0 + lk * 4 + q;
+      const bool valid = row < rows;
+      const float mu = muv[q], rs = rsv[q];
+      // Two passes over the row's columns: the sums, then the outputs, with
+      // x-hat and the masked gradient formed again in the second (fewer
+      // values live across the row reductions).
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float gm = GB[0][b * 16 + lr];
+        const float y = ln_affine(hv[q][b], mu, rs, gm, GB[1][b * 16 + lr]);
+        const float gy = acc[b][q] * act_grad<ACT>(y);
+        const float xh = (hv[q][b] - mu) * rs;
+        const float gx = gy * gm;
+        pg[b] = fmaf(gy, xh, pg[b]);
+        pb[b] += gy;
+        s1 += gx;
+        s2 = fmaf(gx, xh, s2);
+      }
+      s1 = gr_wave::group_sum<16>(s1) * inv_d;
+      s2 = gr_wave::group_sum<16>(s2) * inv_d;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float gm = GB[0][b * 16 + lr];
+        const float y = ln_affine(hv[q][b], mu, rs, gm, GB[1][b * 16 + lr]);
+        const float gx = acc[b][q] * act_grad<ACT>(y) * gm;
+        const float xh = (hv[q][b] - mu) * rs;
+        const float o = rs * (gx - s1 - xh * s2);
+        ph[b] += o;
+        if (valid) gh[row * D + b * 16 + lr] = o;
+      }
+    }
+  }
+  // The four lane quads hold the same columns for different rows.
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    pg[b] = gr_wave::slot_sum<16>(pg[b]);
+    pb[b] = gr_wave::slot_sum<16>(pb[b]);
+    ph[b] = gr_wave::slot_sum<16>(ph[b]);
+  }
+  if (lk == 0) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      part_gamma[wid * D + b * 16 + lr] = pg[b];
+      part_beta[wid * D + b * 16 + lr] = pb[b];
+      if (part_bias != nullptr) part_bias[wid * D + b * 16 + lr] = ph[b];
+    }
   }
 }
 
@@ -1484,6 +1645,91 @@ extern "C" int gr_ln_act_backward(const float* g, const float* h, const float* m
                                          dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
   return gr_agg::run_ln_backward<1, 4>(act, g, h, mean, rstd, gamma, beta, rows, dim, gh,
                                        dgamma, dbeta, dbias, shift, rowdot, workspace, workspace_floats, s);
+}
+
+namespace gr_agg {
+
+template <int NB>
+int run_ln_backward_product(int32_t act, const float* dz, int64_t ldz, int K, const float* bmat,
+                            const float* h, const float* mean, const float* rstd,
+                            const float* gamma, const float* beta, int64_t rows, float* gh,
+                            float* dgamma, float* dbeta, float* dbias, float* workspace,
+                            int64_t workspace_floats, hipStream_t s) {
+  constexpr int D = 16 * NB;
+  const void* kern =
+      act == GR_ACT_RELU
+          ? reinterpret_cast<const void*>(&ln_act_backward_product<NB, GR_ACT_RELU>)
+          : reinterpret_cast<const void*>(&ln_act_backward_product<NB, GR_ACT_ELU>);
+  static std::atomic<int64_t> resident[2];
+  const int ai = act == GR_ACT_RELU ? 0 : 1;
+  int64_t res = resident[ai].load(std::memory_order_relaxed);
+  if (res == 0) {
+    res = resident_waves(kern);
+    resident[ai].store(res, std::memory_order_relaxed);
+  }
+  int64_t nwaves = std::min<int64_t>(res, std::max<int64_t>(4, (rows + 15) / 16));
+  nwaves = (nwaves + 3) / 4 * 4;
+  const int nparts = dbias != nullptr ? 3 : 2;
+  const int64_t cap = (workspace_floats / D - 1) / nparts / 4 * 4;
+  GR_REQUIRE(cap >= 4, "ln_act_backward_product: workspace too small");
+  if (nwaves > cap) nwaves = cap;
+  float* pg = workspace;
+  float* pb = workspace + nwaves * D;
+  float* ph = dbias != nullptr ? workspace + 2 * nwaves * D : nullptr;
+  const unsigned blocks = (unsigned)(nwaves / 4);
+  if (act == GR_ACT_RELU)
+    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_RELU>), dim3(blocks), dim3(256), 0,
+                       s, dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh, pg, pb, ph);
+  else
+    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_ELU>), dim3(blocks), dim3(256), 0, s,
+                       dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh, pg, pb, ph);
+  GR_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(colsum_final3, dim3(final_blocks(D), (unsigned)nparts), dim3(256), 0, s, pg,
+                     (int)nwaves, D, dgamma, dbeta, dbias);
+  GR_HIP_CHECK(hipGetLastError());
+  return GR_OK;
+}
+
+}  // namespace gr_agg
+
+extern "C" int gr_ln_act_backward_product(const float* dz, int64_t ldz, int64_t k,
+                                          const float* bmat, const float* h, const float* mean,
+                                          const float* rstd, const float* gamma,
+                                          const float* beta, int32_t act, int64_t rows,
+                                          int64_t dim, float* gh, float* dgamma, float* dbeta,
+                                          float* dbias, float* workspace,
+                                          int64_t workspace_floats, void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(rows >= 0 && (dim == 64 || dim == 128 || dim == 192 || dim == 256),
+             "ln_act_backward_product: dim %lld must be 64, 128, 192 or 256", (long long)dim);
+  GR_REQUIRE(k >= 1 && k <= gr_agg::kLnpMaxK && k % 4 == 0 && ldz >= k && ldz % 4 == 0,
+             "ln_act_backward_product: k %lld must be a multiple of 4 in [4, %d], ldz a "
+             "multiple of 4 >= k", (long long)k, gr_agg::kLnpMaxK);
+  GR_REQUIRE(act == GR_ACT_RELU || act == GR_ACT_ELU,
+             "ln_act_backward_product: unknown activation %d", act);
+  GR_REQUIRE(bmat && gamma && beta && dgamma && dbeta && workspace &&
+                 (rows == 0 || (dz && h && mean && rstd && gh)),
+             "ln_act_backward_product: NULL pointer");
+  GR_REQUIRE(rows == 0 || gr_agg::aligned(dz, 16), "ln_act_backward_product: dz not 16-byte aligned");
+  hipStream_t s = gr::as_stream(stream);
+  switch (dim) {
+    case 64:
+      return gr_agg::run_ln_backward_product<4>(act, dz, ldz, (int)k, bmat, h, mean, rstd, gamma,
+                                                beta, rows, gh, dgamma, dbeta, dbias, workspace,
+                                                workspace_floats, s);
+    case 128:
+      return gr_agg::run_ln_backward_product<8>(act, dz, ldz, (int)k, bmat, h, mean, rstd, gamma,
+                                                beta, rows, gh, dgamma, dbeta, dbias, workspace,
+                                                workspace_floats, s);
+    case 192:
+      return gr_agg::run_ln_backward_product<12>(act, dz, ldz, (int)k, bmat, h, mean, rstd,
+                                                 gamma, beta, rows, gh, dgamma, dbeta, dbias,
+                                                 workspace, workspace_floats, s);
+    default:
+      return gr_agg::run_ln_backward_product<16>(act, dz, ldz, (int)k, bmat, h, mean, rstd,
+                                                 gamma, beta, rows, gh, dgamma, dbeta, dbias,
+                                                 workspace, workspace_floats, s);
+  }
 }
 
 extern "C" int gr_bias_ln_act(const float* z, int64_t ldz, const float* bias,

@@ -17,8 +17,8 @@ from typing import Dict, List, Optional, Set
 import torch
 from torch import Tensor
 
-from grinnder_amd.aggregation import (KernelTimer, ProjectedSink, dense_region, gather_rows,
-                                     scatter_add_rows)
+from grinnder_amd.aggregation import (KernelTimer, LNProductSink, ProjectedSink, dense_region,
+                                      gather_rows, scatter_add_rows)
 from grinnder_amd.dense import OutputRows, gemm_nt, gemm_tn
 from grinnder_amd.loss import masked_cross_entropy
 
@@ -494,14 +494,7 @@ class ProjectedLayers:
         """Z_layer[lo:hi] = x Wᵀ (no autograd); with Z wider than W's rows,
         through W padded with zero rows, which writes the pad columns' zeros."""
         z = self._zbuf(layer)
-        w = self._proj[layer].detach()
-        if z.size(1) != w.size(0):
-            wp = self._wpad.get(layer)
-            if wp is None:
-                with torch.no_grad():
-                    wp = torch.nn.functional.pad(w, (0, 0, 0, z.size(1) - w.size(0)))
-                self._wpad[layer] = wp
-            w = wp
+        w = self._padded_weight(layer, z.size(1))
         with torch.no_grad(), dense_region("fwd", hi - lo, w.size(1), w.size(0)):
             gemm_nt(x.detach(), w, out=z[lo:hi])
 
@@ -642,18 +635,40 @@ class ProjectedLayers:
                 self.streams.compute.wait_event(ev)
             self._x0pending = None
 
-    def _device_grad(self, layer: int, pid: int) -> Tensor:
+    def _device_grad(self, layer: int, pid: int, consumer: Optional[Tensor] = None) -> Tensor:
         """dL/d(x_layer) of partition pid's rows when layer `layer` keeps that
         gradient in HBM: dZ_layer[rows] W when it runs projected, else (a
         gathered layer) its rows of the layer's dL/dx buffer.  The halo
-        contributions of every partition are already summed in either."""
+        contributions of every partition are already summed in either.
+        `consumer`: the layer output this gradient is for; when it is a fused
+        LayerNorm output that accepts the gradient as a product (narrow W),
+        dZ and W go to its backward (LNProductSink) and the returned tensor is
+        the token that tells it so."""
         lo, hi = self.graph._range(pid)
         if layer not in self._proj:
             return self._gxbufs[layer][lo:hi]
         w = self._proj[layer]
         dz = self._dzbufs[layer][lo:hi]
+        if consumer is not None:
+            wp = self._padded_weight(layer, dz.size(1))
+            ln_sink = LNProductSink.accepts(consumer, wp)
+            if ln_sink is not None:
+                return ln_sink.hand_over(dz, wp, consumer.shape)
         with dense_region("dx", hi - lo, w.size(0), w.size(1)):
             return gemm_nt(dz, self._dx_weight(layer, dz.size(1)))
+
+    def _padded_weight(self, layer: int, width: int) -> Tensor:
+        """The layer's input projection W with zero rows up to `width` (Z's
+        columns), formed once per epoch."""
+        w = self._proj[layer].detach()
+        if width == w.size(0):
+            return w
+        wp = self._wpad.get(layer)
+        if wp is None:
+            with torch.no_grad():
+                wp = torch.nn.functional.pad(w, (0, 0, 0, width - w.size(0)))
+            self._wpad[layer] = wp
+        return wp
 
     def _dx_weight(self, layer: int, width: int) -> Tensor:
         """The B operand of dZ W for the layer's dZ rows of `width` columns:
@@ -722,7 +737,7 @@ class ProjectedLayers:
                     if out is None:
                         out = self._device_recompute(layer, pid)
                     if from_device:
-                        out.backward(self._device_grad(layer + 1, pid))
+                        out.backward(self._device_grad(layer + 1, pid, consumer=out))
                     else:
                         out.backward(gbuf[pid])
                         gbuf.release(pid)

@@ -360,3 +360,79 @@ def test_fused_epilogues_write_into_output_block(gpu):
         with pytest.raises(ValueError):
             fn(*inputs, OutputRows(block[:rows, :dout - 4]))
     assert torch.all(block[:100] == 7.0) and torch.all(block[100 + rows:] == 7.0)
+
+
+@pytest.mark.parametrize("rows,k,dim,act,bias", [(5000, 48, 256, "relu", True),
+                                                 (3001, 20, 256, "elu", False),
+                                                 (777, 64, 128, "relu", True),
+                                                 (17, 4, 64, "elu", True), (0, 48, 256, "relu", True)])
+def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias):
+    """The LayerNorm/activation backward with dL/dout = dz B formed inside the
+    pass, against float64 autograd of act(LayerNorm(h)) with that gradient."""
+    from grinnder_amd.aggregation import ln_act_backward_product
+
+    h = _randn(rows, dim, seed=dim + k, dev=gpu)
+    gamma = 1 + 0.1 * _randn(dim, seed=1, dev=gpu)
+    beta = 0.1 * _randn(dim, seed=2, dev=gpu)
+    dz = _randn(rows, k, seed=3, dev=gpu)
+    b = 0.2 * _randn(k, dim, seed=4, dev=gpu)
+    h64 = h.double()
+    mean = h64.mean(1)
+    rstd = 1.0 / torch.sqrt(h64.var(1, unbiased=False) + 1e-5)
+    gh, dg, db_, dbias = ln_act_backward_product(dz, b, h, mean.float().contiguous(),
+                                                 rstd.float().contiguous(), gamma, beta,
+                                                 bias, act)
+    torch.cuda.synchronize()
+    if rows == 0:
+        assert gh.shape == (0, dim)
+        return
+    hh = h64.clone().requires_grad_(True)
+    g64 = gamma.double().requires_grad_(True)
+    b64 = beta.double().requires_grad_(True)
+    f = torch.relu if act == "relu" else torch.nn.functional.elu
+    out = f(torch.nn.functional.layer_norm(hh, (dim,), g64, b64, 1e-5))
+    out.backward(dz.double() @ b.double())
+    assert max_abs_norm_err(gh, hh.grad) <= TOL
+    assert max_abs_norm_err(dg, g64.grad) <= TOL
+    assert max_abs_norm_err(db_, b64.grad) <= TOL
+    if bias:
+        assert max_abs_norm_err(dbias, hh.grad.sum(0)) <= TOL
+    else:
+        assert dbias is None
+
+
+@pytest.mark.parametrize("extra_consumer", [False, True])
+def test_layernorm_takes_narrow_product_gradient(gpu, extra_consumer):
+    """A fused LayerNorm/ReLU output consumed by a narrow padded GCN product
+    (47 outputs, the C2 last layer's shape) hands its input gradient to the
+    LayerNorm as dZ W: every gradient equals the same model built without the
+    handoff (the LayerNorm output copied first, so it carries no sink), to
+    TOL against each other and against float64.  With a second consumer of
+    the output the LayerNorm receives autograd's sum and completes it."""
+    from grinnder_amd.aggregation import gcn_aggregate_ln_relu, gcn_linear_aggregate
+    from grinnder_amd.data.adjacency import Adjacency
+    from tests.graphs import random_bipartite
+
+    n, d, c = 3000, 256, 47
+    rowptr, col, val = random_bipartite(n, n, 10, seed=9, long_rows=2, long_len=700)
+    adj = Adjacency(rowptr, col, val, (n, n), seg_len=256)
+    z = _randn(n, d, seed=5, dev=gpu)
+    params = [_randn(d, seed=6, dev=gpu), 1 + 0.1 * _randn(d, seed=7, dev=gpu),
+              0.1 * _randn(d, seed=8, dev=gpu), 0.1 * _randn(c, d, seed=9, dev=gpu),
+              _randn(c, seed=10, dev=gpu)]
+    go = _randn(n, c, seed=11, dev=gpu)
+    grads = []
+    for handoff in (True, False):
+        zz = z.clone().requires_grad_(True)
+        b1, g1, be1, w2, b2 = [p.clone().requires_grad_(True) for p in params]
+        out1 = gcn_aggregate_ln_relu(zz, adj, b1, g1, be1)
+        x2 = out1 if handoff else out1 * 1.0
+        y = gcn_linear_aggregate(x2, w2, adj, b2)
+        loss = (y * go).sum()
+        if extra_consumer:
+            loss = loss + out1[:, :3].square().sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        grads.append([t.grad for t in (zz, b1, g1, be1, w2, b2)])
+    for g0, g1 in zip(*grads):
+        assert max_abs_norm_err(g0, g1.double()) <= TOL
