@@ -554,17 +554,28 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
 // The LayerNorm/activation backward of ln_relu_backward with its incoming
 // gradient formed in place: g = dz B (dz [rows, K] the next layer's gradient
 // of its projection, K <= 64; B [K, D] row-major, the next layer's W), on the
-// matrix cores, so g never goes to memory.  D = 16 NB.  A wavefront takes 16
-// rows at a time (grid-stride): it holds g for them as NB blocks of
-// v_mfma_f32_16x16x4_f32 (lane (lr, lk) holds columns b * 16 + lr of rows
-// 4 lk + q), reads h in the same layout (64 contiguous bytes per row per
-// instruction), reduces each row over the 16 lanes that share it, and writes
-// gh.  B is staged in LDS once per workgroup (row stride D + 16: the four rows
-// one instruction reads start 16 banks apart).  Partials of dgamma, dbeta and
-// dbias per wavefront, reduced in order afterwards (colsum_final3).  k runs in
+// matrix cores, so g never goes to memory.  D = 16 NB.
+//
+// A pair of wavefronts takes 16 rows at a time, each wavefront half of the
+// columns (grid-stride over 32-row steps per workgroup): it holds g for its
+// rows and columns as NB / 2 blocks of v_mfma_f32_16x16x4_f32 (lane (lr, lk)
+// holds columns c0 + b * 16 + lr of rows 4 lk + q), reads h in the same
+// layout (64 contiguous bytes per row per instruction), and the two halves'
+// row sums meet in LDS, added in half order by both, before the outputs are
+// formed.  Half the columns per wavefront leaves room for two wavefronts per
+// SIMD, so one's loads overlap the other's work; each also loads the next
+// step's dz, h, mean and rstd while computing this one.  B, gamma and beta
+// are staged in LDS once per workgroup (B's row stride D + 16: the four rows
+// one instruction reads start 16 banks apart).  Partials of dgamma, dbeta
+// and dbias per pair, reduced in order afterwards (colsum_final3).  k runs in
 // slices of 16 with the k order of gemm_nt_kernel (MFMA s of a slice sums
 // k = 4 q + s over the lane quads q), zeros past K.
 constexpr int kLnpMaxK = 64;
+
+template <int NB>
+constexpr size_t lnp_lds_bytes(int kpad) {
+  return ((size_t)kpad * (16 * NB + 16) + 2 * 16 * NB + 4 * 2 * 2 * 4 * 2) * sizeof(float);
+}
 
 template <int NB, int ACT>
 __global__ __launch_bounds__(256) void ln_act_backward_product(
@@ -576,40 +587,42 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
     float* __restrict__ part_bias) {
   typedef float floatx4 __attribute__((ext_vector_type(4)));
   constexpr int D = 16 * NB;
+  constexpr int NH = NB / 2;  // blocks per wavefront
   constexpr int LDB = D + 16;
-  __shared__ float Bs[kLnpMaxK * LDB];
-  __shared__ float GB[2][D];  // gamma, beta
+  static_assert(NB % 2 == 0, "two halves of whole 16-column blocks");
+  extern __shared__ float lnp_smem[];
   const int kpad = (K + 15) / 16 * 16;
+  float* Bs = lnp_smem;
+  float* GB = Bs + kpad * LDB;  // gamma [D], beta [D]
+  float* red = GB + 2 * D;      // [q][pair][half][lk][s1, s2]
   for (int i = threadIdx.x; i < kpad * D; i += 256) {
     const int k = i / D, c = i % D;
     Bs[k * LDB + c] = k < K ? bmat[(int64_t)k * D + c] : 0.f;
   }
   for (int i = threadIdx.x; i < D; i += 256) {
-    GB[0][i] = gamma[i];
-    GB[1][i] = beta[i];
+    GB[i] = gamma[i];
+    GB[D + i] = beta[i];
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
   const int lr = lane & 15;
   const int lk = lane >> 4;
-  const int64_t wid =
-      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t nwaves = (int64_t)gridDim.x * 4;
-  float pg[NB], pb[NB], ph[NB];
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int pair = wave >> 1;
+  const int hf = wave & 1;
+  const int c0 = hf * (D / 2);
+  float pg[NH], pb[NH], ph[NH];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NH; ++b) {
     pg[b] = 0.f;
     pb[b] = 0.f;
     ph[b] = 0.f;
   }
   const float inv_d = 1.0f / (float)D;
   const int nslices = kpad / 16;
-  // One wavefront per SIMD holds this kernel's registers, so nothing hides a
-  // load's latency but the wavefront's own work: the next row block's dz, h,
-  // mean and rstd are loaded while the current block is computed.
   constexpr int kMaxSlices = kLnpMaxK / 16;
   float4 dzn[kMaxSlices];
-  float hn[4][NB], mun[4], rsn[4];
+  float hn[4][NH], mun[4], rsn[4];
   auto prefetch = [&](int64_t r0) {
     const int64_t ra = r0 + lr;
 #pragma unroll
@@ -626,13 +639,17 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
       mun[q] = valid ? mean[row] : 0.f;
       rsn[q] = valid ? rstd[row] : 0.f;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) hn[q][b] = valid ? h[row * D + b * 16 + lr] : 0.f;
+      for (int b = 0; b < NH; ++b) hn[q][b] = valid ? h[row * D + c0 + b * 16 + lr] : 0.f;
     }
   };
-  if (wid * 16 < rows) prefetch(wid * 16);
-  for (int64_t r0 = wid * 16; r0 < rows; r0 += nwaves * 16) {
+  const int64_t step = (int64_t)gridDim.x * 32;
+  if ((int64_t)blockIdx.x * 32 < rows) prefetch((int64_t)blockIdx.x * 32 + 16 * pair);
+  // The loop bound is the workgroup's (not the pair's): every wavefront
+  // reaches every barrier; a pair past the last row computes zeros.
+  for (int64_t rb = (int64_t)blockIdx.x * 32; rb < rows; rb += step) {
+    const int64_t r0 = rb + 16 * pair;
     float4 dzc[kMaxSlices];
-    float hv[4][NB], muv[4], rsv[4];
+    float hv[4][NH], muv[4], rsv[4];
 #pragma unroll
     for (int sl = 0; sl < kMaxSlices; ++sl) dzc[sl] = dzn[sl];
 #pragma unroll
@@ -640,12 +657,12 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
       muv[q] = mun[q];
       rsv[q] = rsn[q];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) hv[q][b] = hn[q][b];
+      for (int b = 0; b < NH; ++b) hv[q][b] = hn[q][b];
     }
-    if (r0 + nwaves * 16 < rows) prefetch(r0 + nwaves * 16);
-    floatx4 acc[NB];
+    if (rb + step < rows) prefetch(r0 + step);
+    floatx4 acc[NH];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < NH; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sl = 0; sl < kMaxSlices; ++sl) {
       if (sl >= nslices) break;
@@ -653,9 +670,9 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
       const float a[4] = {dzc[sl].x, dzc[sl].y, dzc[sl].z, dzc[sl].w};
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const float* brow = Bs + (k0 + st) * LDB + lr;
+        const float* brow = Bs + (k0 + st) * LDB + c0 + lr;
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int b = 0; b < NH; ++b)
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], brow[b * 16], acc[b], 0, 0, 0);
       }
     }
@@ -664,14 +681,15 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
       const int64_t row = r0 + lk * 4 + q;
       const bool valid = row < rows;
       const float mu = muv[q], rs = rsv[q];
-      // Two passes over the row's columns: the sums, then the outputs, with
-      // x-hat and the masked gradient formed again in the second (fewer
-      // values live across the row reductions).
+      // Two passes over the half row: the sums, then the outputs, with x-hat
+      // and the masked gradient formed again in the second (fewer values
+      // live across the row reductions).
       float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const float gm = GB[0][b * 16 + lr];
-        const float y = ln_affine(hv[q][b], mu, rs, gm, GB[1][b * 16 + lr]);
+      for (int b = 0; b < NH; ++b) {
+        const int c = c0 + b * 16 + lr;
+        const float gm = GB[c];
+        const float y = ln_affine(hv[q][b], mu, rs, gm, GB[D + c]);
         const float gy = acc[b][q] * act_grad<ACT>(y);
         const float xh = (hv[q][b] - mu) * rs;
         const float gx = gy * gm;
@@ -680,33 +698,44 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
         s1 += gx;
         s2 = fmaf(gx, xh, s2);
       }
-      s1 = gr_wave::group_sum<16>(s1) * inv_d;
-      s2 = gr_wave::group_sum<16>(s2) * inv_d;
+      s1 = gr_wave::group_sum<16>(s1);
+      s2 = gr_wave::group_sum<16>(s2);
+      float* rq = red + q * 32 + pair * 16;
+      if (lr == 0) {
+        rq[hf * 8 + lk * 2 + 0] = s1;
+        rq[hf * 8 + lk * 2 + 1] = s2;
+      }
+      __syncthreads();
+      s1 = (rq[lk * 2 + 0] + rq[8 + lk * 2 + 0]) * inv_d;
+      s2 = (rq[lk * 2 + 1] + rq[8 + lk * 2 + 1]) * inv_d;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const float gm = GB[0][b * 16 + lr];
-        const float y = ln_affine(hv[q][b], mu, rs, gm, GB[1][b * 16 + lr]);
+      for (int b = 0; b < NH; ++b) {
+        const int c = c0 + b * 16 + lr;
+        const float gm = GB[c];
+        const float y = ln_affine(hv[q][b], mu, rs, gm, GB[D + c]);
         const float gx = acc[b][q] * act_grad<ACT>(y) * gm;
         const float xh = (hv[q][b] - mu) * rs;
         const float o = rs * (gx - s1 - xh * s2);
         ph[b] += o;
-        if (valid) gh[row * D + b * 16 + lr] = o;
+        if (valid) gh[row * D + c] = o;
       }
     }
   }
   // The four lane quads hold the same columns for different rows.
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NH; ++b) {
     pg[b] = gr_wave::slot_sum<16>(pg[b]);
     pb[b] = gr_wave::slot_sum<16>(pb[b]);
     ph[b] = gr_wave::slot_sum<16>(ph[b]);
   }
   if (lk == 0) {
+    const int64_t prow = (int64_t)blockIdx.x * 2 + pair;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      part_gamma[wid * D + b * 16 + lr] = pg[b];
-      part_beta[wid * D + b * 16 + lr] = pb[b];
-      if (part_bias != nullptr) part_bias[wid * D + b * 16 + lr] = ph[b];
+    for (int b = 0; b < NH; ++b) {
+      const int c = c0 + b * 16 + lr;
+      part_gamma[prow * D + c] = pg[b];
+      part_beta[prow * D + c] = pb[b];
+      if (part_bias != nullptr) part_bias[prow * D + c] = ph[b];
     }
   }
 }
@@ -1656,36 +1685,41 @@ int run_ln_backward_product(int32_t act, const float* dz, int64_t ldz, int K, co
                             float* dgamma, float* dbeta, float* dbias, float* workspace,
                             int64_t workspace_floats, hipStream_t s) {
   constexpr int D = 16 * NB;
+  const int kpad = (K + 15) / 16 * 16;
+  const size_t lds = lnp_lds_bytes<NB>(kpad);
   const void* kern =
       act == GR_ACT_RELU
           ? reinterpret_cast<const void*>(&ln_act_backward_product<NB, GR_ACT_RELU>)
           : reinterpret_cast<const void*>(&ln_act_backward_product<NB, GR_ACT_ELU>);
-  static std::atomic<int64_t> resident[2];
-  const int ai = act == GR_ACT_RELU ? 0 : 1;
-  int64_t res = resident[ai].load(std::memory_order_relaxed);
-  if (res == 0) {
-    res = resident_waves(kern);
-    resident[ai].store(res, std::memory_order_relaxed);
-  }
-  int64_t nwaves = std::min<int64_t>(res, std::max<int64_t>(4, (rows + 15) / 16));
-  nwaves = (nwaves + 3) / 4 * 4;
+  // Workgroups the device holds at once with this LDS size (recomputed per
+  // call: the size depends on K).
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess)
+    per_cu = 1, cus = 256;
+  int64_t wgs = std::min<int64_t>((int64_t)std::max(per_cu, 1) * std::max(cus, 1),
+                                  std::max<int64_t>(1, (rows + 31) / 32));
+  // Partial rows: two per workgroup (one per wavefront pair).
   const int nparts = dbias != nullptr ? 3 : 2;
-  const int64_t cap = (workspace_floats / D - 1) / nparts / 4 * 4;
-  GR_REQUIRE(cap >= 4, "ln_act_backward_product: workspace too small");
-  if (nwaves > cap) nwaves = cap;
+  const int64_t cap = (workspace_floats / D - 1) / nparts / 2;
+  GR_REQUIRE(cap >= 1, "ln_act_backward_product: workspace too small");
+  if (wgs > cap) wgs = cap;
+  const int64_t prows = 2 * wgs;
   float* pg = workspace;
-  float* pb = workspace + nwaves * D;
-  float* ph = dbias != nullptr ? workspace + 2 * nwaves * D : nullptr;
-  const unsigned blocks = (unsigned)(nwaves / 4);
+  float* pb = workspace + prows * D;
+  float* ph = dbias != nullptr ? workspace + 2 * prows * D : nullptr;
   if (act == GR_ACT_RELU)
-    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_RELU>), dim3(blocks), dim3(256), 0,
-                       s, dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh, pg, pb, ph);
+    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_RELU>), dim3((unsigned)wgs),
+                       dim3(256), lds, s, dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh,
+                       pg, pb, ph);
   else
-    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_ELU>), dim3(blocks), dim3(256), 0, s,
-                       dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh, pg, pb, ph);
+    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_ELU>), dim3((unsigned)wgs),
+                       dim3(256), lds, s, dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh,
+                       pg, pb, ph);
   GR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(colsum_final3, dim3(final_blocks(D), (unsigned)nparts), dim3(256), 0, s, pg,
-                     (int)nwaves, D, dgamma, dbeta, dbias);
+                     (int)prows, D, dgamma, dbeta, dbias);
   GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
