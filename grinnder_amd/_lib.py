@@ -55,7 +55,7 @@ _SIGNATURES = {
     "gr_gcn_aggregate_ln_relu": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _f32, _i64,
                                  _i64, _P, _P, _P, _P, _P, _i64, _P],
     "gr_ln_act_backward_product": [_P, _i64, _i64, _P, _P, _P, _P, _P, _P, _i32, _i64, _i64, _P,
-                                   _P, _P, _P, _P, _i64, _P],
+                                   _P, _P, _P, _P, _P, _P, _i64, _P],
     "gr_ln_act_backward": [_P, _P, _P, _P, _P, _P, _i32, _i64, _i64, _P, _P, _P, _P, _P, _P,
                            _P, _i64, _P],
     "gr_bias_ln_act": [_P, _i64, _P, _P, _P, _f32, _i32, _i64, _i64, _P, _P, _P, _P, _P],

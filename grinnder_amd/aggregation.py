@@ -450,10 +450,12 @@ class LNProductSink:
 
 def ln_act_backward_product(dz: Tensor, w: Tensor, h: Tensor, mean: Tensor, rstd: Tensor,
                             gamma: Tensor, beta: Tensor, with_bias: bool = False,
-                            act: str = "relu"):
+                            act: str = "relu", shift: Optional[Tensor] = None,
+                            rowdot: Optional[Tensor] = None):
     """ln_act_backward with dL/dout = dz W formed inside the pass (GPU):
     dz [rows, K] (K <= 64, a multiple of 4), w [K, D] with D in {64, 128, 192,
-    256}.  Returns (dL/dh, dgamma, dbeta, dbias or None)."""
+    256}.  Returns (dL/dh, dgamma, dbeta, dbias or None); `shift` / `rowdot`
+    as in ln_act_backward."""
     B, D = h.shape
     dz = dz.contiguous()
     w = w.contiguous()
@@ -469,8 +471,9 @@ def ln_act_backward_product(dz: Tensor, w: Tensor, h: Tensor, mean: Tensor, rstd
     _lib.call("gr_ln_act_backward_product", dz.data_ptr(), dz.size(1), dz.size(1),
               w.data_ptr(), h.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
               gamma.data_ptr(), beta.data_ptr(), _lib.ACTIVATIONS[act], B, D, gh.data_ptr(),
-              dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias), ws.data_ptr(),
-              ws.numel(), _lib.stream_handle())
+              dgamma.data_ptr(), dbeta.data_ptr(), _lib.ptr(dbias),
+              _lib.ptr(shift.contiguous() if shift is not None else None), _lib.ptr(rowdot),
+              ws.data_ptr(), ws.numel(), _lib.stream_handle())
     return gh, dgamma, dbeta, dbias
 
 

@@ -11,6 +11,7 @@
 // not depend on scheduling (no atomics).
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "gr_internal.h"
 #include "wave.h"
@@ -229,10 +230,13 @@ __device__ __forceinline__ float act_fwd(float y) {
   else return y > 0.f ? y : expm1f(y);
 }
 
+// ELU's derivative exp(y) for y <= 0 on the hardware base-2 exponential:
+// relative error about |y| 2^-24 from rounding y log2(e), plus the
+// instruction's own (1 ulp); below y = -87 it flushes to zero.
 template <int ACT>
 __device__ __forceinline__ float act_grad(float y) {
   if constexpr (ACT == GR_ACT_RELU) return y > 0.f ? 1.f : 0.f;
-  else return y > 0.f ? 1.f : expf(y);
+  else return y > 0.f ? 1.f : __builtin_amdgcn_exp2f(y * 1.44269504f);
 }
 
 template <int VEC, int NCH, int ACT = GR_ACT_RELU>
@@ -568,23 +572,30 @@ __global__ __launch_bounds__(256) void ln_relu_backward(
 // are staged in LDS once per workgroup (B's row stride D + 16: the four rows
 // one instruction reads start 16 banks apart).  Partials of dgamma, dbeta
 // and dbias per pair, reduced in order afterwards (colsum_final3).  k runs in
-// slices of 16 with the k order of gemm_nt_kernel (MFMA s of a slice sums
-// k = 4 q + s over the lane quads q), zeros past K.
+// KS slices of 16 (K <= 16 KS) with the k order of gemm_nt_kernel (MFMA s of a
+// slice sums k = 4 q + s over the lane quads q), zeros past K.  With DOT it
+// also forms rowdot[r] = <gh_r, h_r - shift>, the two halves added in half
+// order.  KS and DOT are template arguments so the common case (K <= 32, no
+// dot) keeps its registers within two wavefronts per SIMD; two per SIMD are
+// asked of the compiler (it then holds the accumulators in the VGPR half
+// of the register file, without spills, at every instance).
 constexpr int kLnpMaxK = 64;
 
 template <int NB>
 constexpr size_t lnp_lds_bytes(int kpad) {
-  return ((size_t)kpad * (16 * NB + 16) + 2 * 16 * NB + 4 * 2 * 2 * 4 * 2) * sizeof(float);
+  return ((size_t)kpad * (16 * NB + 16) + 3 * 16 * NB + 4 * 2 * 2 * 4 * 3) * sizeof(float);
 }
 
-template <int NB, int ACT>
-__global__ __launch_bounds__(256) void ln_act_backward_product(
+template <int NB, int ACT, int KS, bool DOT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+ln_act_backward_product(
     const float* __restrict__ dz, int64_t ldz, int K, const float* __restrict__ bmat,
     const float* __restrict__ h, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, int64_t rows, float* __restrict__ gh,
     float* __restrict__ part_gamma, float* __restrict__ part_beta,
-    float* __restrict__ part_bias) {
+    float* __restrict__ part_bias, const float* __restrict__ shift,
+    float* __restrict__ rowdot) {
   typedef float floatx4 __attribute__((ext_vector_type(4)));
   constexpr int D = 16 * NB;
   constexpr int NH = NB / 2;  // blocks per wavefront
@@ -593,8 +604,8 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
   extern __shared__ float lnp_smem[];
   const int kpad = (K + 15) / 16 * 16;
   float* Bs = lnp_smem;
-  float* GB = Bs + kpad * LDB;  // gamma [D], beta [D]
-  float* red = GB + 2 * D;      // [q][pair][half][lk][s1, s2]
+  float* GB = Bs + kpad * LDB;  // gamma [D], beta [D], shift [D]
+  float* red = GB + 3 * D;      // [q][pair][half][lk][s1, s2], then [q][pair][half][lk] dots
   for (int i = threadIdx.x; i < kpad * D; i += 256) {
     const int k = i / D, c = i % D;
     Bs[k * LDB + c] = k < K ? bmat[(int64_t)k * D + c] : 0.f;
@@ -602,6 +613,7 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
   for (int i = threadIdx.x; i < D; i += 256) {
     GB[i] = gamma[i];
     GB[D + i] = beta[i];
+    if (DOT) GB[2 * D + i] = shift != nullptr ? shift[i] : 0.f;
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
@@ -620,7 +632,7 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
   }
   const float inv_d = 1.0f / (float)D;
   const int nslices = kpad / 16;
-  constexpr int kMaxSlices = kLnpMaxK / 16;
+  constexpr int kMaxSlices = KS;
   float4 dzn[kMaxSlices];
   float hn[4][NH], mun[4], rsn[4];
   auto prefetch = [&](int64_t r0) {
@@ -708,6 +720,7 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
       __syncthreads();
       s1 = (rq[lk * 2 + 0] + rq[8 + lk * 2 + 0]) * inv_d;
       s2 = (rq[lk * 2 + 1] + rq[8 + lk * 2 + 1]) * inv_d;
+      float dot = 0.f;
 #pragma unroll
       for (int b = 0; b < NH; ++b) {
         const int c = c0 + b * 16 + lr;
@@ -717,7 +730,25 @@ __global__ __launch_bounds__(256) void ln_act_backward_product(
         const float xh = (hv[q][b] - mu) * rs;
         const float o = rs * (gx - s1 - xh * s2);
         ph[b] += o;
+        if (DOT) dot = fmaf(o, hv[q][b] - GB[2 * D + c], dot);
         if (valid) gh[row * D + c] = o;
+      }
+      if constexpr (DOT) {
+        dot = gr_wave::group_sum<16>(dot);
+        if (lr == 0) red[128 + q * 16 + pair * 8 + hf * 4 + lk] = dot;
+      }
+    }
+    if constexpr (DOT) {
+      // The halves' dots meet after the last row's outputs (the next write
+      // of this region follows the next step's first barrier).
+      __syncthreads();
+      if (hf == 0 && lr == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t row = r0 + lk * 4 + q;
+          const float* rd = red + 128 + q * 16 + pair * 8;
+          if (row < rows) rowdot[row] = rd[lk] + rd[4 + lk];
+        }
       }
     }
   }
@@ -1682,15 +1713,30 @@ template <int NB>
 int run_ln_backward_product(int32_t act, const float* dz, int64_t ldz, int K, const float* bmat,
                             const float* h, const float* mean, const float* rstd,
                             const float* gamma, const float* beta, int64_t rows, float* gh,
-                            float* dgamma, float* dbeta, float* dbias, float* workspace,
-                            int64_t workspace_floats, hipStream_t s) {
+                            float* dgamma, float* dbeta, float* dbias, const float* shift,
+                            float* rowdot, float* workspace, int64_t workspace_floats,
+                            hipStream_t s) {
   constexpr int D = 16 * NB;
   const int kpad = (K + 15) / 16 * 16;
   const size_t lds = lnp_lds_bytes<NB>(kpad);
-  const void* kern =
-      act == GR_ACT_RELU
-          ? reinterpret_cast<const void*>(&ln_act_backward_product<NB, GR_ACT_RELU>)
-          : reinterpret_cast<const void*>(&ln_act_backward_product<NB, GR_ACT_ELU>);
+  // The instance: activation, k slices (K <= 32 or <= 64), with or without
+  // the row dot.
+  const void* kern = nullptr;
+  auto pick = [&](auto actc, auto ksc, auto dotc) {
+    kern = reinterpret_cast<const void*>(
+        &ln_act_backward_product<NB, decltype(actc)::value, decltype(ksc)::value,
+                                 decltype(dotc)::value>);
+  };
+  auto pick_ks = [&](auto actc, auto dotc) {
+    if (kpad <= 32) pick(actc, std::integral_constant<int, 2>{}, dotc);
+    else pick(actc, std::integral_constant<int, 4>{}, dotc);
+  };
+  auto pick_dot = [&](auto actc) {
+    if (rowdot != nullptr) pick_ks(actc, std::true_type{});
+    else pick_ks(actc, std::false_type{});
+  };
+  if (act == GR_ACT_RELU) pick_dot(std::integral_constant<int, GR_ACT_RELU>{});
+  else pick_dot(std::integral_constant<int, GR_ACT_ELU>{});
   // Workgroups the device holds at once with this LDS size (recomputed per
   // call: the size depends on K).
   int dev = 0, cus = 0, per_cu = 0;
@@ -1709,14 +1755,9 @@ int run_ln_backward_product(int32_t act, const float* dz, int64_t ldz, int K, co
   float* pg = workspace;
   float* pb = workspace + prows * D;
   float* ph = dbias != nullptr ? workspace + 2 * prows * D : nullptr;
-  if (act == GR_ACT_RELU)
-    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_RELU>), dim3((unsigned)wgs),
-                       dim3(256), lds, s, dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh,
-                       pg, pb, ph);
-  else
-    hipLaunchKernelGGL((ln_act_backward_product<NB, GR_ACT_ELU>), dim3((unsigned)wgs),
-                       dim3(256), lds, s, dz, ldz, K, bmat, h, mean, rstd, gamma, beta, rows, gh,
-                       pg, pb, ph);
+  void* args[] = {&dz,   &ldz, &K,  &bmat, &h,  &mean, &rstd,  &gamma, &beta,
+                  &rows, &gh,  &pg, &pb,   &ph, &shift, &rowdot};
+  GR_HIP_CHECK(hipLaunchKernel(kern, dim3((unsigned)wgs), dim3(256), args, lds, s));
   GR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(colsum_final3, dim3(final_blocks(D), (unsigned)nparts), dim3(256), 0, s, pg,
                      (int)prows, D, dgamma, dbeta, dbias);
@@ -1731,8 +1772,9 @@ extern "C" int gr_ln_act_backward_product(const float* dz, int64_t ldz, int64_t 
                                           const float* rstd, const float* gamma,
                                           const float* beta, int32_t act, int64_t rows,
                                           int64_t dim, float* gh, float* dgamma, float* dbeta,
-                                          float* dbias, float* workspace,
-                                          int64_t workspace_floats, void* stream) {
+                                          float* dbias, const float* shift, float* rowdot,
+                                          float* workspace, int64_t workspace_floats,
+                                          void* stream) {
   gr::clear_error();
   GR_REQUIRE(rows >= 0 && (dim == 64 || dim == 128 || dim == 192 || dim == 256),
              "ln_act_backward_product: dim %lld must be 64, 128, 192 or 256", (long long)dim);
@@ -1744,25 +1786,19 @@ extern "C" int gr_ln_act_backward_product(const float* dz, int64_t ldz, int64_t 
   GR_REQUIRE(bmat && gamma && beta && dgamma && dbeta && workspace &&
                  (rows == 0 || (dz && h && mean && rstd && gh)),
              "ln_act_backward_product: NULL pointer");
-  GR_REQUIRE(rows == 0 || gr_agg::aligned(dz, 16), "ln_act_backward_product: dz not 16-byte aligned");
+  GR_REQUIRE(rows == 0 || gr_agg::aligned(dz, 16),
+             "ln_act_backward_product: dz not 16-byte aligned");
   hipStream_t s = gr::as_stream(stream);
+  auto run = [&](auto nb) {
+    return gr_agg::run_ln_backward_product<decltype(nb)::value>(
+        act, dz, ldz, (int)k, bmat, h, mean, rstd, gamma, beta, rows, gh, dgamma, dbeta, dbias,
+        shift, rowdot, workspace, workspace_floats, s);
+  };
   switch (dim) {
-    case 64:
-      return gr_agg::run_ln_backward_product<4>(act, dz, ldz, (int)k, bmat, h, mean, rstd, gamma,
-                                                beta, rows, gh, dgamma, dbeta, dbias, workspace,
-                                                workspace_floats, s);
-    case 128:
-      return gr_agg::run_ln_backward_product<8>(act, dz, ldz, (int)k, bmat, h, mean, rstd, gamma,
-                                                beta, rows, gh, dgamma, dbeta, dbias, workspace,
-                                                workspace_floats, s);
-    case 192:
-      return gr_agg::run_ln_backward_product<12>(act, dz, ldz, (int)k, bmat, h, mean, rstd,
-                                                 gamma, beta, rows, gh, dgamma, dbeta, dbias,
-                                                 workspace, workspace_floats, s);
-    default:
-      return gr_agg::run_ln_backward_product<16>(act, dz, ldz, (int)k, bmat, h, mean, rstd,
-                                                 gamma, beta, rows, gh, dgamma, dbeta, dbias,
-                                                 workspace, workspace_floats, s);
+    case 64: return run(std::integral_constant<int, 4>{});
+    case 128: return run(std::integral_constant<int, 8>{});
+    case 192: return run(std::integral_constant<int, 12>{});
+    default: return run(std::integral_constant<int, 16>{});
   }
 }
 

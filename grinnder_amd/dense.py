@@ -194,11 +194,14 @@ def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None,
 
 
 class _BiasLNAct(torch.autograd.Function):
-    """out = act(LayerNorm(z + b)); backward with gr_ln_act_backward."""
+    """out = act(LayerNorm(z + b)); backward with gr_ln_act_backward, or
+    with gr_ln_act_backward_product when the consumer of out handed its
+    gradient over as a product (aggregation.LNProductSink)."""
 
     @staticmethod
     def forward(ctx, z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
-                eps: float, act: str, sink=None, dest: Optional[OutputRows] = None) -> Tensor:
+                eps: float, act: str, sink=None, dest: Optional[OutputRows] = None,
+                ln_sink=None) -> Tensor:
         z = z.contiguous()
         rows, dim = z.shape
         dev = z.device
@@ -215,23 +218,32 @@ class _BiasLNAct(torch.autograd.Function):
         ctx.has_bias = bias is not None
         ctx.act = act
         ctx.sink = sink
+        ctx.ln_sink = ln_sink
         ctx.bias = b
         return out
 
     @staticmethod
     def backward(ctx, gout: Tensor):
-        from grinnder_amd.aggregation import ln_act_backward
+        from grinnder_amd.aggregation import ln_act_backward, ln_act_backward_product
         h, mean, rstd, g, bt = ctx.saved_tensors
         rowdot = None
         if ctx.sink is not None:
             # <dL/dz_r, z_r> with z = h - b, for the attention that produced z.
             rowdot = torch.empty(h.size(0), dtype=torch.float32, device=h.device)
-        gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias,
-                                                ctx.act, shift=ctx.bias, rowdot=rowdot)
+        prod = ctx.ln_sink.take(gout) if ctx.ln_sink is not None else None
+        if prod is not None and prod[2]:
+            gh, dgamma, dbeta, db = ln_act_backward_product(
+                prod[0], prod[1], h, mean, rstd, g, bt, ctx.has_bias, ctx.act,
+                shift=ctx.bias, rowdot=rowdot)
+        else:
+            if prod is not None:
+                gout = gout + gemm_nt(prod[0], prod[1].t().contiguous())
+            gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, ctx.has_bias,
+                                                    ctx.act, shift=ctx.bias, rowdot=rowdot)
         if ctx.sink is not None:
             ctx.sink.cdot = rowdot
             ctx.sink.grad_ptr = gh.data_ptr()
-        return gh, db, dgamma, dbeta, None, None, None, None
+        return gh, db, dgamma, dbeta, None, None, None, None, None
 
 
 def bias_ln_act(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
@@ -242,10 +254,16 @@ def bias_ln_act(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,
     shared with the GAT attention that produced z): the backward also forms
     <dL/dz_r, z_r> and leaves it there.  `dest`: write the result into that
     block and return a view of it."""
+    from grinnder_amd.aggregation import LNProductSink
     _check("z", z)
     if act not in _lib.ACTIVATIONS:
         raise ValueError(f"unknown activation {act!r}")
-    return _BiasLNAct.apply(z, bias, gamma, beta, eps, act, rowdot_sink, dest)
+    ln_sink = LNProductSink()
+    out = _BiasLNAct.apply(z, bias, gamma, beta, eps, act, rowdot_sink, dest, ln_sink)
+    # A product that consumes the output alone may hand its input gradient
+    # back as dZ W (LNProductSink).
+    out._grinnder_ln_sink = ln_sink
+    return out
 
 
 def bias_ln_relu(z: Tensor, bias: Optional[Tensor], gamma: Tensor, beta: Tensor,

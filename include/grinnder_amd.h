@@ -318,14 +318,15 @@ int gr_ln_act_backward(const float* g, const float* h, const float* mean,
  * (grinnder/nn/gcn.py:53-56, torch's Linear backward), which the reference
  * writes out and the LayerNorm/ReLU backward (grinnder/nn/gcn.py:64-73,
  * torch's LayerNorm and ReLU backward) reads back; here the product stays
- * in the matrix cores' accumulators.  Outputs and workspace as
- * gr_ln_act_backward (no rowdot); act = GR_ACT_RELU or GR_ACT_ELU. */
+ * in the matrix cores' accumulators.  Outputs, shift/rowdot and workspace
+ * as gr_ln_act_backward; act = GR_ACT_RELU or GR_ACT_ELU. */
 int gr_ln_act_backward_product(const float* dz, int64_t ldz, int64_t k, const float* b,
                                const float* h, const float* mean, const float* rstd,
                                const float* gamma, const float* beta, int32_t act,
                                int64_t rows, int64_t dim, float* gh, float* dgamma,
-                               float* dbeta, float* dbias, float* workspace,
-                               int64_t workspace_floats, void* stream);
+                               float* dbeta, float* dbias, const float* shift,
+                               float* rowdot, float* workspace, int64_t workspace_floats,
+                               void* stream);
 
 /* Column sums out[f] = sum_i X[i, f] (w == NULL), or weighted sums
  * out[f] = sum_i w[i * ldw + f / group] * X[i, f] (fp32, deterministic: fixed

@@ -362,13 +362,19 @@ def test_fused_epilogues_write_into_output_block(gpu):
     assert torch.all(block[:100] == 7.0) and torch.all(block[100 + rows:] == 7.0)
 
 
-@pytest.mark.parametrize("rows,k,dim,act,bias", [(5000, 48, 256, "relu", True),
-                                                 (3001, 20, 256, "elu", False),
-                                                 (777, 64, 128, "relu", True),
-                                                 (17, 4, 64, "elu", True), (0, 48, 256, "relu", True)])
-def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias):
+@pytest.mark.parametrize("rows,k,dim,act,bias,dot", [(5000, 48, 256, "relu", True, False),
+                                                     (3001, 20, 256, "elu", False, False),
+                                                     (3001, 20, 256, "elu", True, True),
+                                                     (777, 64, 128, "relu", True, True),
+                                                     (995, 32, 192, "elu", False, True),
+                                                     (17, 4, 64, "elu", True, False),
+                                                     (0, 48, 256, "relu", True, True)])
+def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias, dot):
     """The LayerNorm/activation backward with dL/dout = dz B formed inside the
-    pass, against float64 autograd of act(LayerNorm(h)) with that gradient."""
+    pass, against float64 autograd of act(LayerNorm(h)) with that gradient;
+    with `dot`, also rowdot[r] = <dL/dh_r, h_r - shift> (the c_i a GAT
+    attention backward takes when its output, shifted by the bias, feeds the
+    LayerNorm)."""
     from grinnder_amd.aggregation import ln_act_backward_product
 
     h = _randn(rows, dim, seed=dim + k, dev=gpu)
@@ -376,12 +382,15 @@ def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias):
     beta = 0.1 * _randn(dim, seed=2, dev=gpu)
     dz = _randn(rows, k, seed=3, dev=gpu)
     b = 0.2 * _randn(k, dim, seed=4, dev=gpu)
+    shift = 0.3 * _randn(dim, seed=5, dev=gpu)
+    rowdot = torch.full((rows,), float("nan"), device=gpu) if dot else None
     h64 = h.double()
     mean = h64.mean(1)
     rstd = 1.0 / torch.sqrt(h64.var(1, unbiased=False) + 1e-5)
     gh, dg, db_, dbias = ln_act_backward_product(dz, b, h, mean.float().contiguous(),
                                                  rstd.float().contiguous(), gamma, beta,
-                                                 bias, act)
+                                                 bias, act, shift=shift if dot else None,
+                                                 rowdot=rowdot)
     torch.cuda.synchronize()
     if rows == 0:
         assert gh.shape == (0, dim)
@@ -399,6 +408,9 @@ def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias):
         assert max_abs_norm_err(dbias, hh.grad.sum(0)) <= TOL
     else:
         assert dbias is None
+    if dot:
+        ref = (hh.grad * (h64 - shift.double())).sum(1)
+        assert max_abs_norm_err(rowdot, ref) <= TOL
 
 
 @pytest.mark.parametrize("extra_consumer", [False, True])
