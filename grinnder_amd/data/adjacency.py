@@ -149,6 +149,13 @@ class Adjacency:
             self._plans[key] = plan
         return plan
 
+    def has_device_plan(self, device) -> bool:
+        """Whether the device plan for `device` is built already."""
+        dev = torch.device(device)
+        if dev.type == "cuda" and dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        return str(dev) in self._plans
+
     def release_device(self) -> None:
         """Drops cached device plans (device memory returns to torch's allocator)."""
         self._plans.clear()

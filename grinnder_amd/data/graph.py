@@ -5,6 +5,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Any, Dict, List, Optional, Tuple
 
+import torch
 from torch import Tensor
 
 from grinnder_amd.data.adjacency import Adjacency
@@ -36,6 +37,7 @@ class PartitionedGraph:
     perm: Tensor
     ptr: Tensor
     _adjs: Dict[int, Adjacency] = field(default_factory=dict, repr=False, compare=False)
+    _whole: Optional[Adjacency] = field(default=None, repr=False, compare=False)
 
     @property
     def feat_dim(self) -> int:
@@ -79,6 +81,43 @@ class PartitionedGraph:
                             (self.partition_sizes[pid], self.expanded_sizes[pid]))
             self._adjs[pid] = adj
         return adj
+
+    def gathered_rows(self, pid: int) -> Tensor:
+        """Global ids (int64, host) of partition pid's E_p gathered rows, in
+        the column order of adj_csr[pid]: its own rows, then the halo rows
+        from p' = 0..P-1."""
+        lo, hi = self._range(pid)
+        parts = [torch.arange(lo, hi, dtype=torch.int64)]
+        for q, b in enumerate(self.boundaries[pid]):
+            if q != pid and b is not None and b.numel() > 0:
+                parts.append(b.to(torch.int64) + int(self.ptr[q]))
+        rows = torch.cat(parts)
+        if rows.numel() != self.expanded_sizes[pid]:
+            raise RuntimeError(f"partition {pid}: {rows.numel()} gathered rows, "
+                               f"expected {self.expanded_sizes[pid]}")
+        return rows
+
+    def whole_adjacency(self) -> Adjacency:
+        """Every partition's adjacency as one [N, N] adjacency over global
+        row ids (built on first use, cached): row r of partition p is global
+        row ptr[p] + r with the same edges in the same order, each column
+        mapped through gathered_rows(p)."""
+        if self._whole is None:
+            n = int(self.ptr[-1])
+            rowptr = torch.empty(n + 1, dtype=torch.int64)
+            cols, vals = [], []
+            off = 0
+            for pid in range(self.num_parts):
+                rp, col, val = self.adj_csr[pid]
+                lo, hi = self._range(pid)
+                rowptr[lo:hi] = rp[:-1].to(torch.int64) + off
+                off += int(rp[-1])
+                cols.append(self.gathered_rows(pid)[col.to(torch.int64)])
+                vals.append(val.to(torch.float32) if val is not None
+                            else torch.ones(col.numel(), dtype=torch.float32))
+            rowptr[n] = off
+            self._whole = Adjacency(rowptr, torch.cat(cols), torch.cat(vals), (n, n))
+        return self._whole
 
     def halo_amplification(self) -> float:
         """sum_p E_p / N: gathered rows per node per layer."""

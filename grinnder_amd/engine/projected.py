@@ -43,6 +43,23 @@ class _GatherRows(torch.autograd.Function):
         return None, None, None, None
 
 
+class _WholeRows(torch.autograd.Function):
+    """Z itself as the source rows of a merged layer (every partition in one
+    pass: the whole graph's adjacency indexes Z's global rows directly); the
+    backward adds dL/dZ into Z's gradient buffer dz.  `token` as in
+    _GatherRows."""
+
+    @staticmethod
+    def forward(ctx, token: Tensor, z: Tensor, dz: Tensor) -> Tensor:
+        ctx.dz = dz
+        return z.view_as(z)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        ctx.dz.add_(grad)
+        return None, None, None
+
+
 class ProjectedLayers:
     """Projected-layer machinery of Trainer (a mixin: it uses the trainer's
     graph, config, model, streams and host / device buffers)."""
@@ -99,6 +116,11 @@ class ProjectedLayers:
         # for that this epoch.
         self._gkept: Dict[tuple, Tensor] = {}
         self._gkept_left = 0
+        # Whether the last layer runs merged this epoch (every partition in
+        # one pass over the whole graph's adjacency), and its output (with
+        # its graph when training) until the loss and backward take it.
+        self._merged = False
+        self._merged_out: Optional[Tensor] = None
 
     @property
     def projected(self) -> bool:
@@ -256,6 +278,31 @@ class ProjectedLayers:
                     continue
                 free -= need
                 self._keep.add(layer)
+        # The last layer merged: one pass over the whole graph's adjacency
+        # (Z's global rows indexed directly) in place of P passes, each with
+        # its gather of Z rows, scatter of their gradient, loss and dW
+        # product.  Training needs its graph kept (one backward, no
+        # recompute).  The whole adjacency's device plan takes about 24
+        # bytes an edge and 32 a node beside the partitions' plans; its
+        # graph holds less than the P kept graphs it replaces (no gathered
+        # rows).
+        self._merged = False
+        last = self.model.num_layers - 1
+        if (cfg.merge_last_layer == "auto" and last in plan
+                and (not self.model.training or last in self._keep)):
+            whole = g._whole
+            need = 0
+            if whole is None or not whole.has_device_plan(self.device):
+                nnz = sum(int(a[1].numel()) for a in g.adj_csr)
+                need = 24 * nnz + 32 * n
+            if need:
+                if free is None:
+                    free = self._free_device_memory()
+                if need + (8 << 30) <= free:
+                    free -= need
+                    self._merged = True
+            else:
+                self._merged = True
         # A second copy of layer 0's input rows for the next epoch's upload to
         # stream into while this epoch computes.
         self._x0double = False
@@ -354,16 +401,7 @@ class ProjectedLayers:
         rows, laid out [intra | halo from p' = 0..P-1] like the host gather."""
         idx = self._grow.get(pid)
         if idx is None:
-            g = self.graph
-            lo, hi = g._range(pid)
-            parts = [torch.arange(lo, hi, dtype=torch.int64)]
-            for q, b in enumerate(g.boundaries[pid]):
-                if q != pid and b is not None and b.numel() > 0:
-                    parts.append(b.to(torch.int64) + int(g.ptr[q]))
-            idx = torch.cat(parts).to(self.device)
-            if idx.numel() != g.expanded_sizes[pid]:
-                raise RuntimeError(f"partition {pid}: {idx.numel()} gathered rows, "
-                                   f"expected {g.expanded_sizes[pid]}")
+            idx = self.graph.gathered_rows(pid).to(self.device)
             self._grow[pid] = idx
         return idx
 
@@ -456,6 +494,35 @@ class ProjectedLayers:
         s_rows = gather_rows(sc[0], self._global_rows(pid))
         return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]),
                                             dest=dest)
+
+    def _merged_call(self, layer: int, grad: bool) -> Tensor:
+        """forward_projected of every partition at once: over the whole
+        graph's adjacency on Z itself (with the attention scores of all rows,
+        where the model takes them); with grad, the backward adds dL/dZ into
+        dZ."""
+        adj = self.graph.whole_adjacency()
+        z = self._zbufs[layer]
+        if grad:
+            if self._token is None:
+                self._token = torch.zeros(0, device=self.device, requires_grad=True)
+            z = _WholeRows.apply(self._token, z, self._dzbuf(layer))
+        sc = self._scores.get(layer)
+        if sc is None:
+            return self.model.forward_projected(layer, z, adj)
+        return self.model.forward_projected(layer, z, adj, scores=sc)
+
+    def _forward_merged(self, layer: int) -> None:
+        """The merged last layer's forward: every partition's logits in one
+        pass, with its graph when training, for the one loss over all rows
+        (_compute_losses) and its backward (_backward_device)."""
+        self._prepare_layer(layer)
+        with torch.cuda.stream(self.streams.compute):
+            if self.model.training:
+                with torch.enable_grad():
+                    self._merged_out = self._merged_call(layer, grad=True)
+            else:
+                with torch.no_grad():
+                    self._merged_out = self._merged_call(layer, grad=False)
 
     def _device_forward(self, layer: int, pid: int, keep: bool,
                         dest: Optional[Tensor] = None) -> Tensor:
@@ -713,9 +780,18 @@ class ProjectedLayers:
         from_device = not last and self._grad_on_device(layer + 1)
         from_host = not last and not from_device
         gbuf = self.device_gradients[layer + 1] if not last else None
+        merged = last and self._merged_out is not None
+        if merged:
+            # One loss over all rows, formed from the merged logits: its
+            # backward runs the layer's backward once, adding dL/dZ into dZ.
+            with torch.cuda.stream(s.compute):
+                losses[0].backward()
+            self._merged_out = None
+            for pid in pids:
+                self.activations[layer][pid] = None
         if from_host:
             self._upload_grad(layer + 1, pids[0], s.h2d[0])
-        for i, pid in enumerate(pids):
+        for i, pid in enumerate(pids if not merged else []):
             k = i % pool
             if from_host:
                 self.host_gradients[layer + 1].h2d_synchronize(s.h2d[k])
@@ -764,9 +840,14 @@ class ProjectedLayers:
         if layer in self._xin:
             x = self._xres[layer]
             with torch.cuda.stream(s.compute):
-                for pid in pids:
-                    lo, hi = g._range(pid)
-                    accumulate(pid, x[lo:hi], lo, hi)
+                if merged:
+                    # One product over all rows, as the layer's forward.
+                    n = int(g.ptr[-1])
+                    accumulate(None, x[:n], 0, n)
+                else:
+                    for pid in pids:
+                        lo, hi = g._range(pid)
+                        accumulate(pid, x[lo:hi], lo, hi)
         else:
             self._each_input_partition(layer, accumulate)
         with torch.cuda.stream(s.compute):

@@ -282,6 +282,7 @@ class Trainer(ProjectedLayers):
         self._rng = {}
         self._gkept = {}
         self._scores = {}
+        self._merged_out = None
 
     def train_epoch(self, optimizer: torch.optim.Optimizer,
                     criterion: torch.nn.Module) -> Dict[str, float]:
@@ -472,6 +473,9 @@ class Trainer(ProjectedLayers):
         projected = self._device_flow(layer)
         w_next = self._proj.get(layer + 1)
         last = layer == self.model.num_layers - 1
+        if last and self._merged:
+            self._forward_merged(layer)
+            return
         if (layer + 1) in self._xin or (last and self._logits_on_device()):
             self._forward_layer_resident(layer)
             return
@@ -534,6 +538,9 @@ class Trainer(ProjectedLayers):
         if not pids:
             return losses, {"loss": 0.0, "val_acc": 0.0, "test_acc": 0.0, "_n_train": 0}
 
+        if self._merged_out is not None:
+            return self._merged_losses()
+
         loss_sums: List[Tensor] = []
         stat_rows: List[Tensor] = []
 
@@ -587,6 +594,35 @@ class Trainer(ProjectedLayers):
             "_n_train": n_train,
         }
         return losses, metrics
+
+    def _merged_losses(self):
+        """_compute_losses for a merged last layer: one loss, the sum over
+        every train row of the graph (the sum of the per-partition sums), from
+        the logits of all rows at once."""
+        g = self.graph
+        hit = self._label_cache.get(-1)
+        if hit is None:
+            n = int(g.ptr[-1])
+            hit = (g.labels[:n].to(self.device),
+                   mask_codes(g.train_mask[:n], g.val_mask[:n], g.test_mask[:n]).to(self.device))
+            self._label_cache[-1] = hit
+        y, codes = hit
+        with torch.cuda.stream(self.streams.compute):
+            loss, stats = masked_cross_entropy(self._merged_out, y, codes, "sum")
+            if not self.model.training:
+                self._merged_out = None
+            st = stats.tolist()
+            total_loss = float(loss.detach().double())
+        check_stats(st)
+        n_train = st[0]
+        self._pid_to_loss_idx = {pid: 0 for pid in self._my_pids}
+        metrics = {
+            "loss": total_loss / max(n_train, 1),
+            "val_acc": st[1] / max(st[2], 1),
+            "test_acc": st[3] / max(st[4], 1),
+            "_n_train": n_train,
+        }
+        return [loss], metrics
 
     def _labels_and_codes(self, pid: int):
         """Device labels and uint8 train/val/test codes of a partition (cached)."""

@@ -344,6 +344,68 @@ def test_projected_layers_match_gathered(gpu, model_kind, pool_size, resident, m
     assert e0["val_acc"] == e1["val_acc"]
 
 
+@pytest.mark.parametrize("model_kind", ["gcn", "gat", "gat2"])
+def test_merged_last_layer_matches_per_partition(gpu, model_kind):
+    """config.merge_last_layer: the projected last layer (kept graph) runs as
+    one pass over the whole graph's adjacency, with one loss and one dW
+    product, against the per-partition passes ('off') of the same flow, on a
+    20k-node graph with a hub destination and a hub source of 3000 edges
+    each (their rows and columns split into several work units): loss,
+    metrics and every gradient within 1e-5, evaluate() alike, and a second
+    merged epoch bit-identical to the first.  The forward's per-row sums run
+    over the same edges in the same order either way; the backward's
+    per-source sums and dW differ only in fp32 association."""
+    from grinnder_amd.data import synthetic
+
+    n, classes = 20_000, 5
+    ei = synthetic.uniform_graph(n, 200_000, seed=9)
+    hub = torch.arange(2, 3002)
+    ei = torch.cat([ei, torch.stack([hub, torch.zeros_like(hub)]),
+                    torch.stack([torch.ones_like(hub), hub + 3000])], 1)
+    nd = synthetic.node_data(n, 24, classes, seed=9)
+    torch.manual_seed(5)
+    if model_kind == "gcn":
+        make = lambda: GCN(24, 32, classes, num_layers=3, dropout=0.0, norm=True)  # noqa: E731
+    else:
+        heads = 2 if model_kind == "gat2" else 1
+        make = lambda: GAT(24, 16, classes, num_layers=2, heads=heads, dropout=0.0,  # noqa
+                           norm=True)
+    state = make().state_dict()
+    runs = {}
+    for merge in ("off", "auto", "auto"):
+        config = GriNNderConfig(num_parts=6, merge_last_layer=merge)
+        graph = build_partitioned_graph(ei, nd.x, nd.y, nd.train_mask, nd.val_mask,
+                                        nd.test_mask, config)
+        model = make().cuda()
+        model.load_state_dict(state)
+        trainer = Trainer(model, graph, config)
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        metrics = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
+        assert trainer._merged == (merge == "auto")
+        grads = {k: p.grad.detach().clone() for k, p in model.named_parameters()
+                 if p.grad is not None}
+        opt.zero_grad()
+        again = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
+        grads2 = {k: p.grad.detach().clone() for k, p in model.named_parameters()
+                  if p.grad is not None}
+        ev = trainer.evaluate(torch.nn.CrossEntropyLoss())
+        runs.setdefault(merge, []).append((metrics, grads, again, grads2, ev))
+        del trainer, model, graph
+    (m0, g0, _, _, e0), = runs["off"]
+    for m1, g1, a1, g12, e1 in runs["auto"]:
+        assert abs(m0["loss"] - m1["loss"]) <= 1e-5 * max(1.0, abs(m0["loss"]))
+        assert m0["val_acc"] == m1["val_acc"] and m0["test_acc"] == m1["test_acc"]
+        assert set(g0) == set(g1)
+        for k, err in grad_errs(g1, g0).items():
+            assert err <= 1e-5, (k, err)
+        assert a1["loss"] == m1["loss"]
+        assert all(torch.equal(g1[k], g12[k]) for k in g1)
+        assert abs(e0["loss"] - e1["loss"]) <= 1e-5 * max(1.0, abs(e0["loss"]))
+        assert e0["val_acc"] == e1["val_acc"]
+    (_, ga, _, _, _), (_, gb, _, _, _) = runs["auto"]
+    assert all(torch.equal(ga[k], gb[k]) for k in ga)
+
+
 def test_projected_layers_match_dense_vanilla(gpu):
     """The projected flow (layer 0 24 -> 16, last layer 16 -> 3, padded to 4)
     against the float64 dense GCN, and a widening first layer (8 -> 16)."""
