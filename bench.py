@@ -27,13 +27,14 @@ the reference's halo gather/scatter for partitioned configs; the oracle)
 go alongside.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1..c5]
-       [--inputs stream|resident]
+       [--inputs stream|resident] [--merge auto|last|off]
 """
 
 from __future__ import annotations
 
 import argparse
 import contextlib
+import gc
 import json
 import os
 import sys
@@ -75,6 +76,10 @@ def parse_args():
                          "default: inputs resident when the timed region starts) or uploaded "
                          "from host memory every epoch, overlapped ('stream', the "
                          "reference's data movement); GriNNderConfig.input_residency")
+    ap.add_argument("--merge", choices=("auto", "last", "off"), default="auto",
+                    help="partitioned configs: layers run as one pass over the whole "
+                         "graph where they can ('auto'), only the last layer ('last') or "
+                         "partition by partition ('off'); GriNNderConfig.merge_partitions")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
                     help="print a text summary of the rocprofv3 CSV output under DIR and exit")
@@ -106,7 +111,7 @@ CONFIGS = {
 }
 
 
-def build_graph(cfg, device, project_first="auto", inputs="resident"):
+def build_graph(cfg, device, project_first="auto", inputs="resident", merge="auto"):
     import torch
 
     from grinnder_amd.config import GriNNderConfig
@@ -129,7 +134,8 @@ def build_graph(cfg, device, project_first="auto", inputs="resident"):
         nd = synthetic.node_data(n, cfg["feat_dim"], cfg["num_classes"], seed=42)
         x = nd.x
     config = GriNNderConfig(num_parts=cfg["num_parts"], device=device,
-                            project_first=project_first, input_residency=inputs)
+                            project_first=project_first, input_residency=inputs,
+                            merge_partitions=merge)
     graph = build_partitioned_graph(ei, x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
                                     config)
     del ei
@@ -403,7 +409,7 @@ def main():
             f"MemAvailable {int(meminfo['MemAvailable']) / 2**20:.1f} GiB, cpus {os.cpu_count()}")
     except OSError:
         pass
-    graph, config = build_graph(cfg, device, args.project_first, args.inputs)
+    graph, config = build_graph(cfg, device, args.project_first, args.inputs, args.merge)
     nnz = sum(int(a[1].numel()) for a in graph.adj_csr)
 
     torch.manual_seed(42)
@@ -427,6 +433,13 @@ def main():
         graph.adjacency(pid).device_plan(device)
     torch.cuda.synchronize()
     log(f"device plans (CSR + CSC) in {time.perf_counter() - t0:.1f}s")
+    # The objects of the imports and the setup (about 270k, most of them
+    # torch's) go to the collector's permanent generation: a full collection
+    # over them stops the host for 60-70 ms, and one falling inside the few
+    # timed epochs, where the GPU waits for the host at each epoch's start,
+    # would add that to one epoch.  Nothing on the GPU changes.
+    gc.collect()
+    gc.freeze()
     regions = 0
     for w in range(args.warmup):
         # The last warmup epoch counts the timed regions of one epoch, so that
@@ -545,6 +558,7 @@ def main():
                    "projected_layers": trainer.projected_layers,
                    "inplace_layers": trainer.inplace_layers,
                    "gathered_layers": trainer.gathered_layers,
+                   "merged_layers": trainer.merged_layers,
                    "resident_inputs": trainer.resident_inputs},
         "epoch_s": round(epoch_s, 5),
         "edges_per_epoch": sum(r.edges for r in recs_agg) // args.steps,

@@ -43,6 +43,7 @@ _SIGNATURES = {
     "gr_partition_graph": [_P, _P, _i64, _i64, _i32, _dbl, _i32, _P, _P],
     "gr_csr_transpose": [_P, _P, _P, _i64, _i64, _P, _P, _P, _P],
     "gr_spmm_plan": [_P, _i64, _i32, _P, _P, _P, _P, _P],
+    "gr_spmm_plan_blocked": [_P, _i64, _i32, _P, _i64, _P, _P, _P, _P, _P],
     "gr_gcn_aggregate": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64, _i64, _P,
                          _i64, _P],
     "gr_gcn_aggregate_noalloc": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _i64, _P, _i64,

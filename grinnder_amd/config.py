@@ -40,14 +40,16 @@ class GriNNderConfig:
         gradient into one (same results up to fp32 summation order).  'off'
         gathers every layer's input rows from the host buffers as the
         reference does.  Not a field of the reference's config.
-    merge_last_layer: 'auto' runs a projected last layer (its forward graph
-        kept when training) as one pass over the whole graph's adjacency,
-        which indexes Z's global rows directly, with one loss over all rows
-        and one dW product: the same edges and per-row orders as the
-        per-partition passes, without the per-partition launches, gathers
-        and scatters (same results up to fp32 summation order in the
-        backward's per-source sums and in dW).  'off' keeps the per-partition
-        passes.  Not a field of the reference's config.
+    merge_partitions: 'auto' runs each layer that needs no host buffers
+        (projected or in place, its forward graph kept when training, its
+        output and the gradient of that output resident in HBM; and the last
+        layer on those terms) as one pass over the whole graph's adjacency,
+        which indexes Z's (or the input's) global rows directly: the same
+        edges and per-row orders as the P per-partition passes, without their
+        launches, gathers and scatters (same results up to fp32 summation
+        order in the backward's per-source sums and the last layer's dW).
+        'last' merges only the last layer, 'off' none.  Not a field of the
+        reference's config.
     input_residency: 'stream' (the reference's data movement) uploads the
         input features from pinned host memory every epoch, the next epoch's
         upload running on a side stream while this epoch computes (the
@@ -83,5 +85,5 @@ class GriNNderConfig:
     num_gpus: int = 1
 
     project_first: Literal["auto", "off"] = "auto"
-    merge_last_layer: Literal["auto", "off"] = "auto"
+    merge_partitions: Literal["auto", "last", "off"] = "auto"
     input_residency: Literal["stream", "resident"] = "stream"

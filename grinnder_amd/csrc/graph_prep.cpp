@@ -217,16 +217,26 @@ extern "C" int gr_csr_transpose(const int64_t* rowptr, const int64_t* col,
   return GR_OK;
 }
 
-extern "C" int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len,
-                            int32_t* units, int64_t* n_units, int32_t* fixups,
-                            int64_t* n_fix, int64_t* n_slots) {
-  gr::clear_error();
+namespace {
+
+// The plan of gr_spmm_plan / gr_spmm_plan_blocked: whole rows ordered block
+// by block (one block [0, rows) when block_ptr is NULL).
+int spmm_plan_impl(const int64_t* rowptr, int64_t rows, int32_t seg_len,
+                   const int64_t* block_ptr, int64_t n_blocks, int32_t* units,
+                   int64_t* n_units, int32_t* fixups, int64_t* n_fix, int64_t* n_slots) {
   GR_REQUIRE(rowptr != nullptr && rows >= 0 && seg_len > 0,
              "spmm_plan: invalid arguments");
   GR_REQUIRE(n_units != nullptr && n_fix != nullptr && n_slots != nullptr,
              "spmm_plan: count outputs are NULL");
   GR_REQUIRE(rows <= INT32_MAX && rowptr[rows] <= INT32_MAX,
              "spmm_plan: rows/nnz exceed int32");
+  if (block_ptr != nullptr) {
+    GR_REQUIRE(n_blocks >= 1 && block_ptr[0] == 0 && block_ptr[n_blocks] == rows,
+               "spmm_plan: blocks must cover [0, %lld)", (long long)rows);
+    for (int64_t k = 0; k < n_blocks; ++k)
+      GR_REQUIRE(block_ptr[k] <= block_ptr[k + 1], "spmm_plan: block %lld not monotone",
+                 (long long)k);
+  }
 
   int64_t nu = 0, nf = 0, ns = 0;
   for (int64_t r = 0; r < rows; ++r) {
@@ -265,9 +275,10 @@ extern "C" int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len
     fixups[3 * f + 2] = k;
     ++f;
   }
-  // Whole rows next, by length class (longest class first, row order within
-  // a class): kernels that give one wavefront several rows then get rows of
-  // similar length together, and the longest rows start first.
+  // Whole rows next, block by block, by length class within a block
+  // (longest class first, row order within a class): kernels that give one
+  // wavefront several rows then get rows of similar length together, the
+  // longest rows start first, and a block's rows run together.
   auto length_class = [](int64_t len) {
     int c = 0;
     while (len > 0) {
@@ -277,18 +288,43 @@ extern "C" int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len
     return c;  // 0 for empty rows, floor(log2(len)) + 1 otherwise
   };
   const int top = length_class(seg_len);
-  for (int cls = top; cls >= 0; --cls) {
-    for (int64_t r = 0; r < rows; ++r) {
-      const int64_t b = rowptr[r], e = rowptr[r + 1];
-      if (e - b > seg_len || length_class(e - b) != cls) continue;
-      units[4 * u + 0] = static_cast<int32_t>(r);
-      units[4 * u + 1] = static_cast<int32_t>(b);
-      units[4 * u + 2] = static_cast<int32_t>(e);
-      units[4 * u + 3] = -1;
-      ++u;
+  const int64_t nb = block_ptr != nullptr ? n_blocks : 1;
+  for (int64_t blk = 0; blk < nb; ++blk) {
+    const int64_t r0 = block_ptr != nullptr ? block_ptr[blk] : 0;
+    const int64_t r1 = block_ptr != nullptr ? block_ptr[blk + 1] : rows;
+    for (int cls = top; cls >= 0; --cls) {
+      for (int64_t r = r0; r < r1; ++r) {
+        const int64_t b = rowptr[r], e = rowptr[r + 1];
+        if (e - b > seg_len || length_class(e - b) != cls) continue;
+        units[4 * u + 0] = static_cast<int32_t>(r);
+        units[4 * u + 1] = static_cast<int32_t>(b);
+        units[4 * u + 2] = static_cast<int32_t>(e);
+        units[4 * u + 3] = -1;
+        ++u;
+      }
     }
   }
   return GR_OK;
+}
+
+}  // namespace
+
+extern "C" int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len,
+                            int32_t* units, int64_t* n_units, int32_t* fixups,
+                            int64_t* n_fix, int64_t* n_slots) {
+  gr::clear_error();
+  return spmm_plan_impl(rowptr, rows, seg_len, nullptr, 0, units, n_units, fixups, n_fix,
+                        n_slots);
+}
+
+extern "C" int gr_spmm_plan_blocked(const int64_t* rowptr, int64_t rows, int32_t seg_len,
+                                    const int64_t* block_ptr, int64_t n_blocks,
+                                    int32_t* units, int64_t* n_units, int32_t* fixups,
+                                    int64_t* n_fix, int64_t* n_slots) {
+  gr::clear_error();
+  GR_REQUIRE(block_ptr != nullptr, "spmm_plan: block_ptr is NULL");
+  return spmm_plan_impl(rowptr, rows, seg_len, block_ptr, n_blocks, units, n_units, fixups,
+                        n_fix, n_slots);
 }
 
 namespace {

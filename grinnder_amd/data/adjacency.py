@@ -51,27 +51,40 @@ class DevicePlan:
     bwd: Plan
 
 
-def build_plan(rowptr: Tensor, rows: int, seg_len: int, device) -> Plan:
-    """Builds the unit/fixup plan of a CSR row pointer (int64, CPU) on `device`."""
+def build_plan(rowptr: Tensor, rows: int, seg_len: int, device,
+               blocks: Optional[Tensor] = None) -> Plan:
+    """Builds the unit/fixup plan of a CSR row pointer (int64, CPU) on `device`;
+    with `blocks` (int64 row boundaries [0, ..., rows]) the whole rows run
+    block by block (gr_spmm_plan_blocked)."""
     rowptr = rowptr.to(torch.int64).contiguous()
     n_units = torch.zeros(1, dtype=torch.int64)
     n_fix = torch.zeros(1, dtype=torch.int64)
     n_slots = torch.zeros(1, dtype=torch.int64)
-    _lib.call("gr_spmm_plan", rowptr.data_ptr(), rows, seg_len, None, n_units.data_ptr(),
-              None, n_fix.data_ptr(), n_slots.data_ptr())
+    if blocks is None:
+        def plan(units, fixups):
+            _lib.call("gr_spmm_plan", rowptr.data_ptr(), rows, seg_len, units,
+                      n_units.data_ptr(), fixups, n_fix.data_ptr(), n_slots.data_ptr())
+    else:
+        blocks = blocks.to(torch.int64).contiguous()
+
+        def plan(units, fixups):
+            _lib.call("gr_spmm_plan_blocked", rowptr.data_ptr(), rows, seg_len,
+                      blocks.data_ptr(), blocks.numel() - 1, units, n_units.data_ptr(),
+                      fixups, n_fix.data_ptr(), n_slots.data_ptr())
+    plan(None, None)
     nu, nf, ns = int(n_units), int(n_fix), int(n_slots)
     units = torch.empty((max(nu, 1), 4), dtype=torch.int32)
     fixups = torch.empty((max(nf, 1), 3), dtype=torch.int32)
-    _lib.call("gr_spmm_plan", rowptr.data_ptr(), rows, seg_len, units.data_ptr(),
-              n_units.data_ptr(), fixups.data_ptr(), n_fix.data_ptr(), n_slots.data_ptr())
+    plan(units.data_ptr(), fixups.data_ptr())
     return Plan(rows=rows, units=units[:nu].to(device), fixups=fixups[:nf].to(device),
                 n_units=nu, n_fix=nf, n_slots=ns)
 
 
 def build_device_plan(rowptr: Tensor, col: Tensor, value: Optional[Tensor],
-                      sizes: Tuple[int, int], device, seg_len: int = DEFAULT_SEG_LEN
-                      ) -> DevicePlan:
-    """Uploads a host CSR (int64 rowptr/col, fp32 value) with its transpose and plans."""
+                      sizes: Tuple[int, int], device, seg_len: int = DEFAULT_SEG_LEN,
+                      row_blocks: Optional[Tensor] = None) -> DevicePlan:
+    """Uploads a host CSR (int64 rowptr/col, fp32 value) with its transpose and
+    plans; `row_blocks`: row boundaries the forward plan runs block by block."""
     rows, cols = int(sizes[0]), int(sizes[1])
     rowptr = rowptr.to(torch.int64).contiguous()
     col = col.to(torch.int64).contiguous()
@@ -94,7 +107,7 @@ def build_device_plan(rowptr: Tensor, col: Tensor, value: Optional[Tensor],
     perm = torch.empty(max(nnz, 1), dtype=torch.int32)
     _lib.call("gr_csr_transpose", rowptr.data_ptr(), col.data_ptr(), value.data_ptr(), rows,
               cols, colptr.data_ptr(), row_idx.data_ptr(), val_t.data_ptr(), perm.data_ptr())
-    fwd = build_plan(rowptr, rows, seg_len, device)
+    fwd = build_plan(rowptr, rows, seg_len, device, row_blocks)
     bwd = build_plan(colptr, cols, seg_len, device)
     return DevicePlan(
         num_dst=rows,
@@ -118,12 +131,16 @@ class Adjacency:
     """
 
     def __init__(self, rowptr: Tensor, col: Tensor, value: Optional[Tensor],
-                 sparse_sizes: Tuple[int, int], seg_len: int = DEFAULT_SEG_LEN):
+                 sparse_sizes: Tuple[int, int], seg_len: int = DEFAULT_SEG_LEN,
+                 row_blocks: Optional[Tensor] = None):
         self.rowptr = rowptr
         self.col = col
         self.value = value
         self._sizes = (int(sparse_sizes[0]), int(sparse_sizes[1]))
         self.seg_len = seg_len
+        # Row boundaries the forward plan runs block by block (the partitions
+        # of a stacked adjacency), or None.
+        self.row_blocks = row_blocks
         self._plans: Dict[str, DevicePlan] = {}
 
     def sparse_sizes(self) -> Tuple[int, int]:
@@ -145,7 +162,7 @@ class Adjacency:
         plan = self._plans.get(key)
         if plan is None:
             plan = build_device_plan(self.rowptr, self.col, self.value, self._sizes, dev,
-                                     self.seg_len)
+                                     self.seg_len, self.row_blocks)
             self._plans[key] = plan
         return plan
 

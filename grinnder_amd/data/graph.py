@@ -101,7 +101,8 @@ class PartitionedGraph:
         """Every partition's adjacency as one [N, N] adjacency over global
         row ids (built on first use, cached): row r of partition p is global
         row ptr[p] + r with the same edges in the same order, each column
-        mapped through gathered_rows(p)."""
+        mapped through gathered_rows(p).  Its forward plan runs the
+        partitions' rows partition by partition (row_blocks = ptr)."""
         if self._whole is None:
             n = int(self.ptr[-1])
             rowptr = torch.empty(n + 1, dtype=torch.int64)
@@ -116,7 +117,8 @@ class PartitionedGraph:
                 vals.append(val.to(torch.float32) if val is not None
                             else torch.ones(col.numel(), dtype=torch.float32))
             rowptr[n] = off
-            self._whole = Adjacency(rowptr, torch.cat(cols), torch.cat(vals), (n, n))
+            self._whole = Adjacency(rowptr, torch.cat(cols), torch.cat(vals), (n, n),
+                                    row_blocks=self.ptr.to(torch.int64).clone())
         return self._whole
 
     def halo_amplification(self) -> float:

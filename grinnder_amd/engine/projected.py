@@ -116,11 +116,15 @@ class ProjectedLayers:
         # for that this epoch.
         self._gkept: Dict[tuple, Tensor] = {}
         self._gkept_left = 0
-        # Whether the last layer runs merged this epoch (every partition in
-        # one pass over the whole graph's adjacency), and its output (with
-        # its graph when training) until the loss and backward take it.
-        self._merged = False
+        # Layers that run merged this epoch (every partition in one pass over
+        # the whole graph's adjacency), whether HBM has room for that
+        # adjacency's plan, the last layer's merged output (with its graph
+        # when training) until the loss and backward take it, and the whole
+        # adjacency's device row ids.
+        self._merged: Set[int] = set()
+        self._merge_room = False
         self._merged_out: Optional[Tensor] = None
+        self._wids: Optional[tuple] = None
 
     @property
     def projected(self) -> bool:
@@ -199,6 +203,7 @@ class ProjectedLayers:
         self._xin = set()
         self._keep = set()
         self._out_room = False
+        self._merge_room = False
         self._wpad = {}
         self._wtdx = {}
         if (self._fast or cfg.mode != "grinnder" or cfg.project_first == "off"
@@ -278,31 +283,23 @@ class ProjectedLayers:
                     continue
                 free -= need
                 self._keep.add(layer)
-        # The last layer merged: one pass over the whole graph's adjacency
-        # (Z's global rows indexed directly) in place of P passes, each with
-        # its gather of Z rows, scatter of their gradient, loss and dW
-        # product.  Training needs its graph kept (one backward, no
-        # recompute).  The whole adjacency's device plan takes about 24
-        # bytes an edge and 32 a node beside the partitions' plans; its
-        # graph holds less than the P kept graphs it replaces (no gathered
-        # rows).
-        self._merged = False
-        last = self.model.num_layers - 1
-        if (cfg.merge_last_layer == "auto" and last in plan
-                and (not self.model.training or last in self._keep)):
+        # Room for the whole graph's adjacency, which merged layers run on
+        # (_plan_merged): its device plan takes about 24 bytes an edge and 32
+        # a node beside the partitions' plans.  A merged layer's graph holds
+        # no more than the P kept graphs it replaces.
+        self._merge_room = False
+        if cfg.merge_partitions != "off":
             whole = g._whole
-            need = 0
-            if whole is None or not whole.has_device_plan(self.device):
+            if whole is not None and whole.has_device_plan(self.device):
+                self._merge_room = True
+            else:
                 nnz = sum(int(a[1].numel()) for a in g.adj_csr)
                 need = 24 * nnz + 32 * n
-            if need:
                 if free is None:
                     free = self._free_device_memory()
                 if need + (8 << 30) <= free:
                     free -= need
-                    self._merged = True
-            else:
-                self._merged = True
+                    self._merge_room = True
         # A second copy of layer 0's input rows for the next epoch's upload to
         # stream into while this epoch computes.
         self._x0double = False
@@ -351,6 +348,39 @@ class ProjectedLayers:
                 self._inplace.add(layer)
         for layer in self._inplace:
             del self._proj[layer]
+        self._merged = self._plan_merged()
+
+    def _plan_merged(self) -> Set[int]:
+        """The layers that run merged this epoch (config.merge_partitions):
+        projected or in place, with their graph kept when training (one
+        backward, no recompute), drawing no random numbers (dropout masks
+        stay those of the partition-by-partition order), and, below the last
+        layer, with their output and its gradient in HBM (the next layer's
+        input resident, its gradient dZ·W or an HBM buffer)."""
+        mode = self.config.merge_partitions
+        if not self._merge_room or mode == "off":
+            return set()
+        last = self.model.num_layers - 1
+        merged = set()
+        for layer in range(self.model.num_layers):
+            if mode == "last" and layer != last:
+                continue
+            if layer not in self._proj and layer not in self._inplace:
+                continue
+            if self.model.training and layer not in self._keep:
+                continue
+            if self.model.draws_per_partition(layer):
+                continue
+            if layer != last and not (layer + 1 in self._xin
+                                      and self._grad_on_device(layer + 1)):
+                continue
+            merged.add(layer)
+        return merged
+
+    @property
+    def merged_layers(self) -> List[int]:
+        """Layers that run merged this epoch (one pass over the whole graph)."""
+        return sorted(self._merged)
 
     @property
     def inplace_layers(self) -> List[int]:
@@ -495,34 +525,69 @@ class ProjectedLayers:
         return self.model.forward_projected(layer, z, adj, scores=(s_rows, sc[1][lo:hi]),
                                             dest=dest)
 
-    def _merged_call(self, layer: int, grad: bool) -> Tensor:
-        """forward_projected of every partition at once: over the whole
-        graph's adjacency on Z itself (with the attention scores of all rows,
-        where the model takes them); with grad, the backward adds dL/dZ into
-        dZ."""
+    def _whole_ids(self) -> tuple:
+        """(global source row of each edge, global row of each source row) of
+        the whole graph's adjacency, int32 on the device: its own column ids
+        and 0..N-1 (cached)."""
+        if self._wids is None:
+            plan = self.graph.whole_adjacency().device_plan(self.device)
+            n = int(self.graph.ptr[-1])
+            self._wids = (plan.idx, torch.arange(n, dtype=torch.int32, device=self.device))
+        return self._wids
+
+    def _merged_call(self, layer: int, grad: bool,
+                     dest: Optional[OutputRows] = None) -> Tensor:
+        """The layer's forward for every partition at once, over the whole
+        graph's adjacency: in place on its resident input, or on Z itself
+        (read through a sink where the model takes one, else as a tensor
+        whose gradient the backward adds into dZ), with the attention scores
+        of all rows where the model takes them.  `dest`: where the model may
+        put the output."""
         adj = self.graph.whole_adjacency()
+        if layer in self._inplace:
+            return self.model.forward_inplace(layer, self._xres[layer], adj,
+                                              self._whole_ids()[0], dest=dest)
+        sc = self._scores.get(layer)
+        extra = {} if sc is None else {"scores": sc}
+        if self._token is None:
+            self._token = torch.zeros(0, device=self.device, requires_grad=True)
+        if self.model.projected_sink_ok(layer) and int(self.graph.ptr[-1]) < 2 ** 31:
+            gidx, rows = self._whole_ids()
+            sink = ProjectedSink(self._dzbuf(layer), gidx, rows, self._token, 0)
+            return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink,
+                                                dest=dest, **extra)
         z = self._zbufs[layer]
         if grad:
-            if self._token is None:
-                self._token = torch.zeros(0, device=self.device, requires_grad=True)
             z = _WholeRows.apply(self._token, z, self._dzbuf(layer))
-        sc = self._scores.get(layer)
-        if sc is None:
-            return self.model.forward_projected(layer, z, adj)
-        return self.model.forward_projected(layer, z, adj, scores=sc)
+        return self.model.forward_projected(layer, z, adj, dest=dest, **extra)
 
     def _forward_merged(self, layer: int) -> None:
-        """The merged last layer's forward: every partition's logits in one
-        pass, with its graph when training, for the one loss over all rows
-        (_compute_losses) and its backward (_backward_device)."""
+        """A merged layer's forward: every partition's output in one pass,
+        with its graph when training.  The last layer's output waits for the
+        one loss over all rows (_compute_losses) and its backward
+        (_backward_device); a lower layer's goes to the next layer's resident
+        input rows (and through W into Z when that layer runs projected)."""
+        last = layer == self.model.num_layers - 1
         self._prepare_layer(layer)
+        training = self.model.training
         with torch.cuda.stream(self.streams.compute):
-            if self.model.training:
-                with torch.enable_grad():
-                    self._merged_out = self._merged_call(layer, grad=True)
-            else:
+            if last:
+                with torch.set_grad_enabled(training):
+                    self._merged_out = self._merged_call(layer, grad=training)
+                return
+            n = int(self.graph.ptr[-1])
+            x_next = self._xres_buf(layer + 1)[:n]
+            with torch.set_grad_enabled(training):
+                out = self._merged_call(layer, grad=training, dest=OutputRows(x_next))
+            if training:
+                self._graphs.setdefault(layer, {})[-1] = out
+            if (layer + 1) in self._proj:
+                self._project_rows(layer + 1, out, 0, n)
+            if out.data_ptr() != x_next.data_ptr():
                 with torch.no_grad():
-                    self._merged_out = self._merged_call(layer, grad=False)
+                    x_next.copy_(out)
+            for pid in self._my_pids:
+                self.activations[layer][pid] = None
 
     def _device_forward(self, layer: int, pid: int, keep: bool,
                         dest: Optional[Tensor] = None) -> Tensor:
@@ -702,8 +767,10 @@ class ProjectedLayers:
                 self.streams.compute.wait_event(ev)
             self._x0pending = None
 
-    def _device_grad(self, layer: int, pid: int, consumer: Optional[Tensor] = None) -> Tensor:
-        """dL/d(x_layer) of partition pid's rows when layer `layer` keeps that
+    def _device_grad(self, layer: int, pid: Optional[int],
+                     consumer: Optional[Tensor] = None) -> Tensor:
+        """dL/d(x_layer) of partition pid's rows (pid None: of all rows, for a
+        merged layer below) when layer `layer` keeps that
         gradient in HBM: dZ_layer[rows] W when it runs projected, else (a
         gathered layer) its rows of the layer's dL/dx buffer.  The halo
         contributions of every partition are already summed in either.
@@ -711,7 +778,7 @@ class ProjectedLayers:
         LayerNorm output that accepts the gradient as a product (narrow W),
         dZ and W go to its backward (LNProductSink) and the returned tensor is
         the token that tells it so."""
-        lo, hi = self.graph._range(pid)
+        lo, hi = self.graph._range(pid) if pid is not None else (0, int(self.graph.ptr[-1]))
         if layer not in self._proj:
             return self._gxbufs[layer][lo:hi]
         w = self._proj[layer]
@@ -780,12 +847,21 @@ class ProjectedLayers:
         from_device = not last and self._grad_on_device(layer + 1)
         from_host = not last and not from_device
         gbuf = self.device_gradients[layer + 1] if not last else None
-        merged = last and self._merged_out is not None
+        merged = layer in self._merged
         if merged:
-            # One loss over all rows, formed from the merged logits: its
-            # backward runs the layer's backward once, adding dL/dZ into dZ.
+            # One backward for every partition.  The last layer's is that of
+            # the one loss over all rows, formed from the merged logits; a
+            # lower layer's takes the gradient of all its output rows.  Either
+            # adds dL/dZ into dZ (a projected layer).
             with torch.cuda.stream(s.compute):
-                losses[0].backward()
+                if last:
+                    if self._merged_out is None or len(losses) != 1:
+                        raise RuntimeError("merged last layer: its forward did not run merged")
+                    losses[0].backward()
+                else:
+                    out = self._graphs.get(layer, {}).pop(-1)
+                    out.backward(self._device_grad(layer + 1, None, consumer=out))
+                    del out
             self._merged_out = None
             for pid in pids:
                 self.activations[layer][pid] = None
@@ -840,8 +916,9 @@ class ProjectedLayers:
         if layer in self._xin:
             x = self._xres[layer]
             with torch.cuda.stream(s.compute):
-                if merged:
-                    # One product over all rows, as the layer's forward.
+                if merged and last:
+                    # One product over all rows, as the layer's forward (per
+                    # partition measured faster for the wide lower layers).
                     n = int(g.ptr[-1])
                     accumulate(None, x[:n], 0, n)
                 else:
@@ -886,6 +963,9 @@ class ProjectedLayers:
         partition's output goes to the resident copy of x_{layer+1} (and to
         Z_{layer+1} when that layer runs projected), and nothing crosses to
         the host."""
+        if layer in self._merged:
+            self._forward_merged(layer)
+            return
         g, pids, pool, s = self.graph, self._my_pids, self.config.pool_size, self.streams
         projected = self._device_flow(layer)
         x_next = self._xres_buf(layer + 1)

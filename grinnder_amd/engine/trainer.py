@@ -473,7 +473,7 @@ class Trainer(ProjectedLayers):
         projected = self._device_flow(layer)
         w_next = self._proj.get(layer + 1)
         last = layer == self.model.num_layers - 1
-        if last and self._merged:
+        if last and layer in self._merged:
             self._forward_merged(layer)
             return
         if (layer + 1) in self._xin or (last and self._logits_on_device()):

@@ -73,6 +73,14 @@ class GriNNderModel(torch.nn.Module):
         when the layer has none (the default)."""
         return None
 
+    def draws_per_partition(self, layer: int) -> bool:
+        """Whether the layer's forward draws random numbers (an active
+        dropout), so that one pass over all partitions would draw other masks
+        than the partition-by-partition forwards (the reference's order) and
+        a partitioned trainer must not merge it.  The default: in training,
+        when the model has a nonzero `dropout` attribute."""
+        return self.training and float(getattr(self, "dropout", 0.0) or 0.0) > 0.0
+
     def inplace_ok(self, layer: int) -> bool:
         """Whether forward_inplace(layer, ...) exists and is the cheaper form
         of the layer when all partitions' input rows are in device memory

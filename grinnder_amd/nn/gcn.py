@@ -100,6 +100,11 @@ class GCN(GriNNderModel):
             h = F.dropout(h, p=self.dropout, training=self.training)
         return h
 
+    def draws_per_partition(self, layer: int) -> bool:
+        # Dropout acts on the outputs of the layers below the last.
+        return (self.training and self.dropout > 0.0
+                and layer < self.num_layers - 1)
+
     def forward_projected(self, layer: int, z: Tensor, adj, sink=None, dest=None) -> Tensor:
         conv = self.convs[layer]
         d = conv.out_channels

@@ -199,6 +199,18 @@ int gr_spmm_plan(const int64_t* rowptr, int64_t rows, int32_t seg_len,
                  int32_t* units, int64_t* n_units, int32_t* fixups,
                  int64_t* n_fix, int64_t* n_slots);
 
+/* gr_spmm_plan with the whole rows ordered block by block: block k is rows
+ * [block_ptr[k], block_ptr[k+1]) (block_ptr[0] = 0, block_ptr[n_blocks] =
+ * rows), and within a block by length class as gr_spmm_plan orders them; the
+ * split rows' units still come first.  No counterpart in the reference: the
+ * plan of an adjacency that stacks several partitions' rows (one pass for all
+ * of them), so that each partition's rows still run together and its gathered
+ * source rows stay in cache as in a pass of its own. */
+int gr_spmm_plan_blocked(const int64_t* rowptr, int64_t rows, int32_t seg_len,
+                         const int64_t* block_ptr, int64_t n_blocks, int32_t* units,
+                         int64_t* n_units, int32_t* fixups, int64_t* n_fix,
+                         int64_t* n_slots);
+
 /* ------------------------------------------------------------------------ */
 /* GCN aggregation (device)                                                  */
 /* ------------------------------------------------------------------------ */

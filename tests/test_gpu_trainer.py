@@ -345,16 +345,17 @@ def test_projected_layers_match_gathered(gpu, model_kind, pool_size, resident, m
 
 
 @pytest.mark.parametrize("model_kind", ["gcn", "gat", "gat2"])
-def test_merged_last_layer_matches_per_partition(gpu, model_kind):
-    """config.merge_last_layer: the projected last layer (kept graph) runs as
-    one pass over the whole graph's adjacency, with one loss and one dW
-    product, against the per-partition passes ('off') of the same flow, on a
-    20k-node graph with a hub destination and a hub source of 3000 edges
-    each (their rows and columns split into several work units): loss,
-    metrics and every gradient within 1e-5, evaluate() alike, and a second
-    merged epoch bit-identical to the first.  The forward's per-row sums run
-    over the same edges in the same order either way; the backward's
-    per-source sums and dW differ only in fp32 association."""
+def test_merged_layers_match_per_partition(gpu, model_kind):
+    """config.merge_partitions: layers run as one pass over the whole graph's
+    adjacency ('auto': every layer here, GCN's widening first layer in place;
+    'last': the last layer, with one loss and one dW product), against the
+    per-partition passes ('off') of the same flow, on a 20k-node graph with
+    a hub destination and a hub source of 3000 edges each (their rows and
+    columns split into several work units): loss, metrics and every
+    gradient within 1e-5, evaluate() alike, and repeated merged epochs and
+    runs bit-identical.  The forward's per-row sums run over the same edges
+    in the same order either way; the backward's per-source sums and the
+    last layer's dW differ only in fp32 association."""
     from grinnder_amd.data import synthetic
 
     n, classes = 20_000, 5
@@ -372,8 +373,8 @@ def test_merged_last_layer_matches_per_partition(gpu, model_kind):
                            norm=True)
     state = make().state_dict()
     runs = {}
-    for merge in ("off", "auto", "auto"):
-        config = GriNNderConfig(num_parts=6, merge_last_layer=merge)
+    for merge in ("off", "last", "auto", "auto"):
+        config = GriNNderConfig(num_parts=6, merge_partitions=merge)
         graph = build_partitioned_graph(ei, nd.x, nd.y, nd.train_mask, nd.val_mask,
                                         nd.test_mask, config)
         model = make().cuda()
@@ -381,7 +382,9 @@ def test_merged_last_layer_matches_per_partition(gpu, model_kind):
         trainer = Trainer(model, graph, config)
         opt = torch.optim.SGD(model.parameters(), lr=0.0)
         metrics = trainer.train_epoch(opt, torch.nn.CrossEntropyLoss())
-        assert trainer._merged == (merge == "auto")
+        last = model.num_layers - 1
+        expect = {"off": [], "last": [last], "auto": list(range(model.num_layers))}[merge]
+        assert trainer.merged_layers == expect
         grads = {k: p.grad.detach().clone() for k, p in model.named_parameters()
                  if p.grad is not None}
         opt.zero_grad()
@@ -392,7 +395,7 @@ def test_merged_last_layer_matches_per_partition(gpu, model_kind):
         runs.setdefault(merge, []).append((metrics, grads, again, grads2, ev))
         del trainer, model, graph
     (m0, g0, _, _, e0), = runs["off"]
-    for m1, g1, a1, g12, e1 in runs["auto"]:
+    for m1, g1, a1, g12, e1 in runs["last"] + runs["auto"]:
         assert abs(m0["loss"] - m1["loss"]) <= 1e-5 * max(1.0, abs(m0["loss"]))
         assert m0["val_acc"] == m1["val_acc"] and m0["test_acc"] == m1["test_acc"]
         assert set(g0) == set(g1)

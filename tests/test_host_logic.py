@@ -210,6 +210,36 @@ def test_spmm_plan_covers_every_edge_once():
     assert all(x[3] >= 0 for x in u.tolist()[:15]) and all(x[3] < 0 for x in u.tolist()[15:])
 
 
+def test_spmm_plan_blocked_orders_whole_rows_by_block():
+    """gr_spmm_plan_blocked: the same split units, fixups and slots as
+    gr_spmm_plan, and the same whole-row units, reordered so that each
+    block's rows come together (length classes longest first within a
+    block, row order within a class)."""
+    g = torch.Generator().manual_seed(4)
+    deg = torch.randint(0, 40, (300,), generator=g)
+    deg[[7, 150, 299]] = torch.tensor([1300, 600, 2049])
+    rowptr = torch.zeros(deg.numel() + 1, dtype=torch.int64)
+    rowptr[1:] = deg.cumsum(0)
+    blocks = torch.tensor([0, 100, 100, 220, 300])
+    a = build_plan(rowptr, deg.numel(), 512, "cpu")
+    b = build_plan(rowptr, deg.numel(), 512, "cpu", blocks)
+    assert (a.n_units, a.n_fix, a.n_slots) == (b.n_units, b.n_fix, b.n_slots)
+    assert torch.equal(a.fixups, b.fixups)
+    ua, ub = a.units.tolist(), b.units.tolist()
+    nsplit = sum(1 for x in ua if x[3] >= 0)
+    assert ua[:nsplit] == ub[:nsplit]
+    assert sorted(ua[nsplit:]) == sorted(ub[nsplit:])
+    whole = ub[nsplit:]
+
+    def key(x):
+        r, lo, hi, _ = x
+        blk = int(torch.searchsorted(blocks, torch.tensor(r), right=True)) - 1
+        return (blk, -(hi - lo).bit_length(), r)
+    assert whole == sorted(whole, key=key)
+    with pytest.raises(_lib.GrError, match="blocks"):
+        build_plan(rowptr, deg.numel(), 512, "cpu", torch.tensor([0, 100, 299]))
+
+
 def test_rmat_stream_independent_of_threads():
     a = synthetic.rmat_sample(7, 20, 1000, 200000, nthreads=1)
     b = synthetic.rmat_sample(7, 20, 1000, 200000, nthreads=8)
