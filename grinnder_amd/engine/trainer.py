@@ -293,6 +293,9 @@ class Trainer(ProjectedLayers):
         self._plan_inplace()
         self.reset_epoch()
         optimizer.zero_grad()
+        # The layers run on the compute stream; the last optimizer step (and
+        # anything else the caller queued) ran on the current one.
+        self.streams.compute.wait_stream(torch.cuda.current_stream(self.device))
         for l in range(self.model.num_layers):
             self._forward_layer(l)
         losses, metrics = self._compute_losses()
@@ -317,6 +320,7 @@ class Trainer(ProjectedLayers):
         self._proj = self._plan_projection()
         self._plan_inplace()
         self.reset_epoch()
+        self.streams.compute.wait_stream(torch.cuda.current_stream(self.device))
         for l in range(self.model.num_layers):
             self._forward_layer(l)
         _, metrics = self._compute_losses()
