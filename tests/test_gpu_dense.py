@@ -385,8 +385,11 @@ def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias, dot)
     shift = 0.3 * _randn(dim, seed=5, dev=gpu)
     rowdot = torch.full((rows,), float("nan"), device=gpu) if dot else None
     h64 = h.double()
-    mean = h64.mean(1)
-    rstd = 1.0 / torch.sqrt(h64.var(1, unbiased=False) + 1e-5)
+    if rows:
+        mean = h64.mean(1)
+        rstd = 1.0 / torch.sqrt(h64.var(1, unbiased=False) + 1e-5)
+    else:  # no rows: empty statistics (var over an empty row set only warns)
+        mean = rstd = torch.zeros(0, dtype=torch.float64, device=gpu)
     gh, dg, db_, dbias = ln_act_backward_product(dz, b, h, mean.float().contiguous(),
                                                  rstd.float().contiguous(), gamma, beta,
                                                  bias, act, shift=shift if dot else None,
