@@ -285,16 +285,17 @@ class ProjectedLayers:
                 self._keep.add(layer)
         # Room for the whole graph's adjacency, which merged layers run on
         # (_plan_merged): its device plan takes about 24 bytes an edge and 32
-        # a node beside the partitions' plans.  A merged layer's graph holds
-        # no more than the P kept graphs it replaces.
+        # a node beside the partitions' plans, and its int32 edge and row ids
+        # bound the graph to 2^31 - 1 edges.  A merged layer's graph holds no
+        # more than the P kept graphs it replaces.
         self._merge_room = False
-        if cfg.merge_partitions != "off":
+        nnz_all = sum(int(a[1].numel()) for a in g.adj_csr)
+        if cfg.merge_partitions != "off" and nnz_all < 2 ** 31 - 1:
             whole = g._whole
             if whole is not None and whole.has_device_plan(self.device):
                 self._merge_room = True
             else:
-                nnz = sum(int(a[1].numel()) for a in g.adj_csr)
-                need = 24 * nnz + 32 * n
+                need = 24 * nnz_all + 32 * n
                 if free is None:
                     free = self._free_device_memory()
                 if need + (8 << 30) <= free:
