@@ -47,7 +47,7 @@ class GriNNderConfig:
         which indexes Z's (or the input's) global rows directly: the same
         edges and per-row orders as the P per-partition passes, without their
         launches, gathers and scatters (same results up to fp32 summation
-        order in the backward's per-source sums and the last layer's dW).
+        order in the backward's per-source sums and in dW).
         'last' merges only the last layer, 'off' none.  Not a field of the
         reference's config.
     input_residency: 'stream' (the reference's data movement) uploads the

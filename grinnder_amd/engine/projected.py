@@ -917,9 +917,10 @@ class ProjectedLayers:
         if layer in self._xin:
             x = self._xres[layer]
             with torch.cuda.stream(s.compute):
-                if merged and last:
-                    # One product over all rows, as the layer's forward (per
-                    # partition measured faster for the wide lower layers).
+                if merged:
+                    # One product over all rows, as the layer's forward: as
+                    # fast as P products at C4/C5's 10M rows, 15% faster at
+                    # C3's 2.45M x 256 x 256.
                     n = int(g.ptr[-1])
                     accumulate(None, x[:n], 0, n)
                 else:
