@@ -240,6 +240,48 @@ def test_spmm_plan_blocked_orders_whole_rows_by_block():
         build_plan(rowptr, deg.numel(), 512, "cpu", torch.tensor([0, 100, 299]))
 
 
+def test_whole_adjacency_is_the_full_graph_in_partition_order():
+    """PartitionedGraph.whole_adjacency (the adjacency merged layers run on):
+    the per-partition CSRs stacked with every column mapped to its global row
+    equal, row by row and edge by edge, the full graph's CSR built directly
+    from the relabelled edge list (self-loops and GCN weights as the
+    partition pipeline adds them); its forward plan runs block by block
+    over the partitions (row_blocks = ptr)."""
+    from grinnder_amd.data.datasets import append_self_loops, compute_gcn_norm
+    from grinnder_amd.data.partition import _edge_index_to_csr
+
+    n = 3000
+    gen = torch.Generator().manual_seed(1)
+    ei = torch.randint(0, n, (2, 15000), generator=gen)  # directed: one orientation fits
+    ei = ei[:, ei[0] != ei[1]]
+    nd = synthetic.node_data(n, 8, 5)
+    g = build_partitioned_graph(ei, nd.x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
+                                GriNNderConfig(num_parts=4))
+    w = g.whole_adjacency()
+    assert w.sparse_sizes() == (n, n) and torch.equal(w.row_blocks, g.ptr.to(torch.int64))
+    inv = torch.empty_like(g.perm)
+    inv[g.perm] = torch.arange(n)
+    e = inv[ei]
+    val = compute_gcn_norm(e, n, add_self_loops=True)
+    e = append_self_loops(e, n)
+    rows = {}
+    for src, dst in ((0, 1), (1, 0)):
+        rowptr, col, perm = _edge_index_to_csr(torch.stack([e[src], e[dst]]), n)
+        rows[src] = (rowptr, col, val[perm])
+    matched = 0
+    for rowptr, col, v in rows.values():
+        if not torch.equal(rowptr, w.rowptr):
+            continue
+        for r in range(n):
+            a, b = int(rowptr[r]), int(rowptr[r + 1])
+            ka = sorted(zip(w.col[a:b].tolist(), w.value[a:b].tolist()))
+            kb = sorted(zip(col[a:b].tolist(), v[a:b].tolist()))
+            assert ka == kb, r
+        matched += 1
+    assert matched == 1
+    assert g.whole_adjacency() is w
+
+
 def test_rmat_stream_independent_of_threads():
     a = synthetic.rmat_sample(7, 20, 1000, 200000, nthreads=1)
     b = synthetic.rmat_sample(7, 20, 1000, 200000, nthreads=8)
