@@ -20,11 +20,21 @@ the edges the aggregation kernels traverse per epoch (forward and backward
 passes; a widening first layer aggregates first, so its backward traverses
 none) divided by the epoch wall time.  `model_edges_per_epoch` is the
 reference model's 2 x num_layers passes of nnz edges, given beside it.  The
-kernel-level aggregation GTEPS and HBM fraction (time inside the aggregation
-passes), the roofline of the dominant kernel (the D=256 passes, HIP events on
-their stream) and the CPU baselines (torch sparse CSR on the host's threads;
-the reference's halo gather/scatter for partitioned configs; the oracle)
-go alongside.
+kernel-level aggregation GTEPS and algorithmic rate (time inside the
+aggregation passes), the roofline of the dominant kernel (the D=256 passes,
+HIP events on their stream) and the CPU baselines (torch sparse CSR, or for
+GAT the torch index/segment ops, on the host's threads; the reference's halo
+gather/scatter for partitioned configs; the oracle) go alongside.
+
+roofline: `achieved` / `frac` are the bytes the memory fabric moved per
+launch of the dominant kernels (rocprofv3 request-size counters, committed
+in profiles/, exact on a copy of known size) over this run's HIP-event
+durations, so they cannot count a cached byte as an HBM one twice over;
+the R-MAT graph's hub rows are served from the L2 and the Infinity Cache,
+so the algorithmic bytes (every neighbour row charged in full, SURVEY's
+formula) exceed what the memory moved, and their rate is reported beside it
+as `algorithmic_GBps`.  `locality_free_control` runs the same kernels on a
+uniform random graph of the same size, where the caches cannot help.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1..c5]
        [--inputs stream|resident] [--merge auto|last|off]
@@ -45,12 +55,68 @@ HBM_PEAK_GBPS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 CALIBRATION_KIB = 1 << 20      # bytes read (and written) by one calibration launch, in KiB
 CALIBRATION_KERNEL = "bitwise_not"
-# PMC summary whose FETCH_SIZE / WRITE_SIZE rows give roofline.traffic for C2.
+# PMC summary whose BYTES lines (request-size counters) give roofline.traffic
+# for C2, and the D=256 aggregation kernels of C2 by timer region: the fused
+# forward (CSR + bias + LayerNorm + ReLU) and the CSC backward.
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "c2_gcn_aggregate_traffic.txt")
-# The D=256 aggregation kernels of C2 (fused forward, CSC backward).
-C2_DOMINANT = ("aggregate_ln_relu_units<4, 1, 8>", "aggregate_units<4, 64, 1, 8>")
+C2_DOMINANT = {"gcn_fwd": "aggregate_ln_relu_units<4, 1, 8>",
+               "gcn_bwd": "aggregate_units<4, 64, 1, 8>"}
 CONFIGS_NAMES = ("c1", "c2", "c3", "c4", "c5")
+
+
+# Kernels of known traffic for checking the memory counters (--traffic-probe):
+# name -> (rows gathered, row width in floats, rows of the source array).
+# "copy" is torch.bitwise_not over 1 GiB of int32 (reads and writes 1 GiB).
+# The gathers run gr_gather_rows over a random permutation of an array far
+# larger than the L2 and the 256 MB Infinity Cache (gather1: random 4-byte
+# elements, with repeats, of a 4 GiB array), so nearly every access goes to
+# HBM: 1 KiB rows (the D=256 aggregation's neighbour rows), 80-byte rows
+# (the 20-wide attention layer's) and single floats (the per-edge scalars).
+TRAFFIC_PROBES = {
+    "copy": None,
+    "gather256": (1 << 23, 256, 1 << 23),
+    "gather20": (1 << 26, 20, 1 << 26),
+    "gather1": (1 << 28, 1, 1 << 30),
+}
+
+
+def traffic_probe(kind: str, device: str) -> None:
+    """Launches the probe's kernel three times and prints one JSON line with
+    its algorithmic bytes read and written per launch."""
+    import torch
+
+    from grinnder_amd.aggregation import gather_rows
+
+    if kind == "copy":
+        src = torch.ones(1 << 28, dtype=torch.int32, device=device)
+        dst = torch.empty_like(src)
+        fn = lambda: torch.bitwise_not(src, out=dst)  # noqa: E731
+        read = write = 1 << 30
+        kernel = CALIBRATION_KERNEL
+    else:
+        n, dim, x_rows = TRAFFIC_PROBES[kind]
+        g = torch.Generator(device=device).manual_seed(0)
+        x = torch.empty(x_rows, dim, device=device).normal_(generator=g)
+        if n == x_rows:
+            rows = torch.randperm(x_rows, device=device, generator=g)
+        else:
+            rows = torch.randint(x_rows, (n,), device=device, generator=g)
+        fn = lambda: gather_rows(x, rows)  # noqa: E731
+        read = n * dim * 4 + n * 8
+        write = n * dim * 4
+        kernel = "gather_rows"
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms.append(a.elapsed_time(b))
+    print(json.dumps({"probe": kind, "kernel": kernel, "read_bytes": read,
+                      "write_bytes": write, "ms": [round(t, 3) for t in ms]}), flush=True)
 
 
 def log(msg: str) -> None:
@@ -81,11 +147,17 @@ def parse_args():
                          "graph where they can ('auto'), only the last layer ('last') or "
                          "partition by partition ('off'); GriNNderConfig.merge_partitions")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-control", action="store_true",
+                    help="skip the locality-free control (the D=256 passes on a uniform "
+                         "random graph of the headline's size), e.g. under a profiler")
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
                     help="print a text summary of the rocprofv3 CSV output under DIR and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the run, copy a 1 GiB device buffer 3 times (a kernel of "
                          "known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic-probe", choices=sorted(TRAFFIC_PROBES), default=None,
+                    help="run only a kernel of known memory traffic three times (for checking "
+                         "rocprof's memory counters against it) and exit")
     return ap.parse_args()
 
 
@@ -223,6 +295,123 @@ def cpu_baseline(graph, dim: int, sample_edges: int = 24_000_000) -> dict:
             "host": host_info()}
 
 
+def cpu_gat_baseline(graph, dim: int, sample_edges: int = 2_000_000) -> dict:
+    """The reference's CPU arithmetic for a one-head GAT layer (BASELINE.md
+    section 3; PyG GATConv's message passing under grinnder/nn/gat.py:69-78)
+    on every host thread: logits s_j + d_i through index_select, LeakyReLU
+    0.2, the segment softmax (scatter_reduce amax, exp, index_add_ of the
+    sums, + 1e-16), messages alpha * Hs[col] through index_select and their
+    segment sum by index_add_; the backward is torch's autograd of the same
+    ops.  Bounded sample: the first rows of partition 0 up to `sample_edges`
+    edges, sources relabelled to the distinct ones (a partition-shaped
+    [B, E] block), width `dim`.  One warm-up, then the median of 5 runs of
+    forward and of forward + backward.  GTEPS = 2 * edges / (fwd + bwd)."""
+    import torch
+    import torch.nn.functional as F
+
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    rowptr, col, _ = graph.adj_csr[0]
+    r1 = int(torch.searchsorted(rowptr, torch.tensor(sample_edges)).clamp(max=rowptr.numel() - 1))
+    e1 = int(rowptr[r1])
+    src, local = torch.unique(col[:e1], return_inverse=True)
+    dst = torch.repeat_interleave(torch.arange(r1), rowptr[1:r1 + 1] - rowptr[:r1])
+    g = torch.Generator().manual_seed(0)
+    hs = torch.randn(src.numel(), dim, generator=g)
+    a_s = torch.randn(dim, generator=g) / dim ** 0.5
+    a_d = torch.randn(dim, generator=g) / dim ** 0.5
+    hd = torch.randn(r1, dim, generator=g)  # the destination rows X[:B] W^T
+    gy = torch.randn(r1, dim, generator=g)
+
+    def forward(h, h_dst):
+        s = h @ a_s
+        d = h_dst @ a_d
+        t = F.leaky_relu(s.index_select(0, local) + d.index_select(0, dst), 0.2)
+        m = torch.full((r1,), float("-inf")).scatter_reduce(0, dst, t, "amax")
+        ex = torch.exp(t - m.index_select(0, dst).detach())
+        den = torch.zeros(r1).index_add_(0, dst, ex)
+        alpha = ex / (den.index_select(0, dst) + 1e-16)
+        msg = h.index_select(0, local) * alpha.unsqueeze(1)
+        return torch.zeros(r1, dim).index_add_(0, dst, msg)
+
+    def fwd():
+        with torch.no_grad():
+            forward(hs, hd)
+
+    def fwd_bwd():
+        h = hs.detach().requires_grad_(True)
+        h_dst = hd.detach().requires_grad_(True)
+        forward(h, h_dst).backward(gy)
+
+    t_f = _median_time(fwd)
+    t_fb = _median_time(fwd_bwd)
+    t_b = max(t_fb - t_f, 1e-9)
+    return {"value": round(2 * e1 / (t_f + t_b) / 1e9, 6), "unit": "GTEPS", "cores": threads,
+            "kind": "port",
+            "sample": (f"one-head GAT attention at C={dim} with torch CPU ops ({threads} "
+                       f"threads): index_select logits, LeakyReLU 0.2, scatter_reduce amax / exp "
+                       f"/ index_add_ softmax, index_select messages and index_add_ aggregation, "
+                       f"backward by autograd, on rows [0, {r1}) of partition 0 with their "
+                       f"{src.numel()} distinct sources ({e1} edges); median of 5 after a "
+                       f"warm-up: fwd {t_f:.4f} s, fwd+bwd {t_fb:.4f} s"),
+            "host": host_info()}
+
+
+def locality_free_control(num_nodes: int, nnz: int, dim: int, device: str,
+                          runs: int = 5) -> dict:
+    """The D=`dim` GCN aggregation kernels on a graph with no locality: the
+    headline graph's node and edge counts, every row's neighbours drawn
+    uniformly at random (rows of nnz // N or nnz // N + 1 edges).  R-MAT's
+    hub rows are served by the L2 and the Infinity Cache, so there the
+    algorithmic bytes (every neighbour row charged in full) exceed what the
+    memory moved; here almost every neighbour row comes from HBM, so the
+    algorithmic rate is the HBM-bound kernel's own.  The forward runs over
+    the CSR plan, the backward over the CSC plan, `runs` times each, timed
+    with HIP events on the launch stream."""
+    import torch
+
+    from grinnder_amd.aggregation import KernelTimer, spmm
+    from grinnder_amd.data.adjacency import Adjacency
+
+    t0 = time.perf_counter()
+    g = torch.Generator().manual_seed(7)
+    deg = torch.full((num_nodes,), nnz // num_nodes, dtype=torch.int64)
+    deg[:nnz - int(deg.sum())] += 1
+    rowptr = torch.zeros(num_nodes + 1, dtype=torch.int64)
+    rowptr[1:] = deg.cumsum(0)
+    col = torch.randint(0, num_nodes, (nnz,), generator=g)
+    val = torch.rand(nnz, generator=g)
+    adj = Adjacency(rowptr, col, val, (num_nodes, num_nodes))
+    plan = adj.device_plan(device)
+    del col, val
+    z = torch.randn(num_nodes, dim, device=device)
+    gy = torch.randn(num_nodes, dim, device=device)
+    spmm(plan.fwd, plan.idx, plan.val, z, num_nodes)
+    spmm(plan.bwd, plan.row_idx, plan.val_t, gy, num_nodes)
+    torch.cuda.synchronize()
+    setup = time.perf_counter() - t0
+    timer = KernelTimer(capacity=4 * runs)
+    with timer:
+        for _ in range(runs):
+            spmm(plan.fwd, plan.idx, plan.val, z, num_nodes, name="ctl_fwd")
+            spmm(plan.bwd, plan.row_idx, plan.val_t, gy, num_nodes, name="ctl_bwd")
+    torch.cuda.synchronize()
+    out = {"graph": (f"uniform random, {num_nodes} nodes, {nnz} edges (the headline graph's "
+                     f"counts), D={dim}"), "setup_s": round(setup, 1)}
+    tot_b = tot_ms = 0.0
+    for name in ("ctl_fwd", "ctl_bwd"):
+        recs = [r for r in timer.records if r.name == name]
+        ms = sum(r.ms() for r in recs) / len(recs)
+        b = recs[0].nbytes
+        tot_b += b
+        tot_ms += ms
+        out[name[4:]] = {"avg_ms": round(ms, 3), "algorithmic_GBps": round(b / ms / 1e6, 1)}
+    out["algorithmic_GBps"] = round(tot_b / tot_ms / 1e6, 1)
+    out["frac"] = round(tot_b / tot_ms / 1e6 / HBM_PEAK_GBPS, 4)
+    adj.release_device()
+    return out
+
+
 def cpu_halo_baseline(graph, dim: int, max_parts: int = 4) -> Optional[dict]:
     """The reference's CPU halo movement (csrc/cuda/async_transfer.cu:60-186):
     per partition, index_select of the boundary rows of every other
@@ -297,8 +486,30 @@ def oracle_baseline(graph, dim: int, seconds: float):
                        f"{elapsed:.1f}s")}
 
 
+# Bytes per dispatch from the L2's requests to the memory fabric, by request
+# size (rocprofv3 counters, one pass each set): reads of 32, 64 and 128
+# bytes, writes of 32 and 64 bytes.  The fabric serves them from HBM or from
+# the Infinity Cache in front of it; no counter separates the two, so these
+# bytes bound HBM traffic from above.
+READ_COUNTERS = {"TCC_EA0_RDREQ_32B_sum": 32, "TCC_EA0_RDREQ_64B_sum": 64,
+                 "TCC_EA0_RDREQ_128B_sum": 128}
+WRITE_COUNTERS = ("TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum")
+
+
+def request_bytes(means: dict) -> Optional[tuple]:
+    """(read, write) bytes per dispatch from the request-size counters'
+    per-dispatch means, or None when a counter is missing."""
+    if not all(c in means for c in READ_COUNTERS) or not all(c in means for c in WRITE_COUNTERS):
+        return None
+    read = sum(means[c] * size for c, size in READ_COUNTERS.items())
+    wr, wr64 = means["TCC_EA0_WRREQ_sum"], means["TCC_EA0_WRREQ_64B_sum"]
+    return read, 32.0 * (wr - wr64) + 64.0 * wr64
+
+
 def summarize_profile(root: str) -> None:
-    """Text summary of rocprofv3 CSV output (kernel stats and/or PMC counters)."""
+    """Text summary of rocprofv3 CSV output under `root` (kernel stats and/or
+    PMC counters; the counter files of several passes are merged), with
+    each kernel's fabric bytes per dispatch from the request-size counters."""
     import csv
     import glob
     from collections import defaultdict
@@ -314,9 +525,11 @@ def summarize_profile(root: str) -> None:
             tot = float(r["TotalDurationNs"])
             print(f"{int(r['Calls']):>6} {float(r['AverageNs']) / 1e3:>10.1f} "
                   f"{tot / 1e6:>10.3f} {100 * tot / total:>6.2f}  {r['Name'][:150]}")
-    for path in sorted(glob.glob(os.path.join(root, "**", "*counter_collection.csv"),
-                                 recursive=True)):
-        acc = defaultdict(lambda: [0, 0.0, 0.0, float("inf"), 0.0])
+    paths = sorted(glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True))
+    if not paths:
+        return
+    acc = defaultdict(lambda: [0, 0.0, 0.0, float("inf"), 0.0])
+    for path in paths:
         with open(path) as f:
             for r in csv.DictReader(f):
                 key = (r["Kernel_Name"], r["Counter_Name"])
@@ -327,63 +540,55 @@ def summarize_profile(root: str) -> None:
                 e[2] += float(r.get("End_Timestamp", 0)) - float(r.get("Start_Timestamp", 0))
                 e[3] = min(e[3], v)
                 e[4] = max(e[4], v)
-        print(f"# counters ({os.path.basename(path)}): per-dispatch mean / min / max")
-        print(f"{'dispatches':>10} {'mean_value':>16} {'min':>14} {'max':>14} {'avg_us':>10}"
-              f"  counter  kernel")
-        for (k, c), (n, v, t, lo, hi) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
-            if n == 0:
-                continue
-            if not any(s in k for s in ("aggregate", "gat_", "copy", "gemm", "Cijk", "gather",
-                                        "scatter", CALIBRATION_KERNEL, "ln_relu", "xent")):
-                continue
-            print(f"{n:>10} {v / n:>16.1f} {lo:>14.1f} {hi:>14.1f} {t / n / 1e3:>10.1f}  {c}"
-                  f"  {k[:140]}")
-        for (k, c), (n, v, t, lo, hi) in acc.items():
-            if CALIBRATION_KERNEL in k and n:
-                print(f"# calibration {c}: {CALIBRATION_KERNEL} moves {CALIBRATION_KIB} KiB, "
-                      f"counter mean {v / n:.1f} KiB -> scale x{CALIBRATION_KIB / (v / n):.4f}")
+    keep = ("aggregate", "gat_", "copy", "gemm", "Cijk", "gather", "scatter", CALIBRATION_KERNEL,
+            "ln_relu", "ln_act", "xent")
+    print(f"# counters ({len(paths)} file(s)): per-dispatch mean / min / max")
+    print(f"{'dispatches':>10} {'mean_value':>16} {'min':>14} {'max':>14} {'avg_us':>10}"
+          f"  counter  kernel")
+    per_kernel = defaultdict(dict)
+    for (k, c), (n, v, t, lo, hi) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
+        if n == 0 or not any(s in k for s in keep):
+            continue
+        per_kernel[k][c] = v / n
+        print(f"{n:>10} {v / n:>16.1f} {lo:>14.1f} {hi:>14.1f} {t / n / 1e3:>10.1f}  {c}"
+              f"  {k[:140]}")
+    for (k, c), (n, v, t, lo, hi) in acc.items():
+        if CALIBRATION_KERNEL in k and n and c in ("FETCH_SIZE", "WRITE_SIZE"):
+            print(f"# calibration {c}: {CALIBRATION_KERNEL} moves {CALIBRATION_KIB} KiB, "
+                  f"counter mean {v / n:.1f} KiB -> scale x{CALIBRATION_KIB / (v / n):.4f}")
+    print("# fabric bytes per dispatch from request sizes: read = 32*RDREQ_32B + "
+          "64*RDREQ_64B + 128*RDREQ_128B, write = 32*(WRREQ - WRREQ_64B) + 64*WRREQ_64B")
+    for k, means in sorted(per_kernel.items()):
+        rw = request_bytes(means)
+        if rw is not None:
+            print(f"BYTES read={rw[0]:.0f} write={rw[1]:.0f} kernel={k[:200]}")
 
 
-def traffic_from_profile(path: str, kernels) -> Optional[float]:
-    """HBM bytes per launch of `kernels` (averaged) from a committed PMC summary.
-
-    Each counter (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) is scaled by what
-    the same counter read for the calibration kernel, which moves a known
-    CALIBRATION_KIB.  None when the summary or a row is missing."""
+def traffic_from_profile(path: str, kernels) -> Optional[dict]:
+    """Fabric bytes per dispatch (read + write) of each kernel in `kernels`
+    from the BYTES lines of a committed PMC summary (summarize_profile: the
+    request-size counters), or None when the file or a kernel is missing."""
     if not os.path.exists(path):
         return None
-    means = {}
+    found = {}
     with open(path) as f:
         for line in f:
-            parts = line.split(None, 6)
-            if len(parts) < 7 or line.startswith("#"):
+            if not line.startswith("BYTES "):
                 continue
-            try:
-                mean = float(parts[1])
-            except ValueError:
-                continue
-            counter, name = parts[5], parts[6]
-            if CALIBRATION_KERNEL in name:
-                means[("cal", counter)] = mean
+            fields = dict(kv.split("=", 1) for kv in line[6:].split(" ", 2))
             for k in kernels:
-                if k in name:
-                    means[(k, counter)] = mean
-    total = 0.0
-    for k in kernels:
-        b = 0.0
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            cal, val = means.get(("cal", counter)), means.get((k, counter))
-            if not cal or val is None:
-                return None
-            b += val * (CALIBRATION_KIB / cal) * 1024.0
-        total += b
-    return total / len(kernels)
+                if k in fields["kernel"]:
+                    found[k] = float(fields["read"]) + float(fields["write"])
+    return found if all(k in found for k in kernels) else None
 
 
 def main():
     args = parse_args()
     if args.summarize_profile:
         summarize_profile(args.summarize_profile)
+        return
+    if args.traffic_probe:
+        traffic_probe(args.traffic_probe, "cuda:0")
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the "
@@ -506,19 +711,52 @@ def main():
                        "tflop_per_epoch": round(dense_flops / args.steps / 1e12, 4)}
         log(f"dense transform: {dense_stats}")
 
-    traffic = None
-    if args.config == "c2":
-        t = traffic_from_profile(TRAFFIC_PROFILE, C2_DOMINANT)
-        traffic = None if t is None else round(t)
-        if traffic is not None:
-            log(f"roofline.traffic {traffic / 1e9:.1f} GB per D={cfg['hidden']} launch (PMC, "
-                f"calibrated) vs {dom_bytes / len(dom) / 1e9:.1f} GB algorithmic")
+    roofline = {"bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "kernel": (f"aggregate_units (GCN SpMM, D={cfg['hidden']}, fwd CSR + bwd CSC)"
+                           if cfg["model"] == "gcn" else
+                           f"GAT attention fwd+bwd kernels, H*C={cfg['hidden']}"),
+                "algorithmic_bytes": round(dom_bytes / len(dom)),
+                "algorithmic_GBps": round(achieved, 1),
+                "algorithmic_frac": round(achieved / HBM_PEAK_GBPS, 4)}
+    per_kernel = traffic_from_profile(TRAFFIC_PROFILE, C2_DOMINANT.values()) \
+        if args.config == "c2" else None
+    if per_kernel is not None and all(r.name in C2_DOMINANT for r in dom):
+        # Bytes the memory fabric moved per launch (PMC request-size counters,
+        # committed profile) over each launch's HIP-event duration.
+        fabric = sum(per_kernel[C2_DOMINANT[r.name]] for r in dom)
+        rate = fabric / (dom_ms / 1e3) / 1e9
+        roofline.update({
+            "achieved": round(rate, 1), "frac": round(rate / HBM_PEAK_GBPS, 4),
+            "traffic": round(fabric / len(dom)),
+            "bytes_counted": ("fabric: bytes the L2 fetched from and wrote to the memory "
+                              "fabric per launch, from rocprofv3's request-size counters "
+                              "(TCC_EA0_RDREQ_32B/64B/128B, TCC_EA0_WRREQ/WRREQ_64B; exact on a "
+                              "1 GiB copy) in profiles/c2_gcn_aggregate_traffic.txt; they "
+                              "include the Infinity Cache's hits, so they bound HBM bytes "
+                              "from above; durations are this run's HIP events")})
+        log(f"roofline: {fabric / len(dom) / 1e9:.1f} GB fabric traffic per D={cfg['hidden']} "
+            f"launch (PMC) vs {dom_bytes / len(dom) / 1e9:.1f} GB algorithmic")
+    else:
+        roofline.update({"achieved": round(achieved, 1),
+                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "bytes_counted": "algorithmic (no committed traffic profile for this "
+                                          "configuration)"})
+    if args.config == "c2" and not args.no_control:
+        try:
+            roofline["locality_free_control"] = locality_free_control(
+                cfg["num_nodes"], nnz, cfg["hidden"], device)
+            log(f"locality-free control: {roofline['locality_free_control']}")
+        except Exception as exc:
+            log(f"locality-free control failed: {exc!r}")
 
     cpu = None
     if not args.no_cpu_baseline:
         # Reported baselines, never fatal for the GPU number.
         try:
-            cpu = cpu_baseline(graph, cfg["hidden"])
+            if cfg["model"] == "gat":
+                cpu = cpu_gat_baseline(graph, cfg["hidden"])
+            else:
+                cpu = cpu_baseline(graph, cfg["hidden"])
             log(f"cpu baseline: {cpu}")
         except Exception as exc:
             log(f"cpu baseline failed: {exc!r}")
@@ -565,14 +803,9 @@ def main():
         "model_edges_per_epoch": model_edges,
         "model_edge_gteps": round(model_edges * args.steps / wall / 1e9, 4),
         "agg_kernel_gteps": round(sum(r.edges for r in recs_agg) / (agg_ms / 1e3) / 1e9, 4),
-        "agg_hbm_frac": round(agg_bytes / (agg_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "agg_algorithmic_frac": round(agg_bytes / (agg_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "agg_ms_per_epoch": round(agg_ms / args.steps, 3),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic,
-                     "kernel": (f"aggregate_units (GCN SpMM, D={cfg['hidden']}, fwd CSR + bwd CSC)"
-                                if cfg["model"] == "gcn" else
-                                f"GAT attention fwd+bwd kernels, H*C={cfg['hidden']}")},
+        "roofline": roofline,
         "dense_mfma": dense_stats,
         "cpu_baseline": cpu,
         "passes": passes,

@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void aggregate_units(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
     const float* __restrict__ val, const float* __restrict__ x, int64_t ldx,
     float* __restrict__ y, int64_t ldy, const float* __restrict__ bias, int dim,
-    float* __restrict__ ws, const int32_t* __restrict__ orow) {
+    float* __restrict__ ws, int64_t n_slots, const int32_t* __restrict__ orow) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int64_t wid =
@@ -162,7 +162,8 @@ __global__ __launch_bounds__(256) void aggregate_units(
       }
       store_vec<VEC>(out + foff[ch], acc[ch]);
     }
-  } else {
+  } else if (w.w < n_slots) {
+    // A slot outside the caller's n_slots * dim workspace is never written.
     float* out = ws + (int64_t)w.w * dim;
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
@@ -173,10 +174,12 @@ __global__ __launch_bounds__(256) void aggregate_units(
 
 // Ordered reduction of the partial sums of split rows: one workgroup per
 // (split row, 256-feature chunk), one thread per feature; the slot loop is
-// unrolled so its loads are independent.
+// unrolled so its loads are independent.  Slots at or past n_slots (outside
+// the workspace) are never read.
 __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict__ fix,
                                                        const float* __restrict__ ws, int dim,
-                                                       float* __restrict__ y, int64_t ldy,
+                                                       int64_t n_slots, float* __restrict__ y,
+                                                       int64_t ldy,
                                                        const float* __restrict__ bias,
                                                        const int32_t* __restrict__ orow) {
   const int64_t r = blockIdx.x;
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(256) void aggregate_fixup(const int32_t* __restrict
   if (f >= dim) return;
   const int row = fix[3 * r + 0];
   const int first = fix[3 * r + 1];
-  const int n = fix[3 * r + 2];
+  const int n = (int)max((int64_t)0, min((int64_t)fix[3 * r + 2], n_slots - first));
   const float* p = ws + (int64_t)first * dim + f;
   float s = 0.f;
   int k = 0;
@@ -1120,34 +1123,40 @@ hipError_t dispatch_rows(int chunks, const int4* units, int64_t n_units, const i
 template <int VEC, int G, int NCH>
 hipError_t launch_units(const int4* units, int64_t n_units, const int32_t* idx,
                         const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
-                        const float* bias, int dim, float* ws, const int32_t* orow,
-                        hipStream_t s) {
+                        const float* bias, int dim, float* ws, int64_t n_slots,
+                        const int32_t* orow, hipStream_t s) {
   constexpr int EPI = 64 / G;
   // Narrow rows (4 or more edge slots of at most 16 lanes) keep 8 edges a
   // slot in flight: a 512-edge split unit then takes 8 rounds of loads, not 32.
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : (EPI == 2 ? 4 : 8);
   const int64_t blocks = (n_units + 3) / 4;
   hipLaunchKernelGGL((aggregate_units<VEC, G, NCH, U>), dim3((unsigned)blocks), dim3(256), 0, s,
-                     units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow);
+                     units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots, orow);
   return hipGetLastError();
 }
 
 template <int VEC>
 hipError_t dispatch_g(int chunks, const int4* units, int64_t n_units, const int32_t* idx,
                       const float* val, const float* x, int64_t ldx, float* y, int64_t ldy,
-                      const float* bias, int dim, float* ws, const int32_t* orow,
-                      hipStream_t s) {
+                      const float* bias, int dim, float* ws, int64_t n_slots,
+                      const int32_t* orow, hipStream_t s) {
   if (chunks <= 8)
-    return launch_units<VEC, 8, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
+    return launch_units<VEC, 8, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots,
+                                       orow, s);
   if (chunks <= 16)
-    return launch_units<VEC, 16, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
+    return launch_units<VEC, 16, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots,
+                                       orow, s);
   if (chunks <= 32)
-    return launch_units<VEC, 32, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
+    return launch_units<VEC, 32, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots,
+                                       orow, s);
   if (chunks <= 64)
-    return launch_units<VEC, 64, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
+    return launch_units<VEC, 64, 1>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots,
+                                       orow, s);
   if (chunks <= 128)
-    return launch_units<VEC, 64, 2>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
-  return launch_units<VEC, 64, 4>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, orow, s);
+    return launch_units<VEC, 64, 2>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots,
+                                       orow, s);
+  return launch_units<VEC, 64, 4>(units, n_units, idx, val, x, ldx, y, ldy, bias, dim, ws, n_slots,
+                                       orow, s);
 }
 
 inline bool aligned(const void* p, int bytes) {
@@ -1317,6 +1326,10 @@ extern "C" int gr_gcn_aggregate_noalloc(const int32_t* units, int64_t n_units,
              "gcn_aggregate_noalloc: %lld split slots of %lld floats exceed the scratch of "
              "%lld floats; use gr_gcn_aggregate with a workspace",
              (long long)n_slots, (long long)dim, (long long)GR_NOALLOC_SCRATCH_FLOATS);
+  GR_REQUIRE(n_fix >= 0 && n_slots >= 2 * n_fix,
+             "gcn_aggregate_noalloc: n_slots %lld is below the 2 * n_fix = %lld slots of the "
+             "plan's split rows; pass the n_slots gr_spmm_plan returned",
+             (long long)n_slots, (long long)(2 * n_fix));
   float* ws = nullptr;
   if (n_fix > 0 && n_units > 0) {
     const int rc = gr_agg::scratch_address(&ws);
@@ -1355,6 +1368,13 @@ int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t
              "gcn_aggregate: NULL units/x/y");
   GR_REQUIRE(n_fix == 0 || (fixups != nullptr && workspace != nullptr),
              "gcn_aggregate: NULL fixups/workspace with n_fix > 0");
+  // Every split row of a plan has at least two units, each with a slot of its
+  // own, so a plan with n_fix split rows needs n_slots >= 2 * n_fix.  (The
+  // kernels also never touch a slot at or past n_slots.)
+  GR_REQUIRE(n_slots >= 2 * n_fix,
+             "gcn_aggregate: n_slots %lld is below the 2 * n_fix = %lld slots of the plan's "
+             "split rows; pass the n_slots gr_spmm_plan returned",
+             (long long)n_slots, (long long)(2 * n_fix));
   GR_REQUIRE(aligned(units, 16), "gcn_aggregate: units must be 16-byte aligned");
   if (n_units == 0) return GR_OK;
   hipStream_t s = gr::as_stream(stream);
@@ -1383,13 +1403,13 @@ int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t
   if (n_wide > 0) {
     if (vec == 4)
       err = dispatch_g<4>(chunks, u4, n_wide, idx, val, x, ldx, y, ldy, bias, d, workspace,
-                          orow, s);
+                          n_slots, orow, s);
     else if (vec == 2)
       err = dispatch_g<2>(chunks, u4, n_wide, idx, val, x, ldx, y, ldy, bias, d, workspace,
-                          orow, s);
+                          n_slots, orow, s);
     else
       err = dispatch_g<1>(chunks, u4, n_wide, idx, val, x, ldx, y, ldy, bias, d, workspace,
-                          orow, s);
+                          n_slots, orow, s);
     GR_HIP_CHECK(err);
   }
   if (narrow && n_units > n_wide) {
@@ -1407,7 +1427,7 @@ int gr_agg::aggregate_entry(const int32_t* units, int64_t n_units, const int32_t
     GR_REQUIRE(n_fix <= INT32_MAX, "gcn_aggregate: too many split rows");
     const int threads = d >= 256 ? 256 : ((d + 63) / 64) * 64;
     hipLaunchKernelGGL(aggregate_fixup, dim3((unsigned)n_fix, (unsigned)((d + 255) / 256)),
-                       dim3(threads), 0, s, fixups, workspace, d, y, ldy, bias, orow);
+                       dim3(threads), 0, s, fixups, workspace, d, n_slots, y, ldy, bias, orow);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;

@@ -17,7 +17,6 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
-#include <atomic>
 #include <cerrno>
 #include <condition_variable>
 #include <cstring>
@@ -42,7 +41,7 @@ struct Request {
   int64_t offset = 0;
   int64_t nbytes = 0;
   std::string path;
-  std::atomic<int64_t> chunks_left{0};
+  int64_t chunks_left = 0;  // guarded by Engine::mu
   bool done = false;        // guarded by Engine::mu
   std::string error;        // guarded by Engine::mu (first failure)
 };
@@ -87,8 +86,8 @@ class Engine {
       return gr::fail(GR_EINVAL, "io engine: cannot size %s: %s", path, std::strerror(e));
     }
     const int64_t n_chunks = nbytes == 0 ? 0 : (nbytes + kChunkBytes - 1) / kChunkBytes;
-    req->chunks_left.store(n_chunks);
     std::lock_guard<std::mutex> lock(mu);
+    req->chunks_left = n_chunks;
     const int64_t h = next_handle_++;
     requests_[h] = req;
     if (n_chunks == 0) {
@@ -173,14 +172,15 @@ class Engine {
         queue_.pop_front();
       }
       std::string err = transfer(c);
-      if (c.req->chunks_left.fetch_sub(1) == 1 || !err.empty()) {
-        std::lock_guard<std::mutex> lock(mu);
-        if (!err.empty() && c.req->error.empty()) c.req->error = err;
-        if (c.req->chunks_left.load() == 0) {
-          c.req->done = true;
-          close_fd(*c.req);
-          done_cv_.notify_all();
-        }
+      // A chunk publishes its result and its completion under one lock, so
+      // the request is marked done only after every chunk's error (if any)
+      // is recorded, and wait() sees the first failure.
+      std::lock_guard<std::mutex> lock(mu);
+      if (!err.empty() && c.req->error.empty()) c.req->error = std::move(err);
+      if (--c.req->chunks_left == 0) {
+        c.req->done = true;
+        close_fd(*c.req);
+        done_cv_.notify_all();
       }
     }
   }

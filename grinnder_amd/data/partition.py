@@ -147,6 +147,33 @@ def partition_nodes(edge_index: Tensor, num_nodes: int, num_parts: int,
     return perm, ptr
 
 
+def partition_adjacency(edge_index: Tensor, num_nodes: int, perm: Tensor, ptr: Tensor,
+                        workers: int = 1):
+    """Steps 2-6 of build_partitioned_graph (grinnder/data/partition.py:302-363)
+    for a given partition (perm, ptr): relabel the edges by inv_perm, weight
+    them on the full graph (degree counted on edge_index[1] after the
+    self-loops), append the self-loops, build the CSR with edge_index[0] as
+    the row, then every partition's adjacency and boundaries.  Returns
+    [(pid, (rowptr, col, value), boundaries, expanded_size, batch_size)] in
+    partition order."""
+    inv_perm = torch.empty_like(perm)
+    inv_perm[perm] = torch.arange(num_nodes, dtype=torch.long)
+    if not torch.equal(perm, torch.arange(num_nodes)):
+        edge_index = inv_perm[edge_index]
+    edge_weight = compute_gcn_norm(edge_index, num_nodes, add_self_loops=True)
+    edge_index = append_self_loops(edge_index, num_nodes)
+    rowptr, col, sort_perm = _edge_index_to_csr(edge_index, num_nodes)
+    edge_weight = edge_weight[sort_perm]
+    del sort_perm, edge_index
+    P = int(ptr.numel()) - 1
+    args = (ptr, rowptr, col, edge_weight, P)
+    workers = max(1, min(int(workers), P))
+    if workers == 1:
+        return [_build_partition_subgraph(pid, *args) for pid in range(P)]
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        return list(ex.map(lambda pid: _build_partition_subgraph(pid, *args), range(P)))
+
+
 def _reorder_graph_payload(x: Any, y: Tensor, train_mask: Tensor, val_mask: Tensor,
                            test_mask: Tensor, perm: Tensor):
     if hasattr(x, "with_permutation"):
@@ -204,27 +231,12 @@ def build_partitioned_graph(edge_index: Tensor, x: Any, y: Tensor, train_mask: T
 
     perm, ptr = partition_nodes(edge_index, num_nodes, config.num_parts, config.partitioner,
                                 **config.partitioner_kwargs)
-    inv_perm = torch.empty_like(perm)
-    inv_perm[perm] = torch.arange(num_nodes, dtype=torch.long)
     x, y, train_mask, val_mask, test_mask = _reorder_graph_payload(
         x, y, train_mask, val_mask, test_mask, perm)
-    if not torch.equal(perm, torch.arange(num_nodes)):
-        edge_index = inv_perm[edge_index]
-
-    edge_weight = compute_gcn_norm(edge_index, num_nodes, add_self_loops=True)
-    edge_index = append_self_loops(edge_index, num_nodes)
-    rowptr, col, sort_perm = _edge_index_to_csr(edge_index, num_nodes)
-    edge_weight = edge_weight[sort_perm]
-    del sort_perm
-
     P = config.num_parts
-    args = (ptr, rowptr, col, edge_weight, P)
-    workers = max(1, min(int(config.preprocess_workers), P))
-    if workers == 1 or P == 1:
-        results = [_build_partition_subgraph(pid, *args) for pid in range(P)]
-    else:
-        with ThreadPoolExecutor(max_workers=workers) as ex:
-            results = list(ex.map(lambda pid: _build_partition_subgraph(pid, *args), range(P)))
+    results = partition_adjacency(edge_index, num_nodes, perm, ptr,
+                                  workers=int(config.preprocess_workers))
+    graph_num_edges = int(edge_index.size(1)) + num_nodes  # with the appended self-loops
 
     adj_csr: List[Tuple[Tensor, Tensor, Optional[Tensor]]] = []
     boundaries: List[List[Optional[Tensor]]] = []
@@ -237,7 +249,6 @@ def build_partitioned_graph(edge_index: Tensor, x: Any, y: Tensor, train_mask: T
         partition_sizes.append(batch)
 
     _store_adjacency(backend, adj_csr)
-    graph_num_edges = int(edge_index.size(1))
     if cache_path is not None and save_cache:
         path = Path(cache_path)
         path.parent.mkdir(parents=True, exist_ok=True)

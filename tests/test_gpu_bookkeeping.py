@@ -27,6 +27,12 @@ test_box_csr_transpose_is_stable_and_complete = host.test_csr_transpose_is_stabl
 test_box_spmm_plan_covers_every_edge_once = host.test_spmm_plan_covers_every_edge_once
 test_box_rmat_stream_independent_of_threads = host.test_rmat_stream_independent_of_threads
 test_box_partitioner_is_a_balanced_permutation = host.test_partitioner_is_a_balanced_permutation
+test_box_directed_rmat_pipeline_bit_exact = host.test_directed_rmat_pipeline_bit_exact
+test_box_native_directed_pipeline_known_answer_and_brute_force = \
+    host.test_native_directed_pipeline_known_answer_and_brute_force
+test_box_whole_adjacency_orientation = \
+    host.test_whole_adjacency_is_the_full_graph_in_partition_order
+test_box_directed_pipeline_known_answer = orc.test_directed_pipeline_known_answer
 test_box_gcn_norm_triangle_known_answer = orc.test_gcn_norm_triangle_known_answer
 test_box_gcn_norm_matches_brute_force_degrees = orc.test_gcn_norm_matches_brute_force_degrees
 test_box_csr_rows_and_permutation = orc.test_csr_rows_and_permutation

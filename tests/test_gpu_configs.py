@@ -156,7 +156,8 @@ def trainer_epoch(graph, config, state, make):
     metrics = trainer.train_epoch(torch.optim.SGD(model.parameters(), lr=0.0),
                                   torch.nn.CrossEntropyLoss())
     grads = {k: p.grad.detach().cpu().clone() for k, p in model.named_parameters()}
-    flows = (trainer.projected_layers, trainer.inplace_layers, trainer.gathered_layers)
+    flows = (trainer.projected_layers, trainer.inplace_layers, trainer.gathered_layers,
+             trainer.merged_layers)
     del trainer, model
     torch.cuda.empty_cache()
     return metrics["loss"], grads, flows
@@ -337,9 +338,13 @@ def test_c3_epoch_matches_float64(gpu, c2_data, labels):
                                         config)
         loss, grads, flows = trainer_epoch(graph, config, state, _c2_make)
         del graph
+        if parts > 1:
+            # The default flow runs every layer as one pass over the whole
+            # graph; the reference flow runs them partition by partition.
+            assert flows[3] == ([0, 1, 2] if flow == "auto" else []), flows
         err = {k: max_abs_norm_err(grads[k], ref_grads[k]) for k in ref_grads}
         runs[(parts, flow)] = grads
-        log(f"C3 {labels} P={parts} {flow} (projected, in place, gathered) {flows}: loss "
+        log(f"C3 {labels} P={parts} {flow} (projected, in place, gathered, merged) {flows}: loss "
             f"{loss:.8f} (rel err {abs(loss - ref_loss) / abs(ref_loss):.1e}); grads vs "
             f"float64 {({k: f'{v:.1e}' for k, v in err.items()})}")
         assert abs(loss - ref_loss) / abs(ref_loss) <= TOL
@@ -521,3 +526,106 @@ def test_c5_partition_gat_in_place_matches_gathered(gpu, c5_partition):
     for t0, t1 in ((o0, o1), (dz0, dz1), (ad0, ad1), (b0, b1)):
         assert torch.equal(t0, t1)
     assert err <= TOL
+
+
+# ------------------------------------------------ C4 / C5 training epochs --
+
+def _c4_make():
+    return GCN(C4["feat"], 256, C4["classes"], num_layers=3, dropout=0.0, norm=True)
+
+
+def _c5_make():
+    from grinnder_amd.nn import GAT
+
+    return GAT(C4["feat"], 256, C4["classes"], num_layers=2, heads=1, dropout=0.0, norm=True)
+
+
+def _default_vs_reference_flow(graph, make, label):
+    """One epoch of the default flow ('auto': projected layers, Z read in
+    place, every layer merged into one pass over the whole graph) and of
+    the reference flow ('off': the reference's gathers of every layer's
+    input rows from the host buffers, per-partition passes, host scatters)
+    from the same weights, on the same partitioned graph.  The two are the
+    same function with the fp32 sums in another order: the loss within 1e-5
+    relative and every gradient within 1e-5 (grad_errs), as
+    tests/test_gradient_identity.py:290-410 of the reference holds its
+    partition-invariant flows to each other."""
+    torch.manual_seed(42)
+    state = make().state_dict()
+    runs = {}
+    for flow in ("auto", "off"):
+        t0 = time.perf_counter()
+        config = GriNNderConfig(num_parts=graph.num_parts, project_first=flow)
+        loss, grads, flows = trainer_epoch(graph, config, state, make)
+        runs[flow] = (loss, grads, flows)
+        log(f"{label} {flow}: loss {loss:.8f}, (projected, in place, gathered, merged) {flows} "
+            f"in {time.perf_counter() - t0:.1f}s")
+    (la, ga, fa), (lo, go, fo) = runs["auto"], runs["off"]
+    n_layers = len(make().convs)
+    assert fa[3] == list(range(n_layers)) and fo[3] == [], (fa, fo)
+    assert sorted(fa[0] + fa[1]) == list(range(n_layers)) and fo[0] == fo[1] == [], (fa, fo)
+    errs = grad_errs(ga, go)
+    log(f"{label} auto vs off: loss rel err {abs(la - lo) / abs(lo):.1e}; grads "
+        f"{({k: f'{v:.1e}' for k, v in errs.items()})}")
+    assert abs(la - lo) / abs(lo) <= TOL
+    assert max(errs.values()) <= TOL, errs
+    return state, la
+
+
+def gcn_loss_float64(graph, state, make, device):
+    """The loss of one full-graph step of the reference GCN in float64 on the
+    partitioned graph's whole adjacency (every partition's rows with their
+    global columns and the pipeline's fp32 weights, rows in partition
+    order), the input projection formed partition by partition from the
+    generated features, so the 41 GB input never sits in memory whole."""
+    n = graph.num_nodes
+    w = graph.whole_adjacency()
+    a = torch.sparse_csr_tensor(w.rowptr.to(device), w.col.to(device),
+                                w.value.to(torch.float64).to(device), (n, n))
+    model = make().to(torch.float64).to(device)
+    model.load_state_dict({k: v.to(torch.float64) for k, v in state.items()})
+    convs, norms = model.convs, model.norms
+    with torch.no_grad():
+        z = torch.empty(n, convs[0].out_channels, dtype=torch.float64, device=device)
+        w0t = convs[0].lin.weight.t()
+        for pid in range(graph.num_parts):
+            lo, hi = int(graph.ptr[pid]), int(graph.ptr[pid + 1])
+            x = graph.features.partition(lo, hi).to(device).double()
+            z[lo:hi] = x @ w0t
+            del x
+        h = torch.relu(norms[0](torch.sparse.mm(a, z) + convs[0].bias))
+        del z
+        for i in range(1, len(convs)):
+            h = torch.sparse.mm(a, h @ convs[i].lin.weight.t()) + convs[i].bias
+            if i < len(convs) - 1:
+                h = torch.relu(norms[i](h))
+        tr = graph.train_mask.to(device)
+        loss = F.cross_entropy(h[tr], graph.labels.to(device)[tr])
+    out = float(loss)
+    del a, h, model
+    torch.cuda.empty_cache()
+    return out
+
+
+def test_c4_epoch_default_flow_matches_reference_flow(gpu, c4_partition):
+    """C4 at full size (10M nodes, 1024-wide inputs, GCN 1024 -> 256 -> 256
+    -> 19, 16 partitions): the default flow that the bench times against the
+    reference flow, and the loss against float64."""
+    graph, _, _ = c4_partition
+    state, loss = _default_vs_reference_flow(graph, _c4_make, "C4")
+    t0 = time.perf_counter()
+    ref = gcn_loss_float64(graph, state, _c4_make, gpu)
+    log(f"C4 float64 loss {ref:.8f} in {time.perf_counter() - t0:.1f}s (rel err "
+        f"{abs(loss - ref) / abs(ref):.1e})")
+    assert abs(loss - ref) / abs(ref) <= TOL
+
+
+def test_c5_epoch_default_flow_matches_reference_flow(gpu, c5_partition):
+    """C5 at full size (10M nodes, GAT 1024 -> 256 -> 19 with one head, 64
+    partitions): the default flow that the bench times (both layers
+    projected and merged, the 256-wide layer reading Z in place with
+    att_src's gradient formed inside its backward, the 20-wide layer
+    gathered, the LayerNorm + ELU backward taking the next layer's product)
+    against the reference flow."""
+    graph, _ = c5_partition
+    _default_vs_reference_flow(graph, _c5_make, "C5")

@@ -36,6 +36,26 @@ def test_gemm_tn_matches_fp64(gpu, k, m, n):
         assert max_abs_norm_err(c, ref) <= TOL
 
 
+@pytest.mark.parametrize("m,n", [(256, 256), (20, 256)])
+def test_gemm_tn_at_ten_million_rows(gpu, m, n):
+    """dW = dZᵀ X over K = 10,000,000 node rows, the reduction length of the
+    merged layers' weight gradients at C4/C5 (256-wide layer 1, and the
+    20-wide padded last layer in its transposed narrow form).  Operands are
+    generated on the device; the float64 reference is summed over 1M-row
+    slices."""
+    k = 10_000_000
+    g = torch.Generator(device=gpu).manual_seed(m + n)
+    a = torch.randn(k, m, device=gpu, generator=g)
+    b = torch.randn(k, n, device=gpu, generator=g)
+    c = gemm_tn(a, b)
+    ref = torch.zeros(m, n, dtype=torch.float64, device=gpu)
+    for lo in range(0, k, 1 << 20):
+        ref += a[lo:lo + (1 << 20)].double().t() @ b[lo:lo + (1 << 20)].double()
+    err = max_abs_norm_err(c, ref)
+    print(f"gemm_tn K={k} {m}x{n}: {err:.1e}", flush=True)
+    assert err <= TOL
+
+
 @pytest.mark.parametrize("splits", [1, 3, 8, 64, 1000])
 def test_gemm_tn_split_counts(gpu, splits):
     """Any split count gives the same product (chunks of 16-row steps)."""

@@ -20,7 +20,7 @@ from grinnder_amd.data.synthetic import banded_graph
 from grinnder_amd.engine.streams import StreamManager
 from grinnder_amd.engine.trainer import Trainer
 from grinnder_amd.nn import GAT, GCN
-from tests.graphs import grad_errs
+from tests.graphs import TOL, grad_errs
 
 pytestmark = pytest.mark.gpu
 
@@ -472,12 +472,20 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     """The projected flow against the reference flow on a graph large enough
     that the dW pass's uploads run while compute work is still queued
     (300k nodes, 8 partitions, widths 128/256), with the layer inputs kept
-    in HBM for the epoch or uploaded again for dW: the loss agrees to 1e-6,
-    gradients to 1e-3 of their largest entry (sums over 180k training rows in
-    fp32 on both sides: the reference flow itself differs from a float64
-    computation by up to ~3e-4 at this scale), and two projected epochs give
-    bit-identical gradients."""
+    in HBM for the epoch or uploaded again for dW, both against a float64
+    torch restatement of the model on the unpartitioned graph
+    (tests/restate.py):
+
+    - the loss of each flow is within 1e-5 of float64, and the two flows'
+      losses and every gradient agree within 1e-5 (grad_errs);
+    - every gradient of each flow is within 1e-5 of float64, or no further
+      from it than 1.5x the distance of the reference's own fp32 arithmetic
+      (the same restatement in float32: torch sparse / index ops and torch
+      GEMMs) - each weight gradient sums ~180k training rows' contributions
+      that cancel, which no fp32 arithmetic resolves to 1e-5;
+    - two projected epochs give bit-identical gradients."""
     from grinnder_amd.data import synthetic
+    from tests.restate import model_epoch
 
     if not resident:
         _limit_resident_inputs(monkeypatch, set())
@@ -490,6 +498,13 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     else:
         make = lambda: GAT(128, 256, 16, num_layers=2, heads=1, dropout=0.0, norm=True)  # noqa
     state = make().state_dict()
+    ref_loss, ref_grads = model_epoch(model_kind, ei, nd.x, nd.y, nd.train_mask, state, make,
+                                      gpu)
+    t32_loss, t32_grads = model_epoch(model_kind, ei, nd.x, nd.y, nd.train_mask, state, make,
+                                      gpu, dtype=torch.float32)
+    t32_err = grad_errs(t32_grads, ref_grads)
+    print(f"{model_kind} 300k: float64 loss {ref_loss:.8f}, torch fp32 {t32_loss:.8f}; torch "
+          f"fp32 grads vs float64 {({k: f'{v:.1e}' for k, v in t32_err.items()})}", flush=True)
     runs = []
     for proj in ("off", "auto", "auto"):
         config = GriNNderConfig(num_parts=8, project_first=proj)
@@ -509,9 +524,18 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
                                        for k, p in model.named_parameters()}))
         del trainer, model, graph
     (l0, g0), (l1, g1), (l2, g2) = runs
-    assert abs(l0 - l1) < 1e-6
-    for k, err in grad_errs(g1, g0).items():
-        assert err <= 1e-3, (k, err)
+    for name, loss, grads in (("off", l0, g0), ("auto", l1, g1)):
+        err = grad_errs({k: v.cpu() for k, v in grads.items()}, ref_grads)
+        print(f"{model_kind} 300k {name}: loss rel err {abs(loss - ref_loss) / abs(ref_loss):.1e}"
+              f"; grads vs float64 {({k: f'{v:.1e}' for k, v in err.items()})}", flush=True)
+        assert abs(loss - ref_loss) / abs(ref_loss) <= TOL
+        for k, e in err.items():
+            assert e <= max(TOL, 1.5 * t32_err[k]), (name, k, e, t32_err[k])
+    assert abs(l0 - l1) / abs(l0) <= TOL
+    flows = grad_errs(g1, g0)
+    print(f"{model_kind} 300k auto vs off: {({k: f'{v:.1e}' for k, v in flows.items()})}",
+          flush=True)
+    assert max(flows.values()) <= TOL, flows
     assert all(torch.equal(g1[k], g2[k]) for k in g1)
 
 

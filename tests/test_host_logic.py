@@ -61,6 +61,32 @@ def test_errors_are_reported_not_swallowed():
                   n[1:].data_ptr(), n[2:].data_ptr())
 
 
+def test_aggregation_refuses_fewer_slots_than_the_plan_has():
+    """A plan with n_fix split rows has at least 2 * n_fix split units, each
+    writing a slot of its own: a smaller n_slots would put their partial
+    sums past the workspace (or the no-alloc scratch).  Both entry points
+    refuse it before anything is launched, so no GPU is needed here."""
+    rowptr = torch.tensor([0, 700, 705, 1400])  # rows 0 and 2 split at seg_len 256
+    units_n = torch.zeros(3, dtype=torch.int64)
+    _lib.call("gr_spmm_plan", rowptr.data_ptr(), 3, 256, None, units_n.data_ptr(), None,
+              units_n[1:].data_ptr(), units_n[2:].data_ptr())
+    n_units, n_fix, n_slots = units_n.tolist()
+    assert (n_fix, n_slots) == (2, 6)
+    units = torch.zeros(n_units * 4, dtype=torch.int32)
+    fixups = torch.zeros(n_fix * 3, dtype=torch.int32)
+    _lib.call("gr_spmm_plan", rowptr.data_ptr(), 3, 256, units.data_ptr(),
+              units_n.data_ptr(), fixups.data_ptr(), units_n[1:].data_ptr(),
+              units_n[2:].data_ptr())
+    fake = 1 << 20  # never dereferenced: the call is refused first
+    common = (units.data_ptr(), n_units, fixups.data_ptr(), n_fix, fake, fake, fake, 8,
+              fake, 8, None, 3, 8)
+    for short in (0, 3):
+        with pytest.raises(_lib.GrError, match="below the 2 \\* n_fix"):
+            _lib.call("gr_gcn_aggregate", *common, fake, short, None)
+        with pytest.raises(_lib.GrError, match="below the 2 \\* n_fix"):
+            _lib.call("gr_gcn_aggregate_noalloc", *common, short, None)
+
+
 def test_single_hip_runtime_loaded():
     _lib.load()
     maps = Path("/proc/self/maps").read_text().splitlines()
@@ -129,6 +155,46 @@ def test_partition_subgraph_and_pipeline_bit_exact():
     for pid in range(3):
         for a, b in zip(g.adj_csr[pid], ref[pid][1]):
             assert torch.equal(a, b)
+
+
+def _assert_same_partitions(g, ref):
+    for pid in range(g.num_parts):
+        _, adj, bnd, expanded, batch = ref[pid]
+        for a, b in zip(g.adj_csr[pid], adj):
+            assert torch.equal(a, b), pid
+        for a, b in zip(g.boundaries[pid], bnd):
+            assert (a is None and b is None) or torch.equal(a, b), pid
+        assert (g.expanded_sizes[pid], g.partition_sizes[pid]) == (expanded, batch), pid
+
+
+@pytest.mark.parametrize("parts", [4, 16])
+def test_directed_rmat_pipeline_bit_exact(parts):
+    """A directed R-MAT graph (power-law, 50k nodes), where CSR orientation
+    and the degree's side are observable: the whole preprocessing pipeline
+    is bit-exact with the oracle's, whose orientation the known answer and
+    the brute-force check in tests/test_oracle.py pin."""
+    n = 50_000
+    ei = synthetic.rmat_graph(n, 400_000, scale=16, seed=5, undirected=False)
+    assert not torch.equal(torch.sort(ei[0] * n + ei[1]).values,
+                           torch.sort(ei[1] * n + ei[0]).values)  # really directed
+    nd = synthetic.node_data(n, 4, 5)
+    g = build_partitioned_graph(ei, nd.x, nd.y, nd.train_mask, nd.val_mask, nd.test_mask,
+                                GriNNderConfig(num_parts=parts))
+    _assert_same_partitions(g, oracle.partition_pipeline(ei, n, g.perm, g.ptr))
+
+
+def test_native_directed_pipeline_known_answer_and_brute_force():
+    """The product's pipeline (partition_adjacency, the steps after the
+    partitioner) against the hand-derived directed answer and the brute-force
+    orientation check, serial and on worker threads."""
+    from grinnder_amd.data.partition import partition_adjacency
+    from tests.test_oracle import check_directed_brute_force, check_directed_known_answer
+
+    for workers in (1, 3):
+        fn = lambda ei, n, perm, ptr: partition_adjacency(ei, n, perm, ptr, workers=workers)
+        check_directed_known_answer(fn)
+        for seed in range(3):
+            check_directed_brute_force(fn, seed)
 
 
 def test_native_partition_subgraph_halo_order_known_answer():
@@ -264,21 +330,19 @@ def test_whole_adjacency_is_the_full_graph_in_partition_order():
     e = inv[ei]
     val = compute_gcn_norm(e, n, add_self_loops=True)
     e = append_self_loops(e, n)
-    rows = {}
-    for src, dst in ((0, 1), (1, 0)):
-        rowptr, col, perm = _edge_index_to_csr(torch.stack([e[src], e[dst]]), n)
-        rows[src] = (rowptr, col, val[perm])
-    matched = 0
-    for rowptr, col, v in rows.values():
-        if not torch.equal(rowptr, w.rowptr):
-            continue
-        for r in range(n):
-            a, b = int(rowptr[r]), int(rowptr[r + 1])
-            ka = sorted(zip(w.col[a:b].tolist(), w.value[a:b].tolist()))
-            kb = sorted(zip(col[a:b].tolist(), v[a:b].tolist()))
-            assert ka == kb, r
-        matched += 1
-    assert matched == 1
+    # The reference's orientation: rows are edge_index[0]
+    # (grinnder/data/partition.py:79-87).  The graph is directed, so the
+    # transposed CSR differs and would fail here.
+    rowptr, col, perm = _edge_index_to_csr(e, n)
+    v = val[perm]
+    rt, _, _ = _edge_index_to_csr(e.flip(0), n)
+    assert not torch.equal(rt, rowptr)
+    assert torch.equal(rowptr, w.rowptr)
+    for r in range(n):
+        a, b = int(rowptr[r]), int(rowptr[r + 1])
+        ka = sorted(zip(w.col[a:b].tolist(), w.value[a:b].tolist()))
+        kb = sorted(zip(col[a:b].tolist(), v[a:b].tolist()))
+        assert ka == kb, r
     assert g.whole_adjacency() is w
 
 

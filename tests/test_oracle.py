@@ -300,6 +300,132 @@ def test_halo_checks_reject_sorted_within_owner():
         check_halo_layout_property(_sorted_within_owner, 0)
 
 
+# ------------------------------------------- orientation on directed graphs --
+# The reference takes CSR rows from edge_index[0] (grinnder/data/partition.py:
+# 79-87) but counts degrees on edge_index[1] (grinnder/data/datasets.py:356-
+# 360).  On a symmetric graph neither choice is observable; these checks use
+# directed graphs.  `fn(edge_index, n, perm, ptr)` returns the per-partition
+# list [(pid, (rowptr, col, value), boundaries, expanded, batch)].
+
+# 0->1, 0->3, 1->2, 3->0, 4->0, 4->2, 2->4 (edge_index[0] -> edge_index[1])
+DIRECTED_EI = [[0, 0, 1, 3, 4, 4, 2], [1, 3, 2, 0, 0, 2, 4]]
+
+
+def check_directed_known_answer(fn):
+    """Hand-derived on DIRECTED_EI with identity perm and ptr [0, 3, 5].
+    Degrees on edge_index[1] plus the self-loop: [3, 2, 3, 2, 2].  Rows are
+    edge_index[0] (out-neighbours plus self).  Partition 0 (rows 0-2) finds
+    halo 3 in row 0, then 4 in row 2; partition 1 (rows 3-4) finds 0 in row
+    3, then 2 in row 4.  Within-row order is argsort's, so rows compare as
+    multisets of (local column, weight)."""
+    r2, r3 = np.float32(1) / np.sqrt(np.float32(2)), np.float32(1) / np.sqrt(np.float32(3))
+    w = {(a, b): float(a * b) for a in (r2, r3) for b in (r2, r3)}
+    d = [r3, r2, r3, r2, r2]
+    expect = {
+        0: dict(rows=[{(1, w[d[0], d[1]]), (3, w[d[0], d[3]]), (0, w[d[0], d[0]])},
+                      {(2, w[d[1], d[2]]), (1, w[d[1], d[1]])},
+                      {(4, w[d[2], d[4]]), (2, w[d[2], d[2]])}],
+                boundaries=[None, [0, 1]], expanded=5, batch=3),
+        1: dict(rows=[{(2, w[d[3], d[0]]), (0, w[d[3], d[3]])},
+                      {(2, w[d[4], d[0]]), (3, w[d[4], d[2]]), (1, w[d[4], d[4]])}],
+                boundaries=[[0, 2], None], expanded=4, batch=2),
+    }
+    out = fn(torch.tensor(DIRECTED_EI), 5, torch.arange(5), torch.tensor([0, 3, 5]))
+    for pid, (got_pid, (rp, c, v), bnd, expanded, batch) in enumerate(out):
+        exp = expect[pid]
+        assert got_pid == pid
+        rows = [set(zip(c[int(rp[r]):int(rp[r + 1])].tolist(),
+                        v[int(rp[r]):int(rp[r + 1])].tolist())) for r in range(batch)]
+        assert rows == exp["rows"], pid
+        assert [None if b is None else b.tolist() for b in bnd] == exp["boundaries"], pid
+        assert (expanded, batch) == (exp["expanded"], exp["batch"]), pid
+
+
+def check_directed_brute_force(fn, seed, n=300, m=2500, parts=4):
+    """A random directed multigraph under a random perm and random cuts: every
+    partition row r (new id) holds exactly the out-edges r -> j of the
+    relabelled edge list plus its self-loop, each weighted fp32(deg[r]^-1/2)
+    * fp32(deg[j]^-1/2) with deg[j] counted by brute force over the edges'
+    targets (plus 1); columns resolve to global ids through the layout
+    [own rows | boundaries by owner]."""
+    g = torch.Generator().manual_seed(seed)
+    ei = torch.randint(0, n, (2, m), generator=g)
+    ei = ei[:, ei[0] != ei[1]]
+    perm = torch.randperm(n, generator=g)
+    cuts = torch.sort(torch.randperm(n - 1, generator=g)[:parts - 1] + 1).values
+    ptr = torch.cat([torch.tensor([0]), cuts, torch.tensor([n])])
+    inv = [0] * n
+    for new, old in enumerate(perm.tolist()):
+        inv[old] = new
+    src = [inv[s] for s in ei[0].tolist()]
+    dst = [inv[t] for t in ei[1].tolist()]
+    deg = [1] * n
+    for t in dst:
+        deg[t] += 1
+    rs = [np.float32(1) / np.sqrt(np.float32(k)) for k in deg]
+    out_edges = [[] for _ in range(n)]
+    for s, t in zip(src + list(range(n)), dst + list(range(n))):
+        out_edges[s].append((t, float(rs[s] * rs[t])))
+    for pid, (_, (rp, c, v), bnd, expanded, batch) in enumerate(fn(ei, n, perm, ptr)):
+        lo = int(ptr[pid])
+        layout = [lo + k for k in range(batch)]
+        for p, b in enumerate(bnd):
+            if b is not None:
+                layout += [int(ptr[p]) + k for k in b.tolist()]
+        assert len(layout) == expanded
+        for r in range(batch):
+            a, e = int(rp[r]), int(rp[r + 1])
+            got = sorted(zip((layout[k] for k in c[a:e].tolist()), v[a:e].tolist()))
+            assert got == sorted(out_edges[lo + r]), (pid, r)
+
+
+def _swapped_pipeline(ei, n, perm, ptr):
+    """A plausible slip: the pipeline with edge_index[0] and [1] swapped
+    (rows from the targets, degrees on the sources)."""
+    return oracle.partition_pipeline(ei.flip(0), n, perm, ptr)
+
+
+def _row_degree_pipeline(ei, n, perm, ptr):
+    """A plausible slip: degrees counted on edge_index[0] instead of [1].
+    The oracle's structure is kept and every weight recomputed from the
+    out-degrees (plus the self-loop)."""
+    out = oracle.partition_pipeline(ei, n, perm, ptr)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(n)
+    e = inv[ei]
+    deg = torch.bincount(e[0], minlength=n).to(torch.float32) + 1
+    rs = deg.pow(-0.5)
+    fixed = []
+    for pid, (rp, c, v), bnd, expanded, batch in out:
+        lo = int(ptr[pid])
+        layout = torch.tensor([lo + k for k in range(batch)]
+                              + [int(ptr[p]) + k for p, b in enumerate(bnd) if b is not None
+                                 for k in b.tolist()], dtype=torch.long)
+        rows = torch.repeat_interleave(torch.arange(batch), rp[1:] - rp[:-1]) + lo
+        fixed.append((pid, (rp, c, rs[rows] * rs[layout[c]]), bnd, expanded, batch))
+    return fixed
+
+
+def test_directed_pipeline_known_answer():
+    check_directed_known_answer(oracle.partition_pipeline)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_directed_pipeline_brute_force(seed):
+    check_directed_brute_force(oracle.partition_pipeline, seed)
+
+
+def test_directed_checks_reject_swapped_orientation_and_row_degrees():
+    """Both checks fail for a pipeline that swaps edge_index[0] and [1], and
+    for one that counts degrees on edge_index[0] (the mistakes are planted
+    in copies of the oracle, on the CPU)."""
+    for slip in (_swapped_pipeline, _row_degree_pipeline):
+        with pytest.raises(AssertionError):
+            check_directed_known_answer(slip)
+        with pytest.raises(AssertionError):
+            check_directed_brute_force(slip, 0)
+
+
 # ----------------------------------------------------------- arithmetic --
 
 def _dense(rowptr, col, val, rows, cols):
@@ -468,3 +594,55 @@ def test_scatter_repeated_indices_accumulate_in_order():
     src = torch.tensor([[1.0], [2.0], [3.0], [4.0], [5.0]])
     out = oracle.scatter_partitions(0, src, dsts, bnd)
     assert out[1].reshape(-1).tolist() == [0.0, 7.0, 5.0]
+
+
+# ------------------------------------- the GPU epoch tests' torch restatements --
+
+def test_gat_restatement_matches_oracle():
+    """tests/restate.py's one-head GAT attention (the float64 model checker of
+    the epoch-level GPU tests) equals the oracle's GATConv forward and
+    backward on a small square graph, rows from the CSR."""
+    from tests.restate import gat_attention_full
+
+    n, c = 150, 12
+    rowptr, col, _ = random_bipartite(n, n, 6, seed=3, long_rows=2, long_len=40)
+    g = torch.Generator().manual_seed(4)
+    hs = torch.randn(n, c, generator=g, dtype=torch.float64)
+    a_s = torch.randn(1, 1, c, generator=g, dtype=torch.float64)
+    a_d = torch.randn(1, 1, c, generator=g, dtype=torch.float64)
+    b = torch.randn(c, generator=g, dtype=torch.float64)
+    gy = torch.randn(n, c, generator=g, dtype=torch.float64)
+    dst = torch.repeat_interleave(torch.arange(n), rowptr[1:] - rowptr[:-1])
+    leaves = [t.clone().requires_grad_(True) for t in (hs, a_s, a_d, b)]
+    out = gat_attention_full(*leaves, dst, col, n)
+    out.backward(gy)
+    ref_o, alpha, tpre = oracle.gat_forward(rowptr, col, hs.float(), 1, c, a_s.float(),
+                                            a_d.float(), b.float(), True)
+    refs = oracle.gat_backward(rowptr, col, hs.float(), 1, c, a_s.float(), a_d.float(), True,
+                               alpha, tpre, gy.float())
+    # The oracle takes fp32 inputs (accumulating in float64): compare at fp32 input rounding.
+    assert torch.allclose(out.detach(), torch.from_numpy(ref_o), rtol=1e-5, atol=1e-5)
+    for got, ref in zip(leaves, refs):
+        ref = torch.as_tensor(ref).reshape(got.shape)
+        assert torch.allclose(got.grad, ref, rtol=1e-4, atol=1e-4), (got.grad - ref).abs().max()
+
+
+def test_gcn_restatement_matches_dense():
+    """tests/restate.py's GCN layers equal a dense float64 restatement."""
+    from grinnder_amd.nn import GCN
+    from tests.restate import gcn_layers
+
+    n = 120
+    rowptr, col, val = random_bipartite(n, n, 5, seed=8)
+    a = torch.sparse_csr_tensor(rowptr, col, val.double(), (n, n))
+    dense = a.to_dense()
+    torch.manual_seed(1)
+    model = GCN(16, 24, 5, num_layers=3, dropout=0.0, norm=True).double()
+    x = torch.randn(n, 16, dtype=torch.float64)
+    got = gcn_layers(model, a, x)
+    h = x
+    for i, conv in enumerate(model.convs):
+        h = dense @ (h @ conv.lin.weight.t()) + conv.bias
+        if i < 2:
+            h = torch.relu(model.norms[i](h))
+    assert torch.allclose(got, h, rtol=1e-12, atol=1e-12)

@@ -73,6 +73,28 @@ def test_engine_reports_errors(tmp_path):
         e.submit_write(path, torch.ones(4), 0, 17)
 
 
+def test_engine_failed_chunk_fails_the_request(tmp_path):
+    """A read of 5 chunks from a file truncated inside the fourth: the other
+    chunks succeed, and wait() must still report the failure (the request
+    completes only once every chunk has published its result).  Repeated
+    with many workers so that the failing chunk is not reliably the last."""
+    chunk = 8 << 20
+    path = str(tmp_path / "trunc.pt")
+    full = torch.arange(5 * chunk // 4, dtype=torch.int32).view(torch.float32)
+    e = IoUringEngine(8)
+    e.wait(e.submit_write(path, full, 0, full.numel() * 4))
+    os.truncate(path, 3 * chunk + 1234)
+    for _ in range(20):
+        u = torch.zeros_like(full)
+        h = e.submit_read(path, u, 0, u.numel() * 4)
+        with pytest.raises(_lib.GrError, match="shorter"):
+            e.wait(h)
+        # the chunks before the cut still arrived
+        assert torch.equal(u[:3 * chunk // 4].view(torch.int32),
+                           full[:3 * chunk // 4].view(torch.int32))
+    assert e.pending() == 0
+
+
 # ------------------------------------------------------------- the backend --
 
 def test_backend_host_write_read_and_files(backend):
