@@ -77,6 +77,16 @@ _SIGNATURES = {
                             _i64, _i64, _P, _P, _P, _P, _i64, _P],
     "gr_gat_backward_src_into": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _P,
                                  _P, _i64, _i64, _P, _P, _P, _P, _i64, _P, _i64, _P, _P],
+    "gr_gat_forward_ln": [_P, _i64, _P, _i64, _P, _P, _i64, _P, _P, _i64, _i64, _P, _P, _P,
+                          _f32, _i32, _P, _P, _P, _P, _i64, _P, _P, _P, _i64,
+                          _i64, _P],
+    "gr_gat_dst_record": [_P, _P, _P, _P, _i64, _P, _P],
+    "gr_gat_backward_src_h1": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _i64,
+                               _P, _P, _P, _P, _i64, _P, _i64, _P, _P],
+    "gr_gat_narrow_forward": [_P, _i64, _P, _i64, _P, _i64, _P, _P, _i64, _i64, _i64, _i64,
+                              _P, _P, _P, _P, _P, _P, _P, _P, _i64, _P, _P, _i64, _i64, _P],
+    "gr_gat_narrow_backward": [_P, _i64, _P, _i64, _P, _i64, _P, _P, _i64, _i64, _i64, _P,
+                               _i64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _i64, _i64, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],
     "gr_io_create": [_i32, _P],

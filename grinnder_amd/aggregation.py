@@ -563,6 +563,120 @@ def gcn_aggregate_ln_relu(z: Tensor, adj: Adjacency, bias: Optional[Tensor], gam
 _ATT_PARTIAL_ROWS = 8192
 
 
+def _gat_narrow_ok(hs: Tensor, heads: int, channels: int) -> bool:
+    """One head of at most 24 channels, a multiple of 4, on 16-byte rows: the
+    packed-line kernels of gr_gat_narrow_forward / _backward."""
+    return (heads == 1 and channels % 4 == 0 and 4 <= channels <= 24
+            and hs.data_ptr() % 16 == 0 and hs.stride(0) % 4 == 0)
+
+
+def _gat_records_ok(hs: Tensor, heads: int, channels: int) -> bool:
+    """One head whose rows the record-based kernels take (gr_gat_backward_src_h1:
+    at most 256 vectors, 16-byte vectors when aligned): the forward then
+    stores no alpha and the backward recomputes it from the destination
+    records."""
+    if heads != 1:
+        return False
+    if channels % 4 == 0 and hs.data_ptr() % 16 == 0 and hs.stride(0) % 4 == 0:
+        return channels <= 1024
+    return channels <= 256
+
+
+def _attention_backward(plan: DevicePlan, hs: Tensor, a_src: Tensor, a_dst: Tensor, s: Tensor,
+                        d: Tensor, alpha_or_m: Tensor, den: Tensor, go: Tensor, cdot: Tensor,
+                        H: int, C: int, records: bool, zsink: Optional[ProjectedSink]):
+    """dHs (None with zsink: added into zsink.dz), datt_src and datt_dst of the
+    attention given go = dL/dO [B, H*C] and cdot = <go_i, O_i> [B, H].
+    records: one head, the forward stored no alpha (alpha_or_m holds m); the
+    source pass reads the destination records (gr_gat_backward_src_h1)."""
+    HC = H * C
+    E, B = plan.num_src, plan.num_dst
+    dev = hs.device
+    stream = _lib.stream_handle()
+    nnz = plan.nnz
+    region = KernelTimer.region(
+        "gat_bwd", nnz * (8 * HC + 16 * H + 8) + E * (4 * HC + 4 * H) + B * (4 * HC + 4 * H),
+        nnz, HC)
+    region.__enter__()
+    ds = torch.empty((E, H), dtype=torch.float32, device=dev)
+    gt = torch.empty((max(plan.nnz, 1), H), dtype=torch.float32, device=dev)
+    bw = plan.bwd
+    ws_stride = ((HC + 3) // 4) * 4 + ((H + 3) // 4) * 4
+    ws = _workspace(bw.n_slots, ws_stride, dev)
+    rec = None
+    if records:
+        if go.data_ptr() % 16:
+            go = go.clone()  # 16-byte rows for the vector loads
+        rec = torch.empty((B, 4), dtype=torch.float32, device=dev)
+        _lib.call("gr_gat_dst_record", d.data_ptr(), alpha_or_m.data_ptr(), den.data_ptr(),
+                  cdot.data_ptr(), B, rec.data_ptr(), stream)
+    if zsink is None:
+        dhs = torch.empty((E, HC), dtype=torch.float32, device=dev)
+        if rec is not None:
+            _lib.call("gr_gat_backward_src_h1", bw.units.data_ptr(), bw.n_units,
+                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
+                      hs.stride(0), None, go.data_ptr(), s.data_ptr(), rec.data_ptr(),
+                      a_src.data_ptr(), C, dhs.data_ptr(), ds.data_ptr(), gt.data_ptr(),
+                      _lib.ptr(ws), bw.n_slots, None, 0, None, stream)
+        else:
+            _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
+                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
+                      hs.stride(0), go.data_ptr(), s.data_ptr(), d.data_ptr(),
+                      alpha_or_m.data_ptr(), cdot.data_ptr(), a_src.data_ptr(), H, C,
+                      dhs.data_ptr(), ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws),
+                      bw.n_slots, stream)
+        dst_rows = dhs
+    else:
+        # dHs straight into dZ at the partition's global rows; the
+        # destination part below adds into its own rows dZ[lo:lo+B].
+        # The same pass forms per-wavefront partial sums of
+        # datt_src = sum_j ds_j Hs_j while Hs_j is in its registers.
+        dhs = None
+        att_rows = min(bw.n_units, _ATT_PARTIAL_ROWS)
+        att_part = torch.empty((max(att_rows, 1), HC), dtype=torch.float32, device=dev)
+        att_waves = ctypes.c_int64(0)
+        if rec is not None:
+            _lib.call("gr_gat_backward_src_h1", bw.units.data_ptr(), bw.n_units,
+                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
+                      hs.stride(0), zsink.rows.data_ptr(), go.data_ptr(), s.data_ptr(),
+                      rec.data_ptr(), a_src.data_ptr(), C, zsink.dz.data_ptr(),
+                      ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws), bw.n_slots,
+                      att_part.data_ptr(), att_part.size(0), ctypes.addressof(att_waves),
+                      stream)
+        else:
+            _lib.call("gr_gat_backward_src_into", bw.units.data_ptr(), bw.n_units,
+                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
+                      hs.stride(0), zsink.rows.data_ptr(), go.data_ptr(), s.data_ptr(),
+                      d.data_ptr(), alpha_or_m.data_ptr(), cdot.data_ptr(),
+                      a_src.data_ptr(), H, C, zsink.dz.data_ptr(), ds.data_ptr(),
+                      gt.data_ptr(), _lib.ptr(ws), bw.n_slots, att_part.data_ptr(),
+                      att_part.size(0), ctypes.addressof(att_waves), stream)
+        dst_rows = zsink.dz[zsink.lo:zsink.lo + B]
+    dd = torch.empty((B, H), dtype=torch.float32, device=dev)
+    f = plan.fwd
+    ws = _workspace(f.n_slots, H, dev)
+    _lib.call("gr_gat_backward_dst", f.units.data_ptr(), f.n_units,
+              f.fixups.data_ptr() if f.n_fix else None, f.n_fix, gt.data_ptr(),
+              a_dst.data_ptr(), cdot.data_ptr(), den.data_ptr(), H, C, dd.data_ptr(),
+              dst_rows.data_ptr(), _lib.ptr(ws), f.n_slots, stream)
+    region.__exit__(None, None, None)
+    # Attention-vector gradients: per head, ds[:,h]^T Hs[:, h] and dd[:,h]^T Hs[:B, h].
+    if zsink is None:
+        datt_src = column_sum(hs, ds, C)
+        datt_dst = column_sum(hs[:B], dd, C)
+    else:
+        if att_waves.value > 0:
+            datt_src = column_sum(att_part[:att_waves.value])
+        else:  # no units: nothing summed
+            datt_src = torch.zeros(HC, dtype=torch.float32, device=dev)
+        datt_dst = column_sum(hs[zsink.lo:zsink.lo + B], dd, C)
+    return dhs, datt_src, datt_dst
+
+
 class _GATAttention(torch.autograd.Function):
     """Attention logits + edge softmax + weighted aggregation of GATConv."""
 
@@ -587,6 +701,9 @@ class _GATAttention(torch.autograd.Function):
         region = KernelTimer.region(
             "gat_fwd", nnz * (4 * HC + 8 * H + 4) + B * (4 * HC + 4 * H + 4), nnz, HC)
         region.__enter__()
+        if zsink is None and _gat_narrow_ok(hs, H, C):
+            return _GATAttention._forward_narrow(ctx, hs, a_src, a_dst, bias, plan, C, s_pre,
+                                                 d_pre, region, att_src.shape)
         if s_pre is not None:
             # Scores formed beforehand (once per layer for all rows of a
             # projected matrix, by the same kernel): s_pre [E, H], d_pre [B, H].
@@ -598,7 +715,11 @@ class _GATAttention(torch.autograd.Function):
                       a_dst.data_ptr(), s.data_ptr(), d.data_ptr(), stream)
         m = torch.empty((B, H), dtype=torch.float32, device=dev)
         den = torch.empty((B, H), dtype=torch.float32, device=dev)
-        alpha = torch.empty((max(nnz, 1), H), dtype=torch.float32, device=dev)
+        # One head: alpha is not stored; the backward recomputes it from the
+        # destination records (gr_gat_backward_src_h1).
+        records = _gat_records_ok(hs, H, C)
+        alpha = None if records else torch.empty((max(nnz, 1), H), dtype=torch.float32,
+                                                 device=dev)
         f = plan.fwd
         o = torch.empty((B, HC), dtype=torch.float32, device=dev)
         fused_bias = (concat or H == 1) and bias is not None
@@ -610,7 +731,7 @@ class _GATAttention(torch.autograd.Function):
         _lib.call("gr_gat_forward", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix, idx.data_ptr(),
                   hs.data_ptr(), hs.stride(0), s.data_ptr(), d.data_ptr(), B, H, C, _lib.ptr(b),
-                  m.data_ptr(), den.data_ptr(), alpha.data_ptr(), o.data_ptr(), _lib.ptr(y), HC,
+                  m.data_ptr(), den.data_ptr(), _lib.ptr(alpha), o.data_ptr(), _lib.ptr(y), HC,
                   _lib.ptr(ws), 0 if ws is None else ws.numel(), f.n_slots, stream)
         region.__exit__(None, None, None)
         if concat or H == 1:
@@ -620,7 +741,8 @@ class _GATAttention(torch.autograd.Function):
             y = o.view(B, H, C).mean(dim=1)
             if bias is not None:
                 y = y + bias
-        ctx.save_for_backward(hs, a_src, a_dst, s, d, alpha, den, o)
+        ctx.save_for_backward(hs, a_src, a_dst, s, d, m if records else alpha, den, o)
+        ctx.records = records
         ctx.plan = plan
         ctx.shape = (H, C, concat)
         ctx.has_bias = bias is not None
@@ -630,8 +752,76 @@ class _GATAttention(torch.autograd.Function):
         return y
 
     @staticmethod
+    def _forward_narrow(ctx, hs, a_src, a_dst, bias, plan, C, s_pre, d_pre, region,
+                        att_shape):
+        """One head of C <= 24 channels: every row packed into a 128-byte line
+        with its logit halves, an online softmax, no alpha stored."""
+        dev = hs.device
+        E, B = plan.num_src, plan.num_dst
+        f = plan.fwd
+        zx = torch.empty((E, 32), dtype=torch.float32, device=dev)
+        fstate = torch.empty((B, 32), dtype=torch.float32, device=dev)
+        o = torch.empty((B, C), dtype=torch.float32, device=dev)
+        y = torch.empty((B, C), dtype=torch.float32, device=dev) if bias is not None else None
+        ws = _workspace(f.n_slots, 52, dev)
+        s = None if s_pre is None else s_pre.contiguous()
+        d = None if d_pre is None else d_pre.contiguous()
+        _lib.call("gr_gat_narrow_forward", f.units.data_ptr(), f.n_units,
+                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix,
+                  _lib.ptr(f.long_units), f.n_long, plan.idx.data_ptr(), hs.data_ptr(),
+                  hs.stride(0), E, B, C, _lib.ptr(s), _lib.ptr(d), a_src.data_ptr(),
+                  a_dst.data_ptr(), _lib.ptr(bias.contiguous() if bias is not None else None),
+                  zx.data_ptr(), o.data_ptr(), _lib.ptr(y), C, fstate.data_ptr(),
+                  _lib.ptr(ws), 0 if ws is None else ws.numel(), f.n_slots,
+                  _lib.stream_handle())
+        region.__exit__(None, None, None)
+        ctx.save_for_backward(hs, a_src, a_dst, zx, fstate, o)
+        ctx.narrow = True
+        ctx.plan = plan
+        ctx.shape = (1, C, True)
+        ctx.has_bias = bias is not None
+        ctx.att_shape = att_shape
+        return y if y is not None else o
+
+    @staticmethod
+    def _backward_narrow(ctx, gy: Tensor):
+        hs, a_src, a_dst, zx, fstate, o = ctx.saved_tensors
+        plan: DevicePlan = ctx.plan
+        C = ctx.shape[1]
+        E, B = plan.num_src, plan.num_dst
+        dev = hs.device
+        go = gy.contiguous()
+        if go.data_ptr() % 16:
+            go = go.clone()
+        db = column_sum(go) if ctx.has_bias else None
+        nnz = plan.nnz
+        region = KernelTimer.region(
+            "gat_bwd", nnz * (8 * C + 16 + 8) + E * (4 * C + 4) + B * (4 * C + 4), nnz, C)
+        region.__enter__()
+        bw = plan.bwd
+        gx = torch.empty((B, 32), dtype=torch.float32, device=dev)
+        dhs = torch.empty((E, C), dtype=torch.float32, device=dev)
+        ds = torch.empty((E, 1), dtype=torch.float32, device=dev)
+        dd = torch.empty((B, 1), dtype=torch.float32, device=dev)
+        ws = _workspace(bw.n_slots, 28, dev)
+        _lib.call("gr_gat_narrow_backward", bw.units.data_ptr(), bw.n_units,
+                  bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
+                  _lib.ptr(bw.long_units), bw.n_long, plan.row_idx.data_ptr(), zx.data_ptr(),
+                  E, B, C, go.data_ptr(), go.stride(0), o.data_ptr(), fstate.data_ptr(),
+                  a_src.data_ptr(), a_dst.data_ptr(), gx.data_ptr(), dhs.data_ptr(),
+                  ds.data_ptr(), dd.data_ptr(), _lib.ptr(ws), 0 if ws is None else ws.numel(),
+                  bw.n_slots, _lib.stream_handle())
+        region.__exit__(None, None, None)
+        datt_src = column_sum(hs, ds, C)
+        datt_dst = column_sum(hs[:B], dd, C)
+        return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
+                None, None, None, None, None, None, None, None, None)
+
+    @staticmethod
     def backward(ctx, gy: Tensor):
-        hs, a_src, a_dst, s, d, alpha, den, o = ctx.saved_tensors
+        if getattr(ctx, "narrow", False):
+            return _GATAttention._backward_narrow(ctx, gy)
+        hs, a_src, a_dst, s, d, alpha_or_m, den, o = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
         H, C, concat = ctx.shape
         HC = H * C
@@ -654,63 +844,9 @@ class _GATAttention(torch.autograd.Function):
             cdot = torch.empty((B, H), dtype=torch.float32, device=dev)
             _lib.call("gr_gat_row_dot", go.data_ptr(), go.stride(0), o.data_ptr(), o.stride(0),
                       B, H, C, cdot.data_ptr(), stream)
-        nnz = plan.nnz
-        region = KernelTimer.region(
-            "gat_bwd", nnz * (8 * HC + 16 * H + 8) + E * (4 * HC + 4 * H) + B * (4 * HC + 4 * H),
-            nnz, HC)
-        region.__enter__()
         zsink = ctx.zsink
-        ds = torch.empty((E, H), dtype=torch.float32, device=dev)
-        gt = torch.empty((max(plan.nnz, 1), H), dtype=torch.float32, device=dev)
-        bw = plan.bwd
-        ws_stride = ((HC + 3) // 4) * 4 + ((H + 3) // 4) * 4
-        ws = _workspace(bw.n_slots, ws_stride, dev)
-        if zsink is None:
-            dhs = torch.empty((E, HC), dtype=torch.float32, device=dev)
-            _lib.call("gr_gat_backward_src", bw.units.data_ptr(), bw.n_units,
-                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
-                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
-                      hs.stride(0), go.data_ptr(), s.data_ptr(), d.data_ptr(),
-                      alpha.data_ptr(), cdot.data_ptr(), a_src.data_ptr(), H, C,
-                      dhs.data_ptr(), ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws), bw.n_slots,
-                      stream)
-            dst_rows = dhs
-        else:
-            # dHs straight into dZ at the partition's global rows; the
-            # destination part below adds into its own rows dZ[lo:lo+B].
-            # The same pass forms per-wavefront partial sums of
-            # datt_src = sum_j ds_j Hs_j while Hs_j is in its registers.
-            dhs = None
-            att_rows = min(bw.n_units, _ATT_PARTIAL_ROWS)
-            att_part = torch.empty((max(att_rows, 1), HC), dtype=torch.float32, device=dev)
-            att_waves = ctypes.c_int64(0)
-            _lib.call("gr_gat_backward_src_into", bw.units.data_ptr(), bw.n_units,
-                      bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
-                      plan.row_idx.data_ptr(), plan.perm.data_ptr(), hs.data_ptr(),
-                      hs.stride(0), zsink.rows.data_ptr(), go.data_ptr(), s.data_ptr(),
-                      d.data_ptr(), alpha.data_ptr(), cdot.data_ptr(), a_src.data_ptr(), H, C,
-                      zsink.dz.data_ptr(), ds.data_ptr(), gt.data_ptr(), _lib.ptr(ws),
-                      bw.n_slots, att_part.data_ptr(), att_part.size(0),
-                      ctypes.addressof(att_waves), stream)
-            dst_rows = zsink.dz[zsink.lo:zsink.lo + B]
-        dd = torch.empty((B, H), dtype=torch.float32, device=dev)
-        f = plan.fwd
-        ws = _workspace(f.n_slots, H, dev)
-        _lib.call("gr_gat_backward_dst", f.units.data_ptr(), f.n_units,
-                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, gt.data_ptr(),
-                  a_dst.data_ptr(), cdot.data_ptr(), den.data_ptr(), H, C, dd.data_ptr(),
-                  dst_rows.data_ptr(), _lib.ptr(ws), f.n_slots, stream)
-        region.__exit__(None, None, None)
-        # Attention-vector gradients: per head, ds[:,h]^T Hs[:, h] and dd[:,h]^T Hs[:B, h].
-        if zsink is None:
-            datt_src = column_sum(hs, ds, C)
-            datt_dst = column_sum(hs[:B], dd, C)
-        else:
-            if att_waves.value > 0:
-                datt_src = column_sum(att_part[:att_waves.value])
-            else:  # no units: nothing summed
-                datt_src = torch.zeros(HC, dtype=torch.float32, device=dev)
-            datt_dst = column_sum(hs[zsink.lo:zsink.lo + B], dd, C)
+        dhs, datt_src, datt_dst = _attention_backward(plan, hs, a_src, a_dst, s, d, alpha_or_m,
+                                                      den, go, cdot, H, C, ctx.records, zsink)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
                 None, None, None, None, None, None, None, None, None)
 
@@ -781,3 +917,133 @@ def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
         raise ValueError("gat_attention: scores do not match the adjacency and heads")
     return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat, s, d,
                                rowdot_sink)
+
+
+class _GATAttentionLN(torch.autograd.Function):
+    """One head: attention + conv bias + LayerNorm + activation in one pass
+    (gr_gat_forward_ln: the epilogue in the attention kernel's row store, so
+    O never reaches HBM).  Backward: the LayerNorm/activation backward (or
+    its form with the consumer's product, LNProductSink), which also forms
+    c_i = <dL/dO_i, O_i>, then the attention backward with the destination
+    records."""
+
+    @staticmethod
+    def forward(ctx, hs: Tensor, att_src: Tensor, att_dst: Tensor, bias: Optional[Tensor],
+                gamma: Tensor, beta: Tensor, token: Optional[Tensor], plan: DevicePlan,
+                eps: float, act: str, s_pre: Optional[Tensor], d_pre: Optional[Tensor],
+                zsink: Optional[ProjectedSink], dest: Optional[OutputRows],
+                ln_sink) -> Tensor:
+        hs = hs.contiguous()
+        dev = hs.device
+        C = hs.size(1)
+        E, B = plan.num_src, plan.num_dst
+        a_src = att_src.reshape(-1).contiguous()
+        a_dst = att_dst.reshape(-1).contiguous()
+        stream = _lib.stream_handle()
+        nnz = plan.nnz
+        region = KernelTimer.region("gat_fwd", nnz * (4 * C + 12) + B * (4 * C + 8), nnz, C)
+        region.__enter__()
+        if s_pre is not None:
+            s, d = s_pre.contiguous(), d_pre.contiguous()
+        else:
+            s = torch.empty((E, 1), dtype=torch.float32, device=dev)
+            d = torch.empty((B, 1), dtype=torch.float32, device=dev)
+            _lib.call("gr_gat_scores", hs.data_ptr(), hs.stride(0), E, B, 1, C, a_src.data_ptr(),
+                      a_dst.data_ptr(), s.data_ptr(), d.data_ptr(), stream)
+        m = torch.empty((B, 1), dtype=torch.float32, device=dev)
+        den = torch.empty((B, 1), dtype=torch.float32, device=dev)
+        h = torch.empty((B, C), dtype=torch.float32, device=dev)
+        out = output_block(dest, B, C, dev)
+        mean = torch.empty(B, dtype=torch.float32, device=dev)
+        rstd = torch.empty(B, dtype=torch.float32, device=dev)
+        f = plan.fwd
+        ws = _workspace(f.n_slots, C + 4, dev)
+        b = bias.contiguous() if bias is not None else None
+        g, bt = gamma.contiguous(), beta.contiguous()
+        idx = plan.idx if zsink is None else zsink.gidx
+        _lib.call("gr_gat_forward_ln", f.units.data_ptr(), f.n_units,
+                  f.fixups.data_ptr() if f.n_fix else None, f.n_fix, idx.data_ptr(),
+                  hs.data_ptr(), hs.stride(0), s.data_ptr(), d.data_ptr(), B, C, _lib.ptr(b),
+                  g.data_ptr(), bt.data_ptr(), float(eps), _lib.ACTIVATIONS[act],
+                  m.data_ptr(), den.data_ptr(), h.data_ptr(), out.data_ptr(), C,
+                  mean.data_ptr(), rstd.data_ptr(), _lib.ptr(ws),
+                  0 if ws is None else ws.numel(), f.n_slots, stream)
+        region.__exit__(None, None, None)
+        ctx.save_for_backward(hs, a_src, a_dst, s, d, m, den, h, mean, rstd, g, bt)
+        ctx.plan = plan
+        ctx.zsink = zsink
+        ctx.bias = b
+        ctx.act = act
+        ctx.ln_sink = ln_sink
+        ctx.att_shape = att_src.shape
+        return out
+
+    @staticmethod
+    def backward(ctx, gout: Tensor):
+        hs, a_src, a_dst, s, d, m, den, h, mean, rstd, g, bt = ctx.saved_tensors
+        plan: DevicePlan = ctx.plan
+        B, C = h.shape
+        has_bias = ctx.bias is not None
+        rowdot = torch.empty(B, dtype=torch.float32, device=h.device)
+        prod = ctx.ln_sink.take(gout) if ctx.ln_sink is not None else None
+        if prod is not None and prod[2]:
+            gh, dgamma, dbeta, db = ln_act_backward_product(
+                prod[0], prod[1], h, mean, rstd, g, bt, has_bias, ctx.act, shift=ctx.bias,
+                rowdot=rowdot)
+        else:
+            if prod is not None:
+                from grinnder_amd.dense import gemm_nt
+                gout = gout + gemm_nt(prod[0], prod[1].t().contiguous())
+            gh, dgamma, dbeta, db = ln_act_backward(gout, h, mean, rstd, g, bt, has_bias,
+                                                    ctx.act, shift=ctx.bias, rowdot=rowdot)
+        dhs, datt_src, datt_dst = _attention_backward(plan, hs, a_src, a_dst, s, d, m, den, gh,
+                                                      rowdot.view(B, 1), 1, C, True,
+                                                      ctx.zsink)
+        return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db, dgamma,
+                dbeta, None, None, None, None, None, None, None, None, None)
+
+
+def gat_attention_ln_ok(hs: Tensor, heads: int, channels: int, gamma: Tensor) -> bool:
+    """Whether gat_attention_ln runs its fused kernel: one head of 132..1024
+    channels (a multiple of 4, rows held by a whole wavefront) on 16-byte
+    rows, with an affine LayerNorm over the full width."""
+    return (heads == 1 and channels % 4 == 0 and 128 < channels <= 1024
+            and hs.data_ptr() % 16 == 0 and hs.stride(0) % 4 == 0
+            and gamma is not None and tuple(gamma.shape) == (channels,))
+
+
+def gat_attention_ln(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
+                     bias: Optional[Tensor], gamma: Tensor, beta: Tensor, eps: float,
+                     act: str = "elu", scores: Optional[Tuple[Tensor, Tensor]] = None,
+                     sink: Optional[ProjectedSink] = None,
+                     dest: Optional[OutputRows] = None) -> Tensor:
+    """act(LayerNorm(GATConv attention + bias)) of one head (GAT.forward_layer's
+    conv -> LayerNorm -> ELU, grinnder/nn/gat.py:74-78) as one pass per row;
+    hs, scores and sink as gat_attention, dest as dense.bias_ln_act.  The
+    caller checks gat_attention_ln_ok."""
+    _check_device_tensor("hs", hs)
+    plan = adj.device_plan(hs.device)
+    C = hs.size(1)
+    if act not in _lib.ACTIVATIONS:
+        raise ValueError(f"unknown activation {act!r}")
+    if not gat_attention_ln_ok(hs, 1, C, gamma):
+        raise ValueError("gat_attention_ln: one head of 132..1024 channels on 16-byte rows")
+    s_pre = d_pre = None
+    if scores is not None:
+        s_pre, d_pre = scores
+    token = None
+    if sink is not None:
+        if scores is None or sink.gidx.numel() != plan.nnz or sink.rows.numel() != plan.num_src \
+                or sink.dz is None or tuple(sink.dz.shape) != tuple(hs.shape):
+            raise ValueError("gat_attention_ln: sink does not match the adjacency and hs")
+        token = sink.token
+    elif hs.size(0) != plan.num_src:
+        raise ValueError(f"hs has {hs.size(0)} rows, adjacency has {plan.num_src} columns")
+    if s_pre is not None and (tuple(d_pre.shape) != (plan.num_dst, 1)
+                              or s_pre.size(0) != hs.size(0)):
+        raise ValueError("gat_attention_ln: scores do not match the adjacency")
+    ln_sink = LNProductSink()
+    out = _GATAttentionLN.apply(hs, att_src, att_dst, bias, gamma, beta, token, plan, eps, act,
+                                s_pre, d_pre, sink, dest, ln_sink)
+    out._grinnder_ln_sink = ln_sink
+    return out

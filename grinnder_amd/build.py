@@ -29,6 +29,7 @@ SOURCES = [
     "transfer.hip",
     "aggregate.hip",
     "gat.hip",
+    "gat_narrow.hip",
     "gemm.hip",
     "loss.hip",
 ]

@@ -29,6 +29,7 @@
 #include <cfloat>
 
 #include "gr_internal.h"
+#include "ln_row.h"
 #include "wave.h"
 
 namespace gr_gat {
@@ -419,6 +420,47 @@ __global__ __launch_bounds__(256) void gat_aggregate_fixup(const int32_t* __rest
 // registers (gr_spmm_plan's units hold at most 512 edges).
 constexpr int kFwdChunks = 8;
 
+// The conv bias + LayerNorm + activation after the attention (the GAT
+// model's epilogue, grinnder/nn/gat.py:74-78), fused into the whole-row
+// store of one-head rows held by a full wavefront (G = 64): with gamma set,
+// a row writes h = O + bias, out = act(LN(h)) (into y, row stride ldy) and
+// the row's mean and rstd, and neither O nor Y + bias; ln_relu_store_row
+// forms them exactly as the dense epilogue does from the same h.
+struct GatLn {
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float eps = 0.f;
+  int act = GR_ACT_ELU;
+  float* h = nullptr;
+  float* mean = nullptr;
+  float* rstd = nullptr;
+};
+
+template <int VEC, int NCH>
+__device__ __forceinline__ void ln_epilogue(float (&acc)[NCH][VEC], const bool (&fvalid)[NCH],
+                                            const int (&foff)[NCH], const int (&fld)[NCH],
+                                            int C, const float* __restrict__ bias,
+                                            const GatLn& ln, int64_t i, float* __restrict__ y,
+                                            int64_t ldy, int lane) {
+  if (bias != nullptr) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      float b[VEC];
+      ld<VEC>(bias + fld[ch], b);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) acc[ch][q] += b[q];
+    }
+  }
+  if (ln.act == GR_ACT_ELU)
+    gr_ln::ln_relu_store_row<VEC, NCH, GR_ACT_ELU>(acc, fvalid, foff, C, ln.gamma, ln.beta,
+                                                   ln.eps, ln.h + i * C, y + i * ldy,
+                                                   ln.mean + i, ln.rstd + i, lane);
+  else
+    gr_ln::ln_relu_store_row<VEC, NCH, GR_ACT_RELU>(acc, fvalid, foff, C, ln.gamma, ln.beta,
+                                                    ln.eps, ln.h + i * C, y + i * ldy,
+                                                    ln.mean + i, ln.rstd + i, lane);
+}
+
 template <int VEC, int G, int NCH, int U>
 __global__ __launch_bounds__(256) void gat_fwd_fused(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
@@ -426,7 +468,7 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
     const float* __restrict__ d, int C, const float* __restrict__ bias, float* __restrict__ m,
     float* __restrict__ den, float* __restrict__ alpha, float* __restrict__ o,
     float* __restrict__ y, int64_t ldy, float* __restrict__ ws, int64_t ws_stride,
-    int min_len) {
+    int min_len, GatLn ln) {
   constexpr int EPI = 64 / G;
   const int lane = threadIdx.x & 63;
   const int64_t wid = wave_id();
@@ -453,6 +495,17 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
     if (lane == 0) {
       m[i] = 0.f;
       den[i] = 1.f;
+    }
+    if constexpr (G == 64) {
+      if (ln.gamma != nullptr) {
+        float z[NCH][VEC];
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) z[ch][q] = 0.f;
+        ln_epilogue<VEC, NCH>(z, fvalid, foff, fld, C, bias, ln, i, y, ldy, lane);
+        return;
+      }
     }
     if (slot != 0) return;
 #pragma unroll
@@ -583,7 +636,7 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
         eb[q] = eb[q + 1];
       }
       aggregate_chunk(n, k == 0, cl, al);
-      if (ok) alpha[b + lane] = al;
+      if (ok && alpha != nullptr) alpha[b + lane] = al;
     }
   } else {
     // Longer units: statistics in two passes over the logits, the first 64
@@ -622,7 +675,7 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
         al = ok ? expf(v - mx) / dn : 0.f;
       }
       aggregate_chunk(n, first, cl, al);
-      if (ok) alpha[b + lane] = al;
+      if (ok && alpha != nullptr) alpha[b + lane] = al;
     }
   }
 
@@ -641,6 +694,12 @@ __global__ __launch_bounds__(256) void gat_fwd_fused(
     for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
       for (int q = 0; q < VEC; ++q) acc[ch][q] = gr_wave::slot_sum<G>(acc[ch][q]);
+  }
+  if constexpr (G == 64) {
+    if (whole && ln.gamma != nullptr) {
+      ln_epilogue<VEC, NCH>(acc, fvalid, foff, fld, C, bias, ln, i, y, ldy, lane);
+      return;
+    }
   }
   if (slot != 0) return;
   if (whole) {
@@ -714,6 +773,72 @@ __global__ __launch_bounds__(256) void gat_fused_fixup(const int32_t* __restrict
   if (blockIdx.y == 0 && threadIdx.x == 0) {
     m[row] = mx;
     den[row] = dn;
+  }
+}
+
+// Split rows of the forward with the LayerNorm epilogue (GatLn): one
+// workgroup per split row, thread t owning features t, t + 256, ... (C <=
+// 1024).  O as gat_fused_fixup forms it, h = O + bias, the row's statistics
+// by the fixed-order workgroup reduction of the GCN epilogue's fixup, then
+// out = act(LN(h)).
+__global__ __launch_bounds__(256) void gat_fused_fixup_ln(const int32_t* __restrict__ fix,
+                                                          const float* __restrict__ ws,
+                                                          int64_t ws_stride, int C,
+                                                          const float* __restrict__ bias,
+                                                          float* __restrict__ m,
+                                                          float* __restrict__ den, GatLn ln,
+                                                          float* __restrict__ y, int64_t ldy) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int row = fix[3 * r + 0], first = fix[3 * r + 1], n = fix[3 * r + 2];
+  const float* stats = ws + ws_stride - 4;
+  float mx = -FLT_MAX;
+  for (int k = 0; k < n; ++k) mx = fmaxf(mx, stats[(int64_t)(first + k) * ws_stride]);
+  float sum = 0.f;
+  for (int k = 0; k < n; ++k) {
+    const float* st = stats + (int64_t)(first + k) * ws_stride;
+    sum += st[1] * expf(st[0] - mx);
+  }
+  const float dn = sum + 1e-16f;
+  float hv[4];
+  float sacc = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int f = threadIdx.x + q * 256;
+    float a = 0.f;
+    if (f < C) {
+      float acc = 0.f;
+      for (int k = 0; k < n; ++k) {
+        const float* p = ws + (int64_t)(first + k) * ws_stride;
+        acc = fmaf(p[f], expf(p[ws_stride - 4] - mx), acc);
+      }
+      a = acc / dn + (bias != nullptr ? bias[f] : 0.f);
+    }
+    hv[q] = a;
+    sacc += a;
+  }
+  const float mu = gr_ln::block_sum256(sacc, red) / (float)C;
+  float qv = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float dlt = hv[q] - mu;
+    qv += threadIdx.x + q * 256 < C ? dlt * dlt : 0.f;
+  }
+  const float rs = 1.0f / sqrtf(gr_ln::block_sum256(qv, red) / (float)C + ln.eps);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int f = threadIdx.x + q * 256;
+    if (f >= C) continue;
+    const float yv = gr_ln::ln_affine(hv[q], mu, rs, ln.gamma[f], ln.beta[f]);
+    ln.h[(int64_t)row * C + f] = hv[q];
+    y[(int64_t)row * ldy + f] = ln.act == GR_ACT_ELU ? gr_ln::act_fwd<GR_ACT_ELU>(yv)
+                                                     : gr_ln::act_fwd<GR_ACT_RELU>(yv);
+  }
+  if (threadIdx.x == 0) {
+    m[row] = mx;
+    den[row] = dn;
+    ln.mean[row] = mu;
+    ln.rstd[row] = rs;
   }
 }
 
@@ -956,12 +1081,19 @@ __global__ __launch_bounds__(256) void gat_bwd_src_fixup(const int32_t* __restri
 // reduces the rows of att_part in order.  The result does not depend on
 // scheduling.  A split column's share is formed per unit from its partial ds
 // (the sum over its units is the same quantity, re-associated).
+//
+// With rec (not NULL): instead of alpha (through the CSC -> CSR permutation),
+// d and cdot, each edge reads its destination's record rec[i] = (d_i, m_i,
+// den_i, c_i) (one 16-byte load, where the three gathers cost a 128-byte line
+// each) and forms alpha_ij = exp(LeakyReLU(s_j + d_i) - m_i) / den_i, the
+// forward's own expression: for a whole row it gives the forward's bits.
 template <int VEC, int G, int NCH, int U, bool ATT>
 __global__ __launch_bounds__(256) void gat_bwd_src_h1(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
     const int32_t* __restrict__ perm, const float* __restrict__ hs, int64_t ldh,
     const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
     const float* __restrict__ alpha, const float* __restrict__ cdot,
+    const float4* __restrict__ rec,
     const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
     float* __restrict__ gt, float* __restrict__ ws, int min_len,
     const int32_t* __restrict__ src_rows, float* __restrict__ att_part, int64_t waves) {
@@ -1015,9 +1147,17 @@ __global__ __launch_bounds__(256) void gat_bwd_src_h1(
       const int el = b + min(lane, n - 1);
       const int il = row_idx[el];
       const int pl = perm[el];
-      const float al = alpha[pl];
-      const float dl = d[il];
-      const float cl = cdot[il];
+      float al, dl, cl;
+      if (rec != nullptr) {
+        const float4 r = rec[il];
+        dl = r.x;
+        cl = r.w;
+        al = expf(leaky(sj + dl) - r.y) / r.z;
+      } else {
+        al = alpha[pl];
+        dl = d[il];
+        cl = cdot[il];
+      }
       float gtv = 0.f;
       for (int k = 0; k < n; k += EPI * U) {
         int ii[U];
@@ -1253,7 +1393,7 @@ __global__ __launch_bounds__(256) void gat_fwd_rows(
     const bool ok = k + sub < len;
     const float al = ok ? expf(vr[r] - mx) / dn : 0.f;
     gather(k, cr[r], al);
-    if (ok) alpha[w.y + k + sub] = al;
+    if (ok && alpha != nullptr) alpha[w.y + k + sub] = al;
   }
 
   if (!active) return;
@@ -1284,12 +1424,15 @@ __global__ __launch_bounds__(256) void gat_fwd_rows(
 // Writes dHs_j = acc + ds_j att_src and ds_j, as gat_bwd_src_h1 does for a
 // whole column.  Columns of more than max_len edges are left to
 // gat_bwd_src_h1.
+// With rec (not NULL): the destination records instead of alpha, d and
+// cdot, as in gat_bwd_src_h1.
 template <int VEC, int G, int U>
 __global__ __launch_bounds__(256) void gat_bwd_src_rows(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ row_idx,
     const int32_t* __restrict__ perm, const float* __restrict__ hs, int64_t ldh,
     const float* __restrict__ go, const float* __restrict__ s, const float* __restrict__ d,
     const float* __restrict__ alpha, const float* __restrict__ cdot,
+    const float4* __restrict__ rec,
     const float* __restrict__ att_src, int C, float* __restrict__ dhs, float* __restrict__ ds,
     float* __restrict__ gt, int max_len) {
   constexpr int RPW = 64 / G;
@@ -1329,9 +1472,16 @@ __global__ __launch_bounds__(256) void gat_bwd_src_rows(
     if (ok) {
       il = row_idx[w.y + t];
       pl = perm[w.y + t];
-      al = alpha[pl];
-      dl = d[il];
-      cl = cdot[il];
+      if (rec != nullptr) {
+        const float4 r = rec[il];
+        dl = r.x;
+        cl = r.w;
+        al = expf(leaky(sj + dl) - r.y) / r.z;
+      } else {
+        al = alpha[pl];
+        dl = d[il];
+        cl = cdot[il];
+      }
     }
     float gtv = 0.f;
     const int n = min(G, steps - k);
@@ -1729,7 +1879,7 @@ static hipError_t launch_fused(hipStream_t st, const int4* units, int64_t n_unit
                                const int32_t* idx, const float* hs, int64_t ldh, const float* s,
                                const float* d, int C, const float* bias, float* m, float* den,
                                float* alpha, float* o, float* y, int64_t ldy, float* ws,
-                               int64_t ws_stride, int min_len) {
+                               int64_t ws_stride, int min_len, const GatLn& ln) {
   constexpr int EPI = 64 / G;
   // Narrow rows (4 or more edge slots of at most 16 lanes) keep 4 edges a
   // slot in flight: with the unit's logits in registers this measured faster
@@ -1738,7 +1888,7 @@ static hipError_t launch_fused(hipStream_t st, const int4* units, int64_t n_unit
   constexpr int U = (EPI == 1) ? ((NCH == 1) ? 8 : (NCH == 2 ? 4 : 2)) : 4;
   hipLaunchKernelGGL((gat_fwd_fused<VEC, G, NCH, U>), dim3(blocks_for(n_units)), dim3(256), 0,
                      st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, alpha, o, y, ldy,
-                     ws, ws_stride, min_len);
+                     ws, ws_stride, min_len, ln);
   return hipGetLastError();
 }
 
@@ -1747,10 +1897,11 @@ static hipError_t dispatch_fused(int chunks, hipStream_t st, const int4* units, 
                                  const int32_t* idx, const float* hs, int64_t ldh,
                                  const float* s, const float* d, int C, const float* bias,
                                  float* m, float* den, float* alpha, float* o, float* y,
-                                 int64_t ldy, float* ws, int64_t ws_stride, int min_len = 0) {
+                                 int64_t ldy, float* ws, int64_t ws_stride, int min_len = 0,
+                                 const GatLn& ln = GatLn{}) {
 #define GR_FU(G, N)                                                                       \
   return launch_fused<VEC, G, N>(st, units, n_units, idx, hs, ldh, s, d, C, bias, m, den, \
-                                 alpha, o, y, ldy, ws, ws_stride, min_len)
+                                 alpha, o, y, ldy, ws, ws_stride, min_len, ln)
   if (chunks <= 8) GR_FU(8, 1);
   if (chunks <= 16) GR_FU(16, 1);
   if (chunks <= 32) GR_FU(32, 1);
@@ -1793,8 +1944,9 @@ extern "C" int gr_gat_forward(const int32_t* units, int64_t n_units, const int32
              "gat_forward: workspace of %lld floats, %lld needed",
              (long long)ws_floats, (long long)need);
   if (n_units == 0) return GR_OK;
-  GR_REQUIRE(units && aligned16(units) && idx && hs && s && d && m && den && alpha && o,
-             "gat_forward: NULL or misaligned pointer");
+  GR_REQUIRE(units && aligned16(units) && idx && hs && s && d && m && den && o &&
+                 (alpha != nullptr || heads == 1),
+             "gat_forward: NULL or misaligned pointer (alpha may be NULL for one head)");
   hipStream_t st = gr::as_stream(stream);
   if (heads > 1) {
     // Several heads: statistics, then the aggregation.
@@ -1843,6 +1995,7 @@ extern "C" int gr_gat_forward(const int32_t* units, int64_t n_units, const int32
                             o, y, ldy, workspace, ws_stride);
   } else {
     // Unaligned rows wider than 256 floats: statistics, then the aggregation.
+    GR_REQUIRE(alpha != nullptr, "gat_forward: unaligned rows wider than 256 floats need alpha");
     rc = gr_gat_softmax_stats(units, n_units, fixups, n_fix, idx, s, d, 1, m, den, alpha,
                               workspace, n_slots, stream);
     if (rc) return rc;
@@ -1856,8 +2009,61 @@ extern "C" int gr_gat_forward(const int32_t* units, int64_t n_units, const int32
                        dim3(256), 0, st, fixups, workspace, ws_stride, C, bias, m, den, o, y,
                        ldy);
     GR_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(gat_fused_alpha_split, dim3(blocks_for(n_slots)), dim3(256), 0, st, u4,
-                       n_slots, m, den, workspace, ws_stride, alpha);
+    if (alpha != nullptr) {
+      hipLaunchKernelGGL(gat_fused_alpha_split, dim3(blocks_for(n_slots)), dim3(256), 0, st, u4,
+                         n_slots, m, den, workspace, ws_stride, alpha);
+      GR_HIP_CHECK(hipGetLastError());
+    }
+  }
+  return GR_OK;
+}
+
+extern "C" int gr_gat_forward_ln(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                                 int64_t n_fix, const int32_t* idx, const float* hs,
+                                 int64_t ldh, const float* s, const float* d, int64_t n_dst,
+                                 int64_t channels, const float* bias, const float* gamma,
+                                 const float* beta, float eps, int32_t act, float* m, float* den,
+                                 float* h, float* out, int64_t ldo, float* mean, float* rstd,
+                                 float* workspace, int64_t ws_floats, int64_t n_slots,
+                                 void* stream) {
+  gr::clear_error();
+  const int64_t C = channels;
+  GR_REQUIRE(C % 4 == 0 && C > 128 && C <= 1024,
+             "gat_forward_ln: one head of 132..1024 channels, a multiple of 4");
+  GR_REQUIRE(act == GR_ACT_RELU || act == GR_ACT_ELU, "gat_forward_ln: unknown activation %d",
+             (int)act);
+  GR_REQUIRE(n_units >= 0 && n_fix >= 0 && n_slots >= 0 && n_dst >= 0,
+             "gat_forward_ln: negative extent");
+  GR_REQUIRE(ldh >= C && ldh % 4 == 0 && ldo >= C && ldo % 4 == 0,
+             "gat_forward_ln: bad leading dims");
+  const int64_t ws_stride = C + 4;
+  GR_REQUIRE(n_fix == 0 || (fixups && workspace && ws_floats >= n_slots * ws_stride &&
+                            n_slots <= n_units),
+             "gat_forward_ln: workspace of %lld floats, %lld needed", (long long)ws_floats,
+             (long long)(n_slots * ws_stride));
+  if (n_units == 0) return GR_OK;
+  GR_REQUIRE(units && aligned16(units) && idx && hs && aligned16(hs) && s && d && m && den &&
+                 gamma && aligned16(gamma) && beta && aligned16(beta) && h && aligned16(h) &&
+                 out && aligned16(out) && mean && rstd && (bias == nullptr || aligned16(bias)) &&
+                 (workspace == nullptr || aligned16(workspace)),
+             "gat_forward_ln: NULL or misaligned pointer");
+  hipStream_t st = gr::as_stream(stream);
+  GatLn ln;
+  ln.gamma = gamma;
+  ln.beta = beta;
+  ln.eps = eps;
+  ln.act = act;
+  ln.h = h;
+  ln.mean = mean;
+  ln.rstd = rstd;
+  const int4* u4 = reinterpret_cast<const int4*>(units);
+  GR_HIP_CHECK(dispatch_fused<4>((int)(C / 4), st, u4, n_units, idx, hs, ldh, s, d, (int)C, bias,
+                                 m, den, nullptr, nullptr, out, ldo, workspace, ws_stride, 0,
+                                 ln));
+  if (n_fix > 0) {
+    GR_REQUIRE(n_fix <= INT32_MAX, "gat_forward_ln: too many split rows");
+    hipLaunchKernelGGL(gat_fused_fixup_ln, dim3((unsigned)n_fix), dim3(256), 0, st, fixups,
+                       workspace, ws_stride, (int)C, bias, m, den, ln, out, ldo);
     GR_HIP_CHECK(hipGetLastError());
   }
   return GR_OK;
@@ -1907,10 +2113,11 @@ template <int VEC, int G, int NCH>
 static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_units,
                                 const int32_t* row_idx, const int32_t* perm, const float* hs,
                                 int64_t ldh, const float* go, const float* s, const float* d,
-                                const float* alpha, const float* cdot, const float* att_src,
-                                int C, float* dhs, float* ds, float* gt, float* ws, int min_len,
-                                const int32_t* src_rows, float* att_part = nullptr,
-                                int64_t att_rows = 0, int64_t* att_waves = nullptr) {
+                                const float* alpha, const float* cdot, const float4* rec,
+                                const float* att_src, int C, float* dhs, float* ds, float* gt,
+                                float* ws, int min_len, const int32_t* src_rows,
+                                float* att_part = nullptr, int64_t att_rows = 0,
+                                int64_t* att_waves = nullptr) {
   constexpr int EPI = 64 / G;
   // Eight edges a slot in flight measured slower here (0.194 against 0.185 ms
   // for a C5 partition's 20-wide backward): each edge also does a group sum.
@@ -1918,7 +2125,7 @@ static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_uni
   if (att_part == nullptr) {
     hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U, false>), dim3(blocks_for(n_units)),
                        dim3(256), 0, st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha,
-                       cdot, att_src, C, dhs, ds, gt, ws, min_len, src_rows, nullptr,
+                       cdot, rec, att_src, C, dhs, ds, gt, ws, min_len, src_rows, nullptr,
                        (int64_t)0);
     return hipGetLastError();
   }
@@ -1926,7 +2133,7 @@ static hipError_t launch_bwd_h1(hipStream_t st, const int4* units, int64_t n_uni
   *att_waves = waves;
   if (waves <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gat_bwd_src_h1<VEC, G, NCH, U, true>), dim3(blocks_for(waves)), dim3(256),
-                     0, st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot,
+                     0, st, units, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, rec,
                      att_src, C, dhs, ds, gt, ws, min_len, src_rows, att_part, waves);
   return hipGetLastError();
 }
@@ -1936,14 +2143,14 @@ static hipError_t dispatch_bwd_h1(int chunks, hipStream_t st, const int4* units,
                                   int64_t n_units, const int32_t* row_idx, const int32_t* perm,
                                   const float* hs, int64_t ldh, const float* go, const float* s,
                                   const float* d, const float* alpha, const float* cdot,
-                                  const float* att_src, int C, float* dhs, float* ds, float* gt,
-                                  float* ws, int min_len = 0, const int32_t* src_rows = nullptr,
-                                  float* att_part = nullptr, int64_t att_rows = 0,
-                                  int64_t* att_waves = nullptr) {
+                                  const float4* rec, const float* att_src, int C, float* dhs,
+                                  float* ds, float* gt, float* ws, int min_len = 0,
+                                  const int32_t* src_rows = nullptr, float* att_part = nullptr,
+                                  int64_t att_rows = 0, int64_t* att_waves = nullptr) {
 #define GR_BH(G, N)                                                                       \
   return launch_bwd_h1<VEC, G, N>(st, units, n_units, row_idx, perm, hs, ldh, go, s, d,   \
-                                  alpha, cdot, att_src, C, dhs, ds, gt, ws, min_len, src_rows, \
-                                  att_part, att_rows, att_waves)
+                                  alpha, cdot, rec, att_src, C, dhs, ds, gt, ws, min_len,  \
+                                  src_rows, att_part, att_rows, att_waves)
   if (chunks <= 8) GR_BH(8, 1);
   if (chunks <= 16) GR_BH(16, 1);
   if (chunks <= 32) GR_BH(32, 1);
@@ -1980,13 +2187,13 @@ template <int VEC>
 static hipError_t launch_bwd_rows(int chunks, hipStream_t st, const int4* units, int64_t n,
                                   const int32_t* row_idx, const int32_t* perm, const float* hs,
                                   int64_t ldh, const float* go, const float* s, const float* d,
-                                  const float* alpha, const float* cdot, const float* att_src,
-                                  int C, float* dhs, float* ds, float* gt) {
+                                  const float* alpha, const float* cdot, const float4* rec,
+                                  const float* att_src, int C, float* dhs, float* ds, float* gt) {
 #define GR_BR(G)                                                                             \
   hipLaunchKernelGGL((gat_bwd_src_rows<VEC, G, (G < 8 ? G : 8)>),                            \
                      dim3(blocks_for((n + 64 / G - 1) / (64 / G))), dim3(256), 0, st, units, n, \
-                     row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, C, dhs, ds, gt, \
-                     kBwdRowsMaxLen)
+                     row_idx, perm, hs, ldh, go, s, d, alpha, cdot, rec, att_src, C, dhs, ds, \
+                     gt, kBwdRowsMaxLen)
   if (chunks <= 4) GR_BR(4);
   else if (chunks <= 8) GR_BR(8);
   else GR_BR(16);
@@ -1994,22 +2201,23 @@ static hipError_t launch_bwd_rows(int chunks, hipStream_t st, const int4* units,
   return hipGetLastError();
 }
 
-extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const int32_t* fixups,
-                                   int64_t n_fix, const int32_t* row_idx, const int32_t* perm,
-                                   const float* hs, int64_t ldh, const float* go, const float* s,
-                                   const float* d, const float* alpha,
-                                   const float* cdot, const float* att_src, int64_t heads,
-                                   int64_t channels, float* dhs, float* ds, float* gt,
-                                   float* workspace, int64_t n_slots, void* stream) {
-  gr::clear_error();
+// gr_gat_backward_src, with rec (one head) in place of alpha, d and cdot.
+static int backward_src(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                        int64_t n_fix, const int32_t* row_idx, const int32_t* perm,
+                        const float* hs, int64_t ldh, const float* go, const float* s,
+                        const float* d, const float* alpha, const float* cdot, const float4* rec,
+                        const float* att_src, int64_t heads, int64_t channels, float* dhs,
+                        float* ds, float* gt, float* workspace, int64_t n_slots, void* stream) {
   int rc = check_heads(heads, channels);
   if (rc) return rc;
   const int64_t HC = heads * channels;
   GR_REQUIRE(ldh >= HC, "gat_backward_src: ldh < H*C");
   GR_REQUIRE(n_fix == 0 || (fixups && workspace), "gat_backward_src: NULL fixups/workspace");
+  GR_REQUIRE(rec == nullptr || heads == 1, "gat_backward_src: records take one head");
   if (n_units == 0) return GR_OK;
-  GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && go && s && d && alpha &&
-                 cdot && att_src && dhs && ds && gt,
+  GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && go && s &&
+                 (rec != nullptr ? aligned16(rec) : (d && alpha && cdot)) && att_src && dhs &&
+                 ds && gt,
              "gat_backward_src: NULL or misaligned pointer");
   const bool al = aligned16(hs) && aligned16(go) && aligned16(dhs) && aligned16(att_src) &&
                   ldh % 4 == 0 && (workspace == nullptr || aligned16(workspace));
@@ -2020,6 +2228,8 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   const int H = (int)heads, C = (int)channels;
   hipError_t err;
   const int64_t chunks = (HC + vec - 1) / vec;
+  GR_REQUIRE(rec == nullptr || chunks <= 256,
+             "gat_backward_src: records take rows of at most 256 vectors (1024 aligned floats)");
   if (H == 1 && chunks <= 16) {
     // Narrow: split columns and long whole columns one per wavefront
     // (gat_bwd_src_h1), the other whole columns several per wavefront
@@ -2027,28 +2237,28 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
     const int64_t n_split = std::min(n_slots, n_units);
     if (vec == 4)
       err = dispatch_bwd_h1<4>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
-                               alpha, cdot, att_src, C, dhs, ds, gt, workspace,
+                               alpha, cdot, rec, att_src, C, dhs, ds, gt, workspace,
                                kBwdRowsMaxLen + 1);
     else
       err = dispatch_bwd_h1<1>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
-                               alpha, cdot, att_src, C, dhs, ds, gt, workspace,
+                               alpha, cdot, rec, att_src, C, dhs, ds, gt, workspace,
                                kBwdRowsMaxLen + 1);
     GR_HIP_CHECK(err);
     if (n_units > n_split) {
       if (vec == 4)
         err = launch_bwd_rows<4>((int)chunks, st, u4 + n_split, n_units - n_split, row_idx, perm,
-                                 hs, ldh, go, s, d, alpha, cdot, att_src, C, dhs, ds, gt);
+                                 hs, ldh, go, s, d, alpha, cdot, rec, att_src, C, dhs, ds, gt);
       else
         err = launch_bwd_rows<1>((int)chunks, st, u4 + n_split, n_units - n_split, row_idx, perm,
-                                 hs, ldh, go, s, d, alpha, cdot, att_src, C, dhs, ds, gt);
+                                 hs, ldh, go, s, d, alpha, cdot, rec, att_src, C, dhs, ds, gt);
     }
   } else if (H == 1 && chunks <= 256) {
     if (vec == 4)
       err = dispatch_bwd_h1<4>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
-                               alpha, cdot, att_src, C, dhs, ds, gt, workspace);
+                               alpha, cdot, rec, att_src, C, dhs, ds, gt, workspace);
     else
       err = dispatch_bwd_h1<1>((int)chunks, st, u4, n_units, row_idx, perm, hs, ldh, go, s, d,
-                               alpha, cdot, att_src, C, dhs, ds, gt, workspace);
+                               alpha, cdot, rec, att_src, C, dhs, ds, gt, workspace);
   } else if (vec == 4) {
     if (nch == 1) err = launch_gat_bwd<4, 1>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
     else if (nch == 2) err = launch_gat_bwd<4, 2>(st, u4, n_units, row_idx, perm, hs, ldh, go, s, d, alpha, cdot, att_src, H, C, dhs, ds, gt, workspace);
@@ -2069,17 +2279,29 @@ extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const 
   return GR_OK;
 }
 
-extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
-                                        const int32_t* fixups, int64_t n_fix,
-                                        const int32_t* row_idx, const int32_t* perm,
-                                        const float* hs, int64_t ldh, const int32_t* src_rows,
-                                        const float* go, const float* s, const float* d,
-                                        const float* alpha, const float* cdot,
-                                        const float* att_src, int64_t heads, int64_t channels,
-                                        float* dz, float* ds, float* gt, float* workspace,
-                                        int64_t n_slots, float* att_part, int64_t att_rows,
-                                        int64_t* att_waves, void* stream) {
+extern "C" int gr_gat_backward_src(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                                   int64_t n_fix, const int32_t* row_idx, const int32_t* perm,
+                                   const float* hs, int64_t ldh, const float* go, const float* s,
+                                   const float* d, const float* alpha,
+                                   const float* cdot, const float* att_src, int64_t heads,
+                                   int64_t channels, float* dhs, float* ds, float* gt,
+                                   float* workspace, int64_t n_slots, void* stream) {
   gr::clear_error();
+  return backward_src(units, n_units, fixups, n_fix, row_idx, perm, hs, ldh, go, s, d, alpha,
+                      cdot, nullptr, att_src, heads, channels, dhs, ds, gt, workspace, n_slots,
+                      stream);
+}
+
+// gr_gat_backward_src_into, with rec in place of alpha, d and cdot.
+static int backward_src_into(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                             int64_t n_fix, const int32_t* row_idx, const int32_t* perm,
+                             const float* hs, int64_t ldh, const int32_t* src_rows,
+                             const float* go, const float* s, const float* d,
+                             const float* alpha, const float* cdot, const float4* rec,
+                             const float* att_src, int64_t heads, int64_t channels, float* dz,
+                             float* ds, float* gt, float* workspace, int64_t n_slots,
+                             float* att_part, int64_t att_rows, int64_t* att_waves,
+                             void* stream) {
   int rc = check_heads(heads, channels);
   if (rc) return rc;
   const int64_t C = channels;
@@ -2094,15 +2316,16 @@ extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
   if (att_waves != nullptr) *att_waves = 0;
   if (n_units == 0) return GR_OK;
   GR_REQUIRE(units && aligned16(units) && row_idx && perm && hs && aligned16(hs) && src_rows &&
-                 go && aligned16(go) && s && d && alpha && cdot && att_src &&
+                 go && aligned16(go) && s &&
+                 (rec != nullptr ? aligned16(rec) : (d && alpha && cdot)) && att_src &&
                  aligned16(att_src) && dz && aligned16(dz) && ds && gt &&
                  (workspace == nullptr || aligned16(workspace)),
              "gat_backward_src_into: NULL or misaligned pointer");
   hipStream_t st = gr::as_stream(stream);
   const int4* u4 = reinterpret_cast<const int4*>(units);
   const hipError_t err = dispatch_bwd_h1<4>((int)(C / 4), st, u4, n_units, row_idx, perm, hs,
-                                            ldh, go, s, d, alpha, cdot, att_src, (int)C, dz, ds,
-                                            gt, workspace, 0, src_rows, att_part, att_rows,
+                                            ldh, go, s, d, alpha, cdot, rec, att_src, (int)C, dz,
+                                            ds, gt, workspace, 0, src_rows, att_part, att_rows,
                                             att_waves);
   GR_REQUIRE(att_part == nullptr || *att_waves > 0,
              "gat_backward_src_into: occupancy query for the attention partials failed");
@@ -2112,6 +2335,72 @@ extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
                        n_fix, workspace, 1, (int)C, att_src, dz, ds, src_rows);
     GR_HIP_CHECK(hipGetLastError());
   }
+  return GR_OK;
+}
+
+extern "C" int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
+                                        const int32_t* fixups, int64_t n_fix,
+                                        const int32_t* row_idx, const int32_t* perm,
+                                        const float* hs, int64_t ldh, const int32_t* src_rows,
+                                        const float* go, const float* s, const float* d,
+                                        const float* alpha, const float* cdot,
+                                        const float* att_src, int64_t heads, int64_t channels,
+                                        float* dz, float* ds, float* gt, float* workspace,
+                                        int64_t n_slots, float* att_part, int64_t att_rows,
+                                        int64_t* att_waves, void* stream) {
+  gr::clear_error();
+  return backward_src_into(units, n_units, fixups, n_fix, row_idx, perm, hs, ldh, src_rows, go,
+                           s, d, alpha, cdot, nullptr, att_src, heads, channels, dz, ds, gt,
+                           workspace, n_slots, att_part, att_rows, att_waves, stream);
+}
+
+extern "C" int gr_gat_backward_src_h1(const int32_t* units, int64_t n_units,
+                                      const int32_t* fixups, int64_t n_fix,
+                                      const int32_t* row_idx, const int32_t* perm,
+                                      const float* hs, int64_t ldh, const int32_t* src_rows,
+                                      const float* go, const float* s, const float* rec,
+                                      const float* att_src, int64_t channels, float* dhs,
+                                      float* ds, float* gt, float* workspace, int64_t n_slots,
+                                      float* att_part, int64_t att_rows, int64_t* att_waves,
+                                      void* stream) {
+  gr::clear_error();
+  const float4* r = reinterpret_cast<const float4*>(rec);
+  GR_REQUIRE(n_units == 0 || rec != nullptr, "gat_backward_src_h1: NULL rec");
+  if (src_rows == nullptr) {
+    GR_REQUIRE(att_part == nullptr, "gat_backward_src_h1: att_part needs src_rows");
+    return backward_src(units, n_units, fixups, n_fix, row_idx, perm, hs, ldh, go, s, nullptr,
+                        nullptr, nullptr, r, att_src, 1, channels, dhs, ds, gt, workspace,
+                        n_slots, stream);
+  }
+  return backward_src_into(units, n_units, fixups, n_fix, row_idx, perm, hs, ldh, src_rows, go,
+                           s, nullptr, nullptr, nullptr, r, att_src, 1, channels, dhs, ds, gt,
+                           workspace, n_slots, att_part, att_rows, att_waves, stream);
+}
+
+namespace gr_gat {
+
+__global__ __launch_bounds__(256) void gat_record_kernel(const float* __restrict__ d,
+                                                         const float* __restrict__ m,
+                                                         const float* __restrict__ den,
+                                                         const float* __restrict__ cdot,
+                                                         int64_t n, float4* __restrict__ rec) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) rec[i] = make_float4(d[i], m[i], den[i], cdot[i]);
+}
+
+}  // namespace gr_gat
+
+extern "C" int gr_gat_dst_record(const float* d, const float* m, const float* den,
+                                 const float* cdot, int64_t n_dst, float* rec, void* stream) {
+  gr::clear_error();
+  GR_REQUIRE(n_dst >= 0, "gat_dst_record: negative extent");
+  if (n_dst == 0) return GR_OK;
+  GR_REQUIRE(d && m && den && cdot && rec && aligned16(rec),
+             "gat_dst_record: NULL or misaligned pointer");
+  hipLaunchKernelGGL(gat_record_kernel, dim3((unsigned)((n_dst + 255) / 256)), dim3(256), 0,
+                     gr::as_stream(stream), d, m, den, cdot, n_dst,
+                     reinterpret_cast<float4*>(rec));
+  GR_HIP_CHECK(hipGetLastError());
   return GR_OK;
 }
 

@@ -85,12 +85,17 @@ int fifo_pop_wait(EventFifo& f) {
 // ------------------------------------------------------- pinned staging --
 
 // A small ring of pinned host slots.  A slot is reused only after the event
-// recorded behind its last consumer has completed.
+// recorded behind its last consumer has completed.  Slots are only ever
+// filled or drained by the host and copied by hipMemcpyAsync (never read by
+// a kernel through a mapped pointer), so when the driver refuses pinned
+// memory (a cap that the host partitions may have used up) a slot falls
+// back to pageable memory: the copies then run at pageable speed, but run.
 struct Staging {
   std::mutex m;
   struct Slot {
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool pageable = false;  // ptr from std::malloc, not hipHostMalloc
     hipEvent_t done = nullptr;
     bool busy = false;
     void* dev = nullptr;  // device twin (address tables), on device `dev_id`
@@ -126,11 +131,21 @@ int staging_acquire(size_t bytes, void** out, int* slot_id) {
     GR_HIP_CHECK(hipEventSynchronize(sl.done));
   }
   if (sl.bytes < bytes) {
-    if (sl.ptr != nullptr) GR_HIP_CHECK(hipHostFree(sl.ptr));
+    if (sl.ptr != nullptr) {
+      if (sl.pageable)
+        std::free(sl.ptr);
+      else
+        GR_HIP_CHECK(hipHostFree(sl.ptr));
+    }
     sl.ptr = nullptr;
     sl.bytes = 0;
     size_t want = std::max<size_t>(bytes, size_t(1) << 20);
-    GR_HIP_CHECK(hipHostMalloc(&sl.ptr, want, hipHostMallocDefault));
+    sl.pageable = hipHostMalloc(&sl.ptr, want, hipHostMallocDefault) != hipSuccess;
+    if (sl.pageable) {
+      (void)hipGetLastError();  // the refusal is handled here, not reported later
+      sl.ptr = std::malloc(want);
+      GR_REQUIRE(sl.ptr != nullptr, "staging: cannot allocate %zu host bytes", want);
+    }
     sl.bytes = want;
   }
   if (sl.done == nullptr) GR_HIP_CHECK(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming));
@@ -612,11 +627,32 @@ extern "C" int gr_scatter_partitions(int32_t pid, int32_t num_parts, const float
   return fifo_push(d2h_fifo(), s);
 }
 
+namespace {
+
+// Gives every staging slot a pinned chunk of kChunkBytes, once, before the
+// first host partition is pinned: partitions may use up the driver's pinned
+// cap, and the slots would then run from pageable memory.  Best effort.
+void reserve_staging() {
+  static std::once_flag once;
+  std::call_once(once, [] {
+    void* p[4] = {};
+    int ids[4] = {-1, -1, -1, -1};
+    for (int k = 0; k < 4; ++k)
+      if (staging_acquire((size_t)kChunkBytes, &p[k], &ids[k]) != GR_OK) ids[k] = -1;
+    for (int k = 0; k < 4; ++k)
+      if (ids[k] >= 0) (void)staging_release(ids[k], nullptr);
+    gr::clear_error();
+  });
+}
+
+}  // namespace
+
 extern "C" int gr_host_alloc(int64_t nbytes, void** out) {
   gr::clear_error();
   GR_REQUIRE(out != nullptr && nbytes >= 0, "host_alloc: bad arguments");
   *out = nullptr;
   if (nbytes == 0) return GR_OK;
+  reserve_staging();
   hipError_t e = hipHostMalloc(out, (size_t)nbytes, hipHostMallocDefault);
   if (e != hipSuccess) {
     (void)hipGetLastError();

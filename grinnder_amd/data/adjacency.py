@@ -22,6 +22,10 @@ from grinnder_amd import _lib
 # partial sums are combined by an ordered fixup pass.
 DEFAULT_SEG_LEN = 512
 
+# Whole rows longer than this run one per wavefront in the narrow attention
+# kernels (gat_narrow.hip's kRowsMax); shorter ones eight to a wavefront.
+LONG_ROW = 32
+
 
 @dataclass
 class Plan:
@@ -33,6 +37,10 @@ class Plan:
     n_units: int
     n_fix: int
     n_slots: int
+    # int32 [n_long] on device: the units that are split or longer than
+    # LONG_ROW edges, in plan order (the one-per-wavefront kernels' work).
+    long_units: Optional[Tensor] = None
+    n_long: int = 0
 
 
 @dataclass
@@ -76,8 +84,11 @@ def build_plan(rowptr: Tensor, rows: int, seg_len: int, device,
     units = torch.empty((max(nu, 1), 4), dtype=torch.int32)
     fixups = torch.empty((max(nf, 1), 3), dtype=torch.int32)
     plan(units.data_ptr(), fixups.data_ptr())
-    return Plan(rows=rows, units=units[:nu].to(device), fixups=fixups[:nf].to(device),
-                n_units=nu, n_fix=nf, n_slots=ns)
+    u = units[:nu]
+    long_units = torch.nonzero((u[:, 3] >= 0) | (u[:, 2] - u[:, 1] > LONG_ROW)).flatten()
+    return Plan(rows=rows, units=u.to(device), fixups=fixups[:nf].to(device),
+                n_units=nu, n_fix=nf, n_slots=ns,
+                long_units=long_units.to(torch.int32).to(device), n_long=long_units.numel())
 
 
 def build_device_plan(rowptr: Tensor, col: Tensor, value: Optional[Tensor],

@@ -18,10 +18,11 @@ import torch.nn.functional as F
 from torch import Tensor
 from torch.nn import Linear, Module, Parameter
 
-from grinnder_amd.aggregation import (gat_attention, gat_scores, gcn_aggregate,
+from grinnder_amd.aggregation import (RowDotSink, gat_attention, gat_attention_ln,
+                                      gat_attention_ln_ok, gat_scores, gcn_aggregate,
                                       gcn_linear_aggregate)
 from grinnder_amd.data.adjacency import Adjacency
-from grinnder_amd.dense import linear
+from grinnder_amd.dense import bias_ln_act, linear
 
 
 def glorot_(t: Tensor) -> Tensor:
@@ -196,6 +197,32 @@ class GATConv(Module):
             return y[:, :self.out_channels]
         return gat_attention(hs, adj, self.att_src, self.att_dst, bias, self.heads,
                              self.out_channels, self.concat, scores, rowdot_sink, sink)
+
+    def attend_ln(self, hs: Tensor, adj: Adjacency, norm, act: str = "elu",
+                  scores: Optional[Tuple[Tensor, Tensor]] = None, sink=None,
+                  dest=None) -> Tensor:
+        """act(norm(attend(hs) + bias)): the layer, its bias and the LayerNorm
+        and activation that follow it in GAT.forward_layer
+        (grinnder/nn/gat.py:74-78).  One head of 132..1024 channels runs it as
+        one pass per row (gat_attention_ln: the epilogue in the attention
+        kernel); otherwise the attention and then bias_ln_act, which hands
+        the attention's backward c_i.  `dest`: as bias_ln_act."""
+        if self._padded() == 0 and gat_attention_ln_ok(hs, self.heads, self.out_channels,
+                                                        norm.weight):
+            return gat_attention_ln(hs, adj, self.att_src, self.att_dst, self.bias,
+                                    norm.weight, norm.bias, norm.eps, act, scores, sink, dest)
+        dot = RowDotSink()
+        x = self.attend(hs, adj, add_bias=False, scores=scores, rowdot_sink=dot, sink=sink)
+        return bias_ln_act(x, self.bias, norm.weight, norm.bias, norm.eps, act, dot, dest=dest)
+
+    def project(self, x_src: Tensor, reuse: Optional[Tensor] = None,
+                keep: Optional[list] = None) -> Tensor:
+        """hs = lin(x_src) for a head width that needs no padding, as forward
+        forms it (with reuse / keep)."""
+        hs = linear(x_src, self.lin.weight, reuse=reuse)
+        if keep is not None:
+            keep.append(hs.detach())
+        return hs
 
     def scores(self, hs: Tensor) -> Tuple[Tensor, Tensor]:
         """The logit halves (s, d) of every row of hs, as attend forms them

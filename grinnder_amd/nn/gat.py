@@ -69,6 +69,9 @@ class GAT(GriNNderModel):
         conv = self.convs[layer]
         if self._fused_norm(layer, x):
             norm = self.norms[layer]
+            if conv._padded() == 0:
+                hs = conv.project(x, reuse=reuse, keep=keep)
+                return conv.attend_ln(hs, adj, norm)
             sink = RowDotSink()
             x = conv((x, x[:num_dst]), adj, add_bias=False, reuse=reuse, keep=keep,
                      rowdot_sink=sink)
@@ -111,11 +114,8 @@ class GAT(GriNNderModel):
             raise ValueError(f"layer {layer} reads gathered rows; it takes no sink")
         conv = self.convs[layer]
         if self._fused_norm(layer, hs):
-            norm = self.norms[layer]
-            dot = RowDotSink()
-            x = conv.attend(hs, adj, add_bias=False, scores=scores, rowdot_sink=dot, sink=sink)
-            return bias_ln_act(x, conv.bias, norm.weight, norm.bias, norm.eps, "elu", dot,
-                               dest=dest)
+            return conv.attend_ln(hs, adj, self.norms[layer], scores=scores, sink=sink,
+                                  dest=dest)
         return self._finish(layer, conv.attend(hs, adj, scores=scores, sink=sink))
 
     def projected_scores(self, layer: int, z: Tensor):

@@ -488,6 +488,8 @@ int gr_gat_aggregate(const int32_t* units, int64_t n_units,
  * two.  units / fixups as gr_spmm_plan lays them out (split rows' units first,
  * unit k holding slot k).
  * workspace: ws_floats >= n_slots * (round_up(H*C, 4) + round_up(2H, 4)).
+ * alpha may be NULL with one head (rows of at most 256 vectors): it is then
+ * not stored (gr_gat_backward_src_h1 recomputes it).
  * Replaces the attention / softmax / propagate sequence of PyG GATConv as
  * grinnder/nn/gat.py:54-61,73 calls it. */
 int gr_gat_forward(const int32_t* units, int64_t n_units, const int32_t* fixups,
@@ -496,6 +498,23 @@ int gr_gat_forward(const int32_t* units, int64_t n_units, const int32_t* fixups,
                    int64_t channels, const float* bias, float* m, float* den,
                    float* alpha, float* o, float* y, int64_t ldy, float* workspace,
                    int64_t ws_floats, int64_t n_slots, void* stream);
+
+/* One head of C channels (a multiple of 4 in 132..1024): gr_gat_forward with
+ * the GAT model's epilogue after the conv (bias, LayerNorm(gamma, beta,
+ * eps) and act = GR_ACT_ELU or GR_ACT_RELU; grinnder/nn/gat.py:74-78) in the
+ * same pass: each row writes h = O + bias [n_dst, C], out = act(LN(h)) (row
+ * stride ldo), mean and rstd [n_dst], and m, den as gr_gat_forward; neither
+ * O nor alpha.  The row statistics and output are formed as gr_bias_ln_act
+ * forms them from the same h (bit for bit for whole rows).
+ * workspace: n_slots * (C + 4) floats.  No counterpart in the reference: it
+ * fuses the conv and the LayerNorm that follows it. */
+int gr_gat_forward_ln(const int32_t* units, int64_t n_units, const int32_t* fixups,
+                      int64_t n_fix, const int32_t* idx, const float* hs, int64_t ldh,
+                      const float* s, const float* d, int64_t n_dst, int64_t channels,
+                      const float* bias, const float* gamma, const float* beta, float eps,
+                      int32_t act, float* m, float* den, float* h, float* out, int64_t ldo,
+                      float* mean, float* rstd, float* workspace, int64_t ws_floats,
+                      int64_t n_slots, void* stream);
 
 /* Backward over source rows j (CSC plan, row_idx/perm from
  * gr_csr_transpose; alpha [nnz, H] in CSR order from gr_gat_softmax_stats).
@@ -540,6 +559,85 @@ int gr_gat_backward_src_into(const int32_t* units, int64_t n_units,
                              float* dz, float* ds, float* gt, float* workspace,
                              int64_t n_slots, float* att_part, int64_t att_rows,
                              int64_t* att_waves, void* stream);
+
+/* One head: the destination records rec[i] = (d_i, m_i, den_i, cdot_i),
+ * [n_dst, 4] floats (16-byte aligned), from the forward's logit half d, row
+ * max m and denominator den and the backward's cdot, for
+ * gr_gat_backward_src_h1.  No counterpart in the reference: it packs what
+ * PyG GATConv's autograd keeps per destination row into one 16-byte load. */
+int gr_gat_dst_record(const float* d, const float* m, const float* den,
+                      const float* cdot, int64_t n_dst, float* rec, void* stream);
+
+/* gr_gat_backward_src (src_rows NULL: dhs [E, C] written) or
+ * gr_gat_backward_src_into (src_rows given: dHs added into dhs = dz, with
+ * the optional att_part partial sums) for one head, with the destination
+ * records of gr_gat_dst_record in place of alpha, d and cdot: each edge
+ * recomputes alpha_ij = exp(LeakyReLU(s_j + d_i) - m_i) / den_i (for a whole
+ * row the forward's own value), so gr_gat_forward may run with alpha NULL.
+ * The same outputs (ds, gt, workspace) as those entries; C at most 1024
+ * (at most 256 when the rows are not 16-byte aligned).  Replaces the same
+ * PyG GATConv backward (grinnder/nn/gat.py:54-61,73). */
+int gr_gat_backward_src_h1(const int32_t* units, int64_t n_units,
+                           const int32_t* fixups, int64_t n_fix,
+                           const int32_t* row_idx, const int32_t* perm,
+                           const float* hs, int64_t ldh, const int32_t* src_rows,
+                           const float* go, const float* s, const float* rec,
+                           const float* att_src, int64_t channels, float* dhs,
+                           float* ds, float* gt, float* workspace, int64_t n_slots,
+                           float* att_part, int64_t att_rows, int64_t* att_waves,
+                           void* stream);
+
+/* Narrow one-head attention (C channels, a multiple of 4 up to 24): the
+ * forward of gr_gat_forward (PyG GATConv as grinnder/nn/gat.py:54-61,69-78
+ * calls it) with every edge reading one 128-byte packed line.
+ *   zx [n_src, 32]: written; source row j packed as [Hs_j (C) | 0 .. |
+ *     24: s_j, 25: d_j (j < n_dst) | 0 ..], s and d taken from s_pre / d_pre
+ *     when given (both or neither), else formed from att_src / att_dst as
+ *     gr_gat_scores forms them.
+ *   o [n_dst, C] = O; y (optional, row stride ldy) = O + bias (bias optional).
+ *   f_state [n_dst, 32]: written; [N_i (C) | 0 .. | 24: m_i, 25: den_i,
+ *     26: S_i | 0 ..] with N_i = sum_{t_ij <= 0} alpha_ij Hs_j and
+ *     S_i = sum_{t_ij <= 0} alpha_ij, what gr_gat_narrow_backward needs
+ *     instead of alpha (which is not formed).
+ *   long_units (optional, device int32 [n_long]): indices of the plan units
+ *     that are split or longer than 32 edges (run one per wavefront); NULL:
+ *     every unit is examined.  workspace: n_slots * 52 floats.
+ * The softmax runs online (one pass; the running max rescales the sums), so
+ * results equal gr_gat_forward's to rounding, not bit for bit.  No
+ * counterpart in the reference beyond the GATConv it replaces. */
+int gr_gat_narrow_forward(const int32_t* units, int64_t n_units,
+                          const int32_t* fixups, int64_t n_fix,
+                          const int32_t* long_units, int64_t n_long,
+                          const int32_t* idx, const float* hs, int64_t ldh,
+                          int64_t n_src, int64_t n_dst, int64_t channels,
+                          const float* s_pre, const float* d_pre,
+                          const float* att_src, const float* att_dst,
+                          const float* bias, float* zx, float* o, float* y,
+                          int64_t ldy, float* f_state, float* workspace,
+                          int64_t ws_floats, int64_t n_slots, void* stream);
+
+/* Backward of gr_gat_narrow_forward over the CSC plan (units / fixups /
+ * long_units of the transposed adjacency, row_idx from gr_csr_transpose):
+ *   first, per destination row, c_i = <go_i, O_i> and
+ *     dd_i = -0.8 (<go_i, N_i> - c_i S_i) + c_i 1e-16 / den_i (= sum_j g_t,ij:
+ *     sum_j g_e,ij is exactly c_i 1e-16 / den_i), written to dd [n_dst], and
+ *     gx [n_dst, 32] = [go_i (C) | 0 .. | 24: d_i, 25: m_i, 26: 1 / den_i,
+ *     27: c_i, 28: dd_i | 0 ..];
+ *   then, per source column j, with alpha_ij recomputed from s_j and gx_i,
+ *     dhs [n_src, C] = sum_i alpha_ij go_i + ds_j att_src
+ *                      + (j < n_dst) dd_j att_dst,
+ *     ds [n_src] = sum_i g_t,ij.
+ * go: row stride ldg (a multiple of 4).  workspace: n_slots * 28 floats.
+ * Replaces the backward of the same PyG GATConv. */
+int gr_gat_narrow_backward(const int32_t* units, int64_t n_units,
+                           const int32_t* fixups, int64_t n_fix,
+                           const int32_t* long_units, int64_t n_long,
+                           const int32_t* row_idx, const float* zx, int64_t n_src,
+                           int64_t n_dst, int64_t channels, const float* go,
+                           int64_t ldg, const float* o, const float* f_state,
+                           const float* att_src, const float* att_dst, float* gx,
+                           float* dhs, float* ds, float* dd, float* workspace,
+                           int64_t ws_floats, int64_t n_slots, void* stream);
 
 /* Backward over destination rows i (CSR plan):
  * dd[i,h] = sum_e gt[e,h] + cdot[i,h] * 1e-16 / den[i,h] (= sum_j g_t,ij) and

@@ -572,6 +572,17 @@ def _default_vs_reference_flow(graph, make, label):
     return state, la
 
 
+def _spmm_by_columns(a, z):
+    """torch.sparse.mm(a, z) in column blocks of fewer than 2^31 elements
+    (the library's dense operands are indexed with 32 bits: at 10M rows a
+    256-wide product overflows)."""
+    cols = max(1, ((1 << 31) - 1) // max(1, z.size(0)))
+    if cols >= z.size(1):
+        return torch.sparse.mm(a, z)
+    return torch.cat([torch.sparse.mm(a, z[:, c:c + cols].contiguous())
+                      for c in range(0, z.size(1), cols)], dim=1)
+
+
 def gcn_loss_float64(graph, state, make, device):
     """The loss of one full-graph step of the reference GCN in float64 on the
     partitioned graph's whole adjacency (every partition's rows with their
@@ -593,10 +604,10 @@ def gcn_loss_float64(graph, state, make, device):
             x = graph.features.partition(lo, hi).to(device).double()
             z[lo:hi] = x @ w0t
             del x
-        h = torch.relu(norms[0](torch.sparse.mm(a, z) + convs[0].bias))
+        h = torch.relu(norms[0](_spmm_by_columns(a, z) + convs[0].bias))
         del z
         for i in range(1, len(convs)):
-            h = torch.sparse.mm(a, h @ convs[i].lin.weight.t()) + convs[i].bias
+            h = _spmm_by_columns(a, h @ convs[i].lin.weight.t()) + convs[i].bias
             if i < len(convs) - 1:
                 h = torch.relu(norms[i](h))
         tr = graph.train_mask.to(device)

@@ -31,6 +31,10 @@ CASES = [
     (700, 800, 30, 2, 1, 20, True),
     (600, 600, 16, 1, 1, 12, True),
     (650, 700, 31, 1, 1, 13, True),
+    # packed-line kernels (one head, a multiple of 4 up to 24 channels) at
+    # their widest and narrowest
+    (800, 800, 9, 2, 1, 24, True),
+    (500, 700, 6, 1, 1, 4, True),
 ]
 
 
@@ -291,3 +295,50 @@ def test_gat_attention_in_place_matches_gathered(gpu, C, big):
     back = oracle.gat_backward(rowptr, col, hs64, 1, C, att_s.cpu(), att_d.cpu(), True, alpha,
                                tpre, gy.cpu())
     assert max_abs_norm_err(as1.view(-1), torch.as_tensor(back[1]).view(-1)) <= TOL
+
+
+@pytest.mark.parametrize("C,square", [(20, True), (20, False), (24, True), (8, False)])
+def test_gat_narrow_path_runs_and_matches_oracle_with_scores(gpu, C, square, monkeypatch):
+    """One head of C <= 24 channels (a multiple of 4) runs the packed-line
+    kernels (gr_gat_narrow_forward / _backward), not the general ones, with
+    the logit halves formed inside or given (as the projected flow gives
+    them, gat_scores over all rows): both give the same bits, and match the
+    oracle, including split rows and columns (hub rows of 1500 edges at a
+    256-edge segment) and rows past the destinations (E > B)."""
+    from grinnder_amd import _lib
+    from grinnder_amd.aggregation import gat_scores
+
+    B, E = (900, 900) if square else (700, 1000)
+    rowptr, col, val = random_bipartite(B, E, 10, seed=C + int(square), long_rows=3,
+                                        long_len=1500)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=256)
+    g = torch.Generator().manual_seed(C)
+    hs = torch.randn(E, C, generator=g)
+    a_s = torch.randn(1, 1, C, generator=g) * 0.5
+    a_d = torch.randn(1, 1, C, generator=g) * 0.5
+    b = torch.randn(C, generator=g)
+    gy = torch.randn(B, C, generator=g)
+    called = []
+    real = _lib.call
+    monkeypatch.setattr(_lib, "call", lambda name, *a: (called.append(name), real(name, *a))[1])
+    results = []
+    for given in (False, True):
+        leaves = [t.to(gpu).requires_grad_(True) for t in (hs, a_s, a_d, b)]
+        scores = None
+        if given:
+            scores = gat_scores(leaves[0].detach(), leaves[1], leaves[2], 1, C, B)
+        out = gat_attention(leaves[0], adj, leaves[1], leaves[2], leaves[3], 1, C, True,
+                            scores=scores)
+        out.backward(gy.to(gpu))
+        torch.cuda.synchronize()
+        results.append([out.detach()] + [t.grad for t in leaves])
+    assert "gr_gat_narrow_forward" in called and "gr_gat_narrow_backward" in called
+    assert "gr_gat_forward" not in called
+    for a, c in zip(results[0], results[1]):
+        assert torch.equal(a, c)
+    ref_o, alpha, tpre = oracle.gat_forward(rowptr, col, hs, 1, C, a_s, a_d, b, True)
+    refs = oracle.gat_backward(rowptr, col, hs, 1, C, a_s, a_d, True, alpha, tpre, gy)
+    got = results[0]
+    assert max_abs_norm_err(got[0], ref_o) <= TOL
+    for t, r in zip(got[1:], refs):
+        assert max_abs_norm_err(t.reshape(-1), torch.as_tensor(r).reshape(-1)) <= TOL

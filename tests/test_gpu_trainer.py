@@ -477,12 +477,20 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     (tests/restate.py):
 
     - the loss of each flow is within 1e-5 of float64, and the two flows'
-      losses and every gradient agree within 1e-5 (grad_errs);
+      losses agree within 1e-5;
     - every gradient of each flow is within 1e-5 of float64, or no further
       from it than 1.5x the distance of the reference's own fp32 arithmetic
       (the same restatement in float32: torch sparse / index ops and torch
       GEMMs) - each weight gradient sums ~180k training rows' contributions
       that cancel, which no fp32 arithmetic resolves to 1e-5;
+    - the two flows' gradients agree within 1e-5 (grad_errs), or, where
+      both are that far from float64, within twice the fp32 restatement's
+      distance (each is within 1.5x of it).  That case is the first GCN
+      layer with its inputs uploaded again for dW: the reference flow's
+      GCNConv aggregates the 128-wide input first ((A X) Wᵀ) while the
+      default flow projects first (A (X Wᵀ)), so the two weight gradients
+      sum the same terms in another order (both ~6-9e-5 from float64, as
+      torch's fp32 is 6.3e-5);
     - two projected epochs give bit-identical gradients."""
     from grinnder_amd.data import synthetic
     from tests.restate import model_epoch
@@ -535,7 +543,8 @@ def test_projected_layers_match_gathered_at_scale(gpu, model_kind, resident, mon
     flows = grad_errs(g1, g0)
     print(f"{model_kind} 300k auto vs off: {({k: f'{v:.1e}' for k, v in flows.items()})}",
           flush=True)
-    assert max(flows.values()) <= TOL, flows
+    for k, e in flows.items():
+        assert e <= max(TOL, 2.0 * t32_err[k]), (k, e, t32_err[k])
     assert all(torch.equal(g1[k], g2[k]) for k in g1)
 
 
