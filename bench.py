@@ -409,6 +409,31 @@ def locality_free_control(num_nodes: int, nnz: int, dim: int, device: str,
     out["algorithmic_GBps"] = round(tot_b / tot_ms / 1e6, 1)
     out["frac"] = round(tot_b / tot_ms / 1e6 / HBM_PEAK_GBPS, 4)
     adj.release_device()
+    del plan, z, gy
+    # The same box's random-row ceiling: gr_gather_rows of 2^23 rows of `dim`
+    # floats along a random permutation (8 GiB at dim 256, far beyond the
+    # caches), bytes read (rows and indices) and written over its time.
+    from grinnder_amd.aggregation import gather_rows
+
+    n = 1 << 23
+    gen = torch.Generator(device=device).manual_seed(0)
+    x = torch.empty(n, dim, device=device).normal_(generator=gen)
+    rows = torch.randperm(n, device=device, generator=gen)
+    gather_rows(x, rows)
+    times = []
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        y = gather_rows(x, rows)
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+        del y
+    gb = (2 * n * dim * 4 + n * 8) / min(times) / 1e6
+    out["random_row_gather_GBps"] = round(gb, 1)
+    out["frac_of_random_gather"] = round(out["algorithmic_GBps"] / gb, 4)
+    del x, rows
+    torch.cuda.empty_cache()
     return out
 
 

@@ -21,6 +21,7 @@ from grinnder_amd.aggregation import (KernelTimer, LNProductSink, ProjectedSink,
                                       gather_rows, scatter_add_rows)
 from grinnder_amd.dense import OutputRows, gemm_nt, gemm_tn
 from grinnder_amd.loss import masked_cross_entropy
+from grinnder_amd.utils import get_available_host_memory
 
 
 class _GatherRows(torch.autograd.Function):
@@ -298,7 +299,13 @@ class ProjectedLayers:
                 need = 24 * nnz_all + 32 * n
                 if free is None:
                     free = self._free_device_memory()
-                if need + (8 << 30) <= free:
+                # Host side: the whole adjacency keeps int64 row pointers and
+                # column ids and fp32 values (20 bytes an edge) for the
+                # graph's lifetime, and building its device plan briefly
+                # needs about as much again for the transpose.
+                host_need = 48 * nnz_all + 32 * n
+                if (need + (8 << 30) <= free
+                        and host_need + (4 << 30) <= get_available_host_memory()):
                     free -= need
                     self._merge_room = True
         # A second copy of layer 0's input rows for the next epoch's upload to

@@ -583,6 +583,15 @@ def _spmm_by_columns(a, z):
                       for c in range(0, z.size(1), cols)], dim=1)
 
 
+def _bias_ln_relu_by_rows(h, bias, norm, rows=1 << 20):
+    """h = ReLU(norm(h + bias)) in place, a block of rows at a time: torch's
+    LayerNorm kernel indexes its input with 32 bits, and [10M, 256] has more
+    than 2^31 elements."""
+    for lo in range(0, h.size(0), rows):
+        blk = h[lo:lo + rows]
+        blk.copy_(torch.relu(norm(blk + bias)))
+
+
 def gcn_loss_float64(graph, state, make, device):
     """The loss of one full-graph step of the reference GCN in float64 on the
     partitioned graph's whole adjacency (every partition's rows with their
@@ -591,8 +600,14 @@ def gcn_loss_float64(graph, state, make, device):
     generated features, so the 41 GB input never sits in memory whole."""
     n = graph.num_nodes
     w = graph.whole_adjacency()
-    a = torch.sparse_csr_tensor(w.rowptr.to(device), w.col.to(device),
-                                w.value.to(torch.float64).to(device), (n, n))
+    # Through a coalesced COO tensor: the library's CSR product expects the
+    # columns of a row sorted, and the pipeline keeps argsort's order.
+    rp = w.rowptr.to(device)
+    rows = torch.repeat_interleave(torch.arange(n, device=device), rp[1:] - rp[:-1])
+    a = torch.sparse_coo_tensor(torch.stack([rows, w.col.to(device)]),
+                                w.value.to(torch.float64).to(device), (n, n)).coalesce()
+    a = a.to_sparse_csr()
+    del rows, rp
     model = make().to(torch.float64).to(device)
     model.load_state_dict({k: v.to(torch.float64) for k, v in state.items()})
     convs, norms = model.convs, model.norms
@@ -601,15 +616,18 @@ def gcn_loss_float64(graph, state, make, device):
         w0t = convs[0].lin.weight.t()
         for pid in range(graph.num_parts):
             lo, hi = int(graph.ptr[pid]), int(graph.ptr[pid + 1])
-            x = graph.features.partition(lo, hi).to(device).double()
+            x = graph.partition_features(pid).to(device).double()
             z[lo:hi] = x @ w0t
             del x
-        h = torch.relu(norms[0](_spmm_by_columns(a, z) + convs[0].bias))
+        h = _spmm_by_columns(a, z)
         del z
+        _bias_ln_relu_by_rows(h, convs[0].bias, norms[0])
         for i in range(1, len(convs)):
-            h = _spmm_by_columns(a, h @ convs[i].lin.weight.t()) + convs[i].bias
+            h = _spmm_by_columns(a, h @ convs[i].lin.weight.t())
             if i < len(convs) - 1:
-                h = torch.relu(norms[i](h))
+                _bias_ln_relu_by_rows(h, convs[i].bias, norms[i])
+            else:
+                h += convs[i].bias
         tr = graph.train_mask.to(device)
         loss = F.cross_entropy(h[tr], graph.labels.to(device)[tr])
     out = float(loss)

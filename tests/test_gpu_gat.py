@@ -342,3 +342,50 @@ def test_gat_narrow_path_runs_and_matches_oracle_with_scores(gpu, C, square, mon
     assert max_abs_norm_err(got[0], ref_o) <= TOL
     for t, r in zip(got[1:], refs):
         assert max_abs_norm_err(t.reshape(-1), torch.as_tensor(r).reshape(-1)) <= TOL
+
+
+@pytest.mark.parametrize("C,longs", [(256, 3), (132, 0), (1024, 1)])
+def test_gat_attention_ln_matches_attention_then_epilogue(gpu, C, longs):
+    """gat_attention_ln (the attention kernel storing act(LN(O + bias))
+    straight from its accumulators, gr_gat_forward_ln) against the two-step
+    form it replaces in the GAT model, gat_attention then bias_ln_act: output
+    and every gradient (hs, attention vectors, conv bias, LayerNorm gamma and
+    beta) within TOL, and with whole rows only (no split rows) the output
+    bit-identical, since both form the row statistics with the same code
+    from the same h.  Split rows (longs > 0: hub rows of 1500 edges at a
+    256-edge segment) finish in their own fixup."""
+    from grinnder_amd.aggregation import RowDotSink, gat_attention_ln
+    from grinnder_amd.dense import bias_ln_act
+
+    B, E = 600, 900
+    rowptr, col, val = random_bipartite(B, E, 12, seed=C, long_rows=longs, long_len=1500)
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=256)
+    g = torch.Generator().manual_seed(C)
+    hs = torch.randn(E, C, generator=g)
+    a_s = torch.randn(1, 1, C, generator=g) / C ** 0.5
+    a_d = torch.randn(1, 1, C, generator=g) / C ** 0.5
+    b = torch.randn(C, generator=g)
+    gamma = 1 + 0.1 * torch.randn(C, generator=g)
+    beta = 0.1 * torch.randn(C, generator=g)
+    gy = torch.randn(B, C, generator=g)
+    res = []
+    for fused in (True, False):
+        leaves = [t.to(gpu).requires_grad_(True) for t in (hs, a_s, a_d, b, gamma, beta)]
+        if fused:
+            out = gat_attention_ln(leaves[0], adj, leaves[1], leaves[2], leaves[3], leaves[4],
+                                   leaves[5], 1e-5, "elu")
+        else:
+            dot = RowDotSink()
+            x = gat_attention(leaves[0], adj, leaves[1], leaves[2], None, 1, C, True,
+                              rowdot_sink=dot)
+            out = bias_ln_act(x, leaves[3], leaves[4], leaves[5], 1e-5, "elu", dot)
+        out.backward(gy.to(gpu))
+        torch.cuda.synchronize()
+        res.append([out.detach()] + [t.grad for t in leaves])
+    names = ["out", "hs", "att_src", "att_dst", "bias", "gamma", "beta"]
+    for name, a, c in zip(names, res[0], res[1]):
+        err = max_abs_norm_err(a.reshape(-1), c.reshape(-1))
+        print(f"C={C} longs={longs} {name}: {err:.1e}", flush=True)
+        assert err <= TOL, name
+    if longs == 0:
+        assert torch.equal(res[0][0], res[1][0])
