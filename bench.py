@@ -565,8 +565,8 @@ def summarize_profile(root: str) -> None:
                 e[2] += float(r.get("End_Timestamp", 0)) - float(r.get("Start_Timestamp", 0))
                 e[3] = min(e[3], v)
                 e[4] = max(e[4], v)
-    keep = ("aggregate", "gat_", "copy", "gemm", "Cijk", "gather", "scatter", CALIBRATION_KERNEL,
-            "ln_relu", "ln_act", "xent")
+    keep = ("aggregate", "gat_", "gatn_", "copy", "gemm", "Cijk", "gather", "scatter",
+            CALIBRATION_KERNEL, "ln_relu", "ln_act", "xent")
     print(f"# counters ({len(paths)} file(s)): per-dispatch mean / min / max")
     print(f"{'dispatches':>10} {'mean_value':>16} {'min':>14} {'max':>14} {'avg_us':>10}"
           f"  counter  kernel")

@@ -83,10 +83,13 @@ _SIGNATURES = {
     "gr_gat_dst_record": [_P, _P, _P, _P, _i64, _P, _P],
     "gr_gat_backward_src_h1": [_P, _i64, _P, _i64, _P, _P, _P, _i64, _P, _P, _P, _P, _P, _i64,
                                _P, _P, _P, _P, _i64, _P, _i64, _P, _P],
+    "gr_gat_narrow_pack": [_P, _i64, _i64, _i64, _i64, _P, _P, _P, _P, _P, _P],
     "gr_gat_narrow_forward": [_P, _i64, _P, _i64, _P, _i64, _P, _P, _i64, _i64, _i64, _i64,
-                              _P, _P, _P, _P, _P, _P, _P, _P, _i64, _P, _P, _i64, _i64, _P],
-    "gr_gat_narrow_backward": [_P, _i64, _P, _i64, _P, _i64, _P, _P, _i64, _i64, _i64, _P,
-                               _i64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _i64, _i64, _P],
+                              _P, _P, _P, _P, _P, _P, _P, _P, _i64, _P, _P, _P, _i64, _i64,
+                              _P],
+    "gr_gat_narrow_backward": [_P, _i64, _P, _i64, _P, _i64, _P, _P, _P, _i64, _i64, _i64,
+                               _P, _i64, _P, _i64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _i64,
+                               _i64, _P],
     "gr_gat_backward_dst": [_P, _i64, _P, _i64, _P, _P, _P, _P, _i64, _i64, _P, _P, _P, _i64,
                             _P],
     "gr_io_create": [_i32, _P],

@@ -685,10 +685,11 @@ class _GATAttention(torch.autograd.Function):
                 plan: DevicePlan, heads: int, channels: int, concat: bool,
                 s_pre: Optional[Tensor] = None, d_pre: Optional[Tensor] = None,
                 sink: Optional[RowDotSink] = None, zsink: Optional[ProjectedSink] = None,
-                token: Optional[Tensor] = None) -> Tensor:
+                token: Optional[Tensor] = None, zx_pre: Optional[Tensor] = None) -> Tensor:
         # zsink: hs is the matrix of all partitions' rows ([N, H*C], s_pre
         # [N, H] alike), read in place through zsink.gidx; the backward adds
-        # dHs into zsink.dz at zsink.rows.
+        # dHs into zsink.dz at zsink.rows.  zx_pre: hs's packed lines
+        # (gat_scores(packed=True) over these rows), read by the narrow path.
         hs = hs.contiguous()
         dev = hs.device
         H, C = heads, channels
@@ -703,7 +704,7 @@ class _GATAttention(torch.autograd.Function):
         region.__enter__()
         if zsink is None and _gat_narrow_ok(hs, H, C):
             return _GATAttention._forward_narrow(ctx, hs, a_src, a_dst, bias, plan, C, s_pre,
-                                                 d_pre, region, att_src.shape)
+                                                 d_pre, region, att_src.shape, zx_pre)
         if s_pre is not None:
             # Scores formed beforehand (once per layer for all rows of a
             # projected matrix, by the same kernel): s_pre [E, H], d_pre [B, H].
@@ -753,39 +754,49 @@ class _GATAttention(torch.autograd.Function):
 
     @staticmethod
     def _forward_narrow(ctx, hs, a_src, a_dst, bias, plan, C, s_pre, d_pre, region,
-                        att_shape):
+                        att_shape, zx_pre=None):
         """One head of C <= 24 channels: every row packed into a 128-byte line
-        with its logit halves, an online softmax, no alpha stored."""
+        with its logit, an online softmax, no alpha stored.  zx_pre: the
+        lines packed beforehand (with s_pre, d_pre)."""
         dev = hs.device
         E, B = plan.num_src, plan.num_dst
         f = plan.fwd
-        zx = torch.empty((E, 32), dtype=torch.float32, device=dev)
-        fstate = torch.empty((B, 32), dtype=torch.float32, device=dev)
-        o = torch.empty((B, C), dtype=torch.float32, device=dev)
-        y = torch.empty((B, C), dtype=torch.float32, device=dev) if bias is not None else None
+        packed = zx_pre is not None and s_pre is not None
+        zx = zx_pre if packed else torch.empty((E, 32), dtype=torch.float32, device=dev)
+        fstate = torch.empty((B, C + 4), dtype=torch.float32, device=dev)
+        # With a bias only Y = O + bias is written; the backward takes
+        # O = Y - bias.
+        out = torch.empty((B, C), dtype=torch.float32, device=dev)
+        b = bias.contiguous() if bias is not None else None
+        if s_pre is None:
+            s = None
+            dvec = torch.empty((B, 1), dtype=torch.float32, device=dev)
+        else:
+            s, dvec = s_pre.contiguous(), d_pre.contiguous()
         ws = _workspace(f.n_slots, 52, dev)
-        s = None if s_pre is None else s_pre.contiguous()
-        d = None if d_pre is None else d_pre.contiguous()
         _lib.call("gr_gat_narrow_forward", f.units.data_ptr(), f.n_units,
                   f.fixups.data_ptr() if f.n_fix else None, f.n_fix,
-                  _lib.ptr(f.long_units), f.n_long, plan.idx.data_ptr(), hs.data_ptr(),
-                  hs.stride(0), E, B, C, _lib.ptr(s), _lib.ptr(d), a_src.data_ptr(),
-                  a_dst.data_ptr(), _lib.ptr(bias.contiguous() if bias is not None else None),
-                  zx.data_ptr(), o.data_ptr(), _lib.ptr(y), C, fstate.data_ptr(),
+                  _lib.ptr(f.long_units), f.n_long, plan.idx.data_ptr(),
+                  None if packed else hs.data_ptr(),
+                  hs.stride(0), E, B, C, _lib.ptr(s), None if s is None else dvec.data_ptr(),
+                  a_src.data_ptr(), a_dst.data_ptr(), _lib.ptr(b),
+                  zx.data_ptr(), None if b is not None else out.data_ptr(),
+                  out.data_ptr() if b is not None else None, C,
+                  dvec.data_ptr() if s is None else None, fstate.data_ptr(),
                   _lib.ptr(ws), 0 if ws is None else ws.numel(), f.n_slots,
                   _lib.stream_handle())
         region.__exit__(None, None, None)
-        ctx.save_for_backward(hs, a_src, a_dst, zx, fstate, o)
+        ctx.save_for_backward(hs, a_src, a_dst, zx, fstate, out, dvec, b)
         ctx.narrow = True
         ctx.plan = plan
         ctx.shape = (1, C, True)
         ctx.has_bias = bias is not None
         ctx.att_shape = att_shape
-        return y if y is not None else o
+        return out
 
     @staticmethod
     def _backward_narrow(ctx, gy: Tensor):
-        hs, a_src, a_dst, zx, fstate, o = ctx.saved_tensors
+        hs, a_src, a_dst, zx, fstate, out, dvec, b = ctx.saved_tensors
         plan: DevicePlan = ctx.plan
         C = ctx.shape[1]
         E, B = plan.num_src, plan.num_dst
@@ -807,7 +818,8 @@ class _GATAttention(torch.autograd.Function):
         _lib.call("gr_gat_narrow_backward", bw.units.data_ptr(), bw.n_units,
                   bw.fixups.data_ptr() if bw.n_fix else None, bw.n_fix,
                   _lib.ptr(bw.long_units), bw.n_long, plan.row_idx.data_ptr(), zx.data_ptr(),
-                  E, B, C, go.data_ptr(), go.stride(0), o.data_ptr(), fstate.data_ptr(),
+                  dvec.data_ptr(), E, B, C, go.data_ptr(), go.stride(0), out.data_ptr(),
+                  out.stride(0), _lib.ptr(b), fstate.data_ptr(),
                   a_src.data_ptr(), a_dst.data_ptr(), gx.data_ptr(), dhs.data_ptr(),
                   ds.data_ptr(), dd.data_ptr(), _lib.ptr(ws), 0 if ws is None else ws.numel(),
                   bw.n_slots, _lib.stream_handle())
@@ -815,7 +827,7 @@ class _GATAttention(torch.autograd.Function):
         datt_src = column_sum(hs, ds, C)
         datt_dst = column_sum(hs[:B], dd, C)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
-                None, None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, None, None)
 
     @staticmethod
     def backward(ctx, gy: Tensor):
@@ -848,14 +860,17 @@ class _GATAttention(torch.autograd.Function):
         dhs, datt_src, datt_dst = _attention_backward(plan, hs, a_src, a_dst, s, d, alpha_or_m,
                                                       den, go, cdot, H, C, ctx.records, zsink)
         return (dhs, datt_src.view(ctx.att_shape), datt_dst.view(ctx.att_shape), db,
-                None, None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, None, None)
 
 
 def gat_scores(hs: Tensor, att_src: Tensor, att_dst: Tensor, heads: int, channels: int,
-               num_dst: int) -> Tuple[Tensor, Tensor]:
+               num_dst: int, packed: bool = False) -> tuple:
     """The attention logits' two halves of GATConv (no autograd): s[r, h] =
     <hs[r, h], att_src[h]> for every row and d[r, h] = <hs[r, h], att_dst[h]>
-    for the first num_dst rows, by the kernel gat_attention uses."""
+    for the first num_dst rows, by the kernel gat_attention uses.
+    packed: for a head the narrow kernels take, also the packed source lines
+    of these rows, (s, d, zx) (gr_gat_narrow_pack, same s and d): the
+    attention over exactly these rows then reads them instead of packing."""
     _check_device_tensor("hs", hs)
     hs = hs.contiguous()
     E, H = hs.size(0), heads
@@ -865,6 +880,12 @@ def gat_scores(hs: Tensor, att_src: Tensor, att_dst: Tensor, heads: int, channel
     d = torch.empty((num_dst, H), dtype=torch.float32, device=hs.device)
     a_src = att_src.detach().reshape(-1).contiguous()
     a_dst = att_dst.detach().reshape(-1).contiguous()
+    if packed and _gat_narrow_ok(hs, H, channels):
+        zx = torch.empty((E, 32), dtype=torch.float32, device=hs.device)
+        _lib.call("gr_gat_narrow_pack", hs.data_ptr(), hs.stride(0), E, num_dst, channels,
+                  a_src.data_ptr(), a_dst.data_ptr(), zx.data_ptr(), s.data_ptr(),
+                  d.data_ptr(), _lib.stream_handle())
+        return s, d, zx
     _lib.call("gr_gat_scores", hs.data_ptr(), hs.stride(0), E, num_dst, H, channels,
               a_src.data_ptr(), a_dst.data_ptr(), s.data_ptr(), d.data_ptr(),
               _lib.stream_handle())
@@ -912,11 +933,14 @@ def gat_attention(hs: Tensor, adj: Adjacency, att_src: Tensor, att_dst: Tensor,
     if scores is None:
         return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat,
                                    None, None, rowdot_sink)
-    s, d = scores
+    s, d = scores[0], scores[1]
     if tuple(s.shape) != (plan.num_src, heads) or tuple(d.shape) != (plan.num_dst, heads):
         raise ValueError("gat_attention: scores do not match the adjacency and heads")
+    zx = scores[2] if len(scores) > 2 else None
+    if zx is not None and tuple(zx.shape) != (plan.num_src, 32):
+        raise ValueError("gat_attention: packed rows do not match the adjacency")
     return _GATAttention.apply(hs, att_src, att_dst, bias, plan, heads, channels, concat, s, d,
-                               rowdot_sink)
+                               rowdot_sink, None, None, zx)
 
 
 class _GATAttentionLN(torch.autograd.Function):

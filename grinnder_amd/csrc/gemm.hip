@@ -88,7 +88,8 @@ __device__ __forceinline__ void store_tile(float (*lds)[W + PAD], const float (&
 
 constexpr int kXcds = 8;
 
-// BN = 128 or 64 output columns per workgroup (64 for narrow N).
+// BN = 128, 64 or 32 output columns per workgroup (64 and 32 for narrow N;
+// 32 takes B with 4-byte loads).
 template <int VA, int VB, int BN>
 __global__ __launch_bounds__(256) void gemm_tn_splitk(const float* __restrict__ A, int64_t lda,
                                                       const float* __restrict__ B, int64_t ldb,
@@ -242,7 +243,11 @@ extern "C" int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t l
   const bool va = (plda % 4 == 0) && (pm % 4 == 0) && (reinterpret_cast<uintptr_t>(pa) % 16 == 0);
   const bool vb = (pldb % 4 == 0) && (pn % 4 == 0) && (reinterpret_cast<uintptr_t>(pb) % 16 == 0);
   const bool narrow = pn <= 64;
-  const int bn = narrow ? 64 : TN;
+  // At most 32 columns (a 19- or 20-wide layer's dW): 32-column tiles, so the
+  // matrix cores do not work on 44 padded columns of 64; the product is then
+  // bound by streaming the wide operand.
+  const bool narrow32 = pn <= 32;
+  const int bn = narrow32 ? 32 : narrow ? 64 : TN;
   const int tiles_m = (int)((pm + TM - 1) / TM);
   const int tiles = tiles_m * (int)((pn + bn - 1) / bn);
   const int64_t nwg = (used + kXcds - 1) / kXcds * kXcds * tiles;
@@ -251,7 +256,9 @@ extern "C" int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t l
 #define GR_GT(VA_, VB_, BN_)                                                                   \
   hipLaunchKernelGGL((gemm_tn_splitk<VA_, VB_, BN_>), grid, dim3(256), 0, s, pa, plda, pb, pldb, \
                      (int)pm, (int)pn, k, kchunk, (int)used, tiles_m, tiles, workspace)
-  if (narrow) {
+  if (narrow32) {
+    if (va) GR_GT(4, 1, 32); else GR_GT(1, 1, 32);
+  } else if (narrow) {
     if (va && vb) GR_GT(4, 4, 64); else if (va) GR_GT(4, 1, 64);
     else if (vb) GR_GT(1, 4, 64); else GR_GT(1, 1, 64);
   } else {

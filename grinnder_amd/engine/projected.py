@@ -582,11 +582,15 @@ class ProjectedLayers:
             if last:
                 with torch.set_grad_enabled(training):
                     self._merged_out = self._merged_call(layer, grad=training)
+                # The one pass has taken its scores (the graph keeps what its
+                # backward needs).
+                self._scores.pop(layer, None)
                 return
             n = int(self.graph.ptr[-1])
             x_next = self._xres_buf(layer + 1)[:n]
             with torch.set_grad_enabled(training):
                 out = self._merged_call(layer, grad=training, dest=OutputRows(x_next))
+            self._scores.pop(layer, None)
             if training:
                 self._graphs.setdefault(layer, {})[-1] = out
             if (layer + 1) in self._proj:
@@ -963,7 +967,8 @@ class ProjectedLayers:
         self._scores.pop(layer, None)
         if layer in self._proj:
             with torch.cuda.stream(self.streams.compute):
-                sc = self.model.projected_scores(layer, self._zbufs[layer])
+                sc = self.model.projected_scores(layer, self._zbufs[layer],
+                                                 whole=layer in self._merged)
             if sc is not None:
                 self._scores[layer] = sc
 

@@ -66,11 +66,12 @@ class GriNNderModel(torch.nn.Module):
         """Whether forward_projected(layer, ...) accepts a sink."""
         return False
 
-    def projected_scores(self, layer: int, z: Tensor):
+    def projected_scores(self, layer: int, z: Tensor, whole: bool = False):
         """Per-row quantities of the projected matrix z that
         forward_projected(layer, ...) can take precomputed for a partition's
         gathered rows (its `scores` argument), formed once for all rows; None
-        when the layer has none (the default)."""
+        when the layer has none (the default).  whole: the layer then reads
+        all of z in one pass (a merged layer)."""
         return None
 
     def draws_per_partition(self, layer: int) -> bool:

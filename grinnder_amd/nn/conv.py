@@ -224,16 +224,18 @@ class GATConv(Module):
             keep.append(hs.detach())
         return hs
 
-    def scores(self, hs: Tensor) -> Tuple[Tensor, Tensor]:
+    def scores(self, hs: Tensor, packed: bool = False) -> tuple:
         """The logit halves (s, d) of every row of hs, as attend forms them
-        (padding included), for callers that hold hs for many partitions."""
+        (padding included), for callers that hold hs for many partitions.
+        packed: also the packed lines a narrow head's attention over exactly
+        these rows reads, (s, d, zx), when the head takes them."""
         pad = self._padded()
         if pad:
             return gat_scores(self._pad_rows(hs), F.pad(self.att_src, (0, pad)),
                               F.pad(self.att_dst, (0, pad)), 1, self.out_channels + pad,
-                              hs.size(0))
+                              hs.size(0), packed)
         return gat_scores(hs, self.att_src, self.att_dst, self.heads, self.out_channels,
-                          hs.size(0))
+                          hs.size(0), packed)
 
     def __repr__(self) -> str:
         return (f"{self.__class__.__name__}({self.in_channels}, {self.out_channels}, "

@@ -118,12 +118,14 @@ class GAT(GriNNderModel):
                                   dest=dest)
         return self._finish(layer, conv.attend(hs, adj, scores=scores, sink=sink))
 
-    def projected_scores(self, layer: int, z: Tensor):
+    def projected_scores(self, layer: int, z: Tensor, whole: bool = False):
         """The attention logit halves of every row of the projected matrix z,
         formed once for all partitions (no autograd: the attention-vector
-        gradients come from the attention's own backward)."""
+        gradients come from the attention's own backward).  whole: the
+        attention reads all of z at once (a merged layer), so a narrow head
+        also gets z's packed lines (GATConv.scores)."""
         with torch.no_grad():
-            return self.convs[layer].scores(z)
+            return self.convs[layer].scores(z, packed=whole)
 
     def layer_dims(self) -> List[int]:
         dims = [self.convs[0].in_channels]

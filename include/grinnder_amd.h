@@ -587,18 +587,31 @@ int gr_gat_backward_src_h1(const int32_t* units, int64_t n_units,
                            float* att_part, int64_t att_rows, int64_t* att_waves,
                            void* stream);
 
+/* The packed source lines of gr_gat_narrow_forward, with the logit halves,
+ * formed once for rows that several passes read (the projected matrix of a
+ * layer): zx [n_src, 32] = [Hs_j (C) | 0 .. | 24: s_j | 0 ..], s [n_src] and
+ * d [n_dst], s and d as gr_gat_scores forms them (bit for bit at these
+ * widths).  The logits of PyG's GATConv (grinnder/nn/gat.py:69-72). */
+int gr_gat_narrow_pack(const float* hs, int64_t ldh, int64_t n_src, int64_t n_dst,
+                       int64_t channels, const float* att_src, const float* att_dst,
+                       float* zx, float* s, float* d, void* stream);
+
 /* Narrow one-head attention (C channels, a multiple of 4 up to 24): the
  * forward of gr_gat_forward (PyG GATConv as grinnder/nn/gat.py:54-61,69-78
  * calls it) with every edge reading one 128-byte packed line.
- *   zx [n_src, 32]: written; source row j packed as [Hs_j (C) | 0 .. |
- *     24: s_j, 25: d_j (j < n_dst) | 0 ..], s and d taken from s_pre / d_pre
- *     when given (both or neither), else formed from att_src / att_dst as
- *     gr_gat_scores forms them.
- *   o [n_dst, C] = O; y (optional, row stride ldy) = O + bias (bias optional).
- *   f_state [n_dst, 32]: written; [N_i (C) | 0 .. | 24: m_i, 25: den_i,
- *     26: S_i | 0 ..] with N_i = sum_{t_ij <= 0} alpha_ij Hs_j and
- *     S_i = sum_{t_ij <= 0} alpha_ij, what gr_gat_narrow_backward needs
- *     instead of alpha (which is not formed).
+ *   zx [n_src, 32]: source row j packed as [Hs_j (C) | 0 .. | 24: s_j |
+ *     0 ..].  With hs NULL, zx is an input (from gr_gat_narrow_pack over the
+ *     same rows) and d_pre must be given.  Else zx is written from hs: the
+ *     logit halves are taken from s_pre / d_pre when given (both or
+ *     neither); else they are formed from att_src / att_dst as
+ *     gr_gat_scores forms them, and the destination halves are written to
+ *     d_state [n_dst].  The kernels read d_i from d_pre or d_state.
+ *   o [n_dst, C] = O (optional when y is given); y (optional, row stride
+ *     ldy) = O + bias (bias optional).
+ *   f_state [n_dst, C + 4]: written; [N_i (C) | m_i, den_i, S_i, 0] with
+ *     N_i = sum_{t_ij <= 0} alpha_ij Hs_j and S_i = sum_{t_ij <= 0} alpha_ij,
+ *     what gr_gat_narrow_backward needs instead of alpha (which is not
+ *     formed).
  *   long_units (optional, device int32 [n_long]): indices of the plan units
  *     that are split or longer than 32 edges (run one per wavefront); NULL:
  *     every unit is examined.  workspace: n_slots * 52 floats.
@@ -613,12 +626,15 @@ int gr_gat_narrow_forward(const int32_t* units, int64_t n_units,
                           const float* s_pre, const float* d_pre,
                           const float* att_src, const float* att_dst,
                           const float* bias, float* zx, float* o, float* y,
-                          int64_t ldy, float* f_state, float* workspace,
-                          int64_t ws_floats, int64_t n_slots, void* stream);
+                          int64_t ldy, float* d_state, float* f_state,
+                          float* workspace, int64_t ws_floats, int64_t n_slots,
+                          void* stream);
 
 /* Backward of gr_gat_narrow_forward over the CSC plan (units / fixups /
- * long_units of the transposed adjacency, row_idx from gr_csr_transpose):
- *   first, per destination row, c_i = <go_i, O_i> and
+ * long_units of the transposed adjacency, row_idx from gr_csr_transpose).
+ * zx, f_state: the forward's; d: the destination halves it read (d_pre or
+ * d_state); out (row stride ldo): its o, or its y with `bias` (O = y - bias).
+ *   First, per destination row, c_i = <go_i, O_i> and
  *     dd_i = -0.8 (<go_i, N_i> - c_i S_i) + c_i 1e-16 / den_i (= sum_j g_t,ij:
  *     sum_j g_e,ij is exactly c_i 1e-16 / den_i), written to dd [n_dst], and
  *     gx [n_dst, 32] = [go_i (C) | 0 .. | 24: d_i, 25: m_i, 26: 1 / den_i,
@@ -632,9 +648,10 @@ int gr_gat_narrow_forward(const int32_t* units, int64_t n_units,
 int gr_gat_narrow_backward(const int32_t* units, int64_t n_units,
                            const int32_t* fixups, int64_t n_fix,
                            const int32_t* long_units, int64_t n_long,
-                           const int32_t* row_idx, const float* zx, int64_t n_src,
-                           int64_t n_dst, int64_t channels, const float* go,
-                           int64_t ldg, const float* o, const float* f_state,
+                           const int32_t* row_idx, const float* zx, const float* d,
+                           int64_t n_src, int64_t n_dst, int64_t channels,
+                           const float* go, int64_t ldg, const float* out,
+                           int64_t ldo, const float* bias, const float* f_state,
                            const float* att_src, const float* att_dst, float* gx,
                            float* dhs, float* ds, float* dd, float* workspace,
                            int64_t ws_floats, int64_t n_slots, void* stream);

@@ -23,9 +23,11 @@ def _randn(*shape, seed, dev):
 @pytest.mark.parametrize("k,m,n", [(0, 5, 7), (1, 1, 1), (37, 3, 5), (1000, 47, 256),
                                    (5000, 256, 100), (3001, 130, 129), (200_000, 256, 256),
                                    (70_000, 47, 256), (20_000, 256, 48), (20_000, 48, 100),
-                                   (5000, 64, 256), (0, 48, 256)])
+                                   (5000, 64, 256), (0, 48, 256), (20_000, 256, 20),
+                                   (30_000, 19, 256), (5000, 32, 300), (777, 130, 3)])
 def test_gemm_tn_matches_fp64(gpu, k, m, n):
-    """Covers 128- and 64-column tiles and the transposed narrow path (m <= 64 < n)."""
+    """Covers 128-, 64- and 32-column tiles and the transposed narrow path
+    (m <= 64 < n), 32-column tiles with 4-byte loads of the narrow side."""
     a = _randn(k, m, seed=k + m, dev=gpu)
     b = _randn(k, n, seed=k + n + 1, dev=gpu)
     c = gemm_tn(a, b)
@@ -92,14 +94,18 @@ def test_gemm_tn_workspace_checked(gpu):
                                    (5000, 256, 1024), (300, 300, 64), (129, 65, 33),
                                    (4096, 16, 20), (70_000, 256, 48), (3000, 1024, 256),
                                    (2500, 47, 256), (513, 130, 1), (100_003, 256, 19),
-                                   (5000, 512, 20), (2001, 602, 47), (64, 64, 31), (1, 256, 63)])
+                                   (5000, 512, 20), (2001, 602, 47), (64, 64, 31), (1, 256, 63),
+                                   (70_001, 256, 256), (65_536, 20, 256), (200_003, 48, 100),
+                                   (66_000, 128, 12), (70_000, 200, 60), (80_000, 4, 40)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     """Every tile shape (n > 64, 33..64, 17..32, <= 16), K not a multiple of
     the 32-wide step or of 4 (scalar loads), ragged row and column tiles; the
     short-reduction kernel (k <= 64 not a multiple of 4, n >= 64) with one to
     five 128-column blocks, 8-byte and element stores, k just under its 32
-    and 64 register limits."""
+    and 64 register limits; row counts past 65536 with one and two column
+    tiles, a partial second tile (n = 200), k below one step and not a
+    multiple of the step."""
     a = _randn(m, k, seed=m + k, dev=gpu)
     b = _randn(n, k, seed=n + k + 1, dev=gpu)
     bv = _randn(n, seed=n, dev=gpu) if bias else None
@@ -141,6 +147,18 @@ def test_gemm_nt_strided_and_in_place(gpu):
         assert torch.equal(buf[:, c0 + 200:], before[:, c0 + 200:])
     with pytest.raises(ValueError, match="out must be"):
         gemm_nt(a, b, out=torch.empty(9000, 199, device=gpu))
+    # 70k rows with strided rows of a and b, a bias, and a column slice of a
+    # wider buffer as out.
+    big_a = _randn(70_000, 300, seed=7, dev=gpu)
+    a = big_a[:, 16:272]
+    buf = _randn(70_000, 320, seed=8, dev=gpu)
+    before = buf.clone()
+    bv = _randn(200, seed=9, dev=gpu)
+    gemm_nt(a, b, bv, out=buf[:, 40:240])
+    ref = a.double() @ b.double().t() + bv.double()
+    assert max_abs_norm_err(buf[:, 40:240], ref) <= TOL
+    assert torch.equal(buf[:, :40], before[:, :40]) and torch.equal(buf[:, 240:], before[:, 240:])
+    assert torch.equal(gemm_nt(a, b, bv), gemm_nt(a, b, bv))
 
 
 @pytest.mark.parametrize("rows,fin,fout,bias", [(5000, 100, 256, True), (777, 256, 47, False),
@@ -305,8 +323,15 @@ def test_gat_layer_row_dot_handoff(gpu):
         assert max_abs_norm_err(g1, g0.double()) <= TOL
 
 
-@pytest.mark.parametrize("rows,din,dout,act", [(5000, 100, 256, "relu"), (777, 37, 48, "elu"),
-                                               (64, 3, 16, "relu"), (0, 8, 32, "relu")])
+@pytest.mark.parametrize("rows,din,dout,act", [
+    (5000, 100, 256, "relu"), (777, 37, 48, "elu"), (64, 3, 16, "relu"), (0, 8, 32, "relu"),
+    # dout 256 with k tails of 4/8/12 past the 16-k chunks, no full chunk,
+    # eight full chunks, ragged and single rows, and 70k rows.  The large
+    # cases take ELU: among millions of ReLU inputs a few fall within fp32
+    # rounding of 0 and take the other slope in the float64 reference, a
+    # difference of the test, not of the kernel.
+    (70001, 100, 256, "elu"), (33, 4, 256, "elu"), (1000, 12, 256, "elu"),
+    (517, 128, 256, "elu"), (1, 24, 256, "relu"), (16, 16, 256, "relu")])
 def test_linear_ln_act_matches_fp64(gpu, rows, din, dout, act):
     """act(LayerNorm(x Wᵀ + b)) with the LayerNorm in the MFMA GEMM epilogue."""
     from grinnder_amd.dense import linear_ln_act

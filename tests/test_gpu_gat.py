@@ -297,14 +297,20 @@ def test_gat_attention_in_place_matches_gathered(gpu, C, big):
     assert max_abs_norm_err(as1.view(-1), torch.as_tensor(back[1]).view(-1)) <= TOL
 
 
-@pytest.mark.parametrize("C,square", [(20, True), (20, False), (24, True), (8, False)])
-def test_gat_narrow_path_runs_and_matches_oracle_with_scores(gpu, C, square, monkeypatch):
+@pytest.mark.parametrize("C,square,with_bias", [(20, True, True), (20, False, True),
+                                                (24, True, True), (8, False, True),
+                                                (20, False, False), (4, True, False)])
+def test_gat_narrow_path_runs_and_matches_oracle_with_scores(gpu, C, square, with_bias,
+                                                             monkeypatch):
     """One head of C <= 24 channels (a multiple of 4) runs the packed-line
     kernels (gr_gat_narrow_forward / _backward), not the general ones, with
-    the logit halves formed inside or given (as the projected flow gives
-    them, gat_scores over all rows): both give the same bits, and match the
-    oracle, including split rows and columns (hub rows of 1500 edges at a
-    256-edge segment) and rows past the destinations (E > B)."""
+    the logit halves formed inside, given (as the projected flow gives
+    them, gat_scores over all rows), or given with the packed lines
+    (gat_scores(packed=True), as a merged layer gives them): all three give
+    the same bits, and match the oracle, including split rows and columns
+    (hub rows of 1500 edges at a 256-edge segment), rows past the
+    destinations (E > B), and a layer without bias (O itself is the output
+    and what the backward reads)."""
     from grinnder_amd import _lib
     from grinnder_amd.aggregation import gat_scores
 
@@ -322,21 +328,27 @@ def test_gat_narrow_path_runs_and_matches_oracle_with_scores(gpu, C, square, mon
     real = _lib.call
     monkeypatch.setattr(_lib, "call", lambda name, *a: (called.append(name), real(name, *a))[1])
     results = []
-    for given in (False, True):
+    for given in ("inside", "scores", "packed"):
         leaves = [t.to(gpu).requires_grad_(True) for t in (hs, a_s, a_d, b)]
         scores = None
-        if given:
-            scores = gat_scores(leaves[0].detach(), leaves[1], leaves[2], 1, C, B)
-        out = gat_attention(leaves[0], adj, leaves[1], leaves[2], leaves[3], 1, C, True,
-                            scores=scores)
+        if given != "inside":
+            scores = gat_scores(leaves[0].detach(), leaves[1], leaves[2], 1, C, B,
+                                packed=given == "packed")
+            assert len(scores) == (3 if given == "packed" else 2)
+        out = gat_attention(leaves[0], adj, leaves[1], leaves[2],
+                            leaves[3] if with_bias else None, 1, C, True, scores=scores)
         out.backward(gy.to(gpu))
         torch.cuda.synchronize()
-        results.append([out.detach()] + [t.grad for t in leaves])
+        results.append([out.detach()] + [t.grad for t in leaves[:3]]
+                       + ([leaves[3].grad] if with_bias else []))
     assert "gr_gat_narrow_forward" in called and "gr_gat_narrow_backward" in called
+    assert "gr_gat_narrow_pack" in called
     assert "gr_gat_forward" not in called
-    for a, c in zip(results[0], results[1]):
-        assert torch.equal(a, c)
-    ref_o, alpha, tpre = oracle.gat_forward(rowptr, col, hs, 1, C, a_s, a_d, b, True)
+    for other in results[1:]:
+        for a, c in zip(results[0], other):
+            assert torch.equal(a, c)
+    ref_o, alpha, tpre = oracle.gat_forward(rowptr, col, hs, 1, C, a_s, a_d,
+                                            b if with_bias else None, True)
     refs = oracle.gat_backward(rowptr, col, hs, 1, C, a_s, a_d, True, alpha, tpre, gy)
     got = results[0]
     assert max_abs_norm_err(got[0], ref_o) <= TOL
