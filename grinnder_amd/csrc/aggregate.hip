@@ -943,14 +943,17 @@ inline unsigned final_blocks(int64_t dim) {
 }
 
 // Narrow rows (at most G * VEC floats, G <= 16): 64 / G whole rows per
-// wavefront, one per group of G lanes, each lane owning VEC consecutive
-// floats of its row.  A wavefront per row would spend most of its time in
-// the dependent loads that start a row (unit, column ids, first rows) for a
-// handful of short gathers; here 64 / G rows share that latency.  Each group
-// keeps U of its row's edges in flight; the plan lists whole rows by length
-// class, so the groups of a wavefront run similar trip counts.  All lanes of
-// a group read the same column id and weight (one broadcast load).  A row's
-// edges are summed in edge order; the result is deterministic.
+// wavefront step (a batch), one per group of G lanes, each lane owning VEC
+// consecutive floats of its row.  Most short rows hold a handful of edges
+// (an R-MAT graph's rows are mostly the self loop alone), so a batch is bound
+// by its chain of dependent loads (unit, column ids, gathered rows), not by
+// bytes.  The wavefronts therefore stride over the batches and load the next
+// batch's unit's first U column ids and weights, and the unit after it,
+// before the current batch's gathers.  Each group keeps U of its row's edges
+// in flight; the plan lists whole rows by length class, so the groups of a
+// wavefront run similar trip counts.  All lanes of a group read the same
+// column id and weight (one broadcast load).  A row's edges are summed in
+// edge order; the result is deterministic.
 template <int VEC, int G, int U>
 __global__ __launch_bounds__(256) void aggregate_rows(
     const int4* __restrict__ units, int64_t n_units, const int32_t* __restrict__ idx,
@@ -961,71 +964,117 @@ __global__ __launch_bounds__(256) void aggregate_rows(
   const int lane = threadIdx.x & 63;
   const int grp = lane / G;
   const int sub = lane % G;
-  const int64_t wid =
+  const int64_t nb = (n_units + RPW - 1) / RPW;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  int64_t b =
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t u = wid * RPW + grp;
-  if (wid * RPW >= n_units) return;
-  // When G does not divide 64 the last 64 % G lanes form no group.
-  const bool active = grp < RPW && u < n_units;
-  const int4 w = active ? units[u] : make_int4(0, 0, 0, -1);
+  if (b >= nb) return;
+  // When G does not divide 64 the last 64 % G lanes form no group; they and
+  // the groups past the last unit hold no row (x = -1, no edges).
+  auto unit_of = [&](int64_t bb) {
+    const int64_t u = bb * RPW + grp;
+    return grp < RPW && u < n_units ? units[u] : make_int4(-1, 0, 0, -1);
+  };
+  // The first U edges of a unit; past its end the last edge's id again, with
+  // weight 0 (an empty unit reads nothing).
+  auto first_edges = [&](int4 w, int (&c)[U], float (&v)[U]) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int ee = min(w.y + k, w.z - 1);
+      c[k] = w.z > w.y ? idx[ee] : 0;
+      v[k] = w.y + k < w.z ? val[ee] : 0.f;
+    }
+  };
   const int foff = sub * VEC;
   const bool fvalid = foff < dim;
   const int fld = fvalid ? foff : dim - VEC;
 
-  float acc[VEC];
+  int4 w = unit_of(b);
+  int4 wn = unit_of(b + stride);
+  int c0[U];
+  float v0[U];
+  first_edges(w, c0, v0);
+  while (true) {
+    int c1[U];
+    float v1[U];
+    first_edges(wn, c1, v1);
+    const int4 wnn = unit_of(b + 2 * stride);
+
+    float acc[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) acc[j] = 0.f;
-  int e = w.y;
-  const int end = w.z;
-  for (; e + U <= end; e += U) {
-    int c[U];
-    float v[U];
+    for (int j = 0; j < VEC; ++j) acc[j] = 0.f;
+    const int end = w.z;
+    if (end > w.y) {
+      // Edges w.y .. w.y + U - 1: with fewer, the missing ones re-read the
+      // last edge's row (in bounds, cached) with weight 0.
+      float r[U][VEC];
+#pragma unroll
+      for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c0[k] * ldx + fld, r[k]);
+#pragma unroll
+      for (int k = 0; k < U; ++k)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v0[k], r[k][j], acc[j]);
+    }
+    int e = w.y + U;
+    for (; e + U <= end; e += U) {
+      int c[U];
+      float v[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        c[k] = idx[e + k];
+        v[k] = val[e + k];
+      }
+      float r[U][VEC];
+#pragma unroll
+      for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld, r[k]);
+#pragma unroll
+      for (int k = 0; k < U; ++k)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v[k], r[k][j], acc[j]);
+    }
+    if (e < end) {
+      int c[U];
+      float v[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int ee = min(e + k, end - 1);
+        c[k] = idx[ee];
+        v[k] = e + k < end ? val[ee] : 0.f;
+      }
+      float r[U][VEC];
+#pragma unroll
+      for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld, r[k]);
+#pragma unroll
+      for (int k = 0; k < U; ++k)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v[k], r[k][j], acc[j]);
+    }
+    if (w.x >= 0 && fvalid) {
+      float* out = y + (int64_t)(orow != nullptr ? orow[w.x] : w.x) * ldy + foff;
+      if (orow != nullptr) {
+        float o[VEC];
+        load_vec<VEC>(out, o);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] = o[j] + acc[j];
+      } else if (bias != nullptr) {
+        float bb[VEC];
+        load_vec<VEC>(bias + foff, bb);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] += bb[j];
+      }
+      store_vec<VEC>(out, acc);
+    }
+
+    b += stride;
+    if (b >= nb) break;
+    w = wn;
+    wn = wnn;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      c[k] = idx[e + k];
-      v[k] = val[e + k];
+      c0[k] = c1[k];
+      v0[k] = v1[k];
     }
-    float r[U][VEC];
-#pragma unroll
-    for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld, r[k]);
-#pragma unroll
-    for (int k = 0; k < U; ++k)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v[k], r[k][j], acc[j]);
   }
-  if (e < end) {
-    // Fewer than U edges left: the missing ones re-read the last edge's row
-    // (in bounds, cached) with weight 0.
-    int c[U];
-    float v[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int ee = min(e + k, end - 1);
-      c[k] = idx[ee];
-      v[k] = e + k < end ? val[ee] : 0.f;
-    }
-    float r[U][VEC];
-#pragma unroll
-    for (int k = 0; k < U; ++k) load_vec<VEC>(x + (int64_t)c[k] * ldx + fld, r[k]);
-#pragma unroll
-    for (int k = 0; k < U; ++k)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) acc[j] = fmaf(v[k], r[k][j], acc[j]);
-  }
-  if (!active || !fvalid) return;
-  float* out = y + (int64_t)(orow != nullptr ? orow[w.x] : w.x) * ldy + foff;
-  if (orow != nullptr) {
-    float o[VEC];
-    load_vec<VEC>(out, o);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) acc[j] = o[j] + acc[j];
-  } else if (bias != nullptr) {
-    float b[VEC];
-    load_vec<VEC>(bias + foff, b);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) acc[j] += b[j];
-  }
-  store_vec<VEC>(out, acc);
 }
 
 template <int VEC, int G>
@@ -1034,7 +1083,8 @@ hipError_t launch_rows(const int4* units, int64_t n_units, const int32_t* idx, c
                        int dim, const int32_t* orow, hipStream_t s) {
   constexpr int RPW = 64 / G;
   const int64_t waves = (n_units + RPW - 1) / RPW;
-  const int64_t blocks = (waves + 3) / 4;
+  // Enough wavefronts to fill the device; each strides over the batches.
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((waves + 3) / 4, 8192));
   hipLaunchKernelGGL((aggregate_rows<VEC, G, 8>), dim3((unsigned)blocks), dim3(256), 0, s, units,
                      n_units, idx, val, x, ldx, y, ldy, bias, dim, orow);
   return hipGetLastError();
