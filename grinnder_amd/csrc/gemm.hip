@@ -605,6 +605,175 @@ static hipError_t launch_short_k(const float* a, int64_t lda, const float* b, in
   return hipGetLastError();
 }
 
+// Short-K form (K a multiple of 32 up to 256, 16-byte rows of A and B, N a
+// multiple of 4, millions of rows): each workgroup keeps a block of NT = 16 NJ
+// columns of B in LDS as [column][k] for the whole launch (133 KB at
+// NT = 128) and its 16 wavefronts walk blocks of 16 MI rows of A, with no
+// barrier after the fill.  A lane's two 16-byte loads of A take k = 8 lk ..
+// 8 lk + 7 of a 32-k chunk (one 128-byte line of each row a chunk), straight
+// from HBM two chunks ahead; its two ds_read_b128 of B the same eight k, and
+// MFMA s of the chunk sums k = 8 lk + s over lk.  The workgroups of the column
+// blocks of one row stream are on one XCD, so A is read from HBM once.  Each
+// lane quad transposes its 4 x 4 blocks, so C leaves the accumulators as
+// 16-byte row stores.  Measured against gemm_nt_kernel on one box: 2.45M x 48
+// x 256 0.69 against 0.80 ms, 2.45M x 256 x 256 2.84 against 2.96 ms; at 20
+// columns the two are equal, so narrower products keep the tiled kernel.
+constexpr int RS_KST = 256 + 4;  // LDS row stride: 16 lanes' reads fall on distinct banks
+constexpr int RS_WAVES = 16;
+constexpr int64_t kResidentMinRows = 1 << 16;
+
+struct A8 {
+  float4 lo, hi;
+};
+
+template <int MI, int NJ>
+__global__ __launch_bounds__(1024) void gemm_nt_resident(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
+    const float* __restrict__ bias, float* __restrict__ C, int64_t ldc, int64_t M, int N, int K,
+    int tiles_n) {
+  constexpr int NT = 16 * NJ, RB = 16 * MI;
+  __shared__ __align__(16) float Bs[NT * RS_KST];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  const int g = blockIdx.x, slot = g / kXcds, tile = slot % tiles_n;
+  const int64_t stream = (int64_t)(slot / tiles_n) * kXcds + g % kXcds;
+  const int64_t nstreams = (int64_t)gridDim.x / tiles_n;
+  const int n0 = tile * NT;
+  const int kq = K / 4;
+  for (int i = tid; i < NT * kq; i += 1024) {
+    const int c = i / kq, k = (i % kq) * 4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n0 + c < N) v = *reinterpret_cast<const float4*>(B + (int64_t)(n0 + c) * ldb + k);
+    *reinterpret_cast<float4*>(&Bs[c * RS_KST + k]) = v;
+  }
+  __syncthreads();
+  const int64_t nblk = (M + RB - 1) / RB;
+  const int64_t step = nstreams * RS_WAVES;
+  const int64_t blk0 = stream * RS_WAVES + wave;
+  if (blk0 >= nblk) return;
+  // The wavefront's chunks t = 0 .. T - 1: block blk0 + (t / nch) step, k
+  // chunk t % nch.
+  const int nch = K / 32;
+  const int64_t T = (nblk - blk0 + step - 1) / step * nch;
+  const int qc = lane & 3, qa = (lane >> 2) & 3;
+  const float* bl = Bs + lr * RS_KST + 8 * lk;
+
+  auto load = [&](A8 (&dst)[MI], int64_t t) {
+    if (t < T) {
+      const int64_t b = blk0 + (t / nch) * step;
+      const int c = (int)(t % nch);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int64_t r = b * RB + i * 16 + lr;  // rows past M read the block's first
+        const float* p = A + (r < M ? r : b * RB) * lda + c * 32 + 8 * lk;
+        dst[i].lo = *reinterpret_cast<const float4*>(p);
+        dst[i].hi = *reinterpret_cast<const float4*>(p + 4);
+      }
+    }
+  };
+  floatx4 acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const A8 (&cur)[MI], int64_t t) {
+    const int c = (int)(t % nch);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float4 b0 = *reinterpret_cast<const float4*>(bl + j * 16 * RS_KST + c * 32);
+      const float4 b1 = *reinterpret_cast<const float4*>(bl + j * 16 * RS_KST + c * 32 + 4);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].lo.x, b0.x, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].lo.y, b0.y, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].lo.z, b0.z, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].lo.w, b0.w, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].hi.x, b1.x, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].hi.y, b1.y, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].hi.z, b1.z, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].hi.w, b1.w, acc[i][j], 0, 0, 0);
+      }
+    }
+    if (c == nch - 1) {
+      // The block is complete: rows 16 i + 4 lk + q, columns 16 j + lr; after
+      // the quad transpose row 16 i + 4 lk + qc, columns 16 j + 4 qa .. + 3.
+      const int64_t b = blk0 + (t / nch) * step;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int col = n0 + j * 16 + 4 * qa;
+        const bool cin = col < N;  // N % 4 == 0: the four columns are in or out together
+        const float4 bb = cin && bias != nullptr ? *reinterpret_cast<const float4*>(bias + col)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
+          gr_wave::quad_transpose(v0, v1, v2, v3, qc);
+          const int64_t row = b * RB + i * 16 + 4 * lk + qc;
+          if (cin && row < M)
+            *reinterpret_cast<float4*>(C + row * ldc + col) =
+                make_float4(v0 + bb.x, v1 + bb.y, v2 + bb.z, v3 + bb.w);
+          acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  };
+  // Three chunk buffers in rotation: chunk t computes while t + 1 and t + 2
+  // load.
+  A8 r0[MI], r1[MI], r2[MI];
+  load(r0, 0);
+  load(r1, 1);
+  for (int64_t t = 0; t < T; t += 3) {
+    load(r2, t + 2);
+    compute(r0, t);
+    if (t + 1 >= T) break;
+    load(r0, t + 3);
+    compute(r1, t + 1);
+    if (t + 2 >= T) break;
+    load(r1, t + 4);
+    compute(r2, t + 2);
+  }
+}
+
+template <int MI, int NJ>
+static hipError_t launch_resident(const float* a, int64_t lda, const float* b, int64_t ldb,
+                                  const float* bias, float* c, int64_t ldc, int64_t m, int n,
+                                  int k, int tiles_n, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_nt_resident<MI, NJ>), dim3((unsigned)grid), dim3(1024), 0, s, a, lda,
+                     b, ldb, bias, c, ldc, m, n, k, tiles_n);
+  return hipGetLastError();
+}
+
+// The resident form for 32 < n <= 256 (two column blocks past 128): MI * NJ
+// <= 8 keeps the accumulators and three chunks of A within 128 registers (16
+// wavefronts a CU).  Workgroups: a whole number of XCD rounds per column
+// block, four per CU for two blocks and two for one (the counts measured
+// best; the LDS holds one at a time, the rest queue).
+static hipError_t dispatch_resident(const float* a, int64_t lda, const float* b, int64_t ldb,
+                                    const float* bias, float* c, int64_t ldc, int64_t m, int n,
+                                    int k, hipStream_t s) {
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int tiles_n = (n + 127) / 128;
+  const int nj = ((n + tiles_n - 1) / tiles_n + 15) / 16;
+  const int per = kXcds * tiles_n;
+  const int grid = std::max(per, (n > 64 ? 4 : 2) * cus / per * per);
+#define GR_RS(MI, NJ) \
+  return launch_resident<MI, NJ>(a, lda, b, ldb, bias, c, ldc, m, n, k, tiles_n, grid, s)
+  switch (nj) {
+    case 3: GR_RS(2, 3);
+    case 4: GR_RS(1, 4);
+    case 5: GR_RS(1, 5);
+    case 6: GR_RS(1, 6);
+    case 7: GR_RS(1, 7);
+    default: GR_RS(1, 8);
+  }
+#undef GR_RS
+}
+
 }  // namespace gr_gemm
 
 extern "C" int gr_gemm_nt(const float* a, int64_t lda, const float* b, int64_t ldb, int64_t m,
@@ -621,7 +790,12 @@ extern "C" int gr_gemm_nt(const float* a, int64_t lda, const float* b, int64_t l
   const bool vb = k % 4 == 0 && ldb % 4 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0;
   hipStream_t s = gr::as_stream(stream);
   hipError_t err;
-  if (k <= 64 && n >= 64 && !(va && vb)) {
+  if (va && vb && k % 32 == 0 && k <= 256 && n > 32 && n <= 256 && n % 4 == 0 && ldc % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(c) % 16 == 0 &&
+      (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0) &&
+      m >= kResidentMinRows) {
+    err = dispatch_resident(a, lda, b, ldb, bias, c, ldc, m, (int)n, (int)k, s);
+  } else if (k <= 64 && n >= 64 && !(va && vb)) {
     // Short reduction with rows of A or B that 16-byte loads cannot take
     // (k or ld not a multiple of 4, as for a 19- or 47-wide gradient): on the
     // vector units as a stream of C's rows (gemm_nt_short_k), 1.3-1.6x faster

@@ -102,4 +102,37 @@ __device__ __forceinline__ float slot_sum(float v) {
   return v;
 }
 
+// 4 x 4 transpose across each lane quad (c = lane & 3): lane c ends with
+// element j = lane j's element c.  Each round swaps, with the partner lane
+// (lane ^ 1, then lane ^ 2), the elements whose index bit differs from the
+// lane's.  A v_mfma_f32_16x16x4_f32 result (lane holds rows 4 (lane / 16) + q
+// of column lane % 16) becomes four consecutive columns of one row per lane.
+__device__ __forceinline__ void quad_transpose(float& v0, float& v1, float& v2, float& v3,
+                                               int c) {
+  {
+    const bool hi = c & 1;
+    const float r0 = dpp<0xB1>(hi ? v0 : v1);  // quad_perm [1,0,3,2]
+    const float r2 = dpp<0xB1>(hi ? v2 : v3);
+    if (hi) {
+      v0 = r0;
+      v2 = r2;
+    } else {
+      v1 = r0;
+      v3 = r2;
+    }
+  }
+  {
+    const bool hi = c & 2;
+    const float r0 = dpp<0x4E>(hi ? v0 : v2);  // quad_perm [2,3,0,1]
+    const float r1 = dpp<0x4E>(hi ? v1 : v3);
+    if (hi) {
+      v0 = r0;
+      v1 = r1;
+    } else {
+      v2 = r0;
+      v3 = r1;
+    }
+  }
+}
+
 }  // namespace gr_wave

@@ -96,7 +96,9 @@ def test_gemm_tn_workspace_checked(gpu):
                                    (2500, 47, 256), (513, 130, 1), (100_003, 256, 19),
                                    (5000, 512, 20), (2001, 602, 47), (64, 64, 31), (1, 256, 63),
                                    (70_001, 256, 256), (65_536, 20, 256), (200_003, 48, 100),
-                                   (66_000, 128, 12), (70_000, 200, 60), (80_000, 4, 40)])
+                                   (66_000, 128, 12), (70_000, 200, 60), (80_000, 4, 40),
+                                   (70_003, 48, 256), (66_001, 100, 256), (65_536, 200, 64),
+                                   (131_071, 64, 32), (70_000, 36, 128)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     """Every tile shape (n > 64, 33..64, 17..32, <= 16), K not a multiple of
@@ -105,7 +107,9 @@ def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     five 128-column blocks, 8-byte and element stores, k just under its 32
     and 64 register limits; row counts past 65536 with one and two column
     tiles, a partial second tile (n = 200), k below one step and not a
-    multiple of the step."""
+    multiple of the step; the resident-B kernel (m >= 65536, k a multiple of
+    32 up to 256, 32 < n <= 256) with one 32-k chunk to eight, one and two
+    column blocks, partial blocks (n = 36, 100, 200) and ragged row blocks."""
     a = _randn(m, k, seed=m + k, dev=gpu)
     b = _randn(n, k, seed=n + k + 1, dev=gpu)
     bv = _randn(n, seed=n, dev=gpu) if bias else None
@@ -147,8 +151,8 @@ def test_gemm_nt_strided_and_in_place(gpu):
         assert torch.equal(buf[:, c0 + 200:], before[:, c0 + 200:])
     with pytest.raises(ValueError, match="out must be"):
         gemm_nt(a, b, out=torch.empty(9000, 199, device=gpu))
-    # 70k rows with strided rows of a and b, a bias, and a column slice of a
-    # wider buffer as out.
+    # 70k rows (the resident-B kernel) with strided rows of a and b, a bias,
+    # and a column slice of a wider buffer as out.
     big_a = _randn(70_000, 300, seed=7, dev=gpu)
     a = big_a[:, 16:272]
     buf = _randn(70_000, 320, seed=8, dev=gpu)
