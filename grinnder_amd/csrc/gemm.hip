@@ -616,8 +616,8 @@ static hipError_t launch_short_k(const float* a, int64_t lda, const float* b, in
 // blocks of one row stream are on one XCD, so A is read from HBM once.  Each
 // lane quad transposes its 4 x 4 blocks, so C leaves the accumulators as
 // 16-byte row stores.  Measured against gemm_nt_kernel on one box: 2.45M x 48
-// x 256 0.69 against 0.80 ms, 2.45M x 256 x 256 2.84 against 2.96 ms; at 20
-// columns the two are equal, so narrower products keep the tiled kernel.
+// x 256 0.69 against 0.80 ms; at 20 columns the two are equal, so narrower
+// products keep the tiled kernel, and wider ones take the 32 x 32 form below.
 constexpr int RS_KST = 256 + 4;  // LDS row stride: 16 lanes' reads fall on distinct banks
 constexpr int RS_WAVES = 16;
 constexpr int64_t kResidentMinRows = 1 << 16;
@@ -735,6 +735,112 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
   }
 }
 
+// The same resident-B product on v_mfma_f32_32x32x2_f32 blocks, for more than
+// 64 columns: a wavefront owns 32 rows and NJ 32-column blocks (lane (r, q) =
+// (lane % 32, lane / 32) loads k = 16 q .. 16 q + 15 of row r's 32-k chunk as
+// four 16-byte pieces and reads the same k of its B column, MFMA s of the
+// chunk summing k = 16 q + s over q), so a lane's operand reads per flop are
+// half the 16 x 16 form's.  One chunk of A ahead.  Measured on one box:
+// 2.45M x 256 x 256 2.70 ms (118.8 TFLOP/s) against 3.00 for the 16 x 16 form
+// and 2.75 for hipBLASLt; 10M x 256 x 256 10.84 against 11.49 ms.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <int NJ>
+__global__ __launch_bounds__(1024) void gemm_nt_resident32(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
+    const float* __restrict__ bias, float* __restrict__ C, int64_t ldc, int64_t M, int N, int K,
+    int tiles_n) {
+  constexpr int NT = 32 * NJ, RB = 32;
+  __shared__ __align__(16) float Bs[NT * RS_KST];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, q = lane >> 5;
+  const int g = blockIdx.x, slot = g / kXcds, tile = slot % tiles_n;
+  const int64_t stream = (int64_t)(slot / tiles_n) * kXcds + g % kXcds;
+  const int64_t nstreams = (int64_t)gridDim.x / tiles_n;
+  const int n0 = tile * NT;
+  const int kq = K / 4;
+  for (int i = tid; i < NT * kq; i += 1024) {
+    const int c = i / kq, k = (i % kq) * 4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n0 + c < N) v = *reinterpret_cast<const float4*>(B + (int64_t)(n0 + c) * ldb + k);
+    *reinterpret_cast<float4*>(&Bs[c * RS_KST + k]) = v;
+  }
+  __syncthreads();
+  const int64_t nblk = (M + RB - 1) / RB;
+  const int64_t step = nstreams * RS_WAVES;
+  const int64_t blk0 = stream * RS_WAVES + wave;
+  if (blk0 >= nblk) return;
+  const int nch = K / 32;
+  const int64_t T = (nblk - blk0 + step - 1) / step * nch;
+  const float* bl = Bs + l32 * RS_KST + 16 * q;
+  const int qc = lane & 3, qa = (lane >> 2) & 7;
+
+  struct A16 {
+    float4 v[4];
+  };
+  auto load = [&](A16& dst, int64_t t) {
+    if (t < T) {
+      const int64_t b = blk0 + (t / nch) * step;
+      const int c = (int)(t % nch);
+      const int64_t r = b * RB + l32;  // rows past M read the block's first
+      const float* p = A + (r < M ? r : b * RB) * lda + c * 32 + 16 * q;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dst.v[u] = *reinterpret_cast<const float4*>(p + 4 * u);
+    }
+  };
+  floatx16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = floatx16{};
+  auto compute = [&](const A16& cur, int64_t t) {
+    const int c = (int)(t % nch);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float4 bv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        bv[u] = *reinterpret_cast<const float4*>(bl + j * 32 * RS_KST + c * 32 + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.v[u].x, bv[u].x, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.v[u].y, bv[u].y, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.v[u].z, bv[u].z, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.v[u].w, bv[u].w, acc[j], 0, 0, 0);
+      }
+    }
+    if (c == nch - 1) {
+      // Lane holds column 32 j + l32, rows 8 (e / 4) + 4 q + e % 4 (e < 16);
+      // after each quad transpose, row 8 gq + 4 q + qc, columns 32 j + 4 qa
+      // .. + 3.
+      const int64_t b = blk0 + (t / nch) * step;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int col = n0 + j * 32 + 4 * qa;
+        const bool cin = col < N;  // N % 4 == 0
+        const float4 bb = cin && bias != nullptr ? *reinterpret_cast<const float4*>(bias + col)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          float v0 = acc[j][4 * gq + 0], v1 = acc[j][4 * gq + 1], v2 = acc[j][4 * gq + 2],
+                v3 = acc[j][4 * gq + 3];
+          gr_wave::quad_transpose(v0, v1, v2, v3, qc);
+          const int64_t row = b * RB + 8 * gq + 4 * q + qc;
+          if (cin && row < M)
+            *reinterpret_cast<float4*>(C + row * ldc + col) =
+                make_float4(v0 + bb.x, v1 + bb.y, v2 + bb.z, v3 + bb.w);
+        }
+        acc[j] = floatx16{};
+      }
+    }
+  };
+  A16 cur, nxt;
+  load(cur, 0);
+  for (int64_t t = 0; t < T; ++t) {
+    load(nxt, t + 1);
+    compute(cur, t);
+    cur = nxt;
+  }
+}
+
 template <int MI, int NJ>
 static hipError_t launch_resident(const float* a, int64_t lda, const float* b, int64_t ldb,
                                   const float* bias, float* c, int64_t ldc, int64_t m, int n,
@@ -744,11 +850,12 @@ static hipError_t launch_resident(const float* a, int64_t lda, const float* b, i
   return hipGetLastError();
 }
 
-// The resident form for 32 < n <= 256 (two column blocks past 128): MI * NJ
-// <= 8 keeps the accumulators and three chunks of A within 128 registers (16
+// The resident forms for 32 < n <= 256: the 32 x 32 form past 64 columns
+// (two column blocks past 128), the 16 x 16 form below, where MI * NJ <= 8
+// keeps its accumulators and three chunks of A within 128 registers (16
 // wavefronts a CU).  Workgroups: a whole number of XCD rounds per column
-// block, four per CU for two blocks and two for one (the counts measured
-// best; the LDS holds one at a time, the rest queue).
+// block, four per CU for the 32 x 32 form and two for the 16 x 16 one (the
+// counts measured best; the LDS holds one at a time, the rest queue).
 static hipError_t dispatch_resident(const float* a, int64_t lda, const float* b, int64_t ldb,
                                     const float* bias, float* c, int64_t ldc, int64_t m, int n,
                                     int k, hipStream_t s) {
@@ -758,20 +865,18 @@ static hipError_t dispatch_resident(const float* a, int64_t lda, const float* b,
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int tiles_n = (n + 127) / 128;
-  const int nj = ((n + tiles_n - 1) / tiles_n + 15) / 16;
-  const int per = kXcds * tiles_n;
-  const int grid = std::max(per, (n > 64 ? 4 : 2) * cus / per * per);
-#define GR_RS(MI, NJ) \
-  return launch_resident<MI, NJ>(a, lda, b, ldb, bias, c, ldc, m, n, k, tiles_n, grid, s)
-  switch (nj) {
-    case 3: GR_RS(2, 3);
-    case 4: GR_RS(1, 4);
-    case 5: GR_RS(1, 5);
-    case 6: GR_RS(1, 6);
-    case 7: GR_RS(1, 7);
-    default: GR_RS(1, 8);
+  if (n > 64) {
+    // 32 x 32 blocks, 128-column blocks of B, four workgroups per CU.
+    const int per = kXcds * tiles_n;
+    const int grid = std::max(per, 4 * cus / per * per);
+    hipLaunchKernelGGL((gemm_nt_resident32<4>), dim3((unsigned)grid), dim3(1024), 0, s, a, lda,
+                       b, ldb, bias, c, ldc, m, n, k, tiles_n);
+    return hipGetLastError();
   }
-#undef GR_RS
+  // 33..64 columns: 16 x 16 blocks, one column block, two workgroups per CU.
+  const int grid = std::max(kXcds, 2 * cus / kXcds * kXcds);
+  if (n <= 48) return launch_resident<2, 3>(a, lda, b, ldb, bias, c, ldc, m, n, k, 1, grid, s);
+  return launch_resident<1, 4>(a, lda, b, ldb, bias, c, ldc, m, n, k, 1, grid, s);
 }
 
 }  // namespace gr_gemm

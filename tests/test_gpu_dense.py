@@ -98,7 +98,7 @@ def test_gemm_tn_workspace_checked(gpu):
                                    (70_001, 256, 256), (65_536, 20, 256), (200_003, 48, 100),
                                    (66_000, 128, 12), (70_000, 200, 60), (80_000, 4, 40),
                                    (70_003, 48, 256), (66_001, 100, 256), (65_536, 200, 64),
-                                   (131_071, 64, 32), (70_000, 36, 128)])
+                                   (131_071, 64, 32), (70_000, 36, 128), (100_000, 128, 32)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     """Every tile shape (n > 64, 33..64, 17..32, <= 16), K not a multiple of
@@ -107,9 +107,10 @@ def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     five 128-column blocks, 8-byte and element stores, k just under its 32
     and 64 register limits; row counts past 65536 with one and two column
     tiles, a partial second tile (n = 200), k below one step and not a
-    multiple of the step; the resident-B kernel (m >= 65536, k a multiple of
-    32 up to 256, 32 < n <= 256) with one 32-k chunk to eight, one and two
-    column blocks, partial blocks (n = 36, 100, 200) and ragged row blocks."""
+    multiple of the step; the resident-B kernels (m >= 65536, k a multiple
+    of 32 up to 256: 16 x 16 blocks for 33..64 columns, 32 x 32 blocks for
+    65..256) with one 32-k chunk to eight, one and two column blocks,
+    partial blocks (n = 36, 100, 200) and ragged row blocks."""
     a = _randn(m, k, seed=m + k, dev=gpu)
     b = _randn(n, k, seed=n + k + 1, dev=gpu)
     bv = _randn(n, seed=n, dev=gpu) if bias else None
