@@ -494,8 +494,8 @@ static hipError_t launch_nt(const float* a, int64_t lda, const float* b, int64_t
 
 // Tile shape by the product's shape, as measured on the dense transform's
 // products (MI355X, fp32):
-//   n > 64, k > 256: 128 x 128 tiles of 16 x 16 blocks, 32-k steps (116 TFLOP/s
-//     for 625k x 256 x 1024);
+//   n > 64, k > 256: 128 x 128 tiles of 32 x 32 blocks, 32-k steps (126-128
+//     TFLOP/s for 625k and 1M x 256 x 1024, against 124 with 16 x 16 blocks);
 //   n > 64, k <= 256: 128 x 128 tiles of 32 x 32 blocks, 16-k double-buffered
 //     steps at 4 waves per SIMD (114-117 TFLOP/s for 2.45M x 256 x 256, and
 //     30% faster than the first form for k = 48 or 20);
@@ -514,7 +514,7 @@ static hipError_t dispatch_nt(const float* a, int64_t lda, const float* b, int64
   return launch_nt<VA, VB, MI, NJ, WMW, KS, BLK, ##__VA_ARGS__>(a, lda, b, ldb, bias, c, ldc, m, n, k, s)
   if (n > 64) {
     if (k <= 256) GR_NT(2, 2, 2, 16, 32, 4, true);
-    GR_NT(4, 4, 2, 32, 16);
+    GR_NT(2, 2, 2, 32, 32);
   }
   if (n > 48) GR_NT(4, 4, 4, 16, 16, 1, true);
   if (n > 32) GR_NT(4, 3, 4, 32, 16);

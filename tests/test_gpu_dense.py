@@ -98,7 +98,8 @@ def test_gemm_tn_workspace_checked(gpu):
                                    (70_001, 256, 256), (65_536, 20, 256), (200_003, 48, 100),
                                    (66_000, 128, 12), (70_000, 200, 60), (80_000, 4, 40),
                                    (70_003, 48, 256), (66_001, 100, 256), (65_536, 200, 64),
-                                   (131_071, 64, 32), (70_000, 36, 128), (100_000, 128, 32)])
+                                   (131_071, 64, 32), (70_000, 36, 128), (100_000, 128, 32),
+                                   (1000, 300, 300), (777, 130, 513), (20_000, 256, 1024)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_nt_matches_fp64(gpu, m, n, k, bias):
     """Every tile shape (n > 64, 33..64, 17..32, <= 16), K not a multiple of
