@@ -419,13 +419,17 @@ def test_fused_epilogues_write_into_output_block(gpu):
                                                      (777, 64, 128, "relu", True, True),
                                                      (995, 32, 192, "elu", False, True),
                                                      (17, 4, 64, "elu", True, False),
-                                                     (0, 48, 256, "relu", True, True)])
+                                                     (0, 48, 256, "relu", True, True),
+                                                     (100_003, 20, 256, "elu", True, True),
+                                                     (70_001, 48, 256, "elu", True, False),
+                                                     (65_537, 64, 128, "elu", False, True)])
 def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias, dot):
     """The LayerNorm/activation backward with dL/dout = dz B formed inside the
     pass, against float64 autograd of act(LayerNorm(h)) with that gradient;
     with `dot`, also rowdot[r] = <dL/dh_r, h_r - shift> (the c_i a GAT
     attention backward takes when its output, shifted by the bias, feeds the
-    LayerNorm)."""
+    LayerNorm).  The large cases give each workgroup many 32-row steps and
+    take ELU, whose derivative has no jump for fp32 rounding to straddle."""
     from grinnder_amd.aggregation import ln_act_backward_product
 
     h = _randn(rows, dim, seed=dim + k, dev=gpu)
