@@ -55,13 +55,16 @@ HBM_PEAK_GBPS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 CALIBRATION_KIB = 1 << 20      # bytes read (and written) by one calibration launch, in KiB
 CALIBRATION_KERNEL = "bitwise_not"
-# PMC summary whose BYTES lines (request-size counters) give roofline.traffic
-# for C2, and the D=256 aggregation kernels of C2 by timer region: the fused
-# forward (CSR + bias + LayerNorm + ReLU) and the CSC backward.
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "c2_gcn_aggregate_traffic.txt")
-C2_DOMINANT = {"gcn_fwd": "aggregate_ln_relu_units<4, 1, 8>",
-               "gcn_bwd": "aggregate_units<4, 64, 1, 8>"}
+# PMC summaries whose BYTES lines (request-size counters) give roofline.traffic
+# per configuration, and the D=256 aggregation kernels of the GCN configurations
+# by timer region: the fused forward (CSR + bias + LayerNorm + ReLU) and the
+# CSC backward.
+_PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+TRAFFIC_PROFILES = {"c2": os.path.join(_PROFILES, "c2_gcn_aggregate_traffic.txt"),
+                    "c4": os.path.join(_PROFILES, "c4_gcn_resident_traffic.txt")}
+TRAFFIC_PROFILE = TRAFFIC_PROFILES["c2"]
+GCN_DOMINANT = {"gcn_fwd": "aggregate_ln_relu_units<4, 1, 8>",
+                "gcn_bwd": "aggregate_units<4, 64, 1, 8>"}
 CONFIGS_NAMES = ("c1", "c2", "c3", "c4", "c5")
 
 
@@ -743,12 +746,13 @@ def main():
                 "algorithmic_bytes": round(dom_bytes / len(dom)),
                 "algorithmic_GBps": round(achieved, 1),
                 "algorithmic_frac": round(achieved / HBM_PEAK_GBPS, 4)}
-    per_kernel = traffic_from_profile(TRAFFIC_PROFILE, C2_DOMINANT.values()) \
-        if args.config == "c2" else None
-    if per_kernel is not None and all(r.name in C2_DOMINANT for r in dom):
+    prof = TRAFFIC_PROFILES.get(args.config)
+    per_kernel = traffic_from_profile(prof, GCN_DOMINANT.values()) \
+        if prof is not None and cfg["hidden"] == 256 else None
+    if per_kernel is not None and all(r.name in GCN_DOMINANT for r in dom):
         # Bytes the memory fabric moved per launch (PMC request-size counters,
         # committed profile) over each launch's HIP-event duration.
-        fabric = sum(per_kernel[C2_DOMINANT[r.name]] for r in dom)
+        fabric = sum(per_kernel[GCN_DOMINANT[r.name]] for r in dom)
         rate = fabric / (dom_ms / 1e3) / 1e9
         roofline.update({
             "achieved": round(rate, 1), "frac": round(rate / HBM_PEAK_GBPS, 4),
@@ -756,7 +760,7 @@ def main():
             "bytes_counted": ("fabric: bytes the L2 fetched from and wrote to the memory "
                               "fabric per launch, from rocprofv3's request-size counters "
                               "(TCC_EA0_RDREQ_32B/64B/128B, TCC_EA0_WRREQ/WRREQ_64B; exact on a "
-                              "1 GiB copy) in profiles/c2_gcn_aggregate_traffic.txt; they "
+                              f"1 GiB copy) in profiles/{os.path.basename(prof)}; they "
                               "include the Infinity Cache's hits, so they bound HBM bytes "
                               "from above; durations are this run's HIP events")})
         log(f"roofline: {fabric / len(dom) / 1e9:.1f} GB fabric traffic per D={cfg['hidden']} "
