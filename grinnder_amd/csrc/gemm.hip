@@ -416,6 +416,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) v
     }
   };
 
+  float bcol[NJ];  // this lane's bias column of each block
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = n0 + wn + j * BLK + lr;
+    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
+  }
+
   NtTile<VA, TM, KS> ta;
   NtTile<VB, TN, KS> tb;
   ta.load(A, lda, m0, M, 0, K);
@@ -460,19 +467,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, 8))) v
 
   // BLK = 16: lane holds column lr, rows 4 lq + r (r < 4).  BLK = 32: lane
   // holds column lr, rows 8 (r / 4) + 4 lq + r % 4 (r < 16).
+  // The bias was loaded before the K loop and is added to every accumulator
+  // ahead of the stores: a load consumed between guarded stores would make
+  // each store wait for all earlier ones (the vector-memory counter retires
+  // in issue order).
   constexpr int RPL = BLK == 16 ? 4 : 16;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) acc[i][j][r] += bcol[j];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int n = n0 + wn + j * BLK + lr;
     if (n >= N) continue;
-    const float bn = bias != nullptr ? bias[n] : 0.f;
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int r = 0; r < RPL; ++r) {
         const int row = BLK == 16 ? lq * 4 + r : (r / 4) * 8 + lq * 4 + r % 4;
         const int64_t m = m0 + wm + i * BLK + row;
-        if (m < M) C[m * ldc + n] = acc[i][j][r] + bn;
+        if (m < M) C[m * ldc + n] = acc[i][j][r];
       }
   }
 }
@@ -657,6 +673,14 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
   const int64_t T = (nblk - blk0 + step - 1) / step * nch;
   const int qc = lane & 3, qa = (lane >> 2) & 3;
   const float* bl = Bs + lr * RS_KST + 8 * lk;
+  // The bias of this lane's column of each block, loaded once: it is added to
+  // the accumulators before the stores, so no store waits on a load.
+  float bcol[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = n0 + j * 16 + lr;
+    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
+  }
 
   auto load = [&](A8 (&dst)[MI], int64_t t) {
     if (t < T) {
@@ -703,16 +727,14 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
       for (int j = 0; j < NJ; ++j) {
         const int col = n0 + j * 16 + 4 * qa;
         const bool cin = col < N;  // N % 4 == 0: the four columns are in or out together
-        const float4 bb = cin && bias != nullptr ? *reinterpret_cast<const float4*>(bias + col)
-                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
-          float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
+          float v0 = acc[i][j][0] + bcol[j], v1 = acc[i][j][1] + bcol[j],
+                v2 = acc[i][j][2] + bcol[j], v3 = acc[i][j][3] + bcol[j];
           gr_wave::quad_transpose(v0, v1, v2, v3, qc);
           const int64_t row = b * RB + i * 16 + 4 * lk + qc;
           if (cin && row < M)
-            *reinterpret_cast<float4*>(C + row * ldc + col) =
-                make_float4(v0 + bb.x, v1 + bb.y, v2 + bb.z, v3 + bb.w);
+            *reinterpret_cast<float4*>(C + row * ldc + col) = make_float4(v0, v1, v2, v3);
           acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
       }
@@ -774,6 +796,14 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident32(
   const int64_t T = (nblk - blk0 + step - 1) / step * nch;
   const float* bl = Bs + l32 * RS_KST + 16 * q;
   const int qc = lane & 3, qa = (lane >> 2) & 7;
+  // The bias of this lane's column of each block, loaded once (as in
+  // gemm_nt_resident).
+  float bcol[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = n0 + j * 32 + l32;
+    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
+  }
 
   struct A16 {
     float4 v[4];
@@ -816,17 +846,14 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident32(
       for (int j = 0; j < NJ; ++j) {
         const int col = n0 + j * 32 + 4 * qa;
         const bool cin = col < N;  // N % 4 == 0
-        const float4 bb = cin && bias != nullptr ? *reinterpret_cast<const float4*>(bias + col)
-                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
-          float v0 = acc[j][4 * gq + 0], v1 = acc[j][4 * gq + 1], v2 = acc[j][4 * gq + 2],
-                v3 = acc[j][4 * gq + 3];
+          float v0 = acc[j][4 * gq + 0] + bcol[j], v1 = acc[j][4 * gq + 1] + bcol[j],
+                v2 = acc[j][4 * gq + 2] + bcol[j], v3 = acc[j][4 * gq + 3] + bcol[j];
           gr_wave::quad_transpose(v0, v1, v2, v3, qc);
           const int64_t row = b * RB + 8 * gq + 4 * q + qc;
           if (cin && row < M)
-            *reinterpret_cast<float4*>(C + row * ldc + col) =
-                make_float4(v0 + bb.x, v1 + bb.y, v2 + bb.z, v3 + bb.w);
+            *reinterpret_cast<float4*>(C + row * ldc + col) = make_float4(v0, v1, v2, v3);
         }
         acc[j] = floatx16{};
       }
@@ -1076,6 +1103,190 @@ __global__ __launch_bounds__(256) void linear_ln_act_kernel(
   }
 }
 
+// Resident form of the same transform for dout = 256 and 16-byte rows of x
+// with din <= 100 (the aggregate-first layer 0 of a 100-feature graph).  One
+// workgroup of 12 (ELU: 8) wavefronts per CU keeps W (as [column][k], row stride ks
+// with ks / 4 odd, so the 16 columns a quarter-wavefront reads with
+// ds_read_b128 fall on distinct banks), bias, gamma and beta in LDS for the
+// launch; each wavefront then walks 16-row blocks on its own, with no
+// workgroup barrier:
+//   - the next block's rows of x are loaded into registers before this
+//     block's MFMAs, as 16-byte pieces (lane quarter lk takes k = 16 g +
+//     4 lk .. + 3 of 16-k group g), turned by a 4 x 4 transpose across the
+//     lane quarters into the order linear_ln_act_kernel sums in (step j of
+//     group g: k = 16 g + 4 j + lk), with W's groups stored transposed to
+//     match, so the two kernels give the same bits; the din % 16 tail takes
+//     k = 16 G + 4 j + lk directly, one 4-byte load a step;
+//   - the epilogue reads its parameters from LDS, not from global memory:
+//     the vector-memory counter retires in issue order, so a global load
+//     issued after the block's stores would hold the wavefront until those
+//     stores had completed.  Only the next block's loads precede them, so
+//     the stores drain while the next block's MFMAs run.
+// Rows are staged four at a time in the wavefront's own LDS rows and stored
+// as 16-byte pieces of whole rows, as in linear_ln_act_kernel.
+constexpr int LR_DOUT = 256;
+constexpr int LR_STAGE = LR_DOUT + 16;  // staged row stride (floats)
+constexpr int LR_GMAX = 6;              // 16-k groups held in registers: din <= 100
+constexpr int LR_KS_MAX = 100;
+// Wavefronts per workgroup: 12 (three per SIMD) fit ReLU's registers; ELU's
+// expm1f needs more, so it runs eight.
+template <int ACT>
+constexpr int lr_waves() {
+  return ACT == GR_ACT_RELU ? 12 : 8;
+}
+
+// LDS row stride for din (a multiple of 4): din itself when din / 4 is odd,
+// else din + 4.
+inline int lr_row_stride(int din) { return (din / 4) % 2 ? din : din + 4; }
+
+template <int ACT, int LR_WAVES = lr_waves<ACT>()>
+__global__ __launch_bounds__(LR_WAVES * 64) void linear_ln_act_resident(
+    const float* __restrict__ x, int64_t ldx, int64_t rows, int din, int ks,
+    const float* __restrict__ wt, const float* __restrict__ bias,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+    float* __restrict__ h, float* __restrict__ out, float* __restrict__ mean,
+    float* __restrict__ rstd) {
+  constexpr int NB = LR_DOUT / 16;
+  constexpr int LR_LDS = LR_DOUT * LR_KS_MAX + 3 * LR_DOUT + LR_WAVES * 4 * LR_STAGE;
+  __shared__ __align__(16) float lds[LR_LDS];
+  float* Ws = lds;                          // Ws[c * ks + k] = W^T[k][c]
+  float* par = lds + LR_DOUT * LR_KS_MAX;   // bias | gamma | beta
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  const int G = din >> 4, tail = (din & 15) >> 2;
+  for (int i = tid; i < din * LR_DOUT; i += LR_WAVES * 64) {
+    const int k = i / LR_DOUT, c = i % LR_DOUT;
+    // Inside each full 16-k group, k = 16 g + 4 b + a sits at 16 g + 4 a + b:
+    // a lane's ds_read_b128 at 16 g + 4 lk gives k = 16 g + 4 j + lk in
+    // component j.
+    const int p = k < 16 * G ? (k & ~15) | ((k & 3) << 2) | ((k >> 2) & 3) : k;
+    Ws[c * ks + p] = wt[i];
+  }
+  for (int i = tid; i < LR_DOUT; i += LR_WAVES * 64) {
+    par[i] = bias != nullptr ? bias[i] : 0.f;
+    par[LR_DOUT + i] = gamma[i];
+    par[2 * LR_DOUT + i] = beta[i];
+  }
+  __syncthreads();
+
+  float* stage = lds + LR_DOUT * LR_KS_MAX + 3 * LR_DOUT + wave * 4 * LR_STAGE;
+  const int64_t nblk = (rows + 15) / 16;
+  const int64_t step = (int64_t)gridDim.x * LR_WAVES;
+  const float* wl = Ws + lr * ks;
+
+  struct XR {
+    float4 v[LR_GMAX];
+    float t[3];
+  };
+  auto load = [&](XR& d, int64_t blk) {
+    if (blk >= nblk) return;
+    int64_t r = blk * 16 + lr;
+    if (r >= rows) r = rows - 1;  // read a valid row; its results are not stored
+    const float* p = x + r * ldx;
+#pragma unroll
+    for (int g = 0; g < LR_GMAX; ++g)
+      if (g < G) d.v[g] = *reinterpret_cast<const float4*>(p + 16 * g + 4 * lk);
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < tail) d.t[j] = p[16 * G + lk + 4 * j];
+  };
+
+  XR cur, nxt;
+  int64_t blk = (int64_t)blockIdx.x * LR_WAVES + wave;
+  load(cur, blk);
+  const float inv_d = 1.0f / (float)LR_DOUT;
+  for (; blk < nblk; blk += step) {
+    load(nxt, blk + step);
+    floatx4 acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < LR_GMAX; ++g) {
+      if (g < G) {
+        // Lane (lr, lk) loaded k = 16 g + 4 lk .. + 3 of its row; after the
+        // transpose its component j is k = 16 g + 4 j + lk, the k that lane
+        // quarter lk takes in step j of linear_ln_act_kernel's 16-k chunk,
+        // so both kernels sum the same products in the same order.
+        gr_wave::row_transpose4(cur.v[g]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float4 bw = *reinterpret_cast<const float4*>(wl + b * 16 * ks + 16 * g + 4 * lk);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.v[g].x, bw.x, acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.v[g].y, bw.y, acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.v[g].z, bw.z, acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.v[g].w, bw.w, acc[b], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      if (j < tail) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              cur.t[j], wl[b * 16 * ks + 16 * G + lk + 4 * j], acc[b], 0, 0, 0);
+      }
+    }
+
+    // Lane holds rows 4 lk + q of the block, columns 16 b + lr.
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float bb = par[b * 16 + lr];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[b][q] += bb;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t row = blk * 16 + lk * 4 + q;
+      float s = 0.f;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) s += acc[b][q];
+      s = gr_wave::group_sum<16>(s);
+      const float mu = s * inv_d;
+      float v = 0.f;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float dlt = acc[b][q] - mu;
+        v += dlt * dlt;
+      }
+      v = gr_wave::group_sum<16>(v);
+      const float rs = 1.0f / sqrtf(v * inv_d + eps);
+      // The wavefront's LDS operations complete in issue order, so this
+      // stage's writes follow the previous q's reads without a barrier.
+#pragma unroll
+      for (int b = 0; b < NB; ++b) stage[lk * LR_STAGE + b * 16 + lr] = acc[b][q];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (row < rows) {
+        const float* srow = stage + lk * LR_STAGE;
+#pragma unroll
+        for (int i = 0; i < LR_DOUT / 64; ++i) {
+          const int c = lr * 4 + 64 * i;
+          const float4 hv = *reinterpret_cast<const float4*>(srow + c);
+          const float4 gg = *reinterpret_cast<const float4*>(par + LR_DOUT + c);
+          const float4 bt = *reinterpret_cast<const float4*>(par + 2 * LR_DOUT + c);
+          float4 o;
+          o.x = lt_act<ACT>(fmaf((hv.x - mu) * rs, gg.x, bt.x));
+          o.y = lt_act<ACT>(fmaf((hv.y - mu) * rs, gg.y, bt.y));
+          o.z = lt_act<ACT>(fmaf((hv.z - mu) * rs, gg.z, bt.z));
+          o.w = lt_act<ACT>(fmaf((hv.w - mu) * rs, gg.w, bt.w));
+          *reinterpret_cast<float4*>(h + row * LR_DOUT + c) = hv;
+          *reinterpret_cast<float4*>(out + row * LR_DOUT + c) = o;
+        }
+        if (lr == 0) {
+          mean[row] = mu;
+          rstd[row] = rs;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    cur = nxt;
+  }
+}
+
 }  // namespace gr_gemm
 
 extern "C" int gr_linear_ln_act(const float* x, int64_t ldx, int64_t rows, int64_t din,
@@ -1098,6 +1309,24 @@ extern "C" int gr_linear_ln_act(const float* x, int64_t ldx, int64_t rows, int64
   const int64_t blocks = (rows + LT_ROWS - 1) / LT_ROWS;
   GR_REQUIRE(blocks <= INT32_MAX, "linear_ln_act: too many rows");
   hipStream_t s = gr::as_stream(stream);
+  if (dout == LR_DOUT && din % 4 == 0 && din <= LR_KS_MAX &&
+      lr_row_stride((int)din) <= LR_KS_MAX && ldx % 4 == 0 && al16(x) &&
+      rows >= kResidentMinRows) {
+    int dev = 0, cus = 0;
+    GR_HIP_CHECK(hipGetDevice(&dev));
+    GR_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    // One workgroup per CU (the LDS holds one).
+    if (act == GR_ACT_RELU)
+      hipLaunchKernelGGL((linear_ln_act_resident<GR_ACT_RELU>), dim3((unsigned)cus),
+                         dim3(lr_waves<GR_ACT_RELU>() * 64), 0, s, x, ldx, rows, (int)din,
+                         lr_row_stride((int)din), wt, bias, gamma, beta, eps, h, out, mean, rstd);
+    else
+      hipLaunchKernelGGL((linear_ln_act_resident<GR_ACT_ELU>), dim3((unsigned)cus),
+                         dim3(lr_waves<GR_ACT_ELU>() * 64), 0, s, x, ldx, rows, (int)din,
+                         lr_row_stride((int)din), wt, bias, gamma, beta, eps, h, out, mean, rstd);
+    GR_HIP_CHECK(hipGetLastError());
+    return GR_OK;
+  }
   const int nb = (int)(dout / 16);
 #define GR_LT(NB)                                                                              \
   do {                                                                                         \

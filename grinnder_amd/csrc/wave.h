@@ -102,6 +102,36 @@ __device__ __forceinline__ float slot_sum(float v) {
   return v;
 }
 
+// 4 x 4 transpose across the wavefront's four 16-lane rows: afterwards
+// component j of lane l of row r holds what component r of lane l of row j
+// held.  One round of v_permlane32_swap (rows 0-1 against 2-3) on the
+// component pairs (x, z), (y, w), one of v_permlane16_swap (rows 0, 2
+// against 1, 3) on (x, y), (z, w).
+// (The result's elements are copied to ints before the bit casts: a bit cast
+// of a vector element read element 0's storage for both with this compiler.)
+__device__ __forceinline__ void swap_rows32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a),
+                                                  __builtin_bit_cast(int, b), false, false);
+  const int r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);  // rows (a0, a1, b0, b1)
+  b = __builtin_bit_cast(float, r1);  // rows (a2, a3, b2, b3)
+}
+
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, a),
+                                                  __builtin_bit_cast(int, b), false, false);
+  const int r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);  // rows (a0, b0, a2, b2)
+  b = __builtin_bit_cast(float, r1);  // rows (a1, b1, a3, b3)
+}
+
+__device__ __forceinline__ void row_transpose4(float4& v) {
+  swap_rows32(v.x, v.z);
+  swap_rows32(v.y, v.w);
+  swap_rows16(v.x, v.y);
+  swap_rows16(v.z, v.w);
+}
+
 // 4 x 4 transpose across each lane quad (c = lane & 3): lane c ends with
 // element j = lane j's element c.  Each round swaps, with the partner lane
 // (lane ^ 1, then lane ^ 2), the elements whose index bit differs from the

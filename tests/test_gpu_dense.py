@@ -337,7 +337,13 @@ def test_gat_layer_row_dot_handoff(gpu):
     # rounding of 0 and take the other slope in the float64 reference, a
     # difference of the test, not of the kernel.
     (70001, 100, 256, "elu"), (33, 4, 256, "elu"), (1000, 12, 256, "elu"),
-    (517, 128, 256, "elu"), (1, 24, 256, "relu"), (16, 16, 256, "relu")])
+    (517, 128, 256, "elu"), (1, 24, 256, "relu"), (16, 16, 256, "relu"),
+    # The resident form (dout 256, din <= 100 a multiple of 4, >= 65536
+    # rows): 16-k groups with tails of 0-3 four-k steps (din 96: LDS row
+    # stride 100; 92: 92; 64: 68; 8 and 4: tail only), row counts a multiple
+    # of 16 and ragged.
+    (65536, 92, 256, "elu"), (100_003, 96, 256, "elu"), (66_000, 8, 256, "elu"),
+    (65_537, 64, 256, "elu"), (70_001, 4, 256, "elu")])
 def test_linear_ln_act_matches_fp64(gpu, rows, din, dout, act):
     """act(LayerNorm(x Wᵀ + b)) with the LayerNorm in the MFMA GEMM epilogue."""
     from grinnder_amd.dense import linear_ln_act
@@ -360,6 +366,27 @@ def test_linear_ln_act_matches_fp64(gpu, rows, din, dout, act):
     assert max_abs_norm_err(out, ref) <= TOL
     for got, want in zip((x, w, b, gamma, beta), ps):
         assert max_abs_norm_err(got.grad, want.grad) <= TOL
+
+
+@pytest.mark.parametrize("din,act", [(100, "relu"), (92, "elu"), (8, "relu"), (64, "relu")])
+def test_linear_ln_act_resident_form_matches_tiled_form_bit_for_bit(gpu, din, act):
+    """The resident form (taken from 65536 rows) sums the same products in
+    the same order as the tiled kernel (taken below), and rows are
+    independent: the first and last 1000 rows of a 70,001-row call equal
+    1000-row calls on those rows bit for bit."""
+    from grinnder_amd.dense import linear_ln_act
+    rows = 70_001
+    x = _randn(rows, din, seed=din + 7, dev=gpu)
+    w = 0.2 * _randn(256, din, seed=5, dev=gpu)
+    b = _randn(256, seed=6, dev=gpu)
+    gamma = 1 + 0.1 * _randn(256, seed=7, dev=gpu)
+    beta = 0.1 * _randn(256, seed=8, dev=gpu)
+    with torch.no_grad():
+        full = linear_ln_act(x, w, b, gamma, beta, 1e-5, act)
+        head = linear_ln_act(x[:1000].contiguous(), w, b, gamma, beta, 1e-5, act)
+        tail = linear_ln_act(x[-1000:].contiguous(), w, b, gamma, beta, 1e-5, act)
+    assert torch.equal(full[:1000], head)
+    assert torch.equal(full[-1000:], tail)
 
 
 def test_fused_epilogues_write_into_output_block(gpu):
