@@ -1,10 +1,11 @@
 // Weight-gradient GEMM for the dense per-layer transform: C[M,N] = A^T B with
 // A [K, M] and B [K, N] row-major and K (the node count) in the millions,
 // M, N <= a few hundred.  fp32 on the gfx950 matrix cores
-// (v_mfma_f32_16x16x4_f32), deterministic split-K.
+// (v_mfma_f32_16x16x4_f32 or v_mfma_f32_32x32x2_f32), deterministic split-K.
 //
 // Workgroup tile 128 x 128 (4 wavefronts as 2 x 2 tiles of 64 x 64, each
-// 4 x 4 MFMA blocks of 16 x 16); K is walked in steps of 16 rows staged in LDS,
+// 4 x 4 MFMA blocks of 16 x 16 or 2 x 2 of 32 x 32); K is walked in steps of
+// 16 rows staged in LDS,
 // with the next step's global loads issued before the current step's MFMAs.
 // Workgroup (tile t, chunk z) owns the K rows [z*kchunk, (z+1)*kchunk) and
 // writes its partial tile to part[z]; the partials are then summed over z in
@@ -23,6 +24,7 @@
 namespace gr_gemm {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int TM = 128;
 constexpr int TN = 128;
@@ -64,8 +66,8 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ src, int64_t
   }
 }
 
-template <int VEC, int W>
-__device__ __forceinline__ void store_tile(float (*lds)[W + PAD], const float (&r)[W / 16]) {
+template <int VEC, int W, int P = PAD>
+__device__ __forceinline__ void store_tile(float (*lds)[W + P], const float (&r)[W / 16]) {
   const int tid = threadIdx.x;
   if constexpr (VEC == 4) {
     constexpr int Q = W / 4;
@@ -87,18 +89,33 @@ __device__ __forceinline__ void store_tile(float (*lds)[W + PAD], const float (&
 }
 
 constexpr int kXcds = 8;
+// Largest K the split-K weight-gradient product runs on 32 x 32 blocks with
+// 128-column tiles (64-column tiles always take them).  Measured on one box:
+// at K = 2.45M the 32 x 32 form is level at 256 x 256 and 10% faster at
+// 256 x 100 (11% for 64-column tiles, 48 x 256); at K = 10M it is 2-3%
+// slower (256 x 256 and 256 x 1024).
+constexpr int64_t kTn32MaxK = int64_t(1) << 22;
 
 // BN = 128, 64 or 32 output columns per workgroup (64 and 32 for narrow N;
-// 32 takes B with 4-byte loads).
-template <int VA, int VB, int BN>
+// 32 takes B with 4-byte loads).  BLK = 16: each wavefront's 64 x BN/2 tile
+// as 16 x 16 blocks of v_mfma_f32_16x16x4_f32; BLK = 32: as 32 x 32 blocks of
+// v_mfma_f32_32x32x2_f32 (BN 64 or 128), with rows of the LDS tiles 32 floats
+// apart mod 64 banks so the two k rows a 32x32x2 step reads fall on
+// distinct banks.
+template <int VA, int VB, int BN, int BLK = 16>
 __global__ __launch_bounds__(256) void gemm_tn_splitk(const float* __restrict__ A, int64_t lda,
                                                       const float* __restrict__ B, int64_t ldb,
                                                       int M, int N, int64_t K, int64_t kchunk,
                                                       int nchunks, int tiles_m, int tiles,
                                                       float* __restrict__ part) {
-  constexpr int NJ = BN / 32;  // 16-column blocks per wavefront
-  __shared__ float As[TK][TM + PAD];
-  __shared__ float Bs[TK][BN + PAD];
+  static_assert(BLK == 16 || (BLK == 32 && BN >= 64), "32 x 32 blocks need 64+ columns");
+  constexpr int P = BLK == 16 ? PAD : 32;
+  constexpr int MI = 64 / BLK;          // row blocks per wavefront
+  constexpr int NJ = BN / 2 / BLK;      // column blocks per wavefront
+  constexpr int KSTEP = 64 / BLK;       // k per MFMA: 4 or 2
+  typedef typename std::conditional<BLK == 16, floatx4, floatx16>::type accx;
+  __shared__ float As[TK][TM + P];
+  __shared__ float Bs[TK][BN + P];
   const int w = blockIdx.x;
   const int q = w / kXcds;
   const int t = q % tiles;
@@ -112,52 +129,59 @@ __global__ __launch_bounds__(256) void gemm_tn_splitk(const float* __restrict__ 
   const int wave = threadIdx.x >> 6;
   const int wm = (wave & 1) * 64;
   const int wn = (wave >> 1) * (BN / 2);
-  const int lr = lane & 15;  // row (A) / column (B) inside a 16-block
-  const int lk = lane >> 4;  // k inside a 4-step
+  const int lr = lane % BLK;  // row (A) / column (B) inside a block
+  const int lk = lane / BLK;  // k inside an MFMA step
 
-  floatx4 acc[4][NJ];
+  accx acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = accx{};
 
   float ra[TM / 16], rb[BN / 16];
   load_tile<VA, TM>(A, lda, k_begin, k_end, m0, M, ra);
   load_tile<VB, BN>(B, ldb, k_begin, k_end, n0, N, rb);
   for (int64_t k = k_begin; k < k_end; k += TK) {
     __syncthreads();  // previous step's MFMA reads of the LDS tiles are done
-    store_tile<VA, TM>(As, ra);
-    store_tile<VB, BN>(Bs, rb);
+    store_tile<VA, TM, P>(As, ra);
+    store_tile<VB, BN, P>(Bs, rb);
     __syncthreads();
     if (k + TK < k_end) {
       load_tile<VA, TM>(A, lda, k + TK, k_end, m0, M, ra);
       load_tile<VB, BN>(B, ldb, k + TK, k_end, n0, N, rb);
     }
 #pragma unroll
-    for (int kk = 0; kk < TK; kk += 4) {
-      float a[4], b[NJ];
+    for (int kk = 0; kk < TK; kk += KSTEP) {
+      float a[MI], b[NJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[kk + lk][wm + i * 16 + lr];
+      for (int i = 0; i < MI; ++i) a[i] = As[kk + lk][wm + i * BLK + lr];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) b[j] = Bs[kk + lk][wn + j * 16 + lr];
+      for (int j = 0; j < NJ; ++j) b[j] = Bs[kk + lk][wn + j * BLK + lr];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NJ; ++j) {
+          if constexpr (BLK == 16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
     }
   }
 
-  // 16x16 result block: lane holds column lr, rows 4*lk + r (r = 0..3).
+  // BLK = 16: lane holds column lr, rows 4 lk + r (r < 4).  BLK = 32: lane
+  // holds column lr, rows 8 (r / 4) + 4 lk + r % 4 (r < 16).
+  constexpr int RPL = BLK == 16 ? 4 : 16;
   float* out = part + (int64_t)z * M * N;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int n = n0 + wn + j * 16 + lr;
+      const int n = n0 + wn + j * BLK + lr;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + i * 16 + lk * 4 + r;
+      for (int r = 0; r < RPL; ++r) {
+        const int row = BLK == 16 ? lk * 4 + r : (r / 4) * 8 + lk * 4 + r % 4;
+        const int m = m0 + wm + i * BLK + row;
         if (m < M && n < N) out[(int64_t)m * N + n] = acc[i][j][r];
       }
     }
@@ -253,17 +277,25 @@ extern "C" int gr_gemm_tn(const float* a, int64_t lda, const float* b, int64_t l
   const int64_t nwg = (used + kXcds - 1) / kXcds * kXcds * tiles;
   GR_REQUIRE(nwg <= INT32_MAX, "gemm_tn: too many workgroups");
   const dim3 grid((unsigned)nwg);
-#define GR_GT(VA_, VB_, BN_)                                                                   \
-  hipLaunchKernelGGL((gemm_tn_splitk<VA_, VB_, BN_>), grid, dim3(256), 0, s, pa, plda, pb, pldb, \
-                     (int)pm, (int)pn, k, kchunk, (int)used, tiles_m, tiles, workspace)
+#define GR_GT(VA_, VB_, BN_, BLK_)                                                             \
+  hipLaunchKernelGGL((gemm_tn_splitk<VA_, VB_, BN_, BLK_>), grid, dim3(256), 0, s, pa, plda, pb, \
+                     pldb, (int)pm, (int)pn, k, kchunk, (int)used, tiles_m, tiles, workspace)
+  // 32 x 32 blocks for 64-column tiles, and for 128-column tiles up to
+  // kTn32MaxK rows of K; 16 x 16 for 32-column tiles.
+  const bool b32 = k <= kTn32MaxK;
   if (narrow32) {
-    if (va) GR_GT(4, 1, 32); else GR_GT(1, 1, 32);
+    if (va) GR_GT(4, 1, 32, 16); else GR_GT(1, 1, 32, 16);
   } else if (narrow) {
-    if (va && vb) GR_GT(4, 4, 64); else if (va) GR_GT(4, 1, 64);
-    else if (vb) GR_GT(1, 4, 64); else GR_GT(1, 1, 64);
+    if (va && vb) GR_GT(4, 4, 64, 32); else if (va) GR_GT(4, 1, 64, 32);
+    else if (vb) GR_GT(1, 4, 64, 32); else GR_GT(1, 1, 64, 32);
   } else {
-    if (va && vb) GR_GT(4, 4, 128); else if (va) GR_GT(4, 1, 128);
-    else if (vb) GR_GT(1, 4, 128); else GR_GT(1, 1, 128);
+    if (b32) {
+      if (va && vb) GR_GT(4, 4, 128, 32); else if (va) GR_GT(4, 1, 128, 32);
+      else if (vb) GR_GT(1, 4, 128, 32); else GR_GT(1, 1, 128, 32);
+    } else {
+      if (va && vb) GR_GT(4, 4, 128, 16); else if (va) GR_GT(4, 1, 128, 16);
+      else if (vb) GR_GT(1, 4, 128, 16); else GR_GT(1, 1, 128, 16);
+    }
   }
 #undef GR_GT
   GR_HIP_CHECK(hipGetLastError());
@@ -345,8 +377,6 @@ struct NtTile {
     }
   }
 };
-
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // BLK = 16: v_mfma_f32_16x16x4_f32 blocks; lane (r, q) = (lane % 16, lane / 16)
 // reads k = 4q .. 4q + 3 of a 16-k slice.  BLK = 32: v_mfma_f32_32x32x2_f32
@@ -765,8 +795,6 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
 // half the 16 x 16 form's.  One chunk of A ahead.  Measured on one box:
 // 2.45M x 256 x 256 2.70 ms (118.8 TFLOP/s) against 3.00 for the 16 x 16 form
 // and 2.75 for hipBLASLt; 10M x 256 x 256 10.84 against 11.49 ms.
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
 template <int NJ>
 __global__ __launch_bounds__(1024) void gemm_nt_resident32(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,

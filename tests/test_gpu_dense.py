@@ -27,7 +27,10 @@ def _randn(*shape, seed, dev):
                                    (30_000, 19, 256), (5000, 32, 300), (777, 130, 3)])
 def test_gemm_tn_matches_fp64(gpu, k, m, n):
     """Covers 128-, 64- and 32-column tiles and the transposed narrow path
-    (m <= 64 < n), 32-column tiles with 4-byte loads of the narrow side."""
+    (m <= 64 < n), 32-column tiles with 4-byte loads of the narrow side.  At
+    these K the 128- and 64-column tiles run on 32 x 32 blocks (ragged at
+    130 x 129); the 16 x 16 form of the 128-column tiles is taken past
+    2^22 rows (the K = 10M test below)."""
     a = _randn(k, m, seed=k + m, dev=gpu)
     b = _randn(k, n, seed=k + n + 1, dev=gpu)
     c = gemm_tn(a, b)
