@@ -61,6 +61,7 @@ CALIBRATION_KERNEL = "bitwise_not"
 # CSC backward.
 _PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 TRAFFIC_PROFILES = {"c2": os.path.join(_PROFILES, "c2_gcn_aggregate_traffic.txt"),
+                    "c3": os.path.join(_PROFILES, "c3_gcn_traffic.txt"),
                     "c4": os.path.join(_PROFILES, "c4_gcn_resident_traffic.txt")}
 TRAFFIC_PROFILE = TRAFFIC_PROFILES["c2"]
 GCN_DOMINANT = {"gcn_fwd": "aggregate_ln_relu_units<4, 1, 8>",
