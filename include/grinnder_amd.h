@@ -426,9 +426,11 @@ int gr_gemm_nt(const float* a, int64_t lda, const float* b, int64_t ldb,
  * transposed [dout, din] weight), dout a multiple of 16 in [16, 256]; h, out
  * dense [rows, dout]; gamma, beta, h and out 16-byte aligned.  fp32 on the matrix cores.  The
  * epilogue's expressions are those of gr_bias_ln_act, so gr_ln_act_backward is
- * its backward.  Replaces the Linear of an aggregate-first GCNConv (PyG
- * GCNConv's lin, grinnder/nn/gcn.py:53-56) followed by the LayerNorm and ReLU
- * of grinnder/nn/gcn.py:64-72. */
+ * its backward.  A row's result does not depend on the row count (the
+ * large-row form keeps W in LDS and sums in the same order, same bits).
+ * Replaces the Linear of an aggregate-first GCNConv (PyG GCNConv's lin,
+ * grinnder/nn/gcn.py:53-56) followed by the LayerNorm and ReLU of
+ * grinnder/nn/gcn.py:64-72. */
 int gr_linear_ln_act(const float* x, int64_t ldx, int64_t rows, int64_t din,
                      const float* wt, int64_t dout, const float* bias,
                      const float* gamma, const float* beta, float eps, int32_t act,
