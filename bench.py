@@ -436,7 +436,21 @@ def locality_free_control(num_nodes: int, nnz: int, dim: int, device: str,
     gb = (2 * n * dim * 4 + n * 8) / min(times) / 1e6
     out["random_row_gather_GBps"] = round(gb, 1)
     out["frac_of_random_gather"] = round(out["algorithmic_GBps"] / gb, 4)
-    del x, rows
+    del rows
+    # The same box's streaming rate next to the 8 TB/s peak: a device-to-device
+    # copy of the same 8 GiB (torch's copy kernel), bytes read and written.
+    dst = torch.empty_like(x)
+    dst.copy_(x)
+    times = []
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(x)
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    out["device_copy_GBps"] = round(2 * x.numel() * 4 / min(times) / 1e6, 1)
+    del x, dst
     torch.cuda.empty_cache()
     return out
 
