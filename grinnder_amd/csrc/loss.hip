@@ -100,6 +100,31 @@ __global__ __launch_bounds__(256) void xent_rows_small(const float* __restrict__
     } else {
       for (int i = threadIdx.x; i < n; i += 256) tile[i] = src[i];
     }
+  } else if ((ld & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    // Rows of a wider, 16-byte aligned buffer (logits held zero-padded to a
+    // multiple of 4 columns): each row's first C columns, as independent
+    // 16-byte pieces, several in flight per thread.  A piece that reaches
+    // past column C - 1 is read element by element up to it, so no read
+    // leaves the C columns of a row.
+    const float* src = x + row0 * ld;
+    const int q = (int)(ld >> 2);  // pieces per row
+    const int n4 = nr * q;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += 256) {
+      const int r = i / q, c = (i - r * q) * 4;
+      if (c >= C) continue;
+      const float* p = src + (int64_t)r * ld + c;
+      float* trow = tile + r * CP + c;
+      if (c + 4 <= C) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        trow[0] = v.x;
+        trow[1] = v.y;
+        trow[2] = v.z;
+        trow[3] = v.w;
+      } else {
+        for (int j = 0; c + j < C; ++j) trow[j] = p[j];
+      }
+    }
   } else {
     // (r, c) of element i advance by (256 / C, 256 % C) per step.
     const int dq = 256 / C, dr = 256 - dq * C;

@@ -49,6 +49,33 @@ def test_masked_xent_matches_fp64(gpu, rows, classes, reduction):
     assert st == [int(tr.sum()), vc, vn, tc, tn, 0]
 
 
+@pytest.mark.parametrize("rows,classes,ld", [(20_003, 47, 48), (4_000, 19, 20), (777, 10, 12),
+                                             (300, 3, 4), (513, 47, 52)])
+def test_padded_logit_rows_match_fp64(gpu, rows, classes, ld):
+    """Logits held zero-padded to a multiple of 4 columns (the trainer's
+    [rows, 48] and [rows, 20] blocks): the first `classes` columns of a
+    16-byte aligned [rows, ld] buffer, read as 16-byte pieces.  The buffer
+    ends at the last row's last class (no pad after it), and its pad
+    columns hold large values that must not reach the loss."""
+    logits, y, tr, va, te = _case(rows, classes, rows + ld, gpu)
+    flat = torch.full(((rows - 1) * ld + classes,), 1e4, device=gpu)
+    x = flat.as_strided((rows, classes), (ld, 1))
+    x.copy_(logits)
+    x.requires_grad_(True)
+    codes = mask_codes(tr, va, te).to(gpu)
+    loss, stats = masked_cross_entropy(x, y, codes, "sum")
+    loss.backward()
+    xd = logits.double().cpu().requires_grad_(True)
+    trc = tr.cpu()
+    ref = F.cross_entropy(xd[trc], y.cpu()[trc], reduction="sum")
+    ref.backward()
+    assert max_abs_norm_err(loss.detach().reshape(1), ref.detach().reshape(1)) <= TOL
+    assert max_abs_norm_err(x.grad, xd.grad) <= TOL
+    vc, vn = _acc_counts(logits.cpu(), y.cpu(), va)
+    tc, tn = _acc_counts(logits.cpu(), y.cpu(), te)
+    assert stats.tolist() == [int(tr.sum()), vc, vn, tc, tn, 0]
+
+
 def test_strided_logits_and_ties(gpu):
     """ld > C (a column slice) and tied maxima: the first maximal index wins."""
     wide = torch.randn(600, 64, device=gpu)
