@@ -1619,9 +1619,10 @@ int run_ln_backward(int32_t act, const float* g, const float* h, const float* me
                     int64_t dim, float* gh, float* dgamma, float* dbeta, float* dbias,
                     const float* shift, float* rowdot, float* workspace,
                     int64_t workspace_floats, hipStream_t s) {
-  // Six rows in flight at 256 floats a row (measured: 1.52 ms for 2.45M rows at
-  // 4.96 TB/s against 1.68 ms with one, 5.05 against 4.55 TB/s for 625k rows).
-  return run_ln_backward_p<V, N, N == 1 ? 6 : 1>(act, g, h, mean, rstd, gamma, beta, rows, dim,
+  // Eight rows in flight at 256 floats a row (measured on one box, ReLU, 256
+  // wide: 2.45M rows 1.42 ms against 1.53 with six, 1.76 with four; 10M rows
+  // 5.87 against 6.43 and 6.75 ms; ten gain nothing more).
+  return run_ln_backward_p<V, N, N == 1 ? 8 : 1>(act, g, h, mean, rstd, gamma, beta, rows, dim,
                                                  gh, dgamma, dbeta, dbias, shift, rowdot,
                                                  workspace, workspace_floats, s);
 }
