@@ -100,9 +100,9 @@ __global__ __launch_bounds__(256) void xent_rows_small(const float* __restrict__
     } else {
       for (int i = threadIdx.x; i < n; i += 256) tile[i] = src[i];
     }
-  } else if ((ld & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-    // Rows of a wider, 16-byte aligned buffer (logits held zero-padded to a
-    // multiple of 4 columns): each row's first C columns, as independent
+  } else if ((ld & 3) == 0 && ld - C < 4 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    // Rows padded to a multiple of 4 columns in a 16-byte aligned buffer (the
+    // trainer's logit blocks): each row's first C columns, as independent
     // 16-byte pieces, several in flight per thread.  A piece that reaches
     // past column C - 1 is read element by element up to it, so no read
     // leaves the C columns of a row.
