@@ -266,8 +266,8 @@ def _median_time(fn, runs: int = 5) -> float:
 
 
 def cpu_baseline(graph, dim: int, sample_edges: int = 24_000_000) -> dict:
-    """The reference's CPU arithmetic for this path, on
-    every host thread: torch's sparse CSR product for the GCN forward A Z and
+    """The reference's CPU arithmetic for this path (the ops PyG runs on the
+    CPU), on every host thread: torch's sparse CSR product for the GCN forward A Z and
     for the backward Aᵀ G (the transposed CSR, built outside the timing), at
     width `dim`.  Bounded sample: the first rows of partition 0 up to
     `sample_edges` edges, with their source columns relabelled to the
@@ -300,8 +300,8 @@ def cpu_baseline(graph, dim: int, sample_edges: int = 24_000_000) -> dict:
 
 
 def cpu_gat_baseline(graph, dim: int, sample_edges: int = 2_000_000) -> dict:
-    """The reference's CPU arithmetic for a one-head GAT layer (BASELINE.md
-    section 3; PyG GATConv's message passing under grinnder/nn/gat.py:69-78)
+    """The reference's CPU arithmetic for a one-head GAT layer (PyG GATConv's
+    message passing under grinnder/nn/gat.py:69-78)
     on every host thread: logits s_j + d_i through index_select, LeakyReLU
     0.2, the segment softmax (scatter_reduce amax, exp, index_add_ of the
     sums, + 1e-16), messages alpha * Hs[col] through index_select and their
