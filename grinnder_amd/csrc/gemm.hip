@@ -679,12 +679,23 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
     int tiles_n) {
   constexpr int NT = 16 * NJ, RB = 16 * MI;
   __shared__ __align__(16) float Bs[NT * RS_KST];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lk = lane >> 4;
   const int g = blockIdx.x, slot = g / kXcds, tile = slot % tiles_n;
   const int64_t stream = (int64_t)(slot / tiles_n) * kXcds + g % kXcds;
   const int64_t nstreams = (int64_t)gridDim.x / tiles_n;
   const int n0 = tile * NT;
+  // The bias of this lane's column of each block, loaded once: it is added to
+  // the accumulators before the stores, so no store waits on a load.  Loaded
+  // before B's fill, whose loads complete after it, so that no load is in
+  // flight when the chunk loop starts.
+  float bcol[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = n0 + j * 16 + lr;
+    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
+  }
   const int kq = K / 4;
   for (int i = tid; i < NT * kq; i += 1024) {
     const int c = i / kq, k = (i % kq) * 4;
@@ -697,32 +708,31 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
   const int64_t step = nstreams * RS_WAVES;
   const int64_t blk0 = stream * RS_WAVES + wave;
   if (blk0 >= nblk) return;
-  // The wavefront's chunks t = 0 .. T - 1: block blk0 + (t / nch) step, k
-  // chunk t % nch.
+  // The wavefront's chunks t = 0 .. T - 1 (T = its blocks times nch): block
+  // blk0 + (t / nch) step, k chunk t % nch.
   const int nch = K / 32;
   const int64_t T = (nblk - blk0 + step - 1) / step * nch;
   const int qc = lane & 3, qa = (lane >> 2) & 3;
   const float* bl = Bs + lr * RS_KST + 8 * lk;
-  // The bias of this lane's column of each block, loaded once: it is added to
-  // the accumulators before the stores, so no store waits on a load.
-  float bcol[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int n = n0 + j * 16 + lr;
-    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
-  }
 
-  auto load = [&](A8 (&dst)[MI], int64_t t) {
-    if (t < T) {
-      const int64_t b = blk0 + (t / nch) * step;
-      const int c = (int)(t % nch);
+  // Cursors of the next chunk to load (lb, lc) and to compute (cb, cc),
+  // advanced by counting.  Loads are unconditional: past the wavefront's last
+  // chunk a load re-reads block blk0 (and is never used), so the wait before a
+  // chunk's products covers that chunk's loads and not the ones after it.
+  int64_t lb = blk0, cb = blk0;
+  int lc = 0, cc = 0;
+  auto load = [&](A8 (&dst)[MI]) {
+    const int64_t b = lb < nblk ? lb : blk0;
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int64_t r = b * RB + i * 16 + lr;  // rows past M read the block's first
-        const float* p = A + (r < M ? r : b * RB) * lda + c * 32 + 8 * lk;
-        dst[i].lo = *reinterpret_cast<const float4*>(p);
-        dst[i].hi = *reinterpret_cast<const float4*>(p + 4);
-      }
+    for (int i = 0; i < MI; ++i) {
+      const int64_t r = b * RB + i * 16 + lr;  // rows past M read the block's first
+      const float* p = A + (r < M ? r : b * RB) * lda + lc * 32 + 8 * lk;
+      dst[i].lo = *reinterpret_cast<const float4*>(p);
+      dst[i].hi = *reinterpret_cast<const float4*>(p + 4);
+    }
+    if (++lc == nch) {
+      lc = 0;
+      lb += step;
     }
   };
   floatx4 acc[MI][NJ];
@@ -731,8 +741,8 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const A8 (&cur)[MI], int64_t t) {
-    const int c = (int)(t % nch);
+  auto compute = [&](const A8 (&cur)[MI]) {
+    const int c = cc;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const float4 b0 = *reinterpret_cast<const float4*>(bl + j * 16 * RS_KST + c * 32);
@@ -752,7 +762,7 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
     if (c == nch - 1) {
       // The block is complete: rows 16 i + 4 lk + q, columns 16 j + lr; after
       // the quad transpose row 16 i + 4 lk + qc, columns 16 j + 4 qa .. + 3.
-      const int64_t b = blk0 + (t / nch) * step;
+      const int64_t b = cb;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int col = n0 + j * 16 + 4 * qa;
@@ -769,21 +779,28 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
         }
       }
     }
+    if (++cc == nch) {
+      cc = 0;
+      cb += step;
+    }
   };
   // Three chunk buffers in rotation: chunk t computes while t + 1 and t + 2
   // load.
   A8 r0[MI], r1[MI], r2[MI];
-  load(r0, 0);
-  load(r1, 1);
+  load(r0);
+  load(r1);
   for (int64_t t = 0; t < T; t += 3) {
-    load(r2, t + 2);
-    compute(r0, t);
+    load(r2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(r0);
     if (t + 1 >= T) break;
-    load(r0, t + 3);
-    compute(r1, t + 1);
+    load(r0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(r1);
     if (t + 2 >= T) break;
-    load(r1, t + 4);
-    compute(r2, t + 2);
+    load(r1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(r2);
   }
 }
 
@@ -792,22 +809,42 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
 // (lane % 32, lane / 32) loads k = 16 q .. 16 q + 15 of row r's 32-k chunk as
 // four 16-byte pieces and reads the same k of its B column, MFMA s of the
 // chunk summing k = 16 q + s over q), so a lane's operand reads per flop are
-// half the 16 x 16 form's.  One chunk of A ahead.  Measured on one box:
-// 2.45M x 256 x 256 2.70 ms (118.8 TFLOP/s) against 3.00 for the 16 x 16 form
-// and 2.75 for hipBLASLt; 10M x 256 x 256 10.84 against 11.49 ms.
-template <int NJ>
+// half the 16 x 16 form's.  One chunk of A ahead.
+//
+// NCH = K / 32 when it is known at compile time (even), else 0.  With NCH the
+// chunks of a block are unrolled and the block's stores follow its last chunk,
+// so the only wait on memory inside a block is for the chunk about to be
+// used; with a runtime chunk count the stores sit inside the chunk loop, and
+// the compiler's waits there also cover loads issued for later chunks.
+// Measured at 2.45M x 256 x 256 (K = 256; SQ_VALU_MFMA_BUSY_CYCLES over
+// GRBM_GUI_ACTIVE cycles): the matrix pipe busy 81.5% of the kernel's cycles
+// with the runtime loop, 87.7% with the unrolled one, on every operand tried
+// (zeros, ReLU-sparse, randn); 2.57-2.75 -> 2.42-2.56 ms, same bits.  The
+// clock under this load varies from box to box and with the data (1.8-2.3
+// GHz against 2.4 for a copy), which sets the rest of the rate.
+template <int NJ, int NCH>
 __global__ __launch_bounds__(1024) void gemm_nt_resident32(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
     const float* __restrict__ bias, float* __restrict__ C, int64_t ldc, int64_t M, int N, int K,
     int tiles_n) {
+  static_assert(NCH % 2 == 0 && NCH <= 8, "NCH: an even chunk count up to 8, or 0");
   constexpr int NT = 32 * NJ, RB = 32;
   __shared__ __align__(16) float Bs[NT * RS_KST];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, q = lane >> 5;
   const int g = blockIdx.x, slot = g / kXcds, tile = slot % tiles_n;
   const int64_t stream = (int64_t)(slot / tiles_n) * kXcds + g % kXcds;
   const int64_t nstreams = (int64_t)gridDim.x / tiles_n;
   const int n0 = tile * NT;
+  // The bias of this lane's column of each block, loaded once before B's fill
+  // (as in gemm_nt_resident).
+  float bcol[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int n = n0 + j * 32 + l32;
+    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
+  }
   const int kq = K / 4;
   for (int i = tid; i < NT * kq; i += 1024) {
     const int c = i / kq, k = (i % kq) * 4;
@@ -820,37 +857,29 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident32(
   const int64_t step = nstreams * RS_WAVES;
   const int64_t blk0 = stream * RS_WAVES + wave;
   if (blk0 >= nblk) return;
-  const int nch = K / 32;
-  const int64_t T = (nblk - blk0 + step - 1) / step * nch;
+  const int nch = NCH > 0 ? NCH : K / 32;
   const float* bl = Bs + l32 * RS_KST + 16 * q;
   const int qc = lane & 3, qa = (lane >> 2) & 7;
-  // The bias of this lane's column of each block, loaded once (as in
-  // gemm_nt_resident).
-  float bcol[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int n = n0 + j * 32 + l32;
-    bcol[j] = bias != nullptr && n < N ? bias[n] : 0.f;
-  }
 
   struct A16 {
     float4 v[4];
   };
-  auto load = [&](A16& dst, int64_t t) {
-    if (t < T) {
-      const int64_t b = blk0 + (t / nch) * step;
-      const int c = (int)(t % nch);
-      const int64_t r = b * RB + l32;  // rows past M read the block's first
-      const float* p = A + (r < M ? r : b * RB) * lda + c * 32 + 16 * q;
+  // Chunk c of block b into dst.  Loads are unconditional: past the
+  // wavefront's last block a load re-reads block blk0 (and is never used).
+  // The block's base is uniform (scalar registers) and a lane adds a 32-bit
+  // offset (lda < 2^20, checked by the dispatch).
+  auto load_at = [&](A16& dst, int64_t b, int c) {
+    const int64_t bb = b < nblk ? b : blk0;
+    const float* ab = A + bb * RB * lda;
+    const int rows = (int)(M - bb * RB < RB ? M - bb * RB : RB);  // uniform
+    const int off = (l32 < rows ? l32 : 0) * (int)lda + 16 * q + c * 32;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) dst.v[u] = *reinterpret_cast<const float4*>(p + 4 * u);
-    }
+    for (int u = 0; u < 4; ++u) dst.v[u] = *reinterpret_cast<const float4*>(ab + off + 4 * u);
   };
   floatx16 acc[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = floatx16{};
-  auto compute = [&](const A16& cur, int64_t t) {
-    const int c = (int)(t % nch);
+  auto mma = [&](const A16& cur, int c) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       float4 bv[4];
@@ -865,34 +894,78 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident32(
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.v[u].w, bv[u].w, acc[j], 0, 0, 0);
       }
     }
-    if (c == nch - 1) {
-      // Lane holds column 32 j + l32, rows 8 (e / 4) + 4 q + e % 4 (e < 16);
-      // after each quad transpose, row 8 gq + 4 q + qc, columns 32 j + 4 qa
-      // .. + 3.
-      const int64_t b = blk0 + (t / nch) * step;
+  };
+  // Block b is complete.  Lane holds column 32 j + l32, rows 8 (e / 4) + 4 q
+  // + e % 4 (e < 16); after each quad transpose, row 8 gq + 4 q + qc, columns
+  // 32 j + 4 qa .. + 3.
+  auto store_block = [&](int64_t b) {
+    float* cb = C + b * RB * ldc;  // uniform; lanes add 32-bit offsets (ldc < 2^20)
+    const int rows = (int)(M - b * RB < RB ? M - b * RB : RB);
+    const int rl = 4 * q + qc;
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int col = n0 + j * 32 + 4 * qa;
-        const bool cin = col < N;  // N % 4 == 0
+    for (int j = 0; j < NJ; ++j) {
+      const int col = n0 + j * 32 + 4 * qa;
+      const bool cin = col < N;  // N % 4 == 0
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          float v0 = acc[j][4 * gq + 0] + bcol[j], v1 = acc[j][4 * gq + 1] + bcol[j],
-                v2 = acc[j][4 * gq + 2] + bcol[j], v3 = acc[j][4 * gq + 3] + bcol[j];
-          gr_wave::quad_transpose(v0, v1, v2, v3, qc);
-          const int64_t row = b * RB + 8 * gq + 4 * q + qc;
-          if (cin && row < M)
-            *reinterpret_cast<float4*>(C + row * ldc + col) = make_float4(v0, v1, v2, v3);
-        }
-        acc[j] = floatx16{};
+      for (int gq = 0; gq < 4; ++gq) {
+        float v0 = acc[j][4 * gq + 0] + bcol[j], v1 = acc[j][4 * gq + 1] + bcol[j],
+              v2 = acc[j][4 * gq + 2] + bcol[j], v3 = acc[j][4 * gq + 3] + bcol[j];
+        gr_wave::quad_transpose(v0, v1, v2, v3, qc);
+        if (cin && 8 * gq + rl < rows)
+          *reinterpret_cast<float4*>(cb + (8 * gq + rl) * (int)ldc + col) =
+              make_float4(v0, v1, v2, v3);
       }
+      acc[j] = floatx16{};
     }
   };
-  A16 cur, nxt;
-  load(cur, 0);
-  for (int64_t t = 0; t < T; ++t) {
-    load(nxt, t + 1);
-    compute(cur, t);
-    cur = nxt;
+
+  A16 x0, x1;
+  load_at(x0, blk0, 0);
+  if constexpr (NCH > 0) {
+    // Two chunk buffers in turn; the scheduling barriers keep each load ahead
+    // of the products before it (the compiler otherwise sinks the loads to
+    // the end of the chunk).
+    for (int64_t b = blk0; b < nblk; b += step) {
+#pragma unroll
+      for (int c = 0; c < NCH; c += 2) {
+        load_at(x1, b, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(x0, c);
+        load_at(x0, c + 2 < NCH ? b : b + step, c + 2 < NCH ? c + 2 : 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(x1, c + 1);
+      }
+      store_block(b);
+    }
+  } else {
+    // Runtime chunk count: cursors (block, chunk) of the next chunk to load
+    // and to compute, advanced by counting.
+    const int64_t T = (nblk - blk0 + step - 1) / step * nch;
+    int64_t lb = blk0, cb = blk0;
+    int lc = 1, cc = 0;
+    if (lc == nch) {
+      lc = 0;
+      lb += step;
+    }
+    auto step_chunk = [&](A16& nxt, const A16& cur) {
+      load_at(nxt, lb, lc);
+      if (++lc == nch) {
+        lc = 0;
+        lb += step;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma(cur, cc);
+      if (++cc == nch) {
+        store_block(cb);
+        cc = 0;
+        cb += step;
+      }
+    };
+    for (int64_t t = 0; t < T; t += 2) {
+      step_chunk(x1, x0);
+      if (t + 1 >= T) break;
+      step_chunk(x0, x1);
+    }
   }
 }
 
@@ -924,8 +997,12 @@ static hipError_t dispatch_resident(const float* a, int64_t lda, const float* b,
     // 32 x 32 blocks, 128-column blocks of B, four workgroups per CU.
     const int per = kXcds * tiles_n;
     const int grid = std::max(per, 4 * cus / per * per);
-    hipLaunchKernelGGL((gemm_nt_resident32<4>), dim3((unsigned)grid), dim3(1024), 0, s, a, lda,
-                       b, ldb, bias, c, ldc, m, n, k, tiles_n);
+    if (k == 256)
+      hipLaunchKernelGGL((gemm_nt_resident32<4, 8>), dim3((unsigned)grid), dim3(1024), 0, s, a,
+                         lda, b, ldb, bias, c, ldc, m, n, k, tiles_n);
+    else
+      hipLaunchKernelGGL((gemm_nt_resident32<4, 0>), dim3((unsigned)grid), dim3(1024), 0, s, a,
+                         lda, b, ldb, bias, c, ldc, m, n, k, tiles_n);
     return hipGetLastError();
   }
   // 33..64 columns: 16 x 16 blocks, one column block, two workgroups per CU.
