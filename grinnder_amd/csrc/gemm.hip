@@ -657,7 +657,7 @@ static hipError_t launch_short_k(const float* a, int64_t lda, const float* b, in
 // NT = 128) and its 16 wavefronts walk blocks of 16 MI rows of A, with no
 // barrier after the fill.  A lane's two 16-byte loads of A take k = 8 lk ..
 // 8 lk + 7 of a 32-k chunk (one 128-byte line of each row a chunk), straight
-// from HBM two chunks ahead; its two ds_read_b128 of B the same eight k, and
+// from HBM one chunk ahead; its two ds_read_b128 of B the same eight k, and
 // MFMA s of the chunk sums k = 8 lk + s over lk.  The workgroups of the column
 // blocks of one row stream are on one XCD, so A is read from HBM once.  Each
 // lane quad transposes its 4 x 4 blocks, so C leaves the accumulators as
@@ -672,11 +672,15 @@ struct A8 {
   float4 lo, hi;
 };
 
-template <int MI, int NJ>
+// NCH = K / 32 when known at compile time (even), else 0: as in
+// gemm_nt_resident32 below, the chunks of a block are then unrolled with the
+// block's stores after its last chunk, one chunk of A ahead.
+template <int MI, int NJ, int NCH>
 __global__ __launch_bounds__(1024) void gemm_nt_resident(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
     const float* __restrict__ bias, float* __restrict__ C, int64_t ldc, int64_t M, int N, int K,
     int tiles_n) {
+  static_assert(NCH % 2 == 0 && NCH <= 8, "NCH: an even chunk count up to 8, or 0");
   constexpr int NT = 16 * NJ, RB = 16 * MI;
   __shared__ __align__(16) float Bs[NT * RS_KST];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -708,31 +712,24 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
   const int64_t step = nstreams * RS_WAVES;
   const int64_t blk0 = stream * RS_WAVES + wave;
   if (blk0 >= nblk) return;
-  // The wavefront's chunks t = 0 .. T - 1 (T = its blocks times nch): block
-  // blk0 + (t / nch) step, k chunk t % nch.
-  const int nch = K / 32;
-  const int64_t T = (nblk - blk0 + step - 1) / step * nch;
+  const int nch = NCH > 0 ? NCH : K / 32;
   const int qc = lane & 3, qa = (lane >> 2) & 3;
   const float* bl = Bs + lr * RS_KST + 8 * lk;
 
-  // Cursors of the next chunk to load (lb, lc) and to compute (cb, cc),
-  // advanced by counting.  Loads are unconditional: past the wavefront's last
-  // chunk a load re-reads block blk0 (and is never used), so the wait before a
-  // chunk's products covers that chunk's loads and not the ones after it.
-  int64_t lb = blk0, cb = blk0;
-  int lc = 0, cc = 0;
-  auto load = [&](A8 (&dst)[MI]) {
-    const int64_t b = lb < nblk ? lb : blk0;
+  // Chunk c of block b into dst.  Loads are unconditional: past the
+  // wavefront's last block a load re-reads block blk0 (and is never used).
+  // The block's base is uniform; lanes add 32-bit offsets (lda < 2^20,
+  // checked by the dispatch).
+  auto load_at = [&](A8 (&dst)[MI], int64_t b, int c) {
+    const int64_t bb = b < nblk ? b : blk0;
+    const float* ab = A + bb * RB * lda;
+    const int rows = (int)(M - bb * RB < RB ? M - bb * RB : RB);  // uniform
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      const int64_t r = b * RB + i * 16 + lr;  // rows past M read the block's first
-      const float* p = A + (r < M ? r : b * RB) * lda + lc * 32 + 8 * lk;
-      dst[i].lo = *reinterpret_cast<const float4*>(p);
-      dst[i].hi = *reinterpret_cast<const float4*>(p + 4);
-    }
-    if (++lc == nch) {
-      lc = 0;
-      lb += step;
+      const int r = i * 16 + lr;  // rows past M read the block's first
+      const int off = (r < rows ? r : 0) * (int)lda + c * 32 + 8 * lk;
+      dst[i].lo = *reinterpret_cast<const float4*>(ab + off);
+      dst[i].hi = *reinterpret_cast<const float4*>(ab + off + 4);
     }
   };
   floatx4 acc[MI][NJ];
@@ -741,8 +738,7 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const A8 (&cur)[MI]) {
-    const int c = cc;
+  auto mma = [&](const A8 (&cur)[MI], int c) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const float4 b0 = *reinterpret_cast<const float4*>(bl + j * 16 * RS_KST + c * 32);
@@ -759,48 +755,73 @@ __global__ __launch_bounds__(1024) void gemm_nt_resident(
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[i].hi.w, b1.w, acc[i][j], 0, 0, 0);
       }
     }
-    if (c == nch - 1) {
-      // The block is complete: rows 16 i + 4 lk + q, columns 16 j + lr; after
-      // the quad transpose row 16 i + 4 lk + qc, columns 16 j + 4 qa .. + 3.
-      const int64_t b = cb;
+  };
+  // Block b is complete: rows 16 i + 4 lk + q, columns 16 j + lr; after the
+  // quad transpose row 16 i + 4 lk + qc, columns 16 j + 4 qa .. + 3.
+  auto store_block = [&](int64_t b) {
+    float* cb = C + b * RB * ldc;  // uniform; lanes add 32-bit offsets (ldc < 2^20)
+    const int rows = (int)(M - b * RB < RB ? M - b * RB : RB);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int col = n0 + j * 16 + 4 * qa;
-        const bool cin = col < N;  // N % 4 == 0: the four columns are in or out together
+    for (int j = 0; j < NJ; ++j) {
+      const int col = n0 + j * 16 + 4 * qa;
+      const bool cin = col < N;  // N % 4 == 0: the four columns are in or out together
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-          float v0 = acc[i][j][0] + bcol[j], v1 = acc[i][j][1] + bcol[j],
-                v2 = acc[i][j][2] + bcol[j], v3 = acc[i][j][3] + bcol[j];
-          gr_wave::quad_transpose(v0, v1, v2, v3, qc);
-          const int64_t row = b * RB + i * 16 + 4 * lk + qc;
-          if (cin && row < M)
-            *reinterpret_cast<float4*>(C + row * ldc + col) = make_float4(v0, v1, v2, v3);
-          acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+      for (int i = 0; i < MI; ++i) {
+        float v0 = acc[i][j][0] + bcol[j], v1 = acc[i][j][1] + bcol[j],
+              v2 = acc[i][j][2] + bcol[j], v3 = acc[i][j][3] + bcol[j];
+        gr_wave::quad_transpose(v0, v1, v2, v3, qc);
+        const int r = i * 16 + 4 * lk + qc;
+        if (cin && r < rows)
+          *reinterpret_cast<float4*>(cb + r * (int)ldc + col) = make_float4(v0, v1, v2, v3);
+        acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    if (++cc == nch) {
-      cc = 0;
-      cb += step;
-    }
   };
-  // Three chunk buffers in rotation: chunk t computes while t + 1 and t + 2
-  // load.
-  A8 r0[MI], r1[MI], r2[MI];
-  load(r0);
-  load(r1);
-  for (int64_t t = 0; t < T; t += 3) {
-    load(r2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(r0);
-    if (t + 1 >= T) break;
-    load(r0);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(r1);
-    if (t + 2 >= T) break;
-    load(r1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(r2);
+
+  A8 x0[MI], x1[MI];
+  load_at(x0, blk0, 0);
+  if constexpr (NCH > 0) {
+    for (int64_t b = blk0; b < nblk; b += step) {
+#pragma unroll
+      for (int c = 0; c < NCH; c += 2) {
+        load_at(x1, b, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(x0, c);
+        load_at(x0, c + 2 < NCH ? b : b + step, c + 2 < NCH ? c + 2 : 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(x1, c + 1);
+      }
+      store_block(b);
+    }
+  } else {
+    // Runtime chunk count: cursors (block, chunk) of the next chunk to load
+    // and to compute, advanced by counting.
+    const int64_t T = (nblk - blk0 + step - 1) / step * nch;
+    int64_t lb = blk0, cb = blk0;
+    int lc = 1, cc = 0;
+    if (lc == nch) {
+      lc = 0;
+      lb += step;
+    }
+    auto step_chunk = [&](A8 (&nxt)[MI], const A8 (&cur)[MI]) {
+      load_at(nxt, lb, lc);
+      if (++lc == nch) {
+        lc = 0;
+        lb += step;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma(cur, cc);
+      if (++cc == nch) {
+        store_block(cb);
+        cc = 0;
+        cb += step;
+      }
+    };
+    for (int64_t t = 0; t < T; t += 2) {
+      step_chunk(x1, x0);
+      if (t + 1 >= T) break;
+      step_chunk(x0, x1);
+    }
   }
 }
 
@@ -973,14 +994,18 @@ template <int MI, int NJ>
 static hipError_t launch_resident(const float* a, int64_t lda, const float* b, int64_t ldb,
                                   const float* bias, float* c, int64_t ldc, int64_t m, int n,
                                   int k, int tiles_n, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((gemm_nt_resident<MI, NJ>), dim3((unsigned)grid), dim3(1024), 0, s, a, lda,
-                     b, ldb, bias, c, ldc, m, n, k, tiles_n);
+  if (k == 256)
+    hipLaunchKernelGGL((gemm_nt_resident<MI, NJ, 8>), dim3((unsigned)grid), dim3(1024), 0, s, a,
+                       lda, b, ldb, bias, c, ldc, m, n, k, tiles_n);
+  else
+    hipLaunchKernelGGL((gemm_nt_resident<MI, NJ, 0>), dim3((unsigned)grid), dim3(1024), 0, s, a,
+                       lda, b, ldb, bias, c, ldc, m, n, k, tiles_n);
   return hipGetLastError();
 }
 
 // The resident forms for 32 < n <= 256: the 32 x 32 form past 64 columns
 // (two column blocks past 128), the 16 x 16 form below, where MI * NJ <= 8
-// keeps its accumulators and three chunks of A within 128 registers (16
+// keeps its accumulators and two chunks of A within 128 registers (16
 // wavefronts a CU).  Workgroups: a whole number of XCD rounds per column
 // block, four per CU for the 32 x 32 form and two for the 16 x 16 one (the
 // counts measured best; the LDS holds one at a time, the rest queue).
@@ -1030,7 +1055,7 @@ extern "C" int gr_gemm_nt(const float* a, int64_t lda, const float* b, int64_t l
   if (va && vb && k % 32 == 0 && k <= 256 && n > 32 && n <= 256 && n % 4 == 0 && ldc % 4 == 0 &&
       reinterpret_cast<uintptr_t>(c) % 16 == 0 &&
       (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0) &&
-      m >= kResidentMinRows) {
+      m >= kResidentMinRows && lda < (1 << 20) && ldc < (1 << 20)) {
     err = dispatch_resident(a, lda, b, ldb, bias, c, ldc, m, (int)n, (int)k, s);
   } else if (k <= 64 && n >= 64 && !(va && vb)) {
     // Short reduction with rows of A or B that 16-byte loads cannot take
