@@ -123,6 +123,65 @@ def traffic_probe(kind: str, device: str) -> None:
                       "write_bytes": write, "ms": [round(t, 3) for t in ms]}), flush=True)
 
 
+# The epochs' dense products at their full sizes (--dense-probe): name ->
+# (kind, rows, columns of the output, reduction length).  "nt" is x Wᵀ + b
+# (gemm_nt: rows x cols over k), "tn" a weight gradient aᵀ b (gemm_tn: cols
+# x k over `rows`), "lla" layer 0's fused transform (linear_ln_act, ReLU).
+DENSE_PROBES = {
+    "c2_layer1_forward": ("nt", 2_449_029, 256, 256),
+    "c2_layer2_forward": ("nt", 2_449_029, 48, 256),
+    "c2_layer0_transform": ("lla", 2_449_029, 256, 100),
+    "c2_layer1_dW": ("tn", 2_449_029, 256, 256),
+    "c2_layer0_dW": ("tn", 2_449_029, 256, 100),
+    "c4_layer1_forward": ("nt", 10_000_000, 256, 256),
+    "c4_layer1_dW": ("tn", 10_000_000, 256, 256),
+    "c4_layer0_projection": ("nt", 10_000_000, 256, 1024),
+    "c4_layer0_dW": ("tn", 10_000_000, 256, 1024),
+}
+
+
+def dense_probe(device: str, reps: int = 3) -> None:
+    """Runs each DENSE_PROBES product `reps` times after one untimed call on
+    seeded data (ReLU-sparse inputs, as a layer's activations are) and prints
+    one JSON line per product with its HIP-event times and TFLOP/s."""
+    import torch
+
+    from grinnder_amd import dense
+
+    g = torch.Generator(device=device).manual_seed(0)
+    for name, (kind, rows, cols, k) in DENSE_PROBES.items():
+        x = torch.relu(torch.empty(rows, k, device=device).normal_(generator=g))
+        if kind == "nt":
+            w = torch.empty(cols, k, device=device).normal_(generator=g).mul_(k ** -0.5)
+            b = torch.empty(cols, device=device).normal_(generator=g)
+            fn = lambda: dense.gemm_nt(x, w, b)  # noqa: E731
+        elif kind == "lla":
+            w = torch.empty(cols, k, device=device).normal_(generator=g).mul_(k ** -0.5)
+            b = torch.empty(cols, device=device).normal_(generator=g)
+            gamma = torch.ones(cols, device=device)
+            beta = torch.zeros(cols, device=device)
+            fn = lambda: dense.linear_ln_act(x, w, b, gamma, beta)  # noqa: E731
+        else:
+            dz = torch.empty(rows, cols, device=device).normal_(generator=g).mul_(0.01)
+            fn = lambda: dense.gemm_tn(dz, x)  # noqa: E731
+        fn()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(reps):
+            a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            ms.append(a.elapsed_time(e))
+        flop = 2.0 * rows * cols * k
+        print(json.dumps({"product": name, "kind": kind, "rows": rows, "cols": cols, "k": k,
+                          "ms": [round(t, 3) for t in ms],
+                          "TFLOPs": round(flop / (min(ms) / 1e3) / 1e12, 1)}), flush=True)
+        del x, fn
+        torch.cuda.empty_cache()
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -162,6 +221,9 @@ def parse_args():
     ap.add_argument("--traffic-probe", choices=sorted(TRAFFIC_PROBES), default=None,
                     help="run only a kernel of known memory traffic three times (for checking "
                          "rocprof's memory counters against it) and exit")
+    ap.add_argument("--dense-probe", action="store_true",
+                    help="run only the epochs' dense products at full size (C2 and C4/C5 "
+                         "shapes), three timed calls each, and exit")
     return ap.parse_args()
 
 
@@ -599,12 +661,41 @@ def summarize_profile(root: str) -> None:
         if CALIBRATION_KERNEL in k and n and c in ("FETCH_SIZE", "WRITE_SIZE"):
             print(f"# calibration {c}: {CALIBRATION_KERNEL} moves {CALIBRATION_KIB} KiB, "
                   f"counter mean {v / n:.1f} KiB -> scale x{CALIBRATION_KIB / (v / n):.4f}")
+    simds, xcds = _gpu_shape(paths)
+    clock_lines = []
+    for k, means in sorted(per_kernel.items()):
+        if "GRBM_GUI_ACTIVE" in means and "SQ_VALU_MFMA_BUSY_CYCLES" in means and xcds:
+            n, _, t, _, _ = acc[(k, "GRBM_GUI_ACTIVE")]
+            cycles = means["GRBM_GUI_ACTIVE"] / xcds  # per XCD: the kernel's clock cycles
+            busy = means["SQ_VALU_MFMA_BUSY_CYCLES"] / simds / cycles if cycles else 0.0
+            if busy > 0:
+                clock_lines.append(f"MFMA busy={busy:.3f} clock_GHz={cycles / (t / n):.3f} "
+                                   f"kernel={k[:200]}")
+    if clock_lines:
+        print(f"# matrix pipe: busy = SQ_VALU_MFMA_BUSY_CYCLES / ({simds} SIMDs x kernel cycles), "
+              f"kernel cycles = GRBM_GUI_ACTIVE / {xcds} XCDs, clock = cycles / duration")
+        print("\n".join(clock_lines))
     print("# fabric bytes per dispatch from request sizes: read = 32*RDREQ_32B + "
           "64*RDREQ_64B + 128*RDREQ_128B, write = 32*(WRREQ - WRREQ_64B) + 64*WRREQ_64B")
     for k, means in sorted(per_kernel.items()):
         rw = request_bytes(means)
         if rw is not None:
             print(f"BYTES read={rw[0]:.0f} write={rw[1]:.0f} kernel={k[:200]}")
+
+
+def _gpu_shape(counter_paths) -> tuple:
+    """(SIMD count, XCD count) of the GPU from the agent_info.csv beside the
+    counter files, or (0, 0) when there is none."""
+    import csv
+
+    for p in counter_paths:
+        info = p.replace("counter_collection.csv", "agent_info.csv")
+        if os.path.exists(info):
+            with open(info) as f:
+                for r in csv.DictReader(f):
+                    if r.get("Agent_Type") == "GPU":
+                        return int(r["Simd_Count"]), int(r["Num_Xcc"])
+    return 0, 0
 
 
 def traffic_from_profile(path: str, kernels) -> Optional[dict]:
@@ -632,6 +723,9 @@ def main():
         return
     if args.traffic_probe:
         traffic_probe(args.traffic_probe, "cuda:0")
+        return
+    if args.dense_probe:
+        dense_probe("cuda:0")
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the "
