@@ -573,23 +573,49 @@ ln_act_backward_product(
   constexpr int kMaxSlices = KS;
   float4 dzn[kMaxSlices];
   float hn[4][NH], mun[4], rsn[4];
+  // Without the row dot every load is issued (rows past the end read the
+  // last row, k past K the row's first k) and the values that are not the
+  // step's are zeroed after, and gh leaves through a buffer resource (below):
+  // with no branch around them the compiler counts the loads and stores, and
+  // its wait for a step's values does not also wait for the stores after
+  // them.  The row-dot forms keep guarded loads and stores, which fit their
+  // registers.
+  constexpr bool kCounted = !DOT;
   auto prefetch = [&](int64_t r0) {
     const int64_t ra = r0 + lr;
+    const int64_t rac = ra < rows ? ra : rows - 1;
 #pragma unroll
     for (int sl = 0; sl < kMaxSlices; ++sl) {
       const int k0 = sl * 16 + lk * 4;
-      dzn[sl] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (sl < nslices && ra < rows && k0 < K)
-        dzn[sl] = *reinterpret_cast<const float4*>(dz + ra * ldz + k0);
+      const bool ok = sl < nslices && ra < rows && k0 < K;
+      if constexpr (kCounted) {
+        const float4 v = *reinterpret_cast<const float4*>(dz + rac * ldz + (ok ? k0 : 0));
+        dzn[sl] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        dzn[sl] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ok) dzn[sl] = *reinterpret_cast<const float4*>(dz + ra * ldz + k0);
+      }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int64_t row = r0 + lk * 4 + q;
       const bool valid = row < rows;
-      mun[q] = valid ? mean[row] : 0.f;
-      rsn[q] = valid ? rstd[row] : 0.f;
+      if constexpr (kCounted) {
+        const int64_t rowc = valid ? row : rows - 1;
+        const float m = mean[rowc], rsd = rstd[rowc];
+        mun[q] = valid ? m : 0.f;
+        rsn[q] = valid ? rsd : 0.f;
 #pragma unroll
-      for (int b = 0; b < NH; ++b) hn[q][b] = valid ? h[row * D + c0 + b * 16 + lr] : 0.f;
+        for (int b = 0; b < NH; ++b) {
+          const float hv = h[rowc * D + c0 + b * 16 + lr];
+          hn[q][b] = valid ? hv : 0.f;
+        }
+      } else {
+        mun[q] = valid ? mean[row] : 0.f;
+        rsn[q] = valid ? rstd[row] : 0.f;
+#pragma unroll
+        for (int b = 0; b < NH; ++b) hn[q][b] = valid ? h[row * D + c0 + b * 16 + lr] : 0.f;
+      }
     }
   };
   const int64_t step = (int64_t)gridDim.x * 32;
@@ -609,7 +635,14 @@ ln_act_backward_product(
 #pragma unroll
       for (int b = 0; b < NH; ++b) hv[q][b] = hn[q][b];
     }
-    if (rb + step < rows) prefetch(r0 + step);
+    if (kCounted)
+      prefetch(rb + step < rows ? r0 + step : r0);  // issued either way
+    else if (rb + step < rows)
+      prefetch(r0 + step);
+    // The step's rows of gh through a buffer resource that ends at the last
+    // row: rows past it are sent past the end and dropped.
+    const int nrow = (int)(rows - r0 < 16 ? (rows - r0 > 0 ? rows - r0 : 0) : 16);  // uniform
+    const auto ghb = gr_wave::buffer(gh + r0 * D, (uint32_t)nrow * D * 4);
     floatx4 acc[NH];
 #pragma unroll
     for (int b = 0; b < NH; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -669,7 +702,11 @@ ln_act_backward_product(
         const float o = rs * (gx - s1 - xh * s2);
         ph[b] += o;
         if (DOT) dot = fmaf(o, hv[q][b] - GB[2 * D + c], dot);
-        if (valid) gh[row * D + c] = o;
+        if constexpr (kCounted)
+          gr_wave::buffer_store(ghb, valid ? (uint32_t)((lk * 4 + q) * D + c) * 4
+                                           : gr_wave::kBufferDrop, o);
+        else if (valid)
+          gh[row * D + c] = o;
       }
       if constexpr (DOT) {
         dot = gr_wave::group_sum<16>(dot);

@@ -165,4 +165,23 @@ __device__ __forceinline__ void quad_transpose(float& v0, float& v1, float& v2, 
   }
 }
 
+// Raw buffer stores.  A store whose byte offset is at or past the resource's
+// size is dropped by the hardware, so a kernel can send the rows or lanes it
+// must not write past the end instead of branching around the store; with no
+// branch the compiler knows how many stores are in flight and can wait for a
+// later load without waiting for them.  Word 3 of the resource is the gfx9
+// family's raw-buffer format (the value composable_kernel's ck.hpp uses).
+constexpr uint32_t kBufferDrop = 0x80000000u;  // past any resource made below
+
+// `bytes` < 2^31; the base must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ void buffer_store(__amdgpu_buffer_rsrc_t r, uint32_t offset,
+                                             float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, offset, 0, 0);
+}
+
 }  // namespace gr_wave
