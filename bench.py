@@ -140,16 +140,19 @@ DENSE_PROBES = {
 }
 
 
-def dense_probe(device: str, reps: int = 3) -> None:
-    """Runs each DENSE_PROBES product `reps` times after one untimed call on
-    seeded data (ReLU-sparse inputs, as a layer's activations are) and prints
-    one JSON line per product with its HIP-event times and TFLOP/s."""
+def dense_probe(device: str, reps: int = 3, only: Optional[str] = None) -> None:
+    """Runs each DENSE_PROBES product (or only `only`) `reps` times after one
+    untimed call on seeded data (ReLU-sparse inputs, as a layer's activations
+    are) and prints one JSON line per product with its HIP-event times (the
+    first three and the last three calls) and TFLOP/s over all the calls."""
     import torch
 
     from grinnder_amd import dense
 
     g = torch.Generator(device=device).manual_seed(0)
     for name, (kind, rows, cols, k) in DENSE_PROBES.items():
+        if only is not None and name != only:
+            continue
         x = torch.relu(torch.empty(rows, k, device=device).normal_(generator=g))
         if kind == "nt":
             w = torch.empty(cols, k, device=device).normal_(generator=g).mul_(k ** -0.5)
@@ -166,18 +169,31 @@ def dense_probe(device: str, reps: int = 3) -> None:
             fn = lambda: dense.gemm_tn(dz, x)  # noqa: E731
         fn()
         torch.cuda.synchronize()
-        ms = []
-        for _ in range(reps):
-            a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
+        head = min(3, reps)
+        tail = min(3, reps - head)
+        timed = list(range(head)) + list(range(reps - tail, reps))  # calls with own events
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in timed]
+        slot_of = {call: j for j, call in enumerate(timed)}
+        first = torch.cuda.Event(enable_timing=True)
+        last = torch.cuda.Event(enable_timing=True)
+        first.record()
+        for i in range(reps):
+            j = slot_of.get(i)
+            if j is not None:
+                events[j][0].record()
             fn()
-            e.record()
-            torch.cuda.synchronize()
-            ms.append(a.elapsed_time(e))
+            if j is not None:
+                events[j][1].record()
+        last.record()
+        torch.cuda.synchronize()
+        ms = [a.elapsed_time(e) for a, e in events]
         flop = 2.0 * rows * cols * k
+        total_ms = first.elapsed_time(last)
         print(json.dumps({"product": name, "kind": kind, "rows": rows, "cols": cols, "k": k,
-                          "ms": [round(t, 3) for t in ms],
-                          "TFLOPs": round(flop / (min(ms) / 1e3) / 1e12, 1)}), flush=True)
+                          "calls": reps, "ms": [round(t, 3) for t in ms],
+                          "TFLOPs": round(flop * reps / (total_ms / 1e3) / 1e12, 1)}),
+              flush=True)
         del x, fn
         torch.cuda.empty_cache()
 
@@ -224,6 +240,10 @@ def parse_args():
     ap.add_argument("--dense-probe", action="store_true",
                     help="run only the epochs' dense products at full size (C2 and C4/C5 "
                          "shapes), three timed calls each, and exit")
+    ap.add_argument("--dense-repeat", type=int, default=3,
+                    help="timed calls of each product for --dense-probe")
+    ap.add_argument("--dense-only", choices=sorted(DENSE_PROBES), default=None,
+                    help="run only this product for --dense-probe")
     return ap.parse_args()
 
 
@@ -725,7 +745,7 @@ def main():
         traffic_probe(args.traffic_probe, "cuda:0")
         return
     if args.dense_probe:
-        dense_probe("cuda:0")
+        dense_probe("cuda:0", max(1, args.dense_repeat), args.dense_only)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the "
