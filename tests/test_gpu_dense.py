@@ -501,6 +501,41 @@ def test_ln_act_backward_product_matches_fp64(gpu, rows, k, dim, act, bias, dot)
         assert max_abs_norm_err(rowdot, ref) <= TOL
 
 
+@pytest.mark.parametrize("rows", [1, 17, 31, 33, 4099])
+def test_ln_act_backward_product_writes_no_row_past_the_last(gpu, rows):
+    """gh leaves the kernel through a buffer resource that ends at each step's
+    last row, the rows past it sent beyond the end to be dropped: with gh the
+    first rows of a larger buffer filled with a sentinel, every row past the
+    last keeps the sentinel, and the rows written match the float64 result."""
+    dim, k = 256, 48
+    h = _randn(rows, dim, seed=rows, dev=gpu)
+    gamma = 1 + 0.1 * _randn(dim, seed=1, dev=gpu)
+    beta = 0.1 * _randn(dim, seed=2, dev=gpu)
+    dz = _randn(rows, k, seed=3, dev=gpu)
+    b = 0.2 * _randn(k, dim, seed=4, dev=gpu)
+    h64 = h.double()
+    mean = h64.mean(1).float().contiguous()
+    rstd = (1.0 / torch.sqrt(h64.var(1, unbiased=False) + 1e-5)).float().contiguous()
+    pad = 40  # rows of sentinel after the last row (a whole 32-row step and more)
+    gh = torch.full((rows + pad, dim), 12345.0, device=gpu)
+    dgamma = torch.empty(dim, device=gpu)
+    dbeta = torch.empty(dim, device=gpu)
+    nwaves = (min(8192, max(4, (rows + 15) // 16)) + 3) // 4 * 4
+    ws = torch.empty((2 * nwaves + 1) * dim, device=gpu)
+    _lib.call("gr_ln_act_backward_product", dz.data_ptr(), k, k, b.data_ptr(), h.data_ptr(),
+              mean.data_ptr(), rstd.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+              _lib.ACTIVATIONS["relu"], rows, dim, gh.data_ptr(), dgamma.data_ptr(),
+              dbeta.data_ptr(), None, None, None, ws.data_ptr(), ws.numel(),
+              _lib.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.all(gh[rows:] == 12345.0)
+    hh = h64.clone().requires_grad_(True)
+    out = torch.relu(torch.nn.functional.layer_norm(hh, (dim,), gamma.double(),
+                                                    beta.double(), 1e-5))
+    out.backward(dz.double() @ b.double())
+    assert max_abs_norm_err(gh[:rows], hh.grad) <= TOL
+
+
 @pytest.mark.parametrize("extra_consumer", [False, True])
 def test_layernorm_takes_narrow_product_gradient(gpu, extra_consumer):
     """A fused LayerNorm/ReLU output consumed by a narrow padded GCN product
