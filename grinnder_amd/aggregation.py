@@ -215,6 +215,10 @@ class ProjectedSink:
     # First global row of the partition's destination rows (its own rows,
     # the first num_dst of `rows`); read by the attention backward.
     lo: int = 0
+    # `rows` are every row of dz once, in order (a merged layer's whole-graph
+    # pass), and nothing else writes dz: the GCN backward then writes Aᵀ G
+    # into dz (which needs no zeroing) instead of adding it.
+    overwrite: bool = False
 
 
 def spmm_into(plan, idx: Tensor, val: Tensor, x: Tensor, sink: ProjectedSink,
@@ -227,6 +231,12 @@ def spmm_into(plan, idx: Tensor, val: Tensor, x: Tensor, sink: ProjectedSink,
     rows = plan.rows
     if sink.rows.numel() != rows:
         raise ValueError(f"spmm_into: {sink.rows.numel()} row ids for {rows} rows")
+    if sink.overwrite:
+        if dz.size(0) != rows:
+            raise ValueError(f"spmm_into: overwrite needs dz's {dz.size(0)} rows to be the "
+                             f"plan's {rows}")
+        spmm(plan, idx, val, x, rows, out=dz, name=name)
+        return
     ws = _workspace(plan.n_slots, dim, x.device)
     nnz = idx.numel()
     with KernelTimer.region(name, nnz * (4 * dim + 8) + rows * (8 * dim + 4), nnz, dim):

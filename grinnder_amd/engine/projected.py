@@ -543,6 +543,10 @@ class ProjectedLayers:
             self._wids = (plan.idx, torch.arange(n, dtype=torch.int32, device=self.device))
         return self._wids
 
+    def _whole_sink(self, layer: int) -> bool:
+        """A merged layer reads Z in place through a sink over all rows."""
+        return self.model.projected_sink_ok(layer) and int(self.graph.ptr[-1]) < 2 ** 31
+
     def _merged_call(self, layer: int, grad: bool,
                      dest: Optional[OutputRows] = None) -> Tensor:
         """The layer's forward for every partition at once, over the whole
@@ -559,9 +563,10 @@ class ProjectedLayers:
         extra = {} if sc is None else {"scores": sc}
         if self._token is None:
             self._token = torch.zeros(0, device=self.device, requires_grad=True)
-        if self.model.projected_sink_ok(layer) and int(self.graph.ptr[-1]) < 2 ** 31:
+        if self._whole_sink(layer):
             gidx, rows = self._whole_ids()
-            sink = ProjectedSink(self._dzbuf(layer), gidx, rows, self._token, 0)
+            sink = ProjectedSink(self._dzbuf(layer), gidx, rows, self._token, 0,
+                                 overwrite=self.model.sink_writes_whole(layer))
             return self.model.forward_projected(layer, self._zbufs[layer], adj, sink=sink,
                                                 dest=dest, **extra)
         z = self._zbufs[layer]
@@ -854,8 +859,12 @@ class ProjectedLayers:
         elif not inplace:
             w = self._proj[layer]
             dz = self._dzbuf(layer)
-            with torch.cuda.stream(s.compute):
-                dz.zero_()
+            # A merged layer whose sink writes every row of dz (GCN) needs no
+            # zeroed dz; otherwise the backward adds into it.
+            if not (layer in self._merged and self._whole_sink(layer)
+                    and self.model.sink_writes_whole(layer)):
+                with torch.cuda.stream(s.compute):
+                    dz.zero_()
         from_device = not last and self._grad_on_device(layer + 1)
         from_host = not last and not from_device
         gbuf = self.device_gradients[layer + 1] if not last else None

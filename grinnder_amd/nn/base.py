@@ -66,6 +66,13 @@ class GriNNderModel(torch.nn.Module):
         """Whether forward_projected(layer, ...) accepts a sink."""
         return False
 
+    def sink_writes_whole(self, layer: int) -> bool:
+        """Whether the layer's backward, given a sink whose rows are every row
+        of dz once and in order (a merged layer's), may write dz instead of
+        adding into it: true when that sink is the backward's only write of
+        dz."""
+        return False
+
     def projected_scores(self, layer: int, z: Tensor, whole: bool = False):
         """Per-row quantities of the projected matrix z that
         forward_projected(layer, ...) can take precomputed for a partition's

@@ -76,6 +76,10 @@ class GCN(GriNNderModel):
         rows into a compact copy that stays in the caches."""
         return self.convs[layer].out_channels % 4 == 0
 
+    def sink_writes_whole(self, layer: int) -> bool:
+        """The aggregation's backward is the only write of dz."""
+        return True
+
     def inplace_ok(self, layer: int) -> bool:
         """The first layer, when it aggregates first (it widens): (A x) Wᵀ
         aggregates the narrower input, and its input needs no gradient."""
