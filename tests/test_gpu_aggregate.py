@@ -310,6 +310,37 @@ def test_aggregate_into_equals_spmm_then_index_add(gpu, dim):
     assert torch.equal(dz, ref)
 
 
+@pytest.mark.parametrize("dim", [4, 48, 256])
+def test_overwrite_sink_writes_every_row(gpu, dim):
+    """A sink whose rows are every row of dz once, in order (a merged layer's),
+    with overwrite: spmm_into writes the aggregation into dz, which starts as
+    NaN (no zeroing needed), bit for bit the plain aggregation, split and
+    empty rows included; a dz whose row count differs is refused."""
+    from grinnder_amd.aggregation import ProjectedSink, spmm, spmm_into
+    B, E = 700, 900
+    rowptr, col, val = random_bipartite(B, E, 12, seed=dim + 7, long_rows=3)
+    empty = torch.nonzero(rowptr[1:] == rowptr[:-1])[:, 0]  # written as zeros all the same
+    adj = Adjacency(rowptr, col, val, (B, E), seg_len=128)
+    plan = adj.device_plan(torch.device(gpu))
+    g = torch.Generator().manual_seed(dim)
+    x = torch.randn(E, dim, generator=g).to(gpu)
+    ref = spmm(plan.fwd, plan.idx, plan.val, x, B)
+    dz = torch.full((B, dim), float("nan"), device=gpu)
+    rows = torch.arange(B, dtype=torch.int32, device=gpu)
+    sink = ProjectedSink(dz, torch.empty(0, dtype=torch.int32, device=gpu), rows,
+                         torch.zeros(0, device=gpu), overwrite=True)
+    spmm_into(plan.fwd, plan.idx, plan.val, x, sink)
+    torch.cuda.synchronize()
+    assert plan.fwd.n_fix > 0
+    assert torch.equal(dz, ref)
+    assert empty.numel() > 0 and torch.all(dz[empty.to(gpu)] == 0)
+    wide = ProjectedSink(torch.empty(B + 1, dim, device=gpu), sink.gidx,
+                         torch.arange(B, dtype=torch.int32, device=gpu), sink.token,
+                         overwrite=True)
+    with pytest.raises(ValueError):
+        spmm_into(plan.fwd, plan.idx, plan.val, x, wide)
+
+
 @pytest.mark.parametrize("fused", [False, True])
 def test_sink_reads_z_in_place_and_adds_into_dz(gpu, fused):
     """A projected partition through a sink (Z read through global ids, the
